@@ -1,0 +1,179 @@
+/*
+ * inferno_hip — C ABI of the MI355X (gfx950) speculative-verify hot path.
+ *
+ * Plain pointers, sizes and an opaque stream handle (a hipStream_t passed as
+ * void*; NULL = the default stream). No exceptions cross this ABI: the
+ * ihip_* functions return IHIP_OK (0) or a negative status, and
+ * ihip_last_error() gives a message for the calling thread.
+ *
+ * Citations are to the reference (Inferno.jl) interface each entry point
+ * replaces, relative to its repository root.
+ */
+#ifndef INFERNO_HIP_H
+#define INFERNO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---- */
+#define IHIP_OK       0
+#define IHIP_EFAULT (-14)   /* NULL pointer argument */
+#define IHIP_EINVAL (-22)   /* bad shape / type / flag */
+#define IHIP_ENOMEM (-12)   /* workspace too small or allocation failed */
+#define IHIP_ENODEV (-19)   /* no usable gfx950 device */
+#define IHIP_EHIP  (-1000)  /* HIP runtime error; see ihip_last_error() */
+
+/* ---- GGML quant type ids (src/GGUF.jl:25-60) ---- */
+#define IHIP_Q8_0 8
+#define IHIP_Q4_K 12
+#define IHIP_Q5_K 13
+#define IHIP_Q6_K 14
+
+/* ---- ihip_gemm_q flags ---- */
+#define IHIP_GEMM_AUTO   0  /* fp32-accurate for M < 16, half MFMA for M >= 16 */
+#define IHIP_GEMM_F32    1  /* force fp32-accurate: split-fp16 MFMA, rel-L2 <= 1e-5 */
+#define IHIP_GEMM_HALF   2  /* force single-limb fp16 MFMA, rel-L2 <= 1e-2 */
+#define IHIP_GEMM_ACCUM  4  /* y += W x (y is not cleared first) */
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *ihip_last_error(void);
+
+/* Select the device and create the library stream used by the host-pointer
+ * drop-in entry points. Called implicitly by the first drop-in call.
+ * Replaces the library probe of QuantizedKernels._load_libquant
+ * (src/QuantizedKernels.jl:34-47). */
+int ihip_init(int device);
+
+/* 1 if the library initialised on a gfx950 device and was not disabled by
+ * INFERNO_NO_QUANT_KERNELS; replaces quant_kernels_available()
+ * (src/QuantizedKernels.jl:49-50). */
+int ihip_available(void);
+
+/* ======================================================================
+ * 1. Drop-in exports: same symbol names and argument order as the
+ *    reference C kernel (src/kernels/quant_kernels.c:602-697), bound by
+ *    QuantizedKernels.q{4,5,6}_k_gemv! / q8_0_gemv!
+ *    (src/QuantizedKernels.jl:82-146).
+ *    Host pointers; synchronous. weight is GGUF row-major blocks, row r
+ *    owning blocks [r*K/QK, (r+1)*K/QK). The device copy of each weight is
+ *    cached by (host pointer, byte size): weights must not change after
+ *    their first use (ihip_weight_cache_clear() drops the cache). q8_buf is
+ *    accepted and ignored (NULL allowed): the GPU path needs no Q8_K
+ *    scratch. out[r] = sum_k W[r,k] x[k] computed fp32-accurately. On error
+ *    nothing is written to out, the status is kept for ihip_last_error()
+ *    and ihip_last_status(), and a message is printed to stderr.
+ * ====================================================================== */
+void q4_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_buf,
+               int inner_dim, int outer_dim);
+void q5_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_buf,
+               int inner_dim, int outer_dim);
+void q6_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_buf,
+               int inner_dim, int outer_dim);
+void q8_0_gemv(const uint8_t *weight, const float *x, float *out,
+               int inner_dim, int outer_dim);
+
+/* Status of the last drop-in call on this thread (IHIP_OK or negative). */
+int ihip_last_status(void);
+/* Drop every cached device weight copy. */
+void ihip_weight_cache_clear(void);
+
+/* ======================================================================
+ * 2. Device-pointer API (status-returning, explicit stream).
+ * ====================================================================== */
+
+/* Y[M x N] (row-major, token-major) = X[M x K] * W^T for GGUF weight W
+ * [N rows x K] resident on the device. M in 1..64; K a multiple of the
+ * block size (256 for K-quants, 32 for Q8_0); x, w and ws 16-byte aligned.
+ * ws: caller-owned device workspace of at least ihip_gemm_q_ws_bytes()
+ * bytes, holding the prepared activations and the split-K
+ * partials; calls that overlap in time need separate workspaces. The result
+ * is deterministic (no floating-point atomics).
+ * Batched form of q*_gemv (src/kernels/quant_kernels.c:602-697) over the
+ * M verify tokens that forward_cpu! streams one at a time
+ * (src/ModelCPU.jl:970-980). */
+int ihip_gemm_q_ws_bytes(int qtype, int M, int N, int K, int flags,
+                         size_t *bytes);
+int ihip_gemm_q(int qtype, const void *w_dev, const float *x_dev, float *y_dev,
+                int M, int N, int K, int flags, void *ws, size_t ws_bytes,
+                void *stream);
+
+/* Bit-exact dequantization of n_elems weights (a multiple of the block
+ * size) to fp32: the dequantize_*_block! formulas of
+ * src/QuantsCPU.jl:491-658. */
+int ihip_dequant(int qtype, const void *w_dev, float *out_dev, int64_t n_elems,
+                 void *stream);
+
+/* RMSNorm of rows x n fp32 values (src/ModelCPU.jl:110-122); w_dev may be
+ * NULL (unit weight). In place allowed. */
+int ihip_rmsnorm(const float *x_dev, const float *w_dev, float *out_dev,
+                 int rows, int n, float eps, void *stream);
+
+/* ---- LM-head softmax statistics and speculative acceptance ---- */
+
+/* Per row r of logits [rows x V]: zmax[r] = max_j L[r,j]/T and
+ * zsum[r] = sum_j exp(L[r,j]/T - zmax[r]) (the softmax of
+ * src/ModelCPU.jl:1130-1148 and src/SpeculativeDecoding.jl:79-80). */
+int ihip_accept_ws_bytes(int rows, int V, size_t *bytes);
+int ihip_softmax_stats(const float *logits_dev, int rows, int V, float T,
+                       float *zmax_dev, float *zsum_dev, void *ws,
+                       size_t ws_bytes, void *stream);
+
+/* Rejection-sampling verify for `steps` independent verify steps
+ * (speculate_and_verify, src/SpeculativeDecoding.jl:37-107, accept loop
+ * :75-104). Per step s (all arrays device-resident, step-major):
+ *   tgt  [(k+1) x V] target logits, drf [k x V] draft logits,
+ *   draft_tok [k] 0-based draft ids, u_acc [k], u_res [1], u_bonus [1].
+ * mode 0 = standard (p, q at temperature T; residual max(0, p - q)),
+ * mode 1 = reference-compatible (T = 1 ratio with a scalar draft
+ * probability and scalar residual, src/SpeculativeDecoding.jl:61-63,79-93).
+ * out_tok [k+1] receives the accepted drafts followed by the resampled or
+ * bonus token; out_n [1] the number of accepted drafts (0..k). T must be
+ * > 0 (use ihip_greedy_verify for T = 0). */
+int ihip_spec_accept_ws_bytes(int steps, int k, int V, size_t *bytes);
+int ihip_spec_accept(const float *tgt_dev, const float *drf_dev,
+                     const int32_t *draft_tok_dev, int steps, int k, int V,
+                     float T, const float *u_acc_dev, const float *u_res_dev,
+                     const float *u_bonus_dev, int mode, int32_t *out_tok_dev,
+                     int32_t *out_n_dev, void *ws, size_t ws_bytes,
+                     void *stream);
+
+/* Greedy verify (mtp_verify_step!, src/ModelCPU.jl:1914-1930): per step,
+ * logits [(k+1) x V]; out_argmax [k+1] = first-index argmax of each row;
+ * out_n = leading i < k with out_argmax[i] == draft_tok[i]. */
+int ihip_greedy_verify(const float *logits_dev, const int32_t *draft_tok_dev,
+                       int steps, int k, int V, int32_t *out_n_dev,
+                       int32_t *out_argmax_dev, void *ws, size_t ws_bytes,
+                       void *stream);
+
+/* Tree accept walk over n draft-tree nodes (node 0 = root, parent[i] < i),
+ * no counterpart in the reference (it has no tree speculation): node i is
+ * accepted iff its parent is accepted and
+ * u[i] < min(1, p_parent[tok[i]] / q_parent[tok[i]]), p and q the target and
+ * draft softmax at T of the parent's rows. out_path [n] receives the root..
+ * deepest accepted node (ties -> smallest node index); out_len [1] its
+ * length. */
+int ihip_tree_accept(const float *tgt_dev, const float *drf_dev,
+                     const int32_t *tok_dev, const int32_t *parent_dev, int n,
+                     int V, float T, const float *u_dev, int32_t *out_path_dev,
+                     int32_t *out_len_dev, void *ws, size_t ws_bytes,
+                     void *stream);
+
+/* ---- synthetic inputs (benchmark and tests; see csrc/synth.hip) ---- */
+
+/* n_blocks seeded GGUF blocks of qtype starting at block first_block of
+ * the given 64-bit stream (byte-identical to the Python generator). */
+int ihip_synth_blocks(int qtype, uint64_t stream, int64_t first_block,
+                      int64_t n_blocks, void *out_dev, void *stream_handle);
+/* n fp32 N(0,1) samples * scale + (add_dev ? add_dev[i] : 0). */
+int ihip_synth_gaussian(uint64_t stream, int64_t n, float scale,
+                        const float *add_dev, float *out_dev,
+                        void *stream_handle);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* INFERNO_HIP_H */

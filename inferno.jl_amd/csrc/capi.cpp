@@ -1,0 +1,361 @@
+// C ABI of libinferno_hip (declared in include/inferno_hip.h).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+
+#include "../../include/inferno_hip.h"
+
+// kernels (gemm.hip, dequant.hip, accept.hip, misc.hip)
+hipError_t launch_gemm(int qt, const void *W, const float *X, float *Y, int M, int N, int K, int flags, void *ws,
+                       hipStream_t st);
+size_t gemm_ws_bytes(int qt, int M, int N, int K, int flags);
+hipError_t launch_dequant(int qt, const void *w, float *out, int64_t n_blocks, hipStream_t st);
+int accept_nchunk(int V);
+hipError_t launch_stats(const float *L, int rows, int V, float T, float T_last, int period, float2 *part,
+                        hipStream_t st);
+hipError_t launch_stats_merge(const float2 *part, int rows, int V, float *zmax, float *zsum, hipStream_t st);
+hipError_t launch_spec_accept(const float *tgt, const float *drf, const int32_t *draft_tok, int steps, int k,
+                              int V, float T, const float *u_acc, const float *u_res, const float *u_bonus,
+                              int mode, int32_t *out_tok, int32_t *out_n, float2 *part, hipStream_t st);
+hipError_t launch_argmax_partial(const float *L, int rows, int V, float2 *part, hipStream_t st);
+hipError_t launch_greedy(const float2 *part, int V, const int32_t *draft_tok, int steps, int k, int32_t *out_n,
+                         int32_t *out_argmax, hipStream_t st);
+hipError_t launch_tree(const float *tgt, const float *drf, const int32_t *tok, const int32_t *parent, int n, int V,
+                       float T, const float *u, float2 *part, int32_t *out_path, int32_t *out_len, int32_t *wsi,
+                       hipStream_t st);
+hipError_t launch_rmsnorm(const float *x, const float *w, float *out, int rows, int n, float eps, hipStream_t st);
+hipError_t launch_synth(int qt, uint64_t stream, int64_t first, int64_t nblk, void *out, hipStream_t st);
+hipError_t launch_gaussian(uint64_t stream, int64_t n, float scale, const float *add, float *out, hipStream_t st);
+
+namespace {
+
+thread_local std::string t_err;
+thread_local int t_status = IHIP_OK;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    t_err = buf;
+    t_status = code;
+    return code;
+}
+
+int ok() {
+    t_err.clear();
+    t_status = IHIP_OK;
+    return IHIP_OK;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(IHIP_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+inline hipStream_t S(void *s) { return (hipStream_t)s; }
+
+bool is_qtype(int qt) { return qt == IHIP_Q4_K || qt == IHIP_Q5_K || qt == IHIP_Q6_K || qt == IHIP_Q8_0; }
+int block_elems(int qt) { return qt == IHIP_Q8_0 ? 32 : 256; }
+int block_bytes(int qt) {
+    return qt == IHIP_Q4_K ? 144 : qt == IHIP_Q5_K ? 176 : qt == IHIP_Q6_K ? 210 : 34;
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+int check_gemm_shape(int qt, int M, int N, int K, int flags) {
+    if (!is_qtype(qt)) return fail(IHIP_EINVAL, "ihip_gemm_q: unsupported qtype %d", qt);
+    if (M < 1 || M > 64) return fail(IHIP_EINVAL, "ihip_gemm_q: M=%d outside 1..64", M);
+    if (N < 1) return fail(IHIP_EINVAL, "ihip_gemm_q: N=%d", N);
+    if (K < 1 || K % block_elems(qt))
+        return fail(IHIP_EINVAL, "ihip_gemm_q: K=%d is not a positive multiple of %d", K, block_elems(qt));
+    if ((flags & ~7) || ((flags & 3) == 3)) return fail(IHIP_EINVAL, "ihip_gemm_q: bad flags 0x%x", flags);
+    return IHIP_OK;
+}
+
+int check_gemm(int qt, const void *w, const float *x, float *y, int M, int N, int K, int flags) {
+    if (!w || !x || !y) return fail(IHIP_EFAULT, "ihip_gemm_q: NULL pointer");
+    const int rc = check_gemm_shape(qt, M, N, K, flags);
+    if (rc != IHIP_OK) return rc;
+    if (!aligned16(x)) return fail(IHIP_EINVAL, "ihip_gemm_q: x must be 16-byte aligned");
+    if (!aligned16(w)) return fail(IHIP_EINVAL, "ihip_gemm_q: weights must be 16-byte aligned");
+    return IHIP_OK;
+}
+
+// ---- library state for the host-pointer drop-ins ----
+struct Lib {
+    std::mutex mu;
+    bool inited = false;
+    int init_status = IHIP_ENODEV;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::map<std::pair<const void *, size_t>, void *> wcache;
+    float *dx = nullptr, *dy = nullptr, *dws = nullptr;
+    size_t dx_cap = 0, dy_cap = 0, dws_cap = 0;
+};
+Lib &lib() {
+    static Lib L;
+    return L;
+}
+
+bool disabled_by_env() {
+    const char *v = getenv("INFERNO_NO_QUANT_KERNELS");
+    return v && strcmp(v, "0") != 0;
+}
+
+int init_locked(Lib &L, int device) {
+    if (L.inited) return L.init_status;
+    L.inited = true;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= device || device < 0)
+        return L.init_status = fail(IHIP_ENODEV, "ihip_init: no HIP device %d (%d found)", device, n);
+    hipDeviceProp_t prop;
+    if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess) return L.init_status = hip_fail(e, "ihip_init");
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return L.init_status = fail(IHIP_ENODEV, "ihip_init: device %d is %s, not gfx950", device, prop.gcnArchName);
+    if ((e = hipSetDevice(device)) != hipSuccess) return L.init_status = hip_fail(e, "ihip_init");
+    if ((e = hipStreamCreateWithFlags(&L.stream, hipStreamNonBlocking)) != hipSuccess)
+        return L.init_status = hip_fail(e, "ihip_init");
+    L.device = device;
+    return L.init_status = IHIP_OK;
+}
+
+int grow(float **p, size_t *cap, size_t bytes) {
+    if (*cap >= bytes) return IHIP_OK;
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    hipError_t e = hipMalloc((void **)p, bytes);
+    if (e != hipSuccess) return hip_fail(e, "drop-in buffer");
+    *cap = bytes;
+    return IHIP_OK;
+}
+
+// Drop-in GEMV: host pointers, synchronous on the library stream.
+void dropin_gemv(const char *name, int qt, const uint8_t *weight, const float *x, float *out, int K, int N) {
+    Lib &L = lib();
+    std::lock_guard<std::mutex> lk(L.mu);
+    int rc;
+    if (disabled_by_env()) {
+        rc = fail(IHIP_ENODEV, "%s: disabled by INFERNO_NO_QUANT_KERNELS", name);
+    } else if ((rc = init_locked(L, 0)) != IHIP_OK) {
+        // message already set
+    } else if (!weight || !x || !out) {
+        rc = fail(IHIP_EFAULT, "%s: NULL pointer", name);
+    } else if (K < 1 || K % block_elems(qt) || N < 1) {
+        rc = fail(IHIP_EINVAL, "%s: inner_dim=%d outer_dim=%d (inner_dim must be a positive multiple of %d)",
+                  name, K, N, block_elems(qt));
+    } else {
+        (void)hipSetDevice(L.device);
+        const size_t wbytes = (size_t)N * (K / block_elems(qt)) * block_bytes(qt);
+        auto key = std::make_pair((const void *)weight, wbytes);
+        void *dw = nullptr;
+        auto it = L.wcache.find(key);
+        hipError_t e = hipSuccess;
+        if (it != L.wcache.end()) {
+            dw = it->second;
+        } else {
+            e = hipMalloc(&dw, wbytes);
+            if (e == hipSuccess) e = hipMemcpy(dw, weight, wbytes, hipMemcpyHostToDevice);
+            if (e == hipSuccess) L.wcache[key] = dw;
+            else if (dw) (void)hipFree(dw);
+        }
+        if (e != hipSuccess) {
+            rc = hip_fail(e, name);
+        } else if ((rc = grow(&L.dx, &L.dx_cap, (size_t)K * 4)) == IHIP_OK &&
+                   (rc = grow(&L.dy, &L.dy_cap, (size_t)N * 4)) == IHIP_OK &&
+                   (rc = grow(&L.dws, &L.dws_cap, gemm_ws_bytes(qt, 1, N, K, IHIP_GEMM_F32))) == IHIP_OK) {
+            e = hipMemcpyAsync(L.dx, x, (size_t)K * 4, hipMemcpyHostToDevice, L.stream);
+            if (e == hipSuccess) e = launch_gemm(qt, dw, L.dx, L.dy, 1, N, K, IHIP_GEMM_F32, L.dws, L.stream);
+            if (e == hipSuccess) e = hipMemcpyAsync(out, L.dy, (size_t)N * 4, hipMemcpyDeviceToHost, L.stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(L.stream);
+            rc = e == hipSuccess ? ok() : hip_fail(e, name);
+        }
+    }
+    if (rc != IHIP_OK) fprintf(stderr, "inferno_hip: %s\n", t_err.c_str());
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *ihip_last_error(void) { return t_err.c_str(); }
+int ihip_last_status(void) { return t_status; }
+
+int ihip_init(int device) {
+    Lib &L = lib();
+    std::lock_guard<std::mutex> lk(L.mu);
+    const int rc = init_locked(L, device);
+    return rc == IHIP_OK ? ok() : rc;
+}
+
+int ihip_available(void) {
+    if (disabled_by_env()) return 0;
+    return ihip_init(0) == IHIP_OK ? 1 : 0;
+}
+
+void ihip_weight_cache_clear(void) {
+    Lib &L = lib();
+    std::lock_guard<std::mutex> lk(L.mu);
+    for (auto &kv : L.wcache) (void)hipFree(kv.second);
+    L.wcache.clear();
+}
+
+void q4_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_buf, int inner_dim, int outer_dim) {
+    (void)q8_buf;
+    dropin_gemv("q4_k_gemv", IHIP_Q4_K, weight, x, out, inner_dim, outer_dim);
+}
+void q5_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_buf, int inner_dim, int outer_dim) {
+    (void)q8_buf;
+    dropin_gemv("q5_k_gemv", IHIP_Q5_K, weight, x, out, inner_dim, outer_dim);
+}
+void q6_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_buf, int inner_dim, int outer_dim) {
+    (void)q8_buf;
+    dropin_gemv("q6_k_gemv", IHIP_Q6_K, weight, x, out, inner_dim, outer_dim);
+}
+void q8_0_gemv(const uint8_t *weight, const float *x, float *out, int inner_dim, int outer_dim) {
+    dropin_gemv("q8_0_gemv", IHIP_Q8_0, weight, x, out, inner_dim, outer_dim);
+}
+
+int ihip_gemm_q_ws_bytes(int qtype, int M, int N, int K, int flags, size_t *bytes) {
+    if (!bytes) return fail(IHIP_EFAULT, "ihip_gemm_q_ws_bytes: NULL");
+    int rc = check_gemm_shape(qtype, M, N, K, flags);
+    if (rc != IHIP_OK) return rc;
+    *bytes = gemm_ws_bytes(qtype, M, N, K, flags);
+    return ok();
+}
+
+int ihip_gemm_q(int qtype, const void *w_dev, const float *x_dev, float *y_dev, int M, int N, int K, int flags,
+                void *ws, size_t ws_bytes, void *stream) {
+    int rc = check_gemm(qtype, w_dev, x_dev, y_dev, M, N, K, flags);
+    if (rc != IHIP_OK) return rc;
+    const size_t need = gemm_ws_bytes(qtype, M, N, K, flags);
+    if (!ws) return fail(IHIP_EFAULT, "ihip_gemm_q: NULL workspace (%zu bytes needed)", need);
+    if (ws_bytes < need) return fail(IHIP_ENOMEM, "ihip_gemm_q: workspace %zu < %zu bytes", ws_bytes, need);
+    if (!aligned16(ws)) return fail(IHIP_EINVAL, "ihip_gemm_q: workspace must be 16-byte aligned");
+    hipError_t e = launch_gemm(qtype, w_dev, x_dev, y_dev, M, N, K, flags, ws, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_gemm_q");
+}
+
+int ihip_dequant(int qtype, const void *w_dev, float *out_dev, int64_t n_elems, void *stream) {
+    if (!w_dev || !out_dev) return fail(IHIP_EFAULT, "ihip_dequant: NULL pointer");
+    if (!is_qtype(qtype)) return fail(IHIP_EINVAL, "ihip_dequant: unsupported qtype %d", qtype);
+    if (n_elems < 0 || n_elems % block_elems(qtype))
+        return fail(IHIP_EINVAL, "ihip_dequant: n_elems=%lld is not a multiple of %d", (long long)n_elems,
+                    block_elems(qtype));
+    if (((uintptr_t)out_dev & 15) != 0) return fail(IHIP_EINVAL, "ihip_dequant: out must be 16-byte aligned");
+    hipError_t e = launch_dequant(qtype, w_dev, out_dev, n_elems / block_elems(qtype), S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_dequant");
+}
+
+int ihip_rmsnorm(const float *x_dev, const float *w_dev, float *out_dev, int rows, int n, float eps, void *stream) {
+    if (!x_dev || !out_dev) return fail(IHIP_EFAULT, "ihip_rmsnorm: NULL pointer");
+    if (rows < 0 || n < 1) return fail(IHIP_EINVAL, "ihip_rmsnorm: rows=%d n=%d", rows, n);
+    hipError_t e = launch_rmsnorm(x_dev, w_dev, out_dev, rows, n, eps, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_rmsnorm");
+}
+
+int ihip_accept_ws_bytes(int rows, int V, size_t *bytes) {
+    if (!bytes) return fail(IHIP_EFAULT, "ihip_accept_ws_bytes: NULL");
+    if (rows < 0 || V < 1) return fail(IHIP_EINVAL, "ihip_accept_ws_bytes: rows=%d V=%d", rows, V);
+    *bytes = (size_t)rows * accept_nchunk(V) * sizeof(float2) + (size_t)rows * 8 + 256;
+    return ok();
+}
+
+static int need_ws(const char *name, int rows, int V, void *ws, size_t ws_bytes) {
+    size_t need = 0;
+    ihip_accept_ws_bytes(rows, V, &need);
+    if (!ws) return fail(IHIP_EFAULT, "%s: NULL workspace", name);
+    if (ws_bytes < need) return fail(IHIP_ENOMEM, "%s: workspace %zu < %zu bytes", name, ws_bytes, need);
+    if (((uintptr_t)ws & 15) != 0) return fail(IHIP_EINVAL, "%s: workspace must be 16-byte aligned", name);
+    return IHIP_OK;
+}
+
+int ihip_softmax_stats(const float *logits_dev, int rows, int V, float T, float *zmax_dev, float *zsum_dev,
+                       void *ws, size_t ws_bytes, void *stream) {
+    if (!logits_dev || !zmax_dev || !zsum_dev) return fail(IHIP_EFAULT, "ihip_softmax_stats: NULL pointer");
+    if (rows < 1 || V < 1 || !(T > 0.f)) return fail(IHIP_EINVAL, "ihip_softmax_stats: rows=%d V=%d T=%g", rows, V, T);
+    int rc = need_ws("ihip_softmax_stats", rows, V, ws, ws_bytes);
+    if (rc != IHIP_OK) return rc;
+    float2 *part = (float2 *)ws;
+    hipError_t e = launch_stats(logits_dev, rows, V, T, T, 0, part, S(stream));
+    if (e == hipSuccess) e = launch_stats_merge(part, rows, V, zmax_dev, zsum_dev, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_softmax_stats");
+}
+
+int ihip_spec_accept_ws_bytes(int steps, int k, int V, size_t *bytes) {
+    if (steps < 1 || k < 0) return fail(IHIP_EINVAL, "ihip_spec_accept_ws_bytes: steps=%d k=%d", steps, k);
+    return ihip_accept_ws_bytes(steps * (2 * k + 1), V, bytes);
+}
+
+int ihip_spec_accept(const float *tgt_dev, const float *drf_dev, const int32_t *draft_tok_dev, int steps, int k,
+                     int V, float T, const float *u_acc_dev, const float *u_res_dev, const float *u_bonus_dev,
+                     int mode, int32_t *out_tok_dev, int32_t *out_n_dev, void *ws, size_t ws_bytes, void *stream) {
+    if (!tgt_dev || !u_res_dev || !u_bonus_dev || !out_tok_dev || !out_n_dev)
+        return fail(IHIP_EFAULT, "ihip_spec_accept: NULL pointer");
+    if (k > 0 && (!drf_dev || !draft_tok_dev || !u_acc_dev)) return fail(IHIP_EFAULT, "ihip_spec_accept: NULL pointer");
+    if (steps < 1 || k < 0 || V < 1) return fail(IHIP_EINVAL, "ihip_spec_accept: steps=%d k=%d V=%d", steps, k, V);
+    if (!(T > 0.f)) return fail(IHIP_EINVAL, "ihip_spec_accept: T=%g must be > 0 (greedy: ihip_greedy_verify)", T);
+    if (mode != 0 && mode != 1) return fail(IHIP_EINVAL, "ihip_spec_accept: mode=%d", mode);
+    size_t need = 0;
+    ihip_spec_accept_ws_bytes(steps, k, V, &need);
+    if (!ws) return fail(IHIP_EFAULT, "ihip_spec_accept: NULL workspace");
+    if (ws_bytes < need) return fail(IHIP_ENOMEM, "ihip_spec_accept: workspace %zu < %zu bytes", ws_bytes, need);
+    hipError_t e = launch_spec_accept(tgt_dev, drf_dev, draft_tok_dev, steps, k, V, T, u_acc_dev, u_res_dev,
+                                      u_bonus_dev, mode, out_tok_dev, out_n_dev, (float2 *)ws, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_spec_accept");
+}
+
+int ihip_greedy_verify(const float *logits_dev, const int32_t *draft_tok_dev, int steps, int k, int V,
+                       int32_t *out_n_dev, int32_t *out_argmax_dev, void *ws, size_t ws_bytes, void *stream) {
+    if (!logits_dev || !out_n_dev || (k > 0 && !draft_tok_dev)) return fail(IHIP_EFAULT, "ihip_greedy_verify: NULL pointer");
+    if (steps < 1 || k < 0 || V < 1) return fail(IHIP_EINVAL, "ihip_greedy_verify: steps=%d k=%d V=%d", steps, k, V);
+    int rc = need_ws("ihip_greedy_verify", steps * (k + 1), V, ws, ws_bytes);
+    if (rc != IHIP_OK) return rc;
+    float2 *part = (float2 *)ws;
+    hipError_t e = launch_argmax_partial(logits_dev, steps * (k + 1), V, part, S(stream));
+    if (e == hipSuccess) e = launch_greedy(part, V, draft_tok_dev, steps, k, out_n_dev, out_argmax_dev, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_greedy_verify");
+}
+
+int ihip_tree_accept(const float *tgt_dev, const float *drf_dev, const int32_t *tok_dev, const int32_t *parent_dev,
+                     int n, int V, float T, const float *u_dev, int32_t *out_path_dev, int32_t *out_len_dev,
+                     void *ws, size_t ws_bytes, void *stream) {
+    if (!tgt_dev || !drf_dev || !tok_dev || !parent_dev || !u_dev || !out_path_dev || !out_len_dev)
+        return fail(IHIP_EFAULT, "ihip_tree_accept: NULL pointer");
+    if (n < 1 || V < 1 || !(T > 0.f)) return fail(IHIP_EINVAL, "ihip_tree_accept: n=%d V=%d T=%g", n, V, T);
+    int rc = need_ws("ihip_tree_accept", 2 * n, V, ws, ws_bytes);
+    if (rc != IHIP_OK) return rc;
+    float2 *part = (float2 *)ws;
+    int32_t *wsi = (int32_t *)(part + (size_t)2 * n * accept_nchunk(V));
+    hipError_t e = launch_tree(tgt_dev, drf_dev, tok_dev, parent_dev, n, V, T, u_dev, part, out_path_dev,
+                               out_len_dev, wsi, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_tree_accept");
+}
+
+int ihip_synth_blocks(int qtype, uint64_t stream, int64_t first_block, int64_t n_blocks, void *out_dev,
+                      void *stream_handle) {
+    if (!out_dev) return fail(IHIP_EFAULT, "ihip_synth_blocks: NULL pointer");
+    if (!is_qtype(qtype) || n_blocks < 0 || first_block < 0)
+        return fail(IHIP_EINVAL, "ihip_synth_blocks: qtype=%d n_blocks=%lld", qtype, (long long)n_blocks);
+    hipError_t e = launch_synth(qtype, stream, first_block, n_blocks, out_dev, S(stream_handle));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_synth_blocks");
+}
+
+int ihip_synth_gaussian(uint64_t stream, int64_t n, float scale, const float *add_dev, float *out_dev,
+                        void *stream_handle) {
+    if (!out_dev) return fail(IHIP_EFAULT, "ihip_synth_gaussian: NULL pointer");
+    if (n < 0) return fail(IHIP_EINVAL, "ihip_synth_gaussian: n=%lld", (long long)n);
+    hipError_t e = launch_gaussian(stream, n, scale, add_dev, out_dev, S(stream_handle));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_synth_gaussian");
+}
+
+}  // extern "C"

@@ -1,0 +1,21 @@
+"""inferno_hip: MI355X (gfx950) speculative-verify hot path of Inferno.jl.
+
+Host mirror of the reference's QuantizedKernels (quantized GEMV) and
+SpeculativeDecoding (verify / accept) interfaces over the C ABI in
+include/inferno_hip.h, implemented by hand-written HIP kernels in
+lib/libinferno_hip.so. There is no CPU fallback.
+"""
+from . import formats, synth
+from ._lib import HipError, load
+from .quantized_kernels import (GEMM_ACCUM, GEMM_AUTO, GEMM_F32, GEMM_HALF, dequant, gemm_q,
+                                q4_k_gemv_, q5_k_gemv_, q6_k_gemv_, q8_0_gemv_,
+                                quant_kernels_available, rmsnorm)
+from .speculative import (MODE_REFERENCE, MODE_STANDARD, SpeculativeStats, greedy_verify,
+                          mtp_verify_step, softmax_stats, spec_accept, tree_accept)
+
+__all__ = [
+    "formats", "synth", "HipError", "load", "GEMM_ACCUM", "GEMM_AUTO", "GEMM_F32", "GEMM_HALF",
+    "dequant", "gemm_q", "q4_k_gemv_", "q5_k_gemv_", "q6_k_gemv_", "q8_0_gemv_",
+    "quant_kernels_available", "rmsnorm", "MODE_REFERENCE", "MODE_STANDARD", "SpeculativeStats",
+    "greedy_verify", "mtp_verify_step", "softmax_stats", "spec_accept", "tree_accept",
+]

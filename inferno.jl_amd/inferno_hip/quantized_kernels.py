@@ -1,0 +1,154 @@
+"""Host mirror of the reference's QuantizedKernels module
+(src/QuantizedKernels.jl:12-177) over the gfx950 library.
+
+Same names (Julia's `q4_k_gemv!` is `q4_k_gemv_` here), argument order and
+meaning: `out`, `weight_data` (GGUF row-major block bytes), `x`, `inner_dim`
+(K) and `outer_dim` (N); `out[r] = sum_k W[r,k] x[k]`. The reference raises
+`error("Quantized C kernel not available")` when its library is missing
+(src/QuantizedKernels.jl:84); these raise HipError or OSError the same way,
+and there is no CPU fallback. INFERNO_NO_QUANT_KERNELS disables the kernels
+as in the reference (src/QuantizedKernels.jl:26-32).
+
+The device-resident form (`gemm_q`) is the batched path the verify step uses:
+all M verify tokens against one pass over the weights.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from .formats import BLOCK_BYTES, BLOCK_ELEMS, Q4_K, Q5_K, Q6_K, Q8_0, NAMES
+
+GEMM_AUTO, GEMM_F32, GEMM_HALF, GEMM_ACCUM = 0, 1, 2, 4
+
+
+def quant_kernels_available() -> bool:
+    """src/QuantizedKernels.jl:49-50: library present, gfx950 found, not disabled."""
+    try:
+        return bool(_lib.load().ihip_available())
+    except OSError:
+        return False
+
+
+def _host_gemv(sym: str, qtype: int, out, weight_data, x, inner_dim: int, outer_dim: int, with_q8: bool):
+    L = _lib.load()
+    out = np.asarray(out)
+    if out.dtype != np.float32 or not out.flags.c_contiguous or out.size < outer_dim:
+        raise ValueError("out must be a contiguous float32 array of length >= outer_dim")
+    w = np.ascontiguousarray(weight_data, dtype=np.uint8)
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    if xv.size < inner_dim:
+        raise ValueError("x shorter than inner_dim")
+    need = outer_dim * (inner_dim // BLOCK_ELEMS[qtype]) * BLOCK_BYTES[qtype]
+    if inner_dim % BLOCK_ELEMS[qtype] or w.size < need:
+        raise ValueError(f"{NAMES[qtype]} weight: inner_dim={inner_dim} outer_dim={outer_dim} needs {need} bytes")
+    fn = getattr(L, sym)
+    if with_q8:
+        fn(w.ctypes.data, xv.ctypes.data, out.ctypes.data, None, inner_dim, outer_dim)
+    else:
+        fn(w.ctypes.data, xv.ctypes.data, out.ctypes.data, inner_dim, outer_dim)
+    _lib.check(L.ihip_last_status())
+    return out
+
+
+def q4_k_gemv_(out, weight_data, x, inner_dim: int, outer_dim: int):
+    """q4_k_gemv! (src/QuantizedKernels.jl:82-93)."""
+    return _host_gemv("q4_k_gemv", Q4_K, out, weight_data, x, inner_dim, outer_dim, True)
+
+
+def q5_k_gemv_(out, weight_data, x, inner_dim: int, outer_dim: int):
+    """q5_k_gemv! (src/QuantizedKernels.jl:100-111)."""
+    return _host_gemv("q5_k_gemv", Q5_K, out, weight_data, x, inner_dim, outer_dim, True)
+
+
+def q6_k_gemv_(out, weight_data, x, inner_dim: int, outer_dim: int):
+    """q6_k_gemv! (src/QuantizedKernels.jl:119-130)."""
+    return _host_gemv("q6_k_gemv", Q6_K, out, weight_data, x, inner_dim, outer_dim, True)
+
+
+def q8_0_gemv_(out, weight_data, x, inner_dim: int, outer_dim: int):
+    """q8_0_gemv! (src/QuantizedKernels.jl:137-146)."""
+    return _host_gemv("q8_0_gemv", Q8_0, out, weight_data, x, inner_dim, outer_dim, False)
+
+
+GEMV_BY_QTYPE = {Q4_K: q4_k_gemv_, Q5_K: q5_k_gemv_, Q6_K: q6_k_gemv_, Q8_0: q8_0_gemv_}
+
+
+# ---------------------------------------------------------------- device path
+
+def _stream(stream=None) -> int:
+    import torch
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    return getattr(stream, "cuda_stream", stream)
+
+
+def _ptr(t) -> int:
+    return t.data_ptr()
+
+
+def gemm_q(qtype: int, w_dev, x, n: int, k: int, flags: int = GEMM_AUTO, out=None, stream=None, ws=None):
+    """Y[M x N] = X[M x K] W^T for a device-resident GGUF weight (torch
+    uint8 CUDA tensor). x: float32 CUDA tensor [M, K] (M = 1..64). ws: optional
+    caller-owned uint8 CUDA workspace of gemm_ws_bytes() bytes."""
+    import torch
+    if x.dim() == 1:
+        x = x.view(1, -1)
+    if x.dtype != torch.float32 or not x.is_contiguous() or x.shape[1] != k:
+        raise ValueError("x must be a contiguous float32 [M, K] tensor")
+    m = x.shape[0]
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    L = _lib.load()
+    if ws is None:
+        ws = torch.empty(gemm_ws_bytes(qtype, m, n, k, flags), dtype=torch.uint8, device=x.device)
+    _lib.check(L.ihip_gemm_q(qtype, _ptr(w_dev), _ptr(x), _ptr(out), m, n, k, flags, _ptr(ws), ws.numel(),
+                             _stream(stream)))
+    return out
+
+
+def gemm_ws_bytes(qtype: int, m: int, n: int, k: int, flags: int = GEMM_AUTO) -> int:
+    """Workspace bytes ihip_gemm_q needs for this call shape."""
+    nb = C.c_size_t()
+    _lib.check(_lib.load().ihip_gemm_q_ws_bytes(qtype, m, n, k, flags, C.byref(nb)))
+    return max(int(nb.value), 16)
+
+
+def dequant(qtype: int, w_dev, n_elems: int, stream=None):
+    """Bit-exact fp32 dequantization of the first n_elems weights."""
+    import torch
+    out = torch.empty(n_elems, dtype=torch.float32, device=w_dev.device)
+    _lib.check(_lib.load().ihip_dequant(qtype, _ptr(w_dev), _ptr(out), n_elems, _stream(stream)))
+    return out
+
+
+def rmsnorm(x, eps: float = 1e-6, weight=None, out=None, stream=None):
+    """src/ModelCPU.jl:110-122 per row of x [rows, n]."""
+    import torch
+    if x.dim() == 1:
+        x = x.view(1, -1)
+    out = torch.empty_like(x) if out is None else out
+    wp = None if weight is None else _ptr(weight)
+    _lib.check(_lib.load().ihip_rmsnorm(_ptr(x), wp, _ptr(out), x.shape[0], x.shape[1], eps, _stream(stream)))
+    return out
+
+
+def synth_blocks(qtype: int, stream_id: int, n_blocks: int, first_block: int = 0, out=None, stream=None):
+    """Seeded GGUF blocks generated on the device (same bytes as synth.blocks)."""
+    import torch
+    if out is None:
+        out = torch.empty(n_blocks * BLOCK_BYTES[qtype], dtype=torch.uint8, device="cuda")
+    _lib.check(_lib.load().ihip_synth_blocks(qtype, C.c_uint64(stream_id), first_block, n_blocks, _ptr(out),
+                                             _stream(stream)))
+    return out
+
+
+def synth_gaussian(stream_id: int, n: int, scale: float = 1.0, add=None, out=None, stream=None):
+    import torch
+    if out is None:
+        out = torch.empty(n, dtype=torch.float32, device="cuda")
+    ap = None if add is None else _ptr(add)
+    _lib.check(_lib.load().ihip_synth_gaussian(C.c_uint64(stream_id), n, scale, ap, _ptr(out), _stream(stream)))
+    return out

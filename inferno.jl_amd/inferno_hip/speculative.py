@@ -1,0 +1,148 @@
+"""Host mirror of the reference's verify/accept interface over the gfx950
+library: speculate_and_verify's accept loop (src/SpeculativeDecoding.jl:
+37-107), mtp_verify_step!'s greedy verify (src/ModelCPU.jl:1914-1930), the
+speculative statistics of generate_speculative_cpu
+(src/SpeculativeDecoding.jl:163-171), and a tree-accept walk (no reference
+counterpart).
+
+The reference draws its uniforms from Julia's global RNG inside the loop;
+here they are explicit inputs so that CPU and GPU decide on the same draws.
+Token ids are 0-based (the Julia shim adds 1).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+from . import _lib
+from .quantized_kernels import _ptr, _stream
+
+MODE_STANDARD = 0   # p, q at temperature T; residual max(0, p - q)
+MODE_REFERENCE = 1  # src/SpeculativeDecoding.jl:61-63,79-93 as written
+
+
+def _ws(nbytes: int, device):
+    import torch
+    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+
+
+def softmax_stats(logits, temperature: float, stream=None):
+    """(zmax, zsum) per row of logits [rows, V] for z = logits / T."""
+    import torch
+    import ctypes as C
+    rows, V = logits.shape
+    L = _lib.load()
+    nb = C.c_size_t()
+    _lib.check(L.ihip_accept_ws_bytes(rows, V, C.byref(nb)))
+    ws = _ws(nb.value, logits.device)
+    zmax = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    zsum = torch.empty_like(zmax)
+    _lib.check(L.ihip_softmax_stats(_ptr(logits), rows, V, temperature, _ptr(zmax), _ptr(zsum), _ptr(ws),
+                                    ws.numel(), _stream(stream)))
+    return zmax, zsum
+
+
+def spec_accept(target_logits, draft_logits, draft_tokens, temperature: float, u_acc, u_res, u_bonus,
+                mode: int = MODE_STANDARD, stream=None):
+    """Batched accept step.
+
+    target_logits [S, k+1, V], draft_logits [S, k, V], draft_tokens [S, k]
+    int32, u_acc [S, k], u_res [S], u_bonus [S] (float32, CUDA).
+    Returns (out_tok [S, k+1] int32, out_n [S] int32): the accepted drafts
+    followed by the resampled or bonus token at index out_n.
+    """
+    import torch
+    import ctypes as C
+    if target_logits.dim() == 2:
+        target_logits = target_logits.unsqueeze(0)
+        draft_logits = draft_logits.unsqueeze(0)
+        draft_tokens = draft_tokens.view(1, -1)
+        u_acc = u_acc.view(1, -1)
+        u_res = u_res.view(1)
+        u_bonus = u_bonus.view(1)
+    S, k1, V = target_logits.shape
+    k = k1 - 1
+    L = _lib.load()
+    nb = C.c_size_t()
+    _lib.check(L.ihip_spec_accept_ws_bytes(S, k, V, C.byref(nb)))
+    dev = target_logits.device
+    ws = _ws(nb.value, dev)
+    out_tok = torch.zeros((S, k + 1), dtype=torch.int32, device=dev)
+    out_n = torch.zeros(S, dtype=torch.int32, device=dev)
+    for t in (target_logits, draft_logits, draft_tokens, u_acc, u_res, u_bonus):
+        if not t.is_contiguous():
+            raise ValueError("inputs must be contiguous")
+    _lib.check(L.ihip_spec_accept(_ptr(target_logits), _ptr(draft_logits), _ptr(draft_tokens), S, k, V,
+                                  temperature, _ptr(u_acc), _ptr(u_res), _ptr(u_bonus), mode, _ptr(out_tok),
+                                  _ptr(out_n), _ptr(ws), ws.numel(), _stream(stream)))
+    return out_tok, out_n
+
+
+def greedy_verify(logits, draft_tokens, stream=None):
+    """logits [S, k+1, V], draft_tokens [S, k] -> (out_n [S], argmax [S, k+1])."""
+    import torch
+    import ctypes as C
+    if logits.dim() == 2:
+        logits = logits.unsqueeze(0)
+        draft_tokens = draft_tokens.view(1, -1)
+    S, k1, V = logits.shape
+    k = k1 - 1
+    L = _lib.load()
+    nb = C.c_size_t()
+    _lib.check(L.ihip_accept_ws_bytes(S * k1, V, C.byref(nb)))
+    ws = _ws(nb.value, logits.device)
+    out_n = torch.zeros(S, dtype=torch.int32, device=logits.device)
+    am = torch.zeros((S, k1), dtype=torch.int32, device=logits.device)
+    _lib.check(L.ihip_greedy_verify(_ptr(logits), _ptr(draft_tokens) if k else None, S, k, V, _ptr(out_n),
+                                    _ptr(am), _ptr(ws), ws.numel(), _stream(stream)))
+    return out_n, am
+
+
+def mtp_verify_step(logits, draft_tokens, stream=None):
+    """mtp_verify_step! (src/ModelCPU.jl:1914-1930) given the full logits of
+    the verify forward: rows 0..k for tokens [last, d_1..d_k]; draft_tokens
+    are d_1..d_k. Returns (accepted_count, logits)."""
+    n, _ = greedy_verify(logits, draft_tokens, stream)
+    return int(n[0].item()), logits
+
+
+def tree_accept(target_logits, draft_logits, node_tokens, parent, temperature: float, u, stream=None):
+    """Longest accepted root-to-leaf path of a draft tree (node 0 = root)."""
+    import torch
+    import ctypes as C
+    n, V = target_logits.shape
+    L = _lib.load()
+    nb = C.c_size_t()
+    _lib.check(L.ihip_accept_ws_bytes(2 * n, V, C.byref(nb)))
+    ws = _ws(nb.value, target_logits.device)
+    path = torch.zeros(n, dtype=torch.int32, device=target_logits.device)
+    ln = torch.zeros(1, dtype=torch.int32, device=target_logits.device)
+    _lib.check(L.ihip_tree_accept(_ptr(target_logits), _ptr(draft_logits), _ptr(node_tokens), _ptr(parent), n, V,
+                                  temperature, _ptr(u), _ptr(path), _ptr(ln), _ptr(ws), ws.numel(),
+                                  _stream(stream)))
+    return path[: int(ln.item())]
+
+
+@dataclass
+class SpeculativeStats:
+    """The statistics dict of generate_speculative_cpu
+    (src/SpeculativeDecoding.jl:163-171)."""
+    gamma: int
+    draft_tokens_generated: int = 0
+    tokens_accepted: int = 0
+    tokens_generated: int = 0
+    prompt_len: int = 0
+
+    def record(self, n_out_tokens: int) -> None:
+        # the reference counts every returned token (accepted drafts plus the
+        # resampled or bonus token) as "accepted" (:156)
+        self.draft_tokens_generated += self.gamma
+        self.tokens_accepted += n_out_tokens
+        self.tokens_generated += n_out_tokens
+
+    def as_dict(self) -> dict:
+        rate = self.tokens_accepted / self.draft_tokens_generated if self.draft_tokens_generated else 0.0
+        speedup = ((self.tokens_generated - self.prompt_len) /
+                   (self.draft_tokens_generated + self.tokens_generated) * (1 + self.gamma)
+                   if (self.draft_tokens_generated + self.tokens_generated) else 0.0)
+        return {"acceptance_rate": rate, "draft_tokens_generated": self.draft_tokens_generated,
+                "tokens_accepted": self.tokens_accepted, "speedup_estimate": speedup}

@@ -1,0 +1,202 @@
+"""ctypes bindings for the CPU oracle and the reference kernel built in _ref/.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py. The product path never imports this module.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libquant_kernels_ref.so")
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+
+
+def build(ref: bool = False) -> None:
+    targets = ["all"] + (["ref"] if ref else [])
+    subprocess.run(["make", "-s", "-C", HERE] + targets, check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        L.orc_fp16_to_fp32.restype = C.c_float
+        L.orc_fp16_to_fp32.argtypes = [C.c_uint16]
+        L.orc_dequant.argtypes = [C.c_int, _u8p, C.c_int64, _f32p]
+        L.orc_gemv_f64.argtypes = [C.c_int, _u8p, _f32p, _f64p, C.c_int, C.c_int, C.c_int]
+        L.orc_gemv_seq_f32.argtypes = [C.c_int, _u8p, _f32p, _f32p, C.c_int, C.c_int, C.c_int]
+        L.orc_quantize_q8_K.argtypes = [_f32p, _u8p, C.c_int64]
+        for n in ("orc_vec_dot_q4_K_q8_K", "orc_vec_dot_q5_K_q8_K", "orc_vec_dot_q6_K_q8_K"):
+            getattr(L, n).restype = C.c_float
+            getattr(L, n).argtypes = [_u8p, _u8p, C.c_int]
+        L.orc_gemv_q8k.argtypes = [C.c_int, _u8p, _f32p, _f32p, _u8p, C.c_int, C.c_int, C.c_int]
+        L.orc_softmax_stats.argtypes = [_f32p, C.c_int, C.c_float,
+                                        C.POINTER(C.c_double), C.POINTER(C.c_double)]
+        L.orc_argmax_first.restype = C.c_int32
+        L.orc_argmax_first.argtypes = [_f32p, C.c_int]
+        L.orc_spec_accept.argtypes = [_f32p, _f32p, _i32p, C.c_int, C.c_int, C.c_float, _f32p,
+                                      C.c_float, C.c_float, C.c_int, _i32p, C.POINTER(C.c_int32)]
+        L.orc_greedy_verify.argtypes = [_f32p, _i32p, C.c_int, C.c_int,
+                                        C.POINTER(C.c_int32), _i32p]
+        L.orc_tree_accept.argtypes = [_f32p, _f32p, _i32p, _i32p, C.c_int, C.c_int, C.c_float,
+                                      _f32p, _i32p, C.POINTER(C.c_int32)]
+        L.orc_rmsnorm.argtypes = [_f32p, C.c_void_p, C.c_int, C.c_float, _f32p]
+        _lib = L
+    return _lib
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def dequant(qtype: int, data: np.ndarray, n_blocks: int, block_elems: int) -> np.ndarray:
+    out = np.empty(n_blocks * block_elems, dtype=np.float32)
+    rc = lib().orc_dequant(qtype, _c(data, np.uint8), n_blocks, out)
+    assert rc == 0, rc
+    return out
+
+
+def gemv_f64(qtype, w, x, M, N, K) -> np.ndarray:
+    y = np.empty(M * N, dtype=np.float64)
+    rc = lib().orc_gemv_f64(qtype, _c(w, np.uint8), _c(x, np.float32), y, M, N, K)
+    assert rc == 0, rc
+    return y.reshape(M, N)
+
+
+def gemv_seq_f32(qtype, w, x, M, N, K) -> np.ndarray:
+    y = np.empty(M * N, dtype=np.float32)
+    rc = lib().orc_gemv_seq_f32(qtype, _c(w, np.uint8), _c(x, np.float32), y, M, N, K)
+    assert rc == 0, rc
+    return y.reshape(M, N)
+
+
+def quantize_q8_K(x: np.ndarray) -> np.ndarray:
+    x = _c(x, np.float32)
+    q8 = np.zeros((x.size // 256) * 292, dtype=np.uint8)
+    lib().orc_quantize_q8_K(x, q8, x.size)
+    return q8
+
+
+def gemv_q8k(qtype, w, x, K, N, nthreads=1) -> np.ndarray:
+    out = np.empty(N, dtype=np.float32)
+    q8 = np.zeros(max(1, K // 256) * 292, dtype=np.uint8)
+    rc = lib().orc_gemv_q8k(qtype, _c(w, np.uint8), _c(x, np.float32), out, q8, K, N, nthreads)
+    assert rc == 0, rc
+    return out
+
+
+def softmax_stats(L: np.ndarray, T: float):
+    m, s = C.c_double(), C.c_double()
+    L = _c(L, np.float32)
+    lib().orc_softmax_stats(L, L.size, T, C.byref(m), C.byref(s))
+    return m.value, s.value
+
+
+def argmax_first(L: np.ndarray) -> int:
+    L = _c(L, np.float32)
+    return int(lib().orc_argmax_first(L, L.size))
+
+
+def spec_accept(Lt, Ld, draft, T, u_acc, u_res, u_bonus, mode=0):
+    Lt = _c(Lt, np.float32)
+    k, V = Lt.shape[0] - 1, Lt.shape[1]
+    Ld = _c(Ld, np.float32).reshape(max(k, 1) if k else 1, -1) if k else np.zeros((1, V), np.float32)
+    out = np.zeros(k + 1, dtype=np.int32)
+    n = C.c_int32()
+    ua = _c(u_acc if k else np.zeros(1), np.float32)
+    dr = _c(draft if k else np.zeros(1), np.int32)
+    rc = lib().orc_spec_accept(Lt, _c(Ld, np.float32), dr, k, V, T, ua, u_res, u_bonus, mode,
+                               out, C.byref(n))
+    assert rc == 0, rc
+    return out[: n.value + 1].copy(), n.value
+
+
+def greedy_verify(logits, draft):
+    logits = _c(logits, np.float32)
+    k, V = logits.shape[0] - 1, logits.shape[1]
+    n = C.c_int32()
+    am = np.zeros(k + 1, dtype=np.int32)
+    dr = _c(draft if k else np.zeros(1), np.int32)
+    rc = lib().orc_greedy_verify(logits, dr, k, V, C.byref(n), am)
+    assert rc == 0, rc
+    return n.value, am
+
+
+def tree_accept(Lt, Ld, tok, parent, T, u):
+    Lt = _c(Lt, np.float32)
+    n, V = Lt.shape
+    path = np.zeros(n, dtype=np.int32)
+    ln = C.c_int32()
+    rc = lib().orc_tree_accept(Lt, _c(Ld, np.float32), _c(tok, np.int32), _c(parent, np.int32),
+                               n, V, T, _c(u, np.float32), path, C.byref(ln))
+    assert rc == 0, rc
+    return path[: ln.value].copy()
+
+
+def rmsnorm(x, eps=1e-6, w=None):
+    x = _c(x, np.float32)
+    out = np.empty_like(x)
+    wp = None if w is None else _c(w, np.float32)
+    lib().orc_rmsnorm(x, None if wp is None else wp.ctypes.data, x.size, eps, out)
+    return out
+
+
+# ---- the reference's own C kernel, built from its source into _ref/ ----
+
+_ref = None
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_PATH)
+
+
+def ref():
+    """Reference src/kernels/quant_kernels.c (signatures at lines 166, 602-697)."""
+    global _ref
+    if _ref is None:
+        R = C.CDLL(REF_PATH)
+        for n in ("q4_k_gemv", "q5_k_gemv", "q6_k_gemv"):
+            getattr(R, n).restype = None
+            getattr(R, n).argtypes = [_u8p, _f32p, _f32p, _u8p, C.c_int, C.c_int]
+        R.q8_0_gemv.restype = None
+        R.q8_0_gemv.argtypes = [_u8p, _f32p, _f32p, C.c_int, C.c_int]
+        R.quantize_row_q8_K.restype = None
+        R.quantize_row_q8_K.argtypes = [_f32p, _u8p, C.c_int64]
+        _ref = R
+    return _ref
+
+
+def ref_gemv(qtype: int, w: np.ndarray, x: np.ndarray, K: int, N: int) -> np.ndarray:
+    R = ref()
+    out = np.empty(N, dtype=np.float32)
+    w = _c(w, np.uint8)
+    x = _c(x, np.float32)
+    if qtype == 8:
+        R.q8_0_gemv(w, x, out, K, N)
+    else:
+        q8 = np.zeros((K // 256) * 292, dtype=np.uint8)
+        fn = {12: R.q4_k_gemv, 13: R.q5_k_gemv, 14: R.q6_k_gemv}[qtype]
+        fn(w, x, out, q8, K, N)
+    return out
+
+
+def ref_quantize_q8_K(x: np.ndarray) -> np.ndarray:
+    x = _c(x, np.float32)
+    q8 = np.zeros((x.size // 256) * 292, dtype=np.uint8)
+    ref().quantize_row_q8_K(x, q8, x.size)
+    return q8

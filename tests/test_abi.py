@@ -1,0 +1,94 @@
+"""The C-ABI library: it loads, exports every symbol include/inferno_hip.h
+declares, and its host-side argument checks and failure reporting work
+without a GPU (no compute calls)."""
+import ctypes as C
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "inferno_hip.h")
+LIB = os.path.join(ROOT, "inferno.jl_amd", "lib", "libinferno_hip.so")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        subprocess.run(["make", "-s", "-j8", "-C", os.path.join(ROOT, "inferno.jl_amd")], check=True)
+    from inferno_hip import _lib
+    return _lib.load()
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_ ]*[ *]+([A-Za-z_][A-Za-z0-9_]*)\s*\(", text, re.M)
+    return sorted(set(n for n in names if n not in ("if", "while")))
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    for n in ("q4_k_gemv", "q5_k_gemv", "q6_k_gemv", "q8_0_gemv", "ihip_gemm_q", "ihip_dequant",
+              "ihip_spec_accept", "ihip_greedy_verify", "ihip_tree_accept", "ihip_softmax_stats"):
+        assert n in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", LIB], capture_output=True, text=True, check=True).stdout
+    exported = set(l.split()[-1] for l in out.splitlines() if " T " in l)
+    missing = [n for n in declared_functions() if n not in exported]
+    assert not missing, missing
+    from inferno_hip._lib import SIGNATURES
+    assert set(SIGNATURES) == set(declared_functions())
+
+
+def test_argument_checks_without_gpu(lib):
+    nb = C.c_size_t()
+    assert lib.ihip_gemm_q(12, None, None, None, 1, 1, 256, 0, None, 0, None) == -14
+    buf = (C.c_uint8 * 64)()
+    p = C.addressof(buf)
+    p16 = (p + 15) & ~15
+    assert lib.ihip_gemm_q(99, p16, p16, p16, 1, 1, 256, 0, p16, 16, None) == -22
+    assert lib.ihip_gemm_q(12, p16, p16, p16, 0, 1, 256, 0, p16, 16, None) == -22
+    assert lib.ihip_gemm_q(12, p16, p16, p16, 65, 1, 256, 0, p16, 16, None) == -22
+    assert lib.ihip_gemm_q(12, p16, p16, p16, 1, 1, 300, 0, p16, 16, None) == -22
+    assert lib.ihip_gemm_q(12, p16, p16, p16, 1, 1, 256, 3, p16, 16, None) == -22
+    assert lib.ihip_gemm_q(12, p16 + 4, p16, p16, 1, 1, 256, 0, p16, 16, None) == -22
+    assert b"16-byte aligned" in lib.ihip_last_error()
+    assert lib.ihip_gemm_q(12, p16, p16, p16, 1, 1, 256, 0, None, 0, None) == -14
+    assert lib.ihip_gemm_q(12, p16, p16, p16, 1, 1, 256, 0, p16, 1, None) == -12
+    assert lib.ihip_gemm_q_ws_bytes(8, 1, 10, 96, 0, C.byref(nb)) == 0 and nb.value > 0
+    assert lib.ihip_gemm_q_ws_bytes(12, 1, 10, 96, 0, C.byref(nb)) == -22
+    assert lib.ihip_dequant(14, p16, p16, 100, None) == -22
+    assert lib.ihip_spec_accept(None, None, None, 1, 4, 10, 1.0, None, None, None, 0, None, None, None, 0, None) == -14
+    assert lib.ihip_tree_accept(p16, p16, p16, p16, 4, 10, 0.0, p16, p16, p16, p16, 1 << 20, None) == -22
+
+
+def test_dropin_reports_failure_without_gpu():
+    """With no usable device the drop-in sets ENODEV and prints a message
+    (the reference's library-missing error path), and nothing is written."""
+    code = (
+        "import ctypes as C, numpy as np, sys; sys.path.insert(0, %r);"
+        "from inferno_hip import _lib; L = _lib.load();"
+        "w = np.zeros(144, np.uint8); x = np.zeros(256, np.float32); o = np.full(1, 7.0, np.float32);"
+        "L.q4_k_gemv(w.ctypes.data, x.ctypes.data, o.ctypes.data, None, 256, 1);"
+        "print(L.ihip_last_status(), o[0], L.ihip_available())"
+    ) % os.path.join(ROOT, "inferno.jl_amd")
+    env = dict(os.environ, HIP_VISIBLE_DEVICES="-1" if os.environ.get("HIP_VISIBLE_DEVICES") is None else os.environ["HIP_VISIBLE_DEVICES"])
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=120)
+    status, val, avail = r.stdout.split()
+    if int(avail) == 1:
+        pytest.skip("a GPU is visible")
+    assert int(status) == -19 and float(val) == 7.0
+    assert "inferno_hip:" in r.stderr
+
+
+def test_env_kill_switch():
+    code = ("import sys; sys.path.insert(0, %r); from inferno_hip import _lib; L = _lib.load();"
+            "print(L.ihip_available())") % os.path.join(ROOT, "inferno.jl_amd")
+    env = dict(os.environ, INFERNO_NO_QUANT_KERNELS="1")
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=120)
+    assert r.stdout.strip() == "0"

@@ -1,0 +1,169 @@
+"""GPU parity of the LM-head softmax statistics, rejection-sampling accept,
+greedy verify and tree accept against the CPU oracle, with the same explicit
+uniforms. Bars: accepted lengths identical on >= 99.9 % of steps, greedy
+argmax identical (first index on ties), tree paths identical."""
+import numpy as np
+import pytest
+
+from _util import rel_l2
+
+import oracle as O
+from inferno_hip import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ih():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import inferno_hip
+    assert inferno_hip.quant_kernels_available(), inferno_hip._lib.last_error()
+    return inferno_hip
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _case(rng, S, k, V, noise=1.5, scale=3.0):
+    Lt = (rng.standard_normal((S, k + 1, V)) * scale).astype(np.float32)
+    Ld = (Lt[:, :k, :] + rng.standard_normal((S, k, V)) * noise).astype(np.float32)
+    return Lt, Ld
+
+
+def _draw(L, T, u):
+    """Draft token ~ softmax(L/T) by inverse CDF in fp64 (test-side sampler)."""
+    z = L.astype(np.float64) / T
+    p = np.exp(z - z.max())
+    c = np.cumsum(p)
+    return int(min(np.searchsorted(c, u * c[-1]), L.size - 1))
+
+
+def test_softmax_stats(ih):
+    rng = np.random.default_rng(0)
+    L = (rng.standard_normal((7, 151936)) * 4).astype(np.float32)
+    L[3, :] = -2.0   # uniform row
+    L[4, 17] = 80.0  # one dominant entry
+    for T in (1.0, 0.8):
+        zm, zs = ih.softmax_stats(_dev(L), T)
+        zm, zs = zm.cpu().numpy(), zs.cpu().numpy()
+        for r in range(L.shape[0]):
+            m, s = O.softmax_stats(L[r], T)
+            assert abs(zm[r] - m) <= 1e-6 * max(1.0, abs(m))
+            assert abs(zs[r] - s) <= 2e-5 * s, (r, zs[r], s)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("V,S,T", [(16, 2000, 0.8), (1000, 500, 1.0), (151936, 48, 0.8)])
+def test_spec_accept_parity(ih, mode, V, S, T):
+    k = 4
+    rng = np.random.default_rng(V + S + mode)
+    Lt, Ld = _case(rng, S, k, V, scale=3.0 if V > 100 else 1.0)
+    ud = rng.random((S, k))
+    draft = np.array([[_draw(Ld[s, i], T, ud[s, i]) for i in range(k)] for s in range(S)], dtype=np.int32)
+    u_acc = rng.random((S, k)).astype(np.float32)
+    u_res = rng.random(S).astype(np.float32)
+    u_bon = rng.random(S).astype(np.float32)
+    tok, n = ih.spec_accept(_dev(Lt), _dev(Ld), _dev(draft), T, _dev(u_acc), _dev(u_res), _dev(u_bon), mode=mode)
+    tok, n = tok.cpu().numpy(), n.cpu().numpy()
+    same_len = same_tok = 0
+    for s in range(S):
+        rt, rn = O.spec_accept(Lt[s], Ld[s], draft[s], T, u_acc[s], float(u_res[s]), float(u_bon[s]), mode)
+        same_len += int(rn == n[s])
+        same_tok += int(rn == n[s] and np.array_equal(rt, tok[s, : n[s] + 1]))
+    print(f"mode={mode} V={V} S={S}: lengths {same_len}/{S}, tokens {same_tok}/{S}", flush=True)
+    assert same_len >= 0.999 * S
+    assert same_tok >= 0.999 * S
+
+
+def test_spec_accept_special_cases(ih):
+    V, k = 64, 4
+    rng = np.random.default_rng(5)
+    L = rng.standard_normal((1, k + 1, V)).astype(np.float32)
+    draft = np.array([[3, 9, 27, 50]], dtype=np.int32)
+    ones = np.full((1, k), 0.999, dtype=np.float32)
+    u = np.array([0.5], dtype=np.float32)
+    # q == p: every draft accepted whatever u < 1, then a bonus token
+    tok, n = ih.spec_accept(_dev(L), _dev(L[:, :k].copy()), _dev(draft), 1.0, _dev(ones), _dev(u), _dev(u))
+    assert int(n[0]) == k and tok[0, :k].cpu().numpy().tolist() == draft[0].tolist()
+    # p[x_0] ~ 0: the first draft is rejected and the residual draw avoids x_0
+    L2 = L.copy()
+    L2[0, 0, 3] = -1e4
+    zero = np.zeros((1, k), dtype=np.float32)
+    tok, n = ih.spec_accept(_dev(L2), _dev(L[:, :k].copy()), _dev(draft), 1.0, _dev(zero), _dev(u), _dev(u))
+    assert int(n[0]) == 0 and int(tok[0, 0]) != 3
+    rt, rn = O.spec_accept(L2[0], L[0, :k], draft[0], 1.0, zero[0], 0.5, 0.5, 0)
+    assert rn == 0 and int(rt[0]) == int(tok[0, 0])
+    # k = 0: only a bonus token
+    tok, n = ih.spec_accept(_dev(L[:, :1].copy()), _dev(np.zeros((1, 0, V), np.float32)),
+                            _dev(np.zeros((1, 0), np.int32)), 0.7, _dev(np.zeros((1, 0), np.float32)), _dev(u),
+                            _dev(u))
+    rt, rn = O.spec_accept(L[0, :1], np.zeros((0, V), np.float32), np.zeros(0, np.int32), 0.7,
+                           np.zeros(0, np.float32), 0.5, 0.5, 0)
+    assert int(n[0]) == 0 and int(tok[0, 0]) == int(rt[0])
+
+
+def test_greedy_verify(ih):
+    rng = np.random.default_rng(3)
+    S, k, V = 64, 4, 151936
+    L = rng.standard_normal((S, k + 1, V)).astype(np.float32)
+    am = L.argmax(-1)
+    draft = am[:, :k].astype(np.int32).copy()
+    for s in range(S):  # break the chain at a step-dependent position
+        j = s % (k + 1)
+        if j < k:
+            draft[s, j] = (draft[s, j] + 1) % V
+    # planted ties: equal maxima at two indices, the first must win
+    L[0, 1, 5] = L[0, 1, 77] = 50.0
+    L[1, 0, 151935] = L[1, 0, 4096] = 60.0
+    n, a = ih.greedy_verify(_dev(L), _dev(draft))
+    n, a = n.cpu().numpy(), a.cpu().numpy()
+    for s in range(S):
+        rn, ra = O.greedy_verify(L[s], draft[s])
+        assert rn == n[s] and np.array_equal(ra, a[s]), s
+    assert a[0, 1] == 5 and a[1, 0] == 4096
+
+
+def _tree_parents(n, branching=(4, 4, 4)):
+    par = [-1]
+    frontier = [0]
+    for b in branching:
+        nxt = []
+        for p in frontier:
+            for _ in range(b):
+                if len(par) < n:
+                    par.append(p)
+                    nxt.append(len(par) - 1)
+        frontier = nxt
+    while len(par) < n:
+        par.append(frontier[(len(par)) % len(frontier)] if frontier else 0)
+    par[0] = 0
+    return np.array(par, dtype=np.int32)
+
+
+@pytest.mark.parametrize("V", [32, 151936])
+def test_tree_accept(ih, V):
+    rng = np.random.default_rng(V)
+    n = 64
+    par = _tree_parents(n)
+    trials = 8 if V > 1000 else 64
+    for t in range(trials):
+        Lt = (rng.standard_normal((n, V)) * 2).astype(np.float32)
+        Ld = (Lt + rng.standard_normal((n, V)) * 0.7).astype(np.float32)
+        tok = np.zeros(n, dtype=np.int32)
+        for i in range(1, n):
+            tok[i] = _draw(Ld[par[i]], 1.0, rng.random())
+        u = rng.random(n).astype(np.float32) * 0.9
+        path = ih.tree_accept(_dev(Lt), _dev(Ld), _dev(tok), _dev(par), 1.0, _dev(u)).cpu().numpy()
+        ref = O.tree_accept(Lt, Ld, tok, par, 1.0, u)
+        assert np.array_equal(path, ref), (t, path, ref)
+
+
+def test_rmsnorm(ih):
+    x = np.random.default_rng(1).standard_normal((5, 4096)).astype(np.float32) * 3
+    got = ih.rmsnorm(_dev(x)).cpu().numpy()
+    ref = np.stack([O.rmsnorm(r) for r in x])
+    assert rel_l2(got, ref) <= 1e-6

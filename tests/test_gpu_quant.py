@@ -1,0 +1,163 @@
+"""GPU parity: dequant (bit-exact), device synthesis (byte-exact), fused
+dequant-matmul (rel-L2 1e-5 fp32-accurate / 1e-2 half MFMA) and the host
+drop-in q*_gemv entry points, all against the CPU oracle."""
+import numpy as np
+import pytest
+
+from _util import rel_l2
+
+import oracle as O
+from inferno_hip import formats as F
+from inferno_hip import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-5   # north-star bar for the fp32-accumulate path
+TOL_HALF = 1e-2  # north-star bar for the half-precision MFMA path
+
+
+@pytest.fixture(scope="module")
+def ih():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import inferno_hip
+    assert inferno_hip.quant_kernels_available(), inferno_hip._lib.last_error()
+    return inferno_hip
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _edge_blocks(qt):
+    """Synthetic blocks plus hand-set edge cases of the fp16 scale fields."""
+    bb = F.BLOCK_BYTES[qt]
+    b = synth.blocks(qt, 24, synth.stream_for(7, f"edge{qt}")).reshape(24, bb).copy()
+    d_off = 208 if qt == F.Q6_K else 0
+    specials = [0x0000, 0x8000, 0x0001, 0x03FF, 0x0400, 0x7BFF, 0xC000, 0x7C00, 0x7E00]
+    for i, h in enumerate(specials):
+        b[i, d_off:d_off + 2] = np.array([h & 0xFF, h >> 8], dtype=np.uint8)
+        if qt in (F.Q4_K, F.Q5_K):  # dmin too
+            b[i, 2:4] = np.array([specials[-1 - i] & 0xFF, specials[-1 - i] >> 8], dtype=np.uint8)
+    return b.reshape(-1)
+
+
+@pytest.mark.parametrize("qt", F.QTYPES)
+def test_dequant_bit_exact(ih, qt):
+    data = np.concatenate([_edge_blocks(qt), synth.blocks(qt, 1000, synth.stream_for(3, "dq"))])
+    nblk = data.size // F.BLOCK_BYTES[qt]
+    n = nblk * F.BLOCK_ELEMS[qt]
+    ref = O.dequant(qt, data, nblk, F.BLOCK_ELEMS[qt])
+    got = ih.dequant(qt, _dev(data), n).cpu().numpy()
+    rb, gb = ref.view(np.uint32), got.view(np.uint32)
+    both_nan = np.isnan(ref) & np.isnan(got)
+    bad = (rb != gb) & ~both_nan
+    assert not bad.any(), f"{F.NAMES[qt]}: {bad.sum()} mismatches, first at {np.argmax(bad)}"
+
+
+@pytest.mark.parametrize("qt", F.QTYPES)
+def test_device_synth_matches_host(ih, qt):
+    st = synth.stream_for(11, "w")
+    host = synth.blocks(qt, 777, st, first_block=5)
+    dev = ih.quantized_kernels.synth_blocks(qt, st, 777, first_block=5).cpu().numpy()
+    assert np.array_equal(host, dev)
+
+
+SHAPES = [(40, 256), (128, 512), (200, 2048), (3072, 1024)]
+MS = [1, 2, 3, 5, 8, 9, 16, 33, 64]
+
+
+@pytest.mark.parametrize("qt", F.QTYPES)
+@pytest.mark.parametrize("N,K", SHAPES)
+def test_gemm_fp32_accurate(ih, qt, N, K):
+    rng = np.random.default_rng(N * 7 + K + qt)
+    w = synth.matrix(qt, N, K, synth.stream_for(N + K, f"gemm{qt}"))
+    wd = _dev(w)
+    for M in MS:
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        ref = O.gemv_f64(qt, w, x, M, N, K)
+        got = ih.gemm_q(qt, wd, _dev(x), N, K, flags=ih.GEMM_F32).cpu().numpy()
+        err = rel_l2(got, ref)
+        print(f"{F.NAMES[qt]} N={N} K={K} M={M} f32 rel-L2={err:.3e}", flush=True)
+        assert err <= TOL_F32, (M, err)
+
+
+@pytest.mark.parametrize("qt", F.QTYPES)
+def test_gemm_half_mfma(ih, qt):
+    N, K = 512, 2048
+    rng = np.random.default_rng(qt)
+    w = synth.matrix(qt, N, K, synth.stream_for(5, f"half{qt}"))
+    wd = _dev(w)
+    for M in (1, 7, 16, 17, 40, 64):
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        ref = O.gemv_f64(qt, w, x, M, N, K)
+        got = ih.gemm_q(qt, wd, _dev(x), N, K, flags=ih.GEMM_HALF).cpu().numpy()
+        err = rel_l2(got, ref)
+        print(f"{F.NAMES[qt]} M={M} half rel-L2={err:.3e}", flush=True)
+        assert err <= TOL_HALF, (M, err)
+        auto = ih.gemm_q(qt, wd, _dev(x), N, K).cpu().numpy()
+        assert rel_l2(auto, ref) <= (TOL_F32 if M < 16 else TOL_HALF)
+
+
+def test_gemm_invariants(ih):
+    """Linearity, the M-row result equals M independent M=1 calls, the
+    accumulate flag, and large-magnitude activations (per-token scaling)."""
+    import torch
+    qt, N, K = F.Q4_K, 256, 1024
+    w = synth.matrix(qt, N, K, synth.stream_for(1, "inv"))
+    wd = _dev(w)
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((5, K)).astype(np.float32)
+    y = ih.gemm_q(qt, wd, _dev(x), N, K, flags=ih.GEMM_F32).cpu().numpy().astype(np.float64)
+    for m in range(5):
+        y1 = ih.gemm_q(qt, wd, _dev(x[m:m + 1]), N, K, flags=ih.GEMM_F32).cpu().numpy()[0]
+        assert rel_l2(y1, y[m]) <= 1e-6
+    y2 = ih.gemm_q(qt, wd, _dev(2.0 * x[0:1] + x[1:2]), N, K, flags=ih.GEMM_F32).cpu().numpy()[0]
+    assert rel_l2(y2, 2.0 * y[0] + y[1]) <= 1e-5
+    acc = _dev(np.ones((5, N), dtype=np.float32))
+    ih.gemm_q(qt, wd, _dev(x), N, K, flags=ih.GEMM_F32 | ih.GEMM_ACCUM, out=acc)
+    assert rel_l2(acc.cpu().numpy(), y + 1.0) <= 1e-5
+    big = (x * 3.0e4).astype(np.float32)  # beyond fp16 range before scaling
+    ref = O.gemv_f64(qt, w, big, 5, N, K)
+    got = ih.gemm_q(qt, wd, _dev(big), N, K, flags=ih.GEMM_F32).cpu().numpy()
+    assert rel_l2(got, ref) <= TOL_F32
+    tiny = (x * 1.0e-30).astype(np.float32)
+    ref = O.gemv_f64(qt, w, tiny, 5, N, K)
+    got = ih.gemm_q(qt, wd, _dev(tiny), N, K, flags=ih.GEMM_F32).cpu().numpy()
+    assert rel_l2(got, ref) <= TOL_F32
+    zero = torch.zeros((3, K), dtype=torch.float32, device="cuda")
+    assert float(ih.gemm_q(qt, wd, zero, N, K).abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("qt", F.QTYPES)
+def test_dropin_host_gemv(ih, qt):
+    """The reference-named host entry points (quant_kernels.c:602-697)."""
+    N, K = 300, 1024
+    w = synth.matrix(qt, N, K, synth.stream_for(9, f"dropin{qt}"))
+    x = np.random.default_rng(qt).standard_normal(K).astype(np.float32)
+    out = np.zeros(N, dtype=np.float32)
+    ih.quantized_kernels.GEMV_BY_QTYPE[qt](out, w, x, K, N)
+    ref = O.gemv_f64(qt, w, x, 1, N, K)[0]
+    assert rel_l2(out, ref) <= TOL_F32
+    # second call hits the weight cache and must give the same answer
+    out2 = np.zeros(N, dtype=np.float32)
+    ih.quantized_kernels.GEMV_BY_QTYPE[qt](out2, w, x, K, N)
+    assert np.array_equal(out, out2)
+
+
+def test_errors(ih):
+    import torch
+    from inferno_hip._lib import HipError
+    wd = torch.zeros(144 * 4, dtype=torch.uint8, device="cuda")
+    x = torch.zeros((1, 300), dtype=torch.float32, device="cuda")
+    with pytest.raises(HipError) as e:
+        ih.gemm_q(F.Q4_K, wd, x, 4, 300)
+    assert e.value.status == -22
+    x = torch.zeros((65, 256), dtype=torch.float32, device="cuda")
+    with pytest.raises(HipError):
+        ih.gemm_q(F.Q4_K, wd, x, 4, 256)
+    L = ih.load()
+    assert L.ihip_gemm_q(F.Q4_K, None, None, None, 1, 1, 256, 0, None, 0, None) == -14
+    assert L.ihip_dequant(99, wd.data_ptr(), wd.data_ptr(), 256, None) == -22

@@ -1,0 +1,182 @@
+"""Pins of the CPU oracle's softmax statistics, speculative accept (both
+modes), greedy verify and tree accept (no GPU). Beyond the committed
+fixtures, each function is checked against an independent statement:
+closed forms, brute-force path enumeration, and the defining property of
+standard speculative sampling (the output token is distributed exactly as
+the target distribution p)."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden_v1.npz")
+
+
+def softmax(L, T):
+    z = L.astype(np.float64) / T
+    e = np.exp(z - z.max())
+    return e / e.sum()
+
+
+def test_softmax_stats_closed_forms():
+    for V in (1, 7, 1000):
+        m, s = O.softmax_stats(np.full(V, -3.0, np.float32), 1.0)
+        assert m == -3.0 and s == pytest.approx(V)
+    L = np.zeros(10, np.float32)
+    L[4] = 200.0
+    m, s = O.softmax_stats(L, 0.5)
+    assert m == 400.0 and s == pytest.approx(1.0)
+
+
+def test_argmax_first_index():
+    assert O.argmax_first(np.array([1, 5, 2, 5], np.float32)) == 1
+    assert O.argmax_first(np.array([3, 3, 3], np.float32)) == 0
+    assert O.argmax_first(np.array([42], np.float32)) == 0
+    assert O.argmax_first(np.array([-10, -5, -1], np.float32)) == 2
+
+
+def test_standard_accept_preserves_target_distribution():
+    """Mode 0 with draft x ~ q and independent uniforms must output a token
+    distributed as p (k = 1, first output token)."""
+    rng = np.random.default_rng(7)
+    V = 5
+    Lt = rng.standard_normal((2, V)).astype(np.float32)
+    Ld = rng.standard_normal((1, V)).astype(np.float32)
+    T = 0.8
+    p, q = softmax(Lt[0], T), softmax(Ld[0], T)
+    n = 60000
+    xs = rng.choice(V, size=n, p=q)
+    ua, ur = rng.random(n).astype(np.float32), rng.random(n).astype(np.float32)
+    counts = np.zeros(V)
+    for i in range(n):
+        tok, _ = O.spec_accept(Lt, Ld, np.array([xs[i]], np.int32), T, ua[i:i + 1], float(ur[i]), 0.5, 0)
+        counts[tok[0]] += 1
+    freq = counts / n
+    sigma = np.sqrt(p * (1 - p) / n)
+    assert np.all(np.abs(freq - p) < 5 * sigma + 1e-4), (freq, p)
+
+
+def test_accept_special_cases():
+    rng = np.random.default_rng(3)
+    V, k = 12, 4
+    Lt = rng.standard_normal((k + 1, V)).astype(np.float32)
+    draft = np.array([0, 5, 7, 11], np.int32)
+    # q == p: every draft accepted for any u < 1, then a bonus token
+    tok, n = O.spec_accept(Lt, Lt[:k], draft, 1.0, np.full(k, 0.9999, np.float32), 0.3, 0.6, 0)
+    assert n == k and tok[:k].tolist() == draft.tolist()
+    pk = softmax(Lt[k], 1.0)
+    assert tok[k] == int(np.searchsorted(np.cumsum(pk), 0.6 * pk.sum()))
+    # p[x_0] = 0: rejected at 0, residual never returns x_0 for u > 0 (at
+    # u = 0 the rule u*S <= C_j picks index 0 whatever its weight, as the
+    # reference's `r <= cumsum` does, src/SpeculativeDecoding.jl:21-26)
+    L2 = Lt.copy()
+    L2[0, 0] = -1e30
+    for u in np.linspace(0.001, 0.999, 21):
+        tok, n = O.spec_accept(L2, Lt[:k], draft, 1.0, np.zeros(k, np.float32), float(u), 0.5, 0)
+        assert n == 0 and tok[0] != 0
+    # k = 0: a bonus token only
+    tok, n = O.spec_accept(Lt[:1], np.zeros((0, V), np.float32), np.zeros(0, np.int32), 0.7,
+                           np.zeros(0, np.float32), 0.1, 0.25, 0)
+    p0 = softmax(Lt[0], 0.7)
+    assert n == 0 and tok[0] == int(np.searchsorted(np.cumsum(p0), 0.25))
+
+
+def test_reference_mode_hand_case():
+    """Reference mode (src/SpeculativeDecoding.jl:75-97): T = 1 ratio with
+    scalar q_i, residual max(p - q_i, 0) normalised, first j with u <= cumsum."""
+    Lt = np.log(np.array([[0.5, 0.3, 0.2], [0.2, 0.2, 0.6]], np.float32))
+    Ld = np.log(np.array([[0.1, 0.6, 0.3]], np.float32))
+    # draft token 1: p = 0.3, q = 0.6 -> ratio 0.5
+    tok, n = O.spec_accept(Lt, Ld, np.array([1], np.int32), 2.0, np.array([0.49], np.float32), 0.0, 0.0, 1)
+    assert n == 1  # accepted, bonus drawn at T = 2
+    # reject: residual max(p - 0.6, 0) = [0, 0, 0] -> all-zero -> last index
+    tok, n = O.spec_accept(Lt, Ld, np.array([1], np.int32), 1.0, np.array([0.51], np.float32), 0.5, 0.0, 1)
+    assert n == 0 and tok[0] == 2
+    # draft token 2: p = 0.2, q = 0.3; residual max(p - 0.3, 0) = [0.2, 0, 0] -> token 0
+    tok, n = O.spec_accept(Lt, Ld, np.array([2], np.int32), 1.0, np.array([0.9], np.float32), 0.99, 0.0, 1)
+    assert n == 0 and tok[0] == 0
+    # standard mode on the same input: residual max(p - q, 0) = [0.4, 0, 0] -> token 0
+    tok, n = O.spec_accept(Lt, Ld, np.array([2], np.int32), 1.0, np.array([0.9], np.float32), 0.99, 0.0, 0)
+    assert n == 0 and tok[0] == 0
+
+
+def test_accept_fixtures():
+    g = np.load(GOLD, allow_pickle=False)
+    for mode in (0, 1):
+        for s in range(g["accept_Lt"].shape[0]):
+            tok, n = O.spec_accept(g["accept_Lt"][s], g["accept_Ld"][s], g["accept_draft"][s], 0.8,
+                                   g["accept_ua"][s], float(g["accept_ur"][s]), float(g["accept_ub"][s]), mode)
+            assert n == g[f"accept_mode{mode}_n"][s]
+            assert tok.tolist() == g[f"accept_mode{mode}_tok"][s][: n + 1].tolist()
+
+
+def test_greedy_verify():
+    rng = np.random.default_rng(4)
+    L = rng.standard_normal((5, 30)).astype(np.float32)
+    am = L.argmax(-1)
+    n, a = O.greedy_verify(L, am[:4].astype(np.int32))
+    assert n == 4 and a.tolist() == am.tolist()
+    d = am[:4].astype(np.int32).copy()
+    d[2] = (d[2] + 1) % 30
+    assert O.greedy_verify(L, d)[0] == 2
+    L[0, 3] = L[0, 9] = 99.0
+    assert O.greedy_verify(L, np.array([3, 0, 0, 0], np.int32))[0] == 1
+
+
+def _brute_tree(Lt, Ld, tok, par, T, u):
+    """Independent statement: enumerate every node, accept it iff every edge
+    on its root path passes its ratio test; deepest, then smallest index."""
+    n = len(par)
+    ok = []
+    for i in range(n):
+        path, v = [], i
+        while v != 0:
+            path.append(v)
+            v = par[v]
+        good = True
+        for v in path:
+            p, q = softmax(Lt[par[v]], T)[tok[v]], softmax(Ld[par[v]], T)[tok[v]]
+            good &= bool(u[v] < min(1.0, p / q))
+        ok.append((len(path), -i) if good else (-1, 0))
+    best = max(range(n), key=lambda i: ok[i])
+    path, v = [best], best
+    while v != 0:
+        v = par[v]
+        path.append(v)
+    return path[::-1]
+
+
+def test_tree_accept_brute_force():
+    rng = np.random.default_rng(5)
+    for trial in range(200):
+        n = int(rng.integers(1, 9))
+        V = int(rng.integers(2, 7))
+        par = np.array([0] + [int(rng.integers(0, i)) for i in range(1, n)], np.int32)
+        Lt = rng.standard_normal((n, V)).astype(np.float32)
+        Ld = (Lt + rng.standard_normal((n, V))).astype(np.float32)
+        tok = rng.integers(0, V, n).astype(np.int32)
+        u = rng.random(n).astype(np.float32)
+        got = O.tree_accept(Lt, Ld, tok, par, 1.0, u)
+        assert got.tolist() == _brute_tree(Lt, Ld, tok, par, 1.0, u), trial
+
+
+def test_chain_tree_equals_spec_accept():
+    rng = np.random.default_rng(6)
+    V, k = 20, 6
+    for trial in range(50):
+        Lt = rng.standard_normal((k + 1, V)).astype(np.float32)
+        Ld = (Lt[:k] + rng.standard_normal((k, V))).astype(np.float32)
+        draft = rng.integers(0, V, k).astype(np.int32)
+        u = rng.random(k).astype(np.float32)
+        _, n = O.spec_accept(Lt, Ld, draft, 1.0, u, 0.5, 0.5, 0)
+        # tree node i+1 carries draft i, judged at row i of its parent i
+        par = np.arange(-1, k, dtype=np.int32)
+        par[0] = 0
+        tok = np.concatenate([[0], draft]).astype(np.int32)
+        tLt = np.concatenate([Lt[:k], Lt[k:]], 0)
+        tLd = np.concatenate([Ld, np.zeros((1, V), np.float32)], 0)
+        uu = np.concatenate([[0.0], u]).astype(np.float32)
+        path = O.tree_accept(tLt, tLd, tok, par, 1.0, uu)
+        assert len(path) - 1 == n
