@@ -1,0 +1,366 @@
+#!/usr/bin/env python3
+"""Benchmark of the speculative-verify hot path on one MI355X.
+
+Workload (the metric's verify step): a full
+9B-class verify step at M = 5 (1 accepted + k = 4 draft tokens):
+32 decoder layers of projections, hidden 4096 - Q4_K q (4096x4096),
+k/v (2 x 1024x4096), o (4096x4096), gate/up (2 x 12288x4096) and Q6_K down
+(4096x12288) - chained in fp32 with RMSNorm before q/k/v and gate/up, SiLU
+gating and residual adds, then RMSNorm, the Q6_K lm_head (151936x4096) and
+the k = 4 rejection-sampling accept at T = 0.8. Weights are seeded synthetic
+GGUF blocks (no checkpoint is available offline), resident in HBM; a step is
+replayed from a captured HIP graph. `value` is verify steps per second.
+
+Also reported: `roofline` for the dominant dequant-matmul (the Q4_K
+gate/up projection, 24576x4096 at M = 5, timed live with HIP events over
+cold weights), a dequant-matmul GB/s sweep at M = 1..8, and `cpu_baseline`:
+the reference's own CPU kernels (src/kernels/quant_kernels.c built from
+source into oracle/_ref) called once per token per matrix as forward_cpu!
+does, on a bounded sample of the same step, timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "inferno.jl_amd"))
+
+METRIC = "dequant-matmul GB/s & % HBM peak at M=1..8; verify steps/sec (k=4, 1 GPU)"
+HBM_PEAK_GBPS = 8000.0
+SEED = 0x1F3E0003  # configs[3]
+
+H, NQ, NKV, FF, VOCAB = 4096, 4096, 1024, 12288, 151936
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Model:
+    """Device-resident synthetic weights of the config-4 shape."""
+
+    def __init__(self, ih, n_layers: int):
+        import torch
+        F = ih.formats
+        st = ih.synth.stream_for
+        self.layers = []
+        for L in range(n_layers):
+            def blk(qt, rows, k, name):
+                return ih.quantized_kernels.synth_blocks(qt, st(SEED, f"blk{L}.{name}"),
+                                                         rows * k // F.BLOCK_ELEMS[qt])
+            self.layers.append({
+                "q": blk(F.Q4_K, NQ, H, "attn_q"),
+                "kv": blk(F.Q4_K, 2 * NKV, H, "attn_kv"),     # k rows then v rows
+                "o": blk(F.Q4_K, H, NQ, "attn_output"),
+                "gu": blk(F.Q4_K, 2 * FF, H, "ffn_gate_up"),  # gate rows then up rows
+                "down": blk(F.Q6_K, H, FF, "ffn_down"),
+            })
+        self.lm = ih.quantized_kernels.synth_blocks(F.Q6_K, st(SEED, "output"), VOCAB * H // 256)
+        torch.cuda.synchronize()
+
+    def weight_bytes(self, n_layers: int) -> int:
+        per = sum(t.numel() for t in self.layers[0].values())
+        return per * n_layers + self.lm.numel()
+
+
+class VerifyStep:
+    """One verify step: layers, final norm, lm_head, accept."""
+
+    def __init__(self, ih, model: Model, M: int, k: int, T: float):
+        import torch
+        dev = "cuda"
+        F = ih.formats
+        self.ih, self.model, self.M, self.k, self.T = ih, model, M, k, T
+        st = ih.synth.stream_for
+        self.x0 = ih.quantized_kernels.synth_gaussian(st(SEED, "x0"), M * H).view(M, H)
+        self.x = torch.empty_like(self.x0)
+        self.h = torch.empty_like(self.x0)
+        self.q = torch.empty((M, NQ), device=dev)
+        self.kv = torch.empty((M, 2 * NKV), device=dev)
+        self.gu = torch.empty((M, 2 * FF), device=dev)
+        self.hm = torch.empty((M, FF), device=dev)
+        self.logits = torch.empty((M, VOCAB), device=dev)
+        gws = ih.quantized_kernels.gemm_ws_bytes
+        wsb = max(gws(F.Q4_K, M, NQ, H), gws(F.Q4_K, M, 2 * NKV, H), gws(F.Q4_K, M, H, NQ),
+                  gws(F.Q4_K, M, 2 * FF, H), gws(F.Q6_K, M, H, FF), gws(F.Q6_K, M, VOCAB, H))
+        self.ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        # draft side (inputs of the verify step): draft logits, draft tokens, uniforms
+        noise = ih.quantized_kernels.synth_gaussian(st(SEED, "draft_logits"), k * VOCAB, 3.0).view(k, VOCAB)
+        self.drf = noise.contiguous()
+        g = torch.Generator(device="cpu").manual_seed(SEED)
+        p = torch.softmax(self.drf.cpu().double() / T, -1)
+        self.draft = torch.multinomial(p, 1, generator=g).view(1, k).to(torch.int32).to(dev)
+        self.u_acc = torch.rand((1, k), generator=g).to(dev)
+        self.u_res = torch.rand(1, generator=g).to(dev)
+        self.u_bonus = torch.rand(1, generator=g).to(dev)
+        nb = C.c_size_t()
+        ih._lib.check(ih.load().ihip_spec_accept_ws_bytes(1, k, VOCAB, C.byref(nb)))
+        self.acc_ws = torch.empty(nb.value, dtype=torch.uint8, device=dev)
+        self.out_tok = torch.zeros((1, k + 1), dtype=torch.int32, device=dev)
+        self.out_n = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def run(self):
+        ih, F, M = self.ih, self.ih.formats, self.M
+        gemm = ih.gemm_q
+        acc = ih.GEMM_F32 | ih.GEMM_ACCUM
+        self.x.copy_(self.x0)
+        for lw in self.model.layers:
+            ih.rmsnorm(self.x, out=self.h)
+            gemm(F.Q4_K, lw["q"], self.h, NQ, H, flags=ih.GEMM_F32, out=self.q, ws=self.ws)
+            gemm(F.Q4_K, lw["kv"], self.h, 2 * NKV, H, flags=ih.GEMM_F32, out=self.kv, ws=self.ws)
+            gemm(F.Q4_K, lw["o"], self.q, H, NQ, flags=acc, out=self.x, ws=self.ws)
+            ih.rmsnorm(self.x, out=self.h)
+            gemm(F.Q4_K, lw["gu"], self.h, 2 * FF, H, flags=ih.GEMM_F32, out=self.gu, ws=self.ws)
+            ih.quantized_kernels.silu_mul(self.gu, FF, out=self.hm)
+            gemm(F.Q6_K, lw["down"], self.hm, H, FF, flags=acc, out=self.x, ws=self.ws)
+        ih.rmsnorm(self.x, out=self.h)
+        gemm(F.Q6_K, self.model.lm, self.h, VOCAB, H, flags=ih.GEMM_F32, out=self.logits, ws=self.ws)
+        ih.spec_accept(self.logits.view(1, M, VOCAB), self.drf.view(1, self.k, VOCAB), self.draft, self.T,
+                       self.u_acc, self.u_res, self.u_bonus, out_tok=self.out_tok, out_n=self.out_n,
+                       ws=self.acc_ws)
+
+
+def time_op(fn, iters: int, stream):
+    """Average duration of fn() over `iters` launches, HIP events on `stream`."""
+    import torch
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(iters):
+        fn(i)
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / iters * 1e-3
+
+
+def gemm_roofline(ih, model: Model, n_layers: int, M: int, iters: int = 64):
+    """Dominant dequant-matmul: Q4_K gate/up 24576x4096 at M=5 over the
+    layers' weights in turn (1.8 GB, far beyond the 256 MB cache)."""
+    import torch
+    F = ih.formats
+    N, K = 2 * FF, H
+    x = ih.quantized_kernels.synth_gaussian(123, M * K).view(M, K)
+    y = torch.empty((M, N), device="cuda")
+    ws = torch.empty(ih.quantized_kernels.gemm_ws_bytes(F.Q4_K, M, N, K), dtype=torch.uint8, device="cuda")
+    s = torch.cuda.current_stream()
+    fn = lambda i: ih.gemm_q(F.Q4_K, model.layers[i % n_layers]["gu"], x, N, K, flags=ih.GEMM_F32,  # noqa: E731
+                             out=y, ws=ws)
+    for i in range(4):
+        fn(i)
+    torch.cuda.synchronize()
+    t = time_op(fn, iters, s)
+    alg = F.matrix_bytes(F.Q4_K, N, K) + M * K * 4 + M * N * 4
+    return t, alg
+
+
+def gemm_sweep(ih, model: Model, n_layers: int):
+    """GB/s of the Q4_K gate/up and Q6_K down projections at M = 1..8."""
+    import torch
+    F = ih.formats
+    out = {}
+    s = torch.cuda.current_stream()
+    for name, key, qt, N, K in (("q4k_24576x4096", "gu", F.Q4_K, 2 * FF, H),
+                                ("q6k_4096x12288", "down", F.Q6_K, H, FF)):
+        row = {}
+        for M in (1, 2, 4, 5, 8):
+            x = ih.quantized_kernels.synth_gaussian(7 + M, M * K).view(M, K)
+            y = torch.empty((M, N), device="cuda")
+            ws = torch.empty(ih.quantized_kernels.gemm_ws_bytes(qt, M, N, K), dtype=torch.uint8, device="cuda")
+            fn = lambda i: ih.gemm_q(qt, model.layers[i % n_layers][key], x, N, K,  # noqa: E731
+                                     flags=ih.GEMM_F32, out=y, ws=ws)
+            for i in range(3):
+                fn(i)
+            torch.cuda.synchronize()
+            t = time_op(fn, 32, s)
+            gbs = (F.matrix_bytes(qt, N, K) + M * K * 4 + M * N * 4) / t / 1e9
+            row[str(M)] = round(gbs, 1)
+        out[name] = row
+    return out
+
+
+def cpu_baseline(ih, model: Model, n_layers: int, M: int, k: int, budget_s: float):
+    """The reference CPU path on a bounded sample: S_L layers + lm_head + accept,
+    scaled to the full step. Reference kernels from oracle/_ref (kind
+    "reference"); the oracle port if the reference build is absent."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    F = ih.formats
+    kind = "reference" if O.ref_available() else "port"
+    sample_layers = min(4, n_layers)
+    hostw = [{n: t.cpu().numpy() for n, t in model.layers[L].items()} for L in range(sample_layers)]
+    lm = model.lm.cpu().numpy()
+    rng = np.random.default_rng(0)
+    x0 = rng.standard_normal((M, H)).astype(np.float32)
+    Lt = rng.standard_normal((k + 1, VOCAB)).astype(np.float32) * 3
+    Ld = (Lt[:k] + rng.standard_normal((k, VOCAB)).astype(np.float32) * 1.5).astype(np.float32)
+    draft = Ld.argmax(-1).astype(np.int32)
+    if kind == "reference":
+        gemv = lambda qt, w, v, K, N: O.ref_gemv(qt, w, v, K, N)  # noqa: E731
+    else:
+        gemv = lambda qt, w, v, K, N: O.gemv_q8k(qt, w, v, K, N, os.cpu_count() or 1)  # noqa: E731
+
+    def rms(v):
+        return (v / np.sqrt((v.astype(np.float64) ** 2).mean() + 1e-6)).astype(np.float32)
+
+    def layers_pass():
+        x = x0.copy()
+        for lw in hostw:
+            for m in range(M):  # forward_cpu! streams the verify tokens one at a time
+                h = rms(x[m])
+                q = gemv(F.Q4_K, lw["q"], h, H, NQ)
+                gemv(F.Q4_K, lw["kv"], h, H, 2 * NKV)
+                x[m] += gemv(F.Q4_K, lw["o"], q, NQ, H)
+                h = rms(x[m])
+                gu = gemv(F.Q4_K, lw["gu"], h, H, 2 * FF)
+                g, u = gu[:FF], gu[FF:]
+                x[m] += gemv(F.Q6_K, lw["down"], (g / (1 + np.exp(-g)) * u).astype(np.float32), FF, H)
+        return x
+
+    def head_pass(x):
+        for m in range(M):
+            gemv(F.Q6_K, lm, rms(x[m]), H, VOCAB)
+        O.spec_accept(Lt, Ld, draft, 0.8, np.full(k, 0.5, np.float32), 0.5, 0.5, 0)
+
+    gomp = None
+    for name in ("libgomp.so.1", "libgomp.so"):
+        try:
+            gomp = C.CDLL(name)
+            break
+        except OSError:
+            pass
+    ncpu = len(os.sched_getaffinity(0))
+    ref_default = max(2, min(8, ncpu // 2))  # src/QuantizedKernels.jl:40
+    results = {}
+    for threads in sorted({ref_default, ncpu}):
+        if gomp is not None:
+            gomp.omp_set_num_threads(threads)
+        x = layers_pass()  # warm-up
+        head_pass(x)
+        t_l, t_h, reps = 0.0, 0.0, 0
+        t_end = time.perf_counter() + budget_s / 2
+        while time.perf_counter() < t_end or reps == 0:
+            t0 = time.perf_counter()
+            x = layers_pass()
+            t1 = time.perf_counter()
+            head_pass(x)
+            t2 = time.perf_counter()
+            t_l += t1 - t0
+            t_h += t2 - t1
+            reps += 1
+        step_s = (t_l / reps) * (n_layers / sample_layers) + t_h / reps
+        results[threads] = (1.0 / step_s, reps)
+        log(f"cpu baseline threads={threads}: {step_s * 1e3:.1f} ms/step ({reps} samples)")
+    best = max(results)
+    return {
+        "value": round(results[best][0], 4),
+        "unit": "verify steps/s",
+        "cores": best,
+        "kind": kind,
+        "sample": (f"{sample_layers} of {n_layers} layers (each matrix once per token, M={M}) + lm_head x{M} "
+                   f"+ accept, scaled to {n_layers} layers; reference thread default "
+                   f"clamp(nproc/2,2,8)={ref_default}: {results[ref_default][0]:.4f} steps/s; "
+                   f"host cpus={ncpu}"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--m", type=int, default=5)
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(see the sharding design); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import inferno_hip as ih
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    assert ih.quant_kernels_available(), ih._lib.last_error()
+    k, T = 4, 0.8
+    t0 = time.time()
+    model = Model(ih, args.layers)
+    step = VerifyStep(ih, model, args.m, k, T)
+    log(f"setup {time.time() - t0:.1f}s, weights {model.weight_bytes(args.layers) / 1e9:.3f} GB")
+
+    # capture one step in a HIP graph
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step.run()
+        step.run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        step.run()
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    ms = e0.elapsed_time(e1) / args.steps
+    log(f"verify step: {ms:.3f} ms (wall {wall / args.steps * 1e3:.3f} ms), accepted n={int(step.out_n[0])}")
+
+    t_op, alg = gemm_roofline(ih, model, args.layers, args.m)
+    achieved = alg / t_op / 1e9
+    sweep = None if args.no_sweep else gemm_sweep(ih, model, args.layers)
+    cpu = None if args.no_cpu else cpu_baseline(ih, model, args.layers, args.m, k, args.cpu_budget)
+
+    out = {
+        "metric": METRIC,
+        "value": round(1000.0 / ms, 3),
+        "unit": "verify steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 (split-f16 MFMA operands, f32 accumulate)",
+        "data": "synthetic (seeded GGUF blocks and activations, random-init, no checkpoint offline)",
+        "config": {
+            "workload": "configs[3]: full verify step, 32 layers hidden 4096 (Q4_K q/k/v/o/gate/up, "
+                        "Q6_K down), Q6_K lm_head 151936x4096, M=5, k=4 accept at T=0.8",
+            "layers": args.layers, "hidden": H, "vocab": VOCAB, "M": args.m, "k": k,
+            "weight_bytes_per_step": model.weight_bytes(args.layers),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "kernel": "Q4_K dequant-matmul 24576x4096 M=5 (prep + gemm + split-K reduce launches)",
+            "us_per_launch": round(t_op * 1e6, 2),
+            "algorithmic_bytes": alg,
+        },
+        "cpu_baseline": cpu,
+        "gemm_gbps_by_M": sweep,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

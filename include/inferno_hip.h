@@ -112,6 +112,14 @@ int ihip_dequant(int qtype, const void *w_dev, float *out_dev, int64_t n_elems,
 int ihip_rmsnorm(const float *x_dev, const float *w_dev, float *out_dev,
                  int rows, int n, float eps, void *stream);
 
+/* out[m, i] = silu(gu[m, i]) * gu[m, F + i] for M rows of [gate | up]
+ * (the SiLU gating of mlp_forward, src/ModelCPU.jl:447-473). */
+int ihip_silu_mul(const float *gu_dev, int M, int F, float *out_dev, void *stream);
+
+/* y[i] += x[i], i < n (the residual adds of the decoder layer,
+ * src/ModelCPU.jl:870-891). */
+int ihip_add(float *y_dev, const float *x_dev, int64_t n, void *stream);
+
 /* ---- LM-head softmax statistics and speculative acceptance ---- */
 
 /* Per row r of logits [rows x V]: zmax[r] = max_j L[r,j]/T and

@@ -31,6 +31,8 @@ hipError_t launch_tree(const float *tgt, const float *drf, const int32_t *tok, c
                        float T, const float *u, float2 *part, int32_t *out_path, int32_t *out_len, int32_t *wsi,
                        hipStream_t st);
 hipError_t launch_rmsnorm(const float *x, const float *w, float *out, int rows, int n, float eps, hipStream_t st);
+hipError_t launch_silu_mul(const float *gu, int M, int F, float *out, hipStream_t st);
+hipError_t launch_add(float *y, const float *x, int64_t n, hipStream_t st);
 hipError_t launch_synth(int qt, uint64_t stream, int64_t first, int64_t nblk, void *out, hipStream_t st);
 hipError_t launch_gaussian(uint64_t stream, int64_t n, float scale, const float *add, float *out, hipStream_t st);
 
@@ -261,6 +263,20 @@ int ihip_rmsnorm(const float *x_dev, const float *w_dev, float *out_dev, int row
     if (rows < 0 || n < 1) return fail(IHIP_EINVAL, "ihip_rmsnorm: rows=%d n=%d", rows, n);
     hipError_t e = launch_rmsnorm(x_dev, w_dev, out_dev, rows, n, eps, S(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_rmsnorm");
+}
+
+int ihip_silu_mul(const float *gu_dev, int M, int F, float *out_dev, void *stream) {
+    if (!gu_dev || !out_dev) return fail(IHIP_EFAULT, "ihip_silu_mul: NULL pointer");
+    if (M < 0 || F < 1) return fail(IHIP_EINVAL, "ihip_silu_mul: M=%d F=%d", M, F);
+    hipError_t e = launch_silu_mul(gu_dev, M, F, out_dev, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_silu_mul");
+}
+
+int ihip_add(float *y_dev, const float *x_dev, int64_t n, void *stream) {
+    if (!y_dev || !x_dev) return fail(IHIP_EFAULT, "ihip_add: NULL pointer");
+    if (n < 0) return fail(IHIP_EINVAL, "ihip_add: n=%lld", (long long)n);
+    hipError_t e = launch_add(y_dev, x_dev, n, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_add");
 }
 
 int ihip_accept_ws_bytes(int rows, int V, size_t *bytes) {

@@ -107,7 +107,36 @@ __global__ void gaussian_kernel(uint64_t stream, int64_t n, float scale, const f
     out[i] = (float)z * scale + (add ? add[i] : 0.f);
 }
 
+// out[m, i] = silu(gu[m, i]) * gu[m, F + i] for rows of [gate | up]
+// (mlp_forward, src/ModelCPU.jl:447-473); silu(g) = g / (1 + exp(-g)).
+__global__ void silu_mul_kernel(const float *__restrict__ gu, int M, int F, float *__restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)M * F) return;
+    const int64_t m = i / F, c = i % F;
+    const float g = gu[m * 2 * F + c], u = gu[m * 2 * F + F + c];
+    out[i] = g / (1.0f + expf(-g)) * u;
+}
+
+// y[i] += x[i] (residual add of the decoder layer, src/ModelCPU.jl:870-891)
+__global__ void add_kernel(float *__restrict__ y, const float *__restrict__ x, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] += x[i];
+}
+
 }  // namespace
+
+hipError_t launch_silu_mul(const float *gu, int M, int F, float *out, hipStream_t st) {
+    const int64_t n = (int64_t)M * F;
+    if (n <= 0) return hipSuccess;
+    silu_mul_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(gu, M, F, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_add(float *y, const float *x, int64_t n, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    add_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(y, x, n);
+    return hipGetLastError();
+}
 
 hipError_t launch_rmsnorm(const float *x, const float *w, float *out, int rows, int n, float eps, hipStream_t st) {
     if (rows <= 0) return hipSuccess;

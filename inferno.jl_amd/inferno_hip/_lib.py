@@ -32,6 +32,8 @@ SIGNATURES = {
     "ihip_gemm_q": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "ihip_dequant": (_i, [_i, _vp, _vp, _i64, _vp]),
     "ihip_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
+    "ihip_silu_mul": (_i, [_vp, _i, _i, _vp, _vp]),
+    "ihip_add": (_i, [_vp, _vp, _i64, _vp]),
     "ihip_accept_ws_bytes": (_i, [_i, _i, C.POINTER(_sz)]),
     "ihip_softmax_stats": (_i, [_vp, _i, _i, _f, _vp, _vp, _vp, _sz, _vp]),
     "ihip_spec_accept_ws_bytes": (_i, [_i, _i, _i, C.POINTER(_sz)]),

@@ -152,3 +152,18 @@ def synth_gaussian(stream_id: int, n: int, scale: float = 1.0, add=None, out=Non
     ap = None if add is None else _ptr(add)
     _lib.check(_lib.load().ihip_synth_gaussian(C.c_uint64(stream_id), n, scale, ap, _ptr(out), _stream(stream)))
     return out
+
+
+def silu_mul(gu, f: int, out=None, stream=None):
+    """silu(gate) * up for rows of gu = [gate | up] (src/ModelCPU.jl:447-473)."""
+    import torch
+    m = gu.shape[0]
+    out = torch.empty((m, f), dtype=torch.float32, device=gu.device) if out is None else out
+    _lib.check(_lib.load().ihip_silu_mul(_ptr(gu), m, f, _ptr(out), _stream(stream)))
+    return out
+
+
+def add_(y, x, stream=None):
+    """y += x in place (residual add)."""
+    _lib.check(_lib.load().ihip_add(_ptr(y), _ptr(x), y.numel(), _stream(stream)))
+    return y

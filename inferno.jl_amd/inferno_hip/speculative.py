@@ -42,7 +42,7 @@ def softmax_stats(logits, temperature: float, stream=None):
 
 
 def spec_accept(target_logits, draft_logits, draft_tokens, temperature: float, u_acc, u_res, u_bonus,
-                mode: int = MODE_STANDARD, stream=None):
+                mode: int = MODE_STANDARD, stream=None, out_tok=None, out_n=None, ws=None):
     """Batched accept step.
 
     target_logits [S, k+1, V], draft_logits [S, k, V], draft_tokens [S, k]
@@ -65,9 +65,12 @@ def spec_accept(target_logits, draft_logits, draft_tokens, temperature: float, u
     nb = C.c_size_t()
     _lib.check(L.ihip_spec_accept_ws_bytes(S, k, V, C.byref(nb)))
     dev = target_logits.device
-    ws = _ws(nb.value, dev)
-    out_tok = torch.zeros((S, k + 1), dtype=torch.int32, device=dev)
-    out_n = torch.zeros(S, dtype=torch.int32, device=dev)
+    if ws is None:
+        ws = _ws(nb.value, dev)
+    if out_tok is None:
+        out_tok = torch.zeros((S, k + 1), dtype=torch.int32, device=dev)
+    if out_n is None:
+        out_n = torch.zeros(S, dtype=torch.int32, device=dev)
     for t in (target_logits, draft_logits, draft_tokens, u_acc, u_res, u_bonus):
         if not t.is_contiguous():
             raise ValueError("inputs must be contiguous")
