@@ -42,30 +42,44 @@ def log(*a):
 
 
 class Model:
-    """Device-resident synthetic weights of the config-4 shape."""
+    """Device-resident synthetic weights of the config-4 shape, generated as
+    GGUF blocks and repacked once into the matmul's tile-contiguous layout
+    (as a model loader would at load time). The GGUF bytes of the first
+    `keep_gguf` layers and of the lm_head are kept on the host for the CPU
+    baseline."""
 
-    def __init__(self, ih, n_layers: int):
+    SHAPES = {"q": ("Q4_K", NQ, H, "attn_q"), "kv": ("Q4_K", 2 * NKV, H, "attn_kv"),  # k rows then v rows
+              "o": ("Q4_K", H, NQ, "attn_output"), "gu": ("Q4_K", 2 * FF, H, "ffn_gate_up"),  # gate then up
+              "down": ("Q6_K", H, FF, "ffn_down")}
+
+    def __init__(self, ih, n_layers: int, keep_gguf: int = 4):
         import torch
         F = ih.formats
         st = ih.synth.stream_for
-        self.layers = []
+        self.layers, self.host_gguf, self.gguf_bytes = [], [], 0
         for L in range(n_layers):
-            def blk(qt, rows, k, name):
-                return ih.quantized_kernels.synth_blocks(qt, st(SEED, f"blk{L}.{name}"),
-                                                         rows * k // F.BLOCK_ELEMS[qt])
-            self.layers.append({
-                "q": blk(F.Q4_K, NQ, H, "attn_q"),
-                "kv": blk(F.Q4_K, 2 * NKV, H, "attn_kv"),     # k rows then v rows
-                "o": blk(F.Q4_K, H, NQ, "attn_output"),
-                "gu": blk(F.Q4_K, 2 * FF, H, "ffn_gate_up"),  # gate rows then up rows
-                "down": blk(F.Q6_K, H, FF, "ffn_down"),
-            })
-        self.lm = ih.quantized_kernels.synth_blocks(F.Q6_K, st(SEED, "output"), VOCAB * H // 256)
+            lw, hw = {}, {}
+            for key, (qn, rows, k, name) in self.SHAPES.items():
+                qt = getattr(F, qn)
+                g = ih.quantized_kernels.synth_blocks(qt, st(SEED, f"blk{L}.{name}"), rows * k // F.BLOCK_ELEMS[qt])
+                lw[key] = ih.pack_weights(qt, g, rows, k)
+                self.gguf_bytes += g.numel()
+                if L < keep_gguf:
+                    hw[key] = g.cpu().numpy()
+                del g
+            self.layers.append(lw)
+            if L < keep_gguf:
+                self.host_gguf.append(hw)
+        g = ih.quantized_kernels.synth_blocks(F.Q6_K, st(SEED, "output"), VOCAB * H // 256)
+        self.lm = ih.pack_weights(F.Q6_K, g, VOCAB, H)
+        self.gguf_bytes += g.numel()
+        self.host_lm = g.cpu().numpy()
+        del g
         torch.cuda.synchronize()
 
     def weight_bytes(self, n_layers: int) -> int:
-        per = sum(t.numel() for t in self.layers[0].values())
-        return per * n_layers + self.lm.numel()
+        """GGUF bytes of the weights one step streams."""
+        return self.gguf_bytes
 
 
 class VerifyStep:
@@ -86,8 +100,9 @@ class VerifyStep:
         self.hm = torch.empty((M, FF), device=dev)
         self.logits = torch.empty((M, VOCAB), device=dev)
         gws = ih.quantized_kernels.gemm_ws_bytes
-        wsb = max(gws(F.Q4_K, M, NQ, H), gws(F.Q4_K, M, 2 * NKV, H), gws(F.Q4_K, M, H, NQ),
-                  gws(F.Q4_K, M, 2 * FF, H), gws(F.Q6_K, M, H, FF), gws(F.Q6_K, M, VOCAB, H))
+        fl = ih.GEMM_F32 | ih.GEMM_PACKED | ih.GEMM_ACCUM
+        wsb = max(gws(F.Q4_K, M, NQ, H, fl), gws(F.Q4_K, M, 2 * NKV, H, fl), gws(F.Q4_K, M, H, NQ, fl),
+                  gws(F.Q4_K, M, 2 * FF, H, fl), gws(F.Q6_K, M, H, FF, fl), gws(F.Q6_K, M, VOCAB, H, fl))
         self.ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
         # draft side (inputs of the verify step): draft logits, draft tokens, uniforms
         noise = ih.quantized_kernels.synth_gaussian(st(SEED, "draft_logits"), k * VOCAB, 3.0).view(k, VOCAB)
@@ -107,19 +122,20 @@ class VerifyStep:
     def run(self):
         ih, F, M = self.ih, self.ih.formats, self.M
         gemm = ih.gemm_q
-        acc = ih.GEMM_F32 | ih.GEMM_ACCUM
+        f32 = ih.GEMM_F32 | ih.GEMM_PACKED
+        acc = f32 | ih.GEMM_ACCUM
         self.x.copy_(self.x0)
         for lw in self.model.layers:
             ih.rmsnorm(self.x, out=self.h)
-            gemm(F.Q4_K, lw["q"], self.h, NQ, H, flags=ih.GEMM_F32, out=self.q, ws=self.ws)
-            gemm(F.Q4_K, lw["kv"], self.h, 2 * NKV, H, flags=ih.GEMM_F32, out=self.kv, ws=self.ws)
+            gemm(F.Q4_K, lw["q"], self.h, NQ, H, flags=f32, out=self.q, ws=self.ws)
+            gemm(F.Q4_K, lw["kv"], self.h, 2 * NKV, H, flags=f32, out=self.kv, ws=self.ws)
             gemm(F.Q4_K, lw["o"], self.q, H, NQ, flags=acc, out=self.x, ws=self.ws)
             ih.rmsnorm(self.x, out=self.h)
-            gemm(F.Q4_K, lw["gu"], self.h, 2 * FF, H, flags=ih.GEMM_F32, out=self.gu, ws=self.ws)
+            gemm(F.Q4_K, lw["gu"], self.h, 2 * FF, H, flags=f32, out=self.gu, ws=self.ws)
             ih.quantized_kernels.silu_mul(self.gu, FF, out=self.hm)
             gemm(F.Q6_K, lw["down"], self.hm, H, FF, flags=acc, out=self.x, ws=self.ws)
         ih.rmsnorm(self.x, out=self.h)
-        gemm(F.Q6_K, self.model.lm, self.h, VOCAB, H, flags=ih.GEMM_F32, out=self.logits, ws=self.ws)
+        gemm(F.Q6_K, self.model.lm, self.h, VOCAB, H, flags=f32, out=self.logits, ws=self.ws)
         ih.spec_accept(self.logits.view(1, M, VOCAB), self.drf.view(1, self.k, VOCAB), self.draft, self.T,
                        self.u_acc, self.u_res, self.u_bonus, out_tok=self.out_tok, out_n=self.out_n,
                        ws=self.acc_ws)
@@ -146,9 +162,10 @@ def gemm_roofline(ih, model: Model, n_layers: int, M: int, iters: int = 64):
     N, K = 2 * FF, H
     x = ih.quantized_kernels.synth_gaussian(123, M * K).view(M, K)
     y = torch.empty((M, N), device="cuda")
-    ws = torch.empty(ih.quantized_kernels.gemm_ws_bytes(F.Q4_K, M, N, K), dtype=torch.uint8, device="cuda")
+    fl = ih.GEMM_F32 | ih.GEMM_PACKED
+    ws = torch.empty(ih.quantized_kernels.gemm_ws_bytes(F.Q4_K, M, N, K, fl), dtype=torch.uint8, device="cuda")
     s = torch.cuda.current_stream()
-    fn = lambda i: ih.gemm_q(F.Q4_K, model.layers[i % n_layers]["gu"], x, N, K, flags=ih.GEMM_F32,  # noqa: E731
+    fn = lambda i: ih.gemm_q(F.Q4_K, model.layers[i % n_layers]["gu"], x, N, K, flags=fl,  # noqa: E731
                              out=y, ws=ws)
     for i in range(4):
         fn(i)
@@ -170,9 +187,10 @@ def gemm_sweep(ih, model: Model, n_layers: int):
         for M in (1, 2, 4, 5, 8):
             x = ih.quantized_kernels.synth_gaussian(7 + M, M * K).view(M, K)
             y = torch.empty((M, N), device="cuda")
-            ws = torch.empty(ih.quantized_kernels.gemm_ws_bytes(qt, M, N, K), dtype=torch.uint8, device="cuda")
+            fl = ih.GEMM_F32 | ih.GEMM_PACKED
+            ws = torch.empty(ih.quantized_kernels.gemm_ws_bytes(qt, M, N, K, fl), dtype=torch.uint8, device="cuda")
             fn = lambda i: ih.gemm_q(qt, model.layers[i % n_layers][key], x, N, K,  # noqa: E731
-                                     flags=ih.GEMM_F32, out=y, ws=ws)
+                                     flags=fl, out=y, ws=ws)
             for i in range(3):
                 fn(i)
             torch.cuda.synchronize()
@@ -193,9 +211,9 @@ def cpu_baseline(ih, model: Model, n_layers: int, M: int, k: int, budget_s: floa
     import oracle as O
     F = ih.formats
     kind = "reference" if O.ref_available() else "port"
-    sample_layers = min(4, n_layers)
-    hostw = [{n: t.cpu().numpy() for n, t in model.layers[L].items()} for L in range(sample_layers)]
-    lm = model.lm.cpu().numpy()
+    sample_layers = min(len(model.host_gguf), n_layers)
+    hostw = model.host_gguf[:sample_layers]
+    lm = model.host_lm
     rng = np.random.default_rng(0)
     x0 = rng.standard_normal((M, H)).astype(np.float32)
     Lt = rng.standard_normal((k + 1, VOCAB)).astype(np.float32) * 3

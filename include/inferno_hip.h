@@ -38,6 +38,7 @@ extern "C" {
 #define IHIP_GEMM_F32    1  /* force fp32-accurate: split-fp16 MFMA, rel-L2 <= 1e-5 */
 #define IHIP_GEMM_HALF   2  /* force single-limb fp16 MFMA, rel-L2 <= 1e-2 */
 #define IHIP_GEMM_ACCUM  4  /* y += W x (y is not cleared first) */
+#define IHIP_GEMM_PACKED 8  /* w_dev is in the packed layout of ihip_pack_weights */
 
 /* Message for the last failing call on this thread ("" if none). */
 const char *ihip_last_error(void);
@@ -100,6 +101,19 @@ int ihip_gemm_q_ws_bytes(int qtype, int M, int N, int K, int flags,
 int ihip_gemm_q(int qtype, const void *w_dev, const float *x_dev, float *y_dev,
                 int M, int N, int K, int flags, void *ws, size_t ws_bytes,
                 void *stream);
+
+/* Packed weight layout: the GGUF blocks of each 16-row tile and 256-element
+ * K-unit stored as one contiguous chunk, swizzled so that every lane of the
+ * matmul kernel fetches its operand bytes with whole-cache-line 16-byte
+ * loads (bytes and values unchanged, only moved; rows past N and Q8_0 blocks
+ * past K are zero). ihip_packed_bytes gives the size (a multiple of 16);
+ * ihip_pack_weights converts one [N x K] GGUF matrix on the device, once,
+ * at model load: the reference reads GGUF tensors as-is
+ * (src/LoaderCPU.jl:358-372, src/ModelCPU.jl:295-296), and packed matrices
+ * are then passed to ihip_gemm_q with IHIP_GEMM_PACKED. */
+int ihip_packed_bytes(int qtype, int N, int K, size_t *bytes);
+int ihip_pack_weights(int qtype, const void *w_gguf_dev, void *w_packed_dev,
+                      int N, int K, void *stream);
 
 /* Bit-exact dequantization of n_elems weights (a multiple of the block
  * size) to fp32: the dequantize_*_block! formulas of

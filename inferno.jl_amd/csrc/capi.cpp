@@ -16,6 +16,8 @@
 hipError_t launch_gemm(int qt, const void *W, const float *X, float *Y, int M, int N, int K, int flags, void *ws,
                        hipStream_t st);
 size_t gemm_ws_bytes(int qt, int M, int N, int K, int flags);
+size_t packed_bytes(int qt, int N, int K);
+hipError_t launch_pack(int qt, const void *W, void *P, int N, int K, hipStream_t st);
 hipError_t launch_dequant(int qt, const void *w, float *out, int64_t n_blocks, hipStream_t st);
 int accept_nchunk(int V);
 hipError_t launch_stats(const float *L, int rows, int V, float T, float T_last, int period, float2 *part,
@@ -78,7 +80,7 @@ int check_gemm_shape(int qt, int M, int N, int K, int flags) {
     if (N < 1) return fail(IHIP_EINVAL, "ihip_gemm_q: N=%d", N);
     if (K < 1 || K % block_elems(qt))
         return fail(IHIP_EINVAL, "ihip_gemm_q: K=%d is not a positive multiple of %d", K, block_elems(qt));
-    if ((flags & ~7) || ((flags & 3) == 3)) return fail(IHIP_EINVAL, "ihip_gemm_q: bad flags 0x%x", flags);
+    if ((flags & ~15) || ((flags & 3) == 3)) return fail(IHIP_EINVAL, "ihip_gemm_q: bad flags 0x%x", flags);
     return IHIP_OK;
 }
 
@@ -165,18 +167,30 @@ void dropin_gemv(const char *name, int qt, const uint8_t *weight, const float *x
         if (it != L.wcache.end()) {
             dw = it->second;
         } else {
-            e = hipMalloc(&dw, wbytes);
-            if (e == hipSuccess) e = hipMemcpy(dw, weight, wbytes, hipMemcpyHostToDevice);
-            if (e == hipSuccess) L.wcache[key] = dw;
-            else if (dw) (void)hipFree(dw);
+            // first call with this matrix: upload, repack once, keep the packed copy
+            void *raw = nullptr;
+            e = hipMalloc(&raw, wbytes);
+            if (e == hipSuccess) e = hipMalloc(&dw, packed_bytes(qt, N, K));
+            if (e == hipSuccess) e = hipMemcpy(raw, weight, wbytes, hipMemcpyHostToDevice);
+            if (e == hipSuccess) e = launch_pack(qt, raw, dw, N, K, L.stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(L.stream);
+            if (raw) (void)hipFree(raw);
+            if (e == hipSuccess) {
+                L.wcache[key] = dw;
+            } else if (dw) {
+                (void)hipFree(dw);
+                dw = nullptr;
+            }
         }
         if (e != hipSuccess) {
             rc = hip_fail(e, name);
         } else if ((rc = grow(&L.dx, &L.dx_cap, (size_t)K * 4)) == IHIP_OK &&
                    (rc = grow(&L.dy, &L.dy_cap, (size_t)N * 4)) == IHIP_OK &&
-                   (rc = grow(&L.dws, &L.dws_cap, gemm_ws_bytes(qt, 1, N, K, IHIP_GEMM_F32))) == IHIP_OK) {
+                   (rc = grow(&L.dws, &L.dws_cap, gemm_ws_bytes(qt, 1, N, K, IHIP_GEMM_F32 | IHIP_GEMM_PACKED))) ==
+                       IHIP_OK) {
             e = hipMemcpyAsync(L.dx, x, (size_t)K * 4, hipMemcpyHostToDevice, L.stream);
-            if (e == hipSuccess) e = launch_gemm(qt, dw, L.dx, L.dy, 1, N, K, IHIP_GEMM_F32, L.dws, L.stream);
+            if (e == hipSuccess)
+                e = launch_gemm(qt, dw, L.dx, L.dy, 1, N, K, IHIP_GEMM_F32 | IHIP_GEMM_PACKED, L.dws, L.stream);
             if (e == hipSuccess) e = hipMemcpyAsync(out, L.dy, (size_t)N * 4, hipMemcpyDeviceToHost, L.stream);
             if (e == hipSuccess) e = hipStreamSynchronize(L.stream);
             rc = e == hipSuccess ? ok() : hip_fail(e, name);
@@ -245,6 +259,23 @@ int ihip_gemm_q(int qtype, const void *w_dev, const float *x_dev, float *y_dev, 
     if (!aligned16(ws)) return fail(IHIP_EINVAL, "ihip_gemm_q: workspace must be 16-byte aligned");
     hipError_t e = launch_gemm(qtype, w_dev, x_dev, y_dev, M, N, K, flags, ws, S(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_gemm_q");
+}
+
+int ihip_packed_bytes(int qtype, int N, int K, size_t *bytes) {
+    if (!bytes) return fail(IHIP_EFAULT, "ihip_packed_bytes: NULL");
+    const int rc = check_gemm_shape(qtype, 1, N, K, 0);
+    if (rc != IHIP_OK) return rc;
+    *bytes = packed_bytes(qtype, N, K);
+    return ok();
+}
+
+int ihip_pack_weights(int qtype, const void *w_gguf_dev, void *w_packed_dev, int N, int K, void *stream) {
+    if (!w_gguf_dev || !w_packed_dev) return fail(IHIP_EFAULT, "ihip_pack_weights: NULL pointer");
+    const int rc = check_gemm_shape(qtype, 1, N, K, 0);
+    if (rc != IHIP_OK) return rc;
+    if (!aligned16(w_packed_dev)) return fail(IHIP_EINVAL, "ihip_pack_weights: packed buffer must be 16-byte aligned");
+    hipError_t e = launch_pack(qtype, w_gguf_dev, w_packed_dev, N, K, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_pack_weights");
 }
 
 int ihip_dequant(int qtype, const void *w_dev, float *out_dev, int64_t n_elems, void *stream) {

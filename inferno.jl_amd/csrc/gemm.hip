@@ -144,6 +144,112 @@ __device__ __forceinline__ void finish_unit(Unit<QT> &r) {
     }
 }
 
+// ---------------------------------------------------------------- packed weights
+// Tile-contiguous layout: the 16 rows x 256 K-elements of tile t, unit u form
+// one chunk of CHUNK = 16 * UB bytes at (t * n_units + u) * CHUNK, arranged so
+// that lane l = n + 16 g (row n, lane group g) fetches exactly its operand
+// bytes with 16-byte loads at i * 1024 + 16 l plus per-row header loads. Every
+// load of a wave then covers whole cache lines, and no cross-lane transposes
+// remain. Byte map (row n of the tile, offsets into the GGUF block):
+//  Q4_K (2304 B): [1024 i + 16 l, +16) = qs[64 i + 16 g, +16) (i = 0, 1);
+//                 [2048 + 16 n, +16) = d, dmin, scales
+//  Q5_K (2816 B): quants as Q4_K; [2048 + 16 (n + 16 h), +16) = qh[16 h, +16)
+//                 (h = 0, 1); [2560 + 16 n, +16) = d, dmin, scales
+//  Q6_K (3360 B): for i = 0..3, p = 64 (i>>1) + 16 (i&1) + 4 g:
+//                 [16 l + 4 i, +4) = ql[p, +4); [1024 + 16 l + 4 i, +4) =
+//                 ql[p + 32, +4); [2048 + 16 l + 4 i, +4) = qh[32 (i>>1) +
+//                 16 (i&1) + 4 g, +4); [3072 + 16 n, +16) = scales;
+//                 [3328 + 2 n, +2) = d
+//  Q8_0 (4352 B): [1024 i + 16 l + 8 j + 4 h, +4) = qs dword (g + 4 h) of
+//                 block 2 i + j (i = 0..3; j, h = 0, 1); [4096 + 16 n + 2 b,
+//                 +2) = d of block b
+// Rows past N and Q8_0 blocks past K are zero bytes: they contribute zero.
+template <int QT> struct Packed {
+    static constexpr int UB = (QT == QT_Q8_0) ? 8 * 34 : QTraits<QT>::BB;
+    static constexpr int CHUNK = 16 * UB;
+};
+
+template <int QT>
+__device__ __forceinline__ void load_unit_packed(const uint8_t *__restrict__ ch, int lane, Unit<QT> &r) {
+    const int n = lane & 15;
+    if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {
+        r.q0 = *(const uint4 *)(ch + 16 * lane);
+        r.q1 = *(const uint4 *)(ch + 1024 + 16 * lane);
+        if constexpr (QT == QT_Q5_K) {
+            r.qh = *(const uint4 *)(ch + 2048 + 16 * (n + 16 * ((lane >> 4) & 1)));
+            r.hdr = *(const uint4 *)(ch + 2560 + 16 * n);
+        } else {
+            r.hdr = *(const uint4 *)(ch + 2048 + 16 * n);
+        }
+    } else if constexpr (QT == QT_Q6_K) {
+        const uint4 A = *(const uint4 *)(ch + 16 * lane);
+        const uint4 B = *(const uint4 *)(ch + 1024 + 16 * lane);
+        const uint4 H = *(const uint4 *)(ch + 2048 + 16 * lane);
+        r.a[0] = A.x; r.a[1] = A.y; r.a[2] = A.z; r.a[3] = A.w;
+        r.b[0] = B.x; r.b[1] = B.y; r.b[2] = B.z; r.b[3] = B.w;
+        r.h[0] = H.x; r.h[1] = H.y; r.h[2] = H.z; r.h[3] = H.w;
+        r.sc = *(const uint4 *)(ch + 3072 + 16 * n);
+        r.d = ld_u16(ch + 3328 + 2 * n);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint4 v = *(const uint4 *)(ch + 1024 * i + 16 * lane);
+            r.w0[2 * i] = v.x; r.w1[2 * i] = v.y; r.w0[2 * i + 1] = v.z; r.w1[2 * i + 1] = v.w;
+        }
+        const uint4 dv = *(const uint4 *)(ch + 4096 + 16 * n);
+        const uint32_t dw[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+        for (int b = 0; b < 8; b++) r.d[b] = (dw[b >> 1] >> (16 * (b & 1))) & 0xffffu;
+    }
+}
+
+// One thread per (unit, tile, lane): copies that lane's bytes of the chunk.
+template <int QT>
+__global__ __launch_bounds__(64) void pack_kernel(const uint8_t *__restrict__ W, int N, int K,
+                                                  uint8_t *__restrict__ P) {
+    constexpr int BB = QTraits<QT>::BB;
+    const int n_units = (K + UNIT - 1) / UNIT;
+    const int u = blockIdx.x, tile = blockIdx.y;
+    const int l = threadIdx.x, n = l & 15, g = l >> 4;
+    const int row = tile * 16 + n;
+    const bool live = row < N;
+    const size_t row_bytes = (size_t)(K / QTraits<QT>::QK) * BB;
+    uint8_t *ch = P + ((size_t)tile * n_units + u) * Packed<QT>::CHUNK;
+    const uint8_t *src = W + (size_t)(live ? row : 0) * row_bytes + (size_t)u * Packed<QT>::UB;
+    auto cp = [&](uint8_t *dst, const uint8_t *s, int nbytes, bool ok) {
+        for (int e = 0; e < nbytes; e++) dst[e] = ok ? s[e] : (uint8_t)0;
+    };
+    if constexpr (QT == QT_Q4_K) {
+        for (int i = 0; i < 2; i++) cp(ch + 1024 * i + 16 * l, src + 16 + 64 * i + 16 * g, 16, live);
+        if (g == 0) cp(ch + 2048 + 16 * n, src, 16, live);
+    } else if constexpr (QT == QT_Q5_K) {
+        for (int i = 0; i < 2; i++) cp(ch + 1024 * i + 16 * l, src + 48 + 64 * i + 16 * g, 16, live);
+        if (g < 2) cp(ch + 2048 + 16 * (n + 16 * g), src + 16 + 16 * g, 16, live);
+        if (g == 0) cp(ch + 2560 + 16 * n, src, 16, live);
+    } else if constexpr (QT == QT_Q6_K) {
+        for (int i = 0; i < 4; i++) {
+            const int p = 64 * (i >> 1) + 16 * (i & 1) + 4 * g;
+            cp(ch + 16 * l + 4 * i, src + p, 4, live);
+            cp(ch + 1024 + 16 * l + 4 * i, src + p + 32, 4, live);
+            cp(ch + 2048 + 16 * l + 4 * i, src + 128 + 32 * (i >> 1) + 16 * (i & 1) + 4 * g, 4, live);
+        }
+        if (g == 0) {
+            cp(ch + 3072 + 16 * n, src + 192, 16, live);
+            cp(ch + 3328 + 2 * n, src + 208, 2, live);
+        }
+    } else {
+        const int nblk = min(8, K / 32 - 8 * u);  // blocks of this unit inside the row
+        for (int i = 0; i < 4; i++)
+            for (int j = 0; j < 2; j++)
+                for (int h = 0; h < 2; h++) {
+                    const int b = 2 * i + j;
+                    cp(ch + 1024 * i + 16 * l + 8 * j + 4 * h, src + 34 * b + 2 + 4 * (g + 4 * h), 4, live && b < nblk);
+                }
+        if (g == 0)
+            for (int b = 0; b < 8; b++) cp(ch + 4096 + 16 * n + 2 * b, src + 34 * b, 2, live && b < nblk);
+    }
+}
+
 __device__ __forceinline__ f4 mfma32(h8 a, h8 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -338,7 +444,7 @@ template <int LK> struct Layout {
 template <int LK, int MT, bool SPLIT, bool MINS>
 __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ X, int M, int K,
                                                    uint8_t *__restrict__ afrag, float *__restrict__ xs,
-                                                   float *__restrict__ inv) {
+                                                   float *__restrict__ inv, uint8_t *__restrict__ mfrag) {
     constexpr int TOK = MT * (SPLIT ? 8 : 16);
     constexpr int ENTRY = Layout<LK>::ENTRY;
     const int u = blockIdx.x, tid = threadIdx.x;
@@ -374,9 +480,24 @@ __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ X, 
     const float scale = ldexpf(1.f, e2);
     if (t >= TOK) return;
     if (gi == 0) inv[(size_t)u * TOK + t] = ldexpf(1.f, -e2);
-    if (MINS && (gi & 3) == 0) xs[((size_t)u * 8 + (gi >> 2)) * TOK + t] = sm;
+    if (MINS && xs != nullptr && (gi & 3) == 0) xs[((size_t)u * 8 + (gi >> 2)) * TOK + t] = sm;
     const int mt = SPLIT ? t / 8 : t / 16;
     const int slot = SPLIT ? (t % 8) * 2 : t % 16;
+    if (MINS && MT == 1 && mfrag != nullptr && (gi & 3) == 0) {
+        // A operand of the mins MFMA (16x16x16): lane (slot, G) item e holds
+        // sub-block 4G + e of the scaled sub-block sums (G < 2; zero for
+        // G >= 2). X_s * scale / 32 stays below 2^15.
+        const int sb = gi >> 2, G = sb >> 2, e = sb & 3;
+        const float xsum = sm * scale * (1.0f / 32.0f);
+        const _Float16 h = (_Float16)xsum, l = (_Float16)(xsum - (float)h);
+        _Float16 *mf = (_Float16 *)(mfrag + (size_t)u * 64 * 8);
+        mf[(G * 16 + slot) * 4 + e] = h;
+        mf[((G + 2) * 16 + slot) * 4 + e] = (_Float16)0.0f;
+        if (SPLIT) {
+            mf[(G * 16 + slot + 1) * 4 + e] = l;
+            mf[((G + 2) * 16 + slot + 1) * 4 + e] = (_Float16)0.0f;
+        }
+    }
     _Float16 hi[8], lo[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) {
@@ -420,11 +541,11 @@ __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ X, 
 // RING - 1 items ahead, across row-group boundaries.
 template <int QT, int MT> struct Ring { static constexpr int R = (QT == QT_Q6_K && MT >= 3) ? 2 : 4; };
 
-template <int QT, int MT, bool SPLIT>
+template <int QT, int MT, bool SPLIT, bool PK>
 __global__ __launch_bounds__(WG_THREADS)
 void gemm_q_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, int N, int K, int ups, int S,
-                   int accum, const uint8_t *__restrict__ afrag, const float *__restrict__ xs,
-                   const float *__restrict__ invs, float *__restrict__ part) {
+                   const uint8_t *__restrict__ afrag, const float *__restrict__ xs, const float *__restrict__ invs,
+                   float *__restrict__ part) {
     using C = GemmCfg<QT>;
     constexpr int TOK = MT * (SPLIT ? 8 : 16);
     constexpr int TPL = Acc<MT, SPLIT>::TPL;
@@ -436,12 +557,13 @@ void gemm_q_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     const int n_units = (K + UNIT - 1) / UNIT;
     const int u0 = blockIdx.y * ups;
     const int nu = min(ups, n_units - u0);
-    const size_t row_bytes = (size_t)(K / C::QK) * C::BB;
-    const int tail_blk = (QT == QT_Q8_0 && (K % UNIT)) ? (K % UNIT) / 32 : 8;
     const int rowgroups = (N + ROWS_PER_WG - 1) / ROWS_PER_WG;
     const int G = gridDim.x;
-    const int n_rg = blockIdx.x < rowgroups ? (rowgroups - 1 - blockIdx.x) / G + 1 : 0;
+    if ((int)blockIdx.x >= rowgroups) return;  // whole workgroup
+    const int n_rg = (rowgroups - 1 - (int)blockIdx.x) / G + 1;
     const int n_items = n_rg * nu;
+    const size_t row_bytes = (size_t)(K / C::QK) * C::BB;
+    const int tail_blk = (QT == QT_Q8_0 && (K % UNIT)) ? (K % UNIT) / 32 : 8;
 
     uint8_t *a_lds = smem;                                      // [ups][UNIT_A]
     float *x_lds = (float *)(smem + (size_t)ups * UNIT_A);      // [ups][8][TOK]
@@ -449,42 +571,66 @@ void gemm_q_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n_in = lane & 15, g = lane >> 4;
-    // weight bytes of item it (row group blockIdx.x + G*(it/nu), unit u0 + it%nu)
-    auto item_ptr = [&](int it) {
-        const int rg = blockIdx.x + G * (it / nu);
-        const int row = min(rg * ROWS_PER_WG + wave * 16 + n_in, N - 1);
-        return W + (size_t)row * row_bytes + (size_t)(u0 + it % nu) * UNIT_BYTES;
-    };
-    auto item_nblk = [&](int it) { return (u0 + it % nu == n_units - 1) ? tail_blk : 8; };
+    const int row_in = wave * 16 + n_in;
 
-    // 1. start streaming this lane's weights
+    // 1. fetch this slice's prepared activations into registers (uniform
+    //    trip counts and clamped indices: no per-load branches, so every
+    //    load is in flight before the first wait)
+    const uint4 *a_src = (const uint4 *)(afrag + (size_t)u0 * UNIT_A);
+    const int n16 = nu * (UNIT_A / 16);
+    constexpr int A_PER_T = 8;  // 16-byte pieces per thread in the first pass
+    uint4 a_tmp[A_PER_T];
+#pragma unroll
+    for (int j = 0; j < A_PER_T; j++) a_tmp[j] = a_src[min(j * WG_THREADS + tid, n16 - 1)];
+    const int n_x = C::MINS ? nu * 8 * TOK : 0, n_i = nu * TOK;
+    const float *xs_src = xs + (size_t)u0 * 8 * TOK;
+    const float *i_src = invs + (size_t)u0 * TOK;
+    float x_tmp[2], i_tmp = i_src[min(tid, n_i - 1)];
+#pragma unroll
+    for (int j = 0; j < 2; j++) x_tmp[j] = C::MINS ? xs_src[min(j * WG_THREADS + tid, max(n_x - 1, 0))] : 0.f;
+
+    // 2. start streaming weights: the load stream walks items (row group
+    //    blockIdx.x + G*lj, unit lu) in order; past the last item it reloads
+    //    the last one, so every step issues the same batch of loads
+    int lj = 0, lu = 0;
+    auto load_next = [&](Unit<QT> &b) {
+        const bool past = lj >= n_rg;
+        const int j = past ? n_rg - 1 : lj, uu = past ? nu - 1 : lu;
+        if constexpr (PK) {
+            const int tile = min(((int)blockIdx.x + G * j) * (ROWS_PER_WG / 16) + wave, (N + 15) / 16 - 1);
+            load_unit_packed<QT>(W + ((size_t)tile * n_units + u0 + uu) * Packed<QT>::CHUNK, lane, b);
+        } else {
+            const int row = min(((int)blockIdx.x + G * j) * ROWS_PER_WG + row_in, N - 1);
+            load_unit<QT>(W + (size_t)row * row_bytes + (size_t)(u0 + uu) * UNIT_BYTES, g,
+                          (u0 + uu == n_units - 1) ? tail_blk : 8, b);
+        }
+        if (++lu == nu) {
+            lu = 0;
+            ++lj;
+        }
+    };
     Unit<QT> buf[R];
 #pragma unroll
-    for (int p = 0; p < R - 1; p++)
-        if (p < n_items) load_unit<QT>(item_ptr(p), g, item_nblk(p), buf[p]);
+    for (int p = 0; p < R - 1; p++) load_next(buf[p]);
 
-    // 2. copy this slice's prepared activations into LDS (one round of loads)
+    // 3. activations into LDS (clamped lanes rewrite the last entry with its
+    //    own value); a second pass only when a slice exceeds the first
     {
-        const uint4 *src = (const uint4 *)(afrag + (size_t)u0 * UNIT_A);
         uint4 *dst = (uint4 *)a_lds;
-        const int n16 = nu * (UNIT_A / 16);
-        for (int i0 = 0; i0 < n16; i0 += WG_THREADS * 8) {
-            uint4 tmp[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) tmp[j] = src[min(i0 + j * WG_THREADS + tid, n16 - 1)];
+        for (int j = 0; j < A_PER_T; j++) dst[min(j * WG_THREADS + tid, n16 - 1)] = a_tmp[j];
+        for (int i = A_PER_T * WG_THREADS + tid; i < n16; i += WG_THREADS) dst[i] = a_src[i];
+        if constexpr (C::MINS) {
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int i = i0 + j * WG_THREADS + tid;
-                if (i < n16) dst[i] = tmp[j];
-            }
+            for (int j = 0; j < 2; j++) x_lds[min(j * WG_THREADS + tid, n_x - 1)] = x_tmp[j];
+            for (int i = 2 * WG_THREADS + tid; i < n_x; i += WG_THREADS) x_lds[i] = xs_src[i];
         }
-        if constexpr (C::MINS)
-            for (int i = tid; i < nu * 8 * TOK; i += WG_THREADS) x_lds[i] = xs[(size_t)u0 * 8 * TOK + i];
-        for (int i = tid; i < nu * TOK; i += WG_THREADS) i_lds[i] = invs[(size_t)u0 * TOK + i];
+        i_lds[min(tid, n_i - 1)] = i_tmp;
+        for (int i = WG_THREADS + tid; i < n_i; i += WG_THREADS) i_lds[i] = i_src[i];
     }
     __syncthreads();
 
-    // 3. stream items through the MFMA pipe; a row group's epilogue follows
+    // 4. stream items through the MFMA pipe; a row group's epilogue follows
     //    its last unit
     Acc<MT, SPLIT> A;
     auto reset = [&]() {
@@ -497,43 +643,47 @@ void gemm_q_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     };
     reset();
     const uint8_t *a_lane = a_lds + lane * (QT == QT_Q6_K ? 8 : 16);
-    for (int ib = 0; ib < n_items; ib += R) {
+    int cj = 0, cu = 0;  // consume position
+    auto consume = [&](Unit<QT> &b) {
+        if constexpr (!PK) finish_unit<QT>(b);
+        compute_unit<QT, MT, SPLIT>(b, a_lane + (size_t)cu * UNIT_A, x_lds + (size_t)cu * 8 * TOK,
+                                    i_lds + (size_t)cu * TOK, g, A);
+        if (++cu == nu) {
+            // epilogue: lane values are row r, tokens lane_token(mt, g, u);
+            // stores only (an accumulating call reduces through part)
+            const int r = ((int)blockIdx.x + G * cj) * ROWS_PER_WG + row_in;
+            if (r < N) {
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                    for (int u = 0; u < TPL; u++) {
+                        const int t = lane_token<SPLIT>(mt, g, u);
+                        if (t >= M) continue;
+                        float v = SPLIT ? (A.acc[mt][2 * u] + A.acc[mt][2 * u + 1]) : A.acc[mt][u];
+                        if constexpr (C::MINS) v = v - A.macc[mt][u];
+                        if (part == nullptr)
+                            Y[(size_t)t * N + r] = v;
+                        else
+                            part[((size_t)blockIdx.y * M + t) * N + r] = v;
+                    }
+            }
+            reset();
+            cu = 0;
+            ++cj;
+        }
+    };
+    const int n_full = n_items - n_items % R;
+    for (int ib = 0; ib < n_full; ib += R) {
 #pragma unroll
         for (int p = 0; p < R; p++) {
-            const int it = ib + p;
-            if (it < n_items) {
-                const int nxt = it + R - 1;
-                if (nxt < n_items) load_unit<QT>(item_ptr(nxt), g, item_nblk(nxt), buf[(p + R - 1) % R]);
-                const int uu = it % nu;
-                finish_unit<QT>(buf[p]);
-                compute_unit<QT, MT, SPLIT>(buf[p], a_lane + (size_t)uu * UNIT_A, x_lds + (size_t)uu * 8 * TOK,
-                                            i_lds + (size_t)uu * TOK, g, A);
-                if (uu == nu - 1) {
-                    // epilogue: lane values are rows row0 + n_in, tokens lane_token(mt, g, u)
-                    const int rg = blockIdx.x + G * (it / nu);
-                    const int r = rg * ROWS_PER_WG + wave * 16 + n_in;
-                    if (r < N) {
-#pragma unroll
-                        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                            for (int u = 0; u < TPL; u++) {
-                                const int t = lane_token<SPLIT>(mt, g, u);
-                                if (t >= M) continue;
-                                float v = SPLIT ? (A.acc[mt][2 * u] + A.acc[mt][2 * u + 1]) : A.acc[mt][u];
-                                if constexpr (C::MINS) v = v - A.macc[mt][u];
-                                if (S == 1) {
-                                    float *dst = Y + (size_t)t * N + r;
-                                    *dst = accum ? *dst + v : v;
-                                } else {
-                                    part[((size_t)blockIdx.y * M + t) * N + r] = v;
-                                }
-                            }
-                    }
-                    reset();
-                }
-            }
+            load_next(buf[(p + R - 1) % R]);
+            consume(buf[p]);
         }
     }
+    // the last n_items % R items are already in buf[0 ..]
+#pragma unroll
+    for (int p = 0; p < R - 1; p++)
+        if (n_full + p < n_items) consume(buf[p]);
 }
 
 // Y[i] (+)= sum_s part[s][i] in slice order, i over M*N outputs.
@@ -562,25 +712,280 @@ __global__ __launch_bounds__(256) void reduce_kernel(const float *__restrict__ p
     }
 }
 
-template <int QT, int MT, bool SPLIT>
+// ---------------------------------------------------------------- streaming kernel (one token tile)
+// With one token tile (M <= 8 fp32-accurate, M <= 16 half) the activation
+// operand of a few units fits in VGPRs, so the weight stream needs no LDS.
+// Workgroup (w, s) of NW waves covers K-units [s*NW*UPS, (s+1)*NW*UPS):
+// wave i holds the A operand of units s*NW*UPS + i*UPS + [0, UPS) and streams
+// the 16-row tiles w, w + G, w + 2G, ... of those units through a ring of 4
+// units issued 3 ahead. At the end of a tile the NW partial tiles meet in LDS
+// and wave (tile % NW) sums them in wave order (deterministic).
+template <int QT> struct AReg;
+template <> struct AReg<QT_Q4_K> { h8 f[8]; h4 mins; };
+template <> struct AReg<QT_Q5_K> { h8 f[8]; h4 mins; };
+template <> struct AReg<QT_Q6_K> { h4 f[16]; };
+template <> struct AReg<QT_Q8_0> { h8 f[8]; };
+
+// One unit against register operands. acc: scaled dot products, macc: the
+// Q4_K/Q5_K min term / 32 (both in the MFMA D layout: slot 4g + v, row n).
+// A dead unit (past the end of K) contributes exactly zero.
+template <int QT, bool SPLIT>
+__device__ __forceinline__ void compute_v(const Unit<QT> &r, const AReg<QT> &a, const float *inv, int g, bool live,
+                                          f4 &acc, f4 &macc) {
+    if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {
+        float d = half_bits(r.hdr.x), dmin = half_bits(r.hdr.x >> 16);
+        if (!live) { d = 0.f; dmin = 0.f; }
+        const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;
+        const uint32_t sc_lo = s0 & 0x3f3f3f3fu, m_lo = s1 & 0x3f3f3f3fu;
+        const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
+        const uint32_t m_hi = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
+        const int sh = 16 * (g >> 1);
+        const h2 neg1024 = as_h2(0xE400E400u);
+        h2 hs[4], ns[4];
+        hs[0] = h2_of_small((sc_lo >> sh) & 0xffu);
+        hs[1] = h2_of_small((sc_lo >> (sh + 8)) & 0xffu);
+        hs[2] = h2_of_small((sc_hi >> sh) & 0xffu);
+        hs[3] = h2_of_small((sc_hi >> (sh + 8)) & 0xffu);
+#pragma unroll
+        for (int i = 0; i < 4; i++) ns[i] = hs[i] * neg1024;
+        f4 c = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            const int ah = m >> 2, b = (m >> 1) & 1, hw = m & 1;
+            const uint4 Q = ah ? r.q1 : r.q0;
+            const uint32_t x0 = hw ? Q.z : Q.x, x1 = hw ? Q.w : Q.y;
+            uint32_t n0 = (b ? (x0 >> 4) : x0) & 0x0f0f0f0fu;
+            uint32_t n1 = (b ? (x1 >> 4) : x1) & 0x0f0f0f0fu;
+            if constexpr (QT == QT_Q5_K) {
+                const int hb = 4 * ah + 2 * (g >> 1) + b;
+                const uint32_t h0 = hw ? r.qh.z : r.qh.x, h1 = hw ? r.qh.w : r.qh.y;
+                n0 |= ((h0 >> hb) & 0x01010101u) << 4;
+                n1 |= ((h1 >> hb) & 0x01010101u) << 4;
+            }
+            c = mfma32(a.f[m], b_frag_scaled(n0, n1, hs[2 * ah + b], ns[2 * ah + b]), c);
+        }
+        // min term on the matrix core: B = m_s of this row for s = 4g..4g+3
+        // (lane groups 0, 1), zero for lane groups 2, 3
+        const uint32_t mw = g == 0 ? m_lo : (g == 1 ? m_hi : 0u);
+        const h2 p0 = as_h2(pair_lo(mw)) + neg1024, p1 = as_h2(pair_hi(mw)) + neg1024;
+        h4 bm;
+        bm[0] = p0[0]; bm[1] = p0[1]; bm[2] = p1[0]; bm[3] = p1[1];
+        const f4 cm = mfma16(a.mins, bm, f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const float iv = inv[acc_token_u<SPLIT>(v)];
+            acc[v] = __builtin_fmaf(d * iv, c[v], acc[v]);
+            macc[v] = __builtin_fmaf(dmin * iv, cm[v], macc[v]);
+        }
+    } else if constexpr (QT == QT_Q6_K) {
+        const float d = live ? half_bits(r.d) : 0.f;
+        float dinv[SPLIT ? 2 : 4];
+#pragma unroll
+        for (int u = 0; u < (SPLIT ? 2 : 4); u++) dinv[u] = d * inv[u];
+        const h2 off = as_h2(0xE420E420u);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int n = i >> 1, h = i & 1;
+            uint32_t q[4];
+            q[0] = (r.a[i] & 0x0f0f0f0fu) | ((r.h[i] & 0x03030303u) << 4);
+            q[1] = (r.b[i] & 0x0f0f0f0fu) | (((r.h[i] >> 2) & 0x03030303u) << 4);
+            q[2] = ((r.a[i] >> 4) & 0x0f0f0f0fu) | (((r.h[i] >> 4) & 0x03030303u) << 4);
+            q[3] = ((r.b[i] >> 4) & 0x0f0f0f0fu) | (((r.h[i] >> 6) & 0x03030303u) << 4);
+#pragma unroll
+            for (int qq = 0; qq < 4; qq++) {
+                const int sb = 8 * n + 2 * qq + h;
+                const h2 p0 = as_h2(pair_lo(q[qq])) + off, p1 = as_h2(pair_hi(q[qq])) + off;
+                h4 b;
+                b[0] = p0[0]; b[1] = p0[1]; b[2] = p1[0]; b[3] = p1[1];
+                const uint32_t scw = (sb >> 2) == 0 ? r.sc.x : (sb >> 2) == 1 ? r.sc.y : (sb >> 2) == 2 ? r.sc.z : r.sc.w;
+                const float scf = (float)(int)(int8_t)((scw >> (8 * (sb & 3))) & 0xffu);
+                const f4 c = mfma16(a.f[sb], b, f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    acc[v] = __builtin_fmaf(dinv[acc_token_u<SPLIT>(v)] * scf, c[v], acc[v]);
+            }
+        }
+    } else {
+        const h2 off = as_h2(0xE480E480u);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float d = live ? half_bits(r.d[i]) : 0.f;
+            const uint32_t t0 = r.w0[i] ^ 0x80808080u, t1 = r.w1[i] ^ 0x80808080u;
+            const h2 p0 = as_h2(pair_lo(t0)) + off, p1 = as_h2(pair_hi(t0)) + off;
+            const h2 p2 = as_h2(pair_lo(t1)) + off, p3 = as_h2(pair_hi(t1)) + off;
+            h8 b;
+            b[0] = p0[0]; b[1] = p0[1]; b[2] = p1[0]; b[3] = p1[1];
+            b[4] = p2[0]; b[5] = p2[1]; b[6] = p3[0]; b[7] = p3[1];
+            const f4 c = mfma32(a.f[i], b, f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                acc[v] = __builtin_fmaf(d * inv[acc_token_u<SPLIT>(v)], c[v], acc[v]);
+        }
+    }
+}
+
+template <int QT, int NW, int UPS, bool SPLIT, bool PK>
+__global__ __launch_bounds__(NW * 64, 2)
+void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, int N, int K, int accum,
+                   const uint8_t *__restrict__ afrag, const float *__restrict__ invs,
+                   const uint8_t *__restrict__ mfrag, float *__restrict__ part) {
+    using C = GemmCfg<QT>;
+    constexpr int TOK = SPLIT ? 8 : 16;
+    constexpr int TPL = SPLIT ? 2 : 4;
+    constexpr int UNIT_BYTES = (QT == QT_Q8_0) ? 8 * 34 : C::BB;
+    constexpr int R = 4;
+    static_assert(R % UPS == 0, "ring positions must map to fixed units");
+    __shared__ __align__(16) float red[2][NW][64][TPL];
+
+    const int n_units = (K + UNIT - 1) / UNIT;
+    const int n_tiles = (N + 15) / 16;
+    const int G = gridDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n_in = lane & 15, g = lane >> 4;
+    const int my_tiles = (n_tiles - 1 - (int)blockIdx.x) / G + 1;  // the plan keeps G <= n_tiles
+    const int unit0 = ((int)blockIdx.y * NW + wave) * UPS;
+    const size_t row_bytes = (size_t)(K / C::QK) * C::BB;
+    const int tail_blk = (QT == QT_Q8_0 && (K % UNIT)) ? (K % UNIT) / 32 : 8;
+
+    // 1. this wave's A operand (prepared in the MFMA lane layout)
+    AReg<QT> a[UPS];
+    float inv[UPS][TPL];
+    bool live[UPS];
+#pragma unroll
+    for (int u = 0; u < UPS; u++) {
+        live[u] = unit0 + u < n_units;
+        const int un = min(unit0 + u, n_units - 1);
+        const uint8_t *src = afrag + (size_t)un * UNIT_A1;
+        if constexpr (QT == QT_Q6_K) {
+#pragma unroll
+            for (int c = 0; c < 16; c++) a[u].f[c] = *(const h4 *)(src + c * 512 + lane * 8);
+        } else {
+#pragma unroll
+            for (int c = 0; c < 8; c++) a[u].f[c] = *(const h8 *)(src + c * 1024 + lane * 16);
+        }
+        if constexpr (C::MINS) a[u].mins = *(const h4 *)(mfrag + (size_t)un * 512 + lane * 8);
+#pragma unroll
+        for (int k = 0; k < TPL; k++) inv[u][k] = invs[(size_t)un * TOK + lane_token<SPLIT>(0, g, k)];
+    }
+
+    // 2. weight stream over items (tile j, unit u), u fastest; past the last
+    //    tile the loads repeat the last one so every step issues one batch
+    auto load_item = [&](int j, int u, Unit<QT> &b) {
+        j = min(j, my_tiles - 1);
+        const int un = min(unit0 + u, n_units - 1);
+        if constexpr (PK) {
+            const int tile = (int)blockIdx.x + G * j;
+            load_unit_packed<QT>(W + ((size_t)tile * n_units + un) * Packed<QT>::CHUNK, lane, b);
+        } else {
+            const int row = min(((int)blockIdx.x + G * j) * 16 + n_in, N - 1);
+            load_unit<QT>(W + (size_t)row * row_bytes + (size_t)un * UNIT_BYTES, g, un == n_units - 1 ? tail_blk : 8,
+                          b);
+        }
+    };
+    Unit<QT> buf[R];
+#pragma unroll
+    for (int p = 0; p < R - 1; p++) load_item(p / UPS, p % UPS, buf[p]);
+
+    f4 acc = f4{0.f, 0.f, 0.f, 0.f}, macc = f4{0.f, 0.f, 0.f, 0.f};
+    auto consume = [&](int j, int u, Unit<QT> &b) {
+        if constexpr (!PK) finish_unit<QT>(b);
+        compute_v<QT, SPLIT>(b, a[u], inv[u], g, live[u], acc, macc);
+        if (u == UPS - 1) {
+            float vals[TPL];
+#pragma unroll
+            for (int k = 0; k < TPL; k++) {
+                float v = SPLIT ? acc[2 * k] + acc[2 * k + 1] : acc[k];
+                if constexpr (C::MINS) v -= 32.0f * (SPLIT ? macc[2 * k] + macc[2 * k + 1] : macc[k]);
+                vals[k] = v;
+            }
+            float *slot = &red[j & 1][wave][lane][0];
+#pragma unroll
+            for (int k = 0; k < TPL; k++) slot[k] = vals[k];
+            acc = f4{0.f, 0.f, 0.f, 0.f};
+            macc = f4{0.f, 0.f, 0.f, 0.f};
+            __syncthreads();
+            if (wave == j % NW) {
+                float sum[TPL];
+#pragma unroll
+                for (int k = 0; k < TPL; k++) sum[k] = red[j & 1][0][lane][k];
+#pragma unroll
+                for (int w = 1; w < NW; w++)
+#pragma unroll
+                    for (int k = 0; k < TPL; k++) sum[k] += red[j & 1][w][lane][k];
+                const int r = ((int)blockIdx.x + G * j) * 16 + n_in;
+                if (r < N) {
+#pragma unroll
+                    for (int k = 0; k < TPL; k++) {
+                        const int t = lane_token<SPLIT>(0, g, k);
+                        if (t >= M) continue;
+                        if (part != nullptr) {
+                            part[((size_t)blockIdx.y * M + t) * N + r] = sum[k];
+                        } else {
+                            float *dst = Y + (size_t)t * N + r;
+                            *dst = accum ? *dst + sum[k] : sum[k];
+                        }
+                    }
+                }
+            }
+        }
+    };
+    const int n_items = my_tiles * UPS;
+    const int n_full = n_items - n_items % R;
+    for (int ib = 0; ib < n_full; ib += R) {
+        const int jb = ib / UPS;
+#pragma unroll
+        for (int p = 0; p < R; p++) {
+            load_item(jb + (p + R - 1) / UPS, (p + R - 1) % UPS, buf[(p + R - 1) % R]);
+            consume(jb + p / UPS, p % UPS, buf[p]);
+        }
+    }
+    {
+        const int jb = n_full / UPS;
+#pragma unroll
+        for (int p = 0; p < R - 1; p++)
+            if (n_full + p < n_items) consume(jb + p / UPS, p % UPS, buf[p]);
+    }
+}
+
+template <int QT, int NW, int UPS, bool SPLIT, bool PK>
+hipError_t launch_v(const uint8_t *W, const float *X, float *Y, int M, int N, int K, int S, int G, int accum,
+                    uint8_t *afrag, float *inv, uint8_t *mfrag, float *part, hipStream_t st) {
+    using C = GemmCfg<QT>;
+    constexpr int TOK = SPLIT ? 8 : 16;
+    const int n_units = (K + UNIT - 1) / UNIT;
+    prep_kernel<QT == QT_Q6_K ? 1 : QT == QT_Q8_0 ? 2 : 0, 1, SPLIT, C::MINS>
+        <<<dim3(n_units, TOK / 8), 256, 0, st>>>(X, M, K, afrag, nullptr, inv, mfrag);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    gemm_v_kernel<QT, NW, UPS, SPLIT, PK><<<dim3(G, S), NW * 64, 0, st>>>(W, Y, M, N, K, accum, afrag, inv, mfrag,
+                                                                      S > 1 ? part : nullptr);
+    e = hipGetLastError();
+    if (e != hipSuccess || S == 1) return e;
+    const int64_t MN = (int64_t)M * N;
+    reduce_kernel<<<(unsigned)((MN + 1023) / 1024), 256, 0, st>>>(part, Y, S, MN, accum);
+    return hipGetLastError();
+}
+
+template <int QT, int MT, bool SPLIT, bool PK>
 hipError_t launch_t(const uint8_t *W, const float *X, float *Y, int M, int N, int K, int ups, int S, int G, int accum,
                     uint8_t *afrag, float *xs, float *inv, float *part, hipStream_t st) {
     using C = GemmCfg<QT>;
     constexpr int TOK = MT * (SPLIT ? 8 : 16);
     const int n_units = (K + UNIT - 1) / UNIT;
-    prep_kernel<QT == QT_Q6_K ? 1 : QT == QT_Q8_0 ? 2 : 0, MT, SPLIT, C::MINS><<<dim3(n_units, TOK / 8), 256, 0, st>>>(X, M, K, afrag, xs, inv);
+    prep_kernel<QT == QT_Q6_K ? 1 : QT == QT_Q8_0 ? 2 : 0, MT, SPLIT, C::MINS><<<dim3(n_units, TOK / 8), 256, 0, st>>>(X, M, K, afrag, xs, inv, nullptr);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const size_t lds = (size_t)ups * UNIT_A1 * MT + (C::MINS ? (size_t)ups * 8 * TOK * 4 : 0) + (size_t)ups * TOK * 4;
     if (lds > 65536) {
-        e = hipFuncSetAttribute((const void *)gemm_q_kernel<QT, MT, SPLIT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        e = hipFuncSetAttribute((const void *)gemm_q_kernel<QT, MT, SPLIT, PK>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds);
         if (e != hipSuccess) return e;
     }
-    gemm_q_kernel<QT, MT, SPLIT><<<dim3(G, S), WG_THREADS, lds, st>>>(W, Y, M, N, K, ups, S, accum, afrag, xs, inv,
-                                                                     part);
+    const bool reduce = S > 1 || accum;
+    gemm_q_kernel<QT, MT, SPLIT, PK><<<dim3(G, S), WG_THREADS, lds, st>>>(W, Y, M, N, K, ups, S, afrag, xs, inv,
+                                                                     reduce ? part : nullptr);
     e = hipGetLastError();
-    if (e != hipSuccess || S == 1) return e;
+    if (e != hipSuccess || !reduce) return e;
     const int64_t MN = (int64_t)M * N;
     reduce_kernel<<<(unsigned)((MN + 1023) / 1024), 256, 0, st>>>(part, Y, S, MN, accum);
     return hipGetLastError();
@@ -592,10 +997,12 @@ hipError_t launch_t(const uint8_t *W, const float *X, float *Y, int M, int N, in
 struct GemmPlan {
     bool split;      // fp32-accurate two-limb mode
     int MT;          // MFMA token tiles (16 slots each)
-    int ups;         // 256-element units per K-slice
+    bool stream;     // one token tile: streaming kernel with register operands
+    int NW, UPS;     // streaming kernel: waves per workgroup, units per wave
+    int ups;         // LDS kernel: 256-element units per K-slice
     int S;           // K-slices (grid.y)
-    int G;           // persistent workgroups per K-slice (grid.x)
-    size_t off_xs, off_inv, off_part, ws_bytes;
+    int G;           // workgroups per K-slice (grid.x)
+    size_t off_xs, off_inv, off_mfrag, off_part, ws_bytes;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -611,25 +1018,54 @@ static GemmPlan plan_gemm(int qt, int M, int N, int K, int flags) {
     p.split = force_f32 ? true : force_half ? false : (M < 16);
     p.MT = p.split ? (M + 7) / 8 : (M + 15) / 16;
     const int n_units = (K + UNIT - 1) / UNIT;
-    const int rowgroups = (N + ROWS_PER_WG - 1) / ROWS_PER_WG;
-    // tuning overrides: IHIP_GEMM_LDS_A (A-operand bytes per workgroup),
-    // IHIP_GEMM_WGS (target resident workgroups)
-    static const int lds_a = env_int("IHIP_GEMM_LDS_A", 32768);
-    static const int target = env_int("IHIP_GEMM_WGS", 1024);
-    const int ups_max = std::max(1, lds_a / (UNIT_A1 * p.MT));
-    p.S = (n_units + ups_max - 1) / ups_max;
-    p.ups = (n_units + p.S - 1) / p.S;
-    p.S = (n_units + p.ups - 1) / p.ups;
-    p.G = std::max(1, std::min(rowgroups, (target + p.S - 1) / p.S));
     const int TOK = p.MT * (p.split ? 8 : 16);
     const bool mins = (qt == QT_Q4_K || qt == QT_Q5_K);
+    // tuning overrides: IHIP_GEMM_WGS (target workgroups), IHIP_GEMM_LDS_A
+    // (A-operand bytes per workgroup, LDS kernel), IHIP_STREAM_UPS (streaming
+    // kernel units per wave), IHIP_STREAM=0 (LDS kernel)
+    static const int target = env_int("IHIP_GEMM_WGS", 1024);
+    static const int lds_a = env_int("IHIP_GEMM_LDS_A", 32768);
+    static const int use_stream = env_int("IHIP_STREAM", 1);
+    static const int env_ups = env_int("IHIP_STREAM_UPS", 0);
+    p.stream = use_stream && p.MT == 1;
+    if (p.stream) {
+        // K per workgroup NW*UPS units; prefer one K-slice (no partials) with
+        // the fewest units per wave that still covers K, else the largest
+        // chunk that divides K
+        const int nw = 4;
+        int ups = 4;
+        if (env_ups == 1 || env_ups == 2 || env_ups == 4) {
+            ups = env_ups;
+        } else {
+            ups = 4;
+            for (int u : {1, 2, 4})
+                if (nw * u >= n_units) { ups = u; break; }
+            if (nw * ups < n_units)
+                for (int u : {4, 2, 1})
+                    if (n_units % (nw * u) == 0) { ups = u; break; }
+        }
+        p.NW = nw;
+        p.UPS = ups;
+        p.S = (n_units + nw * ups - 1) / (nw * ups);
+        const int n_tiles = (N + 15) / 16;
+        p.G = std::max(1, std::min(n_tiles, (target + p.S - 1) / p.S));
+    } else {
+        const int rowgroups = (N + ROWS_PER_WG - 1) / ROWS_PER_WG;
+        const int ups_max = std::max(1, lds_a / (UNIT_A1 * p.MT));
+        p.S = (n_units + ups_max - 1) / ups_max;
+        p.ups = (n_units + p.S - 1) / p.S;
+        p.S = (n_units + p.ups - 1) / p.ups;
+        p.G = std::max(1, std::min(rowgroups, (target + p.S - 1) / p.S));
+    }
     size_t o = align256((size_t)n_units * UNIT_A1 * p.MT);
     p.off_xs = o;
-    o += mins ? align256((size_t)n_units * 8 * TOK * 4) : 0;
+    o += (mins && !p.stream) ? align256((size_t)n_units * 8 * TOK * 4) : 0;
     p.off_inv = o;
     o += align256((size_t)n_units * TOK * 4);
+    p.off_mfrag = o;
+    o += (mins && p.stream) ? align256((size_t)n_units * 512) : 0;
     p.off_part = o;
-    o += p.S > 1 ? align256((size_t)p.S * M * N * 4) : 0;
+    o += align256((size_t)p.S * M * N * 4);  // partials (split-K or accumulate)
     p.ws_bytes = o;
     return p;
 }
@@ -647,11 +1083,21 @@ size_t gemm_ws_bytes(int qt, int M, int N, int K, int flags) {
     return plan_gemm(qt, m0, N, K, f).ws_bytes;
 }
 
-template <int QT>
+template <int QT, bool PK>
 static hipError_t dispatch_mt(const GemmPlan &p, const uint8_t *W, const float *X, float *Y, int M, int N, int K,
                               int accum, uint8_t *ws, hipStream_t st) {
     float *xs = (float *)(ws + p.off_xs), *inv = (float *)(ws + p.off_inv), *part = (float *)(ws + p.off_part);
-#define L(mt, sp) return launch_t<QT, mt, sp>(W, X, Y, M, N, K, p.ups, p.S, p.G, accum, ws, xs, inv, part, st)
+    uint8_t *mfrag = ws + p.off_mfrag;
+    if (p.stream) {
+#define V(u, sp) return launch_v<QT, 4, u, sp, PK>(W, X, Y, M, N, K, p.S, p.G, accum, ws, inv, mfrag, part, st)
+        if (p.split) {
+            switch (p.UPS) { case 1: V(1, true); case 2: V(2, true); default: V(4, true); }
+        } else {
+            switch (p.UPS) { case 1: V(1, false); case 2: V(2, false); default: V(4, false); }
+        }
+#undef V
+    }
+#define L(mt, sp) return launch_t<QT, mt, sp, PK>(W, X, Y, M, N, K, p.ups, p.S, p.G, accum, ws, xs, inv, part, st)
     if (p.split) {
         switch (p.MT) {
         case 1: L(1, true); case 2: L(2, true); case 3: L(3, true); case 4: L(4, true);
@@ -665,6 +1111,31 @@ static hipError_t dispatch_mt(const GemmPlan &p, const uint8_t *W, const float *
     return hipErrorInvalidValue;
 }
 
+size_t packed_bytes(int qt, int N, int K) {
+    const size_t tiles = (size_t)(N + 15) / 16, units = (size_t)(K + UNIT - 1) / UNIT;
+    switch (qt) {
+    case QT_Q4_K: return tiles * units * Packed<QT_Q4_K>::CHUNK;
+    case QT_Q5_K: return tiles * units * Packed<QT_Q5_K>::CHUNK;
+    case QT_Q6_K: return tiles * units * Packed<QT_Q6_K>::CHUNK;
+    case QT_Q8_0: return tiles * units * Packed<QT_Q8_0>::CHUNK;
+    }
+    return 0;
+}
+
+hipError_t launch_pack(int qt, const void *W, void *P, int N, int K, hipStream_t st) {
+    const dim3 grid((K + UNIT - 1) / UNIT, (N + 15) / 16);
+    const uint8_t *w = (const uint8_t *)W;
+    uint8_t *p = (uint8_t *)P;
+    switch (qt) {
+    case QT_Q4_K: pack_kernel<QT_Q4_K><<<grid, 64, 0, st>>>(w, N, K, p); break;
+    case QT_Q5_K: pack_kernel<QT_Q5_K><<<grid, 64, 0, st>>>(w, N, K, p); break;
+    case QT_Q6_K: pack_kernel<QT_Q6_K><<<grid, 64, 0, st>>>(w, N, K, p); break;
+    case QT_Q8_0: pack_kernel<QT_Q8_0><<<grid, 64, 0, st>>>(w, N, K, p); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm(int qt, const void *W, const float *X, float *Y, int M, int N, int K, int flags, void *ws,
                        hipStream_t st) {
     const int m0 = launch_m(M, flags);
@@ -675,13 +1146,17 @@ hipError_t launch_gemm(int qt, const void *W, const float *X, float *Y, int M, i
     }
     const GemmPlan p = plan_gemm(qt, M, N, K, flags);
     const int accum = (flags & 4) ? 1 : 0;
+    const bool pk = (flags & 8) != 0;
     const uint8_t *w = (const uint8_t *)W;
     uint8_t *wsp = (uint8_t *)ws;
+#define D(q) return pk ? dispatch_mt<q, true>(p, w, X, Y, M, N, K, accum, wsp, st) \
+                       : dispatch_mt<q, false>(p, w, X, Y, M, N, K, accum, wsp, st)
     switch (qt) {
-    case QT_Q4_K: return dispatch_mt<QT_Q4_K>(p, w, X, Y, M, N, K, accum, wsp, st);
-    case QT_Q5_K: return dispatch_mt<QT_Q5_K>(p, w, X, Y, M, N, K, accum, wsp, st);
-    case QT_Q6_K: return dispatch_mt<QT_Q6_K>(p, w, X, Y, M, N, K, accum, wsp, st);
-    case QT_Q8_0: return dispatch_mt<QT_Q8_0>(p, w, X, Y, M, N, K, accum, wsp, st);
+    case QT_Q4_K: D(QT_Q4_K);
+    case QT_Q5_K: D(QT_Q5_K);
+    case QT_Q6_K: D(QT_Q6_K);
+    case QT_Q8_0: D(QT_Q8_0);
     }
+#undef D
     return hipErrorInvalidValue;
 }

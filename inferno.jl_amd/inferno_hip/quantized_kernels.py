@@ -21,7 +21,7 @@ import numpy as np
 from . import _lib
 from .formats import BLOCK_BYTES, BLOCK_ELEMS, Q4_K, Q5_K, Q6_K, Q8_0, NAMES
 
-GEMM_AUTO, GEMM_F32, GEMM_HALF, GEMM_ACCUM = 0, 1, 2, 4
+GEMM_AUTO, GEMM_F32, GEMM_HALF, GEMM_ACCUM, GEMM_PACKED = 0, 1, 2, 4, 8
 
 
 def quant_kernels_available() -> bool:
@@ -114,6 +114,23 @@ def gemm_ws_bytes(qtype: int, m: int, n: int, k: int, flags: int = GEMM_AUTO) ->
     nb = C.c_size_t()
     _lib.check(_lib.load().ihip_gemm_q_ws_bytes(qtype, m, n, k, flags, C.byref(nb)))
     return max(int(nb.value), 16)
+
+
+def packed_bytes(qtype: int, n: int, k: int) -> int:
+    """Size of the packed layout of an [n x k] matrix."""
+    nb = C.c_size_t()
+    _lib.check(_lib.load().ihip_packed_bytes(qtype, n, k, C.byref(nb)))
+    return int(nb.value)
+
+
+def pack_weights(qtype: int, w_dev, n: int, k: int, out=None, stream=None):
+    """Repack a device GGUF matrix [n x k] into the tile-contiguous layout
+    that gemm_q reads with GEMM_PACKED (done once, at model load)."""
+    import torch
+    if out is None:
+        out = torch.empty(packed_bytes(qtype, n, k), dtype=torch.uint8, device=w_dev.device)
+    _lib.check(_lib.load().ihip_pack_weights(qtype, _ptr(w_dev), _ptr(out), n, k, _stream(stream)))
+    return out
 
 
 def dequant(qtype: int, w_dev, n_elems: int, stream=None):
