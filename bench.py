@@ -67,6 +67,9 @@ class Model:
                 if L < keep_gguf:
                     hw[key] = g.cpu().numpy()
                 del g
+            # q and k/v rows share the input: one matrix [q; k; v] (the packed
+            # layout concatenates along tiles)
+            lw["qkv"] = torch.cat([lw.pop("q"), lw.pop("kv")])
             self.layers.append(lw)
             if L < keep_gguf:
                 self.host_gguf.append(hw)
@@ -93,15 +96,12 @@ class VerifyStep:
         st = ih.synth.stream_for
         self.x0 = ih.quantized_kernels.synth_gaussian(st(SEED, "x0"), M * H).view(M, H)
         self.x = torch.empty_like(self.x0)
-        self.h = torch.empty_like(self.x0)
-        self.q = torch.empty((M, NQ), device=dev)
-        self.kv = torch.empty((M, 2 * NKV), device=dev)
+        self.qkv = torch.empty((M, NQ + 2 * NKV), device=dev)
         self.gu = torch.empty((M, 2 * FF), device=dev)
-        self.hm = torch.empty((M, FF), device=dev)
         self.logits = torch.empty((M, VOCAB), device=dev)
         gws = ih.quantized_kernels.gemm_ws_bytes
         fl = ih.GEMM_F32 | ih.GEMM_PACKED | ih.GEMM_ACCUM
-        wsb = max(gws(F.Q4_K, M, NQ, H, fl), gws(F.Q4_K, M, 2 * NKV, H, fl), gws(F.Q4_K, M, H, NQ, fl),
+        wsb = max(gws(F.Q4_K, M, NQ + 2 * NKV, H, fl), gws(F.Q4_K, M, H, NQ, fl),
                   gws(F.Q4_K, M, 2 * FF, H, fl), gws(F.Q6_K, M, H, FF, fl), gws(F.Q6_K, M, VOCAB, H, fl))
         self.ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
         # draft side (inputs of the verify step): draft logits, draft tokens, uniforms
@@ -120,22 +120,21 @@ class VerifyStep:
         self.out_n = torch.zeros(1, dtype=torch.int32, device=dev)
 
     def run(self):
+        """One verify step: per layer RMSNorm -> [q; k; v] -> o (+= into x)
+        -> RMSNorm -> [gate; up] -> SiLU gating -> down (+= into x); final
+        RMSNorm -> lm_head -> accept. RMSNorm and SiLU gating run fused into
+        the matmul that consumes them."""
         ih, F, M = self.ih, self.ih.formats, self.M
-        gemm = ih.gemm_q
+        ex = ih.gemm_q_ex
         f32 = ih.GEMM_F32 | ih.GEMM_PACKED
         acc = f32 | ih.GEMM_ACCUM
         self.x.copy_(self.x0)
         for lw in self.model.layers:
-            ih.rmsnorm(self.x, out=self.h)
-            gemm(F.Q4_K, lw["q"], self.h, NQ, H, flags=f32, out=self.q, ws=self.ws)
-            gemm(F.Q4_K, lw["kv"], self.h, 2 * NKV, H, flags=f32, out=self.kv, ws=self.ws)
-            gemm(F.Q4_K, lw["o"], self.q, H, NQ, flags=acc, out=self.x, ws=self.ws)
-            ih.rmsnorm(self.x, out=self.h)
-            gemm(F.Q4_K, lw["gu"], self.h, 2 * FF, H, flags=f32, out=self.gu, ws=self.ws)
-            ih.quantized_kernels.silu_mul(self.gu, FF, out=self.hm)
-            gemm(F.Q6_K, lw["down"], self.hm, H, FF, flags=acc, out=self.x, ws=self.ws)
-        ih.rmsnorm(self.x, out=self.h)
-        gemm(F.Q6_K, self.model.lm, self.h, VOCAB, H, flags=f32, out=self.logits, ws=self.ws)
+            ex(F.Q4_K, lw["qkv"], self.x, NQ + 2 * NKV, H, act=ih.ACT_RMSNORM, flags=f32, out=self.qkv, ws=self.ws)
+            ex(F.Q4_K, lw["o"], self.qkv[:, :NQ], H, NQ, flags=acc, out=self.x, ws=self.ws)
+            ex(F.Q4_K, lw["gu"], self.x, 2 * FF, H, act=ih.ACT_RMSNORM, flags=f32, out=self.gu, ws=self.ws)
+            ex(F.Q6_K, lw["down"], self.gu, H, FF, act=ih.ACT_SILU_MUL, flags=acc, out=self.x, ws=self.ws)
+        ex(F.Q6_K, self.model.lm, self.x, VOCAB, H, act=ih.ACT_RMSNORM, flags=f32, out=self.logits, ws=self.ws)
         ih.spec_accept(self.logits.view(1, M, VOCAB), self.drf.view(1, self.k, VOCAB), self.draft, self.T,
                        self.u_acc, self.u_res, self.u_bonus, out_tok=self.out_tok, out_n=self.out_n,
                        ws=self.acc_ws)

@@ -39,6 +39,13 @@ extern "C" {
 #define IHIP_GEMM_HALF   2  /* force single-limb fp16 MFMA, rel-L2 <= 1e-2 */
 #define IHIP_GEMM_ACCUM  4  /* y += W x (y is not cleared first) */
 #define IHIP_GEMM_PACKED 8  /* w_dev is in the packed layout of ihip_pack_weights */
+#define IHIP_GEMM_REUSE 16  /* ihip_gemm_q_ex: the activations prepared in ws by the
+                               previous call (same x, act, M, K, flags) are reused */
+
+/* ---- ihip_gemm_q_ex input transforms ---- */
+#define IHIP_ACT_PLAIN    0  /* x */
+#define IHIP_ACT_RMSNORM  1  /* RMSNorm(x) * norm_w (src/ModelCPU.jl:110-122) */
+#define IHIP_ACT_SILU_MUL 2  /* silu(x[:, :K]) * x[:, K:2K] (src/ModelCPU.jl:447-473) */
 
 /* Message for the last failing call on this thread ("" if none). */
 const char *ihip_last_error(void);
@@ -102,6 +109,22 @@ int ihip_gemm_q(int qtype, const void *w_dev, const float *x_dev, float *y_dev,
                 int M, int N, int K, int flags, void *ws, size_t ws_bytes,
                 void *stream);
 
+/* ihip_gemm_q with the producer of its input fused in: Y = f(X) W^T where
+ * f is IHIP_ACT_PLAIN, IHIP_ACT_RMSNORM (per row: x / sqrt(mean(x^2) +
+ * eps) * norm_w, norm_w_dev may be NULL for unit weight) or
+ * IHIP_ACT_SILU_MUL (x rows are [gate | up], 2K wide). ldx: floats between
+ * rows of x (>= K, or >= 2K for SILU_MUL; a multiple of 4). The RMSNorm is
+ * the per-layer renormalisation of the verify forward (src/ModelCPU.jl:
+ * 110-122, before the projections of :755-760 and :455-471), applied as a
+ * row scale of the product. IHIP_GEMM_REUSE skips the input stage when ws
+ * already holds the prepared f(X) of the previous call (e.g. q and k/v
+ * projections of one hidden state); not with fp32-accurate M > 32. Same
+ * workspace size as ihip_gemm_q. */
+int ihip_gemm_q_ex(int qtype, const void *w_dev, const float *x_dev, int ldx,
+                   int act, const float *norm_w_dev, float eps, float *y_dev,
+                   int M, int N, int K, int flags, void *ws, size_t ws_bytes,
+                   void *stream);
+
 /* Packed weight layout: the GGUF blocks of each 16-row tile and 256-element
  * K-unit stored as one contiguous chunk, swizzled so that every lane of the
  * matmul kernel fetches its operand bytes with whole-cache-line 16-byte
@@ -153,8 +176,10 @@ int ihip_softmax_stats(const float *logits_dev, int rows, int V, float T,
  * mode 1 = reference-compatible (T = 1 ratio with a scalar draft
  * probability and scalar residual, src/SpeculativeDecoding.jl:61-63,79-93).
  * out_tok [k+1] receives the accepted drafts followed by the resampled or
- * bonus token; out_n [1] the number of accepted drafts (0..k). T must be
- * > 0 (use ihip_greedy_verify for T = 0). */
+ * bonus token; out_n [1] the number of accepted drafts (0..k), or -1 for
+ * a draft id outside [0, V). T must be > 0 (use ihip_greedy_verify for
+ * T = 0); V <= 4194304. ws: ihip_spec_accept_ws_bytes() bytes, 16-byte
+ * aligned. */
 int ihip_spec_accept_ws_bytes(int steps, int k, int V, size_t *bytes);
 int ihip_spec_accept(const float *tgt_dev, const float *drf_dev,
                      const int32_t *draft_tok_dev, int steps, int k, int V,
@@ -177,14 +202,15 @@ int ihip_greedy_verify(const float *logits_dev, const int32_t *draft_tok_dev,
  * u[i] < min(1, p_parent[tok[i]] / q_parent[tok[i]]), p and q the target and
  * draft softmax at T of the parent's rows. out_path [n] receives the root..
  * deepest accepted node (ties -> smallest node index); out_len [1] its
- * length. */
+ * length, or -1 for a malformed node. ws: ihip_accept_ws_bytes(3 n, V)
+ * bytes. */
 int ihip_tree_accept(const float *tgt_dev, const float *drf_dev,
                      const int32_t *tok_dev, const int32_t *parent_dev, int n,
                      int V, float T, const float *u_dev, int32_t *out_path_dev,
                      int32_t *out_len_dev, void *ws, size_t ws_bytes,
                      void *stream);
 
-/* ---- synthetic inputs (benchmark and tests; see csrc/synth.hip) ---- */
+/* ---- synthetic inputs (benchmark and tests; csrc/misc.hip) ---- */
 
 /* n_blocks seeded GGUF blocks of qtype starting at block first_block of
  * the given 64-bit stream (byte-identical to the Python generator). */

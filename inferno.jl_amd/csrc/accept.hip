@@ -1,15 +1,20 @@
 // LM-head softmax statistics and speculative acceptance on gfx950.
 //
 // Softmax statistics are two-level: a grid of (V-chunk, row) workgroups
-// writes a partial (max, sum exp(z - max)) per chunk; consumers merge the
-// partials in chunk order (deterministic). z = L / T as the reference
-// computes logits ./ temperature (src/ModelCPU.jl:1130-1132).
+// writes a partial (max, sum exp(z - max)) per chunk of 4096 entries (each
+// thread holds its 16 entries in registers: one round of loads); consumers
+// merge the partials in chunk order (deterministic). z = L / T as the
+// reference computes logits ./ temperature (src/ModelCPU.jl:1130-1132).
 //
-// Acceptance (src/SpeculativeDecoding.jl:75-104 with explicit uniforms):
-// one workgroup per verify step merges the statistics of its rows, runs the
-// ratio tests, and draws the residual or bonus token with an inverse CDF
-// over V: per-thread contiguous slices, a block scan of the slice sums, and
-// a sequential scan inside the one slice that holds u*S.
+// Acceptance (src/SpeculativeDecoding.jl:75-104 with explicit uniforms) runs
+// as four launches: statistics of every target and draft row; one wave per
+// verify step for the ratio tests (lane i judges draft i); per (chunk, step)
+// sums of the sampling weights (residual or bonus distribution); and one
+// workgroup per step that locates u * S by a chunk prefix, then a round
+// prefix, then a wave scan inside the chunk. Every partial sum is formed in
+// one fixed order, and the running value C_j at the last entry of a round
+// or chunk equals the prefix the next level starts from, so the search
+// always lands inside the level it selected.
 #include "common.h"
 
 namespace {
@@ -47,20 +52,34 @@ __device__ void block_merge_ms(float &m, float &s, float *sh) {
     __syncthreads();
 }
 
-// partial[row][chunk] = (max z, sum exp(z - max)). Row r uses T_last when period > 0 and r % period == period - 1 (the bonus
-// row of a verify step), T otherwise.
-__global__ __launch_bounds__(NT) void stats_partial_kernel(const float *__restrict__ L, int V, int nchunk,
-                                                           float T, float T_last, int period,
-                                                           float2 *__restrict__ part) {
+// partial[row][chunk] = (max z, sum exp(z - max)). Rows [0, rows1) come from
+// L1 at temperature T1, except every period-th row (r % period == period - 1,
+// the bonus row of a verify step) at T_last; rows [rows1, ..) come from L2 at
+// T2. Entry c * CHUNK + i * NT + t is thread t's i-th value.
+constexpr int PER = CHUNK / NT;  // 16 entries per thread
+__global__ __launch_bounds__(NT) void stats_partial_kernel(const float *__restrict__ L1, int rows1, float T1,
+                                                           float T_last, int period, const float *__restrict__ L2,
+                                                           float T2, int V, int nchunk, float2 *__restrict__ part) {
     __shared__ float sh[2 * NT / 64];
     const int chunk = blockIdx.x, row = blockIdx.y;
-    const float Tr = (period > 0 && row % period == period - 1) ? T_last : T;
-    const float *src = L + (size_t)row * V;
-    const int j0 = chunk * CHUNK, j1 = min(V, j0 + CHUNK);
+    const bool first = row < rows1;
+    const float Tr = first ? ((period > 0 && row % period == period - 1) ? T_last : T1) : T2;
+    const float *src = first ? L1 + (size_t)row * V : L2 + (size_t)(row - rows1) * V;
+    const int j0 = chunk * CHUNK;
+    float z[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int j = j0 + i * NT + threadIdx.x;
+        z[i] = j < V ? src[j] / Tr : -__builtin_huge_valf();
+    }
     float m = -__builtin_huge_valf();
-    for (int j = j0 + threadIdx.x; j < j1; j += NT) m = fmaxf(m, src[j] / Tr);
+#pragma unroll
+    for (int i = 0; i < PER; i++) m = fmaxf(m, z[i]);
     float s = 0.f;
-    for (int j = j0 + threadIdx.x; j < j1; j += NT) s += __expf(src[j] / Tr - m);
+    if (m > -__builtin_huge_valf()) {
+#pragma unroll
+        for (int i = 0; i < PER; i++) s += __expf(z[i] - m);
+    }
     block_merge_ms(m, s, sh);
     if (threadIdx.x == 0) part[(size_t)row * nchunk + chunk] = make_float2(m, s);
 }
@@ -80,146 +99,269 @@ __global__ void stats_merge_kernel(const float2 *__restrict__ part, int rows, in
     zsum[r] = ms.y;
 }
 
-// Weight of entry j of the sampling distribution:
-//   kind 0: p_j (row lt at T)                       bonus / fallback draw
-//   kind 1: max(0, p_j - q_j)  (q from row ld)      standard residual
-//   kind 2: max(0, p_j - qs)   (qs scalar)          reference residual
-struct Dist {
-    const float *lt, *ld;
-    float Tp, mp, sp, Tq, mq, sq, qs;
-    int kind;
-    __device__ __forceinline__ float w(int j) const {
-        const float p = __expf(lt[j] / Tp - mp) / sp;
-        if (kind == 0) return p;
-        const float q = kind == 1 ? __expf(ld[j] / Tq - mq) / sq : qs;
-        return fmaxf(p - q, 0.f);
-    }
+// Sampling distribution of one verify step, set by the ratio tests:
+//   kind 0: p_j (target row, temperature Tp)       bonus draw
+//   kind 1: max(0, p_j - q_j)  (q: draft row)      standard residual
+//   kind 2: max(0, p_j - qs)   (qs: scalar q_i)    reference residual
+//   kind -1: invalid draft id (out_n = -1, nothing drawn)
+// fallback when the weights sum to 0: 1 = draw from p (standard mode),
+// 2 = return V - 1 (the reference's all-NaN residual, length(probs)).
+struct Decision {
+    int kind, n, prow, qrow, fallback, pad0, pad1, pad2;
+    float Tp, mp, sp, Tq, mq, sq, qs, u;
 };
 
-// First j with u*S <= C_j (C inclusive prefix of w), or V-1. Also returns S.
-__device__ int block_inv_cdf(const Dist &D, int V, float u, float *sh, float &S_out) {
-    const int t = threadIdx.x;
-    const int per = (V + NT - 1) / NT;
-    const int j0 = min(V, t * per), j1 = min(V, j0 + per);
-    float loc = 0.f;
-    for (int j = j0; j < j1; j++) loc += D.w(j);
-    // inclusive block scan of loc over threads (Hillis-Steele in LDS)
-    sh[t] = loc;
-    __syncthreads();
-    for (int o = 1; o < NT; o <<= 1) {
-        const float v = t >= o ? sh[t - o] : 0.f;
-        __syncthreads();
-        sh[t] += v;
-        __syncthreads();
-    }
-    const float S = sh[NT - 1];
-    const float before = t > 0 ? sh[t - 1] : 0.f;
-    const float target = u * S;
-    __shared__ int found;
-    if (t == 0) found = V - 1;
-    __syncthreads();
-    // the first thread whose inclusive range reaches target scans its slice
-    const bool mine = (target <= sh[t]) && (t == 0 || target > before) && j1 > j0;
-    if (mine) {
-        float c = before;
-        int res = j1 - 1;
-        for (int j = j0; j < j1; j++) {
-            c += D.w(j);
-            if (target <= c) { res = j; break; }
-        }
-        atomicMin(&found, res);
-    }
-    __syncthreads();
-    S_out = S;
-    const int r = found;
-    __syncthreads();
-    return r;
+__device__ __forceinline__ float p_of(const Decision &D, const float *lt, int j) {
+    return __expf(lt[j] / D.Tp - D.mp) / D.sp;
+}
+__device__ __forceinline__ float w_of(const Decision &D, float p, const float *ld, int j) {
+    if (D.kind == 0) return p;
+    const float q = D.kind == 1 ? __expf(ld[j] / D.Tq - D.mq) / D.sq : D.qs;
+    return fmaxf(p - q, 0.f);
 }
 
-// One workgroup per verify step.
-__global__ __launch_bounds__(NT) void spec_accept_kernel(
-    const float *__restrict__ tgt, const float *__restrict__ drf, const int32_t *__restrict__ draft_tok,
-    int k, int V, float T, const float *__restrict__ u_acc, const float *__restrict__ u_res,
-    const float *__restrict__ u_bonus, int mode, const float2 *__restrict__ part, int nchunk,
-    int32_t *__restrict__ out_tok, int32_t *__restrict__ out_n) {
-    __shared__ float sh[NT];
-    __shared__ int s_n, s_rej;
-    __shared__ float s_qs;
-    const int step = blockIdx.x;
+// Inclusive scan over the 64 lanes of a wave (fixed association).
+__device__ __forceinline__ float wave_scan(float v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float y = __shfl_up(v, o);
+        if (lane >= o) v += y;
+    }
+    return v;
+}
+
+// Ratio tests of one verify step: lane i judges draft i (groups of 64 lanes
+// for k > 64). Writes the accepted drafts, out_n, and the decision.
+__global__ __launch_bounds__(64) void decide_kernel(const float *__restrict__ tgt, const float *__restrict__ drf,
+                                                    const int32_t *__restrict__ draft_tok, int k, int V, float T,
+                                                    const float *__restrict__ u_acc, const float *__restrict__ u_res,
+                                                    const float *__restrict__ u_bonus, int mode,
+                                                    const float2 *__restrict__ part, int nchunk,
+                                                    int32_t *__restrict__ out_tok, int32_t *__restrict__ out_n,
+                                                    Decision *__restrict__ dec) {
+    const int step = blockIdx.x, lane = threadIdx.x;
     const float *Lt = tgt + (size_t)step * (k + 1) * V;
     const float *Ld = drf + (size_t)step * k * V;
     const int32_t *dt = draft_tok + (size_t)step * k;
-    // partials: target rows [steps*(k+1)][nchunk], then draft rows [steps*k][nchunk]
     const float2 *Pt = part + (size_t)step * (k + 1) * nchunk;
     const float2 *Pd = part + ((size_t)gridDim.x * (k + 1) + (size_t)step * k) * nchunk;
     const float Tr = mode == 0 ? T : 1.0f;
-    if (threadIdx.x == 0) {
-        int n = 0, rej = -1;
-        float qs = 0.f;
-        for (int i = 0; i < k; i++) {
-            const float2 pt = merge_row(Pt + (size_t)i * nchunk, nchunk);
-            const float2 pd = merge_row(Pd + (size_t)i * nchunk, nchunk);
+    int first = k;  // first draft that is invalid or rejected
+    bool invalid = false;
+    float2 f_pt = make_float2(0.f, 1.f), f_pd = make_float2(0.f, 1.f);
+    float f_q = 0.f;
+    for (int base = 0; base < k && first == k; base += 64) {
+        const int i = base + lane;
+        bool bad = false, inv = false;
+        float2 pt = make_float2(0.f, 1.f), pd = make_float2(0.f, 1.f);
+        float q = 0.f;
+        if (i < k) {
             const int x = dt[i];
-            if (x < 0 || x >= V) {  // invalid draft id: reported as out_n = -1
-                n = -1;
-                break;
-            }
-            const float p = __expf(Lt[(size_t)i * V + x] / Tr - pt.x) / pt.y;
-            const float q = __expf(Ld[(size_t)i * V + x] / Tr - pd.x) / pd.y;
-            const float ratio = q > 0.f ? fminf(1.0f, p / q) : 1.0f;
-            if (u_acc[(size_t)step * k + i] < ratio) {
-                out_tok[(size_t)step * (k + 1) + n] = x;
-                n++;
+            if (x < 0 || x >= V) {
+                bad = inv = true;
             } else {
-                rej = i;
-                qs = q;
-                break;
+                pt = merge_row(Pt + (size_t)i * nchunk, nchunk);
+                pd = merge_row(Pd + (size_t)i * nchunk, nchunk);
+                const float p = __expf(Lt[(size_t)i * V + x] / Tr - pt.x) / pt.y;
+                q = __expf(Ld[(size_t)i * V + x] / Tr - pd.x) / pd.y;
+                const float ratio = q > 0.f ? fminf(1.0f, p / q) : 1.0f;
+                bad = !(u_acc[(size_t)step * k + i] < ratio);
             }
         }
-        s_n = n;
-        s_rej = rej;
-        s_qs = qs;
+        const uint64_t m = __ballot(bad);
+        if (m) {
+            const int f = __ffsll((unsigned long long)m) - 1;
+            first = base + f;
+            invalid = __shfl(inv ? 1 : 0, f) != 0;
+            f_pt = make_float2(__shfl(pt.x, f), __shfl(pt.y, f));
+            f_pd = make_float2(__shfl(pd.x, f), __shfl(pd.y, f));
+            f_q = __shfl(q, f);
+        }
     }
-    __syncthreads();
-    const int n = s_n, rej = s_rej;
-    if (n < 0) {
-        if (threadIdx.x == 0) out_n[step] = -1;
+    // accepted drafts
+    for (int i = lane; i < first; i += 64) out_tok[(size_t)step * (k + 1) + i] = dt[i];
+    if (lane != 0) return;
+    Decision D{};
+    if (invalid) {
+        D.kind = -1;
+        D.n = -1;
+        out_n[step] = -1;
+        dec[step] = D;
         return;
     }
-    Dist D;
-    int tok;
-    float S;
-    if (rej >= 0) {
-        const float2 pt = merge_row(Pt + (size_t)rej * nchunk, nchunk);
-        const float2 pd = merge_row(Pd + (size_t)rej * nchunk, nchunk);
-        D.lt = Lt + (size_t)rej * V;
-        D.ld = Ld + (size_t)rej * V;
-        D.Tp = Tr; D.mp = pt.x; D.sp = pt.y;
-        D.Tq = Tr; D.mq = pd.x; D.sq = pd.y;
-        D.qs = s_qs;
+    D.n = first;
+    if (first < k) {
         D.kind = mode == 0 ? 1 : 2;
-        const float u = u_res[step];
-        tok = block_inv_cdf(D, V, u, sh, S);
-        if (!(S > 0.f)) {
-            if (mode == 0) {  // p == q: sample from p
-                D.kind = 0;
-                tok = block_inv_cdf(D, V, u, sh, S);
-            } else {
-                tok = V - 1;  // all-NaN residual in the reference returns length(probs)
-            }
-        }
+        D.prow = first;
+        D.qrow = first;
+        D.Tp = Tr; D.mp = f_pt.x; D.sp = f_pt.y;
+        D.Tq = Tr; D.mq = f_pd.x; D.sq = f_pd.y;
+        D.qs = f_q;
+        D.u = u_res[step];
+        D.fallback = mode == 0 ? 1 : 2;
     } else {
         const float2 pt = merge_row(Pt + (size_t)k * nchunk, nchunk);
-        D.lt = Lt + (size_t)k * V;
-        D.ld = nullptr;
+        D.kind = 0;
+        D.prow = k;
+        D.qrow = 0;
         D.Tp = T; D.mp = pt.x; D.sp = pt.y;
         D.Tq = T; D.mq = 0.f; D.sq = 1.f; D.qs = 0.f;
-        D.kind = 0;
-        tok = block_inv_cdf(D, V, u_bonus[step], sh, S);
+        D.u = u_bonus[step];
+        D.fallback = 2;
     }
-    if (threadIdx.x == 0) {
-        out_tok[(size_t)step * (k + 1) + n] = tok;
-        out_n[step] = n;
+    out_n[step] = first;
+    dec[step] = D;
+}
+
+// Sampling weights of the PER x NT entries of chunk c: thread t holds entries
+// c * CHUNK + r * NT + t (r < PER) of w and, for the standard residual, of p.
+// Per round r: wave inclusive scans, round total R_r = ((T0 + T1) + T2) + T3
+// of the four wave totals.
+struct ChunkScan {
+    float w[PER], cw[PER];  // weights and their wave-inclusive scans
+    float R[PER];           // round totals (uniform)
+};
+
+__device__ void chunk_scan(const Decision &D, const float *lt, const float *ld, int V, int c, bool use_p,
+                           ChunkScan &cs, float *sh /* [PER][4] */) {
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+#pragma unroll
+    for (int r = 0; r < PER; r++) {
+        const int j = c * CHUNK + r * NT + t;
+        float w = 0.f;
+        if (j < V) {
+            const float p = p_of(D, lt, j);
+            w = use_p ? p : w_of(D, p, ld, j);
+        }
+        cs.w[r] = w;
+        cs.cw[r] = wave_scan(w);
+        if (lane == 63) sh[r * 4 + wave] = cs.cw[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < PER; r++) cs.R[r] = ((sh[r * 4] + sh[r * 4 + 1]) + sh[r * 4 + 2]) + sh[r * 4 + 3];
+    __syncthreads();
+}
+
+// csum[step][c] = sum of w over chunk c: the sequential sum of its round
+// totals.
+__global__ __launch_bounds__(NT) void chunk_sum_kernel(const float *__restrict__ tgt, const float *__restrict__ drf,
+                                                       int k, int V, const Decision *__restrict__ dec, int nchunk,
+                                                       float *__restrict__ csum) {
+    __shared__ float sh[PER * 4];
+    const int c = blockIdx.x, step = blockIdx.y;
+    const Decision D = dec[step];
+    if (D.kind < 0) return;
+    const float *lt = tgt + ((size_t)step * (k + 1) + D.prow) * V;
+    const float *ld = D.kind == 1 ? drf + ((size_t)step * k + D.qrow) * V : nullptr;
+    ChunkScan cs;
+    chunk_scan(D, lt, ld, V, c, false, cs, sh);
+    float sw = 0.f;
+#pragma unroll
+    for (int r = 0; r < PER; r++) sw += cs.R[r];
+    if (threadIdx.x == 0) csum[(size_t)step * nchunk + c] = sw;
+}
+
+// First j with u * S <= C_j, where C_j = before(chunk) + (P_r + (off_w +
+// scan)): chunk prefix, then round prefix, then lane. When the weights sum
+// to zero the standard mode draws from p (its chunk sums are formed here, in
+// the same order), the reference mode returns V - 1.
+constexpr int MAX_CHUNKS = 1024;
+__global__ __launch_bounds__(NT) void sample_kernel(const float *__restrict__ tgt, const float *__restrict__ drf,
+                                                    int k, int V, const Decision *__restrict__ dec, int nchunk,
+                                                    const float *__restrict__ csum, int32_t *__restrict__ out_tok) {
+    __shared__ float sh[PER * 4];
+    __shared__ float s_psum[MAX_CHUNKS];
+    __shared__ float s_before, s_target;
+    __shared__ int s_chunk, s_usep, s_tok;
+    __shared__ int s_first[NT / 64];
+    const int step = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const Decision D = dec[step];
+    if (D.kind < 0) return;
+    const float *cw = csum + (size_t)step * nchunk;
+    const float *lt = tgt + ((size_t)step * (k + 1) + D.prow) * V;
+    const float *ld = D.kind == 1 ? drf + ((size_t)step * k + D.qrow) * V : nullptr;
+    if (t == 0) {
+        float S = 0.f;
+        for (int c = 0; c < nchunk; c++) S += cw[c];
+        s_usep = 0;
+        s_tok = -1;
+        if (!(S > 0.f)) {
+            if (D.fallback == 1) s_usep = 1;
+            else s_tok = V - 1;
+        }
+    }
+    __syncthreads();
+    if (s_tok >= 0) {
+        if (t == 0) out_tok[(size_t)step * (k + 1) + D.n] = s_tok;
+        return;
+    }
+    const bool usep = s_usep != 0;
+    ChunkScan cs;
+    if (usep) {
+        for (int c = 0; c < nchunk; c++) {
+            chunk_scan(D, lt, ld, V, c, true, cs, sh);
+            if (t == 0) {
+                float sp = 0.f;
+#pragma unroll
+                for (int r = 0; r < PER; r++) sp += cs.R[r];
+                s_psum[c] = sp;
+            }
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        float S = 0.f;
+        for (int c = 0; c < nchunk; c++) S += usep ? s_psum[c] : cw[c];
+        const float target = D.u * S;
+        float before = 0.f;
+        int chunk = nchunk - 1;
+        for (int c = 0; c < nchunk; c++) {
+            const float nb = before + (usep ? s_psum[c] : cw[c]);
+            if (target <= nb) { chunk = c; break; }
+            before = nb;
+        }
+        s_before = before;
+        s_target = target;
+        s_chunk = chunk;
+    }
+    __syncthreads();
+    const int c = s_chunk;
+    const float before = s_before, target = s_target;
+    chunk_scan(D, lt, ld, V, c, usep, cs, sh);
+    // round: first r with target <= before + P_{r+1}
+    float P = 0.f, Pr = 0.f;
+    int rr = -1;
+#pragma unroll
+    for (int r = 0; r < PER; r++) {
+        const float Pn = P + cs.R[r];
+        if (rr < 0 && target <= before + Pn) { rr = r; Pr = P; }
+        P = Pn;
+    }
+    if (rr < 0) {  // unreachable: the chunk total bounds the target
+        rr = PER - 1;
+        Pr = P - cs.R[PER - 1];
+    }
+    float cw_rr = 0.f;
+#pragma unroll
+    for (int r = 0; r < PER; r++)
+        if (r == rr) cw_rr = cs.cw[r];
+    if (lane == 63) sh[wave] = cw_rr;
+    __syncthreads();
+    float off = 0.f;
+    for (int w = 0; w < wave; w++) off += sh[w];
+    const float C = before + (Pr + (off + cw_rr));
+    const int j = c * CHUNK + rr * NT + t;
+    const bool hit = j < V && target <= C;
+    const uint64_t m = __ballot(hit);
+    if (lane == 0) s_first[wave] = m ? (wave * 64 + __ffsll((unsigned long long)m) - 1) : NT;
+    __syncthreads();
+    if (t == 0) {
+        int f = NT;
+        for (int w = 0; w < NT / 64; w++) f = min(f, s_first[w]);
+        const int tok = min(c * CHUNK + rr * NT + (f < NT ? f : NT - 1), V - 1);
+        out_tok[(size_t)step * (k + 1) + D.n] = tok;
     }
 }
 
@@ -273,12 +415,18 @@ __global__ void greedy_kernel(const float2 *__restrict__ part, int nchunk, const
     out_n[step] = n;
 }
 
-// Tree walk: one thread, nodes in index order (parent[i] < i).
-__global__ void tree_kernel(const float *__restrict__ tgt, const float *__restrict__ drf,
-                            const int32_t *__restrict__ tok, const int32_t *__restrict__ parent, int n, int V,
-                            float T, const float *__restrict__ u, const float2 *__restrict__ part, int nchunk,
-                            int32_t *__restrict__ out_path, int32_t *__restrict__ out_len, int32_t *__restrict__ wsi) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+// Tree walk: the workgroup first merges the statistics of every row (target
+// rows then draft rows) into ms, then one thread walks the nodes in index
+// order (parent[i] < i).
+__global__ __launch_bounds__(NT) void tree_kernel(const float *__restrict__ tgt, const float *__restrict__ drf,
+                                                  const int32_t *__restrict__ tok, const int32_t *__restrict__ parent,
+                                                  int n, int V, float T, const float *__restrict__ u,
+                                                  const float2 *__restrict__ part, int nchunk, float2 *__restrict__ ms,
+                                                  int32_t *__restrict__ out_path, int32_t *__restrict__ out_len,
+                                                  int32_t *__restrict__ wsi) {
+    for (int r = threadIdx.x; r < 2 * n; r += blockDim.x) ms[r] = merge_row(part + (size_t)r * nchunk, nchunk);
+    __syncthreads();
+    if (threadIdx.x != 0) return;
     int32_t *acc = wsi, *depth = wsi + n;
     acc[0] = 1;
     depth[0] = 0;
@@ -293,8 +441,8 @@ __global__ void tree_kernel(const float *__restrict__ tgt, const float *__restri
         }
         depth[i] = depth[p] + 1;
         if (!acc[p]) continue;
-        const float2 pt = merge_row(part + (size_t)p * nchunk, nchunk);
-        const float2 pd = merge_row(part + (size_t)(n + p) * nchunk, nchunk);
+        const float2 pt = ms[p];
+        const float2 pd = ms[n + p];
         const float pp = __expf(tgt[(size_t)p * V + x] / T - pt.x) / pt.y;
         const float qq = __expf(drf[(size_t)p * V + x] / T - pd.x) / pd.y;
         const float ratio = qq > 0.f ? fminf(1.0f, pp / qq) : 1.0f;
@@ -320,7 +468,7 @@ hipError_t launch_stats(const float *L, int rows, int V, float T, float T_last, 
                         hipStream_t st) {
     if (rows <= 0) return hipSuccess;
     const int nc = accept_nchunk(V);
-    stats_partial_kernel<<<dim3(nc, rows), NT, 0, st>>>(L, V, nc, T, T_last, period, part);
+    stats_partial_kernel<<<dim3(nc, rows), NT, 0, st>>>(L, rows, T, T_last, period, L, T, V, nc, part);
     return hipGetLastError();
 }
 
@@ -330,18 +478,32 @@ hipError_t launch_stats_merge(const float2 *part, int rows, int V, float *zmax, 
     return hipGetLastError();
 }
 
-// part: float2 [steps*(k+1) + steps*k][nchunk].
+size_t spec_accept_ws(int steps, int k, int V) {
+    const size_t nc = accept_nchunk(V);
+    return (size_t)steps * (2 * k + 1) * nc * sizeof(float2) + (size_t)steps * sizeof(Decision) +
+           (size_t)steps * nc * sizeof(float) + 256;
+}
+
+// ws: float2 part[steps*(k+1) + steps*k][nchunk], Decision dec[steps],
+// float csum[steps][nchunk].
 hipError_t launch_spec_accept(const float *tgt, const float *drf, const int32_t *draft_tok, int steps, int k,
                               int V, float T, const float *u_acc, const float *u_res, const float *u_bonus,
-                              int mode, int32_t *out_tok, int32_t *out_n, float2 *part, hipStream_t st) {
+                              int mode, int32_t *out_tok, int32_t *out_n, void *ws, hipStream_t st) {
     const int nc = accept_nchunk(V);
     const float Tr = mode == 0 ? T : 1.0f;
-    hipError_t e = launch_stats(tgt, steps * (k + 1), V, Tr, T, k + 1, part, st);
+    float2 *part = (float2 *)ws;
+    Decision *dec = (Decision *)(part + (size_t)steps * (2 * k + 1) * nc);
+    float *csum = (float *)(dec + steps);
+    stats_partial_kernel<<<dim3(nc, steps * (2 * k + 1)), NT, 0, st>>>(tgt, steps * (k + 1), Tr, T, k + 1,
+                                                                      drf, Tr, V, nc, part);
+    hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    e = launch_stats(drf, steps * k, V, Tr, Tr, 0, part + (size_t)steps * (k + 1) * nc, st);
-    if (e != hipSuccess) return e;
-    spec_accept_kernel<<<steps, NT, 0, st>>>(tgt, drf, draft_tok, k, V, T, u_acc, u_res, u_bonus, mode, part, nc,
-                                             out_tok, out_n);
+    decide_kernel<<<steps, 64, 0, st>>>(tgt, drf, draft_tok, k, V, T, u_acc, u_res, u_bonus, mode, part, nc,
+                                        out_tok, out_n, dec);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    chunk_sum_kernel<<<dim3(nc, steps), NT, 0, st>>>(tgt, drf, k, V, dec, nc, csum);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    sample_kernel<<<steps, NT, 0, st>>>(tgt, drf, k, V, dec, nc, csum, out_tok);
     return hipGetLastError();
 }
 
@@ -363,10 +525,10 @@ hipError_t launch_tree(const float *tgt, const float *drf, const int32_t *tok, c
                        float T, const float *u, float2 *part, int32_t *out_path, int32_t *out_len,
                        int32_t *wsi, hipStream_t st) {
     const int nc = accept_nchunk(V);
-    hipError_t e = launch_stats(tgt, n, V, T, T, 0, part, st);
+    stats_partial_kernel<<<dim3(nc, 2 * n), NT, 0, st>>>(tgt, n, T, T, 0, drf, T, V, nc, part);
+    hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    e = launch_stats(drf, n, V, T, T, 0, part + (size_t)n * nc, st);
-    if (e != hipSuccess) return e;
-    tree_kernel<<<1, 64, 0, st>>>(tgt, drf, tok, parent, n, V, T, u, part, nc, out_path, out_len, wsi);
+    float2 *ms = (float2 *)(wsi + 2 * n);
+    tree_kernel<<<1, NT, 0, st>>>(tgt, drf, tok, parent, n, V, T, u, part, nc, ms, out_path, out_len, wsi);
     return hipGetLastError();
 }

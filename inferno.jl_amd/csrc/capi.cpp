@@ -17,6 +17,9 @@ hipError_t launch_gemm(int qt, const void *W, const float *X, float *Y, int M, i
                        hipStream_t st);
 size_t gemm_ws_bytes(int qt, int M, int N, int K, int flags);
 size_t packed_bytes(int qt, int N, int K);
+hipError_t launch_gemm_ex(int qt, const void *W, const float *X, int ldx, int op, const float *norm_w, float eps,
+                          float *Y, int M, int N, int K, int flags, void *ws, hipStream_t st);
+bool gemm_reuse_ok(int M, int flags);
 hipError_t launch_pack(int qt, const void *W, void *P, int N, int K, hipStream_t st);
 hipError_t launch_dequant(int qt, const void *w, float *out, int64_t n_blocks, hipStream_t st);
 int accept_nchunk(int V);
@@ -25,7 +28,8 @@ hipError_t launch_stats(const float *L, int rows, int V, float T, float T_last, 
 hipError_t launch_stats_merge(const float2 *part, int rows, int V, float *zmax, float *zsum, hipStream_t st);
 hipError_t launch_spec_accept(const float *tgt, const float *drf, const int32_t *draft_tok, int steps, int k,
                               int V, float T, const float *u_acc, const float *u_res, const float *u_bonus,
-                              int mode, int32_t *out_tok, int32_t *out_n, float2 *part, hipStream_t st);
+                              int mode, int32_t *out_tok, int32_t *out_n, void *ws, hipStream_t st);
+size_t spec_accept_ws(int steps, int k, int V);
 hipError_t launch_argmax_partial(const float *L, int rows, int V, float2 *part, hipStream_t st);
 hipError_t launch_greedy(const float2 *part, int V, const int32_t *draft_tok, int steps, int k, int32_t *out_n,
                          int32_t *out_argmax, hipStream_t st);
@@ -261,6 +265,28 @@ int ihip_gemm_q(int qtype, const void *w_dev, const float *x_dev, float *y_dev, 
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_gemm_q");
 }
 
+int ihip_gemm_q_ex(int qtype, const void *w_dev, const float *x_dev, int ldx, int act, const float *norm_w_dev,
+                   float eps, float *y_dev, int M, int N, int K, int flags, void *ws, size_t ws_bytes, void *stream) {
+    const int base = flags & ~IHIP_GEMM_REUSE;
+    int rc = check_gemm(qtype, w_dev, x_dev, y_dev, M, N, K, base);
+    if (rc != IHIP_OK) return rc;
+    if (act < IHIP_ACT_PLAIN || act > IHIP_ACT_SILU_MUL) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: act=%d", act);
+    const int min_ld = act == IHIP_ACT_SILU_MUL ? 2 * K : K;
+    if (ldx < min_ld || (ldx & 3)) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: ldx=%d (need >= %d, multiple of 4)", ldx, min_ld);
+    if ((K & 7) != 0) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: K=%d must be a multiple of 8", K);
+    if (act == IHIP_ACT_RMSNORM && !(eps >= 0.f)) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: eps=%g", eps);
+    if (norm_w_dev && !aligned16(norm_w_dev)) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: norm_w must be 16-byte aligned");
+    if ((flags & IHIP_GEMM_REUSE) && !gemm_reuse_ok(M, base))
+        return fail(IHIP_EINVAL, "ihip_gemm_q_ex: IHIP_GEMM_REUSE needs M <= 32 in fp32-accurate mode");
+    const size_t need = gemm_ws_bytes(qtype, M, N, K, base);
+    if (!ws) return fail(IHIP_EFAULT, "ihip_gemm_q_ex: NULL workspace (%zu bytes needed)", need);
+    if (ws_bytes < need) return fail(IHIP_ENOMEM, "ihip_gemm_q_ex: workspace %zu < %zu bytes", ws_bytes, need);
+    if (!aligned16(ws)) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: workspace must be 16-byte aligned");
+    hipError_t e = launch_gemm_ex(qtype, w_dev, x_dev, ldx, act, act == IHIP_ACT_RMSNORM ? norm_w_dev : nullptr, eps,
+                                  y_dev, M, N, K, flags, ws, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_gemm_q_ex");
+}
+
 int ihip_packed_bytes(int qtype, int N, int K, size_t *bytes) {
     if (!bytes) return fail(IHIP_EFAULT, "ihip_packed_bytes: NULL");
     const int rc = check_gemm_shape(qtype, 1, N, K, 0);
@@ -339,8 +365,11 @@ int ihip_softmax_stats(const float *logits_dev, int rows, int V, float T, float 
 }
 
 int ihip_spec_accept_ws_bytes(int steps, int k, int V, size_t *bytes) {
-    if (steps < 1 || k < 0) return fail(IHIP_EINVAL, "ihip_spec_accept_ws_bytes: steps=%d k=%d", steps, k);
-    return ihip_accept_ws_bytes(steps * (2 * k + 1), V, bytes);
+    if (!bytes) return fail(IHIP_EFAULT, "ihip_spec_accept_ws_bytes: NULL");
+    if (steps < 1 || k < 0 || V < 1) return fail(IHIP_EINVAL, "ihip_spec_accept_ws_bytes: steps=%d k=%d V=%d", steps, k, V);
+    if (V > 1024 * 4096) return fail(IHIP_EINVAL, "ihip_spec_accept_ws_bytes: V=%d above 4194304", V);
+    *bytes = spec_accept_ws(steps, k, V);
+    return ok();
 }
 
 int ihip_spec_accept(const float *tgt_dev, const float *drf_dev, const int32_t *draft_tok_dev, int steps, int k,
@@ -352,12 +381,13 @@ int ihip_spec_accept(const float *tgt_dev, const float *drf_dev, const int32_t *
     if (steps < 1 || k < 0 || V < 1) return fail(IHIP_EINVAL, "ihip_spec_accept: steps=%d k=%d V=%d", steps, k, V);
     if (!(T > 0.f)) return fail(IHIP_EINVAL, "ihip_spec_accept: T=%g must be > 0 (greedy: ihip_greedy_verify)", T);
     if (mode != 0 && mode != 1) return fail(IHIP_EINVAL, "ihip_spec_accept: mode=%d", mode);
-    size_t need = 0;
-    ihip_spec_accept_ws_bytes(steps, k, V, &need);
+    if (V > 1024 * 4096) return fail(IHIP_EINVAL, "ihip_spec_accept: V=%d above 4194304", V);
+    const size_t need = spec_accept_ws(steps, k, V);
     if (!ws) return fail(IHIP_EFAULT, "ihip_spec_accept: NULL workspace");
     if (ws_bytes < need) return fail(IHIP_ENOMEM, "ihip_spec_accept: workspace %zu < %zu bytes", ws_bytes, need);
+    if (((uintptr_t)ws & 15) != 0) return fail(IHIP_EINVAL, "ihip_spec_accept: workspace must be 16-byte aligned");
     hipError_t e = launch_spec_accept(tgt_dev, drf_dev, draft_tok_dev, steps, k, V, T, u_acc_dev, u_res_dev,
-                                      u_bonus_dev, mode, out_tok_dev, out_n_dev, (float2 *)ws, S(stream));
+                                      u_bonus_dev, mode, out_tok_dev, out_n_dev, ws, S(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_spec_accept");
 }
 
@@ -379,7 +409,7 @@ int ihip_tree_accept(const float *tgt_dev, const float *drf_dev, const int32_t *
     if (!tgt_dev || !drf_dev || !tok_dev || !parent_dev || !u_dev || !out_path_dev || !out_len_dev)
         return fail(IHIP_EFAULT, "ihip_tree_accept: NULL pointer");
     if (n < 1 || V < 1 || !(T > 0.f)) return fail(IHIP_EINVAL, "ihip_tree_accept: n=%d V=%d T=%g", n, V, T);
-    int rc = need_ws("ihip_tree_accept", 2 * n, V, ws, ws_bytes);
+    int rc = need_ws("ihip_tree_accept", 3 * n, V, ws, ws_bytes);
     if (rc != IHIP_OK) return rc;
     float2 *part = (float2 *)ws;
     int32_t *wsi = (int32_t *)(part + (size_t)2 * n * accept_nchunk(V));

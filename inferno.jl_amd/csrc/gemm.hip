@@ -441,10 +441,29 @@ template <int LK> struct Layout {
 // Grid (units, token blocks of 8). Thread (tl = tid/32, gi = tid%32) owns
 // elements [8 gi, 8 gi + 8) of unit blockIdx.x for token blockIdx.y*8 + tl.
 // Padding tokens (M <= t < TOK) get zero operands and unit scale.
+// Input transforms applied while preparing the activations (x row t, column
+// k; ldx elements between rows):
+//   ACT_PLAIN:    a = x[t][k]
+//   ACT_RMSNORM:  a = x[t][k] * w[k] (w = 1 if NULL) and ssq[u][t] = sum over
+//                 the unit of x^2; the matmul multiplies row t of its result
+//                 by 1 / sqrt(sum_u ssq[u][t] / K + eps), which is the RMSNorm
+//                 of src/ModelCPU.jl:110-122 moved past the (linear) product
+//   ACT_SILU_MUL: a = silu(x[t][k]) * x[t][K + k] for rows [gate | up]
+//                 (mlp_forward, src/ModelCPU.jl:447-473)
+enum { ACT_PLAIN = 0, ACT_RMSNORM = 1, ACT_SILU_MUL = 2 };
+struct ActIn {
+    int op, ldx;
+    const float *norm_w;
+    float eps;
+    bool reuse;  // activations already prepared in the workspace
+};
+
 template <int LK, int MT, bool SPLIT, bool MINS>
-__global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ X, int M, int K,
+__global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ X, int ldx, int M, int K, int op,
+                                                   const float *__restrict__ norm_w,
                                                    uint8_t *__restrict__ afrag, float *__restrict__ xs,
-                                                   float *__restrict__ inv, uint8_t *__restrict__ mfrag) {
+                                                   float *__restrict__ inv, uint8_t *__restrict__ mfrag,
+                                                   float *__restrict__ ssq) {
     constexpr int TOK = MT * (SPLIT ? 8 : 16);
     constexpr int ENTRY = Layout<LK>::ENTRY;
     const int u = blockIdx.x, tid = threadIdx.x;
@@ -453,13 +472,36 @@ __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ X, 
     const int k = u * UNIT + gi * 8;
     float v[8];
     if (t < M && k < K) {
-        const float4 a = *(const float4 *)(X + (size_t)t * K + k);
-        const float4 b = *(const float4 *)(X + (size_t)t * K + k + 4);
+        const float *row = X + (size_t)t * ldx + k;
+        const float4 a = *(const float4 *)row;
+        const float4 b = *(const float4 *)(row + 4);
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
         v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        if (op == ACT_SILU_MUL) {
+            const float4 c = *(const float4 *)(row + K);
+            const float4 d = *(const float4 *)(row + K + 4);
+            const float up[8] = {c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = v[e] / (1.0f + expf(-v[e])) * up[e];
+        }
     } else {
 #pragma unroll
         for (int e = 0; e < 8; e++) v[e] = 0.f;
+    }
+    if (op == ACT_RMSNORM) {
+        float q = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) q = __builtin_fmaf(v[e], v[e], q);
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) q += __shfl_xor(q, o);
+        if (gi == 0 && t < TOK) ssq[(size_t)u * TOK + t] = q;
+        if (norm_w != nullptr && k < K) {
+            const float4 a = *(const float4 *)(norm_w + k);
+            const float4 b = *(const float4 *)(norm_w + k + 4);
+            const float w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] *= w[e];
+        }
     }
     float mx = 0.f;
 #pragma unroll
@@ -545,7 +587,7 @@ template <int QT, int MT, bool SPLIT, bool PK>
 __global__ __launch_bounds__(WG_THREADS)
 void gemm_q_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, int N, int K, int ups, int S,
                    const uint8_t *__restrict__ afrag, const float *__restrict__ xs, const float *__restrict__ invs,
-                   float *__restrict__ part) {
+                   const float *__restrict__ ssq, float eps, float *__restrict__ part) {
     using C = GemmCfg<QT>;
     constexpr int TOK = MT * (SPLIT ? 8 : 16);
     constexpr int TPL = Acc<MT, SPLIT>::TPL;
@@ -568,6 +610,7 @@ void gemm_q_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     uint8_t *a_lds = smem;                                      // [ups][UNIT_A]
     float *x_lds = (float *)(smem + (size_t)ups * UNIT_A);      // [ups][8][TOK]
     float *i_lds = x_lds + (C::MINS ? ups * 8 * TOK : 0);       // [ups][TOK]
+    __shared__ float rs[TOK];                                   // RMSNorm row scales
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n_in = lane & 15, g = lane >> 4;
@@ -628,6 +671,15 @@ void gemm_q_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
         i_lds[min(tid, n_i - 1)] = i_tmp;
         for (int i = WG_THREADS + tid; i < n_i; i += WG_THREADS) i_lds[i] = i_src[i];
     }
+    if (tid < TOK) {
+        float r = 1.0f;
+        if (ssq != nullptr) {
+            float sq = 0.f;
+            for (int u = 0; u < n_units; u++) sq += ssq[(size_t)u * TOK + tid];
+            r = 1.0f / sqrtf(sq / (float)K + eps);
+        }
+        rs[tid] = r;
+    }
     __syncthreads();
 
     // 4. stream items through the MFMA pipe; a row group's epilogue follows
@@ -661,6 +713,7 @@ void gemm_q_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
                         if (t >= M) continue;
                         float v = SPLIT ? (A.acc[mt][2 * u] + A.acc[mt][2 * u + 1]) : A.acc[mt][u];
                         if constexpr (C::MINS) v = v - A.macc[mt][u];
+                        v *= rs[t];
                         if (part == nullptr)
                             Y[(size_t)t * N + r] = v;
                         else
@@ -828,7 +881,8 @@ template <int QT, int NW, int UPS, bool SPLIT, bool PK>
 __global__ __launch_bounds__(NW * 64, 2)
 void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, int N, int K, int accum,
                    const uint8_t *__restrict__ afrag, const float *__restrict__ invs,
-                   const uint8_t *__restrict__ mfrag, float *__restrict__ part) {
+                   const uint8_t *__restrict__ mfrag, const float *__restrict__ ssq, float eps,
+                   float *__restrict__ part) {
     using C = GemmCfg<QT>;
     constexpr int TOK = SPLIT ? 8 : 16;
     constexpr int TPL = SPLIT ? 2 : 4;
@@ -836,6 +890,7 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     constexpr int R = 4;
     static_assert(R % UPS == 0, "ring positions must map to fixed units");
     __shared__ __align__(16) float red[2][NW][64][TPL];
+    __shared__ float rs[TOK];  // RMSNorm row scales (1 without RMSNorm)
 
     const int n_units = (K + UNIT - 1) / UNIT;
     const int n_tiles = (N + 15) / 16;
@@ -885,6 +940,16 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     Unit<QT> buf[R];
 #pragma unroll
     for (int p = 0; p < R - 1; p++) load_item(p / UPS, p % UPS, buf[p]);
+    if (tid < TOK) {
+        float r = 1.0f;
+        if (ssq != nullptr) {
+            float sq = 0.f;
+            for (int u = 0; u < n_units; u++) sq += ssq[(size_t)u * TOK + tid];
+            r = 1.0f / sqrtf(sq / (float)K + eps);
+        }
+        rs[tid] = r;
+    }
+    __syncthreads();
 
     f4 acc = f4{0.f, 0.f, 0.f, 0.f}, macc = f4{0.f, 0.f, 0.f, 0.f};
     auto consume = [&](int j, int u, Unit<QT> &b) {
@@ -918,11 +983,12 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
                     for (int k = 0; k < TPL; k++) {
                         const int t = lane_token<SPLIT>(0, g, k);
                         if (t >= M) continue;
+                        const float v = sum[k] * rs[t];
                         if (part != nullptr) {
-                            part[((size_t)blockIdx.y * M + t) * N + r] = sum[k];
+                            part[((size_t)blockIdx.y * M + t) * N + r] = v;
                         } else {
                             float *dst = Y + (size_t)t * N + r;
-                            *dst = accum ? *dst + sum[k] : sum[k];
+                            *dst = accum ? *dst + v : v;
                         }
                     }
                 }
@@ -947,18 +1013,34 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     }
 }
 
-template <int QT, int NW, int UPS, bool SPLIT, bool PK>
-hipError_t launch_v(const uint8_t *W, const float *X, float *Y, int M, int N, int K, int S, int G, int accum,
-                    uint8_t *afrag, float *inv, uint8_t *mfrag, float *part, hipStream_t st) {
+// Prepared-activation workspace (shared by both kernels): the A operand,
+// the Q4_K/Q5_K sub-block sums (LDS kernel) or min-term operand (streaming
+// kernel), the inverse unit scales and the RMSNorm partial sums.
+struct ActWs {
+    uint8_t *afrag;
+    float *xs, *inv;
+    uint8_t *mfrag;
+    float *ssq;
+};
+
+template <int QT, int MT, bool SPLIT>
+hipError_t launch_prep(const float *X, const ActIn &in, int M, int K, const ActWs &a, hipStream_t st) {
     using C = GemmCfg<QT>;
-    constexpr int TOK = SPLIT ? 8 : 16;
+    constexpr int TOK = MT * (SPLIT ? 8 : 16);
     const int n_units = (K + UNIT - 1) / UNIT;
-    prep_kernel<QT == QT_Q6_K ? 1 : QT == QT_Q8_0 ? 2 : 0, 1, SPLIT, C::MINS>
-        <<<dim3(n_units, TOK / 8), 256, 0, st>>>(X, M, K, afrag, nullptr, inv, mfrag);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    gemm_v_kernel<QT, NW, UPS, SPLIT, PK><<<dim3(G, S), NW * 64, 0, st>>>(W, Y, M, N, K, accum, afrag, inv, mfrag,
-                                                                      S > 1 ? part : nullptr);
+    prep_kernel<QT == QT_Q6_K ? 1 : QT == QT_Q8_0 ? 2 : 0, MT, SPLIT, C::MINS><<<dim3(n_units, TOK / 8), 256, 0, st>>>(
+        X, in.ldx, M, K, in.op, in.norm_w, a.afrag, a.xs, a.inv, a.mfrag, a.ssq);
+    return hipGetLastError();
+}
+
+template <int QT, int NW, int UPS, bool SPLIT, bool PK>
+hipError_t launch_v(const uint8_t *W, const float *X, const ActIn &in, float *Y, int M, int N, int K, int S, int G,
+                    int accum, const ActWs &a, float *part, hipStream_t st) {
+    hipError_t e;
+    if (!in.reuse && (e = launch_prep<QT, 1, SPLIT>(X, in, M, K, a, st)) != hipSuccess) return e;
+    gemm_v_kernel<QT, NW, UPS, SPLIT, PK><<<dim3(G, S), NW * 64, 0, st>>>(
+        W, Y, M, N, K, accum, a.afrag, a.inv, a.mfrag, in.op == ACT_RMSNORM ? a.ssq : nullptr, in.eps,
+        S > 1 ? part : nullptr);
     e = hipGetLastError();
     if (e != hipSuccess || S == 1) return e;
     const int64_t MN = (int64_t)M * N;
@@ -967,23 +1049,22 @@ hipError_t launch_v(const uint8_t *W, const float *X, float *Y, int M, int N, in
 }
 
 template <int QT, int MT, bool SPLIT, bool PK>
-hipError_t launch_t(const uint8_t *W, const float *X, float *Y, int M, int N, int K, int ups, int S, int G, int accum,
-                    uint8_t *afrag, float *xs, float *inv, float *part, hipStream_t st) {
+hipError_t launch_t(const uint8_t *W, const float *X, const ActIn &in, float *Y, int M, int N, int K, int ups, int S,
+                    int G, int accum, const ActWs &a, float *part, hipStream_t st) {
     using C = GemmCfg<QT>;
     constexpr int TOK = MT * (SPLIT ? 8 : 16);
-    const int n_units = (K + UNIT - 1) / UNIT;
-    prep_kernel<QT == QT_Q6_K ? 1 : QT == QT_Q8_0 ? 2 : 0, MT, SPLIT, C::MINS><<<dim3(n_units, TOK / 8), 256, 0, st>>>(X, M, K, afrag, xs, inv, nullptr);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    hipError_t e;
+    if (!in.reuse && (e = launch_prep<QT, MT, SPLIT>(X, in, M, K, a, st)) != hipSuccess) return e;
     const size_t lds = (size_t)ups * UNIT_A1 * MT + (C::MINS ? (size_t)ups * 8 * TOK * 4 : 0) + (size_t)ups * TOK * 4;
     if (lds > 65536) {
-        e = hipFuncSetAttribute((const void *)gemm_q_kernel<QT, MT, SPLIT, PK>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds);
+        e = hipFuncSetAttribute((const void *)gemm_q_kernel<QT, MT, SPLIT, PK>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
     const bool reduce = S > 1 || accum;
-    gemm_q_kernel<QT, MT, SPLIT, PK><<<dim3(G, S), WG_THREADS, lds, st>>>(W, Y, M, N, K, ups, S, afrag, xs, inv,
-                                                                     reduce ? part : nullptr);
+    gemm_q_kernel<QT, MT, SPLIT, PK><<<dim3(G, S), WG_THREADS, lds, st>>>(
+        W, Y, M, N, K, ups, S, a.afrag, a.xs, a.inv, in.op == ACT_RMSNORM ? a.ssq : nullptr, in.eps,
+        reduce ? part : nullptr);
     e = hipGetLastError();
     if (e != hipSuccess || !reduce) return e;
     const int64_t MN = (int64_t)M * N;
@@ -1002,7 +1083,7 @@ struct GemmPlan {
     int ups;         // LDS kernel: 256-element units per K-slice
     int S;           // K-slices (grid.y)
     int G;           // workgroups per K-slice (grid.x)
-    size_t off_xs, off_inv, off_mfrag, off_part, ws_bytes;
+    size_t off_xs, off_inv, off_mfrag, off_ssq, off_part, ws_bytes;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -1064,6 +1145,8 @@ static GemmPlan plan_gemm(int qt, int M, int N, int K, int flags) {
     o += align256((size_t)n_units * TOK * 4);
     p.off_mfrag = o;
     o += (mins && p.stream) ? align256((size_t)n_units * 512) : 0;
+    p.off_ssq = o;
+    o += align256((size_t)n_units * TOK * 4);
     p.off_part = o;
     o += align256((size_t)p.S * M * N * 4);  // partials (split-K or accumulate)
     p.ws_bytes = o;
@@ -1084,12 +1167,15 @@ size_t gemm_ws_bytes(int qt, int M, int N, int K, int flags) {
 }
 
 template <int QT, bool PK>
-static hipError_t dispatch_mt(const GemmPlan &p, const uint8_t *W, const float *X, float *Y, int M, int N, int K,
-                              int accum, uint8_t *ws, hipStream_t st) {
-    float *xs = (float *)(ws + p.off_xs), *inv = (float *)(ws + p.off_inv), *part = (float *)(ws + p.off_part);
-    uint8_t *mfrag = ws + p.off_mfrag;
+static hipError_t dispatch_mt(const GemmPlan &p, const uint8_t *W, const float *X, const ActIn &in, float *Y, int M,
+                              int N, int K, int accum, uint8_t *ws, hipStream_t st) {
+    // the sub-block sums feed only the LDS kernel, the min-term operand only
+    // the streaming kernel (the other has no room for them in the workspace)
+    const ActWs a{ws, p.stream ? nullptr : (float *)(ws + p.off_xs), (float *)(ws + p.off_inv),
+                  p.stream ? ws + p.off_mfrag : nullptr, (float *)(ws + p.off_ssq)};
+    float *part = (float *)(ws + p.off_part);
     if (p.stream) {
-#define V(u, sp) return launch_v<QT, 4, u, sp, PK>(W, X, Y, M, N, K, p.S, p.G, accum, ws, inv, mfrag, part, st)
+#define V(u, sp) return launch_v<QT, 4, u, sp, PK>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
         if (p.split) {
             switch (p.UPS) { case 1: V(1, true); case 2: V(2, true); default: V(4, true); }
         } else {
@@ -1097,7 +1183,7 @@ static hipError_t dispatch_mt(const GemmPlan &p, const uint8_t *W, const float *
         }
 #undef V
     }
-#define L(mt, sp) return launch_t<QT, mt, sp, PK>(W, X, Y, M, N, K, p.ups, p.S, p.G, accum, ws, xs, inv, part, st)
+#define L(mt, sp) return launch_t<QT, mt, sp, PK>(W, X, in, Y, M, N, K, p.ups, p.S, p.G, accum, a, part, st)
     if (p.split) {
         switch (p.MT) {
         case 1: L(1, true); case 2: L(2, true); case 3: L(3, true); case 4: L(4, true);
@@ -1136,21 +1222,21 @@ hipError_t launch_pack(int qt, const void *W, void *P, int N, int K, hipStream_t
     return hipGetLastError();
 }
 
-hipError_t launch_gemm(int qt, const void *W, const float *X, float *Y, int M, int N, int K, int flags, void *ws,
-                       hipStream_t st) {
+static hipError_t gemm_in(int qt, const void *W, const float *X, const ActIn &in, float *Y, int M, int N, int K,
+                          int flags, void *ws, hipStream_t st) {
     const int m0 = launch_m(M, flags);
     if (m0 != M) {
-        hipError_t e = launch_gemm(qt, W, X, Y, m0, N, K, flags | 1, ws, st);
+        hipError_t e = gemm_in(qt, W, X, in, Y, m0, N, K, flags | 1, ws, st);
         if (e != hipSuccess) return e;
-        return launch_gemm(qt, W, X + (size_t)m0 * K, Y + (size_t)m0 * N, M - m0, N, K, flags | 1, ws, st);
+        return gemm_in(qt, W, X + (size_t)m0 * in.ldx, in, Y + (size_t)m0 * N, M - m0, N, K, flags | 1, ws, st);
     }
     const GemmPlan p = plan_gemm(qt, M, N, K, flags);
     const int accum = (flags & 4) ? 1 : 0;
     const bool pk = (flags & 8) != 0;
     const uint8_t *w = (const uint8_t *)W;
     uint8_t *wsp = (uint8_t *)ws;
-#define D(q) return pk ? dispatch_mt<q, true>(p, w, X, Y, M, N, K, accum, wsp, st) \
-                       : dispatch_mt<q, false>(p, w, X, Y, M, N, K, accum, wsp, st)
+#define D(q) return pk ? dispatch_mt<q, true>(p, w, X, in, Y, M, N, K, accum, wsp, st) \
+                       : dispatch_mt<q, false>(p, w, X, in, Y, M, N, K, accum, wsp, st)
     switch (qt) {
     case QT_Q4_K: D(QT_Q4_K);
     case QT_Q5_K: D(QT_Q5_K);
@@ -1160,3 +1246,20 @@ hipError_t launch_gemm(int qt, const void *W, const float *X, float *Y, int M, i
 #undef D
     return hipErrorInvalidValue;
 }
+
+hipError_t launch_gemm(int qt, const void *W, const float *X, float *Y, int M, int N, int K, int flags, void *ws,
+                       hipStream_t st) {
+    const ActIn in{ACT_PLAIN, K, nullptr, 0.f, false};
+    return gemm_in(qt, W, X, in, Y, M, N, K, flags, ws, st);
+}
+
+// flags bit 16: reuse prepared activations. Splitting M > 32 (fp32-accurate)
+// into two launches keeps only the second half prepared, so reuse needs
+// M <= 32 there (checked by the caller).
+hipError_t launch_gemm_ex(int qt, const void *W, const float *X, int ldx, int op, const float *norm_w, float eps,
+                          float *Y, int M, int N, int K, int flags, void *ws, hipStream_t st) {
+    const ActIn in{op, ldx, norm_w, eps, (flags & 16) != 0};
+    return gemm_in(qt, W, X, in, Y, M, N, K, flags & ~16, ws, st);
+}
+
+bool gemm_reuse_ok(int M, int flags) { return launch_m(M, flags) == M; }

@@ -30,6 +30,7 @@ SIGNATURES = {
     "q8_0_gemv": (None, [_vp, _vp, _vp, _i, _i]),
     "ihip_gemm_q_ws_bytes": (_i, [_i, _i, _i, _i, _i, C.POINTER(_sz)]),
     "ihip_gemm_q": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "ihip_gemm_q_ex": (_i, [_i, _vp, _vp, _i, _i, _vp, _f, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "ihip_packed_bytes": (_i, [_i, _i, _i, C.POINTER(_sz)]),
     "ihip_pack_weights": (_i, [_i, _vp, _vp, _i, _i, _vp]),
     "ihip_dequant": (_i, [_i, _vp, _vp, _i64, _vp]),

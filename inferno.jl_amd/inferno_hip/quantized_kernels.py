@@ -21,7 +21,8 @@ import numpy as np
 from . import _lib
 from .formats import BLOCK_BYTES, BLOCK_ELEMS, Q4_K, Q5_K, Q6_K, Q8_0, NAMES
 
-GEMM_AUTO, GEMM_F32, GEMM_HALF, GEMM_ACCUM, GEMM_PACKED = 0, 1, 2, 4, 8
+GEMM_AUTO, GEMM_F32, GEMM_HALF, GEMM_ACCUM, GEMM_PACKED, GEMM_REUSE = 0, 1, 2, 4, 8, 16
+ACT_PLAIN, ACT_RMSNORM, ACT_SILU_MUL = 0, 1, 2
 
 
 def quant_kernels_available() -> bool:
@@ -106,6 +107,28 @@ def gemm_q(qtype: int, w_dev, x, n: int, k: int, flags: int = GEMM_AUTO, out=Non
         ws = torch.empty(gemm_ws_bytes(qtype, m, n, k, flags), dtype=torch.uint8, device=x.device)
     _lib.check(L.ihip_gemm_q(qtype, _ptr(w_dev), _ptr(x), _ptr(out), m, n, k, flags, _ptr(ws), ws.numel(),
                              _stream(stream)))
+    return out
+
+
+def gemm_q_ex(qtype: int, w_dev, x, n: int, k: int, act: int = ACT_PLAIN, norm_w=None, eps: float = 1e-6,
+              flags: int = GEMM_AUTO, out=None, stream=None, ws=None, m: int | None = None):
+    """gemm_q with its input transform fused: act = ACT_PLAIN / ACT_RMSNORM
+    (RMSNorm(x) * norm_w per row) / ACT_SILU_MUL (x rows [gate | up]). x may
+    be a row-strided view (x.stride(1) == 1); m defaults to x.shape[0]."""
+    import torch
+    if x.dim() == 1:
+        x = x.view(1, -1)
+    if x.dtype != torch.float32 or x.stride(1) != 1:
+        raise ValueError("x must be float32 with unit column stride")
+    m = x.shape[0] if m is None else m
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    L = _lib.load()
+    if ws is None:
+        ws = torch.empty(gemm_ws_bytes(qtype, m, n, k, flags & ~GEMM_REUSE), dtype=torch.uint8, device=x.device)
+    nw = None if norm_w is None else _ptr(norm_w)
+    _lib.check(L.ihip_gemm_q_ex(qtype, _ptr(w_dev), _ptr(x), x.stride(0), act, nw, eps, _ptr(out), m, n, k, flags,
+                                _ptr(ws), ws.numel(), _stream(stream)))
     return out
 
 

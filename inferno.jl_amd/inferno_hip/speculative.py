@@ -115,7 +115,7 @@ def tree_accept(target_logits, draft_logits, node_tokens, parent, temperature: f
     n, V = target_logits.shape
     L = _lib.load()
     nb = C.c_size_t()
-    _lib.check(L.ihip_accept_ws_bytes(2 * n, V, C.byref(nb)))
+    _lib.check(L.ihip_accept_ws_bytes(3 * n, V, C.byref(nb)))
     ws = _ws(nb.value, target_logits.device)
     path = torch.zeros(n, dtype=torch.int32, device=target_logits.device)
     ln = torch.zeros(1, dtype=torch.int32, device=target_logits.device)

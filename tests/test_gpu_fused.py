@@ -1,0 +1,108 @@
+"""GPU: ihip_gemm_q_ex, the matmul with its input transform fused (RMSNorm,
+SiLU gating, row-strided input, reuse of prepared activations), against the
+oracle's fp64 product of the transformed input (RMSNorm from the oracle's
+rmsnorm, src/ModelCPU.jl:110-122; SiLU gating in float64)."""
+import numpy as np
+import pytest
+
+from _util import rel_l2
+
+import oracle as O
+from inferno_hip import formats as F
+from inferno_hip import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ih():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import inferno_hip
+    assert inferno_hip.quant_kernels_available(), inferno_hip._lib.last_error()
+    return inferno_hip
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _rms_rows(x, w, eps):
+    return np.stack([O.rmsnorm(r, eps, w) for r in x]).astype(np.float32)
+
+
+@pytest.mark.parametrize("qt", F.QTYPES)
+@pytest.mark.parametrize("packed", [False, True])
+def test_rmsnorm_input(ih, qt, packed):
+    N, K = 200, 1024
+    rng = np.random.default_rng(qt + 3 * packed)
+    w = synth.matrix(qt, N, K, synth.stream_for(N, f"rn{qt}"))
+    wd = _dev(w)
+    fl = ih.GEMM_F32
+    if packed:
+        wd = ih.pack_weights(qt, wd, N, K)
+        fl |= ih.GEMM_PACKED
+    nw = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    for M in (1, 5, 8, 24):
+        x = (3.0 * rng.standard_normal((M, K))).astype(np.float32)
+        for weight in (None, nw):
+            ref = O.gemv_f64(qt, w, _rms_rows(x, weight, 1e-6), M, N, K)
+            got = ih.gemm_q_ex(qt, wd, _dev(x), N, K, act=ih.ACT_RMSNORM,
+                               norm_w=None if weight is None else _dev(weight), eps=1e-6, flags=fl).cpu().numpy()
+            assert rel_l2(got, ref) < 1e-5, (M, weight is None)
+
+
+@pytest.mark.parametrize("qt", [F.Q4_K, F.Q6_K])
+def test_silu_mul_input_strided(ih, qt):
+    N, K = 96, 512
+    rng = np.random.default_rng(11)
+    w = synth.matrix(qt, N, K, synth.stream_for(5, f"sl{qt}"))
+    wp = ih.pack_weights(qt, _dev(w), N, K)
+    for M in (1, 5, 8):
+        gu = rng.standard_normal((M, 2 * K + 8)).astype(np.float32)  # ldx = 2K + 8
+        g, u = gu[:, :K].astype(np.float64), gu[:, K:2 * K].astype(np.float64)
+        a = (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
+        ref = O.gemv_f64(qt, w, a, M, N, K)
+        got = ih.gemm_q_ex(qt, wp, _dev(gu), N, K, act=ih.ACT_SILU_MUL,
+                           flags=ih.GEMM_F32 | ih.GEMM_PACKED).cpu().numpy()
+        assert rel_l2(got, ref) < 1e-5, M
+
+
+def test_strided_plain_and_reuse(ih):
+    import torch
+    qt = F.Q4_K
+    K, N1, N2 = 1024, 160, 64
+    rng = np.random.default_rng(12)
+    w1 = synth.matrix(qt, N1, K, synth.stream_for(1, "r1"))
+    w2 = synth.matrix(qt, N2, K, synth.stream_for(2, "r2"))
+    p1, p2 = ih.pack_weights(qt, _dev(w1), N1, K), ih.pack_weights(qt, _dev(w2), N2, K)
+    fl = ih.GEMM_F32 | ih.GEMM_PACKED
+    for M in (1, 5, 8):
+        big = _dev(rng.standard_normal((M, K + 64)).astype(np.float32))
+        x = big[:, 32:32 + K]  # row-strided view
+        xr = x.cpu().numpy()
+        ws = torch.empty(ih.quantized_kernels.gemm_ws_bytes(qt, M, max(N1, N2), K, fl), dtype=torch.uint8,
+                         device="cuda")
+        y1 = ih.gemm_q_ex(qt, p1, x, N1, K, act=ih.ACT_RMSNORM, flags=fl, ws=ws)
+        y2 = ih.gemm_q_ex(qt, p2, x, N2, K, act=ih.ACT_RMSNORM, flags=fl | ih.GEMM_REUSE, ws=ws)
+        y2b = ih.gemm_q_ex(qt, p2, x, N2, K, act=ih.ACT_RMSNORM, flags=fl)
+        assert torch.equal(y2, y2b)
+        rr = _rms_rows(xr, None, 1e-6)
+        assert rel_l2(y1.cpu().numpy(), O.gemv_f64(qt, w1, rr, M, N1, K)) < 1e-5
+        y3 = ih.gemm_q_ex(qt, p1, x, N1, K, flags=fl)
+        assert rel_l2(y3.cpu().numpy(), O.gemv_f64(qt, w1, xr, M, N1, K)) < 1e-5
+
+
+def test_ex_errors(ih):
+    import torch
+    qt = F.Q4_K
+    w = ih.pack_weights(qt, _dev(synth.matrix(qt, 16, 256, 1)), 16, 256)
+    x = torch.zeros(40, 512, device="cuda")
+    with pytest.raises(ih.HipError):
+        ih.gemm_q_ex(qt, w, x[:, :256], 16, 512, act=ih.ACT_SILU_MUL)  # ldx < 2K
+    with pytest.raises(ih.HipError):  # reuse with M > 32 fp32-accurate
+        ih.gemm_q_ex(qt, w, x[:, :256], 16, 256, flags=ih.GEMM_F32 | ih.GEMM_PACKED | ih.GEMM_REUSE)
+    with pytest.raises(ih.HipError):
+        ih.gemm_q_ex(qt, w, x[:5, :256], 16, 256, act=7)
