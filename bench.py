@@ -153,9 +153,13 @@ def time_op(fn, iters: int, stream):
     return e0.elapsed_time(e1) / iters * 1e-3
 
 
-def gemm_roofline(ih, model: Model, n_layers: int, M: int, iters: int = 64):
-    """Dominant dequant-matmul: Q4_K gate/up 24576x4096 at M=5 over the
-    layers' weights in turn (1.8 GB, far beyond the 256 MB cache)."""
+def gemm_roofline(ih, model: Model, n_layers: int, M: int, iters: int = 64, replays: int = 3):
+    """Dominant kernel: the Q4_K gate/up dequant-matmul (24576x4096, M=5)
+    over the layers' weights in turn (1.8 GB, far beyond the 256 MB cache).
+    The activations are prepared once; `iters` matmul launches that reuse
+    them are captured in a HIP graph and timed with events on the graph's
+    stream, so the per-launch figure is the matmul kernel plus its dispatch
+    gap. Returns (seconds per launch, algorithmic bytes per launch)."""
     import torch
     F = ih.formats
     N, K = 2 * FF, H
@@ -163,15 +167,58 @@ def gemm_roofline(ih, model: Model, n_layers: int, M: int, iters: int = 64):
     y = torch.empty((M, N), device="cuda")
     fl = ih.GEMM_F32 | ih.GEMM_PACKED
     ws = torch.empty(ih.quantized_kernels.gemm_ws_bytes(F.Q4_K, M, N, K, fl), dtype=torch.uint8, device="cuda")
-    s = torch.cuda.current_stream()
-    fn = lambda i: ih.gemm_q(F.Q4_K, model.layers[i % n_layers]["gu"], x, N, K, flags=fl,  # noqa: E731
-                             out=y, ws=ws)
-    for i in range(4):
-        fn(i)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ih.gemm_q_ex(F.Q4_K, model.layers[0]["gu"], x, N, K, flags=fl, out=y, ws=ws)  # prepares x
+        for i in range(4):
+            ih.gemm_q_ex(F.Q4_K, model.layers[i % n_layers]["gu"], x, N, K, flags=fl | ih.GEMM_REUSE, out=y, ws=ws)
     torch.cuda.synchronize()
-    t = time_op(fn, iters, s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        for i in range(iters):
+            ih.gemm_q_ex(F.Q4_K, model.layers[i % n_layers]["gu"], x, N, K, flags=fl | ih.GEMM_REUSE, out=y,
+                         ws=ws)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(replays):
+        graph.replay()
+    e1.record(s)
+    e1.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / (replays * iters)
     alg = F.matrix_bytes(F.Q4_K, N, K) + M * K * 4 + M * N * 4
     return t, alg
+
+
+def profile_kernels(ih, model: Model, n_layers: int, M: int):
+    """For rocprofv3 --pmc: the roofline kernel's graph, then a calibration
+    kernel of known traffic (ihip_add over 64 Mi floats: y += x reads 512 MiB,
+    writes 256 MiB)."""
+    import torch
+    gemm_roofline(ih, model, n_layers, M, replays=1)
+    n = 64 << 20
+    a = torch.ones(n, device="cuda")
+    b = torch.ones(n, device="cuda")
+    for _ in range(3):
+        ih.quantized_kernels.add_(a, b)
+    torch.cuda.synchronize()
+    log(f"profile_kernels: roofline graph + ihip_add over {n} floats")
+
+
+def read_traffic():
+    """HBM bytes per launch of the roofline kernel, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (None when absent)."""
+    path = os.path.join(ROOT, "profiles", "q4k_gemm_24576x4096_m5_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def gemm_sweep(ih, model: Model, n_layers: int):
@@ -297,6 +344,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--profile-kernels", action="store_true",
+                    help="only run the roofline kernel and the traffic calibration kernel (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -309,9 +358,12 @@ def main():
     assert ih.quant_kernels_available(), ih._lib.last_error()
     k, T = 4, 0.8
     t0 = time.time()
-    model = Model(ih, args.layers)
+    model = Model(ih, args.layers, keep_gguf=0 if (args.no_cpu or args.profile_kernels) else 4)
     step = VerifyStep(ih, model, args.m, k, T)
     log(f"setup {time.time() - t0:.1f}s, weights {model.weight_bytes(args.layers) / 1e9:.3f} GB")
+    if args.profile_kernels:
+        profile_kernels(ih, model, args.layers, args.m)
+        return
 
     # capture one step in a HIP graph
     s = torch.cuda.Stream()
@@ -368,8 +420,9 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
-            "kernel": "Q4_K dequant-matmul 24576x4096 M=5 (prep + gemm + split-K reduce launches)",
+            "traffic": read_traffic(),
+            "kernel": "gemm_v_kernel<Q4_K>: packed Q4_K dequant-matmul 24576x4096, M=5, fp32-accurate "
+                      "(per launch incl. dispatch gap, activations prepared once)",
             "us_per_launch": round(t_op * 1e6, 2),
             "algorithmic_bytes": alg,
         },
