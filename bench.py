@@ -179,13 +179,14 @@ def gemm_roofline(ih, model: Model, n_layers: int, M: int, iters: int = 64, repl
         for i in range(iters):
             ih.gemm_q_ex(F.Q4_K, model.layers[i % n_layers]["gu"], x, N, K, flags=fl | ih.GEMM_REUSE, out=y,
                          ws=ws)
-    graph.replay()
-    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(s)
-    for _ in range(replays):
+    with torch.cuda.stream(s):  # replay() launches on the current stream
         graph.replay()
-    e1.record(s)
+        torch.cuda.synchronize()
+        e0.record(s)
+        for _ in range(replays):
+            graph.replay()
+        e1.record(s)
     e1.synchronize()
     t = e0.elapsed_time(e1) * 1e-3 / (replays * iters)
     alg = F.matrix_bytes(F.Q4_K, N, K) + M * K * 4 + M * N * 4

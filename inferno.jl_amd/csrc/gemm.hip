@@ -878,7 +878,7 @@ __device__ __forceinline__ void compute_v(const Unit<QT> &r, const AReg<QT> &a, 
 }
 
 template <int QT, int NW, int UPS, bool SPLIT, bool PK>
-__global__ __launch_bounds__(NW * 64, 2)
+__global__ __launch_bounds__(NW * 64, 8 / NW)
 void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, int N, int K, int accum,
                    const uint8_t *__restrict__ afrag, const float *__restrict__ invs,
                    const uint8_t *__restrict__ mfrag, const float *__restrict__ ssq, float eps,
@@ -906,19 +906,32 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     AReg<QT> a[UPS];
     float inv[UPS][TPL];
     bool live[UPS];
+    const bool aslot = (SPLIT ? (n_in >> 1) : n_in) < M;
 #pragma unroll
     for (int u = 0; u < UPS; u++) {
         live[u] = unit0 + u < n_units;
         const int un = min(unit0 + u, n_units - 1);
         const uint8_t *src = afrag + (size_t)un * UNIT_A1;
-        if constexpr (QT == QT_Q6_K) {
+        // slots of padding tokens are zero: not fetched
+        if (aslot) {
+            if constexpr (QT == QT_Q6_K) {
 #pragma unroll
-            for (int c = 0; c < 16; c++) a[u].f[c] = *(const h4 *)(src + c * 512 + lane * 8);
+                for (int c = 0; c < 16; c++) a[u].f[c] = *(const h4 *)(src + c * 512 + lane * 8);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 8; c++) a[u].f[c] = *(const h8 *)(src + c * 1024 + lane * 16);
+            }
+            if constexpr (C::MINS) a[u].mins = *(const h4 *)(mfrag + (size_t)un * 512 + lane * 8);
         } else {
+            if constexpr (QT == QT_Q6_K) {
 #pragma unroll
-            for (int c = 0; c < 8; c++) a[u].f[c] = *(const h8 *)(src + c * 1024 + lane * 16);
+                for (int c = 0; c < 16; c++) a[u].f[c] = h4{};
+            } else {
+#pragma unroll
+                for (int c = 0; c < 8; c++) a[u].f[c] = h8{};
+            }
+            if constexpr (C::MINS) a[u].mins = h4{};
         }
-        if constexpr (C::MINS) a[u].mins = *(const h4 *)(mfrag + (size_t)un * 512 + lane * 8);
 #pragma unroll
         for (int k = 0; k < TPL; k++) inv[u][k] = invs[(size_t)un * TOK + lane_token<SPLIT>(0, g, k)];
     }
@@ -1113,7 +1126,8 @@ static GemmPlan plan_gemm(int qt, int M, int N, int K, int flags) {
         // K per workgroup NW*UPS units; prefer one K-slice (no partials) with
         // the fewest units per wave that still covers K, else the largest
         // chunk that divides K
-        const int nw = 4;
+        static const int env_nw = env_int("IHIP_STREAM_NW", 8);
+        const int nw = env_nw == 8 ? 8 : 4;
         int ups = 4;
         if (env_ups == 1 || env_ups == 2 || env_ups == 4) {
             ups = env_ups;
@@ -1128,8 +1142,16 @@ static GemmPlan plan_gemm(int qt, int M, int N, int K, int flags) {
         p.NW = nw;
         p.UPS = ups;
         p.S = (n_units + nw * ups - 1) / (nw * ups);
+        // every workgroup resident at once (2 per CU at <= 256 VGPRs) and the
+        // same number of tiles for each: no second dispatch wave, no tail
+        // where half the workgroups idle
+        static const int stream_target = env_int("IHIP_GEMM_WGS", 0);
+        const int resident = nw == 8 ? 256 : 512;  // workgroups the chip holds at <= 256 VGPRs
+        const int target = stream_target > 0 ? stream_target : resident;
         const int n_tiles = (N + 15) / 16;
-        p.G = std::max(1, std::min(n_tiles, (target + p.S - 1) / p.S));
+        const int g0 = std::max(1, std::min(n_tiles, target / p.S));
+        const int per = (n_tiles + g0 - 1) / g0;
+        p.G = (n_tiles + per - 1) / per;
     } else {
         const int rowgroups = (N + ROWS_PER_WG - 1) / ROWS_PER_WG;
         const int ups_max = std::max(1, lds_a / (UNIT_A1 * p.MT));
@@ -1175,12 +1197,14 @@ static hipError_t dispatch_mt(const GemmPlan &p, const uint8_t *W, const float *
                   p.stream ? ws + p.off_mfrag : nullptr, (float *)(ws + p.off_ssq)};
     float *part = (float *)(ws + p.off_part);
     if (p.stream) {
-#define V(u, sp) return launch_v<QT, 4, u, sp, PK>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
-        if (p.split) {
-            switch (p.UPS) { case 1: V(1, true); case 2: V(2, true); default: V(4, true); }
+#define V(nw, u, sp) return launch_v<QT, nw, u, sp, PK>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
+#define VU(nw, sp) switch (p.UPS) { case 1: V(nw, 1, sp); case 2: V(nw, 2, sp); default: V(nw, 4, sp); }
+        if (p.NW == 8) {
+            if (p.split) { VU(8, true); } else { VU(8, false); }
         } else {
-            switch (p.UPS) { case 1: V(1, false); case 2: V(2, false); default: V(4, false); }
+            if (p.split) { VU(4, true); } else { VU(4, false); }
         }
+#undef VU
 #undef V
     }
 #define L(mt, sp) return launch_t<QT, mt, sp, PK>(W, X, in, Y, M, N, K, p.ups, p.S, p.G, accum, a, part, st)
