@@ -104,6 +104,7 @@ class VerifyStep:
         wsb = max(gws(F.Q4_K, M, NQ + 2 * NKV, H, fl), gws(F.Q4_K, M, H, NQ, fl),
                   gws(F.Q4_K, M, 2 * FF, H, fl), gws(F.Q6_K, M, H, FF, fl), gws(F.Q6_K, M, VOCAB, H, fl))
         self.ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        self.ws_down = torch.empty(wsb, dtype=torch.uint8, device=dev)  # holds the deferred down partials
         # draft side (inputs of the verify step): draft logits, draft tokens, uniforms
         noise = ih.quantized_kernels.synth_gaussian(st(SEED, "draft_logits"), k * VOCAB, 3.0).view(k, VOCAB)
         self.drf = noise.contiguous()
@@ -120,21 +121,26 @@ class VerifyStep:
         self.out_n = torch.zeros(1, dtype=torch.int32, device=dev)
 
     def run(self):
-        """One verify step: per layer RMSNorm -> [q; k; v] -> o (+= into x)
-        -> RMSNorm -> [gate; up] -> SiLU gating -> down (+= into x); final
-        RMSNorm -> lm_head -> accept. RMSNorm and SiLU gating run fused into
-        the matmul that consumes them."""
+        """One verify step: per layer [residual += previous down] + RMSNorm
+        -> [q; k; v] -> o (+= into the residual) -> RMSNorm -> [gate; up] ->
+        SiLU gating -> down (left as K-slice partials); final residual add +
+        RMSNorm -> lm_head -> accept. RMSNorm, SiLU gating and the residual
+        add of the down projection run inside the input stage of the matmul
+        that consumes them."""
         ih, F, M = self.ih, self.ih.formats, self.M
         ex = ih.gemm_q_ex
         f32 = ih.GEMM_F32 | ih.GEMM_PACKED
         acc = f32 | ih.GEMM_ACCUM
+        parts = ih.gemm_partials(F.Q6_K, M, H, FF, f32, self.ws_down)
         self.x.copy_(self.x0)
-        for lw in self.model.layers:
-            ex(F.Q4_K, lw["qkv"], self.x, NQ + 2 * NKV, H, act=ih.ACT_RMSNORM, flags=f32, out=self.qkv, ws=self.ws)
+        for i, lw in enumerate(self.model.layers):
+            ex(F.Q4_K, lw["qkv"], self.x, NQ + 2 * NKV, H, act=ih.ACT_RMSNORM, flags=f32, out=self.qkv, ws=self.ws,
+               add=parts if i > 0 else None)
             ex(F.Q4_K, lw["o"], self.qkv[:, :NQ], H, NQ, flags=acc, out=self.x, ws=self.ws)
             ex(F.Q4_K, lw["gu"], self.x, 2 * FF, H, act=ih.ACT_RMSNORM, flags=f32, out=self.gu, ws=self.ws)
-            ex(F.Q6_K, lw["down"], self.gu, H, FF, act=ih.ACT_SILU_MUL, flags=acc, out=self.x, ws=self.ws)
-        ex(F.Q6_K, self.model.lm, self.x, VOCAB, H, act=ih.ACT_RMSNORM, flags=f32, out=self.logits, ws=self.ws)
+            ex(F.Q6_K, lw["down"], self.gu, H, FF, act=ih.ACT_SILU_MUL, flags=f32 | ih.GEMM_DEFER, ws=self.ws_down)
+        ex(F.Q6_K, self.model.lm, self.x, VOCAB, H, act=ih.ACT_RMSNORM, flags=f32, out=self.logits, ws=self.ws,
+           add=parts)
         ih.spec_accept(self.logits.view(1, M, VOCAB), self.drf.view(1, self.k, VOCAB), self.draft, self.T,
                        self.u_acc, self.u_res, self.u_bonus, out_tok=self.out_tok, out_n=self.out_n,
                        ws=self.acc_ws)

@@ -109,21 +109,43 @@ int ihip_gemm_q(int qtype, const void *w_dev, const float *x_dev, float *y_dev,
                 int M, int N, int K, int flags, void *ws, size_t ws_bytes,
                 void *stream);
 
-/* ihip_gemm_q with the producer of its input fused in: Y = f(X) W^T where
- * f is IHIP_ACT_PLAIN, IHIP_ACT_RMSNORM (per row: x / sqrt(mean(x^2) +
- * eps) * norm_w, norm_w_dev may be NULL for unit weight) or
- * IHIP_ACT_SILU_MUL (x rows are [gate | up], 2K wide). ldx: floats between
- * rows of x (>= K, or >= 2K for SILU_MUL; a multiple of 4). The RMSNorm is
- * the per-layer renormalisation of the verify forward (src/ModelCPU.jl:
- * 110-122, before the projections of :755-760 and :455-471), applied as a
- * row scale of the product. IHIP_GEMM_REUSE skips the input stage when ws
- * already holds the prepared f(X) of the previous call (e.g. q and k/v
- * projections of one hidden state); not with fp32-accurate M > 32. Same
- * workspace size as ihip_gemm_q. */
-int ihip_gemm_q_ex(int qtype, const void *w_dev, const float *x_dev, int ldx,
-                   int act, const float *norm_w_dev, float eps, float *y_dev,
-                   int M, int N, int K, int flags, void *ws, size_t ws_bytes,
-                   void *stream);
+/* ihip_gemm_q with the producer of its input fused in: Y = f(X') W^T.
+ *   X' = x, or, with add != NULL, x + (add[0] + add[1] + ... + add[n_add-1])
+ *        (slices [M x K], row stride K, slice stride add_stride floats, e.g.
+ *        the K-slice partials an IHIP_GEMM_DEFER call left in its
+ *        workspace), stored back into x: the residual add of the decoder
+ *        layer (src/ModelCPU.jl:870-891) folded into the next matmul.
+ *   f  = IHIP_ACT_PLAIN, IHIP_ACT_RMSNORM (per row: x / sqrt(mean(x^2) +
+ *        eps) * norm_w, norm_w may be NULL for unit weight; the RMSNorm of
+ *        src/ModelCPU.jl:110-122 before the projections of :755-760 and
+ *        :455-471, applied as a row scale of the product) or
+ *        IHIP_ACT_SILU_MUL (x rows are [gate | up], 2K wide).
+ * ldx: floats between rows of x (>= K, or >= 2K for SILU_MUL; a multiple of
+ * 4). IHIP_GEMM_REUSE skips the input stage when ws already holds the
+ * prepared f(X') of the previous call (e.g. two projections of one hidden
+ * state); not with add, nor with fp32-accurate M > 32. IHIP_GEMM_DEFER
+ * leaves the product in ws as K-slice partials (ihip_gemm_q_partials) and
+ * does not touch y; not with IHIP_GEMM_ACCUM, nor with fp32-accurate M > 32.
+ * Same workspace size as ihip_gemm_q; a deferring call and the call that
+ * adds its partials need separate workspaces. */
+#define IHIP_GEMM_DEFER 32
+typedef struct ihip_gemm_input {
+    const float *x;        /* activations (written back when add != NULL) */
+    int ldx;
+    int act;               /* IHIP_ACT_* */
+    const float *norm_w;   /* RMSNorm weight [K] or NULL */
+    float eps;
+    const float *add;      /* NULL or n_add slices folded into x first */
+    int n_add;
+    int64_t add_stride;
+} ihip_gemm_input;
+int ihip_gemm_q_ex(int qtype, const void *w_dev, const ihip_gemm_input *in,
+                   float *y_dev, int M, int N, int K, int flags, void *ws,
+                   size_t ws_bytes, void *stream);
+/* Partials of a deferred call with the same (qtype, M, N, K, flags): n
+ * slices [M x N] at *slices, slice stride *stride floats. */
+int ihip_gemm_q_partials(int qtype, int M, int N, int K, int flags, void *ws,
+                         float **slices, int *n_slices, int64_t *stride);
 
 /* Packed weight layout: the GGUF blocks of each 16-row tile and 256-element
  * K-unit stored as one contiguous chunk, swizzled so that every lane of the
@@ -178,7 +200,7 @@ int ihip_softmax_stats(const float *logits_dev, int rows, int V, float T,
  * out_tok [k+1] receives the accepted drafts followed by the resampled or
  * bonus token; out_n [1] the number of accepted drafts (0..k), or -1 for
  * a draft id outside [0, V). T must be > 0 (use ihip_greedy_verify for
- * T = 0); V <= 4194304. ws: ihip_spec_accept_ws_bytes() bytes, 16-byte
+ * T = 0); V <= 4194304, k <= 127. ws: ihip_spec_accept_ws_bytes() bytes, 16-byte
  * aligned. */
 int ihip_spec_accept_ws_bytes(int steps, int k, int V, size_t *bytes);
 int ihip_spec_accept(const float *tgt_dev, const float *drf_dev,

@@ -90,6 +90,31 @@ __device__ __forceinline__ float2 merge_row(const float2 *part, int nchunk) {
     return make_float2(m, s);
 }
 
+// Merge of a row's chunk partials by one wave: lane l folds chunks l, l+64,
+// ... in order, then a butterfly over the lanes (fixed order: every lane
+// ends with the same value).
+__device__ __forceinline__ float2 wave_merge_row(const float2 *part, int nchunk) {
+    const int lane = threadIdx.x & 63;
+    float m = -__builtin_huge_valf(), s = 0.f;
+    for (int c = lane; c < nchunk; c += 64) {
+        const float2 p = part[c];
+        merge_ms(m, s, p.x, p.y);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
+        // order the pair by lane so both partners compute the same merge
+        if (lane & o) merge_ms(m, s, m2, s2);
+        else {
+            float mm = m2, ss = s2;
+            merge_ms(mm, ss, m, s);
+            m = mm;
+            s = ss;
+        }
+    }
+    return make_float2(m, s);
+}
+
 __global__ void stats_merge_kernel(const float2 *__restrict__ part, int rows, int nchunk,
                                    float *__restrict__ zmax, float *__restrict__ zsum) {
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
@@ -131,8 +156,11 @@ __device__ __forceinline__ float wave_scan(float v) {
     return v;
 }
 
-// Ratio tests of one verify step: lane i judges draft i (groups of 64 lanes
-// for k > 64). Writes the accepted drafts, out_n, and the decision.
+// Ratio tests of one verify step (one wave): the statistics of the step's
+// 2k + 1 rows are merged first (wave_merge_row, kept in LDS), then lane i
+// judges draft i (groups of 64 lanes for k > 64). Writes the accepted
+// drafts, out_n, and the decision.
+constexpr int DECIDE_MAX_ROWS = 255;  // 2k + 1, k <= 127
 __global__ __launch_bounds__(64) void decide_kernel(const float *__restrict__ tgt, const float *__restrict__ drf,
                                                     const int32_t *__restrict__ draft_tok, int k, int V, float T,
                                                     const float *__restrict__ u_acc, const float *__restrict__ u_res,
@@ -140,6 +168,7 @@ __global__ __launch_bounds__(64) void decide_kernel(const float *__restrict__ tg
                                                     const float2 *__restrict__ part, int nchunk,
                                                     int32_t *__restrict__ out_tok, int32_t *__restrict__ out_n,
                                                     Decision *__restrict__ dec) {
+    __shared__ float2 ms[DECIDE_MAX_ROWS];  // target rows 0..k, then draft rows 0..k-1
     const int step = blockIdx.x, lane = threadIdx.x;
     const float *Lt = tgt + (size_t)step * (k + 1) * V;
     const float *Ld = drf + (size_t)step * k * V;
@@ -147,22 +176,24 @@ __global__ __launch_bounds__(64) void decide_kernel(const float *__restrict__ tg
     const float2 *Pt = part + (size_t)step * (k + 1) * nchunk;
     const float2 *Pd = part + ((size_t)gridDim.x * (k + 1) + (size_t)step * k) * nchunk;
     const float Tr = mode == 0 ? T : 1.0f;
+    for (int r = 0; r < 2 * k + 1; r++) {
+        const float2 v = wave_merge_row(r <= k ? Pt + (size_t)r * nchunk : Pd + (size_t)(r - k - 1) * nchunk, nchunk);
+        if (lane == 0) ms[r] = v;
+    }
+    __syncthreads();
     int first = k;  // first draft that is invalid or rejected
     bool invalid = false;
-    float2 f_pt = make_float2(0.f, 1.f), f_pd = make_float2(0.f, 1.f);
     float f_q = 0.f;
     for (int base = 0; base < k && first == k; base += 64) {
         const int i = base + lane;
         bool bad = false, inv = false;
-        float2 pt = make_float2(0.f, 1.f), pd = make_float2(0.f, 1.f);
         float q = 0.f;
         if (i < k) {
             const int x = dt[i];
             if (x < 0 || x >= V) {
                 bad = inv = true;
             } else {
-                pt = merge_row(Pt + (size_t)i * nchunk, nchunk);
-                pd = merge_row(Pd + (size_t)i * nchunk, nchunk);
+                const float2 pt = ms[i], pd = ms[k + 1 + i];
                 const float p = __expf(Lt[(size_t)i * V + x] / Tr - pt.x) / pt.y;
                 q = __expf(Ld[(size_t)i * V + x] / Tr - pd.x) / pd.y;
                 const float ratio = q > 0.f ? fminf(1.0f, p / q) : 1.0f;
@@ -174,8 +205,6 @@ __global__ __launch_bounds__(64) void decide_kernel(const float *__restrict__ tg
             const int f = __ffsll((unsigned long long)m) - 1;
             first = base + f;
             invalid = __shfl(inv ? 1 : 0, f) != 0;
-            f_pt = make_float2(__shfl(pt.x, f), __shfl(pt.y, f));
-            f_pd = make_float2(__shfl(pd.x, f), __shfl(pd.y, f));
             f_q = __shfl(q, f);
         }
     }
@@ -192,16 +221,17 @@ __global__ __launch_bounds__(64) void decide_kernel(const float *__restrict__ tg
     }
     D.n = first;
     if (first < k) {
+        const float2 pt = ms[first], pd = ms[k + 1 + first];
         D.kind = mode == 0 ? 1 : 2;
         D.prow = first;
         D.qrow = first;
-        D.Tp = Tr; D.mp = f_pt.x; D.sp = f_pt.y;
-        D.Tq = Tr; D.mq = f_pd.x; D.sq = f_pd.y;
+        D.Tp = Tr; D.mp = pt.x; D.sp = pt.y;
+        D.Tq = Tr; D.mq = pd.x; D.sq = pd.y;
         D.qs = f_q;
         D.u = u_res[step];
         D.fallback = mode == 0 ? 1 : 2;
     } else {
-        const float2 pt = merge_row(Pt + (size_t)k * nchunk, nchunk);
+        const float2 pt = ms[k];
         D.kind = 0;
         D.prow = k;
         D.qrow = 0;
@@ -226,13 +256,23 @@ struct ChunkScan {
 __device__ void chunk_scan(const Decision &D, const float *lt, const float *ld, int V, int c, bool use_p,
                            ChunkScan &cs, float *sh /* [PER][4] */) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    // every load of the chunk in flight before any arithmetic
+    float lv[PER], dv[PER];
+    const bool need_q = !use_p && D.kind == 1;
+#pragma unroll
+    for (int r = 0; r < PER; r++) {
+        const int j = min(c * CHUNK + r * NT + t, V - 1);
+        lv[r] = lt[j];
+        dv[r] = need_q ? ld[j] : 0.f;
+    }
 #pragma unroll
     for (int r = 0; r < PER; r++) {
         const int j = c * CHUNK + r * NT + t;
         float w = 0.f;
         if (j < V) {
-            const float p = p_of(D, lt, j);
-            w = use_p ? p : w_of(D, p, ld, j);
+            const float p = __expf(lv[r] / D.Tp - D.mp) / D.sp;
+            if (use_p || D.kind == 0) w = p;
+            else w = fmaxf(p - (D.kind == 1 ? __expf(dv[r] / D.Tq - D.mq) / D.sq : D.qs), 0.f);
         }
         cs.w[r] = w;
         cs.cw[r] = wave_scan(w);
@@ -273,6 +313,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(const float *__restrict__ tg
                                                     const float *__restrict__ csum, int32_t *__restrict__ out_tok) {
     __shared__ float sh[PER * 4];
     __shared__ float s_psum[MAX_CHUNKS];
+    __shared__ float s_csum[MAX_CHUNKS];
     __shared__ float s_before, s_target;
     __shared__ int s_chunk, s_usep, s_tok;
     __shared__ int s_first[NT / 64];
@@ -282,9 +323,11 @@ __global__ __launch_bounds__(NT) void sample_kernel(const float *__restrict__ tg
     const float *cw = csum + (size_t)step * nchunk;
     const float *lt = tgt + ((size_t)step * (k + 1) + D.prow) * V;
     const float *ld = D.kind == 1 ? drf + ((size_t)step * k + D.qrow) * V : nullptr;
+    for (int c = t; c < nchunk; c += NT) s_csum[c] = cw[c];
+    __syncthreads();
     if (t == 0) {
         float S = 0.f;
-        for (int c = 0; c < nchunk; c++) S += cw[c];
+        for (int c = 0; c < nchunk; c++) S += s_csum[c];
         s_usep = 0;
         s_tok = -1;
         if (!(S > 0.f)) {
@@ -313,12 +356,12 @@ __global__ __launch_bounds__(NT) void sample_kernel(const float *__restrict__ tg
     }
     if (t == 0) {
         float S = 0.f;
-        for (int c = 0; c < nchunk; c++) S += usep ? s_psum[c] : cw[c];
+        for (int c = 0; c < nchunk; c++) S += usep ? s_psum[c] : s_csum[c];
         const float target = D.u * S;
         float before = 0.f;
         int chunk = nchunk - 1;
         for (int c = 0; c < nchunk; c++) {
-            const float nb = before + (usep ? s_psum[c] : cw[c]);
+            const float nb = before + (usep ? s_psum[c] : s_csum[c]);
             if (target <= nb) { chunk = c; break; }
             before = nb;
         }

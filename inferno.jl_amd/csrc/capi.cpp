@@ -18,8 +18,10 @@ hipError_t launch_gemm(int qt, const void *W, const float *X, float *Y, int M, i
 size_t gemm_ws_bytes(int qt, int M, int N, int K, int flags);
 size_t packed_bytes(int qt, int N, int K);
 hipError_t launch_gemm_ex(int qt, const void *W, const float *X, int ldx, int op, const float *norm_w, float eps,
-                          float *Y, int M, int N, int K, int flags, void *ws, hipStream_t st);
+                          const float *add, int n_add, int64_t add_stride, float *Y, int M, int N, int K, int flags,
+                          void *ws, hipStream_t st);
 bool gemm_reuse_ok(int M, int flags);
+void gemm_partials(int qt, int M, int N, int K, int flags, size_t *offset, int *n_slices);
 hipError_t launch_pack(int qt, const void *W, void *P, int N, int K, hipStream_t st);
 hipError_t launch_dequant(int qt, const void *w, float *out, int64_t n_blocks, hipStream_t st);
 int accept_nchunk(int V);
@@ -265,26 +267,52 @@ int ihip_gemm_q(int qtype, const void *w_dev, const float *x_dev, float *y_dev, 
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_gemm_q");
 }
 
-int ihip_gemm_q_ex(int qtype, const void *w_dev, const float *x_dev, int ldx, int act, const float *norm_w_dev,
-                   float eps, float *y_dev, int M, int N, int K, int flags, void *ws, size_t ws_bytes, void *stream) {
-    const int base = flags & ~IHIP_GEMM_REUSE;
-    int rc = check_gemm(qtype, w_dev, x_dev, y_dev, M, N, K, base);
+int ihip_gemm_q_ex(int qtype, const void *w_dev, const ihip_gemm_input *in, float *y_dev, int M, int N, int K,
+                   int flags, void *ws, size_t ws_bytes, void *stream) {
+    if (!in) return fail(IHIP_EFAULT, "ihip_gemm_q_ex: NULL input descriptor");
+    const int base = flags & ~(IHIP_GEMM_REUSE | IHIP_GEMM_DEFER);
+    const bool defer = flags & IHIP_GEMM_DEFER;
+    int rc = check_gemm(qtype, w_dev, in->x, defer ? const_cast<float *>(in->x) : y_dev, M, N, K, base);
     if (rc != IHIP_OK) return rc;
+    const int act = in->act;
     if (act < IHIP_ACT_PLAIN || act > IHIP_ACT_SILU_MUL) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: act=%d", act);
     const int min_ld = act == IHIP_ACT_SILU_MUL ? 2 * K : K;
-    if (ldx < min_ld || (ldx & 3)) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: ldx=%d (need >= %d, multiple of 4)", ldx, min_ld);
+    if (in->ldx < min_ld || (in->ldx & 3))
+        return fail(IHIP_EINVAL, "ihip_gemm_q_ex: ldx=%d (need >= %d, multiple of 4)", in->ldx, min_ld);
     if ((K & 7) != 0) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: K=%d must be a multiple of 8", K);
-    if (act == IHIP_ACT_RMSNORM && !(eps >= 0.f)) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: eps=%g", eps);
-    if (norm_w_dev && !aligned16(norm_w_dev)) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: norm_w must be 16-byte aligned");
-    if ((flags & IHIP_GEMM_REUSE) && !gemm_reuse_ok(M, base))
-        return fail(IHIP_EINVAL, "ihip_gemm_q_ex: IHIP_GEMM_REUSE needs M <= 32 in fp32-accurate mode");
+    if (act == IHIP_ACT_RMSNORM && !(in->eps >= 0.f)) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: eps=%g", in->eps);
+    if (in->norm_w && !aligned16(in->norm_w)) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: norm_w must be 16-byte aligned");
+    if (in->add) {
+        if (in->n_add < 1 || in->add_stride < (int64_t)M * K || (in->add_stride & 3) || !aligned16(in->add))
+            return fail(IHIP_EINVAL, "ihip_gemm_q_ex: add slices n=%d stride=%lld", in->n_add,
+                        (long long)in->add_stride);
+        if (act == IHIP_ACT_SILU_MUL) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: add with SILU_MUL");
+        if (flags & IHIP_GEMM_REUSE) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: add with IHIP_GEMM_REUSE");
+    }
+    if ((flags & (IHIP_GEMM_REUSE | IHIP_GEMM_DEFER)) && !gemm_reuse_ok(M, base))
+        return fail(IHIP_EINVAL, "ihip_gemm_q_ex: REUSE/DEFER need M <= 32 in fp32-accurate mode");
+    if (defer && (flags & IHIP_GEMM_ACCUM)) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: DEFER with ACCUM");
     const size_t need = gemm_ws_bytes(qtype, M, N, K, base);
     if (!ws) return fail(IHIP_EFAULT, "ihip_gemm_q_ex: NULL workspace (%zu bytes needed)", need);
     if (ws_bytes < need) return fail(IHIP_ENOMEM, "ihip_gemm_q_ex: workspace %zu < %zu bytes", ws_bytes, need);
     if (!aligned16(ws)) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: workspace must be 16-byte aligned");
-    hipError_t e = launch_gemm_ex(qtype, w_dev, x_dev, ldx, act, act == IHIP_ACT_RMSNORM ? norm_w_dev : nullptr, eps,
-                                  y_dev, M, N, K, flags, ws, S(stream));
+    hipError_t e = launch_gemm_ex(qtype, w_dev, in->x, in->ldx, act, act == IHIP_ACT_RMSNORM ? in->norm_w : nullptr,
+                                  in->eps, in->add, in->add ? in->n_add : 0, in->add_stride, y_dev, M, N, K, flags,
+                                  ws, S(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_gemm_q_ex");
+}
+
+int ihip_gemm_q_partials(int qtype, int M, int N, int K, int flags, void *ws, float **slices, int *n_slices,
+                         int64_t *stride) {
+    if (!ws || !slices || !n_slices || !stride) return fail(IHIP_EFAULT, "ihip_gemm_q_partials: NULL pointer");
+    const int base = flags & ~(IHIP_GEMM_REUSE | IHIP_GEMM_DEFER);
+    const int rc = check_gemm_shape(qtype, M, N, K, base);
+    if (rc != IHIP_OK) return rc;
+    size_t off = 0;
+    gemm_partials(qtype, M, N, K, base, &off, n_slices);
+    *slices = (float *)((uint8_t *)ws + off);
+    *stride = (int64_t)M * N;
+    return ok();
 }
 
 int ihip_packed_bytes(int qtype, int N, int K, size_t *bytes) {
@@ -382,6 +410,7 @@ int ihip_spec_accept(const float *tgt_dev, const float *drf_dev, const int32_t *
     if (!(T > 0.f)) return fail(IHIP_EINVAL, "ihip_spec_accept: T=%g must be > 0 (greedy: ihip_greedy_verify)", T);
     if (mode != 0 && mode != 1) return fail(IHIP_EINVAL, "ihip_spec_accept: mode=%d", mode);
     if (V > 1024 * 4096) return fail(IHIP_EINVAL, "ihip_spec_accept: V=%d above 4194304", V);
+    if (k > 127) return fail(IHIP_EINVAL, "ihip_spec_accept: k=%d above 127", k);
     const size_t need = spec_accept_ws(steps, k, V);
     if (!ws) return fail(IHIP_EFAULT, "ihip_spec_accept: NULL workspace");
     if (ws_bytes < need) return fail(IHIP_ENOMEM, "ihip_spec_accept: workspace %zu < %zu bytes", ws_bytes, need);

@@ -455,15 +455,23 @@ struct ActIn {
     int op, ldx;
     const float *norm_w;
     float eps;
-    bool reuse;  // activations already prepared in the workspace
+    bool reuse;          // activations already prepared in the workspace
+    const float *add;    // n_add slices [M][K] folded into x first (x += sum, stored back)
+    int n_add;
+    int64_t add_stride;  // floats between slices
+    bool defer;          // leave the product as K-slice partials in the workspace
 };
 
+// add != nullptr: x[t][k] += ((add_0 + add_1) + ...)[t][k] (the K-slice
+// partials of a previous matmul, the order its reduce would use), stored back
+// into x (each element has one owner thread), before the transform.
 template <int LK, int MT, bool SPLIT, bool MINS>
 __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ X, int ldx, int M, int K, int op,
                                                    const float *__restrict__ norm_w,
                                                    uint8_t *__restrict__ afrag, float *__restrict__ xs,
                                                    float *__restrict__ inv, uint8_t *__restrict__ mfrag,
-                                                   float *__restrict__ ssq) {
+                                                   float *__restrict__ ssq, const float *__restrict__ add, int n_add,
+                                                   int64_t add_stride, float *__restrict__ xw) {
     constexpr int TOK = MT * (SPLIT ? 8 : 16);
     constexpr int ENTRY = Layout<LK>::ENTRY;
     const int u = blockIdx.x, tid = threadIdx.x;
@@ -477,6 +485,24 @@ __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ X, 
         const float4 b = *(const float4 *)(row + 4);
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
         v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        if (add != nullptr) {
+            float sum[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) sum[e] = 0.f;
+            for (int sl = 0; sl < n_add; sl++) {
+                const float *pa = add + (size_t)sl * add_stride + (size_t)t * K + k;
+                const float4 c = *(const float4 *)pa;
+                const float4 d = *(const float4 *)(pa + 4);
+                const float pv[8] = {c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
+#pragma unroll
+                for (int e = 0; e < 8; e++) sum[e] = sl == 0 ? pv[e] : sum[e] + pv[e];
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = v[e] + sum[e];
+            float *wrow = xw + (size_t)t * ldx + k;
+            *(float4 *)wrow = make_float4(v[0], v[1], v[2], v[3]);
+            *(float4 *)(wrow + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        }
         if (op == ACT_SILU_MUL) {
             const float4 c = *(const float4 *)(row + K);
             const float4 d = *(const float4 *)(row + K + 4);
@@ -1042,7 +1068,8 @@ hipError_t launch_prep(const float *X, const ActIn &in, int M, int K, const ActW
     constexpr int TOK = MT * (SPLIT ? 8 : 16);
     const int n_units = (K + UNIT - 1) / UNIT;
     prep_kernel<QT == QT_Q6_K ? 1 : QT == QT_Q8_0 ? 2 : 0, MT, SPLIT, C::MINS><<<dim3(n_units, TOK / 8), 256, 0, st>>>(
-        X, in.ldx, M, K, in.op, in.norm_w, a.afrag, a.xs, a.inv, a.mfrag, a.ssq);
+        X, in.ldx, M, K, in.op, in.norm_w, a.afrag, a.xs, a.inv, a.mfrag, a.ssq, in.add, in.n_add, in.add_stride,
+        const_cast<float *>(X));
     return hipGetLastError();
 }
 
@@ -1053,9 +1080,9 @@ hipError_t launch_v(const uint8_t *W, const float *X, const ActIn &in, float *Y,
     if (!in.reuse && (e = launch_prep<QT, 1, SPLIT>(X, in, M, K, a, st)) != hipSuccess) return e;
     gemm_v_kernel<QT, NW, UPS, SPLIT, PK><<<dim3(G, S), NW * 64, 0, st>>>(
         W, Y, M, N, K, accum, a.afrag, a.inv, a.mfrag, in.op == ACT_RMSNORM ? a.ssq : nullptr, in.eps,
-        S > 1 ? part : nullptr);
+        (S > 1 || in.defer) ? part : nullptr);
     e = hipGetLastError();
-    if (e != hipSuccess || S == 1) return e;
+    if (e != hipSuccess || S == 1 || in.defer) return e;
     const int64_t MN = (int64_t)M * N;
     reduce_kernel<<<(unsigned)((MN + 1023) / 1024), 256, 0, st>>>(part, Y, S, MN, accum);
     return hipGetLastError();
@@ -1077,9 +1104,9 @@ hipError_t launch_t(const uint8_t *W, const float *X, const ActIn &in, float *Y,
     const bool reduce = S > 1 || accum;
     gemm_q_kernel<QT, MT, SPLIT, PK><<<dim3(G, S), WG_THREADS, lds, st>>>(
         W, Y, M, N, K, ups, S, a.afrag, a.xs, a.inv, in.op == ACT_RMSNORM ? a.ssq : nullptr, in.eps,
-        reduce ? part : nullptr);
+        (reduce || in.defer) ? part : nullptr);
     e = hipGetLastError();
-    if (e != hipSuccess || !reduce) return e;
+    if (e != hipSuccess || !reduce || in.defer) return e;
     const int64_t MN = (int64_t)M * N;
     reduce_kernel<<<(unsigned)((MN + 1023) / 1024), 256, 0, st>>>(part, Y, S, MN, accum);
     return hipGetLastError();
@@ -1252,7 +1279,9 @@ static hipError_t gemm_in(int qt, const void *W, const float *X, const ActIn &in
     if (m0 != M) {
         hipError_t e = gemm_in(qt, W, X, in, Y, m0, N, K, flags | 1, ws, st);
         if (e != hipSuccess) return e;
-        return gemm_in(qt, W, X + (size_t)m0 * in.ldx, in, Y + (size_t)m0 * N, M - m0, N, K, flags | 1, ws, st);
+        ActIn in2 = in;
+        if (in2.add != nullptr) in2.add += (size_t)m0 * K;
+        return gemm_in(qt, W, X + (size_t)m0 * in.ldx, in2, Y + (size_t)m0 * N, M - m0, N, K, flags | 1, ws, st);
     }
     const GemmPlan p = plan_gemm(qt, M, N, K, flags);
     const int accum = (flags & 4) ? 1 : 0;
@@ -1273,17 +1302,27 @@ static hipError_t gemm_in(int qt, const void *W, const float *X, const ActIn &in
 
 hipError_t launch_gemm(int qt, const void *W, const float *X, float *Y, int M, int N, int K, int flags, void *ws,
                        hipStream_t st) {
-    const ActIn in{ACT_PLAIN, K, nullptr, 0.f, false};
+    const ActIn in{ACT_PLAIN, K, nullptr, 0.f, false, nullptr, 0, 0, false};
     return gemm_in(qt, W, X, in, Y, M, N, K, flags, ws, st);
 }
 
-// flags bit 16: reuse prepared activations. Splitting M > 32 (fp32-accurate)
-// into two launches keeps only the second half prepared, so reuse needs
+// flags bit 16: reuse prepared activations; bit 32: defer (partials stay in
+// the workspace). Splitting M > 32 (fp32-accurate) into two launches keeps
+// only the second half prepared and its partials, so reuse and defer need
 // M <= 32 there (checked by the caller).
 hipError_t launch_gemm_ex(int qt, const void *W, const float *X, int ldx, int op, const float *norm_w, float eps,
-                          float *Y, int M, int N, int K, int flags, void *ws, hipStream_t st) {
-    const ActIn in{op, ldx, norm_w, eps, (flags & 16) != 0};
-    return gemm_in(qt, W, X, in, Y, M, N, K, flags & ~16, ws, st);
+                          const float *add, int n_add, int64_t add_stride, float *Y, int M, int N, int K, int flags,
+                          void *ws, hipStream_t st) {
+    const ActIn in{op, ldx, norm_w, eps, (flags & 16) != 0, add, n_add, add_stride, (flags & 32) != 0};
+    return gemm_in(qt, W, X, in, Y, M, N, K, flags & ~48, ws, st);
 }
 
 bool gemm_reuse_ok(int M, int flags) { return launch_m(M, flags) == M; }
+
+// Where a deferred call left its K-slice partials: slices [S][M][N] at ws +
+// offset.
+void gemm_partials(int qt, int M, int N, int K, int flags, size_t *offset, int *n_slices) {
+    const GemmPlan p = plan_gemm(qt, M, N, K, flags & ~48);
+    *offset = p.off_part;
+    *n_slices = p.S;
+}

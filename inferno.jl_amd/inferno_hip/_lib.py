@@ -30,7 +30,8 @@ SIGNATURES = {
     "q8_0_gemv": (None, [_vp, _vp, _vp, _i, _i]),
     "ihip_gemm_q_ws_bytes": (_i, [_i, _i, _i, _i, _i, C.POINTER(_sz)]),
     "ihip_gemm_q": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
-    "ihip_gemm_q_ex": (_i, [_i, _vp, _vp, _i, _i, _vp, _f, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "ihip_gemm_q_ex": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "ihip_gemm_q_partials": (_i, [_i, _i, _i, _i, _i, _vp, C.POINTER(_vp), C.POINTER(_i), C.POINTER(_i64)]),
     "ihip_packed_bytes": (_i, [_i, _i, _i, C.POINTER(_sz)]),
     "ihip_pack_weights": (_i, [_i, _vp, _vp, _i, _i, _vp]),
     "ihip_dequant": (_i, [_i, _vp, _vp, _i64, _vp]),
@@ -46,6 +47,12 @@ SIGNATURES = {
     "ihip_synth_blocks": (_i, [_i, _u64, _i64, _i64, _vp, _vp]),
     "ihip_synth_gaussian": (_i, [_u64, _i64, _f, _vp, _vp, _vp]),
 }
+
+
+class GemmInput(C.Structure):
+    """struct ihip_gemm_input"""
+    _fields_ = [("x", _vp), ("ldx", _i), ("act", _i), ("norm_w", _vp), ("eps", _f), ("add", _vp),
+                ("n_add", _i), ("add_stride", _i64)]
 
 
 class HipError(RuntimeError):

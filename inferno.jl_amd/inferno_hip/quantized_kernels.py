@@ -21,7 +21,7 @@ import numpy as np
 from . import _lib
 from .formats import BLOCK_BYTES, BLOCK_ELEMS, Q4_K, Q5_K, Q6_K, Q8_0, NAMES
 
-GEMM_AUTO, GEMM_F32, GEMM_HALF, GEMM_ACCUM, GEMM_PACKED, GEMM_REUSE = 0, 1, 2, 4, 8, 16
+GEMM_AUTO, GEMM_F32, GEMM_HALF, GEMM_ACCUM, GEMM_PACKED, GEMM_REUSE, GEMM_DEFER = 0, 1, 2, 4, 8, 16, 32
 ACT_PLAIN, ACT_RMSNORM, ACT_SILU_MUL = 0, 1, 2
 
 
@@ -111,31 +111,45 @@ def gemm_q(qtype: int, w_dev, x, n: int, k: int, flags: int = GEMM_AUTO, out=Non
 
 
 def gemm_q_ex(qtype: int, w_dev, x, n: int, k: int, act: int = ACT_PLAIN, norm_w=None, eps: float = 1e-6,
-              flags: int = GEMM_AUTO, out=None, stream=None, ws=None, m: int | None = None):
-    """gemm_q with its input transform fused: act = ACT_PLAIN / ACT_RMSNORM
+              flags: int = GEMM_AUTO, out=None, stream=None, ws=None, m: int | None = None, add=None):
+    """gemm_q with its input stage fused: act = ACT_PLAIN / ACT_RMSNORM
     (RMSNorm(x) * norm_w per row) / ACT_SILU_MUL (x rows [gate | up]). x may
-    be a row-strided view (x.stride(1) == 1); m defaults to x.shape[0]."""
+    be a row-strided view (x.stride(1) == 1); m defaults to x.shape[0].
+    add: (pointer, n_slices, slice_stride) of K-slice partials (from
+    gemm_partials) folded into x first and stored back. With GEMM_DEFER the
+    product stays in ws as partials and `out` is not written."""
     import torch
     if x.dim() == 1:
         x = x.view(1, -1)
     if x.dtype != torch.float32 or x.stride(1) != 1:
         raise ValueError("x must be float32 with unit column stride")
     m = x.shape[0] if m is None else m
-    if out is None:
+    if out is None and not (flags & GEMM_DEFER):
         out = torch.empty((m, n), dtype=torch.float32, device=x.device)
     L = _lib.load()
     if ws is None:
-        ws = torch.empty(gemm_ws_bytes(qtype, m, n, k, flags & ~GEMM_REUSE), dtype=torch.uint8, device=x.device)
-    nw = None if norm_w is None else _ptr(norm_w)
-    _lib.check(L.ihip_gemm_q_ex(qtype, _ptr(w_dev), _ptr(x), x.stride(0), act, nw, eps, _ptr(out), m, n, k, flags,
+        ws = torch.empty(gemm_ws_bytes(qtype, m, n, k, flags), dtype=torch.uint8, device=x.device)
+    gi = _lib.GemmInput(_ptr(x), x.stride(0), act, None if norm_w is None else _ptr(norm_w), eps,
+                        None if add is None else add[0], 0 if add is None else add[1],
+                        0 if add is None else add[2])
+    _lib.check(L.ihip_gemm_q_ex(qtype, _ptr(w_dev), C.byref(gi), None if out is None else _ptr(out), m, n, k, flags,
                                 _ptr(ws), ws.numel(), _stream(stream)))
     return out
+
+
+def gemm_partials(qtype: int, m: int, n: int, k: int, flags: int, ws):
+    """(pointer, n_slices, slice_stride) of the partials a GEMM_DEFER call
+    left in ws."""
+    p, ns, st = C.c_void_p(), C.c_int(), C.c_int64()
+    _lib.check(_lib.load().ihip_gemm_q_partials(qtype, m, n, k, flags, _ptr(ws), C.byref(p), C.byref(ns),
+                                                C.byref(st)))
+    return p.value, ns.value, st.value
 
 
 def gemm_ws_bytes(qtype: int, m: int, n: int, k: int, flags: int = GEMM_AUTO) -> int:
     """Workspace bytes ihip_gemm_q needs for this call shape."""
     nb = C.c_size_t()
-    _lib.check(_lib.load().ihip_gemm_q_ws_bytes(qtype, m, n, k, flags, C.byref(nb)))
+    _lib.check(_lib.load().ihip_gemm_q_ws_bytes(qtype, m, n, k, flags & ~(GEMM_REUSE | GEMM_DEFER), C.byref(nb)))
     return max(int(nb.value), 16)
 
 

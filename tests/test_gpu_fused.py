@@ -106,3 +106,35 @@ def test_ex_errors(ih):
         ih.gemm_q_ex(qt, w, x[:, :256], 16, 256, flags=ih.GEMM_F32 | ih.GEMM_PACKED | ih.GEMM_REUSE)
     with pytest.raises(ih.HipError):
         ih.gemm_q_ex(qt, w, x[:5, :256], 16, 256, act=7)
+
+
+@pytest.mark.parametrize("qt2", [F.Q4_K, F.Q6_K])
+def test_defer_and_fold_residual(ih, qt2):
+    """A deferred down projection (K split over slices) folded into the next
+    matmul's input stage equals the accumulate-then-matmul sequence bit for
+    bit: same slice order, same residual add."""
+    import torch
+    K1, H, N2 = 12288, 512, 96  # first matmul: [H x K1] (3 K-slices), second: [N2 x H]
+    rng = np.random.default_rng(31)
+    w1 = synth.matrix(F.Q6_K, H, K1, synth.stream_for(1, "d1"))
+    w2 = synth.matrix(qt2, N2, H, synth.stream_for(2, "d2"))
+    p1, p2 = ih.pack_weights(F.Q6_K, _dev(w1), H, K1), ih.pack_weights(qt2, _dev(w2), N2, H)
+    fl = ih.GEMM_F32 | ih.GEMM_PACKED
+    for M in (1, 5, 8):
+        h = _dev(rng.standard_normal((M, K1)).astype(np.float32))
+        x0 = _dev(rng.standard_normal((M, H)).astype(np.float32))
+        # reference: x += W1 h (reduced), then y = W2 rmsnorm(x)
+        xr = x0.clone()
+        ih.gemm_q(F.Q6_K, p1, h, H, K1, flags=fl | ih.GEMM_ACCUM, out=xr)
+        yr = ih.gemm_q_ex(qt2, p2, xr, N2, H, act=ih.ACT_RMSNORM, flags=fl)
+        # fused: deferred partials, folded by the next input stage
+        ws1 = torch.empty(ih.quantized_kernels.gemm_ws_bytes(F.Q6_K, M, H, K1, fl), dtype=torch.uint8, device="cuda")
+        ih.gemm_q_ex(F.Q6_K, p1, h, H, K1, flags=fl | ih.GEMM_DEFER, ws=ws1)
+        parts = ih.gemm_partials(F.Q6_K, M, H, K1, fl, ws1)
+        assert parts[1] >= 2
+        xf = x0.clone()
+        yf = ih.gemm_q_ex(qt2, p2, xf, N2, H, act=ih.ACT_RMSNORM, flags=fl, add=parts)
+        assert torch.equal(xf, xr), M
+        assert torch.equal(yf, yr), M
+        ref = O.gemv_f64(F.Q6_K, w1, h.cpu().numpy(), M, H, K1) + x0.cpu().numpy()
+        assert rel_l2(xf.cpu().numpy(), ref) < 1e-5
