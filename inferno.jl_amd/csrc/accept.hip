@@ -90,16 +90,10 @@ __device__ __forceinline__ float2 merge_row(const float2 *part, int nchunk) {
     return make_float2(m, s);
 }
 
-// Merge of a row's chunk partials by one wave: lane l folds chunks l, l+64,
-// ... in order, then a butterfly over the lanes (fixed order: every lane
-// ends with the same value).
-__device__ __forceinline__ float2 wave_merge_row(const float2 *part, int nchunk) {
+// Butterfly merge of one (max, sum) pair per lane; merge_ms is symmetric,
+// so every lane ends with the same value.
+__device__ __forceinline__ float2 wave_merge_pairs(float m, float s) {
     const int lane = threadIdx.x & 63;
-    float m = -__builtin_huge_valf(), s = 0.f;
-    for (int c = lane; c < nchunk; c += 64) {
-        const float2 p = part[c];
-        merge_ms(m, s, p.x, p.y);
-    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
@@ -113,6 +107,18 @@ __device__ __forceinline__ float2 wave_merge_row(const float2 *part, int nchunk)
         }
     }
     return make_float2(m, s);
+}
+
+// Merge of a row's chunk partials by one wave: lane l folds chunks l, l+64,
+// ... in order, then the butterfly.
+__device__ __forceinline__ float2 wave_merge_row(const float2 *part, int nchunk) {
+    const int lane = threadIdx.x & 63;
+    float m = -__builtin_huge_valf(), s = 0.f;
+    for (int c = lane; c < nchunk; c += 64) {
+        const float2 p = part[c];
+        merge_ms(m, s, p.x, p.y);
+    }
+    return wave_merge_pairs(m, s);
 }
 
 __global__ void stats_merge_kernel(const float2 *__restrict__ part, int rows, int nchunk,
@@ -176,9 +182,35 @@ __global__ __launch_bounds__(64) void decide_kernel(const float *__restrict__ tg
     const float2 *Pt = part + (size_t)step * (k + 1) * nchunk;
     const float2 *Pd = part + ((size_t)gridDim.x * (k + 1) + (size_t)step * k) * nchunk;
     const float Tr = mode == 0 ? T : 1.0f;
-    for (int r = 0; r < 2 * k + 1; r++) {
-        const float2 v = wave_merge_row(r <= k ? Pt + (size_t)r * nchunk : Pd + (size_t)(r - k - 1) * nchunk, nchunk);
-        if (lane == 0) ms[r] = v;
+    // rows in batches of 8: all their partials in flight before any merge
+    const int nrows = 2 * k + 1;
+    for (int r0 = 0; r0 < nrows; r0 += 8) {
+        float2 pv[8][2];
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            const int r = min(r0 + b, nrows - 1);
+            const float2 *row = r <= k ? Pt + (size_t)r * nchunk : Pd + (size_t)(r - k - 1) * nchunk;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int c = lane + 64 * h;
+                pv[b][h] = c < nchunk ? row[c] : make_float2(-__builtin_huge_valf(), 0.f);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            const int r = r0 + b;
+            if (r >= nrows) break;
+            float2 v;
+            if (nchunk <= 128) {
+                float m = -__builtin_huge_valf(), sm = 0.f;
+                merge_ms(m, sm, pv[b][0].x, pv[b][0].y);
+                merge_ms(m, sm, pv[b][1].x, pv[b][1].y);
+                v = wave_merge_pairs(m, sm);
+            } else {
+                v = wave_merge_row(r <= k ? Pt + (size_t)r * nchunk : Pd + (size_t)(r - k - 1) * nchunk, nchunk);
+            }
+            if (lane == 0) ms[r] = v;
+        }
     }
     __syncthreads();
     int first = k;  // first draft that is invalid or rejected
