@@ -70,13 +70,19 @@ class Model:
             # q and k/v rows share the input: one matrix [q; k; v] (the packed
             # layout concatenates along tiles)
             lw["qkv"] = torch.cat([lw.pop("q"), lw.pop("kv")])
+            for name in ("attn_norm", "ffn_norm"):  # RMSNorm weights around 1
+                lw[name] = 1.0 + ih.quantized_kernels.synth_gaussian(st(SEED, f"blk{L}.{name}"), H, 0.1)
+                if L < keep_gguf:
+                    hw[name] = lw[name].cpu().numpy()
             self.layers.append(lw)
             if L < keep_gguf:
                 self.host_gguf.append(hw)
         g = ih.quantized_kernels.synth_blocks(F.Q6_K, st(SEED, "output"), VOCAB * H // 256)
         self.lm = ih.pack_weights(F.Q6_K, g, VOCAB, H)
+        self.out_norm = 1.0 + ih.quantized_kernels.synth_gaussian(st(SEED, "output_norm"), H, 0.1)
         self.gguf_bytes += g.numel()
         self.host_lm = g.cpu().numpy()
+        self.host_out_norm = self.out_norm.cpu().numpy()
         del g
         torch.cuda.synchronize()
 
@@ -134,13 +140,14 @@ class VerifyStep:
         parts = ih.gemm_partials(F.Q6_K, M, H, FF, f32, self.ws_down)
         self.x.copy_(self.x0)
         for i, lw in enumerate(self.model.layers):
-            ex(F.Q4_K, lw["qkv"], self.x, NQ + 2 * NKV, H, act=ih.ACT_RMSNORM, flags=f32, out=self.qkv, ws=self.ws,
-               add=parts if i > 0 else None)
+            ex(F.Q4_K, lw["qkv"], self.x, NQ + 2 * NKV, H, act=ih.ACT_RMSNORM, norm_w=lw["attn_norm"], flags=f32,
+               out=self.qkv, ws=self.ws, add=parts if i > 0 else None)
             ex(F.Q4_K, lw["o"], self.qkv[:, :NQ], H, NQ, flags=acc, out=self.x, ws=self.ws)
-            ex(F.Q4_K, lw["gu"], self.x, 2 * FF, H, act=ih.ACT_RMSNORM, flags=f32, out=self.gu, ws=self.ws)
+            ex(F.Q4_K, lw["gu"], self.x, 2 * FF, H, act=ih.ACT_RMSNORM, norm_w=lw["ffn_norm"], flags=f32,
+               out=self.gu, ws=self.ws)
             ex(F.Q6_K, lw["down"], self.gu, H, FF, act=ih.ACT_SILU_MUL, flags=f32 | ih.GEMM_DEFER, ws=self.ws_down)
-        ex(F.Q6_K, self.model.lm, self.x, VOCAB, H, act=ih.ACT_RMSNORM, flags=f32, out=self.logits, ws=self.ws,
-           add=parts)
+        ex(F.Q6_K, self.model.lm, self.x, VOCAB, H, act=ih.ACT_RMSNORM, norm_w=self.model.out_norm, flags=f32,
+           out=self.logits, ws=self.ws, add=parts)
         ih.spec_accept(self.logits.view(1, M, VOCAB), self.drf.view(1, self.k, VOCAB), self.draft, self.T,
                        self.u_acc, self.u_res, self.u_bonus, out_tok=self.out_tok, out_n=self.out_n,
                        ws=self.acc_ws)
@@ -277,18 +284,18 @@ def cpu_baseline(ih, model: Model, n_layers: int, M: int, k: int, budget_s: floa
     else:
         gemv = lambda qt, w, v, K, N: O.gemv_q8k(qt, w, v, K, N, os.cpu_count() or 1)  # noqa: E731
 
-    def rms(v):
-        return (v / np.sqrt((v.astype(np.float64) ** 2).mean() + 1e-6)).astype(np.float32)
+    def rms(v, w):
+        return (v / np.sqrt((v.astype(np.float64) ** 2).mean() + 1e-6) * w).astype(np.float32)
 
     def layers_pass():
         x = x0.copy()
         for lw in hostw:
             for m in range(M):  # forward_cpu! streams the verify tokens one at a time
-                h = rms(x[m])
+                h = rms(x[m], lw["attn_norm"])
                 q = gemv(F.Q4_K, lw["q"], h, H, NQ)
                 gemv(F.Q4_K, lw["kv"], h, H, 2 * NKV)
                 x[m] += gemv(F.Q4_K, lw["o"], q, NQ, H)
-                h = rms(x[m])
+                h = rms(x[m], lw["ffn_norm"])
                 gu = gemv(F.Q4_K, lw["gu"], h, H, 2 * FF)
                 g, u = gu[:FF], gu[FF:]
                 x[m] += gemv(F.Q6_K, lw["down"], (g / (1 + np.exp(-g)) * u).astype(np.float32), FF, H)
@@ -296,7 +303,7 @@ def cpu_baseline(ih, model: Model, n_layers: int, M: int, k: int, budget_s: floa
 
     def head_pass(x):
         for m in range(M):
-            gemv(F.Q6_K, lm, rms(x[m]), H, VOCAB)
+            gemv(F.Q6_K, lm, rms(x[m], model.host_out_norm), H, VOCAB)
         O.spec_accept(Lt, Ld, draft, 0.8, np.full(k, 0.5, np.float32), 0.5, 0.5, 0)
 
     gomp = None

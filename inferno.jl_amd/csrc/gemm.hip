@@ -203,6 +203,49 @@ __device__ __forceinline__ void load_unit_packed(const uint8_t *__restrict__ ch,
     }
 }
 
+// The same lane bytes through a buffer resource over the packed matrix: the
+// chunk offset is wave-uniform (a scalar operand), the lane offsets are fixed
+// per lane, so a load needs no per-item vector address arithmetic. Loads
+// past the resource's size return zero.
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+template <int QT>
+__device__ __forceinline__ void load_unit_buf(__amdgpu_buffer_rsrc_t rs, int soff, int lane, Unit<QT> &r) {
+    const int n = lane & 15, l16 = 16 * lane, n16 = 16 * n;
+    if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {
+        r.q0 = bload16(rs, l16, soff);
+        r.q1 = bload16(rs, l16 + 1024, soff);
+        if constexpr (QT == QT_Q5_K) {
+            r.qh = bload16(rs, 2048 + 16 * (n + 16 * ((lane >> 4) & 1)), soff);
+            r.hdr = bload16(rs, n16 + 2560, soff);
+        } else {
+            r.hdr = bload16(rs, n16 + 2048, soff);
+        }
+    } else if constexpr (QT == QT_Q6_K) {
+        const uint4 A = bload16(rs, l16, soff);
+        const uint4 B = bload16(rs, l16 + 1024, soff);
+        const uint4 H = bload16(rs, l16 + 2048, soff);
+        r.a[0] = A.x; r.a[1] = A.y; r.a[2] = A.z; r.a[3] = A.w;
+        r.b[0] = B.x; r.b[1] = B.y; r.b[2] = B.z; r.b[3] = B.w;
+        r.h[0] = H.x; r.h[1] = H.y; r.h[2] = H.z; r.h[3] = H.w;
+        r.sc = bload16(rs, n16 + 3072, soff);
+        r.d = __builtin_amdgcn_raw_buffer_load_b16(rs, 3328 + 2 * n, soff, 0);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint4 v = bload16(rs, l16 + 1024 * i, soff);
+            r.w0[2 * i] = v.x; r.w1[2 * i] = v.y; r.w0[2 * i + 1] = v.z; r.w1[2 * i + 1] = v.w;
+        }
+        const uint4 dv = bload16(rs, n16 + 4096, soff);
+        const uint32_t dw[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+        for (int b = 0; b < 8; b++) r.d[b] = (dw[b >> 1] >> (16 * (b & 1))) & 0xffffu;
+    }
+}
+
 // One thread per (unit, tile, lane): copies that lane's bytes of the chunk.
 template <int QT>
 __global__ __launch_bounds__(64) void pack_kernel(const uint8_t *__restrict__ W, int N, int K,
@@ -462,58 +505,31 @@ struct ActIn {
     bool defer;          // leave the product as K-slice partials in the workspace
 };
 
-// add != nullptr: x[t][k] += ((add_0 + add_1) + ...)[t][k] (the K-slice
-// partials of a previous matmul, the order its reduce would use), stored back
-// into x (each element has one owner thread), before the transform.
+__device__ __forceinline__ float silu_mul1(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+// RMSNorm weights of elements [k, k + 8), loaded with the activations (1 when
+// there are none)
+__device__ __forceinline__ void norm_weights(const float *__restrict__ norm_w, int op, int k, int K, float4 &a,
+                                             float4 &b) {
+    a = make_float4(1.f, 1.f, 1.f, 1.f);
+    b = a;
+    if (op == ACT_RMSNORM && norm_w != nullptr && k < K) {
+        a = *(const float4 *)(norm_w + k);
+        b = *(const float4 *)(norm_w + k + 4);
+    }
+}
+
+// The transform and layout of one thread's 8 elements (token t, unit u,
+// elements [8 gi, 8 gi + 8) of the unit). The 32 threads of a token (one
+// half-wave, gi = lane % 32) must all call it: the token max, the RMSNorm sum
+// of squares and the sub-block sums are reduced across them.
 template <int LK, int MT, bool SPLIT, bool MINS>
-__global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ X, int ldx, int M, int K, int op,
-                                                   const float *__restrict__ norm_w,
-                                                   uint8_t *__restrict__ afrag, float *__restrict__ xs,
-                                                   float *__restrict__ inv, uint8_t *__restrict__ mfrag,
-                                                   float *__restrict__ ssq, const float *__restrict__ add, int n_add,
-                                                   int64_t add_stride, float *__restrict__ xw) {
+__device__ __forceinline__ void prep_finish(float (&v)[8], float4 wa, float4 wb, int u, int t, int gi, int op,
+                                            uint8_t *__restrict__ afrag, float *__restrict__ xs,
+                                            float *__restrict__ inv, uint8_t *__restrict__ mfrag,
+                                            float *__restrict__ ssq) {
     constexpr int TOK = MT * (SPLIT ? 8 : 16);
     constexpr int ENTRY = Layout<LK>::ENTRY;
-    const int u = blockIdx.x, tid = threadIdx.x;
-    const int tl = tid >> 5, gi = tid & 31;
-    const int t = blockIdx.y * 8 + tl;
-    const int k = u * UNIT + gi * 8;
-    float v[8];
-    if (t < M && k < K) {
-        const float *row = X + (size_t)t * ldx + k;
-        const float4 a = *(const float4 *)row;
-        const float4 b = *(const float4 *)(row + 4);
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-        if (add != nullptr) {
-            float sum[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) sum[e] = 0.f;
-            for (int sl = 0; sl < n_add; sl++) {
-                const float *pa = add + (size_t)sl * add_stride + (size_t)t * K + k;
-                const float4 c = *(const float4 *)pa;
-                const float4 d = *(const float4 *)(pa + 4);
-                const float pv[8] = {c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
-#pragma unroll
-                for (int e = 0; e < 8; e++) sum[e] = sl == 0 ? pv[e] : sum[e] + pv[e];
-            }
-#pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = v[e] + sum[e];
-            float *wrow = xw + (size_t)t * ldx + k;
-            *(float4 *)wrow = make_float4(v[0], v[1], v[2], v[3]);
-            *(float4 *)(wrow + 4) = make_float4(v[4], v[5], v[6], v[7]);
-        }
-        if (op == ACT_SILU_MUL) {
-            const float4 c = *(const float4 *)(row + K);
-            const float4 d = *(const float4 *)(row + K + 4);
-            const float up[8] = {c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
-#pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = v[e] / (1.0f + expf(-v[e])) * up[e];
-        }
-    } else {
-#pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = 0.f;
-    }
     if (op == ACT_RMSNORM) {
         float q = 0.f;
 #pragma unroll
@@ -521,13 +537,9 @@ __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ X, 
 #pragma unroll
         for (int o = 1; o < 32; o <<= 1) q += __shfl_xor(q, o);
         if (gi == 0 && t < TOK) ssq[(size_t)u * TOK + t] = q;
-        if (norm_w != nullptr && k < K) {
-            const float4 a = *(const float4 *)(norm_w + k);
-            const float4 b = *(const float4 *)(norm_w + k + 4);
-            const float w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        const float w[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
 #pragma unroll
-            for (int e = 0; e < 8; e++) v[e] *= w[e];
-        }
+        for (int e = 0; e < 8; e++) v[e] *= w[e];
     }
     float mx = 0.f;
 #pragma unroll
@@ -599,6 +611,61 @@ __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ X, 
         *(h4 *)dst = H;
         if (SPLIT) *(h4 *)(dst + ENTRY) = L;  // slot + 1
     }
+}
+
+// add != nullptr: x[t][k] += ((add_0 + add_1) + ...)[t][k] (the K-slice
+// partials of a previous matmul, the order its reduce would use), stored back
+// into x (each element has one owner thread), before the transform.
+template <int LK, int MT, bool SPLIT, bool MINS>
+__global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ X, int ldx, int M, int K, int op,
+                                                   const float *__restrict__ norm_w,
+                                                   uint8_t *__restrict__ afrag, float *__restrict__ xs,
+                                                   float *__restrict__ inv, uint8_t *__restrict__ mfrag,
+                                                   float *__restrict__ ssq, const float *__restrict__ add, int n_add,
+                                                   int64_t add_stride, float *__restrict__ xw) {
+    const int u = blockIdx.x, tid = threadIdx.x;
+    const int tl = tid >> 5, gi = tid & 31;
+    const int t = blockIdx.y * 8 + tl;
+    const int k = u * UNIT + gi * 8;
+    float4 wa, wb;
+    norm_weights(norm_w, op, k, K, wa, wb);
+    float v[8];
+    if (t < M && k < K) {
+        const float *row = X + (size_t)t * ldx + k;
+        const float4 a = *(const float4 *)row;
+        const float4 b = *(const float4 *)(row + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        if (add != nullptr) {
+            float sum[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) sum[e] = 0.f;
+            for (int sl = 0; sl < n_add; sl++) {
+                const float *pa = add + (size_t)sl * add_stride + (size_t)t * K + k;
+                const float4 c = *(const float4 *)pa;
+                const float4 d = *(const float4 *)(pa + 4);
+                const float pv[8] = {c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
+#pragma unroll
+                for (int e = 0; e < 8; e++) sum[e] = sl == 0 ? pv[e] : sum[e] + pv[e];
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = v[e] + sum[e];
+            float *wrow = xw + (size_t)t * ldx + k;
+            *(float4 *)wrow = make_float4(v[0], v[1], v[2], v[3]);
+            *(float4 *)(wrow + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        }
+        if (op == ACT_SILU_MUL) {
+            const float4 c = *(const float4 *)(row + K);
+            const float4 d = *(const float4 *)(row + K + 4);
+            const float up[8] = {c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = silu_mul1(v[e], up[e]);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = 0.f;
+    }
+    prep_finish<LK, MT, SPLIT, MINS>(v, wa, wb, u, t, gi, op, afrag, xs, inv, mfrag, ssq);
 }
 
 // ---------------------------------------------------------------- gemm
@@ -858,9 +925,7 @@ __device__ __forceinline__ void compute_v(const Unit<QT> &r, const AReg<QT> &a, 
         }
     } else if constexpr (QT == QT_Q6_K) {
         const float d = live ? half_bits(r.d) : 0.f;
-        float dinv[SPLIT ? 2 : 4];
-#pragma unroll
-        for (int u = 0; u < (SPLIT ? 2 : 4); u++) dinv[u] = d * inv[u];
+        f4 sacc = f4{0.f, 0.f, 0.f, 0.f};  // sum over sub-blocks of sc_s * (q . x)_s
         const h2 off = as_h2(0xE420E420u);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -880,10 +945,11 @@ __device__ __forceinline__ void compute_v(const Unit<QT> &r, const AReg<QT> &a, 
                 const float scf = (float)(int)(int8_t)((scw >> (8 * (sb & 3))) & 0xffu);
                 const f4 c = mfma16(a.f[sb], b, f4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-                for (int v = 0; v < 4; v++)
-                    acc[v] = __builtin_fmaf(dinv[acc_token_u<SPLIT>(v)] * scf, c[v], acc[v]);
+                for (int v = 0; v < 4; v++) sacc[v] = __builtin_fmaf(scf, c[v], sacc[v]);
             }
         }
+#pragma unroll
+        for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf(d * inv[acc_token_u<SPLIT>(v)], sacc[v], acc[v]);
     } else {
         const h2 off = as_h2(0xE480E480u);
 #pragma unroll
@@ -915,13 +981,17 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     constexpr int UNIT_BYTES = (QT == QT_Q8_0) ? 8 * 34 : C::BB;
     constexpr int R = 4;
     static_assert(R % UPS == 0, "ring positions must map to fixed units");
-    __shared__ __align__(16) float red[2][NW][64][TPL];
+    // partial tiles meet in LDS in batches of F tiles (double-buffered), one
+    // barrier per batch (Q6_K, short of registers: one tile per batch)
+    constexpr int F = (QT == QT_Q6_K) ? 1 : (TPL == 4) ? NW / 2 : NW;
+    __shared__ __align__(16) float red[2][F][NW][64][TPL];
     __shared__ float rs[TOK];  // RMSNorm row scales (1 without RMSNorm)
 
     const int n_units = (K + UNIT - 1) / UNIT;
     const int n_tiles = (N + 15) / 16;
     const int G = gridDim.x;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // wave index as a scalar: everything derived from it stays in SGPRs
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n_in = lane & 15, g = lane >> 4;
     const int my_tiles = (n_tiles - 1 - (int)blockIdx.x) / G + 1;  // the plan keeps G <= n_tiles
     const int unit0 = ((int)blockIdx.y * NW + wave) * UPS;
@@ -964,12 +1034,20 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
 
     // 2. weight stream over items (tile j, unit u), u fastest; past the last
     //    tile the loads repeat the last one so every step issues one batch
+    // packed weights: one buffer resource over the matrix (the host keeps it
+    // below 4 GiB on this path)
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(W), (short)0, (int)(PK ? (uint32_t)n_tiles * n_units * Packed<QT>::CHUNK : 0u),
+        0x00020000);
     auto load_item = [&](int j, int u, Unit<QT> &b) {
         j = min(j, my_tiles - 1);
         const int un = min(unit0 + u, n_units - 1);
         if constexpr (PK) {
             const int tile = (int)blockIdx.x + G * j;
-            load_unit_packed<QT>(W + ((size_t)tile * n_units + un) * Packed<QT>::CHUNK, lane, b);
+            if constexpr (QT == QT_Q6_K)  // (its registers are full: global loads spill less)
+                load_unit_packed<QT>(W + ((size_t)tile * n_units + un) * Packed<QT>::CHUNK, lane, b);
+            else
+                load_unit_buf<QT>(wrs, (tile * n_units + un) * Packed<QT>::CHUNK, lane, b);
         } else {
             const int row = min(((int)blockIdx.x + G * j) * 16 + n_in, N - 1);
             load_unit<QT>(W + (size_t)row * row_bytes + (size_t)un * UNIT_BYTES, g, un == n_units - 1 ? tail_blk : 8,
@@ -1002,21 +1080,23 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
                 if constexpr (C::MINS) v -= 32.0f * (SPLIT ? macc[2 * k] + macc[2 * k + 1] : macc[k]);
                 vals[k] = v;
             }
-            float *slot = &red[j & 1][wave][lane][0];
+            const int jb = j % F, hb = (j / F) & 1;
+            float *slot = &red[hb][jb][wave][lane][0];
 #pragma unroll
             for (int k = 0; k < TPL; k++) slot[k] = vals[k];
             acc = f4{0.f, 0.f, 0.f, 0.f};
             macc = f4{0.f, 0.f, 0.f, 0.f};
-            __syncthreads();
-            if (wave == j % NW) {
+            // batch complete: wave i sums tile i of the batch in wave order
+            if (jb == F - 1 || j == my_tiles - 1) __syncthreads();
+            if ((jb == F - 1 || j == my_tiles - 1) && wave <= jb) {
                 float sum[TPL];
 #pragma unroll
-                for (int k = 0; k < TPL; k++) sum[k] = red[j & 1][0][lane][k];
+                for (int k = 0; k < TPL; k++) sum[k] = red[hb][wave][0][lane][k];
 #pragma unroll
                 for (int w = 1; w < NW; w++)
 #pragma unroll
-                    for (int k = 0; k < TPL; k++) sum[k] += red[j & 1][w][lane][k];
-                const int r = ((int)blockIdx.x + G * j) * 16 + n_in;
+                    for (int k = 0; k < TPL; k++) sum[k] += red[hb][wave][w][lane][k];
+                const int r = ((int)blockIdx.x + G * (j - jb + wave)) * 16 + n_in;
                 if (r < N) {
 #pragma unroll
                     for (int k = 0; k < TPL; k++) {
@@ -1133,6 +1213,8 @@ static int env_int(const char *name, int dflt) {
     return v ? atoi(v) : dflt;
 }
 
+size_t packed_bytes(int qt, int N, int K);
+
 static GemmPlan plan_gemm(int qt, int M, int N, int K, int flags) {
     GemmPlan p{};
     const bool force_f32 = flags & 1, force_half = flags & 2;
@@ -1148,7 +1230,8 @@ static GemmPlan plan_gemm(int qt, int M, int N, int K, int flags) {
     static const int lds_a = env_int("IHIP_GEMM_LDS_A", 32768);
     static const int use_stream = env_int("IHIP_STREAM", 1);
     static const int env_ups = env_int("IHIP_STREAM_UPS", 0);
-    p.stream = use_stream && p.MT == 1;
+    // (the streaming kernel addresses packed weights with 32-bit offsets)
+    p.stream = use_stream && p.MT == 1 && !((flags & 8) && packed_bytes(qt, N, K) >= ((size_t)1 << 31));
     if (p.stream) {
         // K per workgroup NW*UPS units; prefer one K-slice (no partials) with
         // the fewest units per wave that still covers K, else the largest
