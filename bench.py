@@ -153,19 +153,6 @@ class VerifyStep:
                        ws=self.acc_ws)
 
 
-def time_op(fn, iters: int, stream):
-    """Average duration of fn() over `iters` launches, HIP events on `stream`."""
-    import torch
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for i in range(iters):
-        fn(i)
-    e1.record(stream)
-    e1.synchronize()
-    return e0.elapsed_time(e1) / iters * 1e-3
-
-
 def gemm_roofline(ih, model: Model, n_layers: int, M: int, iters: int = 64, replays: int = 3):
     """Dominant kernel: the Q4_K gate/up dequant-matmul (24576x4096, M=5)
     over the layers' weights in turn (1.8 GB, far beyond the 256 MB cache).
@@ -235,12 +222,16 @@ def read_traffic():
     return None
 
 
-def gemm_sweep(ih, model: Model, n_layers: int):
-    """GB/s of the Q4_K gate/up and Q6_K down projections at M = 1..8."""
+def gemm_sweep(ih, model: Model, n_layers: int, launches: int = 32, replays: int = 3):
+    """GB/s of the Q4_K gate/up and Q6_K down projections at M = 1..8: per M,
+    a HIP graph of `launches` matmuls over the layers' weights in turn (cold:
+    1.8 GB and 1.3 GB, far beyond the caches), timed with events on the
+    graph's stream."""
     import torch
     F = ih.formats
     out = {}
-    s = torch.cuda.current_stream()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
     for name, key, qt, N, K in (("q4k_24576x4096", "gu", F.Q4_K, 2 * FF, H),
                                 ("q6k_4096x12288", "down", F.Q6_K, H, FF)):
         row = {}
@@ -249,12 +240,24 @@ def gemm_sweep(ih, model: Model, n_layers: int):
             y = torch.empty((M, N), device="cuda")
             fl = ih.GEMM_F32 | ih.GEMM_PACKED
             ws = torch.empty(ih.quantized_kernels.gemm_ws_bytes(qt, M, N, K, fl), dtype=torch.uint8, device="cuda")
-            fn = lambda i: ih.gemm_q(qt, model.layers[i % n_layers][key], x, N, K,  # noqa: E731
-                                     flags=fl, out=y, ws=ws)
-            for i in range(3):
-                fn(i)
+            with torch.cuda.stream(s):
+                ih.gemm_q_ex(qt, model.layers[0][key], x, N, K, flags=fl, out=y, ws=ws)  # prepares x
             torch.cuda.synchronize()
-            t = time_op(fn, 32, s)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=s):
+                for i in range(launches):
+                    ih.gemm_q_ex(qt, model.layers[i % n_layers][key], x, N, K, flags=fl | ih.GEMM_REUSE, out=y,
+                                 ws=ws)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(s):
+                graph.replay()
+                torch.cuda.synchronize()
+                e0.record(s)
+                for _ in range(replays):
+                    graph.replay()
+                e1.record(s)
+            e1.synchronize()
+            t = e0.elapsed_time(e1) * 1e-3 / (replays * launches)
             gbs = (F.matrix_bytes(qt, N, K) + M * K * 4 + M * N * 4) / t / 1e9
             row[str(M)] = round(gbs, 1)
         out[name] = row
@@ -288,6 +291,7 @@ def cpu_baseline(ih, model: Model, n_layers: int, M: int, k: int, budget_s: floa
         return (v / np.sqrt((v.astype(np.float64) ** 2).mean() + 1e-6) * w).astype(np.float32)
 
     def layers_pass():
+        np.seterr(over="ignore")  # exp(-g) of very negative gates: silu -> -0, as in fp32 C
         x = x0.copy()
         for lw in hostw:
             for m in range(M):  # forward_cpu! streams the verify tokens one at a time

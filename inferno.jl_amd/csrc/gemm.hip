@@ -507,6 +507,35 @@ struct ActIn {
 
 __device__ __forceinline__ float silu_mul1(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
+// Half-wave (32-lane) butterflies: levels lane ^ 1, lane ^ 2 (DPP quad
+// permutes), lane 7 - i within 8 and 15 - i within 16 (DPP mirrors: after
+// the quad levels every lane of a quad holds the same value, so a mirror
+// pairs the same two partial results as lane ^ 4 and lane ^ 8 would), then
+// lane ^ 16 (one swizzle through the LDS crossbar). Every lane ends with the
+// full result; the additions are the xor tree's, in the same pairs.
+template <int CTRL> __device__ __forceinline__ float dppf(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float xor16(float v) {  // bitmask swizzle: and 0x1f, or 0, xor 0x10
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+__device__ __forceinline__ float rows_sum(float v) { return v + xor16(v); }
+__device__ __forceinline__ float rows_max(float v) { return fmaxf(v, xor16(v)); }
+__device__ __forceinline__ float half_wave_sum(float v) {
+    v += dppf<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dppf<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dppf<0x141>(v);  // row_half_mirror
+    v += dppf<0x140>(v);  // row_mirror
+    return rows_sum(v);
+}
+__device__ __forceinline__ float half_wave_max(float v) {
+    v = fmaxf(v, dppf<0xB1>(v));
+    v = fmaxf(v, dppf<0x4E>(v));
+    v = fmaxf(v, dppf<0x141>(v));
+    v = fmaxf(v, dppf<0x140>(v));
+    return rows_max(v);
+}
+
 // RMSNorm weights of elements [k, k + 8), loaded with the activations (1 when
 // there are none)
 __device__ __forceinline__ void norm_weights(const float *__restrict__ norm_w, int op, int k, int K, float4 &a,
@@ -534,8 +563,7 @@ __device__ __forceinline__ void prep_finish(float (&v)[8], float4 wa, float4 wb,
         float q = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; e++) q = __builtin_fmaf(v[e], v[e], q);
-#pragma unroll
-        for (int o = 1; o < 32; o <<= 1) q += __shfl_xor(q, o);
+        q = half_wave_sum(q);
         if (gi == 0 && t < TOK) ssq[(size_t)u * TOK + t] = q;
         const float w[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
 #pragma unroll
@@ -546,11 +574,10 @@ __device__ __forceinline__ void prep_finish(float (&v)[8], float4 wa, float4 wb,
     for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(v[e]));
     float sm = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
     // token max over the 32 threads of this token (one half-wave)
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    mx = half_wave_max(mx);
     // sub-block (32 elements = 4 threads) sums
-    sm += __shfl_xor(sm, 1);
-    sm += __shfl_xor(sm, 2);
+    sm += dppf<0xB1>(sm);
+    sm += dppf<0x4E>(sm);
     int e2 = 0;
     if (mx > 0.f && mx < __builtin_huge_valf()) {
         int ex;
