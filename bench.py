@@ -94,11 +94,11 @@ class Model:
 class VerifyStep:
     """One verify step: layers, final norm, lm_head, accept."""
 
-    def __init__(self, ih, model: Model, M: int, k: int, T: float):
+    def __init__(self, ih, model: Model, M: int, k: int, T: float, prec: int = 1):
         import torch
         dev = "cuda"
         F = ih.formats
-        self.ih, self.model, self.M, self.k, self.T = ih, model, M, k, T
+        self.ih, self.model, self.M, self.k, self.T, self.prec = ih, model, M, k, T, prec
         st = ih.synth.stream_for
         self.x0 = ih.quantized_kernels.synth_gaussian(st(SEED, "x0"), M * H).view(M, H)
         self.x = torch.empty_like(self.x0)
@@ -106,7 +106,7 @@ class VerifyStep:
         self.gu = torch.empty((M, 2 * FF), device=dev)
         self.logits = torch.empty((M, VOCAB), device=dev)
         gws = ih.quantized_kernels.gemm_ws_bytes
-        fl = ih.GEMM_F32 | ih.GEMM_PACKED | ih.GEMM_ACCUM
+        fl = prec | ih.GEMM_PACKED | ih.GEMM_ACCUM
         wsb = max(gws(F.Q4_K, M, NQ + 2 * NKV, H, fl), gws(F.Q4_K, M, H, NQ, fl),
                   gws(F.Q4_K, M, 2 * FF, H, fl), gws(F.Q6_K, M, H, FF, fl), gws(F.Q6_K, M, VOCAB, H, fl))
         self.ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
@@ -127,7 +127,11 @@ class VerifyStep:
         self.out_n = torch.zeros(1, dtype=torch.int32, device=dev)
 
     def run(self):
-        """One verify step: per layer [residual += previous down] + RMSNorm
+        self.forward()
+        self.accept()
+
+    def forward(self):
+        """The target forward of one verify step: per layer [residual += previous down] + RMSNorm
         -> [q; k; v] -> o (+= into the residual) -> RMSNorm -> [gate; up] ->
         SiLU gating -> down (left as K-slice partials); final residual add +
         RMSNorm -> lm_head -> accept. RMSNorm, SiLU gating and the residual
@@ -135,7 +139,7 @@ class VerifyStep:
         that consumes them."""
         ih, F, M = self.ih, self.ih.formats, self.M
         ex = ih.gemm_q_ex
-        f32 = ih.GEMM_F32 | ih.GEMM_PACKED
+        f32 = self.prec | ih.GEMM_PACKED  # (GEMM_F32, or 0: fp32-accurate below 16 tokens, half above)
         acc = f32 | ih.GEMM_ACCUM
         parts = ih.gemm_partials(F.Q6_K, M, H, FF, f32, self.ws_down)
         self.x.copy_(self.x0)
@@ -148,9 +152,51 @@ class VerifyStep:
             ex(F.Q6_K, lw["down"], self.gu, H, FF, act=ih.ACT_SILU_MUL, flags=f32 | ih.GEMM_DEFER, ws=self.ws_down)
         ex(F.Q6_K, self.model.lm, self.x, VOCAB, H, act=ih.ACT_RMSNORM, norm_w=self.model.out_norm, flags=f32,
            out=self.logits, ws=self.ws, add=parts)
-        ih.spec_accept(self.logits.view(1, M, VOCAB), self.drf.view(1, self.k, VOCAB), self.draft, self.T,
-                       self.u_acc, self.u_res, self.u_bonus, out_tok=self.out_tok, out_n=self.out_n,
-                       ws=self.acc_ws)
+
+    def accept(self):
+        self.ih.spec_accept(self.logits.view(1, self.M, VOCAB), self.drf.view(1, self.k, VOCAB), self.draft,
+                            self.T, self.u_acc, self.u_res, self.u_bonus, out_tok=self.out_tok, out_n=self.out_n,
+                            ws=self.acc_ws)
+
+
+class TreeStep(VerifyStep):
+    """Config 5: a 64-node draft tree (branching 4, 4, 4 in BFS order,
+    truncated to 64 nodes) verified in one forward at M = 64 (half-precision
+    MFMA operands, the default at M >= 16), then the tree accept walk at
+    T = 1.0 with one uniform per node."""
+
+    def __init__(self, ih, model: Model, n: int = 64, T: float = 1.0):
+        import torch
+        super().__init__(ih, model, n, 1, T, prec=0)
+        st = ih.synth.stream_for
+        par = [-1]
+        for i in range(1, n):  # node i's parent: BFS over branching 4
+            par.append((i - 1) // 4)
+        self.parent = torch.tensor(par, dtype=torch.int32, device="cuda")
+        self.forward()  # target logits of the tree's rows (the timed steps recompute them)
+        torch.cuda.synchronize()
+        # draft rows around the target rows; each node's token drawn from its parent's draft row
+        self.drf_t = ih.quantized_kernels.synth_gaussian(st(SEED, "tree_draft"), n * VOCAB, 1.5,
+                                                         add=self.logits).view(n, VOCAB)
+        g = torch.Generator(device="cpu").manual_seed(SEED + 5)
+        tok = [0]
+        for i in range(1, n):
+            p = torch.softmax(self.drf_t[par[i]].cpu().double() / T, -1)
+            tok.append(int(torch.multinomial(p, 1, generator=g)))
+        self.tok = torch.tensor(tok, dtype=torch.int32, device="cuda")
+        self.u = torch.rand(n, generator=g).to("cuda")
+        nb = C.c_size_t()
+        ih._lib.check(ih.load().ihip_accept_ws_bytes(3 * n, VOCAB, C.byref(nb)))
+        self.tree_ws = torch.empty(nb.value, dtype=torch.uint8, device="cuda")
+        self.path = torch.zeros(n, dtype=torch.int32, device="cuda")
+        self.plen = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def accept(self):
+        q = self.ih.quantized_kernels
+        self.ih._lib.check(self.ih.load().ihip_tree_accept(
+            q._ptr(self.logits), q._ptr(self.drf_t), q._ptr(self.tok), q._ptr(self.parent), self.M, VOCAB, self.T,
+            q._ptr(self.u), q._ptr(self.path), q._ptr(self.plen), q._ptr(self.tree_ws), self.tree_ws.numel(),
+            q._stream(None)))
 
 
 def gemm_roofline(ih, model: Model, n_layers: int, M: int, iters: int = 64, replays: int = 3):
@@ -264,6 +310,170 @@ def gemm_sweep(ih, model: Model, n_layers: int, launches: int = 32, replays: int
     return out
 
 
+def graph_time(fn, replays: int = 5):
+    """Seconds per replay of a HIP graph of fn()'s launches (captured once on a
+    side stream after one eager run), timed with events on that stream."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        fn()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        graph.replay()
+        torch.cuda.synchronize()
+        e0.record(s)
+        for _ in range(replays):
+            graph.replay()
+        e1.record(s)
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / replays
+
+
+def config1(ih):
+    """Config 1: one Q4_K GEMV, W[3072 x 1024], M = 1; cold (a graph over
+    >= 300 MB of weight copies, beyond the 256 MB infinity cache) and warm
+    (one copy). 'call' is the whole ihip_gemm_q call (input stage + matmul),
+    'matmul' the matmul kernel with the input prepared once."""
+    import torch
+    F = ih.formats
+    N, K = 3072, 1024
+    wb = F.matrix_bytes(F.Q4_K, N, K)
+    copies = int(300e6 // wb) + 1
+    ws_ = [ih.pack_weights(F.Q4_K, ih.quantized_kernels.synth_blocks(F.Q4_K, ih.synth.stream_for(SEED - 2, f"c1.{c}"),
+                                                                     N * K // 256), N, K) for c in range(copies)]
+    x = ih.quantized_kernels.synth_gaussian(ih.synth.stream_for(SEED - 2, "x"), K).view(1, K)
+    y = torch.empty((1, N), device="cuda")
+    fl = ih.GEMM_F32 | ih.GEMM_PACKED
+    wsp = torch.empty(ih.quantized_kernels.gemm_ws_bytes(F.Q4_K, 1, N, K, fl), dtype=torch.uint8, device="cuda")
+    alg = wb + K * 4 + N * 4
+    out = {"weight_bytes": wb, "algorithmic_bytes": alg}
+    for mode, pick in (("cold", lambda i: ws_[i % copies]), ("warm", lambda i: ws_[0])):
+        for kind, extra in (("call", 0), ("matmul", ih.GEMM_REUSE)):
+            ih.gemm_q_ex(F.Q4_K, ws_[0], x, N, K, flags=fl, out=y, ws=wsp)
+            t = graph_time(lambda: [ih.gemm_q_ex(F.Q4_K, pick(i), x, N, K, flags=fl | extra, out=y, ws=wsp)
+                                    for i in range(copies)]) / copies
+            out[f"{mode}_{kind}_us"] = round(t * 1e6, 2)
+            out[f"{mode}_{kind}_GBps"] = round(alg / t / 1e9, 1)
+    del ws_
+    return out
+
+
+def config2(ih):
+    """Config 2: one verify batch at M = 5, hidden 2048: Q4_K q 2048x2048,
+    k/v 512x2048, o 2048x2048, gate/up 6144x2048, Q6_K down 2048x6144, Q8_0
+    2048x2048 (8 matmuls, each with its input stage), cold over >= 300 MB of
+    weight sets."""
+    import torch
+    F = ih.formats
+    M, Hd, Fd = 5, 2048, 6144
+    mats = [("q", F.Q4_K, Hd, Hd), ("k", F.Q4_K, 512, Hd), ("v", F.Q4_K, 512, Hd), ("o", F.Q4_K, Hd, Hd),
+            ("gate", F.Q4_K, Fd, Hd), ("up", F.Q4_K, Fd, Hd), ("down", F.Q6_K, Hd, Fd), ("q8", F.Q8_0, Hd, Hd)]
+    set_bytes = sum(F.matrix_bytes(qt, n, k) for _, qt, n, k in mats)
+    sets = int(300e6 // set_bytes) + 1
+    st = ih.synth.stream_for
+    W = [{name: ih.pack_weights(qt, ih.quantized_kernels.synth_blocks(qt, st(SEED - 1, f"c2.{c}.{name}"),
+                                                                       n * k // F.BLOCK_ELEMS[qt]), n, k)
+          for name, qt, n, k in mats} for c in range(sets)]
+    x = ih.quantized_kernels.synth_gaussian(st(SEED - 1, "x"), M * Hd).view(M, Hd)
+    xf = ih.quantized_kernels.synth_gaussian(st(SEED - 1, "xf"), M * Fd).view(M, Fd)
+    fl = ih.GEMM_F32 | ih.GEMM_PACKED
+    ys = {name: torch.empty((M, n), device="cuda") for name, _, n, _ in mats}
+    wsb = max(ih.quantized_kernels.gemm_ws_bytes(qt, M, n, k, fl) for _, qt, n, k in mats)
+    wsp = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+
+    def batch():
+        for c in range(sets):
+            for name, qt, n, k in mats:
+                ih.gemm_q_ex(qt, W[c][name], xf if name == "down" else x, n, k, flags=fl, out=ys[name], ws=wsp)
+    t = graph_time(batch) / sets
+    alg = set_bytes + sum(M * k * 4 + M * n * 4 for _, _, n, k in mats)
+    del W
+    return {"us_per_batch": round(t * 1e6, 2), "weight_bytes": set_bytes, "algorithmic_bytes": alg,
+            "GBps": round(alg / t / 1e9, 1), "frac": round(alg / t / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
+def config3(ih, n_steps: int = 4096, per_call: int = 6):
+    """Config 3: Q6_K lm_head 151936x2048 + rejection-sampling accept over
+    n_steps independent verify steps (k = 4, T = 0.8, fresh hidden states per
+    step). The target rows of `per_call` steps share one fp32-accurate matmul
+    (5 per_call <= 32 rows) and one accept call covers all steps; inputs are
+    resident in HBM (draft logits = target + N(0, 1.5^2), draft tokens drawn
+    from them beforehand)."""
+    import torch
+    F = ih.formats
+    Hd, k, T = 2048, 4, 0.8
+    st = ih.synth.stream_for
+    lm = ih.pack_weights(F.Q6_K, ih.quantized_kernels.synth_blocks(F.Q6_K, st(SEED - 3, "output"),
+                                                                   VOCAB * Hd // 256), VOCAB, Hd)
+    rows = n_steps * (k + 1)
+    Hs = ih.quantized_kernels.synth_gaussian(st(SEED - 3, "h"), rows * Hd).view(rows, Hd)
+    Lt = torch.empty((rows, VOCAB), device="cuda")
+    fl = ih.GEMM_F32 | ih.GEMM_PACKED
+    m = per_call * (k + 1)
+    wsp = torch.empty(ih.quantized_kernels.gemm_ws_bytes(F.Q6_K, m, VOCAB, Hd, fl), dtype=torch.uint8, device="cuda")
+    calls = [(r0, min(m, rows - r0)) for r0 in range(0, rows, m)]
+
+    def gemms():
+        for r0, mm in calls:
+            ih.gemm_q_ex(F.Q6_K, lm, Hs[r0:r0 + mm], VOCAB, Hd, flags=fl, out=Lt[r0:r0 + mm], ws=wsp)
+    gemms()
+    torch.cuda.synchronize()
+    L3 = Lt.view(n_steps, k + 1, VOCAB)
+    Ld = torch.empty((n_steps, k, VOCAB), device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(SEED + 3)
+    draft = torch.empty((n_steps, k), dtype=torch.int32, device="cuda")
+    for s0 in range(0, n_steps, 256):
+        blk = L3[s0:s0 + 256, :k].contiguous()
+        ih.quantized_kernels.synth_gaussian(st(SEED - 3, f"d{s0}"), blk.numel(), 1.5, add=blk,
+                                            out=Ld[s0:s0 + 256].view(-1))
+        p = torch.softmax(Ld[s0:s0 + 256].view(-1, VOCAB) / T, -1)
+        draft[s0:s0 + 256] = torch.multinomial(p, 1, generator=g).view(-1, k).to(torch.int32)
+        del p
+    u_acc = torch.rand((n_steps, k), generator=g, device="cuda")
+    u_res = torch.rand(n_steps, generator=g, device="cuda")
+    u_bon = torch.rand(n_steps, generator=g, device="cuda")
+    nb = C.c_size_t()
+    ih._lib.check(ih.load().ihip_spec_accept_ws_bytes(n_steps, k, VOCAB, C.byref(nb)))
+    aws = torch.empty(nb.value, dtype=torch.uint8, device="cuda")
+    out_tok = torch.zeros((n_steps, k + 1), dtype=torch.int32, device="cuda")
+    out_n = torch.zeros(n_steps, dtype=torch.int32, device="cuda")
+
+    def accept():
+        ih.spec_accept(L3, Ld, draft, T, u_acc, u_res, u_bon, out_tok=out_tok, out_n=out_n, ws=aws)
+
+    t_gemm = graph_time(gemms, replays=2)
+    t_acc = graph_time(accept, replays=2)
+    acc_rate = float(out_n.double().mean()) / k
+    alg = len(calls) * F.matrix_bytes(F.Q6_K, VOCAB, Hd) + rows * Hd * 4 + rows * VOCAB * 4
+    del Lt, Ld, Hs
+    return {"steps": n_steps, "steps_per_matmul": per_call, "ms_matmuls": round(t_gemm * 1e3, 3),
+            "ms_accept": round(t_acc * 1e3, 3), "steps_per_s": round(n_steps / (t_gemm + t_acc), 1),
+            "matmul_GBps": round(alg / t_gemm / 1e9, 1), "mean_accepted_fraction": round(acc_rate, 4)}
+
+
+def config5(ih, model: Model):
+    """Config 5: 64-node tree verify (32 layers and the lm_head at M = 64 on
+    the half-precision MFMA path, then the tree accept walk)."""
+    F = ih.formats
+    step = TreeStep(ih, model)
+    t = graph_time(step.run, replays=5)
+    t_fwd = graph_time(step.forward, replays=5)
+    weights = sum(F.matrix_bytes(qt, n, k) // F.BLOCK_BYTES[qt] * F.BLOCK_ELEMS[qt]
+                  for qt, n, k in [(F.Q4_K, NQ + 2 * NKV, H), (F.Q4_K, H, NQ), (F.Q4_K, 2 * FF, H),
+                                   (F.Q6_K, H, FF)]) * len(model.layers) + VOCAB * H
+    flops = 2 * 64 * weights
+    return {"ms_per_tree": round(t * 1e3, 3), "trees_per_s": round(1 / t, 2), "ms_forward": round(t_fwd * 1e3, 3),
+            "forward_TFLOPs": round(flops / t_fwd / 1e12, 1),
+            "mfma_frac_fp16_dense": round(flops / t_fwd / 2.5e15, 4),
+            "forward_GBps": round(model.weight_bytes(len(model.layers)) / t_fwd / 1e9, 1),
+            "accepted_path_len": int(step.plen[0])}
+
+
 def cpu_baseline(ih, model: Model, n_layers: int, M: int, k: int, budget_s: float):
     """The reference CPU path on a bounded sample: S_L layers + lm_head + accept,
     scaled to the full step. Reference kernels from oracle/_ref (kind
@@ -364,6 +574,9 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only run the roofline kernel and the traffic calibration kernel (for rocprofv3 --pmc)")
+    ap.add_argument("--configs", type=str, default="",
+                    help="instead of the bench line: measure BASELINE configs (comma list of 1,2,3,5), one JSON "
+                         "object per config")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -376,6 +589,16 @@ def main():
     assert ih.quant_kernels_available(), ih._lib.last_error()
     k, T = 4, 0.8
     t0 = time.time()
+    if args.configs:
+        want = [c.strip() for c in args.configs.split(",") if c.strip()]
+        for c in want:
+            if c == "5":
+                res = config5(ih, Model(ih, args.layers, keep_gguf=0))
+            else:
+                res = {"1": config1, "2": config2, "3": config3}[c](ih)
+            print(json.dumps({"config": int(c), **res}), flush=True)
+            torch.cuda.empty_cache()
+        return
     model = Model(ih, args.layers, keep_gguf=0 if (args.no_cpu or args.profile_kernels) else 4)
     step = VerifyStep(ih, model, args.m, k, T)
     log(f"setup {time.time() - t0:.1f}s, weights {model.weight_bytes(args.layers) / 1e9:.3f} GB")

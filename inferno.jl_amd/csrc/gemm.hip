@@ -590,14 +590,14 @@ __device__ __forceinline__ void prep_finish(float (&v)[8], float4 wa, float4 wb,
     if (MINS && xs != nullptr && (gi & 3) == 0) xs[((size_t)u * 8 + (gi >> 2)) * TOK + t] = sm;
     const int mt = SPLIT ? t / 8 : t / 16;
     const int slot = SPLIT ? (t % 8) * 2 : t % 16;
-    if (MINS && MT == 1 && mfrag != nullptr && (gi & 3) == 0) {
+    if (MINS && mfrag != nullptr && (gi & 3) == 0) {
         // A operand of the mins MFMA (16x16x16): lane (slot, G) item e holds
         // sub-block 4G + e of the scaled sub-block sums (G < 2; zero for
         // G >= 2). X_s * scale / 32 stays below 2^15.
         const int sb = gi >> 2, G = sb >> 2, e = sb & 3;
         const float xsum = sm * scale * (1.0f / 32.0f);
         const _Float16 h = (_Float16)xsum, l = (_Float16)(xsum - (float)h);
-        _Float16 *mf = (_Float16 *)(mfrag + (size_t)u * 64 * 8);
+        _Float16 *mf = (_Float16 *)(mfrag + ((size_t)u * MT + mt) * 512);
         mf[(G * 16 + slot) * 4 + e] = h;
         mf[((G + 2) * 16 + slot) * 4 + e] = (_Float16)0.0f;
         if (SPLIT) {
@@ -899,12 +899,14 @@ template <> struct AReg<QT_Q5_K> { h8 f[8]; h4 mins; };
 template <> struct AReg<QT_Q6_K> { h4 f[16]; };
 template <> struct AReg<QT_Q8_0> { h8 f[8]; };
 
-// One unit against register operands. acc: scaled dot products, macc: the
-// Q4_K/Q5_K min term / 32 (both in the MFMA D layout: slot 4g + v, row n).
+// One unit against register operands of MT token tiles: each weight
+// fragment is dequantized once and multiplies every tile. acc[mt]: scaled dot
+// products, macc[mt]: the Q4_K/Q5_K min term / 32 (both in the MFMA D layout:
+// slot 4g + v, row n); inv[mt][k]: inverse unit scales of the lane's tokens.
 // A dead unit (past the end of K) contributes exactly zero.
-template <int QT, bool SPLIT>
-__device__ __forceinline__ void compute_v(const Unit<QT> &r, const AReg<QT> &a, const float *inv, int g, bool live,
-                                          f4 &acc, f4 &macc) {
+template <int QT, bool SPLIT, int MT>
+__device__ __forceinline__ void compute_v(const Unit<QT> &r, const AReg<QT> (&a)[MT], const float (&inv)[MT][SPLIT ? 2 : 4],
+                                          int g, bool live, f4 (&acc)[MT], f4 (&macc)[MT]) {
     if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {
         float d = half_bits(r.hdr.x), dmin = half_bits(r.hdr.x >> 16);
         if (!live) { d = 0.f; dmin = 0.f; }
@@ -921,7 +923,9 @@ __device__ __forceinline__ void compute_v(const Unit<QT> &r, const AReg<QT> &a, 
         hs[3] = h2_of_small((sc_hi >> (sh + 8)) & 0xffu);
 #pragma unroll
         for (int i = 0; i < 4; i++) ns[i] = hs[i] * neg1024;
-        f4 c = f4{0.f, 0.f, 0.f, 0.f};
+        f4 c[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) c[mt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int m = 0; m < 8; m++) {
             const int ah = m >> 2, b = (m >> 1) & 1, hw = m & 1;
@@ -935,7 +939,9 @@ __device__ __forceinline__ void compute_v(const Unit<QT> &r, const AReg<QT> &a, 
                 n0 |= ((h0 >> hb) & 0x01010101u) << 4;
                 n1 |= ((h1 >> hb) & 0x01010101u) << 4;
             }
-            c = mfma32(a.f[m], b_frag_scaled(n0, n1, hs[2 * ah + b], ns[2 * ah + b]), c);
+            const h8 bf = b_frag_scaled(n0, n1, hs[2 * ah + b], ns[2 * ah + b]);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) c[mt] = mfma32(a[mt].f[m], bf, c[mt]);
         }
         // min term on the matrix core: B = m_s of this row for s = 4g..4g+3
         // (lane groups 0, 1), zero for lane groups 2, 3
@@ -943,16 +949,21 @@ __device__ __forceinline__ void compute_v(const Unit<QT> &r, const AReg<QT> &a, 
         const h2 p0 = as_h2(pair_lo(mw)) + neg1024, p1 = as_h2(pair_hi(mw)) + neg1024;
         h4 bm;
         bm[0] = p0[0]; bm[1] = p0[1]; bm[2] = p1[0]; bm[3] = p1[1];
-        const f4 cm = mfma16(a.mins, bm, f4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const float iv = inv[acc_token_u<SPLIT>(v)];
-            acc[v] = __builtin_fmaf(d * iv, c[v], acc[v]);
-            macc[v] = __builtin_fmaf(dmin * iv, cm[v], macc[v]);
+        for (int mt = 0; mt < MT; mt++) {
+            const f4 cm = mfma16(a[mt].mins, bm, f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float iv = inv[mt][acc_token_u<SPLIT>(v)];
+                acc[mt][v] = __builtin_fmaf(d * iv, c[mt][v], acc[mt][v]);
+                macc[mt][v] = __builtin_fmaf(dmin * iv, cm[v], macc[mt][v]);
+            }
         }
     } else if constexpr (QT == QT_Q6_K) {
         const float d = live ? half_bits(r.d) : 0.f;
-        f4 sacc = f4{0.f, 0.f, 0.f, 0.f};  // sum over sub-blocks of sc_s * (q . x)_s
+        f4 sacc[MT];  // sum over sub-blocks of sc_s * (q . x)_s, per tile
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) sacc[mt] = f4{0.f, 0.f, 0.f, 0.f};
         const h2 off = as_h2(0xE420E420u);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -970,13 +981,19 @@ __device__ __forceinline__ void compute_v(const Unit<QT> &r, const AReg<QT> &a, 
                 b[0] = p0[0]; b[1] = p0[1]; b[2] = p1[0]; b[3] = p1[1];
                 const uint32_t scw = (sb >> 2) == 0 ? r.sc.x : (sb >> 2) == 1 ? r.sc.y : (sb >> 2) == 2 ? r.sc.z : r.sc.w;
                 const float scf = (float)(int)(int8_t)((scw >> (8 * (sb & 3))) & 0xffu);
-                const f4 c = mfma16(a.f[sb], b, f4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-                for (int v = 0; v < 4; v++) sacc[v] = __builtin_fmaf(scf, c[v], sacc[v]);
+                for (int mt = 0; mt < MT; mt++) {
+                    const f4 c = mfma16(a[mt].f[sb], b, f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                    for (int v = 0; v < 4; v++) sacc[mt][v] = __builtin_fmaf(scf, c[v], sacc[mt][v]);
+                }
             }
         }
 #pragma unroll
-        for (int v = 0; v < 4; v++) acc[v] = __builtin_fmaf(d * inv[acc_token_u<SPLIT>(v)], sacc[v], acc[v]);
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                acc[mt][v] = __builtin_fmaf(d * inv[mt][acc_token_u<SPLIT>(v)], sacc[mt][v], acc[mt][v]);
     } else {
         const h2 off = as_h2(0xE480E480u);
 #pragma unroll
@@ -988,30 +1005,36 @@ __device__ __forceinline__ void compute_v(const Unit<QT> &r, const AReg<QT> &a, 
             h8 b;
             b[0] = p0[0]; b[1] = p0[1]; b[2] = p1[0]; b[3] = p1[1];
             b[4] = p2[0]; b[5] = p2[1]; b[6] = p3[0]; b[7] = p3[1];
-            const f4 c = mfma32(a.f[i], b, f4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-            for (int v = 0; v < 4; v++)
-                acc[v] = __builtin_fmaf(d * inv[acc_token_u<SPLIT>(v)], c[v], acc[v]);
+            for (int mt = 0; mt < MT; mt++) {
+                const f4 c = mfma32(a[mt].f[i], b, f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    acc[mt][v] = __builtin_fmaf(d * inv[mt][acc_token_u<SPLIT>(v)], c[v], acc[mt][v]);
+            }
         }
     }
 }
 
-template <int QT, int NW, int UPS, bool SPLIT, bool PK>
-__global__ __launch_bounds__(NW * 64, 8 / NW)
+// (several token tiles: one wave per SIMD, so a wave may use the whole register file)
+template <int QT, int NW, int UPS, bool SPLIT, bool PK, int MT>
+__global__ __launch_bounds__(NW * 64, MT > 1 ? 1 : 8 / NW)
 void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, int N, int K, int accum,
                    const uint8_t *__restrict__ afrag, const float *__restrict__ invs,
                    const uint8_t *__restrict__ mfrag, const float *__restrict__ ssq, float eps,
                    float *__restrict__ part) {
     using C = GemmCfg<QT>;
-    constexpr int TOK = SPLIT ? 8 : 16;
+    constexpr int TOKT = SPLIT ? 8 : 16;  // tokens per MFMA tile
+    constexpr int TOK = MT * TOKT;
     constexpr int TPL = SPLIT ? 2 : 4;
     constexpr int UNIT_BYTES = (QT == QT_Q8_0) ? 8 * 34 : C::BB;
     constexpr int R = 4;
     static_assert(R % UPS == 0, "ring positions must map to fixed units");
     // partial tiles meet in LDS in batches of F tiles (double-buffered), one
-    // barrier per batch (Q6_K, short of registers: one tile per batch)
-    constexpr int F = (QT == QT_Q6_K) ? 1 : (TPL == 4) ? NW / 2 : NW;
-    __shared__ __align__(16) float red[2][F][NW][64][TPL];
+    // barrier per batch (Q6_K, short of registers, and several token tiles,
+    // short of LDS: one tile per batch)
+    constexpr int F = (QT == QT_Q6_K || MT > 1) ? 1 : (TPL == 4) ? NW / 2 : NW;
+    __shared__ __align__(16) float red[2][F][NW][64][TPL * MT];
     __shared__ float rs[TOK];  // RMSNorm row scales (1 without RMSNorm)
 
     const int n_units = (K + UNIT - 1) / UNIT;
@@ -1025,38 +1048,42 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     const size_t row_bytes = (size_t)(K / C::QK) * C::BB;
     const int tail_blk = (QT == QT_Q8_0 && (K % UNIT)) ? (K % UNIT) / 32 : 8;
 
-    // 1. this wave's A operand (prepared in the MFMA lane layout)
-    AReg<QT> a[UPS];
-    float inv[UPS][TPL];
+    // 1. this wave's A operand for MT token tiles (prepared in the MFMA lane
+    //    layout: entry (chunk c, tile mt) at (c MT + mt) 64 + lane)
+    AReg<QT> a[UPS][MT];
+    float inv[UPS][MT][TPL];
     bool live[UPS];
-    const bool aslot = (SPLIT ? (n_in >> 1) : n_in) < M;
 #pragma unroll
     for (int u = 0; u < UPS; u++) {
         live[u] = unit0 + u < n_units;
         const int un = min(unit0 + u, n_units - 1);
-        const uint8_t *src = afrag + (size_t)un * UNIT_A1;
-        // slots of padding tokens are zero: not fetched
-        if (aslot) {
-            if constexpr (QT == QT_Q6_K) {
+        const uint8_t *src = afrag + (size_t)un * UNIT_A1 * MT;
 #pragma unroll
-                for (int c = 0; c < 16; c++) a[u].f[c] = *(const h4 *)(src + c * 512 + lane * 8);
+        for (int mt = 0; mt < MT; mt++) {
+            // slots of padding tokens are zero: not fetched
+            if ((SPLIT ? (n_in >> 1) : n_in) + mt * TOKT < M) {
+                if constexpr (QT == QT_Q6_K) {
+#pragma unroll
+                    for (int c = 0; c < 16; c++) a[u][mt].f[c] = *(const h4 *)(src + ((c * MT + mt) * 64 + lane) * 8);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 8; c++) a[u][mt].f[c] = *(const h8 *)(src + ((c * MT + mt) * 64 + lane) * 16);
+                }
+                if constexpr (C::MINS)
+                    a[u][mt].mins = *(const h4 *)(mfrag + ((size_t)un * MT + mt) * 512 + lane * 8);
             } else {
+                if constexpr (QT == QT_Q6_K) {
 #pragma unroll
-                for (int c = 0; c < 8; c++) a[u].f[c] = *(const h8 *)(src + c * 1024 + lane * 16);
+                    for (int c = 0; c < 16; c++) a[u][mt].f[c] = h4{};
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 8; c++) a[u][mt].f[c] = h8{};
+                }
+                if constexpr (C::MINS) a[u][mt].mins = h4{};
             }
-            if constexpr (C::MINS) a[u].mins = *(const h4 *)(mfrag + (size_t)un * 512 + lane * 8);
-        } else {
-            if constexpr (QT == QT_Q6_K) {
 #pragma unroll
-                for (int c = 0; c < 16; c++) a[u].f[c] = h4{};
-            } else {
-#pragma unroll
-                for (int c = 0; c < 8; c++) a[u].f[c] = h8{};
-            }
-            if constexpr (C::MINS) a[u].mins = h4{};
+            for (int k = 0; k < TPL; k++) inv[u][mt][k] = invs[(size_t)un * TOK + lane_token<SPLIT>(mt, g, k)];
         }
-#pragma unroll
-        for (int k = 0; k < TPL; k++) inv[u][k] = invs[(size_t)un * TOK + lane_token<SPLIT>(0, g, k)];
     }
 
     // 2. weight stream over items (tile j, unit u), u fastest; past the last
@@ -1095,39 +1122,44 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     }
     __syncthreads();
 
-    f4 acc = f4{0.f, 0.f, 0.f, 0.f}, macc = f4{0.f, 0.f, 0.f, 0.f};
+    f4 acc[MT], macc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) acc[mt] = macc[mt] = f4{0.f, 0.f, 0.f, 0.f};
     auto consume = [&](int j, int u, Unit<QT> &b) {
         if constexpr (!PK) finish_unit<QT>(b);
-        compute_v<QT, SPLIT>(b, a[u], inv[u], g, live[u], acc, macc);
+        compute_v<QT, SPLIT, MT>(b, a[u], inv[u], g, live[u], acc, macc);
         if (u == UPS - 1) {
-            float vals[TPL];
+            float vals[MT * TPL];
 #pragma unroll
-            for (int k = 0; k < TPL; k++) {
-                float v = SPLIT ? acc[2 * k] + acc[2 * k + 1] : acc[k];
-                if constexpr (C::MINS) v -= 32.0f * (SPLIT ? macc[2 * k] + macc[2 * k + 1] : macc[k]);
-                vals[k] = v;
-            }
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int k = 0; k < TPL; k++) {
+                    float v = SPLIT ? acc[mt][2 * k] + acc[mt][2 * k + 1] : acc[mt][k];
+                    if constexpr (C::MINS)
+                        v -= 32.0f * (SPLIT ? macc[mt][2 * k] + macc[mt][2 * k + 1] : macc[mt][k]);
+                    vals[mt * TPL + k] = v;
+                }
             const int jb = j % F, hb = (j / F) & 1;
             float *slot = &red[hb][jb][wave][lane][0];
 #pragma unroll
-            for (int k = 0; k < TPL; k++) slot[k] = vals[k];
-            acc = f4{0.f, 0.f, 0.f, 0.f};
-            macc = f4{0.f, 0.f, 0.f, 0.f};
+            for (int k = 0; k < MT * TPL; k++) slot[k] = vals[k];
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) acc[mt] = macc[mt] = f4{0.f, 0.f, 0.f, 0.f};
             // batch complete: wave i sums tile i of the batch in wave order
             if (jb == F - 1 || j == my_tiles - 1) __syncthreads();
             if ((jb == F - 1 || j == my_tiles - 1) && wave <= jb) {
-                float sum[TPL];
+                float sum[MT * TPL];
 #pragma unroll
-                for (int k = 0; k < TPL; k++) sum[k] = red[hb][wave][0][lane][k];
+                for (int k = 0; k < MT * TPL; k++) sum[k] = red[hb][wave][0][lane][k];
 #pragma unroll
                 for (int w = 1; w < NW; w++)
 #pragma unroll
-                    for (int k = 0; k < TPL; k++) sum[k] += red[hb][wave][w][lane][k];
+                    for (int k = 0; k < MT * TPL; k++) sum[k] += red[hb][wave][w][lane][k];
                 const int r = ((int)blockIdx.x + G * (j - jb + wave)) * 16 + n_in;
                 if (r < N) {
 #pragma unroll
-                    for (int k = 0; k < TPL; k++) {
-                        const int t = lane_token<SPLIT>(0, g, k);
+                    for (int k = 0; k < MT * TPL; k++) {
+                        const int t = lane_token<SPLIT>(k / TPL, g, k % TPL);
                         if (t >= M) continue;
                         const float v = sum[k] * rs[t];
                         if (part != nullptr) {
@@ -1180,12 +1212,12 @@ hipError_t launch_prep(const float *X, const ActIn &in, int M, int K, const ActW
     return hipGetLastError();
 }
 
-template <int QT, int NW, int UPS, bool SPLIT, bool PK>
+template <int QT, int NW, int UPS, bool SPLIT, bool PK, int MT>
 hipError_t launch_v(const uint8_t *W, const float *X, const ActIn &in, float *Y, int M, int N, int K, int S, int G,
                     int accum, const ActWs &a, float *part, hipStream_t st) {
     hipError_t e;
-    if (!in.reuse && (e = launch_prep<QT, 1, SPLIT>(X, in, M, K, a, st)) != hipSuccess) return e;
-    gemm_v_kernel<QT, NW, UPS, SPLIT, PK><<<dim3(G, S), NW * 64, 0, st>>>(
+    if (!in.reuse && (e = launch_prep<QT, MT, SPLIT>(X, in, M, K, a, st)) != hipSuccess) return e;
+    gemm_v_kernel<QT, NW, UPS, SPLIT, PK, MT><<<dim3(G, S), NW * 64, 0, st>>>(
         W, Y, M, N, K, accum, a.afrag, a.inv, a.mfrag, in.op == ACT_RMSNORM ? a.ssq : nullptr, in.eps,
         (S > 1 || in.defer) ? part : nullptr);
     e = hipGetLastError();
@@ -1225,7 +1257,7 @@ hipError_t launch_t(const uint8_t *W, const float *X, const ActIn &in, float *Y,
 struct GemmPlan {
     bool split;      // fp32-accurate two-limb mode
     int MT;          // MFMA token tiles (16 slots each)
-    bool stream;     // one token tile: streaming kernel with register operands
+    bool stream;     // streaming kernel with register operands (else the LDS kernel)
     int NW, UPS;     // streaming kernel: waves per workgroup, units per wave
     int ups;         // LDS kernel: 256-element units per K-slice
     int S;           // K-slices (grid.y)
@@ -1258,8 +1290,20 @@ static GemmPlan plan_gemm(int qt, int M, int N, int K, int flags) {
     static const int use_stream = env_int("IHIP_STREAM", 1);
     static const int env_ups = env_int("IHIP_STREAM_UPS", 0);
     // (the streaming kernel addresses packed weights with 32-bit offsets)
-    p.stream = use_stream && p.MT == 1 && !((flags & 8) && packed_bytes(qt, N, K) >= ((size_t)1 << 31));
-    if (p.stream) {
+    static const int stream_mt = env_int("IHIP_STREAM_MT", 4);
+    p.stream = use_stream && p.MT <= stream_mt && !((flags & 8) && packed_bytes(qt, N, K) >= ((size_t)1 << 31));
+    if (p.stream && p.MT > 1) {
+        // several token tiles: their A operand fills the registers; 4 waves
+        // of one unit each per workgroup, one workgroup (one wave per SIMD)
+        // per CU
+        p.NW = 4;
+        p.UPS = 1;
+        p.S = (n_units + 3) / 4;
+        const int n_tiles = (N + 15) / 16;
+        const int g0 = std::max(1, std::min(n_tiles, 256 / p.S));
+        const int per = (n_tiles + g0 - 1) / g0;
+        p.G = (n_tiles + per - 1) / per;
+    } else if (p.stream) {
         // K per workgroup NW*UPS units; prefer one K-slice (no partials) with
         // the fewest units per wave that still covers K, else the largest
         // chunk that divides K
@@ -1303,7 +1347,7 @@ static GemmPlan plan_gemm(int qt, int M, int N, int K, int flags) {
     p.off_inv = o;
     o += align256((size_t)n_units * TOK * 4);
     p.off_mfrag = o;
-    o += (mins && p.stream) ? align256((size_t)n_units * 512) : 0;
+    o += (mins && p.stream) ? align256((size_t)n_units * 512 * p.MT) : 0;
     p.off_ssq = o;
     o += align256((size_t)n_units * TOK * 4);
     p.off_part = o;
@@ -1333,8 +1377,14 @@ static hipError_t dispatch_mt(const GemmPlan &p, const uint8_t *W, const float *
     const ActWs a{ws, p.stream ? nullptr : (float *)(ws + p.off_xs), (float *)(ws + p.off_inv),
                   p.stream ? ws + p.off_mfrag : nullptr, (float *)(ws + p.off_ssq)};
     float *part = (float *)(ws + p.off_part);
+    if (p.stream && p.MT > 1) {
+#define VM(mt) return p.split ? launch_v<QT, 4, 1, true, PK, mt>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st) \
+                              : launch_v<QT, 4, 1, false, PK, mt>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
+        switch (p.MT) { case 2: VM(2); case 3: VM(3); default: VM(4); }
+#undef VM
+    }
     if (p.stream) {
-#define V(nw, u, sp) return launch_v<QT, nw, u, sp, PK>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
+#define V(nw, u, sp) return launch_v<QT, nw, u, sp, PK, 1>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
 #define VU(nw, sp) switch (p.UPS) { case 1: V(nw, 1, sp); case 2: V(nw, 2, sp); default: V(nw, 4, sp); }
         if (p.NW == 8) {
             if (p.split) { VU(8, true); } else { VU(8, false); }
