@@ -30,13 +30,55 @@ __device__ __forceinline__ void merge_ms(float &m, float &s, float m2, float s2)
     m = M;
 }
 
+// Cross-lane moves on the VALU (DPP) and, across rows, one swizzle or
+// bpermute: partner of lane l at butterfly level o (l ^ o for o = 1, 2, 16,
+// 32; the mirror 7 - l within 8 for o = 4 and 15 - l within 16 for o = 8,
+// which pair the same lanes' results once the lower levels have made every
+// quad (octet) uniform).
+template <int CTRL> __device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int O> __device__ __forceinline__ float partner(float v) {
+    if constexpr (O == 1) return dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+    if constexpr (O == 2) return dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+    if constexpr (O == 4) return dpp_mov<0x141>(v);  // row_half_mirror
+    if constexpr (O == 8) return dpp_mov<0x140>(v);  // row_mirror
+    if constexpr (O == 16)                           // swizzle: xor 16 within 32
+        return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+    return __shfl_xor(v, 32);
+}
+
+// Butterfly merge of one (max, sum) pair per lane (levels 1, 2, 4, 8, 16,
+// 32 as above); the lower lane of each pair merges first, so both partners
+// compute the same merge and every lane ends with the same value.
+template <int O> __device__ __forceinline__ void merge_level(float &m, float &s) {
+    const float m2 = partner<O>(m), s2 = partner<O>(s);
+    const bool upper = (threadIdx.x & O) != 0;
+    if (upper) {
+        merge_ms(m, s, m2, s2);
+    } else {
+        float mm = m2, ss = s2;
+        merge_ms(mm, ss, m, s);
+        m = mm;
+        s = ss;
+    }
+}
+__device__ __forceinline__ float2 wave_merge_pairs(float m, float s) {
+    merge_level<1>(m, s);
+    merge_level<2>(m, s);
+    merge_level<4>(m, s);
+    merge_level<8>(m, s);
+    merge_level<16>(m, s);
+    merge_level<32>(m, s);
+    return make_float2(m, s);
+}
+
 // Block-wide (max, sum) merge of per-thread pairs.
 __device__ void block_merge_ms(float &m, float &s, float *sh) {
     // wave level
-    for (int o = 32; o > 0; o >>= 1) {
-        const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
-        merge_ms(m, s, m2, s2);
-    }
+    const float2 wv = wave_merge_pairs(m, s);
+    m = wv.x;
+    s = wv.y;
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
     if (l == 0) { sh[2 * w] = m; sh[2 * w + 1] = s; }
     __syncthreads();
@@ -90,25 +132,6 @@ __device__ __forceinline__ float2 merge_row(const float2 *part, int nchunk) {
     return make_float2(m, s);
 }
 
-// Butterfly merge of one (max, sum) pair per lane; merge_ms is symmetric,
-// so every lane ends with the same value.
-__device__ __forceinline__ float2 wave_merge_pairs(float m, float s) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
-        // order the pair by lane so both partners compute the same merge
-        if (lane & o) merge_ms(m, s, m2, s2);
-        else {
-            float mm = m2, ss = s2;
-            merge_ms(mm, ss, m, s);
-            m = mm;
-            s = ss;
-        }
-    }
-    return make_float2(m, s);
-}
-
 // Merge of a row's chunk partials by one wave: lane l folds chunks l, l+64,
 // ... in order, then the butterfly.
 __device__ __forceinline__ float2 wave_merge_row(const float2 *part, int nchunk) {
@@ -151,14 +174,21 @@ __device__ __forceinline__ float w_of(const Decision &D, float p, const float *l
     return fmaxf(p - q, 0.f);
 }
 
-// Inclusive scan over the 64 lanes of a wave (fixed association).
+// Inclusive scan over the 64 lanes of a wave (fixed association): a
+// Hillis-Steele scan inside each row of 16 (DPP row shifts by 1, 2, 4, 8;
+// lanes shifted in from outside the row read 0), then row r + 1 adds the
+// total of row r (row broadcast of lane 15 into rows 1 and 3) and rows 2, 3
+// add the total of rows 0, 1 (row broadcast of lane 31).
+template <int CTRL, int ROWS> __device__ __forceinline__ float dpp_row(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, true));
+}
 __device__ __forceinline__ float wave_scan(float v) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const float y = __shfl_up(v, o);
-        if (lane >= o) v += y;
-    }
+    v += dpp_row<0x111, 0xF>(v);  // row_shr:1
+    v += dpp_row<0x112, 0xF>(v);  // row_shr:2
+    v += dpp_row<0x114, 0xF>(v);  // row_shr:4
+    v += dpp_row<0x118, 0xF>(v);  // row_shr:8
+    v += dpp_row<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+    v += dpp_row<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
     return v;
 }
 
@@ -182,8 +212,14 @@ __global__ __launch_bounds__(64) void decide_kernel(const float *__restrict__ tg
     const float2 *Pt = part + (size_t)step * (k + 1) * nchunk;
     const float2 *Pd = part + ((size_t)gridDim.x * (k + 1) + (size_t)step * k) * nchunk;
     const float Tr = mode == 0 ? T : 1.0f;
+    // independent loads first: the first 64 drafts' ids and uniforms, then
+    // (once the ids are in) their two logits, issued before the merges
+    const bool has0 = lane < k;
+    const int x0 = has0 ? dt[lane] : 0;
+    const float ua0 = has0 ? u_acc[(size_t)step * k + lane] : 0.f;
     // rows in batches of 8: all their partials in flight before any merge
     const int nrows = 2 * k + 1;
+    float lx0 = 0.f, dx0 = 0.f;
     for (int r0 = 0; r0 < nrows; r0 += 8) {
         float2 pv[8][2];
 #pragma unroll
@@ -195,6 +231,10 @@ __global__ __launch_bounds__(64) void decide_kernel(const float *__restrict__ tg
                 const int c = lane + 64 * h;
                 pv[b][h] = c < nchunk ? row[c] : make_float2(-__builtin_huge_valf(), 0.f);
             }
+        }
+        if (r0 == 0 && has0 && x0 >= 0 && x0 < V) {
+            lx0 = Lt[(size_t)lane * V + x0];
+            dx0 = Ld[(size_t)lane * V + x0];
         }
 #pragma unroll
         for (int b = 0; b < 8; b++) {
@@ -221,15 +261,16 @@ __global__ __launch_bounds__(64) void decide_kernel(const float *__restrict__ tg
         bool bad = false, inv = false;
         float q = 0.f;
         if (i < k) {
-            const int x = dt[i];
+            const bool pre = base == 0;  // the first 64 were fetched up front
+            const int x = pre ? x0 : dt[i];
             if (x < 0 || x >= V) {
                 bad = inv = true;
             } else {
                 const float2 pt = ms[i], pd = ms[k + 1 + i];
-                const float p = __expf(Lt[(size_t)i * V + x] / Tr - pt.x) / pt.y;
-                q = __expf(Ld[(size_t)i * V + x] / Tr - pd.x) / pd.y;
+                const float p = __expf((pre ? lx0 : Lt[(size_t)i * V + x]) / Tr - pt.x) / pt.y;
+                q = __expf((pre ? dx0 : Ld[(size_t)i * V + x]) / Tr - pd.x) / pd.y;
                 const float ratio = q > 0.f ? fminf(1.0f, p / q) : 1.0f;
-                bad = !(u_acc[(size_t)step * k + i] < ratio);
+                bad = !((pre ? ua0 : u_acc[(size_t)step * k + i]) < ratio);
             }
         }
         const uint64_t m = __ballot(bad);
