@@ -179,6 +179,24 @@ int ihip_silu_mul(const float *gu_dev, int M, int F, float *out_dev, void *strea
  * src/ModelCPU.jl:870-891). */
 int ihip_add(float *y_dev, const float *x_dev, int64_t n, void *stream);
 
+/* The MLP half of a decoder layer (DecoderLayerCPU, src/ModelCPU.jl:884-889,
+ * with mlp_forward, src/ModelCPU.jl:447-473), in place on the residual:
+ *   n = rmsnorm(x, norm_w, eps);  x += W_down (silu(W_gate n) * (W_up n))
+ * x: [M x H] fp32 row-major. w_gate_up: the [gate; up] matrix, 2F rows x H
+ * (the gate rows, then the up rows: concatenate the two GGUF tensors; with
+ * IHIP_GEMM_PACKED pack the concatenation). w_down: [H x F]. flags:
+ * IHIP_GEMM_F32 / IHIP_GEMM_HALF / IHIP_GEMM_PACKED (the precision and layout
+ * of both matmuls). Workspace: ihip_mlp_ws_bytes (holds the [M x 2F] gate/up
+ * product). Two input-stage + matmul launches on the stream; the same result
+ * bit for bit as ihip_gemm_q_ex with IHIP_ACT_RMSNORM into a [M x 2F] buffer
+ * followed by ihip_gemm_q_ex with IHIP_ACT_SILU_MUL and IHIP_GEMM_ACCUM. */
+int ihip_mlp_ws_bytes(int qt_gate_up, int qt_down, int M, int H, int F,
+                      int flags, size_t *bytes);
+int ihip_mlp_forward(int qt_gate_up, const void *w_gate_up, int qt_down,
+                     const void *w_down, float *x, const float *norm_w,
+                     float eps, int M, int H, int F, int flags, void *ws,
+                     size_t ws_bytes, void *stream);
+
 /* ---- LM-head softmax statistics and speculative acceptance ---- */
 
 /* Per row r of logits [rows x V]: zmax[r] = max_j L[r,j]/T and

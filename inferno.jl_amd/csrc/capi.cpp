@@ -302,6 +302,59 @@ int ihip_gemm_q_ex(int qtype, const void *w_dev, const ihip_gemm_input *in, floa
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_gemm_q_ex");
 }
 
+// ---- MLP half of a decoder layer ----
+namespace {
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+int check_mlp(const char *name, int qg, int qd, int M, int H, int F, int flags) {
+    if (flags & ~(IHIP_GEMM_F32 | IHIP_GEMM_HALF | IHIP_GEMM_PACKED))
+        return fail(IHIP_EINVAL, "%s: flags 0x%x (only F32, HALF, PACKED)", name, flags);
+    if (H < 1 || F < 1 || (H & 7) || (F & 7))
+        return fail(IHIP_EINVAL, "%s: H=%d F=%d must be positive multiples of 8", name, H, F);
+    int rc = check_gemm_shape(qg, M, 2 * F, H, flags);
+    if (rc != IHIP_OK) return rc;
+    return check_gemm_shape(qd, M, H, F, flags | IHIP_GEMM_ACCUM);
+}
+
+size_t mlp_ws(int qg, int qd, int M, int H, int F, int flags) {
+    const size_t g = gemm_ws_bytes(qg, M, 2 * F, H, flags);
+    const size_t d = gemm_ws_bytes(qd, M, H, F, flags | IHIP_GEMM_ACCUM);
+    return align256((size_t)M * 2 * F * sizeof(float)) + (g > d ? g : d);
+}
+}  // namespace
+
+int ihip_mlp_ws_bytes(int qt_gate_up, int qt_down, int M, int H, int F, int flags, size_t *bytes) {
+    if (!bytes) return fail(IHIP_EFAULT, "ihip_mlp_ws_bytes: NULL");
+    const int rc = check_mlp("ihip_mlp_ws_bytes", qt_gate_up, qt_down, M, H, F, flags);
+    if (rc != IHIP_OK) return rc;
+    *bytes = mlp_ws(qt_gate_up, qt_down, M, H, F, flags);
+    return ok();
+}
+
+int ihip_mlp_forward(int qt_gate_up, const void *w_gate_up, int qt_down, const void *w_down, float *x,
+                     const float *norm_w, float eps, int M, int H, int F, int flags, void *ws, size_t ws_bytes,
+                     void *stream) {
+    if (!w_gate_up || !w_down || !x) return fail(IHIP_EFAULT, "ihip_mlp_forward: NULL pointer");
+    int rc = check_mlp("ihip_mlp_forward", qt_gate_up, qt_down, M, H, F, flags);
+    if (rc != IHIP_OK) return rc;
+    if (!aligned16(x) || !aligned16(w_gate_up) || !aligned16(w_down) || (norm_w && !aligned16(norm_w)))
+        return fail(IHIP_EINVAL, "ihip_mlp_forward: x, weights and norm_w must be 16-byte aligned");
+    if (!(eps >= 0.f)) return fail(IHIP_EINVAL, "ihip_mlp_forward: eps=%g", eps);
+    const size_t need = mlp_ws(qt_gate_up, qt_down, M, H, F, flags);
+    if (!ws) return fail(IHIP_EFAULT, "ihip_mlp_forward: NULL workspace (%zu bytes needed)", need);
+    if (ws_bytes < need) return fail(IHIP_ENOMEM, "ihip_mlp_forward: workspace %zu < %zu bytes", ws_bytes, need);
+    if (!aligned16(ws)) return fail(IHIP_EINVAL, "ihip_mlp_forward: workspace must be 16-byte aligned");
+    float *gu = (float *)ws;
+    void *gws = (uint8_t *)ws + align256((size_t)M * 2 * F * sizeof(float));
+    // [gate; up] of the normalized residual, then x += down(silu(gate) * up)
+    hipError_t e = launch_gemm_ex(qt_gate_up, w_gate_up, x, H, IHIP_ACT_RMSNORM, norm_w, eps, nullptr, 0, 0, gu, M,
+                                  2 * F, H, flags, gws, S(stream));
+    if (e == hipSuccess)
+        e = launch_gemm_ex(qt_down, w_down, gu, 2 * F, IHIP_ACT_SILU_MUL, nullptr, 0.f, nullptr, 0, 0, x, M, H, F,
+                           flags | IHIP_GEMM_ACCUM, gws, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_mlp_forward");
+}
+
 int ihip_gemm_q_partials(int qtype, int M, int N, int K, int flags, void *ws, float **slices, int *n_slices,
                          int64_t *stride) {
     if (!ws || !slices || !n_slices || !stride) return fail(IHIP_EFAULT, "ihip_gemm_q_partials: NULL pointer");

@@ -9,7 +9,7 @@ from . import formats, synth
 from ._lib import HipError, load
 from .quantized_kernels import (ACT_PLAIN, ACT_RMSNORM, ACT_SILU_MUL, GEMM_ACCUM, GEMM_AUTO, GEMM_F32, GEMM_HALF,
                                 GEMM_DEFER, GEMM_PACKED, GEMM_REUSE, dequant, gemm_partials, gemm_q, gemm_q_ex,
-                                pack_weights, packed_bytes, q4_k_gemv_, q5_k_gemv_, q6_k_gemv_, q8_0_gemv_,
+                                mlp_forward_, mlp_ws_bytes, pack_weights, packed_bytes, q4_k_gemv_, q5_k_gemv_, q6_k_gemv_, q8_0_gemv_,
                                 quant_kernels_available, rmsnorm)
 from .speculative import (MODE_REFERENCE, MODE_STANDARD, SpeculativeStats, greedy_verify,
                           mtp_verify_step, softmax_stats, spec_accept, tree_accept)
@@ -17,7 +17,7 @@ from .speculative import (MODE_REFERENCE, MODE_STANDARD, SpeculativeStats, greed
 __all__ = [
     "formats", "synth", "HipError", "load", "GEMM_ACCUM", "GEMM_AUTO", "GEMM_F32", "GEMM_HALF",
     "GEMM_PACKED", "GEMM_REUSE", "GEMM_DEFER", "gemm_partials", "ACT_PLAIN", "ACT_RMSNORM", "ACT_SILU_MUL", "dequant", "gemm_q", "gemm_q_ex",
-    "pack_weights", "packed_bytes", "q4_k_gemv_", "q5_k_gemv_", "q6_k_gemv_", "q8_0_gemv_",
+    "mlp_forward_", "mlp_ws_bytes", "pack_weights", "packed_bytes", "q4_k_gemv_", "q5_k_gemv_", "q6_k_gemv_", "q8_0_gemv_",
     "quant_kernels_available", "rmsnorm", "MODE_REFERENCE", "MODE_STANDARD", "SpeculativeStats",
     "greedy_verify", "mtp_verify_step", "softmax_stats", "spec_accept", "tree_accept",
 ]

@@ -137,6 +137,31 @@ def gemm_q_ex(qtype: int, w_dev, x, n: int, k: int, act: int = ACT_PLAIN, norm_w
     return out
 
 
+def mlp_ws_bytes(qt_gate_up: int, qt_down: int, m: int, h: int, f: int, flags: int = GEMM_AUTO) -> int:
+    """Workspace bytes of mlp_forward_."""
+    nb = C.c_size_t()
+    _lib.check(_lib.load().ihip_mlp_ws_bytes(qt_gate_up, qt_down, m, h, f, flags, C.byref(nb)))
+    return int(nb.value)
+
+
+def mlp_forward_(qt_gate_up: int, w_gate_up, qt_down: int, w_down, x, h: int, f: int, norm_w=None,
+                 eps: float = 1e-6, flags: int = GEMM_AUTO, ws=None, stream=None):
+    """The MLP half of a decoder layer in place on the residual x [M, H]
+    (src/ModelCPU.jl:884-889 with mlp_forward, :447-473): x += W_down
+    (silu(W_gate n) * (W_up n)), n = rmsnorm(x, norm_w, eps). w_gate_up is
+    the [gate; up] matrix (2f rows x h). Returns x."""
+    import torch
+    if x.dim() != 2 or x.dtype != torch.float32 or not x.is_contiguous() or x.shape[1] != h:
+        raise ValueError("x must be a contiguous float32 [M, h] tensor")
+    m = x.shape[0]
+    if ws is None:
+        ws = torch.empty(mlp_ws_bytes(qt_gate_up, qt_down, m, h, f, flags), dtype=torch.uint8, device=x.device)
+    _lib.check(_lib.load().ihip_mlp_forward(qt_gate_up, _ptr(w_gate_up), qt_down, _ptr(w_down), _ptr(x),
+                                            None if norm_w is None else _ptr(norm_w), eps, m, h, f, flags,
+                                            _ptr(ws), ws.numel(), _stream(stream)))
+    return x
+
+
 def gemm_partials(qtype: int, m: int, n: int, k: int, flags: int, ws):
     """(pointer, n_slices, slice_stride) of the partials a GEMM_DEFER call
     left in ws."""

@@ -92,3 +92,18 @@ def test_env_kill_switch():
     env = dict(os.environ, INFERNO_NO_QUANT_KERNELS="1")
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=120)
     assert r.stdout.strip() == "0"
+
+
+def test_mlp_forward_argument_checks(lib):
+    """ihip_mlp_forward validates before touching the GPU."""
+    nb = C.c_size_t()
+    assert lib.ihip_mlp_ws_bytes(12, 14, 5, 512, 1024, 1, None) == -14
+    assert lib.ihip_mlp_ws_bytes(12, 14, 5, 512, 1024, 4, C.byref(nb)) == -22  # ACCUM is implied, not a flag
+    assert lib.ihip_mlp_ws_bytes(12, 14, 5, 500, 1024, 1, C.byref(nb)) == -22  # H not a multiple of 256
+    assert lib.ihip_mlp_ws_bytes(12, 14, 5, 512, 1024, 9, C.byref(nb)) == 0 and nb.value >= 5 * 2048 * 4
+    buf = (C.c_uint8 * 64)()
+    p16 = (C.addressof(buf) + 15) & ~15
+    assert lib.ihip_mlp_forward(12, None, 14, p16, p16, None, 1e-6, 5, 512, 1024, 1, p16, 64, None) == -14
+    assert lib.ihip_mlp_forward(12, p16, 14, p16, p16, None, -1.0, 5, 512, 1024, 1, p16, 64, None) == -22
+    assert lib.ihip_mlp_forward(12, p16, 14, p16, p16, None, 1e-6, 5, 512, 1024, 1, p16, 64, None) == -12
+    assert b"workspace" in lib.ihip_last_error()

@@ -138,3 +138,38 @@ def test_defer_and_fold_residual(ih, qt2):
         assert torch.equal(yf, yr), M
         ref = O.gemv_f64(F.Q6_K, w1, h.cpu().numpy(), M, H, K1) + x0.cpu().numpy()
         assert rel_l2(xf.cpu().numpy(), ref) < 1e-5
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_mlp_forward(ih, packed):
+    """ihip_mlp_forward (the MLP half of a decoder layer, src/ModelCPU.jl:884-889
+    with mlp_forward, :447-473) equals the two ihip_gemm_q_ex calls it stands
+    for bit for bit, and the oracle's rmsnorm -> [gate; up] -> SiLU gating ->
+    down -> residual add in float64 to 1e-5."""
+    import torch
+    H, FF = 512, 1024
+    rng = np.random.default_rng(50 + packed)
+    wgu = synth.matrix(F.Q4_K, 2 * FF, H, synth.stream_for(7, "mlp_gu"))
+    wd = synth.matrix(F.Q6_K, H, FF, synth.stream_for(8, "mlp_down"))
+    gu_d, d_d = _dev(wgu), _dev(wd)
+    fl = ih.GEMM_F32
+    if packed:
+        gu_d, d_d = ih.pack_weights(F.Q4_K, gu_d, 2 * FF, H), ih.pack_weights(F.Q6_K, d_d, H, FF)
+        fl |= ih.GEMM_PACKED
+    nw = (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    nw_d = _dev(nw)
+    for M in (1, 5, 8, 20):
+        x0 = (2.0 * rng.standard_normal((M, H))).astype(np.float32)
+        x1 = _dev(x0)
+        ih.mlp_forward_(F.Q4_K, gu_d, F.Q6_K, d_d, x1, H, FF, norm_w=nw_d, flags=fl)
+        gu = ih.gemm_q_ex(F.Q4_K, gu_d, _dev(x0), 2 * FF, H, act=ih.ACT_RMSNORM, norm_w=nw_d, flags=fl)
+        x2 = _dev(x0)
+        ih.gemm_q_ex(F.Q6_K, d_d, gu, H, FF, act=ih.ACT_SILU_MUL, flags=fl | ih.GEMM_ACCUM, out=x2)
+        assert torch.equal(x1, x2), M
+        n = _rms_rows(x0, nw, 1e-6)
+        gup = O.gemv_f64(F.Q4_K, wgu, n, M, 2 * FF, H)
+        g, u = gup[:, :FF], gup[:, FF:]
+        with np.errstate(over="ignore"):  # exp(-g) = inf for very negative g: silu -> 0
+            h = (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
+        delta = O.gemv_f64(F.Q6_K, wd, h, M, H, FF)
+        assert rel_l2(x1.cpu().numpy() - x0, delta) < 1e-5, M
