@@ -562,6 +562,47 @@ def cpu_baseline(ih, model: Model, n_layers: int, M: int, k: int, budget_s: floa
     }
 
 
+def sampler_config(ih):
+    """The draft-side sampler (ihip_sample: softmax_sample, src/ModelCPU.jl:
+    1123-1200; ihip_apply_penalties: :1202-1225) at the LM head's vocabulary
+    V = 151936: microseconds per call for 1 and 64 rows (seeded Gaussian
+    logits, sd 3), each call replayed in a HIP graph; beside it the oracle's
+    numpy restatement of one row on the host (argsorts for top-k/top-p)."""
+    import torch
+    import numpy as np
+    V = 151936
+    settings = {"plain": dict(temperature=1.0), "top_k=40": dict(temperature=0.8, top_k=40),
+                "top_k=50,top_p=0.95": dict(temperature=0.7, top_k=50, top_p=0.95),
+                "top_p=0.9": dict(temperature=0.8, top_p=0.9), "min_p=0.05": dict(temperature=1.0, min_p=0.05),
+                "greedy": dict(temperature=0.0)}
+    g = torch.Generator(device="cuda").manual_seed(SEED)
+    out = {"V": V, "us_per_call": {}}
+    for rows in (1, 64):
+        L = 3.0 * torch.randn(rows, V, device="cuda", generator=g)
+        u = torch.rand(rows, device="cuda", generator=g)
+        tok = torch.empty(rows, dtype=torch.int32, device="cuda")
+        for name, kw in settings.items():
+            t = graph_time(lambda: [ih.softmax_sample(L, u, out=tok, **kw) for _ in range(10)]) / 10
+            out["us_per_call"][f"rows={rows},{name}"] = round(t * 1e6, 1)
+        ids = torch.arange(0, 4096, 7, dtype=torch.int32, device="cuda")
+        t = graph_time(lambda: [ih.apply_penalties_(L, ids, presence=0.1, repetition=1.1) for _ in range(10)]) / 10
+        out["us_per_call"][f"rows={rows},penalties(586 ids)"] = round(t * 1e6, 1)
+    # host: the oracle's numpy restatement, one row per setting
+    try:
+        sys.path.insert(0, ROOT)
+        from oracle import oracle as O
+        row = (3.0 * np.random.default_rng(SEED).standard_normal(V)).astype(np.float32)
+        cpu = {}
+        for name, kw in settings.items():
+            t0 = time.perf_counter()
+            O.softmax_sample(row, 0.5, **kw)
+            cpu[name] = round((time.perf_counter() - t0) * 1e3, 2)
+        out["cpu_port_ms_per_row"] = cpu
+    except Exception as e:  # (the oracle is test infrastructure; absent means no baseline)
+        out["cpu_port_ms_per_row"] = f"unavailable: {e}"
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -575,8 +616,8 @@ def main():
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only run the roofline kernel and the traffic calibration kernel (for rocprofv3 --pmc)")
     ap.add_argument("--configs", type=str, default="",
-                    help="instead of the bench line: measure BASELINE configs (comma list of 1,2,3,5), one JSON "
-                         "object per config")
+                    help="instead of the bench line: measure BASELINE configs (comma list of 1,2,3,5, and 'sampler' "
+                         "for the draft-side sampler), one JSON object per config")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -594,9 +635,11 @@ def main():
         for c in want:
             if c == "5":
                 res = config5(ih, Model(ih, args.layers, keep_gguf=0))
+            elif c == "sampler":
+                res = sampler_config(ih)
             else:
                 res = {"1": config1, "2": config2, "3": config3}[c](ih)
-            print(json.dumps({"config": int(c), **res}), flush=True)
+            print(json.dumps({"config": c if c == "sampler" else int(c), **res}), flush=True)
             torch.cuda.empty_cache()
         return
     model = Model(ih, args.layers, keep_gguf=0 if (args.no_cpu or args.profile_kernels) else 4)

@@ -250,6 +250,36 @@ int ihip_tree_accept(const float *tgt_dev, const float *drf_dev,
                      int32_t *out_len_dev, void *ws, size_t ws_bytes,
                      void *stream);
 
+/* ---- draft-side sampler (csrc/sample.hip) ---- */
+
+/* softmax_sample (src/ModelCPU.jl:1123-1200) on each row of logits
+ * [rows x V], one token per row (0-based) into out_tok_dev:
+ *   T = 0: first-index argmax. Otherwise z = L / T; top_k > 0 keeps the
+ *   top_k largest z (ties lowest index first; top_k >= V keeps all);
+ *   softmax; top_p < 1 keeps the shortest prefix of the probabilities in
+ *   descending order (ties by index) whose sum reaches top_p, renormalized;
+ *   min_p > 0 drops probabilities below max * min_p, renormalized; the token
+ *   is the first j with u[r] <= cumsum_j (V - 1 if none; 0 when u[r] <= 0,
+ *   as the reference's loop returns its first index then).
+ * Limits: top_k <= 4096 unless >= V; V a multiple of 4 and <= 4194304;
+ * logits 16-byte aligned. No workspace. Sums are trees where the reference
+ * adds sequentially, so a draw can differ only where u lies within rounding
+ * of a step of the cumulative distribution. */
+int ihip_sample(const float *logits_dev, int rows, int V, float T, int top_k,
+                float top_p, float min_p, const float *u_dev,
+                int32_t *out_tok_dev, void *stream);
+
+/* The penalties the generation loop applies before sampling
+ * (apply_presence_penalty!, apply_repetition_penalty!,
+ * src/ModelCPU.jl:1202-1225), in place on logits [rows x V]: row r's token
+ * ids are tok_dev[r * tok_stride + i], i < n_tok (tok_stride 0: one list for
+ * every row); for each distinct id in [0, V): x -= presence (presence != 0),
+ * then x = x > 0 ? x / repetition : x * repetition (repetition != 1).
+ * V <= 262144. */
+int ihip_apply_penalties(float *logits_dev, int rows, int V,
+                         const int32_t *tok_dev, int n_tok, int64_t tok_stride,
+                         float presence, float repetition, void *stream);
+
 /* ---- synthetic inputs (benchmark and tests; csrc/misc.hip) ---- */
 
 /* n_blocks seeded GGUF blocks of qtype starting at block first_block of

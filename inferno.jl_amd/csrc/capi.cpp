@@ -42,6 +42,13 @@ hipError_t launch_rmsnorm(const float *x, const float *w, float *out, int rows, 
 hipError_t launch_silu_mul(const float *gu, int M, int F, float *out, hipStream_t st);
 hipError_t launch_add(float *y, const float *x, int64_t n, hipStream_t st);
 hipError_t launch_synth(int qt, uint64_t stream, int64_t first, int64_t nblk, void *out, hipStream_t st);
+int sample_max_top_k();
+int sample_max_v();
+int penalty_max_v();
+hipError_t launch_sample(const float *L, int rows, int V, float T, int top_k, float top_p, float min_p, const float *u,
+                         int32_t *out, hipStream_t st);
+hipError_t launch_penalties(float *L, int rows, int V, const int32_t *tok, int n_tok, int64_t tok_stride,
+                            float presence, float repetition, hipStream_t st);
 hipError_t launch_gaussian(uint64_t stream, int64_t n, float scale, const float *add, float *out, hipStream_t st);
 
 namespace {
@@ -498,6 +505,34 @@ int ihip_tree_accept(const float *tgt_dev, const float *drf_dev, const int32_t *
     hipError_t e = launch_tree(tgt_dev, drf_dev, tok_dev, parent_dev, n, V, T, u_dev, part, out_path_dev,
                                out_len_dev, wsi, S(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_tree_accept");
+}
+
+int ihip_sample(const float *logits_dev, int rows, int V, float T, int top_k, float top_p, float min_p,
+                const float *u_dev, int32_t *out_tok_dev, void *stream) {
+    if (!logits_dev || !u_dev || !out_tok_dev) return fail(IHIP_EFAULT, "ihip_sample: NULL pointer");
+    if (rows < 1 || V < 4 || (V & 3) || V > sample_max_v())
+        return fail(IHIP_EINVAL, "ihip_sample: rows=%d V=%d (V a multiple of 4 in [4, %d])", rows, V, sample_max_v());
+    if (!aligned16(logits_dev)) return fail(IHIP_EINVAL, "ihip_sample: logits must be 16-byte aligned");
+    if (!(T >= 0.f) || T > 3.0e38f) return fail(IHIP_EINVAL, "ihip_sample: temperature %g", T);
+    if (top_k < 0) return fail(IHIP_EINVAL, "ihip_sample: top_k=%d", top_k);
+    if (top_k >= V) top_k = 0;  // keeps every token (sorted_indices[1:min(top_k, V)])
+    if (top_k > sample_max_top_k())
+        return fail(IHIP_EINVAL, "ihip_sample: top_k=%d above %d (and below V)", top_k, sample_max_top_k());
+    if (top_p != top_p || min_p != min_p) return fail(IHIP_EINVAL, "ihip_sample: NaN top_p/min_p");
+    hipError_t e = launch_sample(logits_dev, rows, V, T, top_k, top_p, min_p, u_dev, out_tok_dev, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_sample");
+}
+
+int ihip_apply_penalties(float *logits_dev, int rows, int V, const int32_t *tok_dev, int n_tok, int64_t tok_stride,
+                         float presence, float repetition, void *stream) {
+    if (!logits_dev || (n_tok > 0 && !tok_dev)) return fail(IHIP_EFAULT, "ihip_apply_penalties: NULL pointer");
+    if (rows < 1 || V < 1 || V > penalty_max_v() || n_tok < 0 || (tok_stride != 0 && tok_stride < n_tok))
+        return fail(IHIP_EINVAL, "ihip_apply_penalties: rows=%d V=%d (<= %d) n_tok=%d stride=%lld", rows, V,
+                    penalty_max_v(), n_tok, (long long)tok_stride);
+    if (presence != presence || repetition != repetition)
+        return fail(IHIP_EINVAL, "ihip_apply_penalties: NaN penalty");
+    hipError_t e = launch_penalties(logits_dev, rows, V, tok_dev, n_tok, tok_stride, presence, repetition, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_apply_penalties");
 }
 
 int ihip_synth_blocks(int qtype, uint64_t stream, int64_t first_block, int64_t n_blocks, void *out_dev,

@@ -1,0 +1,773 @@
+// Draft-side sampler on gfx950: softmax_sample (src/ModelCPU.jl:1123-1200)
+// with temperature, top-k, top-p and min-p, and the presence / repetition
+// penalties the generation loop applies to the logits first
+// (apply_presence_penalty!, apply_repetition_penalty!,
+// src/ModelCPU.jl:1202-1225).
+//
+// One workgroup of 1024 threads per row. Every pass over a row reads it in
+// rounds of 4096 logits (one float4 per thread, coalesced), so after the
+// first pass the row (600 KB at V = 151936) is served from L2.
+//
+//  * T = 0: first-index argmax.
+//  * top-k (1 <= k <= 4096, k < V): exact radix select of the k-th largest
+//    z = L / T (8 bits a pass on an order-preserving key), ties at the
+//    threshold kept lowest index first (the stable descending sortperm);
+//    the k candidates are compacted into LDS in index order, and softmax,
+//    top-p (a bitonic sort by probability, then a scan), min-p and the draw
+//    run there.
+//  * no top-k: softmax statistics by full passes; top-p finds the nucleus by
+//    a radix select over the same keys whose buckets carry the probability
+//    mass in 2^-40 fixed point (integer LDS atomics: deterministic); min-p
+//    is a threshold; the draw sums each round, picks the round, then scans it.
+// Sums and scans are trees, where the reference accumulates sequentially:
+// the drawn token can differ only where u falls within rounding of a CDF
+// step.
+#include "common.h"
+
+#include <climits>
+
+namespace {
+
+constexpr int SNT = 1024;
+constexpr int SNW = SNT / 64;
+constexpr int SROUND = 4 * SNT;
+constexpr int SK_MAX = 4096;
+constexpr int SMAX_ROUNDS = 1024;  // V <= 4194304
+
+struct SampleArgs {
+    float T;       // 0: argmax
+    int top_k;     // 0: off (the host maps k >= V to 0)
+    float top_p;   // >= 1: off
+    float min_p;   // <= 0: off
+};
+
+// Order-preserving 32-bit key of a float (larger float, larger key).
+__device__ __forceinline__ uint32_t okey(float z) {
+    const uint32_t b = __float_as_uint(z);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float okey_inv(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// ---- block primitives (16 waves), fixed reduction trees
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ float block_sum(float v, float *red) {
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    v = wave_sum(v);
+    __syncthreads();  // (red may still be read by the previous call)
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    return wave_sum(l < SNW ? red[l] : 0.f);
+}
+__device__ float block_max(float v, float *red) {
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    v = wave_max(v);
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    return wave_max(l < SNW ? red[l] : -__builtin_huge_valf());
+}
+__device__ int block_min_i(int v, int *red) {
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    v = wave_min_i(v);
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    return wave_min_i(l < SNW ? red[l] : INT_MAX);
+}
+// exclusive scan over the block in thread order; *total = block sum
+__device__ uint32_t block_excl_scan_u(uint32_t v, uint32_t *red, uint32_t &total) {
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    uint32_t inc = v;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(inc, o);
+        if (l >= o) inc += y;
+    }
+    __syncthreads();
+    if (l == 63) red[w] = inc;
+    __syncthreads();
+    uint32_t base = 0, tot = 0;
+    for (int i = 0; i < SNW; i++) {
+        const uint32_t x = red[i];
+        base += i < w ? x : 0u;
+        tot += x;
+    }
+    total = tot;
+    return base + inc - v;
+}
+__device__ float block_excl_scan_f(float v, float *red, float &total) {
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    float inc = v;
+    for (int o = 1; o < 64; o <<= 1) {
+        const float y = __shfl_up(inc, o);
+        if (l >= o) inc += y;
+    }
+    __syncthreads();
+    if (l == 63) red[w] = inc;
+    __syncthreads();
+    float base = 0.f, tot = 0.f;
+    for (int i = 0; i < SNW; i++) {
+        const float x = red[i];
+        if (i < w) base += x;
+        tot += x;
+    }
+    total = tot;
+    return base + (inc - v);
+}
+
+// Round r of a row: this thread's 4 logits z = L * (1 / T) (within an ulp
+// of the reference's L / T, the same order and the same ties), in false past
+// V (the host keeps V a multiple of 4 and rows 16-byte aligned).
+__device__ __forceinline__ void load_round(const float *__restrict__ row, int V, int r, float invT, float (&z)[4],
+                                           bool &in) {
+    const int base = r * SROUND + 4 * (int)threadIdx.x;
+    in = base < V;
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (in) x = *(const float4 *)(row + base);
+    z[0] = x.x; z[1] = x.y; z[2] = x.z; z[3] = x.w;
+    if (invT != 1.0f) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) z[e] = z[e] * invT;
+    }
+}
+
+// A pass over the row: the loads of RB rounds are in flight together, then
+// f(z, in, r) runs for each round in order (uniformly, so f may hold
+// barriers).
+constexpr int RB = 8;
+template <class F>
+__device__ __forceinline__ void for_rounds(const float *__restrict__ row, int V, int nround, float T, F &&f) {
+    for (int r0 = 0; r0 < nround; r0 += RB) {
+        float z[RB][4];
+        bool in[RB];
+#pragma unroll
+        for (int b = 0; b < RB; b++) load_round(row, V, r0 + b, T, z[b], in[b]);
+#pragma unroll
+        for (int b = 0; b < RB; b++)
+            if (r0 + b < nround) f(z[b], in[b], r0 + b);
+    }
+}
+
+// exp for the probabilities (the hardware exp2 after a multiply by log2 e:
+// ~1e-6 relative, the same value in every pass)
+__device__ __forceinline__ float pexp(float x) { return __expf(x); }
+
+// (m, s) = (max, sum exp(z - max)) merged; symmetric, so both partners of a
+// butterfly get the same bits
+__device__ __forceinline__ void merge_ms2(float &m, float &s, float m2, float s2) {
+    const float mm = fmaxf(m, m2);
+    if (mm == -__builtin_huge_valf()) return;
+    s = s * pexp(m - mm) + s2 * pexp(m2 - mm);
+    m = mm;
+}
+__device__ void block_ms(float &m, float &s, float *red) {
+    for (int o = 32; o > 0; o >>= 1) {
+        const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
+        merge_ms2(m, s, m2, s2);
+    }
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    __syncthreads();
+    if (l == 0) {
+        red[w] = m;
+        red[SNW + w] = s;
+    }
+    __syncthreads();
+    m = l < SNW ? red[l] : -__builtin_huge_valf();
+    s = l < SNW ? red[SNW + l] : 0.f;
+    for (int o = 32; o > 0; o >>= 1) {
+        const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
+        merge_ms2(m, s, m2, s2);
+    }
+}
+
+// First j in [0, n) of this thread's 4 values (slot 4t + e) with u <= the
+// inclusive prefix; the block's scan total goes to *total.
+__device__ int first_cdf_hit(const float (&v)[4], int n_here, float before, float u, float *redf, float &total) {
+    float c[4], run = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        run += v[e];
+        c[e] = run;
+    }
+    const float ex = block_excl_scan_f(run, redf, total);
+    int hit = INT_MAX;
+#pragma unroll
+    for (int e = 3; e >= 0; e--)
+        if (e < n_here && u <= before + (ex + c[e])) hit = 4 * (int)threadIdx.x + e;
+    return hit;
+}
+
+// Threshold selection counted from the top (the k-th largest z, or the z
+// where the probability mass from the top reaches top_p). Pass A buckets
+// w = zmax - z linearly, 8 buckets per unit of log-probability (bucket 255:
+// the tail), which spreads real logits over many buckets; then 4 passes of
+// 8 key bits each refine inside the chosen bucket, over its few elements.
+// With MASS the buckets also carry each element's probability in 2^-40
+// fixed point (integer atomics: the same sums in any order).
+__device__ __forceinline__ uint32_t zbin(float z, float zmax) {
+    const float w = (zmax - z) * 8.0f;
+    return w < 255.0f ? (uint32_t)w : 255u;  // (-Inf and NaN: the tail)
+}
+
+struct Select {
+    uint32_t zb;             // the bucket of pass A
+    uint32_t tau;            // key of the threshold element inside it
+    unsigned long long rem;  // units still to reach among the elements equal to tau
+    uint32_t cnt;            // elements equal to tau
+    bool all;                // (MASS) the total ran short of the target: keep every element
+};
+
+// Wave 0 finds, over the 256 buckets (descending or ascending index), the
+// one holding the rem-th unit (~0ull in *selm when the total is short).
+template <bool MASS>
+__device__ void pick_bucket(const uint32_t *hist, const unsigned long long *mass, unsigned long long rem,
+                            uint32_t *sel, unsigned long long *selm, bool descending) {
+    const int t = threadIdx.x;
+    if (t >= 64) return;
+    unsigned long long c[4], sum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int b = descending ? 255 - 4 * t - j : 4 * t + j;
+        c[j] = MASS ? mass[b] : (unsigned long long)hist[b];
+        sum += c[j];
+    }
+    unsigned long long inc = sum;
+    for (int o = 1; o < 64; o <<= 1) {
+        const unsigned long long y = __shfl_up(inc, o);
+        if (t >= o) inc += y;
+    }
+    const unsigned long long before = inc - sum;
+    const bool found = before < rem && rem <= inc;
+    if (found) {
+        unsigned long long cum = before;
+        for (int j = 0; j < 4; j++) {
+            if (cum + c[j] >= rem) {
+                sel[0] = descending ? 255u - 4u * t - j : 4u * t + j;
+                selm[0] = cum;
+                break;
+            }
+            cum += c[j];
+        }
+    }
+    if (__ballot(found) == 0ull && t == 0) {
+        sel[0] = 0u;
+        selm[0] = ~0ull;
+    }
+}
+
+template <bool MASS>
+__device__ void select_threshold(const float *__restrict__ row, int V, int nround, float T, float zmax, float S,
+                                 unsigned long long target, uint32_t *hist, unsigned long long *mass, uint32_t *sel,
+                                 unsigned long long *selm, Select &R) {
+    const int t = threadIdx.x;
+    R.zb = 255u;
+    R.tau = 0u;
+    R.rem = target;
+    R.cnt = 0;
+    R.all = false;
+    const float invS = 1.0f / S;
+    auto mass_of = [&](float z) {
+        return (unsigned long long)(pexp(z - zmax) * invS * 1099511627776.0f);
+    };
+    // pass A: buckets of w = zmax - z, largest z first = bucket 0 first
+    if (t < 256) {
+        hist[t] = 0;
+        if (MASS) mass[t] = 0;
+    }
+    __syncthreads();
+    for_rounds(row, V, nround, T, [&](const float (&z)[4], bool in, int) {
+        if (!in) return;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint32_t b = zbin(z[e], zmax);
+            atomicAdd(&hist[b], 1u);
+            if (MASS) atomicAdd(&mass[b], mass_of(z[e]));
+        }
+    });
+    __syncthreads();
+    pick_bucket<MASS>(hist, mass, R.rem, sel, selm, false);
+    __syncthreads();
+    const uint32_t zb = sel[0];
+    const unsigned long long aboveA = selm[0];
+    __syncthreads();
+    if (aboveA == ~0ull) {
+        R.all = true;
+        return;
+    }
+    R.rem -= aboveA;
+    R.zb = zb;
+    // passes B: the exact key inside bucket zb, 8 bits a pass from the top
+    uint32_t prefix = 0, pmask = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        if (t < 256) {
+            hist[t] = 0;
+            if (MASS) mass[t] = 0;
+        }
+        __syncthreads();
+        for_rounds(row, V, nround, T, [&](const float (&z)[4], bool in, int) {
+            if (!in) return;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t k = okey(z[e]);
+                if ((k & pmask) != prefix || zbin(z[e], zmax) != zb) continue;
+                const uint32_t b = (k >> shift) & 255u;
+                atomicAdd(&hist[b], 1u);
+                if (MASS) atomicAdd(&mass[b], mass_of(z[e]));
+            }
+        });
+        __syncthreads();
+        pick_bucket<MASS>(hist, mass, R.rem, sel, selm, true);
+        __syncthreads();
+        const uint32_t b = sel[0];
+        const unsigned long long above = selm[0];
+        const uint32_t cb = hist[b];
+        __syncthreads();
+        if (above == ~0ull) {  // (MASS: truncated masses just short of the target)
+            R.all = true;
+            return;
+        }
+        R.rem -= above;
+        prefix |= b << shift;
+        pmask |= 255u << shift;
+        R.cnt = cb;
+    }
+    R.tau = prefix;
+}
+
+// Kept by a threshold: a larger z than the bucket (smaller bucket index), or
+// inside it a larger key, or an equal key before index tie_lim.
+__device__ __forceinline__ bool above_threshold(float z, int j, float zmax, uint32_t zb, uint32_t tau, int tie_lim) {
+    const uint32_t b = zbin(z, zmax);
+    if (b != zb) return b < zb;
+    const uint32_t k = okey(z);
+    return k > tau || (k == tau && j < tie_lim);
+}
+
+__global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restrict__ L, int V, SampleArgs a,
+                                                           const float *__restrict__ u, int32_t *__restrict__ out) {
+    __shared__ float s_redf[2 * SNW];
+    __shared__ float s_redv[SNW][RB];
+    __shared__ uint32_t s_redu[SNW];
+    __shared__ int s_redi[SNW];
+    __shared__ uint32_t s_hist[256];
+    __shared__ unsigned long long s_mass[256];
+    __shared__ uint32_t s_sel[2];
+    __shared__ unsigned long long s_selm[2];
+    __shared__ float s_round[SMAX_ROUNDS];
+    __shared__ float s_before;
+    __shared__ int s_cidx[SK_MAX];
+    __shared__ float s_cp[SK_MAX];
+    __shared__ int s_sort[SK_MAX];
+    const int row = blockIdx.x, t = threadIdx.x;
+    const float *Lr = L + (size_t)row * V;
+    const int nround = (V + SROUND - 1) / SROUND;
+    const float ur = u[row];
+    const float invT = a.T > 0.f ? 1.0f / a.T : 1.0f;
+
+    if (a.T == 0.0f) {
+        // first-index argmax (Julia argmax)
+        float bv = 0.f;
+        int bi = INT_MAX;
+        for_rounds(Lr, V, nround, 1.0f, [&](const float (&z)[4], bool in, int r) {
+            if (!in) return;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (bi == INT_MAX || z[e] > bv) {
+                    bv = z[e];
+                    bi = r * SROUND + 4 * t + e;
+                }
+        });
+        const float m = block_max(bi == INT_MAX ? -__builtin_huge_valf() : bv, s_redf);
+        const int first = block_min_i((bi != INT_MAX && bv == m) ? bi : INT_MAX, s_redi);
+        if (t == 0) out[row] = first == INT_MAX ? 0 : first;
+        return;
+    }
+    // the reference's draw returns index 1 (here 0) when r <= 0: cumsum >= 0
+    if (!(ur > 0.f)) {
+        if (t == 0) out[row] = 0;
+        return;
+    }
+
+    const int K = a.top_k;
+    if (K > 0) {
+        // ---- top-k: the k-th largest z, then the k candidates in index order
+        float lmax = -__builtin_huge_valf();
+        for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int) {
+            if (in)
+#pragma unroll
+                for (int e = 0; e < 4; e++) lmax = fmaxf(lmax, z[e]);
+        });
+        const float zm = block_max(lmax, s_redf);
+        Select R;
+        select_threshold<false>(Lr, V, nround, invT, zm, 1.f, (unsigned long long)K, s_hist, s_mass, s_sel, s_selm, R);
+        const uint32_t zb = R.zb, tau = R.tau;
+        const int rem = (int)R.rem;  // elements equal to tau that are kept, lowest index first
+        int run_kept = 0, run_eq = 0;
+        for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int r) {
+            bool g[4], q[4];
+            uint32_t ng = 0, nq = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t b = zbin(z[e], zm);
+                const uint32_t k = okey(z[e]);
+                g[e] = in && (b < zb || (b == zb && k > tau));
+                q[e] = in && b == zb && k == tau;
+                ng += g[e];
+                nq += q[e];
+            }
+            uint32_t tot;
+            const uint32_t ex = block_excl_scan_u(ng | (nq << 16), s_redu, tot);
+            const int eq_before = (int)(ex >> 16);
+            int pos = run_kept + (int)(ex & 0xffffu) + min(max(rem - run_eq, 0), eq_before);
+            int er = run_eq + eq_before;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if (g[e] || (q[e] && er < rem)) {
+                    if (pos < SK_MAX) {
+                        s_cidx[pos] = r * SROUND + 4 * t + e;
+                        s_cp[pos] = z[e];
+                    }
+                    pos++;
+                }
+                if (q[e]) er++;
+            }
+            run_kept += (int)(tot & 0xffffu) + min(max(rem - run_eq, 0), (int)(tot >> 16));
+            run_eq += (int)(tot >> 16);
+        });
+        __syncthreads();
+        const int n = min(run_kept, SK_MAX);  // == K
+        // softmax over the candidates (the rest are exp(-Inf) = 0)
+        float lm = -__builtin_huge_valf();
+        for (int i = t; i < n; i += SNT) lm = fmaxf(lm, s_cp[i]);
+        const float zmax = block_max(lm, s_redf);
+        float ls = 0.f;
+        for (int i = t; i < n; i += SNT) {
+            const float w = pexp(s_cp[i] - zmax);
+            s_cp[i] = w;
+            ls += w;
+        }
+        const float S = block_sum(ls, s_redf);
+        for (int i = t; i < n; i += SNT) s_cp[i] = s_cp[i] / S;
+        __syncthreads();
+        if (a.top_p < 1.0f) {
+            // sort the slots by (p descending, slot ascending) = the stable
+            // descending sortperm of the probabilities
+            int P2 = 1;
+            while (P2 < n) P2 <<= 1;
+            for (int i = t; i < P2; i += SNT) s_sort[i] = i < n ? i : -1;
+            __syncthreads();
+            for (int size = 2; size <= P2; size <<= 1)
+                for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                    for (int i = t; i < P2 / 2; i += SNT) {
+                        const int lo = ((i & ~(stride - 1)) << 1) | (i & (stride - 1));
+                        const int hi = lo + stride;
+                        const int A = s_sort[lo], B = s_sort[hi];
+                        bool a_first;
+                        if (A < 0) a_first = false;
+                        else if (B < 0) a_first = true;
+                        else {
+                            const float pa = s_cp[A], pb = s_cp[B];
+                            a_first = pa > pb || (pa == pb && A < B);
+                        }
+                        if (a_first != ((lo & size) == 0)) {
+                            s_sort[lo] = B;
+                            s_sort[hi] = A;
+                        }
+                    }
+                    __syncthreads();
+                }
+            // the shortest sorted prefix whose mass reaches top_p
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int j = 4 * t + e;
+                v[e] = j < n ? s_cp[s_sort[j]] : 0.f;
+            }
+            float tot;
+            const int hit = first_cdf_hit(v, n - 4 * t, 0.f, a.top_p, s_redf, tot);
+            const int cut = block_min_i(hit, s_redi);
+            const int n_keep = cut == INT_MAX ? n : cut + 1;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int j = 4 * t + e;
+                if (j < n && j >= n_keep) s_cp[s_sort[j]] = 0.f;
+            }
+            __syncthreads();
+            float lt = 0.f;
+            for (int i = t; i < n; i += SNT) lt += s_cp[i];
+            const float total = block_sum(lt, s_redf);
+            if (total > 0.f)
+                for (int i = t; i < n; i += SNT) s_cp[i] = s_cp[i] / total;
+            __syncthreads();
+        }
+        if (a.min_p > 0.f) {
+            float lm2 = 0.f;
+            for (int i = t; i < n; i += SNT) lm2 = fmaxf(lm2, s_cp[i]);
+            const float thr = block_max(lm2, s_redf) * a.min_p;
+            float lt = 0.f;
+            for (int i = t; i < n; i += SNT) {
+                float p = s_cp[i];
+                if (p < thr) p = 0.f;
+                s_cp[i] = p;
+                lt += p;
+            }
+            const float total = block_sum(lt, s_redf);
+            if (total > 0.f)
+                for (int i = t; i < n; i += SNT) s_cp[i] = s_cp[i] / total;
+            __syncthreads();
+        }
+        // inverse CDF in index order over the candidates
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int j = 4 * t + e;
+            v[e] = j < n ? s_cp[j] : 0.f;
+        }
+        float tot;
+        const int hit = first_cdf_hit(v, n - 4 * t, 0.f, ur, s_redf, tot);
+        const int slot = block_min_i(hit, s_redi);
+        if (t == 0) out[row] = slot == INT_MAX ? V - 1 : s_cidx[slot];
+        return;
+    }
+
+    // ---- whole-row path: softmax statistics in one online pass
+    float zmax = -__builtin_huge_valf(), S = 0.f;
+    for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int) {
+        if (!in) return;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            if (z[e] > zmax) {
+                S = S * pexp(zmax - z[e]) + 1.0f;
+                zmax = z[e];
+            } else if (zmax > -__builtin_huge_valf()) {
+                S += pexp(z[e] - zmax);
+            }
+        }
+    });
+    block_ms(zmax, S, s_redf);
+    // kept: above_threshold(zb, tau, tie_lim); everything without top-p
+    uint32_t zb = 256u, tau = 0u;
+    int tie_lim = V;
+    bool div_total = false;  // top-p renormalizes by the nucleus mass
+    float total_p = 1.0f;
+    const float invS = 1.0f / S;  // (probabilities by reciprocals: within an ulp of the divisions)
+    if (a.top_p < 1.0f) {
+        const float tp = fmaxf(a.top_p, 0.f) * 1099511627776.0f;
+        const unsigned long long target = tp < 1.0f ? 1ull : (unsigned long long)ceilf(tp);
+        Select R;
+        select_threshold<true>(Lr, V, nround, invT, zmax, S, target, s_hist, s_mass, s_sel, s_selm, R);
+        if (!R.all) {
+            zb = R.zb;
+            tau = R.tau;
+            // ties at tau share one probability: keep the first n_eq of them
+            const float ptau = pexp(okey_inv(tau) - zmax) * invS;
+            const unsigned long long mt = (unsigned long long)(ptau * 1099511627776.0f);
+            unsigned long long n_eq = mt ? (R.rem + mt - 1) / mt : (unsigned long long)R.cnt;
+            if (n_eq < 1) n_eq = 1;
+            if (n_eq < R.cnt) {
+                // index of the n_eq-th tie in index order
+                int run = 0, lim = V;
+                for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int r) {
+                    bool q[4];
+                    uint32_t nq = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        q[e] = in && zbin(z[e], zmax) == zb && okey(z[e]) == tau;
+                        nq += q[e];
+                    }
+                    uint32_t tot;
+                    const uint32_t ex = block_excl_scan_u(nq, s_redu, tot);
+                    int cand = INT_MAX;
+                    int c = run + (int)ex;
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (q[e]) {
+                            c++;
+                            if (c == (int)n_eq && cand == INT_MAX) cand = r * SROUND + 4 * t + e + 1;
+                        }
+                    const int got = block_min_i(cand, s_redi);
+                    if (lim == V && got != INT_MAX) lim = got;
+                    run += (int)tot;
+                });
+                tie_lim = lim;
+            }
+        }
+        // mass of the nucleus, then p' = p / total
+        float lt = 0.f;
+        for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int r) {
+            if (!in) return;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (zb == 256u || above_threshold(z[e], r * SROUND + 4 * t + e, zmax, zb, tau, tie_lim))
+                    lt += pexp(z[e] - zmax) * invS;
+        });
+        total_p = block_sum(lt, s_redf);
+        div_total = total_p > 0.f;
+    }
+    const float inv_total = div_total ? 1.0f / total_p : 1.0f;
+    auto prob = [&](float z) {
+        float p = pexp(z - zmax) * invS;
+        if (div_total) p = p * inv_total;
+        return p;
+    };
+    auto kept = [&](float z, int j) {
+        return zb == 256u || above_threshold(z, j, zmax, zb, tau, tie_lim);
+    };
+    // min-p: the largest probability is the argmax's, exp(0) / S (renormalized)
+    float thr = 0.f;
+    bool div_total2 = false;
+    float total2 = 1.0f;
+    if (a.min_p > 0.f) {
+        float pmax = invS;
+        if (div_total) pmax = pmax * inv_total;
+        thr = pmax * a.min_p;
+        float lt = 0.f;
+        for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int r) {
+            if (!in) return;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (kept(z[e], r * SROUND + 4 * t + e)) {
+                    const float p = prob(z[e]);
+                    if (!(p < thr)) lt += p;
+                }
+        });
+        total2 = block_sum(lt, s_redf);
+        div_total2 = total2 > 0.f;
+    }
+    const float inv_total2 = div_total2 ? 1.0f / total2 : 1.0f;
+    auto final_p = [&](float z, int j) {
+        if (!kept(z, j)) return 0.f;
+        float p = prob(z);
+        if (a.min_p > 0.f) {
+            if (p < thr) return 0.f;
+            if (div_total2) p = p * inv_total2;
+        }
+        return p;
+    };
+    // the draw: each round's sum (batched: one block reduction per RB
+    // rounds), the round, then the index inside it
+    for (int r0 = 0; r0 < nround; r0 += RB) {
+        float part[RB];
+#pragma unroll
+        for (int b = 0; b < RB; b++) {
+            float z[4];
+            bool in;
+            load_round(Lr, V, r0 + b, invT, z, in);
+            float c = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) c += in ? final_p(z[e], (r0 + b) * SROUND + 4 * t + e) : 0.f;
+            part[b] = wave_sum(c);
+        }
+        __syncthreads();
+        if ((t & 63) == 0)
+#pragma unroll
+            for (int b = 0; b < RB; b++) s_redv[t >> 6][b] = part[b];
+        __syncthreads();
+        if (t < RB && r0 + t < nround) {
+            float sum = 0.f;
+            for (int w = 0; w < SNW; w++) sum += s_redv[w][t];
+            s_round[r0 + t] = sum;
+        }
+    }
+    __syncthreads();
+    if (t == 0) {
+        float cum = 0.f;
+        int rr = -1;
+        for (int r = 0; r < nround; r++) {
+            const float nc = cum + s_round[r];
+            if (ur <= nc) {
+                rr = r;
+                break;
+            }
+            cum = nc;
+        }
+        s_sel[0] = (uint32_t)rr;
+        s_before = cum;
+    }
+    __syncthreads();
+    const int rr = (int)s_sel[0];
+    const float before = s_before;
+    __syncthreads();
+    if (rr < 0) {
+        if (t == 0) out[row] = V - 1;
+        return;
+    }
+    float z[4], v[4];
+    bool in;
+    load_round(Lr, V, rr, invT, z, in);
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = in ? final_p(z[e], rr * SROUND + 4 * t + e) : 0.f;
+    float tot;
+    const int hit = first_cdf_hit(v, in ? 4 : 0, before, ur, s_redf, tot);
+    const int local = block_min_i(hit, s_redi);
+    // (the scan inside the round can end a rounding step below the round's
+    // sum that selected it: then the round's last kept entry)
+    int last = INT_MAX;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        if (v[e] > 0.f) last = INT_MAX - (4 * t + e);
+    const int lastk = block_min_i(last, s_redi);
+    if (t == 0) {
+        int tok = local != INT_MAX ? rr * SROUND + local : lastk != INT_MAX ? rr * SROUND + (INT_MAX - lastk) : V - 1;
+        out[row] = min(tok, V - 1);
+    }
+}
+
+// In place on rows of logits: for every distinct id of the row's list in
+// [0, V): x -= presence (if presence != 0), then x = x > 0 ? x / rep : x * rep
+// (if rep != 1). A bitmap in LDS skips repeated ids.
+constexpr int PEN_NT = 256;
+constexpr int PEN_MAX_V = 262144;
+__global__ __launch_bounds__(PEN_NT) void penalty_kernel(float *__restrict__ L, int V, const int32_t *__restrict__ tok,
+                                                          int n_tok, int64_t tok_stride, float presence,
+                                                          float repetition) {
+    __shared__ uint32_t seen[PEN_MAX_V / 32];
+    const int row = blockIdx.x, t = threadIdx.x;
+    const int nw = (V + 31) / 32;
+    for (int i = t; i < nw; i += PEN_NT) seen[i] = 0u;
+    __syncthreads();
+    const int32_t *ids = tok + (size_t)row * tok_stride;
+    float *x = L + (size_t)row * V;
+    for (int i = t; i < n_tok; i += PEN_NT) {
+        const int id = ids[i];
+        if (id < 0 || id >= V) continue;
+        const uint32_t bit = 1u << (id & 31);
+        if (atomicOr(&seen[id >> 5], bit) & bit) continue;
+        float v = x[id];
+        if (presence != 0.f) v -= presence;
+        if (repetition != 1.0f) v = v > 0.f ? v / repetition : v * repetition;
+        x[id] = v;
+    }
+}
+
+}  // namespace
+
+int sample_max_top_k() { return SK_MAX; }
+int sample_max_v() { return SMAX_ROUNDS * SROUND; }
+int penalty_max_v() { return PEN_MAX_V; }
+
+hipError_t launch_sample(const float *L, int rows, int V, float T, int top_k, float top_p, float min_p, const float *u,
+                         int32_t *out, hipStream_t st) {
+    const SampleArgs a{T, top_k, top_p, min_p};
+    draft_sample_kernel<<<rows, SNT, 0, st>>>(L, V, a, u, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_penalties(float *L, int rows, int V, const int32_t *tok, int n_tok, int64_t tok_stride,
+                            float presence, float repetition, hipStream_t st) {
+    if (n_tok == 0 || (presence == 0.f && repetition == 1.0f)) return hipSuccess;
+    penalty_kernel<<<rows, PEN_NT, 0, st>>>(L, V, tok, n_tok, tok_stride, presence, repetition);
+    return hipGetLastError();
+}

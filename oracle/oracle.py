@@ -156,6 +156,86 @@ def rmsnorm(x, eps=1e-6, w=None):
     return out
 
 
+# ---- draft-side sampler: numpy restatement (float32 like the reference) ----
+
+def sample_dist(logits, temperature: float = 1.0, top_p: float = 1.0, top_k: int = 0,
+                min_p: float = 0.0) -> np.ndarray:
+    """The float32 distribution softmax_sample (src/ModelCPU.jl:1123-1200)
+    draws from at temperature > 0: z = L / T (:1130-1132); top-k by the
+    stable descending sortperm (:1135-1143); softmax with max subtraction
+    (:1146-1148); top-p: the shortest prefix of the stable descending
+    sortperm of p whose cumulative sum is >= top_p, renormalized when the sum
+    is > 0 (:1151-1173); min-p: drop p < max(p) * min_p, renormalize
+    (:1176-1188). Probabilities are float32 element by element as in the
+    reference; its cumulative sums are sequential float32 loops, which over
+    ~10^5 terms drift from the exact prefix sum by up to ~1e-4, so the
+    contract (as for the residual draw of the accept path) is the exact
+    prefix sum, taken here in float64."""
+    L = np.asarray(logits, dtype=np.float32).copy()
+    V = L.size
+    T = np.float32(temperature)
+    if T != np.float32(1.0):
+        L = L / T
+    if top_k > 0:
+        order = np.argsort(-L, kind="stable")
+        keep = np.zeros(V, dtype=bool)
+        keep[order[:min(top_k, V)]] = True
+        L[~keep] = -np.inf
+    m = L.max()
+    with np.errstate(invalid="ignore", over="ignore"):
+        e = np.exp(L - m).astype(np.float32)
+    p = (e / e.sum(dtype=np.float32)).astype(np.float32)
+    if top_p < 1.0:
+        order = np.argsort(-p, kind="stable")
+        c = np.cumsum(p[order], dtype=np.float64)
+        hit = np.nonzero(c >= top_p)[0]
+        n_keep = int(hit[0]) + 1 if hit.size else V
+        keep = np.zeros(V, dtype=bool)
+        keep[order[:n_keep]] = True
+        p[~keep] = 0.0
+        total = p.sum(dtype=np.float32)
+        if total > 0:
+            p = (p / total).astype(np.float32)
+    if min_p > 0.0:
+        thr = np.float32(p.max() * np.float32(min_p))
+        p[p < thr] = 0.0
+        total = p.sum(dtype=np.float32)
+        if total > 0:
+            p = (p / total).astype(np.float32)
+    return p
+
+
+def softmax_sample(logits, r: float, temperature: float = 1.0, top_p: float = 1.0, top_k: int = 0,
+                   min_p: float = 0.0) -> int:
+    """softmax_sample (src/ModelCPU.jl:1123-1200), 0-based, with the uniform r
+    that the reference draws by rand(Float32) at :1191 given explicitly:
+    T = 0 -> first-index argmax (:1125-1127); otherwise the first i with
+    r <= the (exact, float64) prefix sum of sample_dist, else the last index
+    (:1191-1198); r <= 0 gives index 0 as the reference's loop does."""
+    if temperature == 0.0:
+        return int(np.argmax(np.asarray(logits, dtype=np.float32)))
+    p = sample_dist(logits, temperature, top_p, top_k, min_p)
+    c = np.cumsum(p, dtype=np.float64)
+    hit = np.nonzero(float(np.float32(r)) <= c)[0]
+    return int(hit[0]) if hit.size else p.size - 1
+
+
+def apply_penalties(logits, token_ids, presence: float = 0.0, repetition: float = 1.0) -> np.ndarray:
+    """apply_presence_penalty! then apply_repetition_penalty!
+    (src/ModelCPU.jl:1202-1225, in that order at :1247-1248) on a copy, over
+    the distinct ids in [0, V) (the keys of the reference's token_counts)."""
+    L = np.asarray(logits, dtype=np.float32).copy()
+    ids = sorted(set(int(i) for i in np.asarray(token_ids).ravel() if 0 <= int(i) < L.size))
+    pres, rep = np.float32(presence), np.float32(repetition)
+    if presence != 0.0:
+        for i in ids:
+            L[i] = L[i] - pres
+    if repetition != 1.0:
+        for i in ids:
+            L[i] = L[i] / rep if L[i] > 0 else L[i] * rep
+    return L
+
+
 # ---- the reference's own C kernel, built from its source into _ref/ ----
 
 _ref = None

@@ -107,3 +107,20 @@ def test_mlp_forward_argument_checks(lib):
     assert lib.ihip_mlp_forward(12, p16, 14, p16, p16, None, -1.0, 5, 512, 1024, 1, p16, 64, None) == -22
     assert lib.ihip_mlp_forward(12, p16, 14, p16, p16, None, 1e-6, 5, 512, 1024, 1, p16, 64, None) == -12
     assert b"workspace" in lib.ihip_last_error()
+
+
+def test_sampler_argument_checks(lib):
+    """ihip_sample / ihip_apply_penalties validate before touching the GPU."""
+    buf = (C.c_uint8 * 64)()
+    p16 = (C.addressof(buf) + 15) & ~15
+    assert lib.ihip_sample(None, 1, 8, 1.0, 0, 1.0, 0.0, p16, p16, None) == -14
+    assert lib.ihip_sample(p16, 1, 6, 1.0, 0, 1.0, 0.0, p16, p16, None) == -22      # V % 4
+    assert lib.ihip_sample(p16 + 4, 1, 8, 1.0, 0, 1.0, 0.0, p16, p16, None) == -22  # alignment
+    assert lib.ihip_sample(p16, 1, 8, -1.0, 0, 1.0, 0.0, p16, p16, None) == -22     # temperature
+    assert lib.ihip_sample(p16, 1, 151936, 1.0, 5000, 1.0, 0.0, p16, p16, None) == -22  # top_k above 4096
+    assert b"top_k" in lib.ihip_last_error()
+    assert lib.ihip_sample(p16, 1, 8, 1.0, -1, 1.0, 0.0, p16, p16, None) == -22
+    assert lib.ihip_sample(p16, 1, 8, 1.0, 0, float("nan"), 0.0, p16, p16, None) == -22
+    assert lib.ihip_apply_penalties(None, 1, 8, p16, 1, 0, 0.5, 1.0, None) == -14
+    assert lib.ihip_apply_penalties(p16, 1, 300000, p16, 1, 0, 0.5, 1.0, None) == -22
+    assert lib.ihip_apply_penalties(p16, 2, 8, p16, 4, 2, 0.5, 1.0, None) == -22  # stride < n_tok

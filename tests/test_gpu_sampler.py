@@ -1,0 +1,140 @@
+"""GPU: the draft-side sampler (ihip_sample: softmax_sample,
+src/ModelCPU.jl:1123-1200) and the logit penalties (ihip_apply_penalties:
+src/ModelCPU.jl:1202-1225) against the oracle. Known answers are exact; at
+V = 151936 the GPU's tree sums may move a draw only where u lies within
+rounding of a step of the oracle's cumulative distribution (or the nucleus
+edge within rounding of top_p), and at most one draw per setting may do so.
+Penalties are bit-exact."""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+VOCAB = 151936
+
+
+@pytest.fixture(scope="module")
+def ih():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import inferno_hip
+    assert inferno_hip.quant_kernels_available(), inferno_hip._lib.last_error()
+    return inferno_hip
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _pad4(L):
+    L = np.asarray(L, np.float32)
+    n = (-L.size) % 4
+    return np.concatenate([L, np.full(n, -np.inf, np.float32)])
+
+
+def _draw(ih, L, us, **kw):
+    L = np.asarray(L, np.float32)
+    rows = L if L.ndim == 2 else np.broadcast_to(L, (len(us), L.size))
+    return ih.softmax_sample(_dev(np.ascontiguousarray(rows)), _dev(np.asarray(us, np.float32)), **kw).cpu().numpy()
+
+
+def test_known_answers(ih):
+    LOG = lambda ps: np.log(np.asarray(ps, np.float64)).astype(np.float32)
+    L = _pad4(LOG([0.25, 0.75]))
+    assert list(_draw(ih, L, [0.2, 0.25, 0.3, 0.9999])) == [0, 0, 1, 1]
+    U = np.zeros(8, np.float32)
+    rs = [0.01, 0.124, 0.126, 0.3, 0.5, 0.99]
+    assert list(_draw(ih, U, rs)) == [math.ceil(8 * r) - 1 for r in rs]
+    P = LOG([0.1, 0.2, 0.3, 0.4])
+    assert list(_draw(ih, P, [0.42, 0.43], top_p=0.5)) == [2, 3]
+    Q = _pad4(LOG([0.1, 0.3, 0.6]))
+    assert list(_draw(ih, Q, [0.3, 0.34], min_p=0.5)) == [1, 2]
+    assert list(_draw(ih, _pad4(LOG([1e-3, 1.0])), [0.0, 0.5], top_k=1)) == [0, 1]  # r = 0 -> first index
+    E = np.array([1.0, 5.0, 2.0, 4.0], np.float32)
+    rng = np.random.default_rng(5)
+    us = rng.random(64).astype(np.float32)
+    assert set(_draw(ih, E, us, temperature=0.7, top_k=2)) <= {1, 3}
+    assert set(_draw(ih, E, us, temperature=0.7, top_k=1)) == {1}
+    assert set(_draw(ih, E, us, temperature=0.5, top_p=0.01)) == {1}
+    ties = np.array([2.0, 3.0, 3.0, 1.0, 3.0, 0.0, 0.0, 0.0], np.float32)
+    assert list(_draw(ih, ties, [0.5], temperature=0.0)) == [1]
+    assert set(_draw(ih, ties, np.linspace(0.01, 0.99, 50), top_k=2)) == {1, 2}
+
+
+def _near_boundary(row, u, g, o, kw):
+    p = O.sample_dist(row, **kw).astype(np.float64)
+    c = np.cumsum(p)
+    lo, hi = min(g, o), max(g, o)
+    if abs(u - c[lo]) < 1e-5 or abs(u - c[hi - 1]) < 1e-5:
+        return True
+    if kw.get("top_p", 1.0) < 1.0:  # nucleus edge within rounding of top_p
+        q = O.sample_dist(row, temperature=kw.get("temperature", 1.0), top_k=kw.get("top_k", 0)).astype(np.float64)
+        cs = np.cumsum(np.sort(q)[::-1])
+        if np.min(np.abs(cs - kw["top_p"])) < 1e-5:
+            return True
+    return False
+
+
+SETTINGS = [dict(temperature=1.0), dict(temperature=0.8, top_p=0.9), dict(temperature=0.8, top_k=40),
+            dict(temperature=0.7, top_k=50, top_p=0.95), dict(temperature=1.0, min_p=0.05),
+            dict(temperature=0.8, top_p=0.9, min_p=0.02), dict(temperature=1.0, top_k=4096, top_p=0.9),
+            dict(temperature=0.0)]
+
+
+@pytest.mark.parametrize("kw", SETTINGS, ids=lambda kw: ",".join(f"{k}={v}" for k, v in kw.items()))
+def test_parity_full_vocab(ih, kw):
+    rows = 48
+    rng = np.random.default_rng(hash(tuple(sorted(kw.items()))) % 2**32)
+    L = (3.0 * rng.standard_normal((rows, VOCAB))).astype(np.float32)
+    us = rng.random(rows).astype(np.float32)
+    got = _draw(ih, L, us, **kw)
+    bad = 0
+    for r in range(rows):
+        want = O.softmax_sample(L[r], float(us[r]), **kw)
+        if got[r] != want:
+            assert kw.get("temperature", 1.0) != 0.0, (r, got[r], want)
+            assert _near_boundary(L[r], float(us[r]), int(got[r]), want, kw), (r, got[r], want)
+            bad += 1
+    assert bad <= 1
+
+
+def test_topk_ties_exact(ih):
+    # all equal: top_k = 5 keeps indices 0..4, token = ceil(5 u) - 1
+    Z = np.zeros(4096, np.float32)
+    us = np.array([0.03, 0.19, 0.21, 0.5, 0.77, 0.97], np.float32)
+    assert list(_draw(ih, Z, us, top_k=5)) == [math.ceil(5 * u) - 1 for u in us]
+    # quantized logits: ties straddle the k-th place; kept = all 2s, then 1s by index
+    rng = np.random.default_rng(9)
+    L = rng.integers(0, 3, size=(16, 8192)).astype(np.float32)
+    us = rng.random(16).astype(np.float32)
+    for k in (1, 37, 100, 4000):
+        got = _draw(ih, L, us, top_k=k, temperature=0.9)
+        for r in range(16):
+            want = O.softmax_sample(L[r], float(us[r]), temperature=0.9, top_k=k)
+            assert got[r] == want or _near_boundary(L[r], float(us[r]), int(got[r]), want,
+                                                    dict(temperature=0.9, top_k=k)), (k, r)
+
+
+def test_penalties_exact(ih):
+    import torch
+    rng = np.random.default_rng(13)
+    L = (2.0 * rng.standard_normal((3, 1000))).astype(np.float32)
+    ids = np.array([5, 17, 17, 999, 1000, -3, 0, 42, 5], np.int32)  # repeats and out-of-range ids
+    d = _dev(L)
+    ih.apply_penalties_(d, torch.from_numpy(ids), presence=0.4, repetition=1.3)
+    want = np.stack([O.apply_penalties(L[r], ids, 0.4, 1.3) for r in range(3)])
+    np.testing.assert_array_equal(d.cpu().numpy(), want)
+    per_row = rng.integers(-5, 1005, size=(3, 64)).astype(np.int32)
+    d2 = _dev(L)
+    ih.apply_penalties_(d2, torch.from_numpy(per_row), presence=-0.25, repetition=0.8)
+    want2 = np.stack([O.apply_penalties(L[r], per_row[r], -0.25, 0.8) for r in range(3)])
+    np.testing.assert_array_equal(d2.cpu().numpy(), want2)
+    d3 = _dev(L)
+    ih.apply_penalties_(d3, torch.from_numpy(ids))  # presence 0, repetition 1: untouched
+    np.testing.assert_array_equal(d3.cpu().numpy(), L)
