@@ -603,6 +603,42 @@ def sampler_config(ih):
     return out
 
 
+def gguf_config(ih):
+    """GGUF file -> device weights (ihip_gguf_upload, the loader of
+    src/GGUF.jl + src/LoaderCPU.jl:120-175): a 604 MB file of eight Q4_K
+    matrices 16384 x 8192 (seeded bytes) written to local disk, read back
+    (page cache warm after one pass) and uploaded plain and packed; GB/s of
+    file bytes per second, whole call (host memcpy from the mapping into
+    pinned staging, DMA, and for packed the device repack)."""
+    import tempfile
+    import torch
+    import numpy as np
+    N, K = 16384, 8192
+    rng = np.random.default_rng(SEED)
+    nb = N * K // 256 * 144
+    blob = rng.integers(0, 256, size=nb, dtype=np.uint8).tobytes()
+    out = {"file_bytes": 0}
+    with tempfile.TemporaryDirectory(dir=os.environ.get("TMPDIR", "/tmp")) as d:
+        path = os.path.join(d, "w.gguf")
+        ih.gguf.write_gguf(path, [("general.architecture", ih.gguf.GGUF_TYPE_STRING, "bench")],
+                           [(f"blk.{i}.w", (K, N), ih.formats.Q4_K, blob) for i in range(8)])
+        out["file_bytes"] = os.path.getsize(path)
+        with ih.gguf.read_gguf(path) as f:
+            dev = torch.empty(max(nb, ih.quantized_kernels.packed_bytes(ih.formats.Q4_K, N, K)), dtype=torch.uint8,
+                              device="cuda")
+            for name in f.tensors:  # warm the page cache
+                f.upload(name, out=dev)
+            for mode, packed in (("plain", False), ("packed", True)):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for name in f.tensors:
+                    f.upload(name, packed=packed, out=dev)
+                torch.cuda.synchronize()
+                dt = time.perf_counter() - t0
+                out[f"{mode}_GBps"] = round(8 * nb / dt / 1e9, 2)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -616,8 +652,8 @@ def main():
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only run the roofline kernel and the traffic calibration kernel (for rocprofv3 --pmc)")
     ap.add_argument("--configs", type=str, default="",
-                    help="instead of the bench line: measure BASELINE configs (comma list of 1,2,3,5, and 'sampler' "
-                         "for the draft-side sampler), one JSON object per config")
+                    help="instead of the bench line: measure BASELINE configs (comma list of 1,2,3,5, 'sampler' "
+                         "for the draft-side sampler, 'gguf' for file-to-device loading), one JSON object per config")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -637,9 +673,11 @@ def main():
                 res = config5(ih, Model(ih, args.layers, keep_gguf=0))
             elif c == "sampler":
                 res = sampler_config(ih)
+            elif c == "gguf":
+                res = gguf_config(ih)
             else:
                 res = {"1": config1, "2": config2, "3": config3}[c](ih)
-            print(json.dumps({"config": c if c == "sampler" else int(c), **res}), flush=True)
+            print(json.dumps({"config": c if c in ("sampler", "gguf") else int(c), **res}), flush=True)
             torch.cuda.empty_cache()
         return
     model = Model(ih, args.layers, keep_gguf=0 if (args.no_cpu or args.profile_kernels) else 4)

@@ -280,6 +280,47 @@ int ihip_apply_penalties(float *logits_dev, int rows, int V,
                          const int32_t *tok_dev, int n_tok, int64_t tok_stride,
                          float presence, float repetition, void *stream);
 
+/* ---- GGUF file -> device weights (csrc/gguf.cpp) ---- */
+
+/* read_gguf (src/GGUF.jl:119-165): the file is memory-mapped read-only and
+ * its header, metadata and tensor table parsed with bounds checks (a
+ * malformed file returns IHIP_EINVAL with the reason: "Not a valid GGUF
+ * file" for a bad magic, strings over 1 MiB, unknown value types, tensor
+ * data past the end). Metadata keys are unique (a repeated key: the last).
+ * Tensor dims are innermost first (dims[0] = K, dims[1] = N of a matrix);
+ * nbytes is 0 for GGML types whose layout this library does not know (it
+ * knows F32, F16, BF16, Q8_0, Q4_K, Q5_K, Q6_K, I8..I64, F64). Returned
+ * strings and tensor_data point into the mapping: valid until close. */
+int ihip_gguf_open(const char *path, void **handle);
+int ihip_gguf_close(void *handle);
+int ihip_gguf_info(void *handle, uint32_t *version, int64_t *n_tensors,
+                   int64_t *n_kv, uint64_t *alignment, uint64_t *data_offset);
+int ihip_gguf_tensor(void *handle, int64_t i, const char **name,
+                     int *ggml_type, int *ndim, int64_t *dims /* [4] */,
+                     uint64_t *offset, uint64_t *nbytes);
+int64_t ihip_gguf_find_tensor(void *handle, const char *name);  /* -1: absent */
+int64_t ihip_gguf_find_key(void *handle, const char *key);      /* -1: absent */
+/* vtype: GGUF value type (0..12); arrays (9): atype and count, else atype
+ * -1 and count 1. */
+int ihip_gguf_kv(void *handle, int64_t i, const char **key, int *vtype,
+                 int *atype, uint64_t *count);
+/* element index of a numeric value or array: as an integer and as a double */
+int ihip_gguf_kv_number(void *handle, int64_t i, uint64_t index,
+                        int64_t *as_int, double *as_float);
+/* a string value (index 0) or element index of a string array (not
+ * NUL-terminated: len bytes) */
+int ihip_gguf_kv_string(void *handle, int64_t i, uint64_t index,
+                        const char **str, uint64_t *len);
+const void *ihip_gguf_tensor_data(void *handle, int64_t i);  /* host bytes */
+/* Copies tensor i to device memory (through pinned staging, synchronous on
+ * the stream). IHIP_GGUF_PACKED: a 2-D Q4_K/Q5_K/Q6_K/Q8_0 matrix is stored
+ * in the packed layout of ihip_pack_weights (dev_bytes >= ihip_packed_bytes),
+ * else the GGUF bytes as they are (dev_bytes >= nbytes). The handle's pinned
+ * staging (2 x 64 MiB, kept until close) serves one upload at a time. */
+#define IHIP_GGUF_PACKED 1
+int ihip_gguf_upload(void *handle, int64_t i, void *dev, size_t dev_bytes,
+                     int flags, void *stream);
+
 /* ---- synthetic inputs (benchmark and tests; csrc/misc.hip) ---- */
 
 /* n_blocks seeded GGUF blocks of qtype starting at block first_block of

@@ -217,6 +217,17 @@ void dropin_gemv(const char *name, int qt, const uint8_t *weight, const float *x
 extern "C" {
 
 const char *ihip_last_error(void) { return t_err.c_str(); }
+// status reporting for the other host files of the library (gguf.cpp)
+__attribute__((visibility("hidden"))) int ihip_internal_fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    return fail(code, "%s", buf);
+}
+__attribute__((visibility("hidden"))) int ihip_internal_ok() { return ok(); }
+
 int ihip_last_status(void) { return t_status; }
 
 int ihip_init(int device) {

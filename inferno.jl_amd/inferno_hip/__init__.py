@@ -5,7 +5,7 @@ SpeculativeDecoding (verify / accept) interfaces over the C ABI in
 include/inferno_hip.h, implemented by hand-written HIP kernels in
 lib/libinferno_hip.so. There is no CPU fallback.
 """
-from . import formats, synth
+from . import formats, gguf, synth
 from ._lib import HipError, load
 from .quantized_kernels import (ACT_PLAIN, ACT_RMSNORM, ACT_SILU_MUL, GEMM_ACCUM, GEMM_AUTO, GEMM_F32, GEMM_HALF,
                                 GEMM_DEFER, GEMM_PACKED, GEMM_REUSE, dequant, gemm_partials, gemm_q, gemm_q_ex,
@@ -16,7 +16,7 @@ from .speculative import (MODE_REFERENCE, MODE_STANDARD, SpeculativeStats, greed
                           mtp_verify_step, softmax_stats, spec_accept, tree_accept)
 
 __all__ = [
-    "formats", "synth", "HipError", "load", "GEMM_ACCUM", "GEMM_AUTO", "GEMM_F32", "GEMM_HALF",
+    "formats", "gguf", "synth", "HipError", "load", "GEMM_ACCUM", "GEMM_AUTO", "GEMM_F32", "GEMM_HALF",
     "GEMM_PACKED", "GEMM_REUSE", "GEMM_DEFER", "gemm_partials", "ACT_PLAIN", "ACT_RMSNORM", "ACT_SILU_MUL", "dequant", "gemm_q", "gemm_q_ex",
     "mlp_forward_", "mlp_ws_bytes", "pack_weights", "packed_bytes", "q4_k_gemv_", "q5_k_gemv_", "q6_k_gemv_", "q8_0_gemv_",
     "quant_kernels_available", "rmsnorm", "MODE_REFERENCE", "MODE_STANDARD", "SpeculativeStats",

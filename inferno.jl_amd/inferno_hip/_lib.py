@@ -48,6 +48,19 @@ SIGNATURES = {
     "ihip_tree_accept": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ihip_sample": (_i, [_vp, _i, _i, _f, _i, _f, _f, _vp, _vp, _vp]),
     "ihip_apply_penalties": (_i, [_vp, _i, _i, _vp, _i, _i64, _f, _f, _vp]),
+    "ihip_gguf_open": (_i, [C.c_char_p, C.POINTER(_vp)]),
+    "ihip_gguf_close": (_i, [_vp]),
+    "ihip_gguf_info": (_i, [_vp, C.POINTER(C.c_uint32), C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_u64),
+                            C.POINTER(_u64)]),
+    "ihip_gguf_tensor": (_i, [_vp, _i64, C.POINTER(C.c_char_p), C.POINTER(_i), C.POINTER(_i), C.POINTER(_i64),
+                              C.POINTER(_u64), C.POINTER(_u64)]),
+    "ihip_gguf_find_tensor": (_i64, [_vp, C.c_char_p]),
+    "ihip_gguf_find_key": (_i64, [_vp, C.c_char_p]),
+    "ihip_gguf_kv": (_i, [_vp, _i64, C.POINTER(C.c_char_p), C.POINTER(_i), C.POINTER(_i), C.POINTER(_u64)]),
+    "ihip_gguf_kv_number": (_i, [_vp, _i64, _u64, C.POINTER(_i64), C.POINTER(C.c_double)]),
+    "ihip_gguf_kv_string": (_i, [_vp, _i64, _u64, C.POINTER(_vp), C.POINTER(_u64)]),
+    "ihip_gguf_tensor_data": (_vp, [_vp, _i64]),
+    "ihip_gguf_upload": (_i, [_vp, _i64, _vp, _sz, _i, _vp]),
     "ihip_synth_blocks": (_i, [_i, _u64, _i64, _i64, _vp, _vp]),
     "ihip_synth_gaussian": (_i, [_u64, _i64, _f, _vp, _vp, _vp]),
 }
