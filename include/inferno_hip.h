@@ -250,6 +250,27 @@ int ihip_tree_accept(const float *tgt_dev, const float *drf_dev,
                      int32_t *out_len_dev, void *ws, size_t ws_bytes,
                      void *stream);
 
+/* ---- applying the outcome of a verify step (csrc/rollback.hip) ---- */
+
+/* The reference keeps no rollback (src/SpeculativeDecoding.jl:69-70); these
+ * read n = n_accepted_dev[s] (the out_n of ihip_spec_accept / greedy verify:
+ * drafts accepted, -1 for an invalid draft) on the device, so a captured
+ * verify step needs no host round trip. For each step s < steps:
+ *   commit_state: state[s] = snapshot n of step s, the recurrent (SSM) state
+ *   after the verify forward consumed positions 0..n; snapshot j of step s
+ *   at snap_dev + s * snap_step_bytes + j * snap_stride_bytes, j = 0..k;
+ *   state of step s at state_dev + s * state_step_bytes;
+ *   advance_len: len[s] += n + 1 (the KV-cache entries that stand).
+ * n = -1 or n > k leaves the step's state / length unchanged. Sizes, strides
+ * and pointers are multiples of 4 bytes. */
+int ihip_spec_commit_state(void *state_dev, const void *snap_dev, size_t bytes,
+                           int64_t snap_stride_bytes, int k,
+                           const int32_t *n_accepted_dev, int steps,
+                           int64_t state_step_bytes, int64_t snap_step_bytes,
+                           void *stream);
+int ihip_spec_advance_len(int32_t *len_dev, const int32_t *n_accepted_dev,
+                          int steps, void *stream);
+
 /* ---- draft-side sampler (csrc/sample.hip) ---- */
 
 /* softmax_sample (src/ModelCPU.jl:1123-1200) on each row of logits

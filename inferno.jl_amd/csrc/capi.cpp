@@ -42,6 +42,10 @@ hipError_t launch_rmsnorm(const float *x, const float *w, float *out, int rows, 
 hipError_t launch_silu_mul(const float *gu, int M, int F, float *out, hipStream_t st);
 hipError_t launch_add(float *y, const float *x, int64_t n, hipStream_t st);
 hipError_t launch_synth(int qt, uint64_t stream, int64_t first, int64_t nblk, void *out, hipStream_t st);
+hipError_t launch_commit_state(void *state, const void *snap, int64_t words, int64_t snap_stride, int k,
+                               const int32_t *n_acc, int steps, int64_t state_step, int64_t snap_step,
+                               hipStream_t st);
+hipError_t launch_advance_len(int32_t *len, const int32_t *n_acc, int steps, hipStream_t st);
 int sample_max_top_k();
 int sample_max_v();
 int penalty_max_v();
@@ -516,6 +520,29 @@ int ihip_tree_accept(const float *tgt_dev, const float *drf_dev, const int32_t *
     hipError_t e = launch_tree(tgt_dev, drf_dev, tok_dev, parent_dev, n, V, T, u_dev, part, out_path_dev,
                                out_len_dev, wsi, S(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_tree_accept");
+}
+
+int ihip_spec_commit_state(void *state_dev, const void *snap_dev, size_t bytes, int64_t snap_stride_bytes, int k,
+                           const int32_t *n_accepted_dev, int steps, int64_t state_step_bytes,
+                           int64_t snap_step_bytes, void *stream) {
+    if (!state_dev || !snap_dev || !n_accepted_dev) return fail(IHIP_EFAULT, "ihip_spec_commit_state: NULL pointer");
+    if (k < 0 || steps < 1 || bytes == 0 || (bytes & 3) || (snap_stride_bytes & 3) || (state_step_bytes & 3) ||
+        (snap_step_bytes & 3) || ((uintptr_t)state_dev & 3) || ((uintptr_t)snap_dev & 3))
+        return fail(IHIP_EINVAL, "ihip_spec_commit_state: sizes, strides and pointers must be multiples of 4 bytes "
+                                 "(k=%d steps=%d)", k, steps);
+    if ((k > 0 && snap_stride_bytes < (int64_t)bytes) || (steps > 1 && state_step_bytes < (int64_t)bytes) ||
+        (steps > 1 && snap_step_bytes < (int64_t)(k + 1) * snap_stride_bytes))
+        return fail(IHIP_EINVAL, "ihip_spec_commit_state: overlapping strides");
+    hipError_t e = launch_commit_state(state_dev, snap_dev, (int64_t)(bytes / 4), snap_stride_bytes / 4, k,
+                                       n_accepted_dev, steps, state_step_bytes / 4, snap_step_bytes / 4, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_spec_commit_state");
+}
+
+int ihip_spec_advance_len(int32_t *len_dev, const int32_t *n_accepted_dev, int steps, void *stream) {
+    if (!len_dev || !n_accepted_dev) return fail(IHIP_EFAULT, "ihip_spec_advance_len: NULL pointer");
+    if (steps < 1) return fail(IHIP_EINVAL, "ihip_spec_advance_len: steps=%d", steps);
+    hipError_t e = launch_advance_len(len_dev, n_accepted_dev, steps, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_spec_advance_len");
 }
 
 int ihip_sample(const float *logits_dev, int rows, int V, float T, int top_k, float top_p, float min_p,

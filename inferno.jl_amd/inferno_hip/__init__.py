@@ -12,7 +12,7 @@ from .quantized_kernels import (ACT_PLAIN, ACT_RMSNORM, ACT_SILU_MUL, GEMM_ACCUM
                                 mlp_forward_, mlp_ws_bytes, pack_weights, packed_bytes, q4_k_gemv_, q5_k_gemv_, q6_k_gemv_, q8_0_gemv_,
                                 quant_kernels_available, rmsnorm)
 from .sampler import apply_penalties_, softmax_sample
-from .speculative import (MODE_REFERENCE, MODE_STANDARD, SpeculativeStats, greedy_verify,
+from .speculative import (MODE_REFERENCE, MODE_STANDARD, SpeculativeStats, advance_len_, commit_state_, greedy_verify,
                           mtp_verify_step, softmax_stats, spec_accept, tree_accept)
 
 __all__ = [
@@ -21,5 +21,5 @@ __all__ = [
     "mlp_forward_", "mlp_ws_bytes", "pack_weights", "packed_bytes", "q4_k_gemv_", "q5_k_gemv_", "q6_k_gemv_", "q8_0_gemv_",
     "quant_kernels_available", "rmsnorm", "MODE_REFERENCE", "MODE_STANDARD", "SpeculativeStats",
     "greedy_verify", "mtp_verify_step", "softmax_stats", "spec_accept", "tree_accept",
-    "softmax_sample", "apply_penalties_",
+    "softmax_sample", "apply_penalties_", "commit_state_", "advance_len_",
 ]

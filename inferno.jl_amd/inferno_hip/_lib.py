@@ -46,6 +46,8 @@ SIGNATURES = {
     "ihip_spec_accept": (_i, [_vp, _vp, _vp, _i, _i, _i, _f, _vp, _vp, _vp, _i, _vp, _vp, _vp, _sz, _vp]),
     "ihip_greedy_verify": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _sz, _vp]),
     "ihip_tree_accept": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ihip_spec_commit_state": (_i, [_vp, _vp, _sz, _i64, _i, _vp, _i, _i64, _i64, _vp]),
+    "ihip_spec_advance_len": (_i, [_vp, _vp, _i, _vp]),
     "ihip_sample": (_i, [_vp, _i, _i, _f, _i, _f, _f, _vp, _vp, _vp]),
     "ihip_apply_penalties": (_i, [_vp, _i, _i, _vp, _i, _i64, _f, _f, _vp]),
     "ihip_gguf_open": (_i, [C.c_char_p, C.POINTER(_vp)]),

@@ -149,3 +149,26 @@ class SpeculativeStats:
                    if (self.draft_tokens_generated + self.tokens_generated) else 0.0)
         return {"acceptance_rate": rate, "draft_tokens_generated": self.draft_tokens_generated,
                 "tokens_accepted": self.tokens_accepted, "speedup_estimate": speedup}
+
+
+def commit_state_(state, snapshots, n_accepted, stream=None):
+    """After a verify step (no reference counterpart: src/SpeculativeDecoding.jl
+    :69-70 keeps none): state[s] = snapshots[s, n] for n = n_accepted[s] >= 0,
+    read on the device. state [steps, ...], snapshots [steps, k + 1, ...] of the
+    same dtype, contiguous; n_accepted int32 [steps] (out_n of spec_accept)."""
+    steps = state.shape[0]
+    k = snapshots.shape[1] - 1
+    per = state[0].numel() * state.element_size()
+    if snapshots.shape[0] != steps or snapshots[0, 0].numel() != state[0].numel() or not state.is_contiguous() \
+            or not snapshots.is_contiguous() or snapshots.dtype != state.dtype:
+        raise ValueError("snapshots must be [steps, k + 1, *state.shape[1:]] of the state's dtype")
+    _lib.check(_lib.load().ihip_spec_commit_state(_ptr(state), _ptr(snapshots), per, per, k, _ptr(n_accepted), steps,
+                                                  per, (k + 1) * per, _stream(stream)))
+    return state
+
+
+def advance_len_(lengths, n_accepted, stream=None):
+    """lengths[s] += n_accepted[s] + 1 where n_accepted[s] >= 0 (int32, on the device)."""
+    _lib.check(_lib.load().ihip_spec_advance_len(_ptr(lengths), _ptr(n_accepted), lengths.numel(),
+                                                 _stream(stream)))
+    return lengths

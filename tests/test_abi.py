@@ -124,3 +124,13 @@ def test_sampler_argument_checks(lib):
     assert lib.ihip_apply_penalties(None, 1, 8, p16, 1, 0, 0.5, 1.0, None) == -14
     assert lib.ihip_apply_penalties(p16, 1, 300000, p16, 1, 0, 0.5, 1.0, None) == -22
     assert lib.ihip_apply_penalties(p16, 2, 8, p16, 4, 2, 0.5, 1.0, None) == -22  # stride < n_tok
+
+
+def test_commit_state_argument_checks(lib):
+    buf = (C.c_uint8 * 64)()
+    p16 = (C.addressof(buf) + 15) & ~15
+    assert lib.ihip_spec_commit_state(None, p16, 16, 16, 4, p16, 1, 0, 0, None) == -14
+    assert lib.ihip_spec_commit_state(p16, p16, 6, 8, 4, p16, 1, 0, 0, None) == -22   # not whole words
+    assert lib.ihip_spec_commit_state(p16, p16, 16, 8, 4, p16, 1, 0, 0, None) == -22  # snapshot stride < bytes
+    assert lib.ihip_spec_advance_len(None, p16, 1, None) == -14
+    assert lib.ihip_spec_advance_len(p16, p16, 0, None) == -22

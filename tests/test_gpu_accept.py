@@ -167,3 +167,54 @@ def test_rmsnorm(ih):
     got = ih.rmsnorm(_dev(x)).cpu().numpy()
     ref = np.stack([O.rmsnorm(r) for r in x])
     assert rel_l2(got, ref) <= 1e-6
+
+
+def test_commit_state_and_advance_len(ih):
+    """The verify outcome applied on the device (no reference counterpart):
+    state[s] = snapshot n of step s, len[s] += n + 1, nothing for n = -1;
+    driven by a real accept's out_n inside a replayed HIP graph (no host
+    round trip)."""
+    import torch
+    steps, k, shape = 3, 4, (7, 33)
+    snaps = torch.randn(steps, k + 1, *shape, device="cuda")
+    state = torch.zeros(steps, *shape, device="cuda")
+    n = torch.tensor([2, -1, 4], dtype=torch.int32, device="cuda")
+    ih.commit_state_(state, snaps, n)
+    assert torch.equal(state[0], snaps[0, 2]) and torch.equal(state[2], snaps[2, 4])
+    assert torch.count_nonzero(state[1]) == 0
+    lens = torch.tensor([10, 20, 30], dtype=torch.int32, device="cuda")
+    ih.advance_len_(lens, n)
+    assert lens.tolist() == [13, 20, 35]
+    # inside a graph after a real accept
+    V = 1000
+    rng = np.random.default_rng(77)
+    Lt, Ld = _case(rng, steps, k, V, scale=3.0)
+    draft = np.array([[_draw(Ld[s, i], 1.0, rng.random()) for i in range(k)] for s in range(steps)], dtype=np.int32)
+    args = [_dev(Lt), _dev(Ld), _dev(draft), 1.0, _dev(rng.random((steps, k)).astype(np.float32)),
+            _dev(rng.random(steps).astype(np.float32)), _dev(rng.random(steps).astype(np.float32))]
+    out_tok = torch.zeros((steps, k + 1), dtype=torch.int32, device="cuda")
+    out_n = torch.zeros(steps, dtype=torch.int32, device="cuda")
+    state2 = torch.zeros_like(state)
+    lens2 = torch.zeros(steps, dtype=torch.int32, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+
+    def step():
+        ih.spec_accept(*args, out_tok=out_tok, out_n=out_n, stream=s)
+        ih.commit_state_(state2, snaps, out_n, stream=s)
+        ih.advance_len_(lens2, out_n, stream=s)
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.synchronize()
+    lens2.zero_()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step()
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+    nn = out_n.cpu().numpy()
+    for i in range(steps):
+        assert torch.equal(state2[i], snaps[i, nn[i]])
+    assert lens2.cpu().tolist() == [3 * (int(x) + 1) for x in nn]
