@@ -335,6 +335,46 @@ __device__ __forceinline__ constexpr int acc_token_u(int v) {
     return SPLIT ? (v >> 1) : v;
 }
 
+// RMSNorm row scales rs[t] = 1 / sqrt(sum_u ssq[u][t] / K + eps) from the
+// per-unit sums of squares the prep kernel left (1 without RMSNorm). The
+// BT threads of the workgroup split the units, P = BT / TOK threads per
+// token: issue() loads up to 4 units per thread (one round of independent
+// loads, issued before the weight prologue so the latter need not wait for
+// them), finish() adds a thread's units, then combines the P partial sums
+// of each token in LDS in a fixed order. Ends with a barrier.
+template <int TOK, int BT>
+struct RowScales {
+    static constexpr int P = BT / TOK;
+    float q[4];
+    __device__ __forceinline__ void issue(const float *__restrict__ ssq, int n_units, int tid) {
+        const int t = tid % TOK, part = tid / TOK;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int u = part + i * P;
+            q[i] = (ssq != nullptr && part < P && u < n_units) ? ssq[(size_t)u * TOK + t] : 0.f;
+        }
+    }
+    __device__ __forceinline__ void finish(const float *__restrict__ ssq, int n_units, int K, float eps, int tid,
+                                           float *rsp, float *rs) {
+        const int t = tid % TOK, part = tid / TOK;
+        float v = (q[0] + q[1]) + (q[2] + q[3]);
+        if (ssq != nullptr && part < P)
+            for (int u = part + 4 * P; u < n_units; u += P) v += ssq[(size_t)u * TOK + t];
+        rsp[tid] = v;
+        __syncthreads();
+        if (tid < TOK) {
+            float r = 1.0f;
+            if (ssq != nullptr) {
+                float sq = 0.f;
+                for (int i = 0; i < P; i++) sq += rsp[i * TOK + tid];
+                r = 1.0f / sqrtf(sq / (float)K + eps);
+            }
+            rs[tid] = r;
+        }
+        __syncthreads();
+    }
+};
+
 template <int QT, int MT, bool SPLIT>
 __device__ __forceinline__ void compute_unit(const Unit<QT> &r, const uint8_t *a_lane, const float *x_lds,
                                              const float *i_lds, int g, Acc<MT, SPLIT> &A) {
@@ -731,6 +771,7 @@ void gemm_q_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     float *x_lds = (float *)(smem + (size_t)ups * UNIT_A);      // [ups][8][TOK]
     float *i_lds = x_lds + (C::MINS ? ups * 8 * TOK : 0);       // [ups][TOK]
     __shared__ float rs[TOK];                                   // RMSNorm row scales
+    __shared__ float rsp[WG_THREADS];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n_in = lane & 15, g = lane >> 4;
@@ -791,16 +832,11 @@ void gemm_q_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
         i_lds[min(tid, n_i - 1)] = i_tmp;
         for (int i = WG_THREADS + tid; i < n_i; i += WG_THREADS) i_lds[i] = i_src[i];
     }
-    if (tid < TOK) {
-        float r = 1.0f;
-        if (ssq != nullptr) {
-            float sq = 0.f;
-            for (int u = 0; u < n_units; u++) sq += ssq[(size_t)u * TOK + tid];
-            r = 1.0f / sqrtf(sq / (float)K + eps);
-        }
-        rs[tid] = r;
+    {
+        RowScales<TOK, WG_THREADS> rsc;
+        rsc.issue(ssq, n_units, tid);
+        rsc.finish(ssq, n_units, K, eps, tid, rsp, rs);
     }
-    __syncthreads();
 
     // 4. stream items through the MFMA pipe; a row group's epilogue follows
     //    its last unit
@@ -1036,6 +1072,7 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     constexpr int F = (QT == QT_Q6_K || MT > 1) ? 1 : (TPL == 4) ? NW / 2 : NW;
     __shared__ __align__(16) float red[2][F][NW][64][TPL * MT];
     __shared__ float rs[TOK];  // RMSNorm row scales (1 without RMSNorm)
+    __shared__ float rsp[NW * 64];
 
     const int n_units = (K + UNIT - 1) / UNIT;
     const int n_tiles = (N + 15) / 16;
@@ -1108,19 +1145,16 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
                           b);
         }
     };
+    RowScales<TOK, NW * 64> rsc;
+    rsc.issue(ssq, n_units, tid);
+    __builtin_amdgcn_sched_barrier(0);
     Unit<QT> buf[R];
 #pragma unroll
-    for (int p = 0; p < R - 1; p++) load_item(p / UPS, p % UPS, buf[p]);
-    if (tid < TOK) {
-        float r = 1.0f;
-        if (ssq != nullptr) {
-            float sq = 0.f;
-            for (int u = 0; u < n_units; u++) sq += ssq[(size_t)u * TOK + tid];
-            r = 1.0f / sqrtf(sq / (float)K + eps);
-        }
-        rs[tid] = r;
+    for (int p = 0; p < R - 1; p++) {
+        load_item(p / UPS, p % UPS, buf[p]);
+        __builtin_amdgcn_sched_barrier(0);  // ring slots fill in order
     }
-    __syncthreads();
+    rsc.finish(ssq, n_units, K, eps, tid, rsp, rs);
 
     f4 acc[MT], macc[MT];
 #pragma unroll
@@ -1191,6 +1225,298 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     }
 }
 
+// ---------------------------------------------------------------- tall kernel
+// One unit of one tile against MT register token tiles, finished: vals[mt *
+// TPL + k] is the unit's contribution to token lane_token(mt, g, k) of row n
+// (before the RMSNorm row scale).
+//  Q4_K/Q5_K: inv * (d * (sc q . x) - 32 dmin * (m . X/32)), the 6-bit scales
+//             folded into B exactly as in compute_v.
+//  Q6_K, half mode: the int8 sub-block scale is folded into the fp16 weight
+//             operand, B = fp16(sc * q) (|sc q| <= 4096, one rounding, the
+//             same order of error as the fp16 activations), so the 16 MFMAs
+//             of a unit chain in one accumulator per tile and d * inv is
+//             applied once: 2 VALU ops per weight pair instead of an fp32
+//             fma per sub-block, tile and output.
+//  Q8_0 and fp32-accurate Q6_K: per-chunk fp32 scaling (compute_v).
+template <int QT, bool SPLIT, int MT>
+__device__ __forceinline__ void unit_vals(const Unit<QT> &r, const AReg<QT> (&a)[MT],
+                                          const float (&inv)[MT][SPLIT ? 2 : 4], int g, bool live,
+                                          float (&vals)[MT * (SPLIT ? 2 : 4)]) {
+    constexpr int TPL = SPLIT ? 2 : 4;
+    if constexpr (QT == QT_Q6_K && !SPLIT) {
+        const float d = live ? half_bits(r.d) : 0.f;
+        // the 16 scales as exact fp16: (1024 + (sc ^ 0x80)) - 1152 = sc
+        const uint32_t scw[4] = {r.sc.x ^ 0x80808080u, r.sc.y ^ 0x80808080u, r.sc.z ^ 0x80808080u,
+                                 r.sc.w ^ 0x80808080u};
+        const h2 off_sc = as_h2(0xE480E480u);
+        h2 sch[8];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            sch[2 * w] = as_h2(pair_lo(scw[w])) + off_sc;
+            sch[2 * w + 1] = as_h2(pair_hi(scw[w])) + off_sc;
+        }
+        f4 c[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) c[mt] = f4{0.f, 0.f, 0.f, 0.f};
+        const h2 off = as_h2(0xE420E420u);  // (1024 + q) - 1056 = q - 32
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int n = i >> 1, h = i & 1;
+            uint32_t q[4];
+            q[0] = (r.a[i] & 0x0f0f0f0fu) | ((r.h[i] & 0x03030303u) << 4);
+            q[1] = (r.b[i] & 0x0f0f0f0fu) | (((r.h[i] >> 2) & 0x03030303u) << 4);
+            q[2] = ((r.a[i] >> 4) & 0x0f0f0f0fu) | (((r.h[i] >> 4) & 0x03030303u) << 4);
+            q[3] = ((r.b[i] >> 4) & 0x0f0f0f0fu) | (((r.h[i] >> 6) & 0x03030303u) << 4);
+#pragma unroll
+            for (int qq = 0; qq < 4; qq++) {
+                const int s = 8 * n + 2 * qq + h;
+                const _Float16 sv = sch[s >> 1][s & 1];
+                const h2 ss = {sv, sv};
+                const h2 p0 = (as_h2(pair_lo(q[qq])) + off) * ss, p1 = (as_h2(pair_hi(q[qq])) + off) * ss;
+                h4 b;
+                b[0] = p0[0]; b[1] = p0[1]; b[2] = p1[0]; b[3] = p1[1];
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) c[mt] = mfma16(a[mt].f[s], b, c[mt]);
+            }
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) vals[mt * 4 + k] = (d * inv[mt][k]) * c[mt][k];
+    } else if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {
+        float d = half_bits(r.hdr.x), dmin = half_bits(r.hdr.x >> 16);
+        if (!live) { d = 0.f; dmin = 0.f; }
+        const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;
+        const uint32_t sc_lo = s0 & 0x3f3f3f3fu, m_lo = s1 & 0x3f3f3f3fu;
+        const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
+        const uint32_t m_hi = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
+        const int sh = 16 * (g >> 1);
+        const h2 neg1024 = as_h2(0xE400E400u);
+        h2 hs[4], ns[4];
+        hs[0] = h2_of_small((sc_lo >> sh) & 0xffu);
+        hs[1] = h2_of_small((sc_lo >> (sh + 8)) & 0xffu);
+        hs[2] = h2_of_small((sc_hi >> sh) & 0xffu);
+        hs[3] = h2_of_small((sc_hi >> (sh + 8)) & 0xffu);
+#pragma unroll
+        for (int i = 0; i < 4; i++) ns[i] = hs[i] * neg1024;
+        f4 c[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) c[mt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            const int ah = m >> 2, b = (m >> 1) & 1, hw = m & 1;
+            const uint4 Q = ah ? r.q1 : r.q0;
+            const uint32_t x0 = hw ? Q.z : Q.x, x1 = hw ? Q.w : Q.y;
+            uint32_t n0 = (b ? (x0 >> 4) : x0) & 0x0f0f0f0fu;
+            uint32_t n1 = (b ? (x1 >> 4) : x1) & 0x0f0f0f0fu;
+            if constexpr (QT == QT_Q5_K) {
+                const int hb = 4 * ah + 2 * (g >> 1) + b;
+                const uint32_t h0 = hw ? r.qh.z : r.qh.x, h1 = hw ? r.qh.w : r.qh.y;
+                n0 |= ((h0 >> hb) & 0x01010101u) << 4;
+                n1 |= ((h1 >> hb) & 0x01010101u) << 4;
+            }
+            const h8 bf = b_frag_scaled(n0, n1, hs[2 * ah + b], ns[2 * ah + b]);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) c[mt] = mfma32(a[mt].f[m], bf, c[mt]);
+        }
+        const uint32_t mw = g == 0 ? m_lo : (g == 1 ? m_hi : 0u);
+        const h2 p0 = as_h2(pair_lo(mw)) + neg1024, p1 = as_h2(pair_hi(mw)) + neg1024;
+        h4 bm;
+        bm[0] = p0[0]; bm[1] = p0[1]; bm[2] = p1[0]; bm[3] = p1[1];
+        const float dm32 = -32.0f * dmin;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const f4 cm = mfma16(a[mt].mins, bm, f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int k = 0; k < TPL; k++) {
+                const float s = SPLIT ? c[mt][2 * k] + c[mt][2 * k + 1] : c[mt][k];
+                const float sm = SPLIT ? cm[2 * k] + cm[2 * k + 1] : cm[k];
+                vals[mt * TPL + k] = inv[mt][k] * __builtin_fmaf(dm32, sm, d * s);
+            }
+        }
+    } else {
+        f4 acc[MT], macc[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[mt] = macc[mt] = f4{0.f, 0.f, 0.f, 0.f};
+        compute_v<QT, SPLIT, MT>(r, a, inv, g, live, acc, macc);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int k = 0; k < TPL; k++) vals[mt * TPL + k] = SPLIT ? acc[mt][2 * k] + acc[mt][2 * k + 1] : acc[mt][k];
+    }
+}
+
+// Several token tiles (M up to 32 fp32-accurate, 64 half): one wave per
+// SIMD, each wave holding one 256-element unit of the A operand for all MT
+// tiles in registers, so a dequantized weight fragment feeds MT MFMAs. A
+// workgroup covers 4 units (one K-slice, grid.y) of every G-th 16-row tile
+// (grid.x). Per tile the four waves' unit results meet in LDS; they are
+// gathered in batches of F = 4 tiles (double-buffered, one barrier per
+// batch) and wave i sums tile i of the batch in wave order, so every wave
+// does the same reduction work. Weight items stream through an 8-deep
+// register ring. Results go out with bounds-checked buffer stores (no
+// branches, no read-modify-write in the loop): to the K-slice's partials
+// when part is set (the caller reduces or folds them), else to Y.
+template <int QT, bool SPLIT, bool PK, int MT>
+__global__ __launch_bounds__(256, 1)
+void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, int N, int K,
+                   const uint8_t *__restrict__ afrag, const float *__restrict__ invs,
+                   const uint8_t *__restrict__ mfrag, const float *__restrict__ ssq, float eps,
+                   float *__restrict__ part) {
+    using C = GemmCfg<QT>;
+    constexpr int NW = 4;
+    constexpr int TOKT = SPLIT ? 8 : 16;
+    constexpr int TOK = MT * TOKT;
+    constexpr int TPL = SPLIT ? 2 : 4;
+    constexpr int NV = MT * TPL;           // results per lane and tile
+    constexpr int NVP = (NV + 3) & ~3;     // (padded to whole 16-byte LDS accesses)
+    constexpr int UNIT_BYTES = (QT == QT_Q8_0) ? 8 * 34 : C::BB;
+    // ring depth: 8 items where the registers allow it (Q8_0 items and the
+    // fp32-accurate Q6_K operands of 3-4 tiles are larger)
+    constexpr int R = (QT == QT_Q8_0 || (QT == QT_Q6_K && SPLIT && MT >= 3)) ? 4 : 8;
+    constexpr int F = 4;
+    static_assert(R % F == 0, "a ring pass holds whole reduction batches");
+    __shared__ __align__(16) float red[2][F][NW][64][NVP];
+    __shared__ float rs[TOK];
+    __shared__ float rsp[NW * 64];
+
+    const int n_units = (K + UNIT - 1) / UNIT;
+    const int n_tiles = (N + 15) / 16;
+    const int G = gridDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n_in = lane & 15, g = lane >> 4;
+    const int my_tiles = (n_tiles - 1 - (int)blockIdx.x) / G + 1;  // the plan keeps G <= n_tiles
+    const int unit = (int)blockIdx.y * NW + wave;
+    const bool live = unit < n_units;
+    const int un = min(unit, n_units - 1);
+    const size_t row_bytes = (size_t)(K / C::QK) * C::BB;
+    const int tail_blk = (QT == QT_Q8_0 && (K % UNIT)) ? (K % UNIT) / 32 : 8;
+
+    // 1. this wave's A operand (MFMA lane layout: entry (chunk c, tile mt) at
+    //    (c MT + mt) 64 + lane); slots of padding tokens are zero, not fetched
+    AReg<QT> a[MT];
+    float inv[MT][TPL];
+    {
+        const uint8_t *src = afrag + (size_t)un * UNIT_A1 * MT;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            if ((SPLIT ? (n_in >> 1) : n_in) + mt * TOKT < M) {
+                if constexpr (QT == QT_Q6_K) {
+#pragma unroll
+                    for (int c = 0; c < 16; c++) a[mt].f[c] = *(const h4 *)(src + ((c * MT + mt) * 64 + lane) * 8);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 8; c++) a[mt].f[c] = *(const h8 *)(src + ((c * MT + mt) * 64 + lane) * 16);
+                }
+                if constexpr (C::MINS) a[mt].mins = *(const h4 *)(mfrag + ((size_t)un * MT + mt) * 512 + lane * 8);
+            } else {
+                if constexpr (QT == QT_Q6_K) {
+#pragma unroll
+                    for (int c = 0; c < 16; c++) a[mt].f[c] = h4{};
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 8; c++) a[mt].f[c] = h8{};
+                }
+                if constexpr (C::MINS) a[mt].mins = h4{};
+            }
+#pragma unroll
+            for (int k = 0; k < TPL; k++) inv[mt][k] = invs[(size_t)un * TOK + lane_token<SPLIT>(mt, g, k)];
+        }
+    }
+
+    // 2. weight stream over this workgroup's tiles; past the last tile the
+    //    loads repeat it so every ring step issues one item
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(W), (short)0, (int)(PK ? (uint32_t)n_tiles * n_units * Packed<QT>::CHUNK : 0u),
+        0x00020000);
+    auto load_item = [&](int j, Unit<QT> &b) {
+        j = min(j, my_tiles - 1);
+        if constexpr (PK) {
+            const int tile = (int)blockIdx.x + G * j;
+            if constexpr (QT == QT_Q6_K)
+                load_unit_packed<QT>(W + ((size_t)tile * n_units + un) * Packed<QT>::CHUNK, lane, b);
+            else
+                load_unit_buf<QT>(wrs, (tile * n_units + un) * Packed<QT>::CHUNK, lane, b);
+        } else {
+            const int row = min(((int)blockIdx.x + G * j) * 16 + n_in, N - 1);
+            load_unit<QT>(W + (size_t)row * row_bytes + (size_t)un * UNIT_BYTES, g, un == n_units - 1 ? tail_blk : 8,
+                          b);
+        }
+    };
+    RowScales<TOK, NW * 64> rsc;
+    rsc.issue(ssq, n_units, tid);
+    __builtin_amdgcn_sched_barrier(0);
+    Unit<QT> buf[R];
+#pragma unroll
+    for (int p = 0; p < R - 1; p++) {
+        load_item(p, buf[p]);
+        __builtin_amdgcn_sched_barrier(0);  // ring slots fill in order
+    }
+    // output: element (t, r) at byte 4 (t N + r) of this K-slice's [M x N]
+    // block, the token's tile part in the scalar offset, the lane part (row
+    // r, token base tb) in the vector offset; tokens at or past M land at or
+    // past the resource's size, and padding rows get an offset past it, so
+    // those stores are dropped
+    float *dst = part != nullptr ? part + (size_t)blockIdx.y * M * N : Y;
+    const uint32_t out_bytes = (uint32_t)((size_t)M * N * 4);
+    const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(dst, (short)0, (int)out_bytes, 0x00020000);
+    const int tb = lane_token<SPLIT>(0, g, 0);
+    rsc.finish(ssq, n_units, K, eps, tid, rsp, rs);
+
+    // flush (a batch is complete): wave i sums tile i of the batch in wave
+    // order and stores it
+    auto consume = [&](int j, int jb, bool flush, Unit<QT> &b) {
+        if constexpr (!PK) finish_unit<QT>(b);
+        float vals[NVP];
+        unit_vals<QT, SPLIT, MT>(b, a, inv, g, live, *(float(*)[NV])vals);
+#pragma unroll
+        for (int k = NV; k < NVP; k++) vals[k] = 0.f;
+        const int hb = (j / F) & 1;
+        float *slot = &red[hb][jb][wave][lane][0];
+#pragma unroll
+        for (int k = 0; k < NVP; k += 4) *(f4 *)(slot + k) = f4{vals[k], vals[k + 1], vals[k + 2], vals[k + 3]};
+        if (flush) {
+            __syncthreads();
+            if (wave <= jb) {
+                float sum[NVP];
+#pragma unroll
+                for (int k = 0; k < NVP; k += 4) {
+                    const f4 v = *(const f4 *)&red[hb][wave][0][lane][k];
+                    sum[k] = v[0]; sum[k + 1] = v[1]; sum[k + 2] = v[2]; sum[k + 3] = v[3];
+                }
+#pragma unroll
+                for (int w = 1; w < NW; w++)
+#pragma unroll
+                    for (int k = 0; k < NVP; k += 4) {
+                        const f4 v = *(const f4 *)&red[hb][wave][w][lane][k];
+                        sum[k] += v[0]; sum[k + 1] += v[1]; sum[k + 2] += v[2]; sum[k + 3] += v[3];
+                    }
+                const int r = ((int)blockIdx.x + G * (j - jb + wave)) * 16 + n_in;
+                const uint32_t voff = r < N ? (uint32_t)(tb * N + r) * 4u : 0x80000000u;
+#pragma unroll
+                for (int k = 0; k < NV; k++) {
+                    const int tk = lane_token<SPLIT>(k / TPL, 0, k % TPL);
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum[k] * rs[tb + tk]), ors,
+                                                          (int)voff, tk * N * 4, 0);
+                }
+            }
+        }
+    };
+    // whole ring passes: every R-th item completes a batch at a fixed ring
+    // position (straight-line code); the last partial pass checks the end
+    const int n_full = my_tiles - my_tiles % R;
+    for (int ib = 0; ib < n_full; ib += R) {
+#pragma unroll
+        for (int p = 0; p < R; p++) {
+            load_item(ib + p + R - 1, buf[(p + R - 1) % R]);
+            consume(ib + p, p % F, p % F == F - 1, buf[p]);
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < R - 1; p++)
+        if (n_full + p < my_tiles) consume(n_full + p, p % F, p % F == F - 1 || n_full + p == my_tiles - 1, buf[p]);
+}
+
 // Prepared-activation workspace (shared by both kernels): the A operand,
 // the Q4_K/Q5_K sub-block sums (LDS kernel) or min-term operand (streaming
 // kernel), the inverse unit scales and the RMSNorm partial sums.
@@ -1222,6 +1548,24 @@ hipError_t launch_v(const uint8_t *W, const float *X, const ActIn &in, float *Y,
         (S > 1 || in.defer) ? part : nullptr);
     e = hipGetLastError();
     if (e != hipSuccess || S == 1 || in.defer) return e;
+    const int64_t MN = (int64_t)M * N;
+    reduce_kernel<<<(unsigned)((MN + 1023) / 1024), 256, 0, st>>>(part, Y, S, MN, accum);
+    return hipGetLastError();
+}
+
+template <int QT, bool SPLIT, bool PK, int MT>
+hipError_t launch_w(const uint8_t *W, const float *X, const ActIn &in, float *Y, int M, int N, int K, int S, int G,
+                    int accum, const ActWs &a, float *part, hipStream_t st) {
+    hipError_t e;
+    if (!in.reuse && (e = launch_prep<QT, MT, SPLIT>(X, in, M, K, a, st)) != hipSuccess) return e;
+    // several K-slices, accumulation and deferral all go through the
+    // partials (the kernel itself never reads its output)
+    const bool via_part = S > 1 || accum || in.defer;
+    gemm_w_kernel<QT, SPLIT, PK, MT><<<dim3(G, S), 256, 0, st>>>(
+        W, Y, M, N, K, a.afrag, a.inv, a.mfrag, in.op == ACT_RMSNORM ? a.ssq : nullptr, in.eps,
+        via_part ? part : nullptr);
+    e = hipGetLastError();
+    if (e != hipSuccess || !via_part || in.defer) return e;
     const int64_t MN = (int64_t)M * N;
     reduce_kernel<<<(unsigned)((MN + 1023) / 1024), 256, 0, st>>>(part, Y, S, MN, accum);
     return hipGetLastError();
@@ -1378,6 +1722,14 @@ static hipError_t dispatch_mt(const GemmPlan &p, const uint8_t *W, const float *
                   p.stream ? ws + p.off_mfrag : nullptr, (float *)(ws + p.off_ssq)};
     float *part = (float *)(ws + p.off_part);
     if (p.stream && p.MT > 1) {
+        // (IHIP_TALL=0: the per-tile-barrier variant of the streaming kernel)
+        static const int tall = env_int("IHIP_TALL", 1);
+        if (tall && (size_t)p.MT * 16 * N * 4 < ((size_t)1 << 31)) {
+#define WM(mt) return p.split ? launch_w<QT, true, PK, mt>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st) \
+                              : launch_w<QT, false, PK, mt>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
+            switch (p.MT) { case 2: WM(2); case 3: WM(3); default: WM(4); }
+#undef WM
+        }
 #define VM(mt) return p.split ? launch_v<QT, 4, 1, true, PK, mt>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st) \
                               : launch_v<QT, 4, 1, false, PK, mt>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
         switch (p.MT) { case 2: VM(2); case 3: VM(3); default: VM(4); }

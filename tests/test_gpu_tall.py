@@ -1,0 +1,103 @@
+"""GPU: the several-token-tile matmul (M = 16..64 half precision, 9..32
+fp32-accurate) against the oracle's fp64 product of the dequantized weights
+(dequant formulas of src/QuantizedKernels.jl:55-190 for the K-quants and
+Q8_0). Shapes hit the edges of that kernel: rows past N inside the last
+16-row tile, tokens past M inside the last token tile, one K-slice and
+several, accumulation and deferred partials (both through the K-slice
+partial buffer), and the RMSNorm input stage."""
+import numpy as np
+import pytest
+
+from _util import rel_l2
+
+import oracle as O
+from inferno_hip import formats as F
+from inferno_hip import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL_HALF = 1e-2  # north-star bar for the half-precision MFMA path
+SANITY_HALF = 2e-3  # fp16 operands land near 4e-4; a dropped term or index lands far above
+TOL_F32 = 1e-5
+
+
+@pytest.fixture(scope="module")
+def ih():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import inferno_hip
+    assert inferno_hip.quant_kernels_available(), inferno_hip._lib.last_error()
+    return inferno_hip
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("qt", F.QTYPES)
+@pytest.mark.parametrize("K", [768, 2560])  # 3 units (one K-slice), 10 units (three)
+def test_tall_half(ih, qt, K):
+    import torch
+    N = 200  # 12.5 tiles: the last tile has 8 padding rows
+    rng = np.random.default_rng(K + 11 * qt)
+    w = synth.matrix(qt, N, K, synth.stream_for(N + K, f"tall{qt}"))
+    wp = ih.pack_weights(qt, _dev(w), N, K)
+    fl = ih.GEMM_HALF | ih.GEMM_PACKED
+    for M in (16, 37, 64):
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        ref = O.gemv_f64(qt, w, x, M, N, K)
+        got = ih.gemm_q(qt, wp, _dev(x), N, K, flags=fl).cpu().numpy()
+        err = rel_l2(got, ref)
+        print(f"{F.NAMES[qt]} K={K} M={M} half rel-L2={err:.3e}", flush=True)
+        assert err <= TOL_HALF and err <= SANITY_HALF, (M, err)
+        y0 = torch.randn(M, N, device="cuda")
+        y = y0.clone()
+        ih.gemm_q(qt, wp, _dev(x), N, K, flags=fl | ih.GEMM_ACCUM, out=y)
+        assert rel_l2((y - y0).cpu().numpy(), ref) <= SANITY_HALF, M
+
+
+@pytest.mark.parametrize("qt", [F.Q4_K, F.Q6_K])
+def test_tall_fp32_accurate(ih, qt):
+    N, K = 144, 1536
+    rng = np.random.default_rng(3 + qt)
+    w = synth.matrix(qt, N, K, synth.stream_for(21, f"tallf{qt}"))
+    wp = ih.pack_weights(qt, _dev(w), N, K)
+    for M in (9, 24, 32):
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        got = ih.gemm_q(qt, wp, _dev(x), N, K, flags=ih.GEMM_F32 | ih.GEMM_PACKED).cpu().numpy()
+        err = rel_l2(got, O.gemv_f64(qt, w, x, M, N, K))
+        print(f"{F.NAMES[qt]} M={M} f32 rel-L2={err:.3e}", flush=True)
+        assert err <= TOL_F32, (M, err)
+
+
+def test_tall_rmsnorm_and_fold(ih):
+    """RMSNorm input stage at M = 64, and a deferred Q6_K down projection
+    (4 K-slices) folded into the next matmul's input stage: equal bit for bit
+    to accumulate-then-matmul, and to the oracle's float64 sequence."""
+    import torch
+    H, FF, N2, M = 512, 4096, 96, 64
+    rng = np.random.default_rng(64)
+    wd = synth.matrix(F.Q6_K, H, FF, synth.stream_for(3, "tall_down"))
+    w2 = synth.matrix(F.Q4_K, N2, H, synth.stream_for(4, "tall_next"))
+    pd, p2 = ih.pack_weights(F.Q6_K, _dev(wd), H, FF), ih.pack_weights(F.Q4_K, _dev(w2), N2, H)
+    fl = ih.GEMM_HALF | ih.GEMM_PACKED
+    nw = (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    h = _dev(rng.standard_normal((M, FF)).astype(np.float32))
+    x0 = _dev((2.0 * rng.standard_normal((M, H))).astype(np.float32))
+    xr = x0.clone()
+    ih.gemm_q(F.Q6_K, pd, h, H, FF, flags=fl | ih.GEMM_ACCUM, out=xr)
+    yr = ih.gemm_q_ex(F.Q4_K, p2, xr, N2, H, act=ih.ACT_RMSNORM, norm_w=_dev(nw), flags=fl)
+    ws = torch.empty(ih.quantized_kernels.gemm_ws_bytes(F.Q6_K, M, H, FF, fl), dtype=torch.uint8, device="cuda")
+    ih.gemm_q_ex(F.Q6_K, pd, h, H, FF, flags=fl | ih.GEMM_DEFER, ws=ws)
+    parts = ih.gemm_partials(F.Q6_K, M, H, FF, fl, ws)
+    assert parts[1] >= 2
+    xf = x0.clone()
+    yf = ih.gemm_q_ex(F.Q4_K, p2, xf, N2, H, act=ih.ACT_RMSNORM, norm_w=_dev(nw), flags=fl, add=parts)
+    assert torch.equal(xf, xr)
+    assert torch.equal(yf, yr)
+    xref = O.gemv_f64(F.Q6_K, wd, h.cpu().numpy(), M, H, FF) + x0.cpu().numpy()
+    assert rel_l2(xf.cpu().numpy(), xref) <= SANITY_HALF
+    n = np.stack([O.rmsnorm(r, 1e-6, nw) for r in xf.cpu().numpy()]).astype(np.float32)
+    assert rel_l2(yf.cpu().numpy(), O.gemv_f64(F.Q4_K, w2, n, M, N2, H)) <= SANITY_HALF
