@@ -111,6 +111,7 @@ class VerifyStep:
                   gws(F.Q4_K, M, 2 * FF, H, fl), gws(F.Q6_K, M, H, FF, fl), gws(F.Q6_K, M, VOCAB, H, fl))
         self.ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
         self.ws_down = torch.empty(wsb, dtype=torch.uint8, device=dev)  # holds the deferred down partials
+        self.ws_o = torch.empty(wsb, dtype=torch.uint8, device=dev)  # the deferred o partials (when K-sliced)
         # draft side (inputs of the verify step): draft logits, draft tokens, uniforms
         noise = ih.quantized_kernels.synth_gaussian(st(SEED, "draft_logits"), k * VOCAB, 3.0).view(k, VOCAB)
         self.drf = noise.contiguous()
@@ -141,15 +142,29 @@ class VerifyStep:
         ex = ih.gemm_q_ex
         f32 = self.prec | ih.GEMM_PACKED  # (GEMM_F32, or 0: fp32-accurate below 16 tokens, half above)
         acc = f32 | ih.GEMM_ACCUM
+        dfr = f32 | ih.GEMM_DEFER
         parts = ih.gemm_partials(F.Q6_K, M, H, FF, f32, self.ws_down)
+        # K-sliced o and [gate; up] (several token tiles) leave their partials
+        # to the next input stage instead of a reduce launch
+        o_parts = ih.gemm_partials(F.Q4_K, M, H, NQ, f32, self.ws_o)
+        gu_parts = ih.gemm_partials(F.Q4_K, M, 2 * FF, H, f32, self.ws)
+        fold_o, fold_gu = o_parts[1] > 1, gu_parts[1] > 1
         self.x.copy_(self.x0)
         for i, lw in enumerate(self.model.layers):
             ex(F.Q4_K, lw["qkv"], self.x, NQ + 2 * NKV, H, act=ih.ACT_RMSNORM, norm_w=lw["attn_norm"], flags=f32,
                out=self.qkv, ws=self.ws, add=parts if i > 0 else None)
-            ex(F.Q4_K, lw["o"], self.qkv[:, :NQ], H, NQ, flags=acc, out=self.x, ws=self.ws)
-            ex(F.Q4_K, lw["gu"], self.x, 2 * FF, H, act=ih.ACT_RMSNORM, norm_w=lw["ffn_norm"], flags=f32,
-               out=self.gu, ws=self.ws)
-            ex(F.Q6_K, lw["down"], self.gu, H, FF, act=ih.ACT_SILU_MUL, flags=f32 | ih.GEMM_DEFER, ws=self.ws_down)
+            if fold_o:
+                ex(F.Q4_K, lw["o"], self.qkv[:, :NQ], H, NQ, flags=dfr, ws=self.ws_o)
+            else:
+                ex(F.Q4_K, lw["o"], self.qkv[:, :NQ], H, NQ, flags=acc, out=self.x, ws=self.ws)
+            ex(F.Q4_K, lw["gu"], self.x, 2 * FF, H, act=ih.ACT_RMSNORM, norm_w=lw["ffn_norm"],
+               flags=dfr if fold_gu else f32, out=None if fold_gu else self.gu, ws=self.ws,
+               add=o_parts if fold_o else None)
+            if fold_gu:
+                ex(F.Q6_K, lw["down"], None, H, FF, act=ih.ACT_SILU_MUL, flags=dfr, ws=self.ws_down, add=gu_parts,
+                   m=M, ldx=2 * FF)
+            else:
+                ex(F.Q6_K, lw["down"], self.gu, H, FF, act=ih.ACT_SILU_MUL, flags=dfr, ws=self.ws_down)
         ex(F.Q6_K, self.model.lm, self.x, VOCAB, H, act=ih.ACT_RMSNORM, norm_w=self.model.out_norm, flags=f32,
            out=self.logits, ws=self.ws, add=parts)
 

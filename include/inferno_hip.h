@@ -130,12 +130,18 @@ int ihip_gemm_q(int qtype, const void *w_dev, const float *x_dev, float *y_dev,
  * adds its partials need separate workspaces. */
 #define IHIP_GEMM_DEFER 32
 typedef struct ihip_gemm_input {
-    const float *x;        /* activations (written back when add != NULL) */
+    const float *x;        /* activations (written back when add != NULL), or
+                              NULL when the add slices are the input */
     int ldx;
     int act;               /* IHIP_ACT_* */
     const float *norm_w;   /* RMSNorm weight [K] or NULL */
     float eps;
-    const float *add;      /* NULL or n_add slices folded into x first */
+    const float *add;      /* NULL or n_add slices: with x, [M x K] slices
+                              folded into x first (x += sum, stored back);
+                              without x, [M x ldx] slices whose sum is the
+                              input (e.g. the deferred [gate | up] product
+                              feeding IHIP_ACT_SILU_MUL). Summed in slice
+                              order, as the reduce of a non-deferred call. */
     int n_add;
     int64_t add_stride;
 } ihip_gemm_input;

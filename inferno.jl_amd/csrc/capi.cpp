@@ -294,7 +294,10 @@ int ihip_gemm_q_ex(int qtype, const void *w_dev, const ihip_gemm_input *in, floa
     if (!in) return fail(IHIP_EFAULT, "ihip_gemm_q_ex: NULL input descriptor");
     const int base = flags & ~(IHIP_GEMM_REUSE | IHIP_GEMM_DEFER);
     const bool defer = flags & IHIP_GEMM_DEFER;
-    int rc = check_gemm(qtype, w_dev, in->x, defer ? const_cast<float *>(in->x) : y_dev, M, N, K, base);
+    // x absent: the input is the sum of the add slices themselves
+    if (!in->x && !in->add) return fail(IHIP_EFAULT, "ihip_gemm_q_ex: NULL x without add slices");
+    const float *xin = in->x ? in->x : in->add;
+    int rc = check_gemm(qtype, w_dev, xin, defer ? const_cast<float *>(xin) : y_dev, M, N, K, base);
     if (rc != IHIP_OK) return rc;
     const int act = in->act;
     if (act < IHIP_ACT_PLAIN || act > IHIP_ACT_SILU_MUL) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: act=%d", act);
@@ -305,10 +308,12 @@ int ihip_gemm_q_ex(int qtype, const void *w_dev, const ihip_gemm_input *in, floa
     if (act == IHIP_ACT_RMSNORM && !(in->eps >= 0.f)) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: eps=%g", in->eps);
     if (in->norm_w && !aligned16(in->norm_w)) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: norm_w must be 16-byte aligned");
     if (in->add) {
-        if (in->n_add < 1 || in->add_stride < (int64_t)M * K || (in->add_stride & 3) || !aligned16(in->add))
+        const int64_t slice = (int64_t)M * (in->x ? K : in->ldx);
+        if (in->n_add < 1 || in->add_stride < slice || (in->add_stride & 3) || !aligned16(in->add))
             return fail(IHIP_EINVAL, "ihip_gemm_q_ex: add slices n=%d stride=%lld", in->n_add,
                         (long long)in->add_stride);
-        if (act == IHIP_ACT_SILU_MUL) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: add with SILU_MUL");
+        if (act == IHIP_ACT_SILU_MUL && in->x)
+            return fail(IHIP_EINVAL, "ihip_gemm_q_ex: add with SILU_MUL needs x = NULL (the slices are the input)");
         if (flags & IHIP_GEMM_REUSE) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: add with IHIP_GEMM_REUSE");
     }
     if ((flags & (IHIP_GEMM_REUSE | IHIP_GEMM_DEFER)) && !gemm_reuse_ok(M, base))

@@ -682,7 +682,9 @@ __device__ __forceinline__ void prep_finish(float (&v)[8], float4 wa, float4 wb,
 
 // add != nullptr: x[t][k] += ((add_0 + add_1) + ...)[t][k] (the K-slice
 // partials of a previous matmul, the order its reduce would use), stored back
-// into x (each element has one owner thread), before the transform.
+// into x (each element has one owner thread), before the transform; slices
+// [M][K]. X == nullptr: x is that sum itself (slices [M][ldx], rows of 2K
+// for ACT_SILU_MUL), nothing is stored back.
 template <int LK, int MT, bool SPLIT, bool MINS>
 __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ X, int ldx, int M, int K, int op,
                                                    const float *__restrict__ norm_w,
@@ -698,33 +700,46 @@ __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ X, 
     norm_weights(norm_w, op, k, K, wa, wb);
     float v[8];
     if (t < M && k < K) {
-        const float *row = X + (size_t)t * ldx + k;
-        const float4 a = *(const float4 *)row;
-        const float4 b = *(const float4 *)(row + 4);
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-        if (add != nullptr) {
-            float sum[8];
+        // the sum of the partial slices at column c of row t
+        auto slices = [&](int64_t rs, int c, float (&sum)[8]) {
 #pragma unroll
             for (int e = 0; e < 8; e++) sum[e] = 0.f;
             for (int sl = 0; sl < n_add; sl++) {
-                const float *pa = add + (size_t)sl * add_stride + (size_t)t * K + k;
-                const float4 c = *(const float4 *)pa;
-                const float4 d = *(const float4 *)(pa + 4);
-                const float pv[8] = {c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
+                const float *pa = add + (size_t)sl * add_stride + (size_t)t * rs + c;
+                const float4 a = *(const float4 *)pa;
+                const float4 b = *(const float4 *)(pa + 4);
+                const float pv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
                 for (int e = 0; e < 8; e++) sum[e] = sl == 0 ? pv[e] : sum[e] + pv[e];
             }
+        };
+        float up[8];
+        if (X != nullptr) {
+            const float *row = X + (size_t)t * ldx + k;
+            const float4 a = *(const float4 *)row;
+            const float4 b = *(const float4 *)(row + 4);
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+            if (add != nullptr) {
+                float sum[8];
+                slices(K, k, sum);
 #pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = v[e] + sum[e];
-            float *wrow = xw + (size_t)t * ldx + k;
-            *(float4 *)wrow = make_float4(v[0], v[1], v[2], v[3]);
-            *(float4 *)(wrow + 4) = make_float4(v[4], v[5], v[6], v[7]);
+                for (int e = 0; e < 8; e++) v[e] = v[e] + sum[e];
+                float *wrow = xw + (size_t)t * ldx + k;
+                *(float4 *)wrow = make_float4(v[0], v[1], v[2], v[3]);
+                *(float4 *)(wrow + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            }
+            if (op == ACT_SILU_MUL) {
+                const float4 c = *(const float4 *)(row + K);
+                const float4 d = *(const float4 *)(row + K + 4);
+                up[0] = c.x; up[1] = c.y; up[2] = c.z; up[3] = c.w;
+                up[4] = d.x; up[5] = d.y; up[6] = d.z; up[7] = d.w;
+            }
+        } else {
+            slices(ldx, k, v);
+            if (op == ACT_SILU_MUL) slices(ldx, K + k, up);
         }
         if (op == ACT_SILU_MUL) {
-            const float4 c = *(const float4 *)(row + K);
-            const float4 d = *(const float4 *)(row + K + 4);
-            const float up[8] = {c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
 #pragma unroll
             for (int e = 0; e < 8; e++) v[e] = silu_mul1(v[e], up[e]);
         }
@@ -1792,8 +1807,9 @@ static hipError_t gemm_in(int qt, const void *W, const float *X, const ActIn &in
         hipError_t e = gemm_in(qt, W, X, in, Y, m0, N, K, flags | 1, ws, st);
         if (e != hipSuccess) return e;
         ActIn in2 = in;
-        if (in2.add != nullptr) in2.add += (size_t)m0 * K;
-        return gemm_in(qt, W, X + (size_t)m0 * in.ldx, in2, Y + (size_t)m0 * N, M - m0, N, K, flags | 1, ws, st);
+        if (in2.add != nullptr) in2.add += (size_t)m0 * (X != nullptr ? K : in.ldx);
+        const float *X2 = X != nullptr ? X + (size_t)m0 * in.ldx : nullptr;  // (absent: the slices are the input)
+        return gemm_in(qt, W, X2, in2, Y + (size_t)m0 * N, M - m0, N, K, flags | 1, ws, st);
     }
     const GemmPlan p = plan_gemm(qt, M, N, K, flags);
     const int accum = (flags & 4) ? 1 : 0;

@@ -111,25 +111,34 @@ def gemm_q(qtype: int, w_dev, x, n: int, k: int, flags: int = GEMM_AUTO, out=Non
 
 
 def gemm_q_ex(qtype: int, w_dev, x, n: int, k: int, act: int = ACT_PLAIN, norm_w=None, eps: float = 1e-6,
-              flags: int = GEMM_AUTO, out=None, stream=None, ws=None, m: int | None = None, add=None):
+              flags: int = GEMM_AUTO, out=None, stream=None, ws=None, m: int | None = None, add=None,
+              ldx: int | None = None):
     """gemm_q with its input stage fused: act = ACT_PLAIN / ACT_RMSNORM
     (RMSNorm(x) * norm_w per row) / ACT_SILU_MUL (x rows [gate | up]). x may
     be a row-strided view (x.stride(1) == 1); m defaults to x.shape[0].
     add: (pointer, n_slices, slice_stride) of K-slice partials (from
-    gemm_partials) folded into x first and stored back. With GEMM_DEFER the
-    product stays in ws as partials and `out` is not written."""
+    gemm_partials) folded into x first and stored back; with x None the
+    slices' sum is the input itself ([m, ldx] slices, m and ldx given). With
+    GEMM_DEFER the product stays in ws as partials and `out` is not
+    written."""
     import torch
-    if x.dim() == 1:
-        x = x.view(1, -1)
-    if x.dtype != torch.float32 or x.stride(1) != 1:
-        raise ValueError("x must be float32 with unit column stride")
-    m = x.shape[0] if m is None else m
+    if x is None:
+        if add is None or m is None or ldx is None:
+            raise ValueError("x=None needs add, m and ldx")
+        dev, xp = torch.device("cuda"), None
+    else:
+        if x.dim() == 1:
+            x = x.view(1, -1)
+        if x.dtype != torch.float32 or x.stride(1) != 1:
+            raise ValueError("x must be float32 with unit column stride")
+        m = x.shape[0] if m is None else m
+        dev, xp, ldx = x.device, _ptr(x), x.stride(0)
     if out is None and not (flags & GEMM_DEFER):
-        out = torch.empty((m, n), dtype=torch.float32, device=x.device)
+        out = torch.empty((m, n), dtype=torch.float32, device=dev)
     L = _lib.load()
     if ws is None:
-        ws = torch.empty(gemm_ws_bytes(qtype, m, n, k, flags), dtype=torch.uint8, device=x.device)
-    gi = _lib.GemmInput(_ptr(x), x.stride(0), act, None if norm_w is None else _ptr(norm_w), eps,
+        ws = torch.empty(gemm_ws_bytes(qtype, m, n, k, flags), dtype=torch.uint8, device=dev)
+    gi = _lib.GemmInput(xp, ldx, act, None if norm_w is None else _ptr(norm_w), eps,
                         None if add is None else add[0], 0 if add is None else add[1],
                         0 if add is None else add[2])
     _lib.check(L.ihip_gemm_q_ex(qtype, _ptr(w_dev), C.byref(gi), None if out is None else _ptr(out), m, n, k, flags,

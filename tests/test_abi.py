@@ -134,3 +134,21 @@ def test_commit_state_argument_checks(lib):
     assert lib.ihip_spec_commit_state(p16, p16, 16, 8, 4, p16, 1, 0, 0, None) == -22  # snapshot stride < bytes
     assert lib.ihip_spec_advance_len(None, p16, 1, None) == -14
     assert lib.ihip_spec_advance_len(p16, p16, 0, None) == -22
+
+
+def test_gemm_ex_input_checks(lib):
+    """ihip_gemm_q_ex: x may be absent only when the add slices are the input
+    (then [M x ldx] slices); SILU_MUL folds only in that form."""
+    from inferno_hip import _lib as L
+    buf = (C.c_uint8 * 64)()
+    p16 = (C.addressof(buf) + 15) & ~15
+    gi = L.GemmInput(None, 512, 2, None, 1e-6, None, 0, 0)
+    assert lib.ihip_gemm_q_ex(12, p16, C.byref(gi), p16, 5, 256, 256, 9, p16, 64, None) == -14
+    gi = L.GemmInput(p16, 512, 2, None, 1e-6, p16, 2, 5 * 512)
+    assert lib.ihip_gemm_q_ex(12, p16, C.byref(gi), p16, 5, 256, 256, 9, p16, 64, None) == -22
+    assert b"SILU_MUL" in lib.ihip_last_error()
+    gi = L.GemmInput(None, 512, 2, None, 1e-6, p16, 2, 5 * 256)  # slice stride below M x ldx
+    assert lib.ihip_gemm_q_ex(12, p16, C.byref(gi), p16, 5, 256, 256, 9, p16, 64, None) == -22
+    assert b"add slices" in lib.ihip_last_error()
+    gi = L.GemmInput(None, 512, 2, None, 1e-6, p16, 2, 5 * 512)  # well-formed: fails only on the workspace size
+    assert lib.ihip_gemm_q_ex(12, p16, C.byref(gi), p16, 5, 256, 256, 9, p16, 64, None) == -12

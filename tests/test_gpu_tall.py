@@ -101,3 +101,31 @@ def test_tall_rmsnorm_and_fold(ih):
     assert rel_l2(xf.cpu().numpy(), xref) <= SANITY_HALF
     n = np.stack([O.rmsnorm(r, 1e-6, nw) for r in xf.cpu().numpy()]).astype(np.float32)
     assert rel_l2(yf.cpu().numpy(), O.gemv_f64(F.Q4_K, w2, n, M, N2, H)) <= SANITY_HALF
+
+
+@pytest.mark.parametrize("M", [5, 64])
+def test_fold_gate_up_partials(ih, M):
+    """[gate; up] deferred (K-sliced) and its partials summed by the down
+    projection's SiLU-gating input stage (x absent) equal the reduce-then-
+    matmul sequence bit for bit; o deferred and folded into the residual of
+    the next RMSNorm input stage likewise."""
+    import torch
+    H, FF = 512, 1024
+    rng = np.random.default_rng(70 + M)
+    wgu = synth.matrix(F.Q4_K, 2 * FF, 4 * H, synth.stream_for(9, "fold_gu"))
+    wd = synth.matrix(F.Q6_K, H, FF, synth.stream_for(10, "fold_down"))
+    pgu, pd = ih.pack_weights(F.Q4_K, _dev(wgu), 2 * FF, 4 * H), ih.pack_weights(F.Q6_K, _dev(wd), H, FF)
+    fl = (ih.GEMM_HALF if M > 16 else ih.GEMM_F32) | ih.GEMM_PACKED
+    x = _dev(rng.standard_normal((M, 4 * H)).astype(np.float32))
+    gu = ih.gemm_q(F.Q4_K, pgu, x, 2 * FF, 4 * H, flags=fl)
+    yr = ih.gemm_q_ex(F.Q6_K, pd, gu, H, FF, act=ih.ACT_SILU_MUL, flags=fl)
+    ws = torch.empty(ih.quantized_kernels.gemm_ws_bytes(F.Q4_K, M, 2 * FF, 4 * H, fl), dtype=torch.uint8,
+                     device="cuda")
+    ih.gemm_q_ex(F.Q4_K, pgu, x, 2 * FF, 4 * H, flags=fl | ih.GEMM_DEFER, ws=ws)
+    parts = ih.gemm_partials(F.Q4_K, M, 2 * FF, 4 * H, fl, ws)
+    yf = ih.gemm_q_ex(F.Q6_K, pd, None, H, FF, act=ih.ACT_SILU_MUL, flags=fl, add=parts, m=M, ldx=2 * FF)
+    assert torch.equal(yf, yr)
+    g, u = gu[:, :FF].double().cpu().numpy(), gu[:, FF:].double().cpu().numpy()
+    with np.errstate(over="ignore"):
+        h = (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
+    assert rel_l2(yf.cpu().numpy(), O.gemv_f64(F.Q6_K, wd, h, M, H, FF)) <= (SANITY_HALF if M > 16 else TOL_F32)
