@@ -52,15 +52,16 @@ class Model:
               "o": ("Q4_K", H, NQ, "attn_output"), "gu": ("Q4_K", 2 * FF, H, "ffn_gate_up"),  # gate then up
               "down": ("Q6_K", H, FF, "ffn_down")}
 
-    def __init__(self, ih, n_layers: int, keep_gguf: int = 4):
+    def __init__(self, ih, n_layers: int, keep_gguf: int = 4, proj: str = "Q4_K"):
         import torch
         F = ih.formats
         st = ih.synth.stream_for
+        self.proj = getattr(F, proj)  # format of the q/k/v/o/gate/up projections (config 5: Q4_K or Q5_K)
         self.layers, self.host_gguf, self.gguf_bytes = [], [], 0
         for L in range(n_layers):
             lw, hw = {}, {}
             for key, (qn, rows, k, name) in self.SHAPES.items():
-                qt = getattr(F, qn)
+                qt = self.proj if qn == "Q4_K" else getattr(F, qn)
                 g = ih.quantized_kernels.synth_blocks(qt, st(SEED, f"blk{L}.{name}"), rows * k // F.BLOCK_ELEMS[qt])
                 lw[key] = ih.pack_weights(qt, g, rows, k)
                 self.gguf_bytes += g.numel()
@@ -107,8 +108,9 @@ class VerifyStep:
         self.logits = torch.empty((M, VOCAB), device=dev)
         gws = ih.quantized_kernels.gemm_ws_bytes
         fl = prec | ih.GEMM_PACKED | ih.GEMM_ACCUM
-        wsb = max(gws(F.Q4_K, M, NQ + 2 * NKV, H, fl), gws(F.Q4_K, M, H, NQ, fl),
-                  gws(F.Q4_K, M, 2 * FF, H, fl), gws(F.Q6_K, M, H, FF, fl), gws(F.Q6_K, M, VOCAB, H, fl))
+        P = model.proj
+        wsb = max(gws(P, M, NQ + 2 * NKV, H, fl), gws(P, M, H, NQ, fl),
+                  gws(P, M, 2 * FF, H, fl), gws(F.Q6_K, M, H, FF, fl), gws(F.Q6_K, M, VOCAB, H, fl))
         self.ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
         self.ws_down = torch.empty(wsb, dtype=torch.uint8, device=dev)  # holds the deferred down partials
         self.ws_o = torch.empty(wsb, dtype=torch.uint8, device=dev)  # the deferred o partials (when K-sliced)
@@ -139,6 +141,7 @@ class VerifyStep:
         add of the down projection run inside the input stage of the matmul
         that consumes them."""
         ih, F, M = self.ih, self.ih.formats, self.M
+        P = self.model.proj
         ex = ih.gemm_q_ex
         f32 = self.prec | ih.GEMM_PACKED  # (GEMM_F32, or 0: fp32-accurate below 16 tokens, half above)
         acc = f32 | ih.GEMM_ACCUM
@@ -146,18 +149,18 @@ class VerifyStep:
         parts = ih.gemm_partials(F.Q6_K, M, H, FF, f32, self.ws_down)
         # K-sliced o and [gate; up] (several token tiles) leave their partials
         # to the next input stage instead of a reduce launch
-        o_parts = ih.gemm_partials(F.Q4_K, M, H, NQ, f32, self.ws_o)
-        gu_parts = ih.gemm_partials(F.Q4_K, M, 2 * FF, H, f32, self.ws)
+        o_parts = ih.gemm_partials(P, M, H, NQ, f32, self.ws_o)
+        gu_parts = ih.gemm_partials(P, M, 2 * FF, H, f32, self.ws)
         fold_o, fold_gu = o_parts[1] > 1, gu_parts[1] > 1
         self.x.copy_(self.x0)
         for i, lw in enumerate(self.model.layers):
-            ex(F.Q4_K, lw["qkv"], self.x, NQ + 2 * NKV, H, act=ih.ACT_RMSNORM, norm_w=lw["attn_norm"], flags=f32,
+            ex(P, lw["qkv"], self.x, NQ + 2 * NKV, H, act=ih.ACT_RMSNORM, norm_w=lw["attn_norm"], flags=f32,
                out=self.qkv, ws=self.ws, add=parts if i > 0 else None)
             if fold_o:
-                ex(F.Q4_K, lw["o"], self.qkv[:, :NQ], H, NQ, flags=dfr, ws=self.ws_o)
+                ex(P, lw["o"], self.qkv[:, :NQ], H, NQ, flags=dfr, ws=self.ws_o)
             else:
-                ex(F.Q4_K, lw["o"], self.qkv[:, :NQ], H, NQ, flags=acc, out=self.x, ws=self.ws)
-            ex(F.Q4_K, lw["gu"], self.x, 2 * FF, H, act=ih.ACT_RMSNORM, norm_w=lw["ffn_norm"],
+                ex(P, lw["o"], self.qkv[:, :NQ], H, NQ, flags=acc, out=self.x, ws=self.ws)
+            ex(P, lw["gu"], self.x, 2 * FF, H, act=ih.ACT_RMSNORM, norm_w=lw["ffn_norm"],
                flags=dfr if fold_gu else f32, out=None if fold_gu else self.gu, ws=self.ws,
                add=o_parts if fold_o else None)
             if fold_gu:
@@ -473,20 +476,32 @@ def config3(ih, n_steps: int = 4096, per_call: int = 6):
 
 def config5(ih, model: Model):
     """Config 5: 64-node tree verify (32 layers and the lm_head at M = 64 on
-    the half-precision MFMA path, then the tree accept walk)."""
+    the half-precision MFMA path, then the tree accept walk), with the
+    projections in Q4_K (the config-4 model) and again in Q5_K."""
+    import torch
     F = ih.formats
-    step = TreeStep(ih, model)
-    t = graph_time(step.run, replays=5)
-    t_fwd = graph_time(step.forward, replays=5)
-    weights = sum(F.matrix_bytes(qt, n, k) // F.BLOCK_BYTES[qt] * F.BLOCK_ELEMS[qt]
-                  for qt, n, k in [(F.Q4_K, NQ + 2 * NKV, H), (F.Q4_K, H, NQ), (F.Q4_K, 2 * FF, H),
-                                   (F.Q6_K, H, FF)]) * len(model.layers) + VOCAB * H
-    flops = 2 * 64 * weights
-    return {"ms_per_tree": round(t * 1e3, 3), "trees_per_s": round(1 / t, 2), "ms_forward": round(t_fwd * 1e3, 3),
-            "forward_TFLOPs": round(flops / t_fwd / 1e12, 1),
-            "mfma_frac_fp16_dense": round(flops / t_fwd / 2.5e15, 4),
-            "forward_GBps": round(model.weight_bytes(len(model.layers)) / t_fwd / 1e9, 1),
-            "accepted_path_len": int(step.plen[0])}
+
+    def measure(m: Model):
+        step = TreeStep(ih, m)
+        t = graph_time(step.run, replays=5)
+        t_fwd = graph_time(step.forward, replays=5)
+        P = m.proj
+        weights = sum(F.matrix_bytes(qt, n, k) // F.BLOCK_BYTES[qt] * F.BLOCK_ELEMS[qt]
+                      for qt, n, k in [(P, NQ + 2 * NKV, H), (P, H, NQ), (P, 2 * FF, H),
+                                       (F.Q6_K, H, FF)]) * len(m.layers) + VOCAB * H
+        flops = 2 * 64 * weights
+        return {"ms_per_tree": round(t * 1e3, 3), "trees_per_s": round(1 / t, 2),
+                "ms_forward": round(t_fwd * 1e3, 3), "forward_TFLOPs": round(flops / t_fwd / 1e12, 1),
+                "mfma_frac_fp16_dense": round(flops / t_fwd / 2.5e15, 4),
+                "forward_GBps": round(m.weight_bytes(len(m.layers)) / t_fwd / 1e9, 1),
+                "accepted_path_len": int(step.plen[0])}
+
+    out = measure(model)
+    m5 = Model(ih, len(model.layers), keep_gguf=0, proj="Q5_K")
+    out["q5k_projections"] = measure(m5)
+    del m5
+    torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(ih, model: Model, n_layers: int, M: int, k: int, budget_s: float):

@@ -1361,6 +1361,16 @@ __device__ __forceinline__ void unit_vals(const Unit<QT> &r, const AReg<QT> (&a)
     }
 }
 
+// Waves per workgroup of the tall kernel: two per SIMD (8) where the A
+// operand, the ring (4-deep, 2-deep for the larger Q5_K/Q6_K items at 4
+// tiles) and the rest fit in 256 registers without spilling (two waves then
+// overlap one's MFMAs with the other's dequantization), else one per SIMD
+// (4) with the full register file. Independent of the weight layout, so
+// packed and GGUF-layout weights sum the same K-slices in the same order.
+__host__ __device__ constexpr int tall_waves(int qt, bool split, int mt) {
+    return (qt == QT_Q4_K || qt == QT_Q5_K || (qt == QT_Q6_K && !split) || (qt == QT_Q8_0 && mt <= 2)) ? 8 : 4;
+}
+
 // Several token tiles (M up to 32 fp32-accurate, 64 half): one wave per
 // SIMD, each wave holding one 256-element unit of the A operand for all MT
 // tiles in registers, so a dequantized weight fragment feeds MT MFMAs. A
@@ -1372,14 +1382,14 @@ __device__ __forceinline__ void unit_vals(const Unit<QT> &r, const AReg<QT> (&a)
 // register ring. Results go out with bounds-checked buffer stores (no
 // branches, no read-modify-write in the loop): to the K-slice's partials
 // when part is set (the caller reduces or folds them), else to Y.
-template <int QT, bool SPLIT, bool PK, int MT>
-__global__ __launch_bounds__(256, 1)
+template <int QT, bool SPLIT, bool PK, int MT, int NW>
+__global__ __launch_bounds__(NW * 64, 1)
 void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, int N, int K,
                    const uint8_t *__restrict__ afrag, const float *__restrict__ invs,
                    const uint8_t *__restrict__ mfrag, const float *__restrict__ ssq, float eps,
                    float *__restrict__ part) {
     using C = GemmCfg<QT>;
-    constexpr int NW = 4;
+    static_assert(NW == 4 || NW == 8, "one or two waves per SIMD");
     constexpr int TOKT = SPLIT ? 8 : 16;
     constexpr int TOK = MT * TOKT;
     constexpr int TPL = SPLIT ? 2 : 4;
@@ -1388,8 +1398,12 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     constexpr int UNIT_BYTES = (QT == QT_Q8_0) ? 8 * 34 : C::BB;
     // ring depth: 8 items where the registers allow it (Q8_0 items and the
     // fp32-accurate Q6_K operands of 3-4 tiles are larger)
-    constexpr int R = (QT == QT_Q8_0 || (QT == QT_Q6_K && SPLIT && MT >= 3)) ? 4 : 8;
-    constexpr int F = 4;
+    // (two waves per SIMD: half the registers each, a 4-deep ring and
+    // batches of 2 tiles, each tile summed by 4 waves a value group each)
+    constexpr int R = (NW == 8 && MT == 4 && (QT == QT_Q5_K || (QT == QT_Q6_K && !PK))) ? 2
+                      : (NW == 8 || QT == QT_Q8_0 || (QT == QT_Q6_K && SPLIT && MT >= 3)) ? 4 : 8;
+    constexpr int F = NW == 8 ? 2 : 4;
+    constexpr int WPT = NW / F;  // waves per tile in a batch's reduction
     static_assert(R % F == 0, "a ring pass holds whole reduction batches");
     __shared__ __align__(16) float red[2][F][NW][64][NVP];
     __shared__ float rs[TOK];
@@ -1492,27 +1506,24 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
         for (int k = 0; k < NVP; k += 4) *(f4 *)(slot + k) = f4{vals[k], vals[k + 1], vals[k + 2], vals[k + 3]};
         if (flush) {
             __syncthreads();
-            if (wave <= jb) {
-                float sum[NVP];
-#pragma unroll
-                for (int k = 0; k < NVP; k += 4) {
-                    const f4 v = *(const f4 *)&red[hb][wave][0][lane][k];
-                    sum[k] = v[0]; sum[k + 1] = v[1]; sum[k + 2] = v[2]; sum[k + 3] = v[3];
-                }
-#pragma unroll
-                for (int w = 1; w < NW; w++)
-#pragma unroll
-                    for (int k = 0; k < NVP; k += 4) {
-                        const f4 v = *(const f4 *)&red[hb][wave][w][lane][k];
-                        sum[k] += v[0]; sum[k + 1] += v[1]; sum[k + 2] += v[2]; sum[k + 3] += v[3];
-                    }
-                const int r = ((int)blockIdx.x + G * (j - jb + wave)) * 16 + n_in;
+            const int tl = wave / WPT, grp = wave % WPT;  // tile of the batch, first value group
+            if (tl <= jb) {
+                const int r = ((int)blockIdx.x + G * (j - jb + tl)) * 16 + n_in;
                 const uint32_t voff = r < N ? (uint32_t)(tb * N + r) * 4u : 0x80000000u;
 #pragma unroll
-                for (int k = 0; k < NV; k++) {
-                    const int tk = lane_token<SPLIT>(k / TPL, 0, k % TPL);
-                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum[k] * rs[tb + tk]), ors,
-                                                          (int)voff, tk * N * 4, 0);
+                for (int q = 0; q < NVP / 4; q++) {
+                    if (q % WPT != grp) continue;
+                    f4 sum = *(const f4 *)&red[hb][tl][0][lane][4 * q];
+#pragma unroll
+                    for (int w = 1; w < NW; w++) sum += *(const f4 *)&red[hb][tl][w][lane][4 * q];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int k = 4 * q + e;
+                        if (k >= NV) continue;
+                        const int tk = lane_token<SPLIT>(k / TPL, 0, k % TPL);
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum[e] * rs[tb + tk]),
+                                                              ors, (int)voff, tk * N * 4, 0);
+                    }
                 }
             }
         }
@@ -1568,7 +1579,7 @@ hipError_t launch_v(const uint8_t *W, const float *X, const ActIn &in, float *Y,
     return hipGetLastError();
 }
 
-template <int QT, bool SPLIT, bool PK, int MT>
+template <int QT, bool SPLIT, bool PK, int MT, int NW>
 hipError_t launch_w(const uint8_t *W, const float *X, const ActIn &in, float *Y, int M, int N, int K, int S, int G,
                     int accum, const ActWs &a, float *part, hipStream_t st) {
     hipError_t e;
@@ -1576,7 +1587,7 @@ hipError_t launch_w(const uint8_t *W, const float *X, const ActIn &in, float *Y,
     // several K-slices, accumulation and deferral all go through the
     // partials (the kernel itself never reads its output)
     const bool via_part = S > 1 || accum || in.defer;
-    gemm_w_kernel<QT, SPLIT, PK, MT><<<dim3(G, S), 256, 0, st>>>(
+    gemm_w_kernel<QT, SPLIT, PK, MT, NW><<<dim3(G, S), NW * 64, 0, st>>>(
         W, Y, M, N, K, a.afrag, a.inv, a.mfrag, in.op == ACT_RMSNORM ? a.ssq : nullptr, in.eps,
         via_part ? part : nullptr);
     e = hipGetLastError();
@@ -1617,6 +1628,7 @@ struct GemmPlan {
     bool split;      // fp32-accurate two-limb mode
     int MT;          // MFMA token tiles (16 slots each)
     bool stream;     // streaming kernel with register operands (else the LDS kernel)
+    bool tall;       // several token tiles on the batched-reduction kernel
     int NW, UPS;     // streaming kernel: waves per workgroup, units per wave
     int ups;         // LDS kernel: 256-element units per K-slice
     int S;           // K-slices (grid.y)
@@ -1653,11 +1665,16 @@ static GemmPlan plan_gemm(int qt, int M, int N, int K, int flags) {
     p.stream = use_stream && p.MT <= stream_mt && !((flags & 8) && packed_bytes(qt, N, K) >= ((size_t)1 << 31));
     if (p.stream && p.MT > 1) {
         // several token tiles: their A operand fills the registers; 4 waves
-        // of one unit each per workgroup, one workgroup (one wave per SIMD)
-        // per CU
-        p.NW = 4;
+        // (one per SIMD) or 8 (two per SIMD, IHIP_TALL_NW=8) of one unit
+        // each per workgroup, one workgroup per CU
+        // (IHIP_TALL=0: the per-tile-barrier variant of the streaming kernel)
+        static const int tall_env = env_int("IHIP_TALL", 1);
+        // (IHIP_TALL_NW=4: one wave per SIMD throughout)
+        static const int tall_nw = env_int("IHIP_TALL_NW", 0);
+        p.tall = tall_env && (size_t)p.MT * 16 * N * 4 < ((size_t)1 << 31);
+        p.NW = p.tall && tall_nw != 4 ? tall_waves(qt, p.split, p.MT) : 4;
         p.UPS = 1;
-        p.S = (n_units + 3) / 4;
+        p.S = (n_units + p.NW - 1) / p.NW;
         const int n_tiles = (N + 15) / 16;
         const int g0 = std::max(1, std::min(n_tiles, 256 / p.S));
         const int per = (n_tiles + g0 - 1) / g0;
@@ -1737,12 +1754,26 @@ static hipError_t dispatch_mt(const GemmPlan &p, const uint8_t *W, const float *
                   p.stream ? ws + p.off_mfrag : nullptr, (float *)(ws + p.off_ssq)};
     float *part = (float *)(ws + p.off_part);
     if (p.stream && p.MT > 1) {
-        // (IHIP_TALL=0: the per-tile-barrier variant of the streaming kernel)
-        static const int tall = env_int("IHIP_TALL", 1);
-        if (tall && (size_t)p.MT * 16 * N * 4 < ((size_t)1 << 31)) {
-#define WM(mt) return p.split ? launch_w<QT, true, PK, mt>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st) \
-                              : launch_w<QT, false, PK, mt>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
-            switch (p.MT) { case 2: WM(2); case 3: WM(3); default: WM(4); }
+        if (p.tall) {
+#define WM(mt, nw) return p.split ? launch_w<QT, true, PK, mt, nw>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st) \
+                                  : launch_w<QT, false, PK, mt, nw>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
+            // (instantiated only where tall_waves allows two waves per SIMD)
+            constexpr bool w8s2 = tall_waves(QT, true, 2) == 8, w8s3 = tall_waves(QT, true, 3) == 8,
+                           w8s4 = tall_waves(QT, true, 4) == 8, w8h2 = tall_waves(QT, false, 2) == 8,
+                           w8h3 = tall_waves(QT, false, 3) == 8, w8h4 = tall_waves(QT, false, 4) == 8;
+            if (p.NW == 8) {
+                if (p.split) {
+                    if constexpr (w8s2) if (p.MT == 2) return launch_w<QT, true, PK, 2, 8>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st);
+                    if constexpr (w8s3) if (p.MT == 3) return launch_w<QT, true, PK, 3, 8>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st);
+                    if constexpr (w8s4) if (p.MT == 4) return launch_w<QT, true, PK, 4, 8>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st);
+                } else {
+                    if constexpr (w8h2) if (p.MT == 2) return launch_w<QT, false, PK, 2, 8>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st);
+                    if constexpr (w8h3) if (p.MT == 3) return launch_w<QT, false, PK, 3, 8>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st);
+                    if constexpr (w8h4) if (p.MT == 4) return launch_w<QT, false, PK, 4, 8>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st);
+                }
+                return hipErrorInvalidValue;  // (the plan picks 8 waves only where instantiated)
+            }
+            switch (p.MT) { case 2: WM(2, 4); case 3: WM(3, 4); default: WM(4, 4); }
 #undef WM
         }
 #define VM(mt) return p.split ? launch_v<QT, 4, 1, true, PK, mt>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st) \
