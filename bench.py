@@ -272,6 +272,26 @@ def profile_kernels(ih, model: Model, n_layers: int, M: int):
     log(f"profile_kernels: roofline graph + ihip_add over {n} floats")
 
 
+def profile_tall(ih, reps: int = 5):
+    """For rocprofv3 --pmc: the M = 64 (config 5) half-precision matmuls of
+    one layer, each launched `reps` times: Q4_K [gate; up] 24576x4096 with
+    the RMSNorm input stage, Q6_K down 4096x12288 with the SiLU-gating
+    stage (packed weights, seeded blocks)."""
+    import torch
+    F, q = ih.formats, ih.quantized_kernels
+    st = ih.synth.stream_for
+    M = 64
+    gu = ih.pack_weights(F.Q4_K, q.synth_blocks(F.Q4_K, st(SEED, "pt.gu"), 2 * FF * H // 256), 2 * FF, H)
+    dn = ih.pack_weights(F.Q6_K, q.synth_blocks(F.Q6_K, st(SEED, "pt.down"), H * FF // 256), H, FF)
+    x = q.synth_gaussian(st(SEED, "pt.x"), M * H).view(M, H)
+    g = q.synth_gaussian(st(SEED, "pt.g"), M * 2 * FF).view(M, 2 * FF)
+    for _ in range(reps):
+        ih.gemm_q_ex(F.Q4_K, gu, x, 2 * FF, H, act=ih.ACT_RMSNORM, flags=ih.GEMM_PACKED)
+        ih.gemm_q_ex(F.Q6_K, dn, g, H, FF, act=ih.ACT_SILU_MUL, flags=ih.GEMM_PACKED)
+    torch.cuda.synchronize()
+    log(f"profile_tall: {reps} x (gate/up Q4_K 24576x4096, down Q6_K 4096x12288) at M = {M}")
+
+
 def read_traffic():
     """HBM bytes per launch of the roofline kernel, from the committed
     rocprofv3 FETCH_SIZE/WRITE_SIZE summary (None when absent)."""
@@ -681,6 +701,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only run the roofline kernel and the traffic calibration kernel (for rocprofv3 --pmc)")
+    ap.add_argument("--profile-tall", action="store_true",
+                    help="only run the M = 64 gate/up and down matmuls five times each (for rocprofv3 --pmc)")
     ap.add_argument("--configs", type=str, default="",
                     help="instead of the bench line: measure BASELINE configs (comma list of 1,2,3,5, 'sampler' "
                          "for the draft-side sampler, 'gguf' for file-to-device loading), one JSON object per config")
@@ -696,6 +718,9 @@ def main():
     assert ih.quant_kernels_available(), ih._lib.last_error()
     k, T = 4, 0.8
     t0 = time.time()
+    if args.profile_tall:
+        profile_tall(ih)
+        return
     if args.configs:
         want = [c.strip() for c in args.configs.split(",") if c.strip()]
         for c in want:
