@@ -126,9 +126,18 @@ __global__ __launch_bounds__(NT) void stats_partial_kernel(const float *__restri
     if (threadIdx.x == 0) part[(size_t)row * nchunk + chunk] = make_float2(m, s);
 }
 
+// Sequential merge of a row's chunk partials (chunk order), the loads issued
+// eight at a time.
 __device__ __forceinline__ float2 merge_row(const float2 *part, int nchunk) {
     float m = -__builtin_huge_valf(), s = 0.f;
-    for (int c = 0; c < nchunk; c++) merge_ms(m, s, part[c].x, part[c].y);
+    for (int c = 0; c < nchunk; c += 8) {
+        float2 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = part[min(c + j, nchunk - 1)];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (c + j < nchunk) merge_ms(m, s, v[j].x, v[j].y);
+    }
     return make_float2(m, s);
 }
 
@@ -532,46 +541,67 @@ __global__ void greedy_kernel(const float2 *__restrict__ part, int nchunk, const
 }
 
 // Tree walk: the workgroup first merges the statistics of every row (target
-// rows then draft rows) into ms, then one thread walks the nodes in index
-// order (parent[i] < i).
+// rows then draft rows) into ms, then tests every node in parallel (the test
+// of node i reads only its parent's rows and its own token: pass = u_i <
+// min(1, p/q)), then one thread walks the nodes in index order (parent[i] <
+// i) with integers only: st[i] = depth of i if i and all its ancestors
+// passed, else -1; the deepest accepted node, smallest index on ties, ends
+// the path. Node state lives in LDS up to TREE_LDS nodes (in the workspace
+// beyond that).
+constexpr int TREE_LDS = 4096;
 __global__ __launch_bounds__(NT) void tree_kernel(const float *__restrict__ tgt, const float *__restrict__ drf,
                                                   const int32_t *__restrict__ tok, const int32_t *__restrict__ parent,
                                                   int n, int V, float T, const float *__restrict__ u,
                                                   const float2 *__restrict__ part, int nchunk, float2 *__restrict__ ms,
                                                   int32_t *__restrict__ out_path, int32_t *__restrict__ out_len,
                                                   int32_t *__restrict__ wsi) {
+    __shared__ int32_t s_par[TREE_LDS], s_st[TREE_LDS];
+    __shared__ int8_t s_pass[TREE_LDS];
+    const bool in_lds = n <= TREE_LDS;
+    int32_t *par = in_lds ? s_par : wsi;
+    int32_t *st = in_lds ? s_st : wsi + n;
+    int8_t *pass = in_lds ? s_pass : (int8_t *)(ms + 2 * n);
     for (int r = threadIdx.x; r < 2 * n; r += blockDim.x) ms[r] = merge_row(part + (size_t)r * nchunk, nchunk);
     __syncthreads();
-    if (threadIdx.x != 0) return;
-    int32_t *acc = wsi, *depth = wsi + n;
-    acc[0] = 1;
-    depth[0] = 0;
-    int best = 0;
-    for (int i = 1; i < n; i++) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
         const int p = parent[i];
         const int x = tok[i];
-        acc[i] = 0;
-        if (p < 0 || p >= i || x < 0 || x >= V) {  // malformed node: reported as out_len = -1
+        par[i] = p;
+        int8_t r = 1;  // (the root is accepted)
+        if (i > 0) {
+            if (p < 0 || p >= i || x < 0 || x >= V) {
+                r = -1;  // malformed node: reported as out_len = -1
+            } else {
+                const float2 pt = ms[p];
+                const float2 pd = ms[n + p];
+                const float pp = __expf(tgt[(size_t)p * V + x] / T - pt.x) / pt.y;
+                const float qq = __expf(drf[(size_t)p * V + x] / T - pd.x) / pd.y;
+                const float ratio = qq > 0.f ? fminf(1.0f, pp / qq) : 1.0f;
+                r = u[i] < ratio ? 1 : 0;
+            }
+        }
+        pass[i] = r;
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    st[0] = 0;
+    int best = 0;
+    for (int i = 1; i < n; i++) {
+        const int r = pass[i];
+        if (r < 0) {
             *out_len = -1;
             return;
         }
-        depth[i] = depth[p] + 1;
-        if (!acc[p]) continue;
-        const float2 pt = ms[p];
-        const float2 pd = ms[n + p];
-        const float pp = __expf(tgt[(size_t)p * V + x] / T - pt.x) / pt.y;
-        const float qq = __expf(drf[(size_t)p * V + x] / T - pd.x) / pd.y;
-        const float ratio = qq > 0.f ? fminf(1.0f, pp / qq) : 1.0f;
-        if (u[i] < ratio) {
-            acc[i] = 1;
-            if (depth[i] > depth[best]) best = i;
-        }
+        const int sp = st[par[i]];
+        const int d = (sp >= 0 && r) ? sp + 1 : -1;
+        st[i] = d;
+        if (d > st[best]) best = i;
     }
-    const int len = depth[best] + 1;
+    const int len = st[best] + 1;
     int v = best;
     for (int d = len - 1; d >= 0; d--) {
         out_path[d] = v;
-        v = d > 0 ? parent[v] : 0;
+        v = d > 0 ? par[v] : 0;
     }
     *out_len = len;
 }
@@ -636,7 +666,8 @@ hipError_t launch_greedy(const float2 *part, int V, const int32_t *draft_tok, in
     return hipGetLastError();
 }
 
-// part: float2 [2n][nchunk] (target rows then draft rows); wsi: int32 [2n].
+// part: float2 [2n][nchunk] (target rows then draft rows); wsi: int32 [2n], then
+// ms: float2 [2n], then (above TREE_LDS nodes) int8 [n].
 hipError_t launch_tree(const float *tgt, const float *drf, const int32_t *tok, const int32_t *parent, int n, int V,
                        float T, const float *u, float2 *part, int32_t *out_path, int32_t *out_len,
                        int32_t *wsi, hipStream_t st) {

@@ -109,7 +109,10 @@ def mtp_verify_step(logits, draft_tokens, stream=None):
 
 
 def tree_accept(target_logits, draft_logits, node_tokens, parent, temperature: float, u, stream=None):
-    """Longest accepted root-to-leaf path of a draft tree (node 0 = root)."""
+    """Longest accepted root-to-leaf path of a draft tree (node 0 = root).
+    Raises ValueError for a malformed tree (a parent not earlier than its
+    node, or a token outside the vocabulary), which the device reports as
+    out_len = -1."""
     import torch
     import ctypes as C
     n, V = target_logits.shape
@@ -122,7 +125,10 @@ def tree_accept(target_logits, draft_logits, node_tokens, parent, temperature: f
     _lib.check(L.ihip_tree_accept(_ptr(target_logits), _ptr(draft_logits), _ptr(node_tokens), _ptr(parent), n, V,
                                   temperature, _ptr(u), _ptr(path), _ptr(ln), _ptr(ws), ws.numel(),
                                   _stream(stream)))
-    return path[: int(ln.item())]
+    n_path = int(ln.item())
+    if n_path < 0:
+        raise ValueError("tree_accept: malformed tree (parent[i] must lie in [0, i), tokens in [0, V))")
+    return path[:n_path]
 
 
 @dataclass

@@ -162,6 +162,32 @@ def test_tree_accept(ih, V):
         assert np.array_equal(path, ref), (t, path, ref)
 
 
+def test_tree_accept_large_and_malformed(ih):
+    """A tree larger than the walk's LDS capacity (its state then lives in the
+    workspace), a chain (the walk reduces to the sequential accept), and a
+    malformed parent array reported as an error."""
+    rng = np.random.default_rng(5000)
+    V = 32
+    for n, chain in ((5000, False), (300, True)):
+        par = np.array([0] + [i - 1 if chain else int(rng.integers(0, i)) for i in range(1, n)], dtype=np.int32)
+        Lt = (rng.standard_normal((n, V)) * 1.5).astype(np.float32)
+        Ld = (Lt + rng.standard_normal((n, V)) * 0.3).astype(np.float32)
+        tok = np.zeros(n, dtype=np.int32)
+        for i in range(1, n):
+            tok[i] = _draw(Ld[par[i]], 1.0, rng.random())
+        u = (rng.random(n) * 0.5).astype(np.float32)
+        path = ih.tree_accept(_dev(Lt), _dev(Ld), _dev(tok), _dev(par), 1.0, _dev(u)).cpu().numpy()
+        ref = O.tree_accept(Lt, Ld, tok, par, 1.0, u)
+        assert np.array_equal(path, ref), (n, path[:8], ref[:8])
+        assert len(path) > 3
+    bad = _tree_parents(64)
+    bad[7] = 9  # parent after its node
+    Lt = np.zeros((64, V), dtype=np.float32)
+    with pytest.raises(ValueError):
+        ih.tree_accept(_dev(Lt), _dev(Lt), _dev(np.zeros(64, dtype=np.int32)), _dev(bad), 1.0,
+                       _dev(np.zeros(64, dtype=np.float32)))
+
+
 def test_rmsnorm(ih):
     x = np.random.default_rng(1).standard_normal((5, 4096)).astype(np.float32) * 3
     got = ih.rmsnorm(_dev(x)).cpu().numpy()
