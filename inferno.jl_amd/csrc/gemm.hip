@@ -1361,9 +1361,17 @@ __device__ __forceinline__ void unit_vals(const Unit<QT> &r, const AReg<QT> (&a)
     }
 }
 
+// Most units (of 256 K) per wave of the one-tile streaming kernel that fit
+// its registers without spilling: each unit of A operand is 32 VGPRs (one
+// tile), and the larger Q5_K/Q6_K/Q8_0 items leave less room.
+__host__ __device__ constexpr int stream_ups_cap(int qt, bool split) {
+    return qt == QT_Q4_K ? (split ? 4 : 2) : qt == QT_Q5_K ? 2 : qt == QT_Q6_K ? (split ? 2 : 1) : 1;
+}
+
 // Waves per workgroup of the tall kernel: two per SIMD (8) where the A
 // operand, the ring (4-deep, 2-deep for the larger Q5_K/Q6_K items at 4
-// tiles) and the rest fit in 256 registers without spilling (two waves then
+// tiles, which Q6_K also prefers when it fits) and the rest fit in 256
+// registers without spilling (two waves then
 // overlap one's MFMAs with the other's dequantization), else one per SIMD
 // (4) with the full register file. Independent of the weight layout, so
 // packed and GGUF-layout weights sum the same K-slices in the same order.
@@ -1397,11 +1405,11 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     constexpr int NVP = (NV + 3) & ~3;     // (padded to whole 16-byte LDS accesses)
     constexpr int UNIT_BYTES = (QT == QT_Q8_0) ? 8 * 34 : C::BB;
     // ring depth: 8 items where the registers allow it (Q8_0 items and the
-    // fp32-accurate Q6_K operands of 3-4 tiles are larger)
+    // fp32-accurate Q6_K operands are larger)
     // (two waves per SIMD: half the registers each, a 4-deep ring and
     // batches of 2 tiles, each tile summed by 4 waves a value group each)
-    constexpr int R = (NW == 8 && MT == 4 && (QT == QT_Q5_K || (QT == QT_Q6_K && !PK))) ? 2
-                      : (NW == 8 || QT == QT_Q8_0 || (QT == QT_Q6_K && SPLIT && MT >= 3)) ? 4 : 8;
+    constexpr int R = (NW == 8 && MT == 4 && (QT == QT_Q5_K || QT == QT_Q6_K)) ? 2
+                      : (NW == 8 || QT == QT_Q8_0 || (QT == QT_Q6_K && SPLIT)) ? 4 : 8;
     constexpr int F = NW == 8 ? 2 : 4;
     constexpr int WPT = NW / F;  // waves per tile in a batch's reduction
     static_assert(R % F == 0, "a ring pass holds whole reduction batches");
@@ -1513,9 +1521,13 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
 #pragma unroll
                 for (int q = 0; q < NVP / 4; q++) {
                     if (q % WPT != grp) continue;
-                    f4 sum = *(const f4 *)&red[hb][tl][0][lane][4 * q];
+                    // all waves' slices first (one LDS wait), then the sum in wave order
+                    f4 pv[NW];
 #pragma unroll
-                    for (int w = 1; w < NW; w++) sum += *(const f4 *)&red[hb][tl][w][lane][4 * q];
+                    for (int w = 0; w < NW; w++) pv[w] = *(const f4 *)&red[hb][tl][w][lane][4 * q];
+                    f4 sum = pv[0];
+#pragma unroll
+                    for (int w = 1; w < NW; w++) sum += pv[w];
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         const int k = 4 * q + e;
@@ -1535,6 +1547,10 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
 #pragma unroll
         for (int p = 0; p < R; p++) {
             load_item(ib + p + R - 1, buf[(p + R - 1) % R]);
+            // (the loads stay at the head of their step: left to itself the
+            // scheduler sinks them to the end of the pass, next to their use,
+            // and the ring stops prefetching)
+            __builtin_amdgcn_sched_barrier(0);
             consume(ib + p, p % F, p % F == F - 1, buf[p]);
         }
     }
@@ -1680,21 +1696,21 @@ static GemmPlan plan_gemm(int qt, int M, int N, int K, int flags) {
         const int per = (n_tiles + g0 - 1) / g0;
         p.G = (n_tiles + per - 1) / per;
     } else if (p.stream) {
-        // K per workgroup NW*UPS units; prefer one K-slice (no partials) with
-        // the fewest units per wave that still covers K, else the largest
-        // chunk that divides K
+        // K per workgroup NW*UPS units (UPS at most stream_ups_cap); prefer
+        // one K-slice (no partials) with the fewest units per wave that still
+        // covers K, else the largest chunk that divides K
         static const int env_nw = env_int("IHIP_STREAM_NW", 8);
         const int nw = env_nw == 8 ? 8 : 4;
-        int ups = 4;
+        const int cap = stream_ups_cap(qt, p.split);
+        int ups = cap;
         if (env_ups == 1 || env_ups == 2 || env_ups == 4) {
             ups = env_ups;
         } else {
-            ups = 4;
             for (int u : {1, 2, 4})
-                if (nw * u >= n_units) { ups = u; break; }
+                if (u <= cap && nw * u >= n_units) { ups = u; break; }
             if (nw * ups < n_units)
                 for (int u : {4, 2, 1})
-                    if (n_units % (nw * u) == 0) { ups = u; break; }
+                    if (u <= cap && n_units % (nw * u) == 0) { ups = u; break; }
         }
         p.NW = nw;
         p.UPS = ups;
