@@ -1547,10 +1547,10 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
 #pragma unroll
         for (int p = 0; p < R; p++) {
             load_item(ib + p + R - 1, buf[(p + R - 1) % R]);
-            // (the loads stay at the head of their step: left to itself the
-            // scheduler sinks them to the end of the pass, next to their use,
-            // and the ring stops prefetching)
-            __builtin_amdgcn_sched_barrier(0);
+            // (two waves per SIMD: the loads stay at the head of their step;
+            // under that register budget the scheduler sinks them to the end
+            // of the pass, next to their use, and the ring stops prefetching)
+            if constexpr (NW == 8) __builtin_amdgcn_sched_barrier(0);
             consume(ib + p, p % F, p % F == F - 1, buf[p]);
         }
     }
@@ -1644,7 +1644,6 @@ struct GemmPlan {
     bool split;      // fp32-accurate two-limb mode
     int MT;          // MFMA token tiles (16 slots each)
     bool stream;     // streaming kernel with register operands (else the LDS kernel)
-    bool tall;       // several token tiles on the batched-reduction kernel
     int NW, UPS;     // streaming kernel: waves per workgroup, units per wave
     int ups;         // LDS kernel: 256-element units per K-slice
     int S;           // K-slices (grid.y)
@@ -1676,19 +1675,18 @@ static GemmPlan plan_gemm(int qt, int M, int N, int K, int flags) {
     static const int lds_a = env_int("IHIP_GEMM_LDS_A", 32768);
     static const int use_stream = env_int("IHIP_STREAM", 1);
     static const int env_ups = env_int("IHIP_STREAM_UPS", 0);
-    // (the streaming kernel addresses packed weights with 32-bit offsets)
+    // (the streaming kernels address packed weights, and the tall kernel its
+    // outputs, with 32-bit offsets: larger cases take the LDS kernel)
     static const int stream_mt = env_int("IHIP_STREAM_MT", 4);
-    p.stream = use_stream && p.MT <= stream_mt && !((flags & 8) && packed_bytes(qt, N, K) >= ((size_t)1 << 31));
+    p.stream = use_stream && p.MT <= stream_mt && !((flags & 8) && packed_bytes(qt, N, K) >= ((size_t)1 << 31)) &&
+               !(p.MT > 1 && (size_t)p.MT * 16 * N * 4 >= ((size_t)1 << 31));
     if (p.stream && p.MT > 1) {
         // several token tiles: their A operand fills the registers; 4 waves
         // (one per SIMD) or 8 (two per SIMD, IHIP_TALL_NW=8) of one unit
         // each per workgroup, one workgroup per CU
-        // (IHIP_TALL=0: the per-tile-barrier variant of the streaming kernel)
-        static const int tall_env = env_int("IHIP_TALL", 1);
         // (IHIP_TALL_NW=4: one wave per SIMD throughout)
         static const int tall_nw = env_int("IHIP_TALL_NW", 0);
-        p.tall = tall_env && (size_t)p.MT * 16 * N * 4 < ((size_t)1 << 31);
-        p.NW = p.tall && tall_nw != 4 ? tall_waves(qt, p.split, p.MT) : 4;
+        p.NW = tall_nw != 4 ? tall_waves(qt, p.split, p.MT) : 4;
         p.UPS = 1;
         p.S = (n_units + p.NW - 1) / p.NW;
         const int n_tiles = (N + 15) / 16;
@@ -1704,7 +1702,7 @@ static GemmPlan plan_gemm(int qt, int M, int N, int K, int flags) {
         const int cap = stream_ups_cap(qt, p.split);
         int ups = cap;
         if (env_ups == 1 || env_ups == 2 || env_ups == 4) {
-            ups = env_ups;
+            ups = std::min(env_ups, cap);
         } else {
             for (int u : {1, 2, 4})
                 if (u <= cap && nw * u >= n_units) { ups = u; break; }
@@ -1770,43 +1768,27 @@ static hipError_t dispatch_mt(const GemmPlan &p, const uint8_t *W, const float *
                   p.stream ? ws + p.off_mfrag : nullptr, (float *)(ws + p.off_ssq)};
     float *part = (float *)(ws + p.off_part);
     if (p.stream && p.MT > 1) {
-        if (p.tall) {
 #define WM(mt, nw) return p.split ? launch_w<QT, true, PK, mt, nw>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st) \
-                                  : launch_w<QT, false, PK, mt, nw>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
-            // (instantiated only where tall_waves allows two waves per SIMD)
-            constexpr bool w8s2 = tall_waves(QT, true, 2) == 8, w8s3 = tall_waves(QT, true, 3) == 8,
-                           w8s4 = tall_waves(QT, true, 4) == 8, w8h2 = tall_waves(QT, false, 2) == 8,
-                           w8h3 = tall_waves(QT, false, 3) == 8, w8h4 = tall_waves(QT, false, 4) == 8;
-            if (p.NW == 8) {
-                if (p.split) {
-                    if constexpr (w8s2) if (p.MT == 2) return launch_w<QT, true, PK, 2, 8>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st);
-                    if constexpr (w8s3) if (p.MT == 3) return launch_w<QT, true, PK, 3, 8>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st);
-                    if constexpr (w8s4) if (p.MT == 4) return launch_w<QT, true, PK, 4, 8>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st);
-                } else {
-                    if constexpr (w8h2) if (p.MT == 2) return launch_w<QT, false, PK, 2, 8>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st);
-                    if constexpr (w8h3) if (p.MT == 3) return launch_w<QT, false, PK, 3, 8>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st);
-                    if constexpr (w8h4) if (p.MT == 4) return launch_w<QT, false, PK, 4, 8>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st);
-                }
-                return hipErrorInvalidValue;  // (the plan picks 8 waves only where instantiated)
-            }
-            switch (p.MT) { case 2: WM(2, 4); case 3: WM(3, 4); default: WM(4, 4); }
-#undef WM
+                              : launch_w<QT, false, PK, mt, nw>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
+        // (8 waves instantiated only where tall_waves allows two per SIMD)
+        if (p.NW == 8) {
+#define W8(sp, mt) if constexpr (tall_waves(QT, sp, mt) == 8) if (p.split == sp && p.MT == mt) \
+    return launch_w<QT, sp, PK, mt, 8>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
+            W8(true, 2); W8(true, 3); W8(true, 4); W8(false, 2); W8(false, 3); W8(false, 4);
+#undef W8
+            return hipErrorInvalidValue;  // (the plan picks 8 waves only where instantiated)
         }
-#define VM(mt) return p.split ? launch_v<QT, 4, 1, true, PK, mt>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st) \
-                              : launch_v<QT, 4, 1, false, PK, mt>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
-        switch (p.MT) { case 2: VM(2); case 3: VM(3); default: VM(4); }
-#undef VM
+        switch (p.MT) { case 2: WM(2, 4); case 3: WM(3, 4); default: WM(4, 4); }
+#undef WM
     }
     if (p.stream) {
-#define V(nw, u, sp) return launch_v<QT, nw, u, sp, PK, 1>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
-#define VU(nw, sp) switch (p.UPS) { case 1: V(nw, 1, sp); case 2: V(nw, 2, sp); default: V(nw, 4, sp); }
-        if (p.NW == 8) {
-            if (p.split) { VU(8, true); } else { VU(8, false); }
-        } else {
-            if (p.split) { VU(4, true); } else { VU(4, false); }
-        }
-#undef VU
+        // (instantiated up to the units per wave stream_ups_cap allows)
+#define V(nw, u, sp) if constexpr (u <= stream_ups_cap(QT, sp)) if (p.NW == nw && p.UPS == u && p.split == sp) \
+    return launch_v<QT, nw, u, sp, PK, 1>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
+        V(8, 1, true); V(8, 2, true); V(8, 4, true); V(8, 1, false); V(8, 2, false); V(8, 4, false);
+        V(4, 1, true); V(4, 2, true); V(4, 4, true); V(4, 1, false); V(4, 2, false); V(4, 4, false);
 #undef V
+        return hipErrorInvalidValue;  // (the plan keeps UPS within the cap)
     }
 #define L(mt, sp) return launch_t<QT, mt, sp, PK>(W, X, in, Y, M, N, K, p.ups, p.S, p.G, accum, a, part, st)
     if (p.split) {
