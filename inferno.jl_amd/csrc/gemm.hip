@@ -1067,14 +1067,15 @@ __device__ __forceinline__ void compute_v(const Unit<QT> &r, const AReg<QT> (&a)
     }
 }
 
-// (several token tiles: one wave per SIMD, so a wave may use the whole register file)
+// One token tile (MT = 1; several tiles run gemm_w_kernel).
 template <int QT, int NW, int UPS, bool SPLIT, bool PK, int MT>
-__global__ __launch_bounds__(NW * 64, MT > 1 ? 1 : 8 / NW)
+__global__ __launch_bounds__(NW * 64, 8 / NW)
 void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, int N, int K, int accum,
                    const uint8_t *__restrict__ afrag, const float *__restrict__ invs,
                    const uint8_t *__restrict__ mfrag, const float *__restrict__ ssq, float eps,
                    float *__restrict__ part) {
     using C = GemmCfg<QT>;
+    static_assert(MT == 1, "one token tile");
     constexpr int TOKT = SPLIT ? 8 : 16;  // tokens per MFMA tile
     constexpr int TOK = MT * TOKT;
     constexpr int TPL = SPLIT ? 2 : 4;
@@ -1082,9 +1083,8 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     constexpr int R = 4;
     static_assert(R % UPS == 0, "ring positions must map to fixed units");
     // partial tiles meet in LDS in batches of F tiles (double-buffered), one
-    // barrier per batch (Q6_K, short of registers, and several token tiles,
-    // short of LDS: one tile per batch)
-    constexpr int F = (QT == QT_Q6_K || MT > 1) ? 1 : (TPL == 4) ? NW / 2 : NW;
+    // barrier per batch (Q6_K, short of registers: one tile per batch)
+    constexpr int F = QT == QT_Q6_K ? 1 : (TPL == 4) ? NW / 2 : NW;
     __shared__ __align__(16) float red[2][F][NW][64][TPL * MT];
     __shared__ float rs[TOK];  // RMSNorm row scales (1 without RMSNorm)
     __shared__ float rsp[NW * 64];
