@@ -135,11 +135,11 @@ class VerifyStep:
 
     def forward(self):
         """The target forward of one verify step: per layer [residual += previous down] + RMSNorm
-        -> [q; k; v] -> o (+= into the residual) -> RMSNorm -> [gate; up] ->
-        SiLU gating -> down (left as K-slice partials); final residual add +
+        -> [q; k; v] -> o -> [residual += o] + RMSNorm -> [gate; up] -> SiLU
+        gating -> down (left as K-slice partials); final residual add +
         RMSNorm -> lm_head -> accept. RMSNorm, SiLU gating and the residual
-        add of the down projection run inside the input stage of the matmul
-        that consumes them."""
+        adds of o and down run inside the input stage of the matmul that
+        consumes them."""
         ih, F, M = self.ih, self.ih.formats, self.M
         P = self.model.proj
         ex = ih.gemm_q_ex
@@ -147,11 +147,13 @@ class VerifyStep:
         acc = f32 | ih.GEMM_ACCUM
         dfr = f32 | ih.GEMM_DEFER
         parts = ih.gemm_partials(F.Q6_K, M, H, FF, f32, self.ws_down)
-        # K-sliced o and [gate; up] (several token tiles) leave their partials
-        # to the next input stage instead of a reduce launch
+        # o leaves its partials to the next input stage, which adds them into
+        # the residual while it reads it (no read-modify-write at the end of
+        # o, no reduce launch when K-sliced); K-sliced [gate; up] (several
+        # token tiles) likewise, summed by the SiLU-gating stage
         o_parts = ih.gemm_partials(P, M, H, NQ, f32, self.ws_o)
         gu_parts = ih.gemm_partials(P, M, 2 * FF, H, f32, self.ws)
-        fold_o, fold_gu = o_parts[1] > 1, gu_parts[1] > 1
+        fold_o, fold_gu = True, gu_parts[1] > 1
         self.x.copy_(self.x0)
         for i, lw in enumerate(self.model.layers):
             ex(P, lw["qkv"], self.x, NQ + 2 * NKV, H, act=ih.ACT_RMSNORM, norm_w=lw["attn_norm"], flags=f32,
