@@ -129,3 +129,32 @@ def test_fold_gate_up_partials(ih, M):
     with np.errstate(over="ignore"):
         h = (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
     assert rel_l2(yf.cpu().numpy(), O.gemv_f64(F.Q6_K, wd, h, M, H, FF)) <= (SANITY_HALF if M > 16 else TOL_F32)
+
+
+@pytest.mark.parametrize("qt", [F.Q4_K, F.Q6_K])
+def test_fold_split_launch(ih, qt):
+    """fp32-accurate M = 40 runs as two launches (32 + 8 tokens); slices given
+    directly: the SiLU-gating input as the sum of two [M x 2K] slices (x
+    absent) and a residual fold of two [M x K] slices both equal the
+    explicit sum followed by the plain call, bit for bit."""
+    import torch
+    N, K, M = 96, 512, 40
+    w = synth.matrix(qt, N, K, synth.stream_for(40, f"split{qt}"))
+    wp = ih.pack_weights(qt, _dev(w), N, K)
+    fl = ih.GEMM_F32 | ih.GEMM_PACKED
+    g = torch.Generator(device="cpu").manual_seed(qt)
+    sl = torch.randn(2, M, 2 * K, generator=g).cuda()
+    y1 = ih.gemm_q_ex(qt, wp, None, N, K, act=ih.ACT_SILU_MUL, flags=fl,
+                      add=(sl.data_ptr(), 2, M * 2 * K), m=M, ldx=2 * K)
+    y2 = ih.gemm_q_ex(qt, wp, (sl[0] + sl[1]).contiguous(), N, K, act=ih.ACT_SILU_MUL, flags=fl)
+    assert torch.equal(y1, y2)
+    sr = torch.randn(2, M, K, generator=g).cuda()
+    x0 = torch.randn(M, K, generator=g).cuda()
+    xa = x0.clone()
+    ya = ih.gemm_q_ex(qt, wp, xa, N, K, act=ih.ACT_RMSNORM, flags=fl, add=(sr.data_ptr(), 2, M * K))
+    xb = x0 + (sr[0] + sr[1])
+    yb = ih.gemm_q_ex(qt, wp, xb.clone(), N, K, act=ih.ACT_RMSNORM, flags=fl)
+    assert torch.equal(xa, xb)
+    assert torch.equal(ya, yb)
+    n = np.stack([O.rmsnorm(r, 1e-6) for r in xb.cpu().numpy()]).astype(np.float32)
+    assert rel_l2(ya.cpu().numpy(), O.gemv_f64(qt, w, n, M, N, K)) <= TOL_F32
