@@ -700,17 +700,26 @@ __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ X, 
     norm_weights(norm_w, op, k, K, wa, wb);
     float v[8];
     if (t < M && k < K) {
-        // the sum of the partial slices at column c of row t
+        // the sum of the partial slices at column c of row t, in slice order
+        // (loads issued four slices at a time)
         auto slices = [&](int64_t rs, int c, float (&sum)[8]) {
 #pragma unroll
             for (int e = 0; e < 8; e++) sum[e] = 0.f;
-            for (int sl = 0; sl < n_add; sl++) {
-                const float *pa = add + (size_t)sl * add_stride + (size_t)t * rs + c;
-                const float4 a = *(const float4 *)pa;
-                const float4 b = *(const float4 *)(pa + 4);
-                const float pv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            for (int s0 = 0; s0 < n_add; s0 += 4) {
+                float4 va[4], vb[4];
 #pragma unroll
-                for (int e = 0; e < 8; e++) sum[e] = sl == 0 ? pv[e] : sum[e] + pv[e];
+                for (int j = 0; j < 4; j++) {
+                    const float *pa = add + (size_t)min(s0 + j, n_add - 1) * add_stride + (size_t)t * rs + c;
+                    va[j] = *(const float4 *)pa;
+                    vb[j] = *(const float4 *)(pa + 4);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    if (s0 + j >= n_add) break;
+                    const float pv[8] = {va[j].x, va[j].y, va[j].z, va[j].w, vb[j].x, vb[j].y, vb[j].z, vb[j].w};
+#pragma unroll
+                    for (int e = 0; e < 8; e++) sum[e] = s0 + j == 0 ? pv[e] : sum[e] + pv[e];
+                }
             }
         };
         float up[8];
