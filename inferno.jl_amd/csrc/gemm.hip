@@ -685,16 +685,16 @@ __device__ __forceinline__ void prep_finish(float (&v)[8], float4 wa, float4 wb,
 // into x (each element has one owner thread), before the transform; slices
 // [M][K]. X == nullptr: x is that sum itself (slices [M][ldx], rows of 2K
 // for ACT_SILU_MUL), nothing is stored back.
-template <int LK, int MT, bool SPLIT, bool MINS>
-__global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ X, int ldx, int M, int K, int op,
+template <int LK, int MT, bool SPLIT, bool MINS, int TPW>
+__global__ __launch_bounds__(32 * TPW) void prep_kernel(const float *__restrict__ X, int ldx, int M, int K, int op,
                                                    const float *__restrict__ norm_w,
                                                    uint8_t *__restrict__ afrag, float *__restrict__ xs,
                                                    float *__restrict__ inv, uint8_t *__restrict__ mfrag,
                                                    float *__restrict__ ssq, const float *__restrict__ add, int n_add,
                                                    int64_t add_stride, float *__restrict__ xw) {
     const int u = blockIdx.x, tid = threadIdx.x;
-    const int tl = tid >> 5, gi = tid & 31;
-    const int t = blockIdx.y * 8 + tl;
+    const int tl = tid >> 5, gi = tid & 31;  // (a token per 32 threads, TPW per workgroup)
+    const int t = blockIdx.y * TPW + tl;
     const int k = u * UNIT + gi * 8;
     float4 wa, wb;
     norm_weights(norm_w, op, k, K, wa, wb);
@@ -1578,14 +1578,26 @@ struct ActWs {
     float *ssq;
 };
 
+int env_int_prep(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return v ? atoi(v) : dflt;
+}
+
 template <int QT, int MT, bool SPLIT>
 hipError_t launch_prep(const float *X, const ActIn &in, int M, int K, const ActWs &a, hipStream_t st) {
     using C = GemmCfg<QT>;
     constexpr int TOK = MT * (SPLIT ? 8 : 16);
     const int n_units = (K + UNIT - 1) / UNIT;
-    prep_kernel<QT == QT_Q6_K ? 1 : QT == QT_Q8_0 ? 2 : 0, MT, SPLIT, C::MINS><<<dim3(n_units, TOK / 8), 256, 0, st>>>(
-        X, in.ldx, M, K, in.op, in.norm_w, a.afrag, a.xs, a.inv, a.mfrag, a.ssq, in.add, in.n_add, in.add_stride,
-        const_cast<float *>(X));
+    constexpr int LK = QT == QT_Q6_K ? 1 : QT == QT_Q8_0 ? 2 : 0;
+    // tokens per workgroup: 2 (one wave) spreads the stage over the most CUs
+    // (measured: the verify step 1.1 % faster than 8 per workgroup; the
+    // M = 64 tree forward unchanged); IHIP_PREP_TPW selects 4 or 8
+    static const int tpw = env_int_prep("IHIP_PREP_TPW", 2);
+#define PREP(tp) prep_kernel<LK, MT, SPLIT, C::MINS, tp><<<dim3(n_units, TOK / tp), 32 * tp, 0, st>>>( \
+        X, in.ldx, M, K, in.op, in.norm_w, a.afrag, a.xs, a.inv, a.mfrag, a.ssq, in.add, in.n_add, in.add_stride, \
+        const_cast<float *>(X))
+    if (tpw == 2) PREP(2); else if (tpw == 4) PREP(4); else PREP(8);
+#undef PREP
     return hipGetLastError();
 }
 
