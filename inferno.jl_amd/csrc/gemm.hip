@@ -1578,7 +1578,8 @@ struct ActWs {
     float *ssq;
 };
 
-int env_int_prep(const char *name, int dflt) {
+// Integer tuning override from the environment (read once per call site).
+int env_int(const char *name, int dflt) {
     const char *v = getenv(name);
     return v ? atoi(v) : dflt;
 }
@@ -1592,7 +1593,7 @@ hipError_t launch_prep(const float *X, const ActIn &in, int M, int K, const ActW
     // tokens per workgroup: 2 (one wave) spreads the stage over the most CUs
     // (measured: the verify step 1.1 % faster than 8 per workgroup; the
     // M = 64 tree forward unchanged); IHIP_PREP_TPW selects 4 or 8
-    static const int tpw = env_int_prep("IHIP_PREP_TPW", 2);
+    static const int tpw = env_int("IHIP_PREP_TPW", 2);
 #define PREP(tp) prep_kernel<LK, MT, SPLIT, C::MINS, tp><<<dim3(n_units, TOK / tp), 32 * tp, 0, st>>>( \
         X, in.ldx, M, K, in.op, in.norm_w, a.afrag, a.xs, a.inv, a.mfrag, a.ssq, in.add, in.n_add, in.add_stride, \
         const_cast<float *>(X))
@@ -1674,10 +1675,6 @@ struct GemmPlan {
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-static int env_int(const char *name, int dflt) {
-    const char *v = getenv(name);
-    return v ? atoi(v) : dflt;
-}
 
 size_t packed_bytes(int qt, int N, int K);
 
