@@ -219,13 +219,42 @@ class TreeStep(VerifyStep):
             q._stream(None)))
 
 
-def gemm_roofline(ih, model: Model, n_layers: int, M: int, iters: int = 64, replays: int = 3):
+def graph_launch_time(launch, iters: int, replays: int, warm: int) -> float:
+    """`iters` calls of launch(i) captured in one HIP graph on a side stream,
+    replayed `warm` times untimed, then `replays` times with an event pair
+    around each replay on that stream: the median replay over `iters`, in
+    seconds per launch."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        for i in range(iters):
+            launch(i)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
+    with torch.cuda.stream(s):  # replay() launches on the current stream
+        for _ in range(warm):
+            graph.replay()
+        torch.cuda.synchronize()
+        ev[0].record(s)
+        for r in range(replays):
+            graph.replay()
+            ev[r + 1].record(s)
+    ev[-1].synchronize()
+    per = sorted(ev[r].elapsed_time(ev[r + 1]) for r in range(replays))
+    del graph
+    return per[len(per) // 2] * 1e-3 / iters
+
+
+def gemm_roofline(ih, model: Model, n_layers: int, M: int, iters: int = 64, replays: int = 15, warm: int = 4):
     """Dominant kernel: the Q4_K gate/up dequant-matmul (24576x4096, M=5)
     over the layers' weights in turn (1.8 GB, far beyond the 256 MB cache).
     The activations are prepared once; `iters` matmul launches that reuse
-    them are captured in a HIP graph and timed with events on the graph's
-    stream, so the per-launch figure is the matmul kernel plus its dispatch
-    gap. Returns (seconds per launch, algorithmic bytes per launch)."""
+    them are timed as one replayed graph (graph_launch_time): the matmul
+    kernel plus its dispatch gap, which is what a kernel trace reports as
+    its duration (its launches run back to back). Returns (seconds per
+    launch, algorithmic bytes per launch)."""
     import torch
     F = ih.formats
     N, K = 2 * FF, H
@@ -233,28 +262,12 @@ def gemm_roofline(ih, model: Model, n_layers: int, M: int, iters: int = 64, repl
     y = torch.empty((M, N), device="cuda")
     fl = ih.GEMM_F32 | ih.GEMM_PACKED
     ws = torch.empty(ih.quantized_kernels.gemm_ws_bytes(F.Q4_K, M, N, K, fl), dtype=torch.uint8, device="cuda")
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        ih.gemm_q_ex(F.Q4_K, model.layers[0]["gu"], x, N, K, flags=fl, out=y, ws=ws)  # prepares x
-        for i in range(4):
-            ih.gemm_q_ex(F.Q4_K, model.layers[i % n_layers]["gu"], x, N, K, flags=fl | ih.GEMM_REUSE, out=y, ws=ws)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=s):
-        for i in range(iters):
-            ih.gemm_q_ex(F.Q4_K, model.layers[i % n_layers]["gu"], x, N, K, flags=fl | ih.GEMM_REUSE, out=y,
-                         ws=ws)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(s):  # replay() launches on the current stream
-        graph.replay()
-        torch.cuda.synchronize()
-        e0.record(s)
-        for _ in range(replays):
-            graph.replay()
-        e1.record(s)
-    e1.synchronize()
-    t = e0.elapsed_time(e1) * 1e-3 / (replays * iters)
+    ih.gemm_q_ex(F.Q4_K, model.layers[0]["gu"], x, N, K, flags=fl, out=y, ws=ws)  # prepares x
+
+    def mat(i):
+        ih.gemm_q_ex(F.Q4_K, model.layers[i % n_layers]["gu"], x, N, K, flags=fl | ih.GEMM_REUSE, out=y, ws=ws)
+
+    t = graph_launch_time(mat, iters, replays, warm)
     alg = F.matrix_bytes(F.Q4_K, N, K) + M * K * 4 + M * N * 4
     return t, alg
 
@@ -264,7 +277,7 @@ def profile_kernels(ih, model: Model, n_layers: int, M: int):
     kernel of known traffic (ihip_add over 64 Mi floats: y += x reads 512 MiB,
     writes 256 MiB)."""
     import torch
-    gemm_roofline(ih, model, n_layers, M, replays=1)
+    gemm_roofline(ih, model, n_layers, M, replays=1, warm=1)
     n = 64 << 20
     a = torch.ones(n, device="cuda")
     b = torch.ones(n, device="cuda")
@@ -308,16 +321,14 @@ def read_traffic():
     return None
 
 
-def gemm_sweep(ih, model: Model, n_layers: int, launches: int = 32, replays: int = 3):
+def gemm_sweep(ih, model: Model, n_layers: int, launches: int = 32, replays: int = 5, warm: int = 2):
     """GB/s of the Q4_K gate/up and Q6_K down projections at M = 1..8: per M,
-    a HIP graph of `launches` matmuls over the layers' weights in turn (cold:
-    1.8 GB and 1.3 GB, far beyond the caches), timed with events on the
-    graph's stream."""
+    `launches` matmuls over the layers' weights in turn (cold: 1.8 GB and
+    1.3 GB, far beyond the caches) timed as one replayed graph
+    (graph_launch_time; per launch, dispatch gap included)."""
     import torch
     F = ih.formats
     out = {}
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
     for name, key, qt, N, K in (("q4k_24576x4096", "gu", F.Q4_K, 2 * FF, H),
                                 ("q6k_4096x12288", "down", F.Q6_K, H, FF)):
         row = {}
@@ -326,24 +337,12 @@ def gemm_sweep(ih, model: Model, n_layers: int, launches: int = 32, replays: int
             y = torch.empty((M, N), device="cuda")
             fl = ih.GEMM_F32 | ih.GEMM_PACKED
             ws = torch.empty(ih.quantized_kernels.gemm_ws_bytes(qt, M, N, K, fl), dtype=torch.uint8, device="cuda")
-            with torch.cuda.stream(s):
-                ih.gemm_q_ex(qt, model.layers[0][key], x, N, K, flags=fl, out=y, ws=ws)  # prepares x
-            torch.cuda.synchronize()
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=s):
-                for i in range(launches):
-                    ih.gemm_q_ex(qt, model.layers[i % n_layers][key], x, N, K, flags=fl | ih.GEMM_REUSE, out=y,
-                                 ws=ws)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            with torch.cuda.stream(s):
-                graph.replay()
-                torch.cuda.synchronize()
-                e0.record(s)
-                for _ in range(replays):
-                    graph.replay()
-                e1.record(s)
-            e1.synchronize()
-            t = e0.elapsed_time(e1) * 1e-3 / (replays * launches)
+            ih.gemm_q_ex(qt, model.layers[0][key], x, N, K, flags=fl, out=y, ws=ws)  # prepares x
+
+            def mat(i):
+                ih.gemm_q_ex(qt, model.layers[i % n_layers][key], x, N, K, flags=fl | ih.GEMM_REUSE, out=y, ws=ws)
+
+            t = graph_launch_time(mat, launches, replays, warm)
             gbs = (F.matrix_bytes(qt, N, K) + M * K * 4 + M * N * 4) / t / 1e9
             row[str(M)] = round(gbs, 1)
         out[name] = row
@@ -810,7 +809,8 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": read_traffic(),
             "kernel": "gemm_v_kernel<Q4_K>: packed Q4_K dequant-matmul 24576x4096, M=5, fp32-accurate "
-                      "(per launch incl. dispatch gap, activations prepared once)",
+                      "(activations prepared once); per launch in a replayed graph of 64 launches over cold "
+                      "weights, median of 15 replays, HIP events (dispatch gap included, as in a kernel trace)",
             "us_per_launch": round(t_op * 1e6, 2),
             "algorithmic_bytes": alg,
         },
