@@ -504,6 +504,25 @@ def config3(ih, n_steps: int = 4096, per_call: int = 6):
             "matmul_GBps": round(alg / t_gemm / 1e9, 1), "mean_accepted_fraction": round(acc_rate, 4)}
 
 
+def config4(ih, model: Model, replays: int = 20):
+    """Config 4 across its token counts: the full verify step (32 layers,
+    lm_head, accept at T = 0.8) at M = 1, 2, 4, 5, 8 with k = M - 1 drafts;
+    M = 1 has no draft, so it is the forward alone (a plain decode step).
+    fp32-accurate at every M (one token tile)."""
+    import torch
+    out = {}
+    for M in (1, 2, 4, 5, 8):
+        k = M - 1
+        step = VerifyStep(ih, model, M, max(k, 1), 0.8)  # (M = 1: the draft side is set up, not used)
+        t = graph_time(step.forward if k == 0 else step.run, replays=replays)
+        w = model.weight_bytes(len(model.layers))
+        out[str(M)] = {"k": k, "ms_per_step": round(t * 1e3, 4), "steps_per_s": round(1 / t, 1),
+                       "weight_GBps": round(w / t / 1e9, 1)}
+        del step
+        torch.cuda.empty_cache()
+    return out
+
+
 def config5(ih, model: Model):
     """Config 5: 64-node tree verify (32 layers and the lm_head at M = 64 on
     the half-precision MFMA path, then the tree accept walk), with the
@@ -714,7 +733,7 @@ def main():
     ap.add_argument("--profile-tall", action="store_true",
                     help="only run the M = 64 gate/up and down matmuls five times each (for rocprofv3 --pmc)")
     ap.add_argument("--configs", type=str, default="",
-                    help="instead of the bench line: measure BASELINE configs (comma list of 1,2,3,5, 'sampler' "
+                    help="instead of the bench line: measure BASELINE configs (comma list of 1,2,3,4,5, 'sampler' "
                          "for the draft-side sampler, 'gguf' for file-to-device loading), one JSON object per config")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -736,6 +755,8 @@ def main():
         for c in want:
             if c == "5":
                 res = config5(ih, Model(ih, args.layers, keep_gguf=0))
+            elif c == "4":
+                res = config4(ih, Model(ih, args.layers, keep_gguf=0))
             elif c == "sampler":
                 res = sampler_config(ih)
             elif c == "gguf":
