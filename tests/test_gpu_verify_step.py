@@ -170,12 +170,13 @@ def test_tree_step_end_to_end(ih):
     then the tree accept walk over a 64-node tree (branching 4, BFS order).
     The half-precision bar applies per matmul output, so every operation of
     the chain is checked against the oracle applied to the GPU's own inputs of
-    that operation (each fold as the change it makes to the residual): a
-    single fp16 limb per 256-element unit rounds the small elements next to
-    the large ones, and this synthetic chain (o fed by [q; k; v] itself, no
-    attention, residuals growing to ~1e6) compounds that to ~4e-2 over two
-    layers where every single operation stays near 2e-4. The walk over the
-    GPU logits is identical to the oracle's walk over the same logits."""
+    that operation (each fold as the change it makes to the residual): this
+    synthetic chain (o fed by [q; k; v] itself, no attention, residuals
+    growing to ~1e6) amplifies fp16-sized rounding of its matmul inputs to
+    ~1e-2 .. 4e-2 at the logits (the oracle chain alone, with random 2^-11
+    relative perturbations, does so too) while every single operation stays
+    near 2e-4. The walk over the GPU logits is identical to the oracle's
+    walk over the same logits."""
     import torch
     n, ex = 64, ih.gemm_q_ex
     layers, lm, out_norm, x0 = _weights(n)
