@@ -325,27 +325,41 @@ def gemm_sweep(ih, model: Model, n_layers: int, launches: int = 32, replays: int
     """GB/s of the Q4_K gate/up and Q6_K down projections at M = 1..8: per M,
     `launches` matmuls over the layers' weights in turn (cold: 1.8 GB and
     1.3 GB, far beyond the caches) timed as one replayed graph
-    (graph_launch_time; per launch, dispatch gap included)."""
+    (graph_launch_time; per launch, dispatch gap included); and the same at
+    the lm_head's shape in both formats (8 launches of one 350 / 510 MB
+    matrix), where the per-launch fixed cost is amortized."""
     import torch
     F = ih.formats
     out = {}
-    for name, key, qt, N, K in (("q4k_24576x4096", "gu", F.Q4_K, 2 * FF, H),
-                                ("q6k_4096x12288", "down", F.Q6_K, H, FF)):
+    # the lm_head shape (151936 x 4096: 510 MB in Q6_K, 350 MB in Q4_K, each
+    # beyond the 256 MB cache, so repeated launches stream it from HBM): the
+    # model's own lm_head, and a Q4_K matrix of that shape made for the sweep
+    big_q4k = ih.pack_weights(F.Q4_K, ih.quantized_kernels.synth_blocks(
+        F.Q4_K, ih.synth.stream_for(SEED, "sweep_q4k_big"), VOCAB * H // 256), VOCAB, H)
+    mats = {"gu": [lw["gu"] for lw in model.layers[:n_layers]], "down": [lw["down"] for lw in model.layers[:n_layers]],
+            "lm": [model.lm], "big_q4k": [big_q4k]}
+    for name, key, qt, N, K, n_launch in (("q4k_24576x4096", "gu", F.Q4_K, 2 * FF, H, launches),
+                                          ("q6k_4096x12288", "down", F.Q6_K, H, FF, launches),
+                                          ("q4k_151936x4096", "big_q4k", F.Q4_K, VOCAB, H, 8),
+                                          ("q6k_151936x4096", "lm", F.Q6_K, VOCAB, H, 8)):
         row = {}
+        ws_list = mats[key]
         for M in (1, 2, 4, 5, 8):
             x = ih.quantized_kernels.synth_gaussian(7 + M, M * K).view(M, K)
             y = torch.empty((M, N), device="cuda")
             fl = ih.GEMM_F32 | ih.GEMM_PACKED
             ws = torch.empty(ih.quantized_kernels.gemm_ws_bytes(qt, M, N, K, fl), dtype=torch.uint8, device="cuda")
-            ih.gemm_q_ex(qt, model.layers[0][key], x, N, K, flags=fl, out=y, ws=ws)  # prepares x
+            ih.gemm_q_ex(qt, ws_list[0], x, N, K, flags=fl, out=y, ws=ws)  # prepares x
 
             def mat(i):
-                ih.gemm_q_ex(qt, model.layers[i % n_layers][key], x, N, K, flags=fl | ih.GEMM_REUSE, out=y, ws=ws)
+                ih.gemm_q_ex(qt, ws_list[i % len(ws_list)], x, N, K, flags=fl | ih.GEMM_REUSE, out=y, ws=ws)
 
-            t = graph_launch_time(mat, launches, replays, warm)
+            t = graph_launch_time(mat, n_launch, replays, warm)
             gbs = (F.matrix_bytes(qt, N, K) + M * K * 4 + M * N * 4) / t / 1e9
             row[str(M)] = round(gbs, 1)
         out[name] = row
+    del big_q4k
+    torch.cuda.empty_cache()
     return out
 
 
