@@ -72,13 +72,21 @@ def test_packed_gemm_identical(ih, qt, N, K):
 
 
 def test_packed_q8_0_tail(ih):
-    """Q8_0 with K % 256 != 0: the padded blocks of the last unit add nothing."""
+    """Q8_0 with K % 256 != 0 (the last unit holds 5 of 8 blocks): the padded
+    blocks of the packed layout and the short last unit of the GGUF layout
+    add nothing, at one token tile and at several, fp32-accurate and half;
+    both layouts agree bit for bit."""
     qt = F.Q8_0
     N, K = 48, 32 * 13
     rng = np.random.default_rng(9)
     w = synth.matrix(qt, N, K, synth.stream_for(77, "tail"))
-    wp = ih.pack_weights(qt, _dev(w), N, K)
-    for M in (1, 5, 16):
+    wd = _dev(w)
+    wp = ih.pack_weights(qt, wd, N, K)
+    for M in (1, 5, 16, 24, 37, 64):
         x = rng.standard_normal((M, K)).astype(np.float32)
-        got = ih.gemm_q(qt, wp, _dev(x), N, K, flags=ih.GEMM_F32 | ih.GEMM_PACKED).cpu().numpy()
-        assert rel_l2(got, O.gemv_f64(qt, w, x, M, N, K)) < 1e-5
+        ref = O.gemv_f64(qt, w, x, M, N, K)
+        for fl, bar in ((ih.GEMM_F32, 1e-5), (ih.GEMM_HALF, 2e-3)):
+            got = ih.gemm_q(qt, wp, _dev(x), N, K, flags=fl | ih.GEMM_PACKED).cpu().numpy()
+            raw = ih.gemm_q(qt, wd, _dev(x), N, K, flags=fl).cpu().numpy()
+            assert rel_l2(got, ref) < bar, (M, fl)
+            assert np.array_equal(got, raw), (M, fl)
