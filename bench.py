@@ -95,7 +95,7 @@ class Model:
 class VerifyStep:
     """One verify step: layers, final norm, lm_head, accept."""
 
-    def __init__(self, ih, model: Model, M: int, k: int, T: float, prec: int = 1):
+    def __init__(self, ih, model: Model, M: int, k: int, T: float, prec: int = 1, draft_from_target: bool = True):
         import torch
         dev = "cuda"
         F = ih.formats
@@ -114,9 +114,15 @@ class VerifyStep:
         self.ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
         self.ws_down = torch.empty(wsb, dtype=torch.uint8, device=dev)  # holds the deferred down partials
         self.ws_o = torch.empty(wsb, dtype=torch.uint8, device=dev)  # the deferred o partials (when K-sliced)
-        # draft side (inputs of the verify step): draft logits, draft tokens, uniforms
-        noise = ih.quantized_kernels.synth_gaussian(st(SEED, "draft_logits"), k * VOCAB, 3.0).view(k, VOCAB)
-        self.drf = noise.contiguous()
+        # draft side (inputs of the verify step): draft logits around the
+        # target rows (target + N(0, 1.5^2), as configs[2] draws them), draft
+        # tokens drawn from the draft softmax at T, uniforms
+        if draft_from_target and k <= M:
+            self.forward()  # the step's target logits (every timed step recomputes the same)
+            self.drf = ih.quantized_kernels.synth_gaussian(st(SEED, "draft_logits"), k * VOCAB, 1.5,
+                                                           add=self.logits[:k].contiguous()).view(k, VOCAB)
+        else:
+            self.drf = ih.quantized_kernels.synth_gaussian(st(SEED, "draft_logits"), k * VOCAB, 3.0).view(k, VOCAB)
         g = torch.Generator(device="cpu").manual_seed(SEED)
         p = torch.softmax(self.drf.cpu().double() / T, -1)
         self.draft = torch.multinomial(p, 1, generator=g).view(1, k).to(torch.int32).to(dev)
@@ -133,13 +139,17 @@ class VerifyStep:
         self.forward()
         self.accept()
 
-    def forward(self):
+    def forward(self, probe=None):
         """The target forward of one verify step: per layer [residual += previous down] + RMSNorm
         -> [q; k; v] -> o -> [residual += o] + RMSNorm -> [gate; up] -> SiLU
         gating -> down (left as K-slice partials); final residual add +
         RMSNorm -> lm_head -> accept. RMSNorm, SiLU gating and the residual
         adds of o and down run inside the input stage of the matmul that
-        consumes them."""
+        consumes them. probe(tag, layer), when given, is called (outside any
+        graph capture) before each layer's [q; k; v] ("pre"), after it
+        ("qkv"), after o ("o"), after [gate; up] ("gu") and after the
+        lm_head ("head"), so a test can read x, qkv, gu, logits and the
+        deferred partials in the workspaces at each point."""
         ih, F, M = self.ih, self.ih.formats, self.M
         P = self.model.proj
         ex = ih.gemm_q_ex
@@ -156,15 +166,23 @@ class VerifyStep:
         fold_o, fold_gu = True, gu_parts[1] > 1
         self.x.copy_(self.x0)
         for i, lw in enumerate(self.model.layers):
+            if probe:
+                probe("pre", i)
             ex(P, lw["qkv"], self.x, NQ + 2 * NKV, H, act=ih.ACT_RMSNORM, norm_w=lw["attn_norm"], flags=f32,
                out=self.qkv, ws=self.ws, add=parts if i > 0 else None)
+            if probe:
+                probe("qkv", i)
             if fold_o:
                 ex(P, lw["o"], self.qkv[:, :NQ], H, NQ, flags=dfr, ws=self.ws_o)
             else:
                 ex(P, lw["o"], self.qkv[:, :NQ], H, NQ, flags=acc, out=self.x, ws=self.ws)
+            if probe:
+                probe("o", i)
             ex(P, lw["gu"], self.x, 2 * FF, H, act=ih.ACT_RMSNORM, norm_w=lw["ffn_norm"],
                flags=dfr if fold_gu else f32, out=None if fold_gu else self.gu, ws=self.ws,
                add=o_parts if fold_o else None)
+            if probe:
+                probe("gu", i)
             if fold_gu:
                 ex(F.Q6_K, lw["down"], None, H, FF, act=ih.ACT_SILU_MUL, flags=dfr, ws=self.ws_down, add=gu_parts,
                    m=M, ldx=2 * FF)
@@ -172,6 +190,24 @@ class VerifyStep:
                 ex(F.Q6_K, lw["down"], self.gu, H, FF, act=ih.ACT_SILU_MUL, flags=dfr, ws=self.ws_down)
         ex(F.Q6_K, self.model.lm, self.x, VOCAB, H, act=ih.ACT_RMSNORM, norm_w=self.model.out_norm, flags=f32,
            out=self.logits, ws=self.ws, add=parts)
+        if probe:
+            probe("head", len(self.model.layers))
+
+    def accept_histogram(self, n_steps: int = 256):
+        """Accepted lengths of n_steps verify steps over this step's logits,
+        each with its own draft tokens (drawn from the draft softmax at T) and
+        uniforms: counts of out_n = 0..k (one batched accept call, untimed)."""
+        import torch
+        k, dev = self.k, self.logits.device
+        g = torch.Generator(device="cpu").manual_seed(SEED + 11)
+        p = torch.softmax(self.drf.cpu().double() / self.T, -1)
+        draft = torch.multinomial(p, n_steps, replacement=True, generator=g).t().contiguous().to(torch.int32).to(dev)
+        tgt = self.logits[:k + 1].unsqueeze(0).expand(n_steps, k + 1, VOCAB).contiguous()
+        drf = self.drf.unsqueeze(0).expand(n_steps, k, VOCAB).contiguous()
+        ua = torch.rand((n_steps, k), generator=g).to(dev)
+        ur, ub = torch.rand(n_steps, generator=g).to(dev), torch.rand(n_steps, generator=g).to(dev)
+        _, n = self.ih.spec_accept(tgt, drf, draft, self.T, ua, ur, ub)
+        return torch.bincount(n.cpu().long(), minlength=k + 1).tolist()
 
     def accept(self):
         self.ih.spec_accept(self.logits.view(1, self.M, VOCAB), self.drf.view(1, self.k, VOCAB), self.draft,
@@ -187,7 +223,7 @@ class TreeStep(VerifyStep):
 
     def __init__(self, ih, model: Model, n: int = 64, T: float = 1.0):
         import torch
-        super().__init__(ih, model, n, 1, T, prec=0)
+        super().__init__(ih, model, n, 1, T, prec=0, draft_from_target=False)
         st = ih.synth.stream_for
         par = [-1]
         for i in range(1, n):  # node i's parent: BFS over branching 4
@@ -305,6 +341,27 @@ def profile_tall(ih, reps: int = 5):
         ih.gemm_q_ex(F.Q6_K, dn, g, H, FF, act=ih.ACT_SILU_MUL, flags=ih.GEMM_PACKED)
     torch.cuda.synchronize()
     log(f"profile_tall: {reps} x (gate/up Q4_K 24576x4096, down Q6_K 4096x12288) at M = {M}")
+
+
+def read_peak(ih, sizes=(57_196_544, 510_504_960, 4_398_624_768), replays: int = 10):
+    """The plain-read ceiling beside the vendor peak: GB/s of ihip_stream_read
+    (16-byte loads, XOR sink) over buffers of the dominant matmul's weight
+    size, the lm_head's and one whole verify step's weights, each timed as the
+    median per replay of a graph of 8 launches over rotating copies (cold:
+    the copies of the small sizes together exceed the 256 MB cache)."""
+    import torch
+    out = {}
+    for nb in sizes:
+        copies = max(1, min(8, int(600e6 // nb) + 1))
+        bufs = [torch.empty(nb, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+        for b in bufs:
+            b.fill_(1)
+        sink = torch.zeros(2048, dtype=torch.int32, device="cuda")
+        t = graph_launch_time(lambda i: ih.quantized_kernels.stream_read(bufs[i % copies], out=sink), 8, replays, 2)
+        out[str(nb)] = round(nb / t / 1e9, 1)
+        del bufs
+        torch.cuda.empty_cache()
+    return out
 
 
 def read_traffic():
@@ -812,8 +869,12 @@ def main():
     ms = e0.elapsed_time(e1) / args.steps
     log(f"verify step: {ms:.3f} ms (wall {wall / args.steps * 1e3:.3f} ms), accepted n={int(step.out_n[0])}")
 
+    hist = step.accept_histogram()
+    log(f"accepted lengths over 256 draws on the step's logits: {hist}")
     t_op, alg = gemm_roofline(ih, model, args.layers, args.m)
     achieved = alg / t_op / 1e9
+    peaks = read_peak(ih)
+    log(f"plain-read ceiling (GB/s by buffer bytes): {peaks}")
     sweep = None if args.no_sweep else gemm_sweep(ih, model, args.layers)
     cpu = None if args.no_cpu else cpu_baseline(ih, model, args.layers, args.m, k, args.cpu_budget)
 
@@ -848,7 +909,15 @@ def main():
                       "weights, median of 15 replays, HIP events (dispatch gap included, as in a kernel trace)",
             "us_per_launch": round(t_op * 1e6, 2),
             "algorithmic_bytes": alg,
+            "measured_peak": max(peaks.values()),
+            "measured_peak_by_bytes": peaks,
+            "frac_of_measured_peak": round(achieved / max(peaks.values()), 4),
+            "step_frac": round(model.weight_bytes(args.layers) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "step_GBps": round(model.weight_bytes(args.layers) / (ms * 1e-3) / 1e9, 1),
         },
+        "accept": {"timed_step_accepted": int(step.out_n[0]),
+                   "accepted_length_histogram_256_draws": hist,
+                   "draft_logits": "target + N(0, 1.5^2)"},
         "cpu_baseline": cpu,
         "gemm_gbps_by_M": sweep,
     }

@@ -68,12 +68,19 @@ int ihip_available(void);
  *    (src/QuantizedKernels.jl:82-146).
  *    Host pointers; synchronous. weight is GGUF row-major blocks, row r
  *    owning blocks [r*K/QK, (r+1)*K/QK). The device copy of each weight is
- *    cached by (host pointer, byte size): weights must not change after
- *    their first use (ihip_weight_cache_clear() drops the cache). q8_buf is
- *    accepted and ignored (NULL allowed): the GPU path needs no Q8_K
- *    scratch. out[r] = sum_k W[r,k] x[k] computed fp32-accurately. On error
- *    nothing is written to out, the status is kept for ihip_last_error()
- *    and ihip_last_status(), and a message is printed to stderr.
+ *    cached by (host pointer, byte size, type, outer_dim, inner_dim) with a
+ *    fingerprint of sampled bytes (first, middle, last 256) checked on each
+ *    call, so a host buffer freed and reused at the same address with other
+ *    contents is uploaded again; weights are otherwise taken as immutable
+ *    after their first use (ihip_weight_cache_clear() drops the cache).
+ *    Cached bytes stay under INFERNO_HIP_WEIGHT_CACHE_BYTES (default 3/4 of
+ *    device memory), least recently used evicted first. q8_buf is accepted
+ *    and ignored (NULL allowed): the GPU path needs no Q8_K scratch.
+ *    out[r] = sum_k W[r,k] x[k] computed fp32-accurately. On error out[0 ..
+ *    outer_dim) is filled with NaN (these entry points return void like the
+ *    reference's, so the failure shows downstream), the status is kept for
+ *    ihip_last_error() and ihip_last_status(), and a message is printed to
+ *    stderr.
  * ====================================================================== */
 void q4_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_buf,
                int inner_dim, int outer_dim);
@@ -222,8 +229,12 @@ int ihip_softmax_stats(const float *logits_dev, int rows, int V, float T,
  * mode 1 = reference-compatible (T = 1 ratio with a scalar draft
  * probability and scalar residual, src/SpeculativeDecoding.jl:61-63,79-93).
  * out_tok [k+1] receives the accepted drafts followed by the resampled or
- * bonus token; out_n [1] the number of accepted drafts (0..k), or -1 for
- * a draft id outside [0, V). T must be > 0 (use ihip_greedy_verify for
+ * bonus token (out_n + 1 tokens); out_n [1] the number of accepted drafts
+ * (0..k), or -1 for a draft id outside [0, V). Mode 1 also reproduces the
+ * reference's bonus after a rejection of the last draft: when out_n ==
+ * k - 1, out_tok[k] holds a bonus token drawn from target row k at T with
+ * u_bonus (k + 1 tokens; src/SpeculativeDecoding.jl:100 appends it whenever
+ * length(accepted) == gamma). T must be > 0 (use ihip_greedy_verify for
  * T = 0); V <= 4194304, k <= 127. ws: ihip_spec_accept_ws_bytes() bytes, 16-byte
  * aligned. */
 int ihip_spec_accept_ws_bytes(int steps, int k, int V, size_t *bytes);
@@ -235,8 +246,10 @@ int ihip_spec_accept(const float *tgt_dev, const float *drf_dev,
                      void *stream);
 
 /* Greedy verify (mtp_verify_step!, src/ModelCPU.jl:1914-1930): per step,
- * logits [(k+1) x V]; out_argmax [k+1] = first-index argmax of each row;
- * out_n = leading i < k with out_argmax[i] == draft_tok[i]. */
+ * logits [(k+1) x V]; out_argmax [k+1] = first-index argmax of each row in
+ * Julia's isless order (-0.0 below +0.0, NaN above every number, so the
+ * first NaN wins; a row of -Inf gives index 0); out_n = leading i < k with
+ * out_argmax[i] == draft_tok[i]. */
 int ihip_greedy_verify(const float *logits_dev, const int32_t *draft_tok_dev,
                        int steps, int k, int V, int32_t *out_n_dev,
                        int32_t *out_argmax_dev, void *ws, size_t ws_bytes,
@@ -358,6 +371,14 @@ int ihip_synth_blocks(int qtype, uint64_t stream, int64_t first_block,
 int ihip_synth_gaussian(uint64_t stream, int64_t n, float scale,
                         const float *add_dev, float *out_dev,
                         void *stream_handle);
+
+/* HBM read-bandwidth probe (measurement only): streams `bytes` (a multiple
+ * of 16, src 16-byte aligned) with 16-byte loads, each of up to 2048
+ * workgroups XORing what it read into its own word of out_dev (2048
+ * words), so the plain-read ceiling can be reported beside the vendor peak
+ * for the matmul kernels whose bound is HBM. */
+int ihip_stream_read(const void *src_dev, size_t bytes, uint32_t *out_dev,
+                     void *stream);
 
 #ifdef __cplusplus
 }

@@ -162,17 +162,24 @@ __global__ void stats_merge_kernel(const float2 *__restrict__ part, int rows, in
     zsum[r] = ms.y;
 }
 
-// Sampling distribution of one verify step, set by the ratio tests:
+// Sampling distribution of one draw of a verify step, set by the ratio
+// tests:
 //   kind 0: p_j (target row, temperature Tp)       bonus draw
 //   kind 1: max(0, p_j - q_j)  (q: draft row)      standard residual
 //   kind 2: max(0, p_j - qs)   (qs: scalar q_i)    reference residual
 //   kind -1: invalid draft id (out_n = -1, nothing drawn)
+//   kind -2: no draw in this slot
 // fallback when the weights sum to 0: 1 = draw from p (standard mode),
 // 2 = return V - 1 (the reference's all-NaN residual, length(probs)).
+// pos: the index of the drawn token in the step's out_tok row. A step has
+// one draw slot in the standard mode and two in the reference mode, whose
+// second slot holds the bonus the reference appends after a rejection of
+// the last draft (src/SpeculativeDecoding.jl:100: length(accepted) == gamma).
 struct Decision {
-    int kind, n, prow, qrow, fallback, pad0, pad1, pad2;
+    int kind, n, prow, qrow, fallback, pos, pad1, pad2;
     float Tp, mp, sp, Tq, mq, sq, qs, u;
 };
+__host__ __device__ constexpr int draw_slots(int mode) { return mode == 1 ? 2 : 1; }
 
 __device__ __forceinline__ float p_of(const Decision &D, const float *lt, int j) {
     return __expf(lt[j] / D.Tp - D.mp) / D.sp;
@@ -293,15 +300,19 @@ __global__ __launch_bounds__(64) void decide_kernel(const float *__restrict__ tg
     // accepted drafts
     for (int i = lane; i < first; i += 64) out_tok[(size_t)step * (k + 1) + i] = dt[i];
     if (lane != 0) return;
-    Decision D{};
+    const int nd = draw_slots(mode);
+    Decision D{}, D2{};
+    D2.kind = -2;
     if (invalid) {
         D.kind = -1;
         D.n = -1;
         out_n[step] = -1;
-        dec[step] = D;
+        dec[(size_t)step * nd] = D;
+        if (nd > 1) dec[(size_t)step * nd + 1] = D2;
         return;
     }
     D.n = first;
+    D.pos = first;
     if (first < k) {
         const float2 pt = ms[first], pd = ms[k + 1 + first];
         D.kind = mode == 0 ? 1 : 2;
@@ -312,6 +323,17 @@ __global__ __launch_bounds__(64) void decide_kernel(const float *__restrict__ tg
         D.qs = f_q;
         D.u = u_res[step];
         D.fallback = mode == 0 ? 1 : 2;
+        if (mode == 1 && first == k - 1) {  // the reference's bonus after the residual
+            const float2 pk = ms[k];
+            D2.kind = 0;
+            D2.n = first;
+            D2.pos = first + 1;
+            D2.prow = k;
+            D2.Tp = T; D2.mp = pk.x; D2.sp = pk.y;
+            D2.Tq = T; D2.mq = 0.f; D2.sq = 1.f;
+            D2.u = u_bonus[step];
+            D2.fallback = 2;
+        }
     } else {
         const float2 pt = ms[k];
         D.kind = 0;
@@ -323,7 +345,8 @@ __global__ __launch_bounds__(64) void decide_kernel(const float *__restrict__ tg
         D.fallback = 2;
     }
     out_n[step] = first;
-    dec[step] = D;
+    dec[(size_t)step * nd] = D;
+    if (nd > 1) dec[(size_t)step * nd + 1] = D2;
 }
 
 // Sampling weights of the PER x NT entries of chunk c: thread t holds entries
@@ -366,14 +389,15 @@ __device__ void chunk_scan(const Decision &D, const float *lt, const float *ld, 
     __syncthreads();
 }
 
-// csum[step][c] = sum of w over chunk c: the sequential sum of its round
-// totals.
+// csum[step][slot][c] = sum of w over chunk c: the sequential sum of its
+// round totals (grid z = draw slot).
 __global__ __launch_bounds__(NT) void chunk_sum_kernel(const float *__restrict__ tgt, const float *__restrict__ drf,
                                                        int k, int V, const Decision *__restrict__ dec, int nchunk,
                                                        float *__restrict__ csum) {
     __shared__ float sh[PER * 4];
     const int c = blockIdx.x, step = blockIdx.y;
-    const Decision D = dec[step];
+    const size_t slot = (size_t)step * gridDim.z + blockIdx.z;
+    const Decision D = dec[slot];
     if (D.kind < 0) return;
     const float *lt = tgt + ((size_t)step * (k + 1) + D.prow) * V;
     const float *ld = D.kind == 1 ? drf + ((size_t)step * k + D.qrow) * V : nullptr;
@@ -382,7 +406,7 @@ __global__ __launch_bounds__(NT) void chunk_sum_kernel(const float *__restrict__
     float sw = 0.f;
 #pragma unroll
     for (int r = 0; r < PER; r++) sw += cs.R[r];
-    if (threadIdx.x == 0) csum[(size_t)step * nchunk + c] = sw;
+    if (threadIdx.x == 0) csum[slot * nchunk + c] = sw;
 }
 
 // First j with u * S <= C_j, where C_j = before(chunk) + (P_r + (off_w +
@@ -400,9 +424,10 @@ __global__ __launch_bounds__(NT) void sample_kernel(const float *__restrict__ tg
     __shared__ int s_chunk, s_usep, s_tok;
     __shared__ int s_first[NT / 64];
     const int step = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
-    const Decision D = dec[step];
+    const size_t slot = (size_t)step * gridDim.y + blockIdx.y;
+    const Decision D = dec[slot];
     if (D.kind < 0) return;
-    const float *cw = csum + (size_t)step * nchunk;
+    const float *cw = csum + slot * nchunk;
     const float *lt = tgt + ((size_t)step * (k + 1) + D.prow) * V;
     const float *ld = D.kind == 1 ? drf + ((size_t)step * k + D.qrow) * V : nullptr;
     for (int c = t; c < nchunk; c += NT) s_csum[c] = cw[c];
@@ -419,7 +444,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(const float *__restrict__ tg
     }
     __syncthreads();
     if (s_tok >= 0) {
-        if (t == 0) out_tok[(size_t)step * (k + 1) + D.n] = s_tok;
+        if (t == 0) out_tok[(size_t)step * (k + 1) + D.pos] = s_tok;
         return;
     }
     const bool usep = s_usep != 0;
@@ -486,11 +511,24 @@ __global__ __launch_bounds__(NT) void sample_kernel(const float *__restrict__ tg
         int f = NT;
         for (int w = 0; w < NT / 64; w++) f = min(f, s_first[w]);
         const int tok = min(c * CHUNK + rr * NT + (f < NT ? f : NT - 1), V - 1);
-        out_tok[(size_t)step * (k + 1) + D.n] = tok;
+        out_tok[(size_t)step * (k + 1) + D.pos] = tok;
     }
 }
 
-// Partial first-index argmax per (chunk, row).
+// Julia's findmax order (the argmax of mtp_verify_step!): isless, the total
+// order -Inf < ... < -0.0 < +0.0 < ... < +Inf < NaN; among equals (and among
+// NaNs) the first index wins. `beats` is the strict order, `first_of` picks
+// (value, index) pairs under it.
+__device__ __forceinline__ bool beats(float a, float b) {
+    if (isnan(a) || isnan(b)) return isnan(a) && !isnan(b);
+    return a > b || (a == b && signbit(b) && !signbit(a));
+}
+__device__ __forceinline__ bool first_of(float v2, int i2, float bv, int bi) {
+    return beats(v2, bv) || (!beats(bv, v2) && i2 < bi);
+}
+
+// Partial first-index argmax per (chunk, row). Every thread of a non-empty
+// chunk holds a real index (a row of -Inf gives its first index).
 __global__ __launch_bounds__(NT) void argmax_partial_kernel(const float *__restrict__ L, int V, int nchunk,
                                                             float2 *__restrict__ part) {
     __shared__ float sv[NT / 64];
@@ -502,19 +540,19 @@ __global__ __launch_bounds__(NT) void argmax_partial_kernel(const float *__restr
     int bi = 0x7fffffff;
     for (int j = j0 + threadIdx.x; j < j1; j += NT) {
         const float v = src[j];
-        if (v > bv) { bv = v; bi = j; }  // strided: first j per thread wins ties
+        if (first_of(v, j, bv, bi)) { bv = v; bi = j; }
     }
     for (int o = 32; o > 0; o >>= 1) {
         const float v2 = __shfl_xor(bv, o);
         const int i2 = __shfl_xor(bi, o);
-        if (v2 > bv || (v2 == bv && i2 < bi)) { bv = v2; bi = i2; }
+        if (first_of(v2, i2, bv, bi)) { bv = v2; bi = i2; }
     }
     const int w = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) { sv[w] = bv; si[w] = bi; }
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int i = 1; i < NT / 64; i++)
-            if (sv[i] > bv || (sv[i] == bv && si[i] < bi)) { bv = sv[i]; bi = si[i]; }
+            if (first_of(sv[i], si[i], bv, bi)) { bv = sv[i]; bi = si[i]; }
         part[(size_t)row * nchunk + chunk] = make_float2(bv, __int_as_float(bi));
     }
 }
@@ -529,8 +567,8 @@ __global__ void greedy_kernel(const float2 *__restrict__ part, int nchunk, const
         const float2 *p = part + ((size_t)step * (k + 1) + i) * nchunk;
         float bv = p[0].x;
         int bi = __float_as_int(p[0].y);
-        for (int c = 1; c < nchunk; c++)
-            if (p[c].x > bv) { bv = p[c].x; bi = __float_as_int(p[c].y); }  // chunks ascend: strict > keeps first
+        for (int c = 1; c < nchunk; c++)  // chunks ascend: the strict order keeps the first
+            if (beats(p[c].x, bv)) { bv = p[c].x; bi = __float_as_int(p[c].y); }
         if (out_argmax) out_argmax[(size_t)step * (k + 1) + i] = bi;
         if (i < k && go) {
             if (bi == draft_tok[(size_t)step * k + i]) n++;
@@ -626,20 +664,21 @@ hipError_t launch_stats_merge(const float2 *part, int rows, int V, float *zmax, 
 
 size_t spec_accept_ws(int steps, int k, int V) {
     const size_t nc = accept_nchunk(V);
-    return (size_t)steps * (2 * k + 1) * nc * sizeof(float2) + (size_t)steps * sizeof(Decision) +
-           (size_t)steps * nc * sizeof(float) + 256;
+    return (size_t)steps * (2 * k + 1) * nc * sizeof(float2) + (size_t)steps * 2 * sizeof(Decision) +
+           (size_t)steps * 2 * nc * sizeof(float) + 256;
 }
 
-// ws: float2 part[steps*(k+1) + steps*k][nchunk], Decision dec[steps],
-// float csum[steps][nchunk].
+// ws: float2 part[steps*(k+1) + steps*k][nchunk], Decision dec[steps][slots],
+// float csum[steps][slots][nchunk] (slots = draw_slots(mode)).
 hipError_t launch_spec_accept(const float *tgt, const float *drf, const int32_t *draft_tok, int steps, int k,
                               int V, float T, const float *u_acc, const float *u_res, const float *u_bonus,
                               int mode, int32_t *out_tok, int32_t *out_n, void *ws, hipStream_t st) {
     const int nc = accept_nchunk(V);
     const float Tr = mode == 0 ? T : 1.0f;
+    const int nd = draw_slots(mode);
     float2 *part = (float2 *)ws;
     Decision *dec = (Decision *)(part + (size_t)steps * (2 * k + 1) * nc);
-    float *csum = (float *)(dec + steps);
+    float *csum = (float *)(dec + (size_t)steps * nd);
     stats_partial_kernel<<<dim3(nc, steps * (2 * k + 1)), NT, 0, st>>>(tgt, steps * (k + 1), Tr, T, k + 1,
                                                                       drf, Tr, V, nc, part);
     hipError_t e = hipGetLastError();
@@ -647,9 +686,9 @@ hipError_t launch_spec_accept(const float *tgt, const float *drf, const int32_t 
     decide_kernel<<<steps, 64, 0, st>>>(tgt, drf, draft_tok, k, V, T, u_acc, u_res, u_bonus, mode, part, nc,
                                         out_tok, out_n, dec);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    chunk_sum_kernel<<<dim3(nc, steps), NT, 0, st>>>(tgt, drf, k, V, dec, nc, csum);
+    chunk_sum_kernel<<<dim3(nc, steps, nd), NT, 0, st>>>(tgt, drf, k, V, dec, nc, csum);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    sample_kernel<<<steps, NT, 0, st>>>(tgt, drf, k, V, dec, nc, csum, out_tok);
+    sample_kernel<<<dim3(steps, nd), NT, 0, st>>>(tgt, drf, k, V, dec, nc, csum, out_tok);
     return hipGetLastError();
 }
 

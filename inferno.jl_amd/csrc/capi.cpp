@@ -54,6 +54,7 @@ hipError_t launch_sample(const float *L, int rows, int V, float T, int top_k, fl
 hipError_t launch_penalties(float *L, int rows, int V, const int32_t *tok, int n_tok, int64_t tok_stride,
                             float presence, float repetition, hipStream_t st);
 hipError_t launch_gaussian(uint64_t stream, int64_t n, float scale, const float *add, float *out, hipStream_t st);
+hipError_t launch_stream_read(const void *src, int64_t bytes, uint32_t *out, hipStream_t st);
 
 namespace {
 
@@ -111,16 +112,54 @@ int check_gemm(int qt, const void *w, const float *x, float *y, int M, int N, in
 }
 
 // ---- library state for the host-pointer drop-ins ----
+// Device copies of drop-in weights, keyed by (host pointer, bytes, qtype, N,
+// K). Each entry keeps a fingerprint of sampled host bytes (first, middle
+// and last 256 bytes), checked on every call: a host buffer freed and
+// reallocated at the same address with other contents (a garbage-collected
+// array) is uploaded again instead of served stale. Entries are evicted
+// least recently used first when the cached bytes would pass the cap
+// (INFERNO_HIP_WEIGHT_CACHE_BYTES, default three quarters of the device's
+// memory).
+struct WKey {
+    const void *ptr;
+    size_t bytes;
+    int qt, N, K;
+    bool operator<(const WKey &o) const {
+        if (ptr != o.ptr) return ptr < o.ptr;
+        if (bytes != o.bytes) return bytes < o.bytes;
+        if (qt != o.qt) return qt < o.qt;
+        if (N != o.N) return N < o.N;
+        return K < o.K;
+    }
+};
+struct WEntry {
+    void *dev;
+    size_t dev_bytes;
+    uint64_t fingerprint;
+    uint64_t last_use;
+};
 struct Lib {
     std::mutex mu;
     bool inited = false;
     int init_status = IHIP_ENODEV;
     int device = 0;
     hipStream_t stream = nullptr;
-    std::map<std::pair<const void *, size_t>, void *> wcache;
+    std::map<WKey, WEntry> wcache;
+    size_t wcache_bytes = 0, wcache_cap = 0;
+    uint64_t use_clock = 0;
     float *dx = nullptr, *dy = nullptr, *dws = nullptr;
     size_t dx_cap = 0, dy_cap = 0, dws_cap = 0;
 };
+
+// FNV-1a over the first, middle and last (up to) 256 bytes of the weights.
+uint64_t weight_fingerprint(const uint8_t *p, size_t n) {
+    uint64_t h = 1469598103934665603ull;
+    const size_t span = n < 256 ? n : 256;
+    const size_t starts[3] = {0, (n - span) / 2, n - span};
+    for (size_t s : starts)
+        for (size_t i = 0; i < span; i++) h = (h ^ p[s + i]) * 1099511628211ull;
+    return h ^ n;
+}
 Lib &lib() {
     static Lib L;
     return L;
@@ -146,7 +185,25 @@ int init_locked(Lib &L, int device) {
     if ((e = hipStreamCreateWithFlags(&L.stream, hipStreamNonBlocking)) != hipSuccess)
         return L.init_status = hip_fail(e, "ihip_init");
     L.device = device;
+    const char *cap = getenv("INFERNO_HIP_WEIGHT_CACHE_BYTES");
+    L.wcache_cap = cap && *cap ? (size_t)strtoull(cap, nullptr, 10) : prop.totalGlobalMem / 4 * 3;
     return L.init_status = IHIP_OK;
+}
+
+void wcache_drop(Lib &L, std::map<WKey, WEntry>::iterator it) {
+    (void)hipFree(it->second.dev);
+    L.wcache_bytes -= it->second.dev_bytes;
+    L.wcache.erase(it);
+}
+
+// Evicts least-recently-used entries until `need` more bytes fit under the cap.
+void wcache_make_room(Lib &L, size_t need) {
+    while (!L.wcache.empty() && L.wcache_bytes + need > L.wcache_cap) {
+        auto lru = L.wcache.begin();
+        for (auto it = L.wcache.begin(); it != L.wcache.end(); ++it)
+            if (it->second.last_use < lru->second.last_use) lru = it;
+        wcache_drop(L, lru);
+    }
 }
 
 int grow(float **p, size_t *cap, size_t bytes) {
@@ -160,7 +217,10 @@ int grow(float **p, size_t *cap, size_t bytes) {
     return IHIP_OK;
 }
 
-// Drop-in GEMV: host pointers, synchronous on the library stream.
+// Drop-in GEMV: host pointers, synchronous on the library stream. On any
+// failure out[0..N) is filled with NaN (the reference's C entry points
+// return void, so an unmodified caller never reads the status: NaN makes the
+// failure visible downstream instead of leaving stale values).
 void dropin_gemv(const char *name, int qt, const uint8_t *weight, const float *x, float *out, int K, int N) {
     Lib &L = lib();
     std::lock_guard<std::mutex> lk(L.mu);
@@ -177,23 +237,32 @@ void dropin_gemv(const char *name, int qt, const uint8_t *weight, const float *x
     } else {
         (void)hipSetDevice(L.device);
         const size_t wbytes = (size_t)N * (K / block_elems(qt)) * block_bytes(qt);
-        auto key = std::make_pair((const void *)weight, wbytes);
+        const WKey key{(const void *)weight, wbytes, qt, N, K};
+        const uint64_t fp = weight_fingerprint(weight, wbytes);
         void *dw = nullptr;
         auto it = L.wcache.find(key);
+        if (it != L.wcache.end() && it->second.fingerprint != fp) {
+            wcache_drop(L, it);  // same address, other contents: upload again
+            it = L.wcache.end();
+        }
         hipError_t e = hipSuccess;
         if (it != L.wcache.end()) {
-            dw = it->second;
+            dw = it->second.dev;
+            it->second.last_use = ++L.use_clock;
         } else {
             // first call with this matrix: upload, repack once, keep the packed copy
+            const size_t pbytes = packed_bytes(qt, N, K);
+            wcache_make_room(L, pbytes);
             void *raw = nullptr;
             e = hipMalloc(&raw, wbytes);
-            if (e == hipSuccess) e = hipMalloc(&dw, packed_bytes(qt, N, K));
+            if (e == hipSuccess) e = hipMalloc(&dw, pbytes);
             if (e == hipSuccess) e = hipMemcpy(raw, weight, wbytes, hipMemcpyHostToDevice);
             if (e == hipSuccess) e = launch_pack(qt, raw, dw, N, K, L.stream);
             if (e == hipSuccess) e = hipStreamSynchronize(L.stream);
             if (raw) (void)hipFree(raw);
             if (e == hipSuccess) {
-                L.wcache[key] = dw;
+                L.wcache[key] = WEntry{dw, pbytes, fp, ++L.use_clock};
+                L.wcache_bytes += pbytes;
             } else if (dw) {
                 (void)hipFree(dw);
                 dw = nullptr;
@@ -213,7 +282,11 @@ void dropin_gemv(const char *name, int qt, const uint8_t *weight, const float *x
             rc = e == hipSuccess ? ok() : hip_fail(e, name);
         }
     }
-    if (rc != IHIP_OK) fprintf(stderr, "inferno_hip: %s\n", t_err.c_str());
+    if (rc != IHIP_OK) {
+        fprintf(stderr, "inferno_hip: %s\n", t_err.c_str());
+        if (out && N > 0)
+            for (int i = 0; i < N; i++) out[i] = __builtin_nanf("");
+    }
 }
 
 }  // namespace
@@ -249,8 +322,9 @@ int ihip_available(void) {
 void ihip_weight_cache_clear(void) {
     Lib &L = lib();
     std::lock_guard<std::mutex> lk(L.mu);
-    for (auto &kv : L.wcache) (void)hipFree(kv.second);
+    for (auto &kv : L.wcache) (void)hipFree(kv.second.dev);
     L.wcache.clear();
+    L.wcache_bytes = 0;
 }
 
 void q4_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_buf, int inner_dim, int outer_dim) {
@@ -593,6 +667,14 @@ int ihip_synth_gaussian(uint64_t stream, int64_t n, float scale, const float *ad
     if (n < 0) return fail(IHIP_EINVAL, "ihip_synth_gaussian: n=%lld", (long long)n);
     hipError_t e = launch_gaussian(stream, n, scale, add_dev, out_dev, S(stream_handle));
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_synth_gaussian");
+}
+
+int ihip_stream_read(const void *src_dev, size_t bytes, uint32_t *out_dev, void *stream) {
+    if (!src_dev || !out_dev) return fail(IHIP_EFAULT, "ihip_stream_read: NULL pointer");
+    if (!aligned16(src_dev) || (bytes & 15))
+        return fail(IHIP_EINVAL, "ihip_stream_read: src must be 16-byte aligned and bytes a multiple of 16");
+    hipError_t e = launch_stream_read(src_dev, (int64_t)bytes, out_dev, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_stream_read");
 }
 
 }  // extern "C"

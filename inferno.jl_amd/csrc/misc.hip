@@ -123,7 +123,42 @@ __global__ void add_kernel(float *__restrict__ y, const float *__restrict__ x, i
     if (i < n) y[i] += x[i];
 }
 
+// Read-bandwidth probe: every thread XORs the 16-byte words it streams (grid
+// stride, four loads in flight) and each workgroup stores its XOR in its own
+// word of out, so no load can be dropped, only one word per workgroup is
+// written and no atomic serializes the tail.
+__global__ __launch_bounds__(256) void stream_read_kernel(const uint4 *__restrict__ src, int64_t n16,
+                                                          uint32_t *__restrict__ out) {
+    __shared__ uint32_t sh[4];
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t acc = 0;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const uint4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+        acc ^= (a.x ^ a.y ^ a.z ^ a.w) ^ (b.x ^ b.y ^ b.z ^ b.w) ^ (c.x ^ c.y ^ c.z ^ c.w) ^ (d.x ^ d.y ^ d.z ^ d.w);
+    }
+    for (; i < n16; i += stride) {
+        const uint4 a = src[i];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    for (int o = 32; o > 0; o >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, o);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) out[blockIdx.x] = sh[0] ^ sh[1] ^ sh[2] ^ sh[3];
+}
+
 }  // namespace
+
+hipError_t launch_stream_read(const void *src, int64_t bytes, uint32_t *out, hipStream_t st) {
+    const int64_t n16 = bytes / 16;
+    if (n16 <= 0) return hipSuccess;
+    // 8 workgroups of 256 threads per CU on 256 CUs (one output word each),
+    // fewer for small buffers
+    const int64_t want = (n16 + 1023) / 1024;
+    const unsigned grid = (unsigned)(want < 2048 ? (want < 1 ? 1 : want) : 2048);
+    stream_read_kernel<<<grid, 256, 0, st>>>((const uint4 *)src, n16, out);
+    return hipGetLastError();
+}
 
 hipError_t launch_silu_mul(const float *gu, int M, int F, float *out, hipStream_t st) {
     const int64_t n = (int64_t)M * F;

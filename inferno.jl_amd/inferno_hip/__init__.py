@@ -13,13 +13,13 @@ from .quantized_kernels import (ACT_PLAIN, ACT_RMSNORM, ACT_SILU_MUL, GEMM_ACCUM
                                 quant_kernels_available, rmsnorm)
 from .sampler import apply_penalties_, softmax_sample
 from .speculative import (MODE_REFERENCE, MODE_STANDARD, SpeculativeStats, advance_len_, commit_state_, greedy_verify,
-                          mtp_verify_step, softmax_stats, spec_accept, tree_accept)
+                          mtp_verify_step, n_tokens, softmax_stats, spec_accept, tree_accept)
 
 __all__ = [
     "formats", "gguf", "synth", "HipError", "load", "GEMM_ACCUM", "GEMM_AUTO", "GEMM_F32", "GEMM_HALF",
     "GEMM_PACKED", "GEMM_REUSE", "GEMM_DEFER", "gemm_partials", "ACT_PLAIN", "ACT_RMSNORM", "ACT_SILU_MUL", "dequant", "gemm_q", "gemm_q_ex",
     "mlp_forward_", "mlp_ws_bytes", "pack_weights", "packed_bytes", "q4_k_gemv_", "q5_k_gemv_", "q6_k_gemv_", "q8_0_gemv_",
     "quant_kernels_available", "rmsnorm", "MODE_REFERENCE", "MODE_STANDARD", "SpeculativeStats",
-    "greedy_verify", "mtp_verify_step", "softmax_stats", "spec_accept", "tree_accept",
+    "greedy_verify", "mtp_verify_step", "n_tokens", "softmax_stats", "spec_accept", "tree_accept",
     "softmax_sample", "apply_penalties_", "commit_state_", "advance_len_",
 ]

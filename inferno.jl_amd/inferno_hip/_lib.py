@@ -65,6 +65,7 @@ SIGNATURES = {
     "ihip_gguf_upload": (_i, [_vp, _i64, _vp, _sz, _i, _vp]),
     "ihip_synth_blocks": (_i, [_i, _u64, _i64, _i64, _vp, _vp]),
     "ihip_synth_gaussian": (_i, [_u64, _i64, _f, _vp, _vp, _vp]),
+    "ihip_stream_read": (_i, [_vp, _sz, _vp, _vp]),
 }
 
 

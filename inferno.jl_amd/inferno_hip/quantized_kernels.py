@@ -242,6 +242,18 @@ def synth_gaussian(stream_id: int, n: int, scale: float = 1.0, add=None, out=Non
     return out
 
 
+def stream_read(buf, out=None, stream=None):
+    """Read every byte of the uint8 CUDA tensor buf once (the HBM
+    read-bandwidth probe); returns the XOR sink (one word per workgroup)."""
+    import torch
+    if out is None:
+        out = torch.zeros(2048, dtype=torch.int32, device=buf.device)
+    if out.numel() < 2048:
+        raise ValueError("stream_read: out needs 2048 words")
+    _lib.check(_lib.load().ihip_stream_read(_ptr(buf), buf.numel() // 16 * 16, _ptr(out), _stream(stream)))
+    return out
+
+
 def silu_mul(gu, f: int, out=None, stream=None):
     """silu(gate) * up for rows of gu = [gate | up] (src/ModelCPU.jl:447-473)."""
     import torch

@@ -48,7 +48,10 @@ def spec_accept(target_logits, draft_logits, draft_tokens, temperature: float, u
     target_logits [S, k+1, V], draft_logits [S, k, V], draft_tokens [S, k]
     int32, u_acc [S, k], u_res [S], u_bonus [S] (float32, CUDA).
     Returns (out_tok [S, k+1] int32, out_n [S] int32): the accepted drafts
-    followed by the resampled or bonus token at index out_n.
+    followed by the resampled or bonus token at index out_n; in
+    MODE_REFERENCE a step whose last draft is rejected (out_n == k - 1) also
+    carries the reference's bonus token at index k
+    (src/SpeculativeDecoding.jl:100). n_tokens() gives the count.
     """
     import torch
     import ctypes as C
@@ -78,6 +81,16 @@ def spec_accept(target_logits, draft_logits, draft_tokens, temperature: float, u
                                   temperature, _ptr(u_acc), _ptr(u_res), _ptr(u_bonus), mode, _ptr(out_tok),
                                   _ptr(out_n), _ptr(ws), ws.numel(), _stream(stream)))
     return out_tok, out_n
+
+
+def n_tokens(n: int, k: int, mode: int = MODE_STANDARD) -> int:
+    """Number of tokens a step of spec_accept returns for out_n = n: the
+    accepted drafts and the resampled or bonus token, plus the reference
+    mode's bonus after a rejection of the last draft (0 for an invalid
+    step)."""
+    if n < 0:
+        return 0
+    return n + 1 + (1 if mode == MODE_REFERENCE and k >= 1 and n == k - 1 else 0)
 
 
 def greedy_verify(logits, draft_tokens, stream=None):

@@ -173,6 +173,9 @@ int orc_gemv_f64(int qtype, const uint8_t *w, const float *x, double *y,
     const int bb = orc_block_bytes(qtype), be = orc_block_elems(qtype);
     if (K % be) return -22;
     const int nb = K / be;
+    /* Each output is one sequential fp64 sum over k; up to 8 outputs of a row
+     * are summed side by side (independent accumulators, same order each),
+     * which changes no result. */
     #pragma omp parallel
     {
         float *row = (float *)malloc(sizeof(float) * (size_t)K);
@@ -180,11 +183,15 @@ int orc_gemv_f64(int qtype, const uint8_t *w, const float *x, double *y,
         for (int r = 0; r < N; r++) {
             for (int b = 0; b < nb; b++)
                 f(w + ((size_t)r * nb + b) * bb, row + (size_t)b * be);
-            for (int m = 0; m < M; m++) {
-                double s = 0.0;
-                const float *xm = x + (size_t)m * K;
-                for (int k = 0; k < K; k++) s += (double)row[k] * (double)xm[k];
-                y[(size_t)m * N + r] = s;
+            for (int m0 = 0; m0 < M; m0 += 8) {
+                const int mn = M - m0 < 8 ? M - m0 : 8;
+                double s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                const float *xm = x + (size_t)m0 * K;
+                for (int k = 0; k < K; k++) {
+                    const double wk = (double)row[k];
+                    for (int j = 0; j < mn; j++) s[j] += wk * (double)xm[(size_t)j * K + k];
+                }
+                for (int j = 0; j < mn; j++) y[(size_t)(m0 + j) * N + r] = s[j];
             }
         }
         free(row);
@@ -437,11 +444,19 @@ void orc_softmax_stats(const float *L, int V, float T, double *zmax,
     *zsum = s;
 }
 
-/* Julia argmax: first index of the maximum (tests/unit/test_engine.jl:56-69). */
+/* Julia argmax: first index of the maximum (tests/unit/test_engine.jl:56-69).
+ * findmax replaces its current maximum m by x iff isless(m, x), Julia's total
+ * order of floats: -Inf < ... < -0.0 < +0.0 < ... < +Inf < NaN, NaNs equal.
+ * So a NaN replaces a number, +0.0 replaces -0.0, and a later equal value
+ * (or a later NaN) never replaces the current one. */
+static inline int beats(float a, float b) {
+    if (isnan(a) || isnan(b)) return isnan(a) && !isnan(b);
+    return a > b || (a == b && signbit(b) && !signbit(a));
+}
 int32_t orc_argmax_first(const float *L, int V) {
     int32_t best = 0;
     for (int j = 1; j < V; j++)
-        if (L[j] > L[best]) best = j;
+        if (beats(L[j], L[best])) best = j;
     return best;
 }
 
@@ -510,6 +525,17 @@ int orc_spec_accept(const float *Lt, const float *Ld, const int32_t *draft,
         }
         out_tok[n] = tok;
         *out_n = n;
+        /* mode 1: the reference appends the bonus whenever length(accepted)
+         * == gamma (src/SpeculativeDecoding.jl:100), which a rejection at the
+         * last draft also reaches (k - 1 drafts + the residual): the bonus
+         * from target row k at T follows the residual token. */
+        if (mode == 1 && n == k - 1) {
+            const float *lk = Lt + (size_t)k * V;
+            double m, s;
+            orc_softmax_stats(lk, V, T, &m, &s);
+            for (int j = 0; j < V; j++) w[j] = prob_at(lk, j, T, m, s);
+            out_tok[n + 1] = inv_cdf(w, V, 1.0, u_bonus);
+        }
         free(w);
         return 0;
     }
@@ -529,6 +555,24 @@ int orc_spec_accept(const float *Lt, const float *Ld, const int32_t *draft,
     *out_n = n;
     free(w);
     return 0;
+}
+
+int orc_spec_accept_batch(const float *Lt, const float *Ld,
+                          const int32_t *draft, int steps, int k, int V,
+                          float T, const float *u_acc, const float *u_res,
+                          const float *u_bonus, int mode, int32_t *out_tok,
+                          int32_t *out_n) {
+    if (steps < 0 || k < 0 || V < 1) return -22;
+    int bad = 0;
+    #pragma omp parallel for schedule(dynamic, 4) reduction(| : bad)
+    for (int s = 0; s < steps; s++) {
+        const int rc = orc_spec_accept(Lt + (size_t)s * (k + 1) * V, Ld + (size_t)s * k * V, draft + (size_t)s * k,
+                                       k, V, T, u_acc + (size_t)s * k, u_res[s], u_bonus[s], mode,
+                                       out_tok + (size_t)s * (k + 1), out_n + s);
+        if (rc == -22) out_n[s] = -1;
+        else if (rc != 0) bad = 1;
+    }
+    return bad ? -12 : 0;
 }
 
 int orc_greedy_verify(const float *logits, const int32_t *draft, int k, int V,

@@ -71,14 +71,30 @@ int orc_gemv_q8k(int qtype, const uint8_t *w, const float *x, float *out,
  * (fp64). T == 0 is rejected (greedy uses argmax). */
 void orc_softmax_stats(const float *L, int V, float T, double *zmax,
                        double *zsum);
+/* Julia argmax: the first index of the maximum in Julia's isless order
+ * (-0.0 below +0.0, NaN above every number: the first NaN wins), so a row
+ * of -Inf gives 0. */
 int32_t orc_argmax_first(const float *L, int V);
 
 /* Speculative accept (src/SpeculativeDecoding.jl:37-107 and the build's
  * standard contract). mode 0 = standard, mode 1 = reference-compatible.
- * Tokens are 0-based. Returns 0 or a negative error. */
+ * Tokens are 0-based. out_tok receives *out_n + 1 tokens (the accepted
+ * drafts, then the resampled or bonus token), and in mode 1 one more when
+ * the last draft is rejected (*out_n == k - 1): the bonus the reference
+ * appends whenever length(accepted) == gamma (:100). Returns 0 or a
+ * negative error. */
 int orc_spec_accept(const float *Lt, const float *Ld, const int32_t *draft,
                     int k, int V, float T, const float *u_acc, float u_res,
                     float u_bonus, int mode, int32_t *out_tok, int32_t *out_n);
+/* orc_spec_accept over `steps` independent steps laid out step-major as
+ * ihip_spec_accept takes them (Lt [steps][k+1][V], Ld [steps][k][V],
+ * draft / u_acc [steps][k], out_tok [steps][k+1], out_n [steps]); steps in
+ * parallel (OpenMP). out_n[s] = -1 for a step with an invalid draft id. */
+int orc_spec_accept_batch(const float *Lt, const float *Ld,
+                          const int32_t *draft, int steps, int k, int V,
+                          float T, const float *u_acc, const float *u_res,
+                          const float *u_bonus, int mode, int32_t *out_tok,
+                          int32_t *out_n);
 
 /* Greedy verify (src/ModelCPU.jl:1914-1930): logits [(k+1) x V]; accepted =
  * leading i < k with argmax(logits[i]) == draft[i]. */

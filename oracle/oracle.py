@@ -51,6 +51,8 @@ def lib():
         L.orc_argmax_first.argtypes = [_f32p, C.c_int]
         L.orc_spec_accept.argtypes = [_f32p, _f32p, _i32p, C.c_int, C.c_int, C.c_float, _f32p,
                                       C.c_float, C.c_float, C.c_int, _i32p, C.POINTER(C.c_int32)]
+        L.orc_spec_accept_batch.argtypes = [_f32p, _f32p, _i32p, C.c_int, C.c_int, C.c_int, C.c_float, _f32p,
+                                            _f32p, _f32p, C.c_int, _i32p, _i32p]
         L.orc_greedy_verify.argtypes = [_f32p, _i32p, C.c_int, C.c_int,
                                         C.POINTER(C.c_int32), _i32p]
         L.orc_tree_accept.argtypes = [_f32p, _f32p, _i32p, _i32p, C.c_int, C.c_int, C.c_float,
@@ -123,7 +125,33 @@ def spec_accept(Lt, Ld, draft, T, u_acc, u_res, u_bonus, mode=0):
     rc = lib().orc_spec_accept(Lt, _c(Ld, np.float32), dr, k, V, T, ua, u_res, u_bonus, mode,
                                out, C.byref(n))
     assert rc == 0, rc
-    return out[: n.value + 1].copy(), n.value
+    return out[: n_tokens(n.value, k, mode)].copy(), n.value
+
+
+def n_tokens(n: int, k: int, mode: int) -> int:
+    """Tokens a step returns: the n accepted drafts and the resampled or
+    bonus token, plus in mode 1 the bonus the reference appends after a
+    rejection of the last draft (src/SpeculativeDecoding.jl:100)."""
+    if n < 0:
+        return 0
+    return n + 1 + (1 if mode == 1 and k >= 1 and n == k - 1 else 0)
+
+
+def spec_accept_batch(Lt, Ld, draft, T, u_acc, u_res, u_bonus, mode=0):
+    """orc_spec_accept over steps (parallel on the host): Lt [S, k+1, V],
+    Ld [S, k, V], draft / u_acc [S, k], u_res / u_bonus [S] ->
+    (out_tok [S, k+1] padded with -1, out_n [S], -1 for an invalid draft)."""
+    Lt = _c(Lt, np.float32)
+    S, k1, V = Lt.shape
+    k = k1 - 1
+    out = np.full((S, k1), -1, dtype=np.int32)
+    n = np.zeros(S, dtype=np.int32)
+    rc = lib().orc_spec_accept_batch(Lt, _c(Ld, np.float32), _c(draft, np.int32), S, k, V, T, _c(u_acc, np.float32),
+                                     _c(u_res, np.float32), _c(u_bonus, np.float32), mode, out, n)
+    assert rc == 0, rc
+    for s in range(S):  # entries past the step's tokens are left as -1
+        out[s, n_tokens(int(n[s]), k, mode):] = -1
+    return out, n
 
 
 def greedy_verify(logits, draft):

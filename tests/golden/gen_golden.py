@@ -70,7 +70,7 @@ def main():
         ns = np.zeros(S, dtype=np.int32)
         for s in range(S):
             t, n = O.spec_accept(Lt[s], Ld[s], draft[s], 0.8, ua[s], float(ur[s]), float(ub[s]), mode)
-            toks[s, : n + 1] = t
+            toks[s, : len(t)] = t
             ns[s] = n
         fx[f"accept_mode{mode}_tok"] = toks
         fx[f"accept_mode{mode}_n"] = ns

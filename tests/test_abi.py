@@ -67,23 +67,42 @@ def test_argument_checks_without_gpu(lib):
     assert lib.ihip_tree_accept(p16, p16, p16, p16, 4, 10, 0.0, p16, p16, p16, p16, 1 << 20, None) == -22
 
 
-def test_dropin_reports_failure_without_gpu():
-    """With no usable device the drop-in sets ENODEV and prints a message
-    (the reference's library-missing error path), and nothing is written."""
+def _dropin_child(env_extra, inner_dim, outer_dim=3):
     code = (
         "import ctypes as C, numpy as np, sys; sys.path.insert(0, %r);"
         "from inferno_hip import _lib; L = _lib.load();"
-        "w = np.zeros(144, np.uint8); x = np.zeros(256, np.float32); o = np.full(1, 7.0, np.float32);"
-        "L.q4_k_gemv(w.ctypes.data, x.ctypes.data, o.ctypes.data, None, 256, 1);"
-        "print(L.ihip_last_status(), o[0], L.ihip_available())"
-    ) % os.path.join(ROOT, "inferno.jl_amd")
-    env = dict(os.environ, HIP_VISIBLE_DEVICES="-1" if os.environ.get("HIP_VISIBLE_DEVICES") is None else os.environ["HIP_VISIBLE_DEVICES"])
+        "w = np.zeros(144 * 4 * %d, np.uint8); x = np.zeros(1024, np.float32); o = np.full(%d, 7.0, np.float32);"
+        "L.q4_k_gemv(w.ctypes.data, x.ctypes.data, o.ctypes.data, None, %d, %d);"
+        "print(L.ihip_last_status(), ' '.join(repr(float(v)) for v in o), L.ihip_available())"
+    ) % (os.path.join(ROOT, "inferno.jl_amd"), outer_dim, outer_dim + 1, inner_dim, outer_dim)
+    env = dict(os.environ, **env_extra)
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=120)
-    status, val, avail = r.stdout.split()
-    if int(avail) == 1:
+    f = r.stdout.split()
+    return int(f[0]), [float(v) for v in f[1:-1]], int(f[-1]), r.stderr
+
+
+def test_dropin_reports_failure_without_gpu():
+    """With no usable device the drop-in sets ENODEV and prints a message
+    (the reference's library-missing error path), and fills out[0..N) with
+    NaN so an unmodified caller, which never reads the status, sees it;
+    nothing past N is touched."""
+    vis = os.environ.get("HIP_VISIBLE_DEVICES")
+    status, out, avail, err = _dropin_child({"HIP_VISIBLE_DEVICES": "-1" if vis is None else vis}, 256)
+    if avail == 1:
         pytest.skip("a GPU is visible")
-    assert int(status) == -19 and float(val) == 7.0
-    assert "inferno_hip:" in r.stderr
+    assert status == -19
+    assert all(v != v for v in out[:3]) and out[3] == 7.0
+    assert "inferno_hip:" in err
+
+
+def test_dropin_nan_on_bad_shape_and_kill_switch():
+    """A bad inner_dim (not a multiple of 256) and the INFERNO_NO_QUANT_KERNELS
+    switch also leave NaN in out[0..N), GPU or not."""
+    status, out, _, err = _dropin_child({"INFERNO_NO_QUANT_KERNELS": "1"}, 256)
+    assert status == -19 and all(v != v for v in out[:3]) and out[3] == 7.0
+    assert "INFERNO_NO_QUANT_KERNELS" in err
+    status, out, _, err = _dropin_child({}, 300)
+    assert status in (-19, -22) and all(v != v for v in out[:3]) and out[3] == 7.0
 
 
 def test_env_kill_switch():

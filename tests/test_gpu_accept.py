@@ -73,7 +73,7 @@ def test_spec_accept_parity(ih, mode, V, S, T):
     for s in range(S):
         rt, rn = O.spec_accept(Lt[s], Ld[s], draft[s], T, u_acc[s], float(u_res[s]), float(u_bon[s]), mode)
         same_len += int(rn == n[s])
-        same_tok += int(rn == n[s] and np.array_equal(rt, tok[s, : n[s] + 1]))
+        same_tok += int(rn == n[s] and np.array_equal(rt, tok[s, : ih.n_tokens(int(n[s]), k, mode)]))
     print(f"mode={mode} V={V} S={S}: lengths {same_len}/{S}, tokens {same_tok}/{S}", flush=True)
     assert same_len >= 0.999 * S
     assert same_tok >= 0.999 * S
@@ -106,6 +106,40 @@ def test_spec_accept_special_cases(ih):
     assert int(n[0]) == 0 and int(tok[0, 0]) == int(rt[0])
 
 
+def test_reference_mode_bonus_after_last_rejection(ih):
+    """Mode 1 reproduces src/SpeculativeDecoding.jl:100: a rejection of the
+    last draft leaves length(accepted) == gamma, so a bonus token from target
+    row k at T follows the residual; an earlier rejection has no bonus. The
+    hand-worked two-draft case of the oracle tests at V = 3, and a batch at
+    V = 151936 whose steps are forced to reject at every position."""
+    Lt = np.log(np.array([[[0.5, 0.3, 0.2], [0.5, 0.3, 0.2], [0.1, 0.1, 0.8]]], np.float32)).repeat(3, 0)
+    Ld = np.log(np.array([[[0.1, 0.6, 0.3], [0.1, 0.6, 0.3]]], np.float32)).repeat(3, 0)
+    d = np.array([[1, 1]] * 3, np.int32)
+    ua = np.array([[0.7, 0.1], [0.1, 0.7], [0.1, 0.2]], np.float32)
+    ur = np.full(3, 0.5, np.float32)
+    ub = np.array([0.9, 0.9, 0.15], np.float32)
+    tok, n = ih.spec_accept(_dev(Lt), _dev(Ld), _dev(d), 1.0, _dev(ua), _dev(ur), _dev(ub), mode=1)
+    tok, n = tok.cpu().numpy(), n.cpu().numpy()
+    assert n.tolist() == [0, 1, 2]
+    assert tok[0, :1].tolist() == [2] and tok[1].tolist() == [1, 2, 2] and tok[2].tolist() == [1, 1, 1]
+    # V = 151936: draft i rejected by u_acc = 1 at position j = s % k (earlier ones accepted by u = 0)
+    S, k, V = 16, 4, 151936
+    rng = np.random.default_rng(9)
+    Lt2, Ld2 = _case(rng, S, k, V)
+    draft = np.array([[_draw(Ld2[s, i], 1.0, rng.random()) for i in range(k)] for s in range(S)], np.int32)
+    ua2 = np.zeros((S, k), np.float32)
+    for s in range(S):
+        ua2[s, s % k] = 1.0
+    ur2, ub2 = rng.random(S).astype(np.float32), rng.random(S).astype(np.float32)
+    tok, n = ih.spec_accept(_dev(Lt2), _dev(Ld2), _dev(draft), 0.8, _dev(ua2), _dev(ur2), _dev(ub2), mode=1)
+    tok, n = tok.cpu().numpy(), n.cpu().numpy()
+    for s in range(S):
+        rt, rn = O.spec_accept(Lt2[s], Ld2[s], draft[s], 0.8, ua2[s], float(ur2[s]), float(ub2[s]), 1)
+        assert n[s] == rn == s % k
+        assert len(rt) == ih.n_tokens(rn, k, 1) == (k + 1 if rn == k - 1 else rn + 1)
+        assert tok[s, :len(rt)].tolist() == rt.tolist(), (s, tok[s], rt)
+
+
 def test_greedy_verify(ih):
     rng = np.random.default_rng(3)
     S, k, V = 64, 4, 151936
@@ -125,6 +159,27 @@ def test_greedy_verify(ih):
         rn, ra = O.greedy_verify(L[s], draft[s])
         assert rn == n[s] and np.array_equal(ra, a[s]), s
     assert a[0, 1] == 5 and a[1, 0] == 4096
+
+
+def test_greedy_verify_nonfinite_rows(ih):
+    """Rows of -Inf, NaN and signed zeros follow Julia's argmax (isless
+    order: the first NaN wins, +0.0 above -0.0, a row of -Inf gives its
+    first index), never an index outside [0, V)."""
+    k, V = 5, 151936
+    L = np.random.default_rng(4).standard_normal((1, k + 1, V)).astype(np.float32)
+    L[0, 0, :] = -np.inf                      # all -Inf
+    L[0, 1, 70000] = np.nan                   # one NaN
+    L[0, 1, 90000] = np.nan
+    L[0, 2, :] = 0.0                          # -0.0 first, +0.0 later
+    L[0, 2, :5000] = -0.0
+    L[0, 3, :] = np.nan                       # all NaN
+    L[0, 4, 4095] = L[0, 4, 4096] = np.inf    # +Inf tie across a chunk edge
+    draft = np.array([[0, 70000, 5000, 0, 4095]], np.int32)
+    n, a = ih.greedy_verify(_dev(L), _dev(draft))
+    n, a = n.cpu().numpy(), a.cpu().numpy()
+    rn, ra = O.greedy_verify(L[0], draft[0])
+    assert a[0].tolist() == ra.tolist(), (a, ra)
+    assert a[0, :5].tolist() == [0, 70000, 5000, 0, 4095] and rn == n[0] == 5
 
 
 def _tree_parents(n, branching=(4, 4, 4)):

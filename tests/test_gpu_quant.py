@@ -147,6 +147,39 @@ def test_dropin_host_gemv(ih, qt):
     assert np.array_equal(out, out2)
 
 
+def test_dropin_cache_sees_reused_buffer(ih):
+    """The drop-in weight cache is keyed by (pointer, bytes, type, N, K) with a
+    fingerprint of sampled bytes: a host buffer overwritten in place (as a
+    garbage-collected array's address reused by a new one of the same size)
+    gives the new matrix's result, and the same bytes read as another type
+    of equal byte size (Q4_K 272 x 1024 and Q8_0 288 x 512: 156672 bytes)
+    give that type's result."""
+    qk = ih.quantized_kernels
+    N, K = 272, 1024
+    buf = np.empty(N * (K // 256) * 144, dtype=np.uint8)
+    x = np.random.default_rng(11).standard_normal(K).astype(np.float32)
+    outs = []
+    for tag in ("first", "second"):
+        buf[:] = synth.matrix(F.Q4_K, N, K, synth.stream_for(12, f"reuse.{tag}"))
+        out = np.zeros(N, dtype=np.float32)
+        qk.q4_k_gemv_(out, buf, x, K, N)  # (np.ascontiguousarray keeps buf's address)
+        assert rel_l2(out, O.gemv_f64(F.Q4_K, buf, x, 1, N, K)[0]) <= TOL_F32, tag
+        outs.append(out)
+    assert not np.array_equal(outs[0], outs[1])
+    n8, k8 = 288, 512
+    assert n8 * (k8 // 32) * 34 == buf.size
+    xq = np.random.default_rng(12).standard_normal(k8).astype(np.float32)
+    out8 = np.zeros(n8, dtype=np.float32)
+    qk.q8_0_gemv_(out8, buf, xq, k8, n8)
+    ref8 = O.gemv_f64(F.Q8_0, buf, xq, 1, n8, k8)[0]
+    # (Q4_K bytes read as Q8_0 blocks: some fp16 d fields are NaN or Inf, and
+    # those rows are NaN in both; the finite rows carry the comparison)
+    assert np.array_equal(np.isnan(out8), np.isnan(ref8))
+    fin = np.isfinite(ref8)
+    assert fin.sum() > n8 // 4 and rel_l2(out8[fin], ref8[fin]) <= TOL_F32
+    ih.load().ihip_weight_cache_clear()
+
+
 def test_errors(ih):
     import torch
     from inferno_hip._lib import HipError

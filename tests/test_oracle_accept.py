@@ -37,6 +37,31 @@ def test_argmax_first_index():
     assert O.argmax_first(np.array([-10, -5, -1], np.float32)) == 2
 
 
+def test_argmax_nan_and_inf_rows():
+    """Julia's findmax order (argmax of mtp_verify_step!): isless, where NaN
+    lies above every number (the first NaN wins) and -0.0 below +0.0; a row of
+    -Inf returns its first index, as Julia's argmax returns 1 for a vector of
+    -Inf. Cross-checked with numpy, whose argmax also returns the first NaN
+    and the first of equal values (it differs only on signed zeros), and with
+    a brute force over Python's sort by (isless key, index)."""
+    inf, nan = np.inf, np.nan
+
+    def key(v):  # Julia's isless as a sort key: NaN last, -0.0 before +0.0
+        return (2, 0.0) if np.isnan(v) else (1, float(v), 0 if np.signbit(v) else 1)
+
+    rows = ([-inf] * 5, [1.0, nan, 3.0, nan], [nan, 2.0], [-inf, -inf, 2.0, inf, inf], [0.0, -0.0, 0.0],
+            [-inf, nan], [-0.0, 0.0], [-0.0, -0.0, 0.0, 0.0], [5.0, 5.0])
+    for row in rows:
+        a = np.array(row, np.float32)
+        want = max(range(len(a)), key=lambda i: (key(a[i]), -i))
+        assert O.argmax_first(a) == want, row
+        if not (a == 0).any():
+            assert O.argmax_first(a) == int(np.argmax(a)), row
+    assert O.argmax_first(np.full(7, -inf, np.float32)) == 0
+    assert O.argmax_first(np.array([1.0, nan, 3.0, nan], np.float32)) == 1
+    assert O.argmax_first(np.array([-0.0, 0.0], np.float32)) == 1
+
+
 def test_standard_accept_preserves_target_distribution():
     """Mode 0 with draft x ~ q and independent uniforms must output a token
     distributed as p (k = 1, first output token)."""
@@ -91,15 +116,52 @@ def test_reference_mode_hand_case():
     # draft token 1: p = 0.3, q = 0.6 -> ratio 0.5
     tok, n = O.spec_accept(Lt, Ld, np.array([1], np.int32), 2.0, np.array([0.49], np.float32), 0.0, 0.0, 1)
     assert n == 1  # accepted, bonus drawn at T = 2
-    # reject: residual max(p - 0.6, 0) = [0, 0, 0] -> all-zero -> last index
+    # reject: residual max(p - 0.6, 0) = [0, 0, 0] -> all-zero -> last index;
+    # with gamma = 1 the rejection leaves length(accepted) == gamma, so the
+    # reference appends a bonus from target row 1 (:100): p1 = [0.2, 0.2, 0.6]
+    # at T = 1, u_bonus 0.0 -> first index with 0 <= cumsum -> token 0
     tok, n = O.spec_accept(Lt, Ld, np.array([1], np.int32), 1.0, np.array([0.51], np.float32), 0.5, 0.0, 1)
-    assert n == 0 and tok[0] == 2
-    # draft token 2: p = 0.2, q = 0.3; residual max(p - 0.3, 0) = [0.2, 0, 0] -> token 0
-    tok, n = O.spec_accept(Lt, Ld, np.array([2], np.int32), 1.0, np.array([0.9], np.float32), 0.99, 0.0, 1)
-    assert n == 0 and tok[0] == 0
-    # standard mode on the same input: residual max(p - q, 0) = [0.4, 0, 0] -> token 0
-    tok, n = O.spec_accept(Lt, Ld, np.array([2], np.int32), 1.0, np.array([0.9], np.float32), 0.99, 0.0, 0)
-    assert n == 0 and tok[0] == 0
+    assert n == 0 and tok.tolist() == [2, 0]
+    # the bonus row's inverse CDF: u_bonus 0.5 -> cumsum [0.2, 0.4, 1.0] -> token 2
+    tok, n = O.spec_accept(Lt, Ld, np.array([1], np.int32), 1.0, np.array([0.51], np.float32), 0.5, 0.5, 1)
+    assert n == 0 and tok.tolist() == [2, 2]
+    # draft token 2: p = 0.2, q = 0.3; residual max(p - 0.3, 0) = [0.2, 0, 0] -> token 0, then the bonus
+    # (u_bonus 0.3 -> cumsum 0.2 < 0.3 <= 0.4 -> token 1)
+    tok, n = O.spec_accept(Lt, Ld, np.array([2], np.int32), 1.0, np.array([0.9], np.float32), 0.99, 0.3, 1)
+    assert n == 0 and tok.tolist() == [0, 1]
+    # standard mode on the same input: residual max(p - q, 0) = [0.4, 0, 0] -> token 0, no bonus
+    tok, n = O.spec_accept(Lt, Ld, np.array([2], np.int32), 1.0, np.array([0.9], np.float32), 0.99, 0.3, 0)
+    assert n == 0 and tok.tolist() == [0]
+
+
+def test_reference_mode_bonus_only_after_last_draft():
+    """src/SpeculativeDecoding.jl:100 appends the bonus iff length(accepted)
+    == gamma: after all gamma drafts stand, or after a rejection of the last
+    draft (gamma - 1 drafts + the residual); never after an earlier
+    rejection. Two drafts over V = 3, hand-worked at T = 1."""
+    Lt = np.log(np.array([[0.5, 0.3, 0.2], [0.5, 0.3, 0.2], [0.1, 0.1, 0.8]], np.float32))
+    Ld = np.log(np.array([[0.1, 0.6, 0.3], [0.1, 0.6, 0.3]], np.float32))
+    d = np.array([1, 1], np.int32)  # p = 0.3, q = 0.6 at both positions: ratio 0.5
+    # reject at position 0: residual max(p - 0.6, 0) = 0 -> last index, no bonus (length 1 < 2)
+    tok, n = O.spec_accept(Lt, Ld, d, 1.0, np.array([0.7, 0.1], np.float32), 0.5, 0.9, 1)
+    assert n == 0 and tok.tolist() == [2]
+    # accept position 0, reject position 1: [1, residual 2] has length gamma -> bonus from row 2
+    # (u_bonus 0.9 -> cumsum [0.1, 0.2, 1.0] -> token 2; u_bonus 0.15 -> token 1)
+    tok, n = O.spec_accept(Lt, Ld, d, 1.0, np.array([0.1, 0.7], np.float32), 0.5, 0.9, 1)
+    assert n == 1 and tok.tolist() == [1, 2, 2]
+    tok, n = O.spec_accept(Lt, Ld, d, 1.0, np.array([0.1, 0.7], np.float32), 0.5, 0.15, 1)
+    assert n == 1 and tok.tolist() == [1, 2, 1]
+    # both accepted: the ordinary bonus
+    tok, n = O.spec_accept(Lt, Ld, d, 1.0, np.array([0.1, 0.2], np.float32), 0.5, 0.15, 1)
+    assert n == 2 and tok.tolist() == [1, 1, 1]
+    # the batched oracle returns the same rows, padded with -1
+    Lb = np.stack([Lt] * 3)
+    Db = np.stack([Ld] * 3)
+    ua = np.array([[0.7, 0.1], [0.1, 0.7], [0.1, 0.2]], np.float32)
+    out, ns = O.spec_accept_batch(Lb, Db, np.stack([d] * 3), 1.0, ua, np.full(3, 0.5, np.float32),
+                                  np.array([0.9, 0.9, 0.15], np.float32), 1)
+    assert ns.tolist() == [0, 1, 2]
+    assert out.tolist() == [[2, -1, -1], [1, 2, 2], [1, 1, 1]]
 
 
 def test_accept_fixtures():
@@ -109,7 +171,8 @@ def test_accept_fixtures():
             tok, n = O.spec_accept(g["accept_Lt"][s], g["accept_Ld"][s], g["accept_draft"][s], 0.8,
                                    g["accept_ua"][s], float(g["accept_ur"][s]), float(g["accept_ub"][s]), mode)
             assert n == g[f"accept_mode{mode}_n"][s]
-            assert tok.tolist() == g[f"accept_mode{mode}_tok"][s][: n + 1].tolist()
+            want = g[f"accept_mode{mode}_tok"][s]
+            assert tok.tolist() == want[: len(tok)].tolist() and (want[len(tok):] == -1).all()
 
 
 def test_greedy_verify():
