@@ -116,6 +116,21 @@ int ihip_gemm_q(int qtype, const void *w_dev, const float *x_dev, float *y_dev,
                 int M, int N, int K, int flags, void *ws, size_t ws_bytes,
                 void *stream);
 
+/* ihip_gemm_q without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). No counterpart in the reference. The workspace is
+ * a fixed 64 MiB device array of the library (one per GPU, held from module
+ * load to process exit); shapes whose ihip_gemm_q_ws_bytes exceed it are
+ * rejected with IHIP_ENOMEM (e.g. the 151936-row LM head at M = 64). The
+ * call allocates nothing. All calls on one GPU share its array: calls that
+ * overlap in time on one GPU (other streams, other threads) race, so
+ * serialize them. The kernels write every scratch byte they read, so the
+ * previous call's contents need no clearing. Same results, bit for bit, as
+ * ihip_gemm_q with the same arguments. */
+int ihip_gemm_q_noalloc(int qtype, const void *w_dev, const float *x_dev,
+                        float *y_dev, int M, int N, int K, int flags,
+                        void *stream);
+
 /* ihip_gemm_q with the producer of its input fused in: Y = f(X') W^T.
  *   X' = x, or, with add != NULL, x + (add[0] + add[1] + ... + add[n_add-1])
  *        (slices [M x K], row stride K, slice stride add_stride floats, e.g.

@@ -55,6 +55,8 @@ hipError_t launch_penalties(float *L, int rows, int V, const int32_t *tok, int n
                             float presence, float repetition, hipStream_t st);
 hipError_t launch_gaussian(uint64_t stream, int64_t n, float scale, const float *add, float *out, hipStream_t st);
 hipError_t launch_stream_read(const void *src, int64_t bytes, uint32_t *out, hipStream_t st);
+size_t noalloc_scratch_bytes();
+hipError_t noalloc_scratch(void **out);
 
 namespace {
 
@@ -361,6 +363,21 @@ int ihip_gemm_q(int qtype, const void *w_dev, const float *x_dev, float *y_dev, 
     if (!aligned16(ws)) return fail(IHIP_EINVAL, "ihip_gemm_q: workspace must be 16-byte aligned");
     hipError_t e = launch_gemm(qtype, w_dev, x_dev, y_dev, M, N, K, flags, ws, S(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_gemm_q");
+}
+
+int ihip_gemm_q_noalloc(int qtype, const void *w_dev, const float *x_dev, float *y_dev, int M, int N, int K,
+                        int flags, void *stream) {
+    int rc = check_gemm(qtype, w_dev, x_dev, y_dev, M, N, K, flags);
+    if (rc != IHIP_OK) return rc;
+    const size_t need = gemm_ws_bytes(qtype, M, N, K, flags);
+    if (need > noalloc_scratch_bytes())
+        return fail(IHIP_ENOMEM, "ihip_gemm_q_noalloc: this shape needs %zu bytes of scratch, above the fixed %zu "
+                    "(use ihip_gemm_q with a caller workspace)", need, noalloc_scratch_bytes());
+    void *scr = nullptr;
+    hipError_t e = noalloc_scratch(&scr);
+    if (e != hipSuccess) return hip_fail(e, "ihip_gemm_q_noalloc: device scratch");
+    e = launch_gemm(qtype, w_dev, x_dev, y_dev, M, N, K, flags, scr, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_gemm_q_noalloc");
 }
 
 int ihip_gemm_q_ex(int qtype, const void *w_dev, const ihip_gemm_input *in, float *y_dev, int M, int N, int K,

@@ -31,6 +31,7 @@ SIGNATURES = {
     "ihip_gemm_q_ws_bytes": (_i, [_i, _i, _i, _i, _i, C.POINTER(_sz)]),
     "ihip_gemm_q": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "ihip_gemm_q_ex": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "ihip_gemm_q_noalloc": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "ihip_gemm_q_partials": (_i, [_i, _i, _i, _i, _i, _vp, C.POINTER(_vp), C.POINTER(_i), C.POINTER(_i64)]),
     "ihip_mlp_ws_bytes": (_i, [_i, _i, _i, _i, _i, _i, C.POINTER(_sz)]),
     "ihip_mlp_forward": (_i, [_i, _vp, _i, _vp, _vp, _vp, _f, _i, _i, _i, _i, _vp, _sz, _vp]),
