@@ -323,6 +323,51 @@ def profile_kernels(ih, model: Model, n_layers: int, M: int):
     log(f"profile_kernels: roofline graph + ihip_add over {n} floats")
 
 
+def profile_m5(ih, reps: int = 5):
+    """For rocprofv3 --pmc / --kernel-trace: one config-4 layer's four M = 5
+    matmuls as the verify step runs them (input stage + matmul, packed
+    weights, fp32-accurate), each launched `reps` times in a row, in the order
+    [q; k; v], o (deferred), [gate; up], down (deferred); then the plain-read
+    probe over 57,196,544 B (the [gate; up] weights) and 510,504,960 B (the
+    lm_head's), `reps` times each, and the calibration kernel (ihip_add over 64
+    Mi floats: reads 512 MiB, writes 256 MiB) three times."""
+    import torch
+    F, q = ih.formats, ih.quantized_kernels
+    model = Model(ih, 1, keep_gguf=0)
+    step = VerifyStep(ih, model, 5, 4, 0.8)
+    lw = model.layers[0]
+    ex = ih.gemm_q_ex
+    f32 = ih.GEMM_F32 | ih.GEMM_PACKED
+    dfr = f32 | ih.GEMM_DEFER
+    o_parts = ih.gemm_partials(F.Q4_K, 5, H, NQ, f32, step.ws_o)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        ex(F.Q4_K, lw["qkv"], step.x, NQ + 2 * NKV, H, act=ih.ACT_RMSNORM, norm_w=lw["attn_norm"], flags=f32,
+           out=step.qkv, ws=step.ws)
+    for _ in range(reps):
+        ex(F.Q4_K, lw["o"], step.qkv[:, :NQ], H, NQ, flags=dfr, ws=step.ws_o)
+    for _ in range(reps):
+        ex(F.Q4_K, lw["gu"], step.x, 2 * FF, H, act=ih.ACT_RMSNORM, norm_w=lw["ffn_norm"], flags=f32, out=step.gu,
+           ws=step.ws, add=o_parts)
+    for _ in range(reps):
+        ex(F.Q6_K, lw["down"], step.gu, H, FF, act=ih.ACT_SILU_MUL, flags=dfr, ws=step.ws_down)
+    torch.cuda.synchronize()
+    sink = torch.zeros(2048, dtype=torch.int32, device="cuda")
+    for nb in (57_196_544, 510_504_960):
+        buf = torch.ones(nb // 4, dtype=torch.float32, device="cuda").view(torch.uint8)
+        for _ in range(reps):
+            q.stream_read(buf, out=sink)
+        torch.cuda.synchronize()
+        del buf
+    n = 64 << 20
+    a = torch.ones(n, device="cuda")
+    b = torch.ones(n, device="cuda")
+    for _ in range(3):
+        q.add_(a, b)
+    torch.cuda.synchronize()
+    log(f"profile_m5: {reps} x (qkv, o, gate/up, down) at M = 5, stream_read 57 MB and 510 MB, 3 x ihip_add")
+
+
 def profile_tall(ih, reps: int = 5):
     """For rocprofv3 --pmc: the M = 64 (config 5) half-precision matmuls of
     one layer, each launched `reps` times: Q4_K [gate; up] 24576x4096 with
@@ -801,6 +846,9 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only run the roofline kernel and the traffic calibration kernel (for rocprofv3 --pmc)")
+    ap.add_argument("--profile-m5", action="store_true",
+                    help="only run one layer's four M = 5 matmuls five times each, the plain-read probe and the "
+                         "traffic calibration kernel (for rocprofv3 --pmc)")
     ap.add_argument("--profile-tall", action="store_true",
                     help="only run the M = 64 gate/up and down matmuls five times each (for rocprofv3 --pmc)")
     ap.add_argument("--configs", type=str, default="",
@@ -820,6 +868,9 @@ def main():
     t0 = time.time()
     if args.profile_tall:
         profile_tall(ih)
+        return
+    if args.profile_m5:
+        profile_m5(ih)
         return
     if args.configs:
         want = [c.strip() for c in args.configs.split(",") if c.strip()]

@@ -91,6 +91,25 @@ void q6_k_gemv(const uint8_t *weight, const float *x, float *out, void *q8_buf,
 void q8_0_gemv(const uint8_t *weight, const float *x, float *out,
                int inner_dim, int outer_dim);
 
+/* The remaining exports of the reference library, computed on the GPU with
+ * the same host-pointer, synchronous convention (the matmul path does not use
+ * them; they let this library stand in for libquant_kernels.so symbol for
+ * symbol). Results equal the reference's bit for bit.
+ *   quantize_row_q8_K: k fp32 values (k a multiple of 256) to k/256
+ *     block_q8_K (float d = amax/127; int8 qs[256] = round(x/d) half away
+ *     from zero; int16 bsums[16] of 16 values each): 292 bytes per block
+ *     (src/kernels/quant_kernels.c:166-194). Bound by quantize_q8_k!
+ *     (src/QuantizedKernels.jl:149-154), whose ccall passes (q8_buf, x, k) in
+ *     the wrong order and width for this C signature, as it does for the
+ *     reference's own library. On error every block's d is set to NaN.
+ *   vec_dot_q{4,5,6}_K_q8_K: one row of nb K-quant blocks x nb block_q8_K
+ *     (src/kernels/quant_kernels.c:204-521; vec_dot_q*_k_q8_k,
+ *     src/QuantizedKernels.jl:157-175). NaN on error. */
+void  quantize_row_q8_K(const float *x, void *y, int64_t k);
+float vec_dot_q4_K_q8_K(const void *x, const void *y, int nb);
+float vec_dot_q5_K_q8_K(const void *x, const void *y, int nb);
+float vec_dot_q6_K_q8_K(const void *x, const void *y, int nb);
+
 /* Status of the last drop-in call on this thread (IHIP_OK or negative). */
 int ihip_last_status(void);
 /* Drop every cached device weight copy. */

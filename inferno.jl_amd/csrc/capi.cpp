@@ -55,6 +55,9 @@ hipError_t launch_penalties(float *L, int rows, int V, const int32_t *tok, int n
                             float presence, float repetition, hipStream_t st);
 hipError_t launch_gaussian(uint64_t stream, int64_t n, float scale, const float *add, float *out, hipStream_t st);
 hipError_t launch_stream_read(const void *src, int64_t bytes, uint32_t *out, hipStream_t st);
+size_t q8k_block_bytes();
+hipError_t launch_quantize_q8k(const float *x, void *y, int64_t k, hipStream_t st);
+hipError_t launch_vec_dot_q8k(int qt, const void *x, const void *y, int nb, float *out, hipStream_t st);
 size_t noalloc_scratch_bytes();
 hipError_t noalloc_scratch(void **out);
 
@@ -291,9 +294,85 @@ void dropin_gemv(const char *name, int qt, const uint8_t *weight, const float *x
     }
 }
 
+// Host-pointer round trip of the Q8_K helpers on the library stream: copies
+// `nin` input buffers to scratch device memory, runs `launch`, copies `out_bytes`
+// back. The scratch buffers (dx, dws) grow as needed and stay allocated.
+template <class F>
+int dropin_roundtrip(Lib &L, const char *name, const void *in0, size_t b0, const void *in1, size_t b1, void *out,
+                     size_t out_bytes, F launch) {
+    int rc;
+    if (disabled_by_env()) return fail(IHIP_ENODEV, "%s: disabled by INFERNO_NO_QUANT_KERNELS", name);
+    if ((rc = init_locked(L, 0)) != IHIP_OK) return rc;
+    (void)hipSetDevice(L.device);
+    const size_t a0 = (b0 + 255) & ~(size_t)255, a1 = (b1 + 255) & ~(size_t)255;
+    if ((rc = grow(&L.dws, &L.dws_cap, a0 + a1 + out_bytes)) != IHIP_OK) return rc;
+    uint8_t *base = (uint8_t *)L.dws;
+    hipError_t e = hipMemcpyAsync(base, in0, b0, hipMemcpyHostToDevice, L.stream);
+    if (e == hipSuccess && in1) e = hipMemcpyAsync(base + a0, in1, b1, hipMemcpyHostToDevice, L.stream);
+    if (e == hipSuccess) e = launch(base, base + a0, base + a0 + a1, L.stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(out, base + a0 + a1, out_bytes, hipMemcpyDeviceToHost, L.stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(L.stream);
+    return e == hipSuccess ? ok() : hip_fail(e, name);
+}
+
+float dropin_vec_dot(const char *name, int qt, const void *x, const void *y, int nb) {
+    Lib &L = lib();
+    std::lock_guard<std::mutex> lk(L.mu);
+    float r = __builtin_nanf("");
+    int rc;
+    if (!x || !y) {
+        rc = fail(IHIP_EFAULT, "%s: NULL pointer", name);
+    } else if (nb < 0) {
+        rc = fail(IHIP_EINVAL, "%s: nb=%d", name, nb);
+    } else if (nb == 0) {
+        ok();
+        return 0.0f;
+    } else {
+        rc = dropin_roundtrip(L, name, x, (size_t)nb * block_bytes(qt), y, (size_t)nb * q8k_block_bytes(), &r,
+                              sizeof(float), [&](uint8_t *dx, uint8_t *dy, uint8_t *dout, hipStream_t st) {
+                                  return launch_vec_dot_q8k(qt, dx, dy, nb, (float *)dout, st);
+                              });
+    }
+    if (rc != IHIP_OK) {
+        fprintf(stderr, "inferno_hip: %s\n", t_err.c_str());
+        return __builtin_nanf("");
+    }
+    return r;
+}
+
 }  // namespace
 
 extern "C" {
+
+void quantize_row_q8_K(const float *x, void *y, int64_t k) {
+    Lib &L = lib();
+    std::lock_guard<std::mutex> lk(L.mu);
+    int rc;
+    if (!x || !y) {
+        rc = fail(IHIP_EFAULT, "quantize_row_q8_K: NULL pointer");
+    } else if (k < 0 || k % 256) {
+        rc = fail(IHIP_EINVAL, "quantize_row_q8_K: k=%lld is not a multiple of 256", (long long)k);
+    } else if (k == 0) {
+        rc = ok();
+    } else {
+        const size_t nb = (size_t)(k / 256);
+        rc = dropin_roundtrip(L, "quantize_row_q8_K", x, (size_t)k * 4, nullptr, 0, y, nb * q8k_block_bytes(),
+                              [&](uint8_t *dx, uint8_t *, uint8_t *dout, hipStream_t st) {
+                                  return launch_quantize_q8k((const float *)dx, dout, k, st);
+                              });
+    }
+    if (rc != IHIP_OK) {
+        fprintf(stderr, "inferno_hip: %s\n", t_err.c_str());
+        if (y && k > 0 && k % 256 == 0) {  // d = NaN in every block: downstream dot products show the failure
+            const float nan = __builtin_nanf("");
+            for (int64_t b = 0; b < k / 256; b++) memcpy((uint8_t *)y + b * q8k_block_bytes(), &nan, 4);
+        }
+    }
+}
+
+float vec_dot_q4_K_q8_K(const void *x, const void *y, int nb) { return dropin_vec_dot("vec_dot_q4_K_q8_K", IHIP_Q4_K, x, y, nb); }
+float vec_dot_q5_K_q8_K(const void *x, const void *y, int nb) { return dropin_vec_dot("vec_dot_q5_K_q8_K", IHIP_Q5_K, x, y, nb); }
+float vec_dot_q6_K_q8_K(const void *x, const void *y, int nb) { return dropin_vec_dot("vec_dot_q6_K_q8_K", IHIP_Q6_K, x, y, nb); }
 
 const char *ihip_last_error(void) { return t_err.c_str(); }
 // status reporting for the other host files of the library (gguf.cpp)

@@ -28,6 +28,10 @@ SIGNATURES = {
     "q5_k_gemv": (None, [_vp, _vp, _vp, _vp, _i, _i]),
     "q6_k_gemv": (None, [_vp, _vp, _vp, _vp, _i, _i]),
     "q8_0_gemv": (None, [_vp, _vp, _vp, _i, _i]),
+    "quantize_row_q8_K": (None, [_vp, _vp, _i64]),
+    "vec_dot_q4_K_q8_K": (C.c_float, [_vp, _vp, _i]),
+    "vec_dot_q5_K_q8_K": (C.c_float, [_vp, _vp, _i]),
+    "vec_dot_q6_K_q8_K": (C.c_float, [_vp, _vp, _i]),
     "ihip_gemm_q_ws_bytes": (_i, [_i, _i, _i, _i, _i, C.POINTER(_sz)]),
     "ihip_gemm_q": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "ihip_gemm_q_ex": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),

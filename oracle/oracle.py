@@ -285,6 +285,9 @@ def ref():
         R.q8_0_gemv.argtypes = [_u8p, _f32p, _f32p, C.c_int, C.c_int]
         R.quantize_row_q8_K.restype = None
         R.quantize_row_q8_K.argtypes = [_f32p, _u8p, C.c_int64]
+        for n in ("vec_dot_q4_K_q8_K", "vec_dot_q5_K_q8_K", "vec_dot_q6_K_q8_K"):
+            getattr(R, n).restype = C.c_float
+            getattr(R, n).argtypes = [_u8p, _u8p, C.c_int]
         _ref = R
     return _ref
 
@@ -308,3 +311,16 @@ def ref_quantize_q8_K(x: np.ndarray) -> np.ndarray:
     q8 = np.zeros((x.size // 256) * 292, dtype=np.uint8)
     ref().quantize_row_q8_K(x, q8, x.size)
     return q8
+
+
+_DOT = {12: "vec_dot_q4_K_q8_K", 13: "vec_dot_q5_K_q8_K", 14: "vec_dot_q6_K_q8_K"}
+
+
+def ref_vec_dot(qtype: int, w: np.ndarray, q8: np.ndarray, nb: int) -> float:
+    """The reference's vec_dot_q*_K_q8_K (src/kernels/quant_kernels.c:204-521)."""
+    return float(getattr(ref(), _DOT[qtype])(_c(w, np.uint8), _c(q8, np.uint8), nb))
+
+
+def vec_dot(qtype: int, w: np.ndarray, q8: np.ndarray, nb: int) -> float:
+    """The oracle's restatement of the same lane order (orc_vec_dot_*)."""
+    return float(getattr(lib(), "orc_" + _DOT[qtype])(_c(w, np.uint8), _c(q8, np.uint8), nb))

@@ -171,3 +171,26 @@ def test_gemm_ex_input_checks(lib):
     assert b"add slices" in lib.ihip_last_error()
     gi = L.GemmInput(None, 512, 2, None, 1e-6, p16, 2, 5 * 512)  # well-formed: fails only on the workspace size
     assert lib.ihip_gemm_q_ex(12, p16, C.byref(gi), p16, 5, 256, 256, 9, p16, 64, None) == -12
+
+
+def test_q8k_exports_report_failure():
+    """The Q8_K exports have no status return (void / float, as the
+    reference's): with the kill switch set, quantize_row_q8_K leaves d = NaN
+    in every block and vec_dot_q*_K_q8_K return NaN."""
+    code = (
+        "import numpy as np, sys; sys.path.insert(0, %r);"
+        "from inferno_hip import _lib; L = _lib.load();"
+        "x = np.ones(512, np.float32); y = np.zeros(584, np.uint8);"
+        "L.quantize_row_q8_K(x.ctypes.data, y.ctypes.data, 512);"
+        "d = np.frombuffer(y.tobytes(), np.uint8).reshape(2, 292)[:, :4].copy().view(np.float32).ravel();"
+        "w = np.zeros(210, np.uint8);"
+        "r = [L.vec_dot_q4_K_q8_K(w.ctypes.data, y.ctypes.data, 1), L.vec_dot_q5_K_q8_K(w.ctypes.data, y.ctypes.data, 1),"
+        "     L.vec_dot_q6_K_q8_K(w.ctypes.data, y.ctypes.data, 1)];"
+        "print(' '.join(repr(float(v)) for v in list(d) + r), L.ihip_last_status())"
+    ) % os.path.join(ROOT, "inferno.jl_amd")
+    env = dict(os.environ, INFERNO_NO_QUANT_KERNELS="1")
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=120)
+    f = r.stdout.split()
+    vals = [float(v) for v in f[:-1]]
+    assert len(vals) == 5 and all(v != v for v in vals), r.stdout + r.stderr
+    assert int(f[-1]) == -19

@@ -82,6 +82,22 @@ def test_live_reference_kernel(qt):
         assert rel(b, O.gemv_f64(qt, w, xr, 1, N, K)[0]) > 1e-5 or qt == F.Q8_0
 
 
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (needs /root/reference)")
+@pytest.mark.parametrize("qt", [F.Q4_K, F.Q5_K, F.Q6_K])
+def test_live_reference_vec_dot(qt):
+    """orc_vec_dot_* against the reference's exported vec_dot_q*_K_q8_K on
+    single rows (the symbols QuantizedKernels binds at src/QuantizedKernels.jl
+    :157-175), bit for bit."""
+    rng = np.random.default_rng(100 + qt)
+    for nb in (1, 3, 16):
+        w = synth.blocks(qt, nb, synth.stream_for(qt, f"vdref{nb}"))
+        for scale in (1.0, 1e-3, 50.0):
+            q8 = O.ref_quantize_q8_K((rng.standard_normal(256 * nb) * scale).astype(np.float32))
+            a = np.float32(O.vec_dot(qt, w, q8, nb))
+            b = np.float32(O.ref_vec_dot(qt, w, q8, nb))
+            assert a.view(np.uint32) == b.view(np.uint32), (nb, scale, a, b)
+
+
 def test_fp16_conversion_all_patterns():
     bits = np.arange(65536, dtype=np.uint32)
     ref = bits.astype(np.uint16).view(np.float16).astype(np.float32)
