@@ -90,6 +90,37 @@ def _ptr(t) -> int:
     return t.data_ptr()
 
 
+def check_tensor(t, name: str, dtype=None, shape=None, contiguous: bool = True, min_numel: int | None = None):
+    """Raise ValueError unless t is a GPU tensor of the given dtype, shape
+    (None entries match any size) and layout: the C ABI sees only raw
+    pointers, so a mis-shaped or host tensor would become out-of-bounds
+    device accesses."""
+    import torch
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a torch tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if contiguous and not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if shape is not None:
+        if t.dim() != len(shape) or any(w is not None and int(g) != int(w) for g, w in zip(t.shape, shape)):
+            raise ValueError(f"{name} must have shape {tuple('*' if w is None else w for w in shape)}, "
+                             f"got {tuple(t.shape)}")
+    if min_numel is not None and t.numel() < min_numel:
+        raise ValueError(f"{name} needs at least {min_numel} elements, has {t.numel()}")
+    return t
+
+
+def _check_weights(qtype: int, w_dev, n: int, k: int, flags: int):
+    import torch
+    if qtype not in BLOCK_BYTES:
+        raise ValueError(f"unsupported qtype {qtype}")
+    need = packed_bytes(qtype, n, k) if flags & GEMM_PACKED else n * (k // BLOCK_ELEMS[qtype]) * BLOCK_BYTES[qtype]
+    check_tensor(w_dev, "w_dev", torch.uint8, min_numel=need)
+
+
 def gemm_q(qtype: int, w_dev, x, n: int, k: int, flags: int = GEMM_AUTO, out=None, stream=None, ws=None):
     """Y[M x N] = X[M x K] W^T for a device-resident GGUF weight (torch
     uint8 CUDA tensor). x: float32 CUDA tensor [M, K] (M = 1..64). ws: optional
@@ -97,14 +128,16 @@ def gemm_q(qtype: int, w_dev, x, n: int, k: int, flags: int = GEMM_AUTO, out=Non
     import torch
     if x.dim() == 1:
         x = x.view(1, -1)
-    if x.dtype != torch.float32 or not x.is_contiguous() or x.shape[1] != k:
-        raise ValueError("x must be a contiguous float32 [M, K] tensor")
+    check_tensor(x, "x", torch.float32, (None, k))
     m = x.shape[0]
+    _check_weights(qtype, w_dev, n, k, flags)
     if out is None:
         out = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    check_tensor(out, "out", torch.float32, (m, n))
     L = _lib.load()
     if ws is None:
         ws = torch.empty(gemm_ws_bytes(qtype, m, n, k, flags), dtype=torch.uint8, device=x.device)
+    check_tensor(ws, "ws", torch.uint8, min_numel=gemm_ws_bytes(qtype, m, n, k, flags))
     _lib.check(L.ihip_gemm_q(qtype, _ptr(w_dev), _ptr(x), _ptr(out), m, n, k, flags, _ptr(ws), ws.numel(),
                              _stream(stream)))
     return out
@@ -122,6 +155,7 @@ def gemm_q_ex(qtype: int, w_dev, x, n: int, k: int, act: int = ACT_PLAIN, norm_w
     GEMM_DEFER the product stays in ws as partials and `out` is not
     written."""
     import torch
+    width = 2 * k if act == ACT_SILU_MUL else k
     if x is None:
         if add is None or m is None or ldx is None:
             raise ValueError("x=None needs add, m and ldx")
@@ -129,15 +163,22 @@ def gemm_q_ex(qtype: int, w_dev, x, n: int, k: int, act: int = ACT_PLAIN, norm_w
     else:
         if x.dim() == 1:
             x = x.view(1, -1)
-        if x.dtype != torch.float32 or x.stride(1) != 1:
-            raise ValueError("x must be float32 with unit column stride")
+        check_tensor(x, "x", torch.float32, contiguous=False)
+        if x.dim() != 2 or x.stride(1) != 1 or x.shape[1] < width or (m is not None and m > x.shape[0]):
+            raise ValueError(f"x must be [M, >= {width}] float32 with unit column stride")
         m = x.shape[0] if m is None else m
         dev, xp, ldx = x.device, _ptr(x), x.stride(0)
+    _check_weights(qtype, w_dev, n, k, flags)
+    if norm_w is not None:
+        check_tensor(norm_w, "norm_w", torch.float32, min_numel=k)
     if out is None and not (flags & GEMM_DEFER):
         out = torch.empty((m, n), dtype=torch.float32, device=dev)
+    if out is not None:
+        check_tensor(out, "out", torch.float32, (m, n))
     L = _lib.load()
     if ws is None:
         ws = torch.empty(gemm_ws_bytes(qtype, m, n, k, flags), dtype=torch.uint8, device=dev)
+    check_tensor(ws, "ws", torch.uint8, min_numel=gemm_ws_bytes(qtype, m, n, k, flags))
     gi = _lib.GemmInput(xp, ldx, act, None if norm_w is None else _ptr(norm_w), eps,
                         None if add is None else add[0], 0 if add is None else add[1],
                         0 if add is None else add[2])

@@ -14,7 +14,7 @@ from __future__ import annotations
 from dataclasses import dataclass
 
 from . import _lib
-from .quantized_kernels import _ptr, _stream
+from .quantized_kernels import _ptr, _stream, check_tensor
 
 MODE_STANDARD = 0   # p, q at temperature T; residual max(0, p - q)
 MODE_REFERENCE = 1  # src/SpeculativeDecoding.jl:61-63,79-93 as written
@@ -55,6 +55,7 @@ def spec_accept(target_logits, draft_logits, draft_tokens, temperature: float, u
     """
     import torch
     import ctypes as C
+    check_tensor(target_logits, "target_logits", torch.float32)
     if target_logits.dim() == 2:
         target_logits = target_logits.unsqueeze(0)
         draft_logits = draft_logits.unsqueeze(0)
@@ -62,21 +63,28 @@ def spec_accept(target_logits, draft_logits, draft_tokens, temperature: float, u
         u_acc = u_acc.view(1, -1)
         u_res = u_res.view(1)
         u_bonus = u_bonus.view(1)
+    if target_logits.dim() != 3:
+        raise ValueError("target_logits must be [S, k+1, V] (or [k+1, V])")
     S, k1, V = target_logits.shape
     k = k1 - 1
+    check_tensor(draft_logits, "draft_logits", torch.float32, (S, k, V))
+    check_tensor(draft_tokens, "draft_tokens", torch.int32, (S, k))
+    check_tensor(u_acc, "u_acc", torch.float32, (S, k))
+    check_tensor(u_res, "u_res", torch.float32, (S,))
+    check_tensor(u_bonus, "u_bonus", torch.float32, (S,))
     L = _lib.load()
     nb = C.c_size_t()
     _lib.check(L.ihip_spec_accept_ws_bytes(S, k, V, C.byref(nb)))
     dev = target_logits.device
     if ws is None:
         ws = _ws(nb.value, dev)
+    check_tensor(ws, "ws", torch.uint8, min_numel=nb.value)
     if out_tok is None:
         out_tok = torch.zeros((S, k + 1), dtype=torch.int32, device=dev)
     if out_n is None:
         out_n = torch.zeros(S, dtype=torch.int32, device=dev)
-    for t in (target_logits, draft_logits, draft_tokens, u_acc, u_res, u_bonus):
-        if not t.is_contiguous():
-            raise ValueError("inputs must be contiguous")
+    check_tensor(out_tok, "out_tok", torch.int32, (S, k + 1))
+    check_tensor(out_n, "out_n", torch.int32, (S,))
     _lib.check(L.ihip_spec_accept(_ptr(target_logits), _ptr(draft_logits), _ptr(draft_tokens), S, k, V,
                                   temperature, _ptr(u_acc), _ptr(u_res), _ptr(u_bonus), mode, _ptr(out_tok),
                                   _ptr(out_n), _ptr(ws), ws.numel(), _stream(stream)))
@@ -97,11 +105,15 @@ def greedy_verify(logits, draft_tokens, stream=None):
     """logits [S, k+1, V], draft_tokens [S, k] -> (out_n [S], argmax [S, k+1])."""
     import torch
     import ctypes as C
+    check_tensor(logits, "logits", torch.float32)
     if logits.dim() == 2:
         logits = logits.unsqueeze(0)
         draft_tokens = draft_tokens.view(1, -1)
+    if logits.dim() != 3:
+        raise ValueError("logits must be [S, k+1, V] (or [k+1, V])")
     S, k1, V = logits.shape
     k = k1 - 1
+    check_tensor(draft_tokens, "draft_tokens", torch.int32, (S, k))
     L = _lib.load()
     nb = C.c_size_t()
     _lib.check(L.ihip_accept_ws_bytes(S * k1, V, C.byref(nb)))
@@ -128,7 +140,12 @@ def tree_accept(target_logits, draft_logits, node_tokens, parent, temperature: f
     out_len = -1."""
     import torch
     import ctypes as C
+    check_tensor(target_logits, "target_logits", torch.float32, (None, None))
     n, V = target_logits.shape
+    check_tensor(draft_logits, "draft_logits", torch.float32, (n, V))
+    check_tensor(node_tokens, "node_tokens", torch.int32, (n,))
+    check_tensor(parent, "parent", torch.int32, (n,))
+    check_tensor(u, "u", torch.float32, (n,))
     L = _lib.load()
     nb = C.c_size_t()
     _lib.check(L.ihip_accept_ws_bytes(3 * n, V, C.byref(nb)))

@@ -25,7 +25,8 @@
  *                        tree reduces to orc_spec_accept's accepted length.
  *                        The reference has no tree code: reference parity is
  *                        unpinned by construction (no counterpart).
- *   orc_rmsnorm          pinned: closed form on constant vectors.
+ *   orc_rmsnorm          pinned: closed forms (constant vectors, [3, 4], one
+ *                        nonzero element, zeros): tests/test_host_logic.py.
  */
 #ifndef INFERNO_ORACLE_H
 #define INFERNO_ORACLE_H

@@ -12,7 +12,7 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+LIB_PATH = os.environ.get("INFERNO_ORACLE_LIB", os.path.join(HERE, "liboracle.so"))
 REF_PATH = os.path.join(HERE, "_ref", "libquant_kernels_ref.so")
 
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")

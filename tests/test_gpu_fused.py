@@ -100,8 +100,15 @@ def test_ex_errors(ih):
     qt = F.Q4_K
     w = ih.pack_weights(qt, _dev(synth.matrix(qt, 16, 256, 1)), 16, 256)
     x = torch.zeros(40, 512, device="cuda")
-    with pytest.raises(ih.HipError):
-        ih.gemm_q_ex(qt, w, x[:, :256], 16, 512, act=ih.ACT_SILU_MUL)  # ldx < 2K
+    with pytest.raises(ValueError):  # rows narrower than 2K: the wrapper refuses before the C ABI
+        ih.gemm_q_ex(qt, w, x[:, :256], 16, 256, act=ih.ACT_SILU_MUL)
+    # the C ABI's own check of the same case (ldx < 2K)
+    import ctypes as C
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    y = torch.empty(40, 16, device="cuda")
+    gi = ih._lib.GemmInput(x.data_ptr(), 256, ih.ACT_SILU_MUL, None, 1e-6, None, 0, 0)
+    assert ih.load().ihip_gemm_q_ex(qt, w.data_ptr(), C.byref(gi), y.data_ptr(), 40, 16, 256, ih.GEMM_PACKED,
+                                    ws.data_ptr(), ws.numel(), None) == -22
     with pytest.raises(ih.HipError):  # reuse with M > 32 fp32-accurate
         ih.gemm_q_ex(qt, w, x[:, :256], 16, 256, flags=ih.GEMM_F32 | ih.GEMM_PACKED | ih.GEMM_REUSE)
     with pytest.raises(ih.HipError):

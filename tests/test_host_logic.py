@@ -46,13 +46,74 @@ def test_gaussian_moments():
     assert abs(z.mean()) < 0.01 and abs(z.std() - 1) < 0.01
 
 
-def test_speculative_stats_formula():
-    # src/SpeculativeDecoding.jl:163-164
+def test_speculative_stats_hand_trace():
+    """generate_speculative_cpu's counters (src/SpeculativeDecoding.jl:114-172),
+    worked by hand for gamma = 4, a 3-token prompt, max_tokens = 10 and steps
+    returning 5 tokens (4 drafts + bonus), 2 (1 draft + residual), 5:
+      after step 1: tokens_generated 5, total_draft_tokens 4, total_accepted 5
+      after step 2: 7, 8, 7
+      after step 3: 12 (the inner loop pushes every returned token), 12, 12,
+      and 12 >= 10 ends the loop.
+    acceptance_rate = 12 / 12 = 1.0 (:163, returned tokens over drafted ones);
+    speedup_estimate = (12 - 3) / (12 + 12) * (1 + 4) = 1.875 (:164; the
+    prompt length is subtracted although tokens_generated never counted it)."""
     s = SpeculativeStats(gamma=4, prompt_len=3)
-    s.tokens_generated = 0
-    for n_out in (5, 2, 1, 5):
-        s.record(n_out)
+    returned = iter((5, 2, 5, 5, 5))
+    steps = 0
+    while s.tokens_generated < 10:   # the loop condition of :142 (and the break of :158)
+        s.record(next(returned))
+        steps += 1
     d = s.as_dict()
-    assert d["draft_tokens_generated"] == 16 and d["tokens_accepted"] == 13
-    assert d["acceptance_rate"] == 13 / 16
-    assert d["speedup_estimate"] == (13 - 3) / (16 + 13) * 5
+    assert steps == 3
+    assert d == {"acceptance_rate": 1.0, "draft_tokens_generated": 12, "tokens_accepted": 12,
+                 "speedup_estimate": 1.875}
+    # a run that rejects early: two steps of 1 token each (residual at position 0)
+    s = SpeculativeStats(gamma=4, prompt_len=0)
+    s.record(1)
+    s.record(1)
+    assert s.as_dict() == {"acceptance_rate": 0.25, "draft_tokens_generated": 8, "tokens_accepted": 2,
+                           "speedup_estimate": 2 / 10 * 5}
+
+
+def test_oracle_rmsnorm_closed_forms():
+    """orc_rmsnorm (src/ModelCPU.jl:110-122: x / sqrt(mean(x^2) + eps) * w) on
+    inputs whose result is known in closed form."""
+    import oracle as O
+    eps = 1e-6
+    # constant vector c: mean square c^2, result c / sqrt(c^2 + eps) * w
+    for c, n in ((3.0, 16), (-0.5, 7), (1e3, 4096)):
+        x = np.full(n, c, np.float32)
+        w = np.linspace(0.5, 2.0, n).astype(np.float32)
+        want = c / np.sqrt(c * c + eps) * w.astype(np.float64)
+        assert np.allclose(O.rmsnorm(x, eps, w), want, rtol=3e-7, atol=0)
+    # [3, 4]: mean square 12.5
+    got = O.rmsnorm(np.array([3.0, 4.0], np.float32), 0.0)
+    assert np.allclose(got, [3 / np.sqrt(12.5), 4 / np.sqrt(12.5)], rtol=3e-7, atol=0)
+    # one nonzero of n = 4: mean square a^2 / 4, result +-2 (eps negligible)
+    got = O.rmsnorm(np.array([0.0, -7.0, 0.0, 0.0], np.float32), 0.0)
+    assert got.tolist() == [0.0, -2.0, 0.0, 0.0]
+    # all zeros: eps alone, result 0
+    assert not O.rmsnorm(np.zeros(8, np.float32), eps).any()
+
+
+def test_wrappers_reject_bad_tensors_before_the_library():
+    """The Python wrappers validate every tensor (device, dtype, shape,
+    layout) before a pointer reaches the C ABI, which cannot see sizes: host
+    tensors, wrong dtypes and mis-shaped arguments raise ValueError."""
+    import pytest
+    import torch
+    import inferno_hip as ih
+    f32 = lambda *s: torch.zeros(*s, dtype=torch.float32)  # noqa: E731  (host tensors)
+    i32 = lambda *s: torch.zeros(*s, dtype=torch.int32)  # noqa: E731
+    with pytest.raises(ValueError, match="GPU"):
+        ih.spec_accept(f32(2, 5, 64), f32(2, 4, 64), i32(2, 4), 0.8, f32(2, 4), f32(2), f32(2))
+    with pytest.raises(ValueError, match="GPU"):
+        ih.greedy_verify(f32(1, 5, 64), i32(1, 4))
+    with pytest.raises(ValueError, match="GPU"):
+        ih.tree_accept(f32(4, 64), f32(4, 64), i32(4), i32(4), 1.0, f32(4))
+    with pytest.raises(ValueError, match="GPU"):
+        ih.gemm_q(ih.formats.Q4_K, torch.zeros(144, dtype=torch.uint8), f32(1, 256), 1, 256)
+    with pytest.raises(ValueError):
+        ih.gemm_q_ex(ih.formats.Q4_K, torch.zeros(144, dtype=torch.uint8), f32(1, 256), 1, 256)
+    with pytest.raises(ValueError, match="torch tensor"):
+        ih.quantized_kernels.check_tensor(None, "x")
