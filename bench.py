@@ -52,18 +52,23 @@ class Model:
               "o": ("Q4_K", H, NQ, "attn_output"), "gu": ("Q4_K", 2 * FF, H, "ffn_gate_up"),  # gate then up
               "down": ("Q6_K", H, FF, "ffn_down")}
 
-    def __init__(self, ih, n_layers: int, keep_gguf: int = 4, proj: str = "Q4_K"):
+    def __init__(self, ih, n_layers: int, keep_gguf: int = 4, proj: str = "Q4_K", gated: bool = False):
         import torch
         F = ih.formats
         st = ih.synth.stream_for
         self.proj = getattr(F, proj)  # format of the q/k/v/o/gate/up projections (config 5: Q4_K or Q5_K)
+        # gated: [gate; up] packed in tiles of 8 gate rows and their 8 up rows (the chained step's layout)
+        self.gated = gated
         self.layers, self.host_gguf, self.gguf_bytes = [], [], 0
         for L in range(n_layers):
             lw, hw = {}, {}
             for key, (qn, rows, k, name) in self.SHAPES.items():
                 qt = self.proj if qn == "Q4_K" else getattr(F, qn)
                 g = ih.quantized_kernels.synth_blocks(qt, st(SEED, f"blk{L}.{name}"), rows * k // F.BLOCK_ELEMS[qt])
-                lw[key] = ih.pack_weights(qt, g, rows, k)
+                if key == "gu" and gated:
+                    lw[key] = ih.pack_weights_gated(qt, g, rows // 2, k)
+                else:
+                    lw[key] = ih.pack_weights(qt, g, rows, k)
                 self.gguf_bytes += g.numel()
                 if L < keep_gguf:
                     hw[key] = g.cpu().numpy()
@@ -215,6 +220,68 @@ class VerifyStep:
                             ws=self.acc_ws)
 
 
+class ChainStep(VerifyStep):
+    """The verify step with chained matmuls (ihip_gemm_q_chain, gated model
+    weights): per layer one input stage, that of [q; k; v] (the previous
+    layer's down partials folded into the residual, RMSNorm). [q; k; v]
+    writes o's operand (its q rows, split fp16 at per-tile scales); o adds
+    its product into the residual and writes [gate; up]'s operand (the
+    residual times the FFN norm weight) with the tile sums of squares of the
+    RMSNorm; [gate; up] writes h = silu(gate) up and down's operand; down
+    leaves K-slice partials. Same arithmetic as VerifyStep.forward
+    (fp32-accurate, M <= 8), three input-stage launches fewer per layer."""
+
+    def __init__(self, ih, model: Model, M: int, k: int, T: float):
+        import torch
+        assert model.gated and M <= 8, "the chained step needs gated weights and one token tile"
+        F = ih.formats
+        self.h = torch.empty((M, FF), device="cuda")
+        self.op_q, self.ts_q, _ = ih.chain_buffers(NQ)
+        self.op_x, self.ts_x, self.ssq_x = ih.chain_buffers(H, ssq=True)
+        self.op_h, _, _ = ih.chain_buffers(FF, tiles_per_unit=32)
+        super().__init__(ih, model, M, k, T, prec=1)
+
+    def _descriptors(self):
+        # (built at the first forward: VerifyStep's constructor runs one, after making x and qkv)
+        ih, F = self.ih, self.ih.formats
+        cin, cout = ih.chain_in, ih.chain_out
+        self.o_in = cin(self.op_q, self.ts_q, 16)
+        self.gu_in = cin(self.op_x, self.ts_x, 16, tile_ssq=self.ssq_x, eps=1e-6)
+        self.down_in = cin(self.op_h, None, 32)
+        self.qkv_out = cout(ih.EPI_STATS, self.qkv, F.Q4_K, self.op_q, self.ts_q, stat_rows=NQ)
+        self.o_out = [cout(ih.EPI_RESID, self.x, F.Q4_K, self.op_x, self.ts_x, norm_w=lw["ffn_norm"],
+                           tile_ssq=self.ssq_x) for lw in self.model.layers]
+        self.gu_out = cout(ih.EPI_GATE, self.h, F.Q6_K, self.op_h)
+
+    def forward(self, probe=None):
+        ih, F, M = self.ih, self.ih.formats, self.M
+        if not hasattr(self, "qkv_out"):
+            self._descriptors()
+        P = self.model.proj
+        chain = ih.gemm_q_chain
+        fl = ih.GEMM_F32 | ih.GEMM_PACKED
+        parts = ih.gemm_partials(F.Q6_K, M, H, FF, fl, self.ws_down)
+        self.x.copy_(self.x0)
+        for i, lw in enumerate(self.model.layers):
+            if probe:
+                probe("pre", i)
+            chain(P, lw["qkv"], NQ + 2 * NKV, H, M, x=self.x, act=ih.ACT_RMSNORM, norm_w=lw["attn_norm"],
+                  add=parts if i > 0 else None, ws=self.ws, cout=self.qkv_out)
+            if probe:
+                probe("qkv", i)
+            chain(P, lw["o"], H, NQ, M, cin=self.o_in, ws=self.ws_o, cout=self.o_out[i])
+            if probe:
+                probe("o", i)
+            chain(P, lw["gu"], 2 * FF, H, M, ws=self.ws, cin=self.gu_in, cout=self.gu_out)
+            if probe:
+                probe("gu", i)
+            chain(F.Q6_K, lw["down"], H, FF, M, cin=self.down_in, flags=fl | ih.GEMM_DEFER, ws=self.ws_down)
+        ih.gemm_q_ex(F.Q6_K, self.model.lm, self.x, VOCAB, H, act=ih.ACT_RMSNORM, norm_w=self.model.out_norm,
+                     flags=fl, out=self.logits, ws=self.ws, add=parts)
+        if probe:
+            probe("head", len(self.model.layers))
+
+
 class TreeStep(VerifyStep):
     """Config 5: a 64-node draft tree (branching 4, 4, 4 in BFS order,
     truncated to 64 nodes) verified in one forward at M = 64 (half-precision
@@ -285,26 +352,47 @@ def graph_launch_time(launch, iters: int, replays: int, warm: int) -> float:
 
 def gemm_roofline(ih, model: Model, n_layers: int, M: int, iters: int = 64, replays: int = 15, warm: int = 4):
     """Dominant kernel: the Q4_K gate/up dequant-matmul (24576x4096, M=5)
-    over the layers' weights in turn (1.8 GB, far beyond the 256 MB cache).
-    The activations are prepared once; `iters` matmul launches that reuse
-    them are timed as one replayed graph (graph_launch_time): the matmul
-    kernel plus its dispatch gap, which is what a kernel trace reports as
-    its duration (its launches run back to back). Returns (seconds per
-    launch, algorithmic bytes per launch)."""
+    over the layers' weights in turn (1.8 GB, far beyond the 256 MB cache),
+    as the timed step runs it: with gated weights (the chained step) the
+    chained call that loads the operand its producer wrote (rescaled per unit
+    in registers) and writes h = silu(gate) up and down's operand
+    (algorithmic bytes: weights + operand + h and its operand); otherwise the
+    classic call with its activations
+    prepared once and reused (weights + x + y). `iters` launches are timed as
+    one replayed graph (graph_launch_time): the kernel plus its dispatch gap,
+    which is what a kernel trace reports as its duration (its launches run
+    back to back). Returns (seconds per launch, algorithmic bytes per
+    launch)."""
     import torch
-    F = ih.formats
+    F, q = ih.formats, ih.quantized_kernels
     N, K = 2 * FF, H
-    x = ih.quantized_kernels.synth_gaussian(123, M * K).view(M, K)
-    y = torch.empty((M, N), device="cuda")
+    x = q.synth_gaussian(123, M * K).view(M, K)
     fl = ih.GEMM_F32 | ih.GEMM_PACKED
-    ws = torch.empty(ih.quantized_kernels.gemm_ws_bytes(F.Q4_K, M, N, K, fl), dtype=torch.uint8, device="cuda")
-    ih.gemm_q_ex(F.Q4_K, model.layers[0]["gu"], x, N, K, flags=fl, out=y, ws=ws)  # prepares x
+    ws = torch.empty(q.gemm_ws_bytes(F.Q4_K, M, N, K, fl), dtype=torch.uint8, device="cuda")
+    if model.gated:
+        # gate/up's operand as the chained o leaves it: here from a producer call on the same
+        # residual rows (the first layer's o as the matrix, an input stage), with the RMSNorm sums
+        op, ts, ssq = ih.chain_buffers(K, ssq=True)
+        y0 = torch.empty((M, K), device="cuda")
+        ih.gemm_q_chain(F.Q4_K, model.layers[0]["o"], K, NQ, M, x=x[:, :NQ].contiguous(), ws=ws,
+                        cout=ih.chain_out(ih.EPI_STATS, y0, F.Q4_K, op, ts, tile_ssq=ssq, stat_rows=K))
+        h = torch.empty((M, FF), device="cuda")
+        op_h, _, _ = ih.chain_buffers(FF, tiles_per_unit=32)
+        cin = ih.chain_in(op, ts, 16, tile_ssq=ssq, eps=1e-6)
+        cout = ih.chain_out(ih.EPI_GATE, h, F.Q6_K, op_h)
 
-    def mat(i):
-        ih.gemm_q_ex(F.Q4_K, model.layers[i % n_layers]["gu"], x, N, K, flags=fl | ih.GEMM_REUSE, out=y, ws=ws)
+        def mat(i):
+            ih.gemm_q_chain(F.Q4_K, model.layers[i % n_layers]["gu"], N, K, M, cin=cin, cout=cout, ws=ws)
+        # algorithmic bytes: weights, the operand in (split fp16: 4 bytes a value) and h out with its operand
+        alg = F.matrix_bytes(F.Q4_K, N, K) + M * K * 4 + M * FF * 8
+    else:
+        y = torch.empty((M, N), device="cuda")
+        ih.gemm_q_ex(F.Q4_K, model.layers[0]["gu"], x, N, K, flags=fl, out=y, ws=ws)  # prepares x
 
+        def mat(i):
+            ih.gemm_q_ex(F.Q4_K, model.layers[i % n_layers]["gu"], x, N, K, flags=fl | ih.GEMM_REUSE, out=y, ws=ws)
+        alg = F.matrix_bytes(F.Q4_K, N, K) + M * K * 4 + M * N * 4
     t = graph_launch_time(mat, iters, replays, warm)
-    alg = F.matrix_bytes(F.Q4_K, N, K) + M * K * 4 + M * N * 4
     return t, alg
 
 
@@ -629,7 +717,8 @@ def config4(ih, model: Model, replays: int = 20):
     out = {}
     for M in (1, 2, 4, 5, 8):
         k = M - 1
-        step = VerifyStep(ih, model, M, max(k, 1), 0.8)  # (M = 1: the draft side is set up, not used)
+        make = ChainStep if model.gated else VerifyStep
+        step = make(ih, model, M, max(k, 1), 0.8)  # (M = 1: the draft side is set up, not used)
         t = graph_time(step.forward if k == 0 else step.run, replays=replays)
         w = model.weight_bytes(len(model.layers))
         out[str(M)] = {"k": k, "ms_per_step": round(t * 1e3, 4), "steps_per_s": round(1 / t, 1),
@@ -843,6 +932,8 @@ def main():
     ap.add_argument("--m", type=int, default=5)
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--classic", action="store_true",
+                    help="time the verify step with an input stage before every matmul (no chained matmuls)")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--profile-kernels", action="store_true",
                     help="only run the roofline kernel and the traffic calibration kernel (for rocprofv3 --pmc)")
@@ -878,7 +969,7 @@ def main():
             if c == "5":
                 res = config5(ih, Model(ih, args.layers, keep_gguf=0))
             elif c == "4":
-                res = config4(ih, Model(ih, args.layers, keep_gguf=0))
+                res = config4(ih, Model(ih, args.layers, keep_gguf=0, gated=not args.classic))
             elif c == "sampler":
                 res = sampler_config(ih)
             elif c == "gguf":
@@ -888,8 +979,9 @@ def main():
             print(json.dumps({"config": c if c in ("sampler", "gguf") else int(c), **res}), flush=True)
             torch.cuda.empty_cache()
         return
-    model = Model(ih, args.layers, keep_gguf=0 if (args.no_cpu or args.profile_kernels) else 4)
-    step = VerifyStep(ih, model, args.m, k, T)
+    chained = not args.classic and args.m <= 8
+    model = Model(ih, args.layers, keep_gguf=0 if (args.no_cpu or args.profile_kernels) else 4, gated=chained)
+    step = ChainStep(ih, model, args.m, k, T) if chained else VerifyStep(ih, model, args.m, k, T)
     log(f"setup {time.time() - t0:.1f}s, weights {model.weight_bytes(args.layers) / 1e9:.3f} GB")
     if args.profile_kernels:
         profile_kernels(ih, model, args.layers, args.m)
@@ -955,9 +1047,15 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": read_traffic(),
-            "kernel": "gemm_v_kernel<Q4_K>: packed Q4_K dequant-matmul 24576x4096, M=5, fp32-accurate "
-                      "(activations prepared once); per launch in a replayed graph of 64 launches over cold "
+            "kernel": ("gemm_v_kernel<Q4_K, chained input>: packed Q4_K [gate; up] dequant-matmul 24576x4096, "
+                       "M=5, fp32-accurate, operand written by its producer (rescaled per unit in registers), "
+                       "h = silu(gate) up and down's operand out"
+                       if model.gated else
+                       "gemm_v_kernel<Q4_K>: packed Q4_K dequant-matmul 24576x4096, M=5, fp32-accurate "
+                       "(activations prepared once)") +
+                      "; per launch in a replayed graph of 64 launches over cold "
                       "weights, median of 15 replays, HIP events (dispatch gap included, as in a kernel trace)",
+            "step_composition": "chained (one input stage per layer)" if chained else "classic (input stage per matmul)",
             "us_per_launch": round(t_op * 1e6, 2),
             "algorithmic_bytes": alg,
             "measured_peak": max(peaks.values()),

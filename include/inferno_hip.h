@@ -194,6 +194,87 @@ int ihip_gemm_q_ex(int qtype, const void *w_dev, const ihip_gemm_input *in,
 int ihip_gemm_q_partials(int qtype, int M, int N, int K, int flags, void *ws,
                          float **slices, int *n_slices, int64_t *stride);
 
+/* ---- chained matmuls: one input stage per decoder layer instead of four ----
+ * fp32-accurate calls on packed weights with one token tile (M <= 8) can hand
+ * their output to the next matmul without its input stage. The producer's
+ * epilogue (ihip_chain_out) stores the fp32 result y and writes the next
+ * matmul's split-fp16 operand of v = y w (w: the next input's RMSNorm weight,
+ * or 1) in the consumer's layout (consumer_qtype), each 16-row output tile
+ * (8 channels for IHIP_EPI_GATE) scaled by its own power of two (its largest
+ * |v| in [2^14, 2^15)) and tagged with that exponent; beside it the tile's sum
+ * of v (min terms of Q4_K/Q5_K consumers) and, for an RMSNorm that follows,
+ * the tile's sum of y^2. The consumer (ihip_chain_in) loads that operand as a
+ * classic call loads its prepared one and rescales it to the power of two of
+ * each 256-element unit (the input stage's), exactly wherever the result
+ * stays a normal fp16; it applies the RMSNorm row scale 1 / sqrt(sum ssq / K
+ * + eps) to its result. The layer arithmetic stays that of
+ * src/ModelCPU.jl:110-122 (RMSNorm), :447-473 (SiLU gating) and :870-891
+ * (residual adds).
+ * Epilogues:
+ *   IHIP_EPI_STORE: y = the product (no operand, no statistics);
+ *   IHIP_EPI_STATS: y = the product; operand and statistics of rows
+ *                   [0, stat_rows) (e.g. the q rows of [q; k; v], the input
+ *                   of o);
+ *   IHIP_EPI_RESID: y += the product (y: the residual), operand and
+ *                   statistics of the sum (the input of the next RMSNorm'd
+ *                   matmul);
+ *   IHIP_EPI_GATE:  the weights were packed by ihip_pack_weights_gated (tiles
+ *                   of 8 gate rows and their 8 up rows, N = 2F rows); y [M x
+ *                   ldy] receives h = silu(gate) * up, F values per row, and
+ *                   the operand and statistics are of h (tiles of 8
+ *                   channels: the consumer's tiles_per_unit is 32).
+ * Tile sums: tile_sum [8 tokens][sum_stride] (16-byte aligned, sum_stride a
+ * multiple of 4 covering every tile), tile_ssq [tiles][8]. */
+#define IHIP_EPI_STORE 0
+#define IHIP_EPI_STATS 1
+#define IHIP_EPI_RESID 2
+#define IHIP_EPI_GATE  3
+/* Bytes of a chained operand for a consumer with K inputs (K a multiple of
+ * 256): limbs, then one exponent byte per lane entry, per 256-element unit. */
+size_t ihip_chain_operand_bytes(int K);
+typedef struct ihip_chain_in {
+    const void *operand;     /* the producer's operand (ihip_chain_operand_bytes(K), 16-byte aligned) */
+    const float *tile_sum;   /* the producer's tile sums [8][sum_stride]
+                                (Q4_K/Q5_K consumers; may be NULL otherwise) */
+    int sum_stride;
+    int tiles_per_unit;      /* 16, or 32 after IHIP_EPI_GATE */
+    const float *tile_ssq;   /* the producer's tile sums of squares [ssq_tiles][8]
+                                (RMSNorm row scale), or NULL (none) */
+    int ssq_tiles;
+    float eps;
+} ihip_chain_in;
+typedef struct ihip_chain_out {
+    int epi;                 /* IHIP_EPI_* */
+    float *y;
+    int ldy;                 /* floats between rows of y */
+    const float *norm_w;     /* RMSNorm weight of the next input [width], or NULL */
+    int consumer_qtype;      /* IHIP_Q4_K / Q5_K / Q6_K / Q8_0: the next matmul's */
+    void *operand;           /* ihip_chain_operand_bytes(width) bytes, or NULL */
+    float *tile_sum;         /* [8][sum_stride], or NULL (needed by Q4_K/Q5_K consumers) */
+    int sum_stride;
+    float *tile_ssq;         /* [tiles][8], or NULL */
+    int stat_rows;           /* IHIP_EPI_STATS: rows [0, stat_rows), a multiple of 256 */
+} ihip_chain_out;
+/* Y = f(X) W^T for packed weights, fp32-accurate, M <= 8, one of in (the usual
+ * input stage, e.g. RMSNorm with the previous layer's partials folded) or cin
+ * (a chained producer's operand), and cout (NULL only with IHIP_GEMM_DEFER,
+ * which leaves K-slice partials as ihip_gemm_q_ex does). flags: IHIP_GEMM_F32,
+ * IHIP_GEMM_PACKED, IHIP_GEMM_DEFER. Epilogues other than IHIP_EPI_STORE need
+ * a matmul that is not split over K (K up to 8192 for Q4_K, 4096 for Q5_K /
+ * Q6_K, 2048 for Q8_0); shapes off the one-tile streaming plan return
+ * IHIP_EINVAL. The width an operand covers (N; N / 2 for IHIP_EPI_GATE;
+ * stat_rows for IHIP_EPI_STATS) must be a multiple of 256. Workspace as
+ * ihip_gemm_q. */
+int ihip_gemm_q_chain(int qtype, const void *w_packed, const ihip_gemm_input *in,
+                      const ihip_chain_in *cin, const ihip_chain_out *cout,
+                      int M, int N, int K, int flags, void *ws, size_t ws_bytes,
+                      void *stream);
+/* The [gate; up] GGUF matrix [2F x K] (gate rows, then up rows) packed into
+ * tiles of 8 gate rows and their 8 up rows, for IHIP_EPI_GATE (F a multiple
+ * of 8; ihip_packed_bytes(qtype, 2F, K) bytes). */
+int ihip_pack_weights_gated(int qtype, const void *w_gguf_dev, void *w_packed_dev,
+                            int F, int K, void *stream);
+
 /* Packed weight layout: the GGUF blocks of each 16-row tile and 256-element
  * K-unit stored as one contiguous chunk, swizzled so that every lane of the
  * matmul kernel fetches its operand bytes with whole-cache-line 16-byte

@@ -11,6 +11,7 @@
 #include <utility>
 
 #include "../../include/inferno_hip.h"
+#include "chain.h"
 
 // kernels (gemm.hip, dequant.hip, accept.hip, misc.hip)
 hipError_t launch_gemm(int qt, const void *W, const float *X, float *Y, int M, int N, int K, int flags, void *ws,
@@ -22,7 +23,7 @@ hipError_t launch_gemm_ex(int qt, const void *W, const float *X, int ldx, int op
                           void *ws, hipStream_t st);
 bool gemm_reuse_ok(int M, int flags);
 void gemm_partials(int qt, int M, int N, int K, int flags, size_t *offset, int *n_slices);
-hipError_t launch_pack(int qt, const void *W, void *P, int N, int K, hipStream_t st);
+hipError_t launch_pack(int qt, const void *W, void *P, int N, int K, hipStream_t st, int gated);
 hipError_t launch_dequant(int qt, const void *w, float *out, int64_t n_blocks, hipStream_t st);
 int accept_nchunk(int V);
 hipError_t launch_stats(const float *L, int rows, int V, float T, float T_last, int period, float2 *part,
@@ -55,6 +56,11 @@ hipError_t launch_penalties(float *L, int rows, int V, const int32_t *tok, int n
                             float presence, float repetition, hipStream_t st);
 hipError_t launch_gaussian(uint64_t stream, int64_t n, float scale, const float *add, float *out, hipStream_t st);
 hipError_t launch_stream_read(const void *src, int64_t bytes, uint32_t *out, hipStream_t st);
+// chained matmuls (gemm.hip)
+hipError_t launch_gemm_chain_ex(int qt, const void *W, const float *X, int ldx, int op, const float *norm_w,
+                                float eps_in, const float *add, int n_add, int64_t add_stride, const Chain &ch,
+                                const float *ssq_in, int n_ssq_in, float eps, float *Y, int M, int N, int K,
+                                int flags, void *ws, hipStream_t st);
 size_t q8k_block_bytes();
 hipError_t launch_quantize_q8k(const float *x, void *y, int64_t k, hipStream_t st);
 hipError_t launch_vec_dot_q8k(int qt, const void *x, const void *y, int nb, float *out, hipStream_t st);
@@ -262,7 +268,7 @@ void dropin_gemv(const char *name, int qt, const uint8_t *weight, const float *x
             e = hipMalloc(&raw, wbytes);
             if (e == hipSuccess) e = hipMalloc(&dw, pbytes);
             if (e == hipSuccess) e = hipMemcpy(raw, weight, wbytes, hipMemcpyHostToDevice);
-            if (e == hipSuccess) e = launch_pack(qt, raw, dw, N, K, L.stream);
+            if (e == hipSuccess) e = launch_pack(qt, raw, dw, N, K, L.stream, 0);
             if (e == hipSuccess) e = hipStreamSynchronize(L.stream);
             if (raw) (void)hipFree(raw);
             if (e == hipSuccess) {
@@ -459,6 +465,118 @@ int ihip_gemm_q_noalloc(int qtype, const void *w_dev, const float *x_dev, float 
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_gemm_q_noalloc");
 }
 
+int ihip_pack_weights_gated(int qtype, const void *w_gguf_dev, void *w_packed_dev, int F, int K, void *stream) {
+    if (!w_gguf_dev || !w_packed_dev) return fail(IHIP_EFAULT, "ihip_pack_weights_gated: NULL pointer");
+    if (!is_qtype(qtype) || F < 8 || F % 8 || K < 1 || K % block_elems(qtype))
+        return fail(IHIP_EINVAL, "ihip_pack_weights_gated: qtype %d F=%d K=%d (F a multiple of 8)", qtype, F, K);
+    hipError_t e = launch_pack(qtype, w_gguf_dev, w_packed_dev, 2 * F, K, S(stream), F);
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_pack_weights_gated");
+}
+
+size_t ihip_chain_operand_bytes(int K) { return K > 0 ? (size_t)chain_operand_bytes(K) : 0; }
+
+int ihip_gemm_q_chain(int qtype, const void *w_packed, const ihip_gemm_input *in, const ihip_chain_in *cin,
+                      const ihip_chain_out *cout, int M, int N, int K, int flags, void *ws, size_t ws_bytes,
+                      void *stream) {
+    const char *fn = "ihip_gemm_q_chain";
+    if (!w_packed || !ws) return fail(IHIP_EFAULT, "%s: NULL weights or workspace", fn);
+    if ((in == nullptr) == (cin == nullptr)) return fail(IHIP_EINVAL, "%s: pass exactly one of in / cin", fn);
+    const bool defer = flags & IHIP_GEMM_DEFER;
+    if (flags & ~(IHIP_GEMM_F32 | IHIP_GEMM_PACKED | IHIP_GEMM_DEFER))
+        return fail(IHIP_EINVAL, "%s: flags 0x%x (fp32-accurate packed only, IHIP_GEMM_DEFER allowed)", fn, flags);
+    int rc = check_gemm_shape(qtype, M, N, K, IHIP_GEMM_F32 | IHIP_GEMM_PACKED);
+    if (rc != IHIP_OK) return rc;
+    if (M > 8) return fail(IHIP_EINVAL, "%s: M=%d (chained calls hold one token tile: M <= 8)", fn, M);
+    if (!aligned16(w_packed) || !aligned16(ws)) return fail(IHIP_EINVAL, "%s: weights/workspace 16-byte aligned", fn);
+    const size_t need = gemm_ws_bytes(qtype, M, N, K, IHIP_GEMM_F32 | IHIP_GEMM_PACKED);
+    if (ws_bytes < need) return fail(IHIP_ENOMEM, "%s: workspace %zu < %zu bytes", fn, ws_bytes, need);
+    Chain ch{};
+    ch.epi = IHIP_EPI_STORE;
+    ch.ldy = N;
+    float *y = nullptr;
+    if (cout) {
+        const int e = cout->epi;
+        if (e < IHIP_EPI_STORE || e > IHIP_EPI_GATE) return fail(IHIP_EINVAL, "%s: epi=%d", fn, e);
+        if (!cout->y) return fail(IHIP_EFAULT, "%s: NULL y", fn);
+        if (defer) return fail(IHIP_EINVAL, "%s: IHIP_GEMM_DEFER leaves partials: no output descriptor", fn);
+        const int width = e == IHIP_EPI_GATE ? N / 2 : N;
+        if (cout->ldy < width || (e == IHIP_EPI_GATE && N % 16))
+            return fail(IHIP_EINVAL, "%s: ldy=%d (need >= %d; IHIP_EPI_GATE needs N %% 16 == 0)", fn, cout->ldy, width);
+        if (e != IHIP_EPI_STORE) {
+            // the next matmul's K: whole 256-element units
+            const int kn = e == IHIP_EPI_STATS ? cout->stat_rows : width;
+            const int tiles = e == IHIP_EPI_GATE ? kn / 8 : kn / 16;
+            if (e == IHIP_EPI_STATS && (cout->stat_rows < 256 || cout->stat_rows > N))
+                return fail(IHIP_EINVAL, "%s: stat_rows=%d (within N)", fn, cout->stat_rows);
+            if (kn % 256) return fail(IHIP_EINVAL, "%s: the operand covers %d values (a multiple of 256)", fn, kn);
+            const int cq = cout->consumer_qtype;
+            if (cq != IHIP_Q4_K && cq != IHIP_Q5_K && cq != IHIP_Q6_K && cq != IHIP_Q8_0)
+                return fail(IHIP_EINVAL, "%s: consumer_qtype=%d", fn, cq);
+            if (cout->operand && !aligned16(cout->operand)) return fail(IHIP_EINVAL, "%s: operand 16-byte aligned", fn);
+            if (cout->tile_sum && (!aligned16(cout->tile_sum) || (cout->sum_stride & 3) || cout->sum_stride < tiles))
+                return fail(IHIP_EINVAL, "%s: tile_sum 16-byte aligned, sum_stride=%d >= %d tiles and a multiple of 4",
+                            fn, cout->sum_stride, tiles);
+            ch.op_lk = cq == IHIP_Q6_K ? 1 : cq == IHIP_Q8_0 ? 2 : 0;
+            ch.yop = (uint8_t *)cout->operand;
+            ch.y_units = kn / 256;
+            ch.ysum = cout->tile_sum;
+            ch.ysum_stride = cout->sum_stride;
+            ch.yssq = cout->tile_ssq;
+            ch.stat_rows = cout->stat_rows;
+        }
+        ch.epi = e;
+        ch.ldy = cout->ldy;
+        ch.yw = cout->norm_w;
+        y = cout->y;
+    } else if (!defer) {
+        return fail(IHIP_EINVAL, "%s: no output descriptor and no IHIP_GEMM_DEFER", fn);
+    }
+    const float *ssq_in = nullptr;
+    int n_ssq = 0;
+    float eps = 0.f;
+    hipError_t err;
+    if (cin) {
+        if (K % 256) return fail(IHIP_EINVAL, "%s: a chained input needs K %% 256 == 0", fn);
+        const int tpu = cin->tiles_per_unit;
+        if (!cin->operand) return fail(IHIP_EFAULT, "%s: NULL operand", fn);
+        if (!aligned16(cin->operand)) return fail(IHIP_EINVAL, "%s: operand 16-byte aligned", fn);
+        if (tpu != 16 && tpu != 32) return fail(IHIP_EINVAL, "%s: tiles_per_unit=%d (16 or 32)", fn, tpu);
+        const bool mins = qtype == IHIP_Q4_K || qtype == IHIP_Q5_K;
+        if (mins && (!cin->tile_sum || !aligned16(cin->tile_sum) || (cin->sum_stride & 3) ||
+                     cin->sum_stride < (K / 256) * tpu))
+            return fail(IHIP_EINVAL, "%s: Q4_K/Q5_K need tile_sum (16-byte aligned, sum_stride=%d >= %d, a multiple "
+                                     "of 4)", fn, cin->sum_stride, (K / 256) * tpu);
+        if (cin->tile_ssq && (cin->ssq_tiles < 1 || !(cin->eps >= 0.f)))
+            return fail(IHIP_EINVAL, "%s: ssq_tiles=%d eps=%g", fn, cin->ssq_tiles, cin->eps);
+        ch.xop = (const uint8_t *)cin->operand;
+        ch.xsum = cin->tile_sum;
+        ch.xsum_stride = cin->sum_stride;
+        ch.x_tiles_per_unit = tpu;
+        ssq_in = cin->tile_ssq;
+        n_ssq = cin->tile_ssq ? cin->ssq_tiles : 0;
+        eps = cin->eps;
+        err = launch_gemm_chain_ex(qtype, w_packed, nullptr, 0, 0, nullptr, 0.f, nullptr, 0, 0, ch, ssq_in, n_ssq,
+                                   eps, y, M, N, K, flags, ws, S(stream));
+    } else {
+        const int act = in->act;
+        if (!in->x) return fail(IHIP_EFAULT, "%s: NULL in->x", fn);
+        if (act < IHIP_ACT_PLAIN || act > IHIP_ACT_SILU_MUL) return fail(IHIP_EINVAL, "%s: act=%d", fn, act);
+        const int min_ld = act == IHIP_ACT_SILU_MUL ? 2 * K : K;
+        if (in->ldx < min_ld || (in->ldx & 3) || !aligned16(in->x))
+            return fail(IHIP_EINVAL, "%s: ldx=%d (need >= %d, multiple of 4; x 16-byte aligned)", fn, in->ldx, min_ld);
+        if (act == IHIP_ACT_RMSNORM && !(in->eps >= 0.f)) return fail(IHIP_EINVAL, "%s: eps=%g", fn, in->eps);
+        if (in->add && (in->n_add < 1 || in->add_stride < (int64_t)M * K || (in->add_stride & 3) || !aligned16(in->add)))
+            return fail(IHIP_EINVAL, "%s: add slices n=%d stride=%lld", fn, in->n_add, (long long)in->add_stride);
+        err = launch_gemm_chain_ex(qtype, w_packed, in->x, in->ldx, act, act == IHIP_ACT_RMSNORM ? in->norm_w : nullptr,
+                                   in->eps, in->add, in->add ? in->n_add : 0, in->add_stride, ch, nullptr, 0, 0.f, y, M,
+                                   N, K, flags, ws, S(stream));
+    }
+    if (err == hipErrorInvalidValue)
+        return fail(IHIP_EINVAL, "%s: shape not on the one-tile streaming plan (or a statistics epilogue on a "
+                                 "K-split matmul)", fn);
+    return err == hipSuccess ? ok() : hip_fail(err, fn);
+}
+
 int ihip_gemm_q_ex(int qtype, const void *w_dev, const ihip_gemm_input *in, float *y_dev, int M, int N, int K,
                    int flags, void *ws, size_t ws_bytes, void *stream) {
     if (!in) return fail(IHIP_EFAULT, "ihip_gemm_q_ex: NULL input descriptor");
@@ -578,7 +696,7 @@ int ihip_pack_weights(int qtype, const void *w_gguf_dev, void *w_packed_dev, int
     const int rc = check_gemm_shape(qtype, 1, N, K, 0);
     if (rc != IHIP_OK) return rc;
     if (!aligned16(w_packed_dev)) return fail(IHIP_EINVAL, "ihip_pack_weights: packed buffer must be 16-byte aligned");
-    hipError_t e = launch_pack(qtype, w_gguf_dev, w_packed_dev, N, K, S(stream));
+    hipError_t e = launch_pack(qtype, w_gguf_dev, w_packed_dev, N, K, S(stream), 0);
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_pack_weights");
 }
 

@@ -32,6 +32,7 @@
 // workgroup stores its partial tile and a reduce kernel sums the partials in
 // slice order (no floating-point atomics).
 #include "common.h"
+#include "chain.h"
 
 #include <algorithm>
 #include <cstdlib>
@@ -42,6 +43,7 @@ constexpr int WG_THREADS = 256;  // 4 waves
 constexpr int ROWS_PER_WG = 64;
 constexpr int UNIT = 256;        // K elements per loop unit
 constexpr int UNIT_A1 = 8192;    // A-operand bytes per unit and 16-slot token tile
+constexpr int CHAIN_MAX_TILES = 32;  // 16-row tiles per workgroup of a chained producer
 
 template <int QT> struct GemmCfg {
     static constexpr int BB = QTraits<QT>::BB;
@@ -247,15 +249,18 @@ __device__ __forceinline__ void load_unit_buf(__amdgpu_buffer_rsrc_t rs, int sof
 }
 
 // One thread per (unit, tile, lane): copies that lane's bytes of the chunk.
+// gated > 0: W is a [gate; up] matrix of 2 gated rows and tile t holds gate
+// rows 8t .. 8t + 7 followed by the same up rows (row gated + 8t + n - 8 for
+// n >= 8), the layout a chained EPI_GATE epilogue reads.
 template <int QT>
 __global__ __launch_bounds__(64) void pack_kernel(const uint8_t *__restrict__ W, int N, int K,
-                                                  uint8_t *__restrict__ P) {
+                                                  uint8_t *__restrict__ P, int gated) {
     constexpr int BB = QTraits<QT>::BB;
     const int n_units = (K + UNIT - 1) / UNIT;
     const int u = blockIdx.x, tile = blockIdx.y;
     const int l = threadIdx.x, n = l & 15, g = l >> 4;
-    const int row = tile * 16 + n;
-    const bool live = row < N;
+    const int row = gated > 0 ? (n < 8 ? 8 * tile + n : gated + 8 * tile + n - 8) : tile * 16 + n;
+    const bool live = gated > 0 ? 8 * tile + (n & 7) < gated : row < N;
     const size_t row_bytes = (size_t)(K / QTraits<QT>::QK) * BB;
     uint8_t *ch = P + ((size_t)tile * n_units + u) * Packed<QT>::CHUNK;
     const uint8_t *src = W + (size_t)(live ? row : 0) * row_bytes + (size_t)u * Packed<QT>::UB;
@@ -1076,15 +1081,256 @@ __device__ __forceinline__ void compute_v(const Unit<QT> &r, const AReg<QT> (&a)
     }
 }
 
+// ---------------------------------------------------------------- chained matmuls
+// A chain of fp32-accurate one-tile matmuls (M <= 8) that hand each other
+// their activations without an input stage:
+//  * the producer's epilogue writes its fp32 result y and, for the next
+//    matmul, the split-fp16 operand of v = y w (w: the next RMSNorm weight,
+//    or 1) in the input stage's byte layout, but scaled by a power of two of
+//    its own 16-row tile (8 gated channels for EPI_GATE): the tile's largest
+//    |v| lands in [2^14, 2^15), as the input stage does per 256-element unit.
+//    Beside the limbs it stores the tile's exponent once per lane entry, the
+//    tile's sum of v (the min terms of Q4_K/Q5_K) and, where an RMSNorm
+//    follows, its sum of y^2; EPI_RESID adds into the residual y itself,
+//    EPI_GATE reads tiles of 8 gate rows and their 8 up rows
+//    (ihip_pack_weights_gated) and writes h = silu(g) u;
+//  * the consumer loads the limbs as a classic matmul loads its prepared
+//    operand, takes the unit's exponent as the smallest over its tiles (the
+//    input stage's, from the largest |v|) and rescales each entry by the
+//    exact power of two 2^(e_unit - e_tile): the input stage's limbs wherever
+//    the result stays a normal fp16 (else the same value to within 2^-24 of
+//    the unit's scale).
+// Sum of 8 values in the input stage's order.
+__device__ __forceinline__ float sum8(const float (&v)[8]) {
+    return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+}
+
+// Where element o (0..255) of a unit sits in the fp32-accurate operand of
+// layout LK (0: Q4_K/Q5_K, 1: Q6_K, 2: Q8_0): chunk c, lane group G, item
+// (element within the lane entry), and the entry's exponent index ei (0..15).
+// The input stage's map (prep_finish) written per element.
+template <int LK>
+__device__ __forceinline__ void operand_pos(int o, int &c, int &G, int &item, int &ei) {
+    if constexpr (LK == 0) {
+        c = ((o >> 3) & 1) + 2 * ((o >> 5) & 1) + 4 * ((o >> 7) & 1);
+        G = ((o >> 4) & 1) + 2 * ((o >> 6) & 1);
+        item = o & 7;
+        ei = c;
+    } else if constexpr (LK == 1) {
+        c = o >> 4;
+        G = (o >> 2) & 3;
+        item = o & 3;
+        ei = c;
+    } else {
+        const int q = (o >> 3) & 3;
+        c = o >> 5;
+        G = 2 * (q & 1) + ((o >> 2) & 1);
+        item = (q < 2 ? 0 : 4) + (o & 3);
+        ei = 2 * c + (q >> 1);
+    }
+}
+
+// Exponent of a tile scale: largest |v| in [2^14, 2^15) after scaling (the
+// input stage's rule), 127 for an all-zero tile (no bound on the unit's
+// exponent), 0 when the tile holds Inf or NaN.
+__device__ __forceinline__ int tile_exp(float mx) {
+    if (mx == 0.f) return 127;
+    if (!(mx < __builtin_huge_valf())) return 0;
+    int ex;
+    frexpf(mx, &ex);
+    return min(max(15 - ex, -120), 120);
+}
+
+// What one lane stages per unit before the weight ring: its entries'
+// exponents and, for the min terms, the producer's tile sums of its
+// sub-blocks (the limbs go straight into the A registers).
+struct XStage {
+    uint4 ex;      // 16 exponent bytes (Q4_K/Q5_K use the first 8)
+    float4 ts[4];  // tile sums of sub-blocks 4 G' .. 4 G' + 3 (G' = G & 1): 8 or 16
+};
+
+template <int QT>
+__device__ __forceinline__ void stage_unit_x(const Chain &ch, int M, int un, int n_units, int lane, XStage &s) {
+    const int slot = lane & 15, G = lane >> 4;
+    const int t = min(slot >> 1, M - 1);
+    s.ex = *(const uint4 *)(ch.xop + (size_t)n_units * CHAIN_UNIT_LIMBS + (size_t)un * CHAIN_UNIT_EXPS + lane * 16);
+    if constexpr (GemmCfg<QT>::MINS) {
+        // sub-blocks 4 G' .. 4 G' + 3: tiles 8 G' .. (16-row) or 16 G' .. (8-row tiles)
+        const int tpu = ch.x_tiles_per_unit;
+        const float *ps = ch.xsum + (size_t)t * ch.xsum_stride + (size_t)un * tpu + (tpu / 2) * (G & 1);
+        s.ts[0] = *(const float4 *)ps;
+        s.ts[1] = *(const float4 *)(ps + 4);
+        s.ts[2] = *(const float4 *)(ps + (tpu == 32 ? 8 : 0));
+        s.ts[3] = *(const float4 *)(ps + (tpu == 32 ? 12 : 4));
+    }
+}
+
+// The staged unit's operand finished in place: entries rescaled to the
+// unit's power of two, the min-term operand, inv[k] (inverse unit scales of
+// the accumulator tokens 2G + k). tok: the lane's token is real and the unit
+// exists. Every lane must call it (the unit exponent crosses lanes).
+template <int QT>
+__device__ __forceinline__ void finish_unit_x(const XStage &s, const Chain &ch, bool tok, int lane, AReg<QT> &a,
+                                              float (&inv)[2]) {
+    constexpr int LK = QT == QT_Q6_K ? 1 : QT == QT_Q8_0 ? 2 : 0;
+    constexpr int NE = LK == 0 ? 8 : 16;  // exponent entries per lane
+    const int slot = lane & 15, G = lane >> 4;
+    const bool L = slot & 1;
+    int e[NE];
+    const uint32_t w[4] = {s.ex.x, s.ex.y, s.ex.z, s.ex.w};
+#pragma unroll
+    for (int i = 0; i < NE; i++) e[i] = (int)(int8_t)(w[i >> 2] >> (8 * (i & 3)));
+    // the unit's exponent: the smallest over the token's tiles (its 4 lane groups hold all of them)
+    int eu = 127;
+#pragma unroll
+    for (int i = 0; i < NE; i++) eu = min(eu, e[i]);
+    eu = min(eu, __shfl_xor(eu, 16));
+    eu = min(eu, __shfl_xor(eu, 32));
+    if (eu == 127 || !tok) eu = 0;
+    inv[0] = ldexpf(1.f, -__shfl(eu, 4 * G));
+    inv[1] = ldexpf(1.f, -__shfl(eu, 4 * G + 2));
+    // 2^(eu - e) as fp16: exact down to 2^-24, 0 below (and for all-zero tiles)
+    auto factor = [&](int ei) -> _Float16 {
+        const int d = max(e[ei] - eu, 0);  // (>= 0 for a real token; padding lanes hold zeros)
+        return (_Float16)(d <= 24 ? ldexpf(1.f, -d) : 0.f);
+    };
+    if constexpr (LK == 0) {
+#pragma unroll
+        for (int c = 0; c < 8; c++) a.f[c] = a.f[c] * factor(c);
+    } else if constexpr (LK == 1) {
+#pragma unroll
+        for (int c = 0; c < 16; c++) a.f[c] = a.f[c] * factor(c);
+    } else {
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const _Float16 f0 = factor(2 * c), f1 = factor(2 * c + 1);
+            const h8 f = {f0, f0, f0, f0, f1, f1, f1, f1};
+            a.f[c] = a.f[c] * f;
+        }
+    }
+    if constexpr (GemmCfg<QT>::MINS) {
+        // min-term operand: lane group G < 2 holds sub-blocks 4 G .. 4 G + 3, each the sum of its
+        // 2 (16-row) or 4 (8-row) tiles
+        const float scale = ldexpf(1.f, eu) * (1.0f / 32.0f);
+        const float t[16] = {s.ts[0].x, s.ts[0].y, s.ts[0].z, s.ts[0].w, s.ts[1].x, s.ts[1].y, s.ts[1].z, s.ts[1].w,
+                             s.ts[2].x, s.ts[2].y, s.ts[2].z, s.ts[2].w, s.ts[3].x, s.ts[3].y, s.ts[3].z, s.ts[3].w};
+        const bool eight = ch.x_tiles_per_unit == 32;
+        h4 mn;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float xsb = eight ? (t[4 * j] + t[4 * j + 1]) + (t[4 * j + 2] + t[4 * j + 3])
+                                    : t[2 * j] + t[2 * j + 1];
+            const float xsum = xsb * scale;
+            const _Float16 hi = (_Float16)xsum;
+            mn[j] = (G < 2 && tok) ? (L ? (_Float16)(xsum - (float)hi) : hi) : (_Float16)0.0f;
+        }
+        a.mins = mn;
+    }
+}
+
+// Maximum / sum over the 16 lanes of a DPP row (the lanes of one token pair).
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dppf<0xB1>(v));
+    v = fmaxf(v, dppf<0x4E>(v));
+    v = fmaxf(v, dppf<0x141>(v));
+    return fmaxf(v, dppf<0x140>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dppf<0xB1>(v);
+    v += dppf<0x4E>(v);
+    v += dppf<0x141>(v);
+    return v + dppf<0x140>(v);
+}
+
+// The consumer operand of one value (token t, consumer element k) at the
+// tile's exponent e2: hi and lo limbs at slots 2t, 2t + 1; the entry's
+// exponent written by the entry's first element.
+template <int LK>
+__device__ __forceinline__ void put_operand(const Chain &ch, int t, int k, float v, int e2) {
+    constexpr int ENTRY = LK == 1 ? 8 : 16;
+    const int u = k >> 8;
+    int c, G, item, ei;
+    operand_pos<LK>(k & 255, c, G, item, ei);
+    const float xs = v * ldexpf(1.f, e2 == 127 ? 0 : e2);
+    const _Float16 hi = (_Float16)xs, lo = (_Float16)(xs - (float)hi);
+    uint8_t *q = ch.yop + (size_t)u * CHAIN_UNIT_LIMBS + (size_t)(c * 64 + 16 * G + 2 * t) * ENTRY + item * 2;
+    *(_Float16 *)q = hi;
+    *(_Float16 *)(q + ENTRY) = lo;
+    if ((item & 3) == 0 && (LK == 2 || item == 0)) {
+        int8_t *x = (int8_t *)ch.yop + (size_t)ch.y_units * CHAIN_UNIT_LIMBS + (size_t)u * CHAIN_UNIT_EXPS +
+                    (16 * G + 2 * t) * 16 + ei;
+        x[0] = (int8_t)e2;
+        x[16] = (int8_t)e2;
+    }
+}
+
+// Epilogue of a chained producer (one 16-row tile; lanes n_in = row, g =
+// token pair 2g, 2g + 1): stores the tile, the consumer's operand and the
+// statistics. Whole waves call it (row reductions across the 16 lanes of
+// each token pair).
+__device__ __forceinline__ void chain_epilogue(const Chain &ch, float *__restrict__ Y, const float (&sum)[2],
+                                               const float *rs, int M, int N, int tile, int n_in, int g,
+                                               const float *pre_y, const float *pre_w) {
+    const int r = tile * 16 + n_in;
+    float sv[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int t = 2 * g + k;
+        const bool ok = r < N && t < M;
+        const float v = ok ? sum[k] * rs[t] : 0.f;
+        float y = v;
+        if (ch.epi == EPI_GATE) {
+            // rows 16 tile + n are gate channel 8 tile + n (n < 8) and its up row (n + 8)
+            const float u = __shfl_xor(v, 8);
+            y = (n_in < 8 && ok) ? silu_mul1(v, u) : 0.f;
+            if (n_in < 8 && ok) Y[(size_t)t * ch.ldy + tile * 8 + n_in] = y;
+        } else if (ch.epi == EPI_RESID) {
+            if (ok) {
+                float *dst = Y + (size_t)t * ch.ldy + r;
+                y = (pre_y != nullptr ? pre_y[k] : *dst) + v;
+                *dst = y;
+            }
+        } else if (ok) {
+            Y[(size_t)t * ch.ldy + r] = v;
+        }
+        sv[k] = y;
+    }
+    const bool stats = ch.epi != EPI_STATS || tile * 16 < ch.stat_rows;
+    if (!stats) return;
+    const int kcons = ch.epi == EPI_GATE ? tile * 8 + (n_in & 7) : r;  // the consumer's element
+    const bool real = r < N && (ch.epi != EPI_GATE || n_in < 8);
+    const float w = (ch.yw != nullptr && r < N) ? (pre_w != nullptr ? *pre_w : ch.yw[kcons]) : 1.0f;
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int t = 2 * g + k;
+        const float v = sv[k] * w;
+        if (ch.yop != nullptr) {
+            const int e2 = tile_exp(row16_max(fabsf(v)));
+            if (real && t < M) {
+                if (ch.op_lk == 0) put_operand<0>(ch, t, kcons, v, e2);
+                else if (ch.op_lk == 1) put_operand<1>(ch, t, kcons, v, e2);
+                else put_operand<2>(ch, t, kcons, v, e2);
+            }
+        }
+        const float ts = ch.ysum != nullptr ? row16_sum(v) : 0.f;
+        const float sq = ch.yssq != nullptr ? row16_sum(sv[k] * sv[k]) : 0.f;
+        if (n_in == 0 && t < M) {
+            if (ch.ysum != nullptr) ch.ysum[(size_t)t * ch.ysum_stride + tile] = ts;
+            if (ch.yssq != nullptr) ch.yssq[(size_t)tile * 8 + t] = sq;
+        }
+    }
+}
+
 // One token tile (MT = 1; several tiles run gemm_w_kernel).
-template <int QT, int NW, int UPS, bool SPLIT, bool PK, int MT>
+template <int QT, int NW, int UPS, bool SPLIT, bool PK, int MT, bool XIN, bool CE>
 __global__ __launch_bounds__(NW * 64, 8 / NW)
 void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, int N, int K, int accum,
                    const uint8_t *__restrict__ afrag, const float *__restrict__ invs,
-                   const uint8_t *__restrict__ mfrag, const float *__restrict__ ssq, float eps,
-                   float *__restrict__ part) {
+                   const uint8_t *__restrict__ mfrag, const float *__restrict__ ssq, int n_ssq, float eps,
+                   float *__restrict__ part, Chain ch) {
     using C = GemmCfg<QT>;
     static_assert(MT == 1, "one token tile");
+    static_assert((!XIN && !CE) || (SPLIT && MT == 1), "chained calls: fp32-accurate, one token tile");
     constexpr int TOKT = SPLIT ? 8 : 16;  // tokens per MFMA tile
     constexpr int TOK = MT * TOKT;
     constexpr int TPL = SPLIT ? 2 : 4;
@@ -1097,6 +1343,9 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     __shared__ __align__(16) float red[2][F][NW][64][TPL * MT];
     __shared__ float rs[TOK];  // RMSNorm row scales (1 without RMSNorm)
     __shared__ float rsp[NW * 64];
+    // a chained producer's reduced tiles wait here for the epilogue after the
+    // loop (at most CHAIN_MAX_TILES per workgroup, which the host checks)
+    __shared__ float2 pend[CE ? CHAIN_MAX_TILES : 1][64];
 
     const int n_units = (K + UNIT - 1) / UNIT;
     const int n_tiles = (N + 15) / 16;
@@ -1118,7 +1367,8 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     for (int u = 0; u < UPS; u++) {
         live[u] = unit0 + u < n_units;
         const int un = min(unit0 + u, n_units - 1);
-        const uint8_t *src = afrag + (size_t)un * UNIT_A1 * MT;
+        // (a chained input: the producer's limbs, rescaled once the ring is in flight)
+        const uint8_t *src = (XIN ? ch.xop : afrag) + (size_t)un * UNIT_A1 * MT;
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             // slots of padding tokens are zero: not fetched
@@ -1130,7 +1380,7 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
 #pragma unroll
                     for (int c = 0; c < 8; c++) a[u][mt].f[c] = *(const h8 *)(src + ((c * MT + mt) * 64 + lane) * 16);
                 }
-                if constexpr (C::MINS)
+                if constexpr (C::MINS && !XIN)
                     a[u][mt].mins = *(const h4 *)(mfrag + ((size_t)un * MT + mt) * 512 + lane * 8);
             } else {
                 if constexpr (QT == QT_Q6_K) {
@@ -1142,8 +1392,10 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
                 }
                 if constexpr (C::MINS) a[u][mt].mins = h4{};
             }
+            if constexpr (!XIN) {
 #pragma unroll
-            for (int k = 0; k < TPL; k++) inv[u][mt][k] = invs[(size_t)un * TOK + lane_token<SPLIT>(mt, g, k)];
+                for (int k = 0; k < TPL; k++) inv[u][mt][k] = invs[(size_t)un * TOK + lane_token<SPLIT>(mt, g, k)];
+            }
         }
     }
 
@@ -1169,16 +1421,50 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
                           b);
         }
     };
+    // chained producer: the old residual (EPI_RESID) and the next norm weight
+    // of this wave's first epilogue tile, loaded now and used at the end
+    float pre_y[2] = {0.f, 0.f}, pre_w = 1.f;
+    if constexpr (CE) {
+        if (wave < my_tiles && blockIdx.y == 0) {
+            const int tile = (int)blockIdx.x + G * wave;
+            const int r = min(tile * 16 + n_in, N - 1);
+            if (ch.epi == EPI_RESID) {
+                pre_y[0] = Y[(size_t)min(2 * g, M - 1) * ch.ldy + r];
+                pre_y[1] = Y[(size_t)min(2 * g + 1, M - 1) * ch.ldy + r];
+            }
+            if (ch.yw != nullptr) pre_w = ch.yw[ch.epi == EPI_GATE ? tile * 8 + (n_in & 7) : r];
+        }
+    }
+    // chained input: the exponents and tile sums of each unit, before the ring
+    XStage xs[XIN ? UPS : 1];
+    if constexpr (XIN) {
+#pragma unroll
+        for (int u = 0; u < UPS; u++) stage_unit_x<QT>(ch, M, min(unit0 + u, n_units - 1), n_units, lane, xs[u]);
+    }
     RowScales<TOK, NW * 64> rsc;
-    rsc.issue(ssq, n_units, tid);
+    rsc.issue(ssq, n_ssq, tid);
     __builtin_amdgcn_sched_barrier(0);
+    // the ring: slot p holds item p, then p + R, p + 2R, ... (consumed, then
+    // refilled in place: every slot stays live across the loop, so the
+    // register allocator never moves a slot, and a move of a register still
+    // being loaded would wait for every load in flight)
     Unit<QT> buf[R];
 #pragma unroll
     for (int p = 0; p < R - 1; p++) {
         load_item(p / UPS, p % UPS, buf[p]);
         __builtin_amdgcn_sched_barrier(0);  // ring slots fill in order
     }
-    rsc.finish(ssq, n_units, K, eps, tid, rsp, rs);
+    if constexpr (XIN) {
+        const bool tok = (n_in >> 1) < M;
+#pragma unroll
+        for (int u = 0; u < UPS; u++) {
+            float iv[2];
+            finish_unit_x<QT>(xs[u], ch, tok && live[u], lane, a[u][0], iv);
+            inv[u][0][0] = iv[0];
+            inv[u][0][1] = iv[1];
+        }
+    }
+    rsc.finish(ssq, n_ssq, K, eps, tid, rsp, rs);
 
     f4 acc[MT], macc[MT];
 #pragma unroll
@@ -1213,18 +1499,23 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
                 for (int w = 1; w < NW; w++)
 #pragma unroll
                     for (int k = 0; k < MT * TPL; k++) sum[k] += red[hb][wave][w][lane][k];
-                const int r = ((int)blockIdx.x + G * (j - jb + wave)) * 16 + n_in;
-                if (r < N) {
+                const int tile = (int)blockIdx.x + G * (j - jb + wave);
+                const int r = tile * 16 + n_in;
+                if constexpr (CE) {
+                    pend[j - jb + wave][lane] = make_float2(sum[0], sum[1]);
+                } else if (ch.epi == EPI_STORE) {
+                    if (r < N) {
 #pragma unroll
-                    for (int k = 0; k < MT * TPL; k++) {
-                        const int t = lane_token<SPLIT>(k / TPL, g, k % TPL);
-                        if (t >= M) continue;
-                        const float v = sum[k] * rs[t];
-                        if (part != nullptr) {
-                            part[((size_t)blockIdx.y * M + t) * N + r] = v;
-                        } else {
-                            float *dst = Y + (size_t)t * N + r;
-                            *dst = accum ? *dst + v : v;
+                        for (int k = 0; k < MT * TPL; k++) {
+                            const int t = lane_token<SPLIT>(k / TPL, g, k % TPL);
+                            if (t >= M) continue;
+                            const float v = sum[k] * rs[t];
+                            if (part != nullptr) {
+                                part[((size_t)blockIdx.y * M + t) * N + r] = v;
+                            } else {
+                                float *dst = Y + (size_t)t * ch.ldy + r;
+                                *dst = accum ? *dst + v : v;
+                            }
                         }
                     }
                 }
@@ -1246,6 +1537,18 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
 #pragma unroll
         for (int p = 0; p < R - 1; p++)
             if (n_full + p < n_items) consume(jb + p / UPS, p % UPS, buf[p]);
+    }
+    if constexpr (CE) {
+        // the chained producer's epilogues, outside the weight loop (its
+        // registers free): tile slot js by wave js % NW
+        __syncthreads();
+        for (int js = wave; js < my_tiles; js += NW) {
+            const float2 p2 = pend[js][lane];
+            const float sm[2] = {p2.x, p2.y};
+            const bool first = js == wave;
+            chain_epilogue(ch, Y, sm, rs, M, N, (int)blockIdx.x + G * js, n_in, g, first ? pre_y : nullptr,
+                           first ? &pre_w : nullptr);
+        }
     }
 }
 
@@ -1602,18 +1905,54 @@ hipError_t launch_prep(const float *X, const ActIn &in, int M, int K, const ActW
     return hipGetLastError();
 }
 
+// The store-only epilogue of an unchained call (rows of Y are N apart).
+inline Chain plain_chain(int N) {
+    Chain c{};
+    c.epi = EPI_STORE;
+    c.ldy = N;
+    return c;
+}
+
 template <int QT, int NW, int UPS, bool SPLIT, bool PK, int MT>
 hipError_t launch_v(const uint8_t *W, const float *X, const ActIn &in, float *Y, int M, int N, int K, int S, int G,
-                    int accum, const ActWs &a, float *part, hipStream_t st) {
+                    int accum, const ActWs &a, float *part, hipStream_t st, const Chain *chain = nullptr) {
     hipError_t e;
     if (!in.reuse && (e = launch_prep<QT, MT, SPLIT>(X, in, M, K, a, st)) != hipSuccess) return e;
-    gemm_v_kernel<QT, NW, UPS, SPLIT, PK, MT><<<dim3(G, S), NW * 64, 0, st>>>(
-        W, Y, M, N, K, accum, a.afrag, a.inv, a.mfrag, in.op == ACT_RMSNORM ? a.ssq : nullptr, in.eps,
-        (S > 1 || in.defer) ? part : nullptr);
+    const int n_units = (K + UNIT - 1) / UNIT;
+    // (the chained-producer epilogue is its own instantiation: classic calls keep their registers)
+    if constexpr (SPLIT && MT == 1 && PK && NW == 8) {  // (the chained calls' plan)
+        if (chain != nullptr && chain->epi != EPI_STORE) {
+            gemm_v_kernel<QT, NW, UPS, SPLIT, PK, MT, false, true><<<dim3(G, S), NW * 64, 0, st>>>(
+                W, Y, M, N, K, accum, a.afrag, a.inv, a.mfrag, in.op == ACT_RMSNORM ? a.ssq : nullptr, n_units,
+                in.eps, (S > 1 || in.defer) ? part : nullptr, *chain);
+            return hipGetLastError();  // (statistics epilogues: one K-slice, nothing to reduce)
+        }
+    }
+    gemm_v_kernel<QT, NW, UPS, SPLIT, PK, MT, false, false><<<dim3(G, S), NW * 64, 0, st>>>(
+        W, Y, M, N, K, accum, a.afrag, a.inv, a.mfrag, in.op == ACT_RMSNORM ? a.ssq : nullptr, n_units, in.eps,
+        (S > 1 || in.defer) ? part : nullptr, chain != nullptr ? *chain : plain_chain(N));
     e = hipGetLastError();
     if (e != hipSuccess || S == 1 || in.defer) return e;
     const int64_t MN = (int64_t)M * N;
     reduce_kernel<<<(unsigned)((MN + 1023) / 1024), 256, 0, st>>>(part, Y, S, MN, accum);
+    return hipGetLastError();
+}
+
+// A chained call whose input comes from a chained producer (XIN): no input
+// stage; RMSNorm row scales from the producer's tile sums of squares.
+template <int QT, int NW, int UPS>
+hipError_t launch_vx(const uint8_t *W, float *Y, int M, int N, int K, int S, int G, int defer, const float *ssq,
+                     int n_ssq, float eps, float *part, const Chain &ch, hipStream_t st) {
+    if (ch.epi != EPI_STORE)
+        gemm_v_kernel<QT, NW, UPS, true, true, 1, true, true><<<dim3(G, S), NW * 64, 0, st>>>(
+            W, Y, M, N, K, 0, nullptr, nullptr, nullptr, ssq, n_ssq, eps, (S > 1 || defer) ? part : nullptr, ch);
+    else
+        gemm_v_kernel<QT, NW, UPS, true, true, 1, true, false><<<dim3(G, S), NW * 64, 0, st>>>(
+            W, Y, M, N, K, 0, nullptr, nullptr, nullptr, ssq, n_ssq, eps, (S > 1 || defer) ? part : nullptr, ch);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || S == 1 || defer) return e;
+    const int64_t MN = (int64_t)M * N;
+    reduce_kernel<<<(unsigned)((MN + 1023) / 1024), 256, 0, st>>>(part, Y, S, MN, 0);
     return hipGetLastError();
 }
 
@@ -1833,15 +2172,17 @@ size_t packed_bytes(int qt, int N, int K) {
     return 0;
 }
 
-hipError_t launch_pack(int qt, const void *W, void *P, int N, int K, hipStream_t st) {
+// gated > 0: pack a [gate; up] matrix of N = 2 gated rows into tiles of 8
+// gate rows and their up rows (gated a multiple of 8).
+hipError_t launch_pack(int qt, const void *W, void *P, int N, int K, hipStream_t st, int gated) {
     const dim3 grid((K + UNIT - 1) / UNIT, (N + 15) / 16);
     const uint8_t *w = (const uint8_t *)W;
     uint8_t *p = (uint8_t *)P;
     switch (qt) {
-    case QT_Q4_K: pack_kernel<QT_Q4_K><<<grid, 64, 0, st>>>(w, N, K, p); break;
-    case QT_Q5_K: pack_kernel<QT_Q5_K><<<grid, 64, 0, st>>>(w, N, K, p); break;
-    case QT_Q6_K: pack_kernel<QT_Q6_K><<<grid, 64, 0, st>>>(w, N, K, p); break;
-    case QT_Q8_0: pack_kernel<QT_Q8_0><<<grid, 64, 0, st>>>(w, N, K, p); break;
+    case QT_Q4_K: pack_kernel<QT_Q4_K><<<grid, 64, 0, st>>>(w, N, K, p, gated); break;
+    case QT_Q5_K: pack_kernel<QT_Q5_K><<<grid, 64, 0, st>>>(w, N, K, p, gated); break;
+    case QT_Q6_K: pack_kernel<QT_Q6_K><<<grid, 64, 0, st>>>(w, N, K, p, gated); break;
+    case QT_Q8_0: pack_kernel<QT_Q8_0><<<grid, 64, 0, st>>>(w, N, K, p, gated); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -1879,6 +2220,57 @@ hipError_t launch_gemm(int qt, const void *W, const float *X, float *Y, int M, i
                        hipStream_t st) {
     const ActIn in{ACT_PLAIN, K, nullptr, 0.f, false, nullptr, 0, 0, false};
     return gemm_in(qt, W, X, in, Y, M, N, K, flags, ws, st);
+}
+
+// A chained fp32-accurate call on packed weights (one token tile, M <= 8):
+// input either from the input stage (in != nullptr: prepared into ws as
+// usual) or a chained producer's operand (in == nullptr: ch.xop, rescaled in
+// registers), the RMSNorm row scales then from the producer's tile
+// sums of squares (ssq_in, n_ssq_in parts; null = none); epilogue ch.epi
+// (EPI_STORE with flags bit 32 leaves K-slice partials in ws). Returns
+// hipErrorInvalidValue where the plan is not the one-tile streaming kernel or
+// a statistics epilogue meets a K-split.
+hipError_t launch_gemm_chain(int qt, const void *W, const ActIn *in, const float *X, const Chain &ch,
+                             const float *ssq_in, int n_ssq_in, float eps, float *Y, int M, int N, int K, int flags,
+                             void *ws, hipStream_t st) {
+    const bool defer = (flags & 32) != 0;
+    const int f = (flags & ~48) | 1 | 8;  // fp32-accurate, packed
+    const GemmPlan p = plan_gemm(qt, M, N, K, f);
+    if (!p.stream || p.MT != 1 || !p.split) return hipErrorInvalidValue;
+    if (ch.epi != EPI_STORE && (p.S != 1 || defer)) return hipErrorInvalidValue;
+    if (ch.epi != EPI_STORE && ((N + 15) / 16 + p.G - 1) / p.G > CHAIN_MAX_TILES) return hipErrorInvalidValue;
+    uint8_t *wsp = (uint8_t *)ws;
+    float *part = (float *)(wsp + p.off_part);
+    const uint8_t *w = (const uint8_t *)W;
+    if (p.NW != 8) return hipErrorInvalidValue;  // (chained calls: the default 8-wave plan only)
+    // (instantiated up to the units per wave stream_ups_cap allows)
+#define CV(q, u) if constexpr (u <= stream_ups_cap(q, true)) if (qt == q && p.UPS == u) \
+    return launch_v<q, 8, u, true, true, 1>(w, X, ai, Y, M, N, K, p.S, p.G, 0, a, part, st, &ch)
+#define XV(q, u) if constexpr (u <= stream_ups_cap(q, true)) if (qt == q && p.UPS == u) \
+    return launch_vx<q, 8, u>(w, Y, M, N, K, p.S, p.G, defer, ssq_in, n_ssq_in, eps, part, ch, st)
+    if (in != nullptr) {
+        const ActWs a{wsp, nullptr, (float *)(wsp + p.off_inv), wsp + p.off_mfrag, (float *)(wsp + p.off_ssq)};
+        ActIn ai = *in;
+        ai.defer = defer;
+        CV(QT_Q4_K, 1); CV(QT_Q4_K, 2); CV(QT_Q4_K, 4); CV(QT_Q5_K, 1); CV(QT_Q5_K, 2);
+        CV(QT_Q6_K, 1); CV(QT_Q6_K, 2); CV(QT_Q8_0, 1);
+        return hipErrorInvalidValue;
+    }
+    XV(QT_Q4_K, 1); XV(QT_Q4_K, 2); XV(QT_Q4_K, 4); XV(QT_Q5_K, 1); XV(QT_Q5_K, 2);
+    XV(QT_Q6_K, 1); XV(QT_Q6_K, 2); XV(QT_Q8_0, 1);
+#undef XV
+#undef CV
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemm_chain_ex(int qt, const void *W, const float *X, int ldx, int op, const float *norm_w,
+                                float eps_in, const float *add, int n_add, int64_t add_stride, const Chain &ch,
+                                const float *ssq_in, int n_ssq_in, float eps, float *Y, int M, int N, int K,
+                                int flags, void *ws, hipStream_t st) {
+    if (X == nullptr)
+        return launch_gemm_chain(qt, W, nullptr, nullptr, ch, ssq_in, n_ssq_in, eps, Y, M, N, K, flags, ws, st);
+    const ActIn in{op, ldx, norm_w, eps_in, false, add, n_add, add_stride, false};
+    return launch_gemm_chain(qt, W, &in, X, ch, nullptr, 0, 0.f, Y, M, N, K, flags, ws, st);
 }
 
 // flags bit 16: reuse prepared activations; bit 32: defer (partials stay in

@@ -39,7 +39,7 @@
 extern "C" int ihip_internal_fail(int code, const char *fmt, ...);  // (status reporting, capi.cpp)
 extern "C" int ihip_internal_ok();
 size_t packed_bytes(int qt, int N, int K);
-hipError_t launch_pack(int qt, const void *W, void *P, int N, int K, hipStream_t st);
+hipError_t launch_pack(int qt, const void *W, void *P, int N, int K, hipStream_t st, int gated);
 
 namespace {
 
@@ -573,7 +573,7 @@ int ihip_gguf_upload(void *handle, int64_t i, void *dev, size_t dev_bytes, int f
         e = hipMemcpyAsync(dst + o, f->pin[b], n, hipMemcpyHostToDevice, st);
         if (e == hipSuccess) e = hipEventRecord(f->done[b], st);
     }
-    if (e == hipSuccess && pack) e = launch_pack(qt, tmp, dev, (int)N, (int)K, st);
+    if (e == hipSuccess && pack) e = launch_pack(qt, tmp, dev, (int)N, (int)K, st, 0);
     const hipError_t es = hipStreamSynchronize(st);  // tmp is released below
     if (e == hipSuccess) e = es;
     if (tmp) (void)hipFree(tmp);

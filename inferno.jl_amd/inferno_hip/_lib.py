@@ -36,6 +36,9 @@ SIGNATURES = {
     "ihip_gemm_q": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "ihip_gemm_q_ex": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     "ihip_gemm_q_noalloc": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "ihip_gemm_q_chain": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "ihip_chain_operand_bytes": (_sz, [_i]),
+    "ihip_pack_weights_gated": (_i, [_i, _vp, _vp, _i, _i, _vp]),
     "ihip_gemm_q_partials": (_i, [_i, _i, _i, _i, _i, _vp, C.POINTER(_vp), C.POINTER(_i), C.POINTER(_i64)]),
     "ihip_mlp_ws_bytes": (_i, [_i, _i, _i, _i, _i, _i, C.POINTER(_sz)]),
     "ihip_mlp_forward": (_i, [_i, _vp, _i, _vp, _vp, _vp, _f, _i, _i, _i, _i, _vp, _sz, _vp]),
@@ -78,6 +81,18 @@ class GemmInput(C.Structure):
     """struct ihip_gemm_input"""
     _fields_ = [("x", _vp), ("ldx", _i), ("act", _i), ("norm_w", _vp), ("eps", _f), ("add", _vp),
                 ("n_add", _i), ("add_stride", _i64)]
+
+
+class ChainIn(C.Structure):
+    """struct ihip_chain_in"""
+    _fields_ = [("operand", _vp), ("tile_sum", _vp), ("sum_stride", _i), ("tiles_per_unit", _i),
+                ("tile_ssq", _vp), ("ssq_tiles", _i), ("eps", _f)]
+
+
+class ChainOut(C.Structure):
+    """struct ihip_chain_out"""
+    _fields_ = [("epi", _i), ("y", _vp), ("ldy", _i), ("norm_w", _vp), ("consumer_qtype", _i), ("operand", _vp),
+                ("tile_sum", _vp), ("sum_stride", _i), ("tile_ssq", _vp), ("stat_rows", _i)]
 
 
 class HipError(RuntimeError):

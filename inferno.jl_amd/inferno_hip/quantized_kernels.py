@@ -187,6 +187,105 @@ def gemm_q_ex(qtype: int, w_dev, x, n: int, k: int, act: int = ACT_PLAIN, norm_w
     return out
 
 
+EPI_STORE, EPI_STATS, EPI_RESID, EPI_GATE = 0, 1, 2, 3
+
+
+def chain_operand_bytes(k: int) -> int:
+    """ihip_chain_operand_bytes: bytes of a chained operand for k inputs."""
+    return int(_lib.load().ihip_chain_operand_bytes(k))
+
+
+def chain_buffers(k: int, tiles_per_unit: int = 16, ssq: bool = False, device="cuda"):
+    """Buffers a chained producer fills for a consumer with k inputs: the
+    operand (uint8), tile sums [8, stride] (stride = k / 256 * tiles_per_unit)
+    and, with ssq, tile sums of squares [tiles, 8]."""
+    import torch
+    tiles = k // 256 * tiles_per_unit
+    op = torch.zeros(chain_operand_bytes(k), dtype=torch.uint8, device=device)
+    tsum = torch.zeros((8, (tiles + 3) // 4 * 4), dtype=torch.float32, device=device)
+    tssq = torch.zeros((tiles, 8), dtype=torch.float32, device=device) if ssq else None
+    return op, tsum, tssq
+
+
+def chain_in(operand, tile_sum, tiles_per_unit: int = 16, tile_ssq=None, eps: float = 1e-6):
+    """ihip_chain_in: the consumer's operand as a chained producer wrote it
+    (operand, tile_sum from chain_buffers); tile_ssq applies the RMSNorm row
+    scale from the producer's sums of squares."""
+    import torch
+    check_tensor(operand, "operand", torch.uint8)
+    if tile_sum is not None:
+        check_tensor(tile_sum, "tile_sum", torch.float32, (8, None))
+    ci = _lib.ChainIn(_ptr(operand), None if tile_sum is None else _ptr(tile_sum),
+                      0 if tile_sum is None else tile_sum.stride(0), tiles_per_unit,
+                      None if tile_ssq is None else _ptr(tile_ssq), 0 if tile_ssq is None else tile_ssq.shape[0], eps)
+    ci._refs = (operand, tile_sum, tile_ssq)
+    return ci
+
+
+def chain_out(epi: int, y, consumer_qtype: int = Q4_K, operand=None, tile_sum=None, norm_w=None, tile_ssq=None,
+              stat_rows: int = 0):
+    """ihip_chain_out: where a chained producer leaves its output (y, unit
+    column stride; EPI_RESID adds into it), the consumer's operand of y *
+    norm_w in consumer_qtype's layout, its tile sums and sums of squares."""
+    import torch
+    check_tensor(y, "y", torch.float32, contiguous=False)
+    if y.dim() != 2 or y.stride(1) != 1:
+        raise ValueError("y must be [M, N] float32 with unit column stride")
+    if operand is not None:
+        check_tensor(operand, "operand", torch.uint8)
+    if tile_sum is not None:
+        check_tensor(tile_sum, "tile_sum", torch.float32, (8, None))
+    co = _lib.ChainOut(epi, _ptr(y), y.stride(0), None if norm_w is None else _ptr(norm_w), consumer_qtype,
+                       None if operand is None else _ptr(operand), None if tile_sum is None else _ptr(tile_sum),
+                       0 if tile_sum is None else tile_sum.stride(0), None if tile_ssq is None else _ptr(tile_ssq),
+                       stat_rows)
+    co._refs = (y, operand, tile_sum, norm_w, tile_ssq)
+    return co
+
+
+def gemm_q_chain(qtype: int, w_packed, n: int, k: int, m: int, x=None, act: int = ACT_PLAIN, norm_w=None,
+                 eps: float = 1e-6, add=None, cin=None, cout=None, flags: int = GEMM_F32 | GEMM_PACKED, ws=None,
+                 stream=None):
+    """ihip_gemm_q_chain: a fp32-accurate one-tile matmul (m <= 8) on packed
+    weights whose input is either x through the usual input stage (act,
+    norm_w, add as gemm_q_ex) or a chained producer's rows (cin, from
+    chain_in), and whose output goes through cout (chain_out), or stays as
+    K-slice partials in ws with GEMM_DEFER."""
+    import torch
+    if (x is None) == (cin is None):
+        raise ValueError("pass exactly one of x / cin")
+    _check_weights(qtype, w_packed, n, k, GEMM_PACKED)
+    gi = None
+    if x is not None:
+        check_tensor(x, "x", torch.float32, contiguous=False)
+        if x.dim() != 2 or x.stride(1) != 1 or x.shape[0] < m:
+            raise ValueError("x must be [M, K] float32 with unit column stride")
+        gi = _lib.GemmInput(_ptr(x), x.stride(0), act, None if norm_w is None else _ptr(norm_w), eps,
+                            None if add is None else add[0], 0 if add is None else add[1],
+                            0 if add is None else add[2])
+    need = gemm_ws_bytes(qtype, m, n, k, GEMM_F32 | GEMM_PACKED)
+    if ws is None:
+        ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    check_tensor(ws, "ws", torch.uint8, min_numel=need)
+    _lib.check(_lib.load().ihip_gemm_q_chain(qtype, _ptr(w_packed), None if gi is None else C.byref(gi),
+                                             None if cin is None else C.byref(cin),
+                                             None if cout is None else C.byref(cout), m, n, k, flags, _ptr(ws),
+                                             ws.numel(), _stream(stream)))
+    return ws
+
+
+def pack_weights_gated(qtype: int, w_gate_up_dev, f: int, k: int, out=None, stream=None):
+    """Pack a device [gate; up] GGUF matrix [2f x k] into tiles of 8 gate rows
+    and their 8 up rows (the layout of an EPI_GATE chained producer)."""
+    import torch
+    check_tensor(w_gate_up_dev, "w_gate_up_dev", torch.uint8,
+                 min_numel=2 * f * (k // BLOCK_ELEMS[qtype]) * BLOCK_BYTES[qtype])
+    if out is None:
+        out = torch.empty(packed_bytes(qtype, 2 * f, k), dtype=torch.uint8, device=w_gate_up_dev.device)
+    _lib.check(_lib.load().ihip_pack_weights_gated(qtype, _ptr(w_gate_up_dev), _ptr(out), f, k, _stream(stream)))
+    return out
+
+
 def mlp_ws_bytes(qt_gate_up: int, qt_down: int, m: int, h: int, f: int, flags: int = GEMM_AUTO) -> int:
     """Workspace bytes of mlp_forward_."""
     nb = C.c_size_t()

@@ -153,6 +153,87 @@ def _run_step_with_checks(ih, B, model, step, chk, fold_chk, prec_flags):
     torch.cuda.synchronize()
 
 
+def _run_chain_step_with_checks(ih, B, model, step, chk, fold_chk):
+    """The chained composition (bench.ChainStep) checked operation by
+    operation: [q; k; v] and the tile sums of o's operand, o's product added
+    into the residual (x_new against x_old + the oracle's o within fp32 rounding of
+    the residual), h = silu(gate) up from [gate; up] on the RMSNorm'd
+    residual, down's K-slice partials, the folds, the head."""
+    import torch
+    P, M = model.proj, step.M
+    H, NQ, NKV, FF, V = B.H, B.NQ, B.NKV, B.FF, B.VOCAB
+    hw = model.host_gguf
+    st = {}
+    fl = ih.GEMM_F32 | ih.GEMM_PACKED
+
+    def down_check(i):
+        d = _partials_sum(ih, F.Q6_K, M, H, FF, fl, step.ws_down)
+        chk("down", d, O.gemv_f64(F.Q6_K, hw[i - 1]["down"], st["h"], M, H, FF))
+        return d
+
+    def probe(tag, i):
+        torch.cuda.synchronize()
+        x = _h(step.x).astype(np.float64)
+        if tag == "pre":
+            st["x_pre"] = x
+            if i > 0:
+                st["down"] = down_check(i)
+        elif tag == "qkv":
+            if i > 0:
+                fold_chk("x += down", x, st["x_pre"] + st["down"])
+            wq = np.concatenate([hw[i]["q"], hw[i]["kv"]])
+            qkv = _h(step.qkv)
+            chk("qkv", qkv, O.gemv_f64(P, wq, _rms(x, hw[i]["attn_norm"]), M, NQ + 2 * NKV, H))
+            a = qkv[:, :NQ].astype(np.float64).reshape(M, NQ // 16, 16)
+            bound = 16 * 2.0 ** -23 * np.abs(a).sum(axis=2) + 1e-30  # fp32 sums in any order
+            assert np.all(np.abs(_h(step.ts_q)[:M, :NQ // 16] - a.sum(axis=2)) <= bound)
+            st["x_qkv"], st["qkv"] = x, qkv
+        elif tag == "o":
+            fold_chk("x += o", x, st["x_qkv"] + O.gemv_f64(P, hw[i]["o"], st["qkv"][:, :NQ], M, H, NQ))
+            st["x_o"] = x
+        elif tag == "gu":
+            g = O.gemv_f64(P, hw[i]["gu"], _rms(st["x_o"], hw[i]["ffn_norm"]), M, 2 * FF, H)
+            with np.errstate(over="ignore"):
+                h_ref = g[:, :FF] / (1.0 + np.exp(-g[:, :FF])) * g[:, FF:]
+            st["h"] = _h(step.h)
+            chk("h = silu(gate) up", st["h"], h_ref)
+            st["x_gu"] = x
+        elif tag == "head":
+            d = down_check(i)
+            fold_chk("x += down", x, st["x_gu"] + d)
+            chk("lm_head", _h(step.logits), O.gemv_f64(F.Q6_K, model.host_lm, _rms(x, model.host_out_norm), M, V, H))
+            print(f"{chk.label}: every layer and the head checked", flush=True)
+
+    step.forward(probe=probe)
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("M", [1, 5, 8])
+def test_config4_chained_step(ih, bench, M):
+    """configs[3] through the chained composition the benchmark times
+    (bench.ChainStep: one input stage per layer), two real layers and the
+    151936 x 4096 head, every operation checked, then the accept on the
+    step's logits against the oracle's."""
+    import torch
+    B = bench
+    model = B.Model(ih, 2, keep_gguf=2, gated=True)
+    k = max(M - 1, 1)
+    step = B.ChainStep(ih, model, M, k, 0.8)
+    chk = Checker(TOL_F32, f"config 4 chained (M = {M})")
+    fold = Checker(TOL_FOLD, f"config 4 chained (M = {M}) residual folds")
+    _run_chain_step_with_checks(ih, B, model, step, chk, fold)
+    chk.report()
+    fold.report()
+    if M == 1:
+        return
+    step.accept()
+    torch.cuda.synchronize()
+    rt, rn = O.spec_accept(_h(step.logits), _h(step.drf), _h(step.draft)[0], 0.8, _h(step.u_acc)[0],
+                           float(_h(step.u_res)[0]), float(_h(step.u_bonus)[0]), 0)
+    n = int(step.out_n[0])
+    assert n == rn and _h(step.out_tok)[0, : n + 1].tolist() == rt.tolist(), (n, rn)
+
+
 # ----------------------------------------------------------------- config 2
 
 def test_config2_verify_batch(ih):
