@@ -1105,31 +1105,6 @@ __device__ __forceinline__ float sum8(const float (&v)[8]) {
     return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
 }
 
-// Where element o (0..255) of a unit sits in the fp32-accurate operand of
-// layout LK (0: Q4_K/Q5_K, 1: Q6_K, 2: Q8_0): chunk c, lane group G, item
-// (element within the lane entry), and the entry's exponent index ei (0..15).
-// The input stage's map (prep_finish) written per element.
-template <int LK>
-__device__ __forceinline__ void operand_pos(int o, int &c, int &G, int &item, int &ei) {
-    if constexpr (LK == 0) {
-        c = ((o >> 3) & 1) + 2 * ((o >> 5) & 1) + 4 * ((o >> 7) & 1);
-        G = ((o >> 4) & 1) + 2 * ((o >> 6) & 1);
-        item = o & 7;
-        ei = c;
-    } else if constexpr (LK == 1) {
-        c = o >> 4;
-        G = (o >> 2) & 3;
-        item = o & 3;
-        ei = c;
-    } else {
-        const int q = (o >> 3) & 3;
-        c = o >> 5;
-        G = 2 * (q & 1) + ((o >> 2) & 1);
-        item = (q < 2 ? 0 : 4) + (o & 3);
-        ei = 2 * c + (q >> 1);
-    }
-}
-
 // Exponent of a tile scale: largest |v| in [2^14, 2^15) after scaling (the
 // input stage's rule), 127 for an all-zero tile (no bound on the unit's
 // exponent), 0 when the tile holds Inf or NaN.
@@ -1153,15 +1128,25 @@ template <int QT>
 __device__ __forceinline__ void stage_unit_x(const Chain &ch, int M, int un, int n_units, int lane, XStage &s) {
     const int slot = lane & 15, G = lane >> 4;
     const int t = min(slot >> 1, M - 1);
-    s.ex = *(const uint4 *)(ch.xop + (size_t)n_units * CHAIN_UNIT_LIMBS + (size_t)un * CHAIN_UNIT_EXPS + lane * 16);
+    const uint8_t *pe = ch.xop + (size_t)n_units * CHAIN_UNIT_LIMBS + (size_t)un * CHAIN_UNIT_EXPS + lane * 16;
+    if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {  // (8 entries)
+        const uint2 e8 = *(const uint2 *)pe;
+        s.ex = make_uint4(e8.x, e8.y, 0u, 0u);
+    } else {
+        s.ex = *(const uint4 *)pe;
+    }
     if constexpr (GemmCfg<QT>::MINS) {
-        // sub-blocks 4 G' .. 4 G' + 3: tiles 8 G' .. (16-row) or 16 G' .. (8-row tiles)
+        // sub-blocks 4 G .. 4 G + 3 (lane groups G < 2 only): tiles 8 G .. (16-row) or 16 G .. (8-row)
         const int tpu = ch.x_tiles_per_unit;
-        const float *ps = ch.xsum + (size_t)t * ch.xsum_stride + (size_t)un * tpu + (tpu / 2) * (G & 1);
-        s.ts[0] = *(const float4 *)ps;
-        s.ts[1] = *(const float4 *)(ps + 4);
-        s.ts[2] = *(const float4 *)(ps + (tpu == 32 ? 8 : 0));
-        s.ts[3] = *(const float4 *)(ps + (tpu == 32 ? 12 : 4));
+        if (G < 2) {
+            const float *ps = ch.xsum + (size_t)t * ch.xsum_stride + (size_t)un * tpu + (tpu / 2) * G;
+            s.ts[0] = *(const float4 *)ps;
+            s.ts[1] = *(const float4 *)(ps + 4);
+            if (tpu == 32) {
+                s.ts[2] = *(const float4 *)(ps + 8);
+                s.ts[3] = *(const float4 *)(ps + 12);
+            }
+        }
     }
 }
 
@@ -1243,20 +1228,24 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 
 // The consumer operand of one value (token t, consumer element k) at the
-// tile's exponent e2: hi and lo limbs at slots 2t, 2t + 1; the entry's
-// exponent written by the entry's first element.
-template <int LK>
+// tile's exponent e2, for the consumer layout ch.op_lk (operand_pos's maps,
+// selected arithmetically: one copy of the code for the three layouts): hi
+// and lo limbs at slots 2t, 2t + 1; the entry's exponent written by the
+// entry's first element.
 __device__ __forceinline__ void put_operand(const Chain &ch, int t, int k, float v, int e2) {
-    constexpr int ENTRY = LK == 1 ? 8 : 16;
-    const int u = k >> 8;
-    int c, G, item, ei;
-    operand_pos<LK>(k & 255, c, G, item, ei);
+    const int lk = ch.op_lk, o = k & 255, u = k >> 8;
+    const int q = (o >> 3) & 3;
+    const int c = lk == 0 ? ((o >> 3) & 1) + 2 * ((o >> 5) & 1) + 4 * ((o >> 7) & 1) : lk == 1 ? o >> 4 : o >> 5;
+    const int G = lk == 0 ? ((o >> 4) & 1) + 2 * ((o >> 6) & 1) : lk == 1 ? (o >> 2) & 3 : 2 * (q & 1) + ((o >> 2) & 1);
+    const int item = lk == 0 ? o & 7 : lk == 1 ? o & 3 : (q < 2 ? 0 : 4) + (o & 3);
+    const int ei = lk == 2 ? 2 * c + (q >> 1) : c;
+    const int entry = lk == 1 ? 8 : 16;
     const float xs = v * ldexpf(1.f, e2 == 127 ? 0 : e2);
     const _Float16 hi = (_Float16)xs, lo = (_Float16)(xs - (float)hi);
-    uint8_t *q = ch.yop + (size_t)u * CHAIN_UNIT_LIMBS + (size_t)(c * 64 + 16 * G + 2 * t) * ENTRY + item * 2;
-    *(_Float16 *)q = hi;
-    *(_Float16 *)(q + ENTRY) = lo;
-    if ((item & 3) == 0 && (LK == 2 || item == 0)) {
+    uint8_t *p = ch.yop + (size_t)u * CHAIN_UNIT_LIMBS + (size_t)(c * 64 + 16 * G + 2 * t) * entry + item * 2;
+    *(_Float16 *)p = hi;
+    *(_Float16 *)(p + entry) = lo;
+    if ((item & 3) == 0 && (lk == 2 || item == 0)) {
         int8_t *x = (int8_t *)ch.yop + (size_t)ch.y_units * CHAIN_UNIT_LIMBS + (size_t)u * CHAIN_UNIT_EXPS +
                     (16 * G + 2 * t) * 16 + ei;
         x[0] = (int8_t)e2;
@@ -1267,53 +1256,40 @@ __device__ __forceinline__ void put_operand(const Chain &ch, int t, int k, float
 // Epilogue of a chained producer (one 16-row tile; lanes n_in = row, g =
 // token pair 2g, 2g + 1): stores the tile, the consumer's operand and the
 // statistics. Whole waves call it (row reductions across the 16 lanes of
-// each token pair).
-__device__ __forceinline__ void chain_epilogue(const Chain &ch, float *__restrict__ Y, const float (&sum)[2],
-                                               const float *rs, int M, int N, int tile, int n_in, int g,
-                                               const float *pre_y, const float *pre_w) {
+// each token pair). yold: the residual's old values (EPI_RESID), w: the
+// next norm weight of this lane's row. Written to stay small (one pass per
+// token, one operand writer): it runs once per tile at a kernel's end, where
+// every instruction is fetched cold.
+__device__ __forceinline__ void chain_epilogue(const Chain &ch, float *__restrict__ Y, float s0, float s1,
+                                               const float *rs, int M, int N, int tile, int n_in, int g, float yold0,
+                                               float yold1, float w) {
     const int r = tile * 16 + n_in;
-    float sv[2];
-#pragma unroll
+    const bool stats = ch.epi != EPI_STATS || tile * 16 < ch.stat_rows;
+    const int kcons = ch.epi == EPI_GATE ? tile * 8 + (n_in & 7) : r;  // the consumer's element
+    const bool real = r < N && (ch.epi != EPI_GATE || n_in < 8);
+#pragma unroll 1
     for (int k = 0; k < 2; k++) {
         const int t = 2 * g + k;
         const bool ok = r < N && t < M;
-        const float v = ok ? sum[k] * rs[t] : 0.f;
-        float y = v;
+        const float v0 = ok ? (k ? s1 : s0) * rs[t] : 0.f;
+        float y = v0;
         if (ch.epi == EPI_GATE) {
             // rows 16 tile + n are gate channel 8 tile + n (n < 8) and its up row (n + 8)
-            const float u = __shfl_xor(v, 8);
-            y = (n_in < 8 && ok) ? silu_mul1(v, u) : 0.f;
-            if (n_in < 8 && ok) Y[(size_t)t * ch.ldy + tile * 8 + n_in] = y;
-        } else if (ch.epi == EPI_RESID) {
-            if (ok) {
-                float *dst = Y + (size_t)t * ch.ldy + r;
-                y = (pre_y != nullptr ? pre_y[k] : *dst) + v;
-                *dst = y;
-            }
+            const float u = __shfl_xor(v0, 8);
+            y = (n_in < 8 && ok) ? silu_mul1(v0, u) : 0.f;
+            if (n_in < 8 && ok) Y[(size_t)t * ch.ldy + kcons] = y;
         } else if (ok) {
-            Y[(size_t)t * ch.ldy + r] = v;
+            if (ch.epi == EPI_RESID) y += k ? yold1 : yold0;
+            Y[(size_t)t * ch.ldy + r] = y;
         }
-        sv[k] = y;
-    }
-    const bool stats = ch.epi != EPI_STATS || tile * 16 < ch.stat_rows;
-    if (!stats) return;
-    const int kcons = ch.epi == EPI_GATE ? tile * 8 + (n_in & 7) : r;  // the consumer's element
-    const bool real = r < N && (ch.epi != EPI_GATE || n_in < 8);
-    const float w = (ch.yw != nullptr && r < N) ? (pre_w != nullptr ? *pre_w : ch.yw[kcons]) : 1.0f;
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-        const int t = 2 * g + k;
-        const float v = sv[k] * w;
+        if (!stats) continue;
+        const float v = y * w;
         if (ch.yop != nullptr) {
             const int e2 = tile_exp(row16_max(fabsf(v)));
-            if (real && t < M) {
-                if (ch.op_lk == 0) put_operand<0>(ch, t, kcons, v, e2);
-                else if (ch.op_lk == 1) put_operand<1>(ch, t, kcons, v, e2);
-                else put_operand<2>(ch, t, kcons, v, e2);
-            }
+            if (real && t < M) put_operand(ch, t, kcons, v, e2);
         }
         const float ts = ch.ysum != nullptr ? row16_sum(v) : 0.f;
-        const float sq = ch.yssq != nullptr ? row16_sum(sv[k] * sv[k]) : 0.f;
+        const float sq = ch.yssq != nullptr ? row16_sum(y * y) : 0.f;
         if (n_in == 0 && t < M) {
             if (ch.ysum != nullptr) ch.ysum[(size_t)t * ch.ysum_stride + tile] = ts;
             if (ch.yssq != nullptr) ch.yssq[(size_t)tile * 8 + t] = sq;
@@ -1322,7 +1298,7 @@ __device__ __forceinline__ void chain_epilogue(const Chain &ch, float *__restric
 }
 
 // One token tile (MT = 1; several tiles run gemm_w_kernel).
-template <int QT, int NW, int UPS, bool SPLIT, bool PK, int MT, bool XIN, bool CE>
+template <int QT, int NW, int UPS, bool SPLIT, bool PK, int MT, bool XIN, int DE>
 __global__ __launch_bounds__(NW * 64, 8 / NW)
 void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, int N, int K, int accum,
                    const uint8_t *__restrict__ afrag, const float *__restrict__ invs,
@@ -1330,7 +1306,15 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
                    float *__restrict__ part, Chain ch) {
     using C = GemmCfg<QT>;
     static_assert(MT == 1, "one token tile");
-    static_assert((!XIN && !CE) || (SPLIT && MT == 1), "chained calls: fp32-accurate, one token tile");
+    // DE: where the tiles' epilogue runs: 0 in the weight loop as each batch
+    // of tiles completes (plain stores); 2 (a chained producer's) after the
+    // loop, from the reduced tiles kept in LDS, with the loop's registers free
+    // (at most CHAIN_MAX_TILES per workgroup, which the host checks).
+    // Measured: plain stores after the loop are slower (the step 1.5 %): the
+    // stores then all wait at the kernel's end.
+    static_assert(DE == 0 || DE == 2, "epilogue placement");
+    static_assert((!XIN && DE == 0) || (SPLIT && MT == 1), "chained calls: fp32-accurate, one token tile");
+    constexpr bool CE = DE == 2;
     constexpr int TOKT = SPLIT ? 8 : 16;  // tokens per MFMA tile
     constexpr int TOK = MT * TOKT;
     constexpr int TPL = SPLIT ? 2 : 4;
@@ -1343,9 +1327,7 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     __shared__ __align__(16) float red[2][F][NW][64][TPL * MT];
     __shared__ float rs[TOK];  // RMSNorm row scales (1 without RMSNorm)
     __shared__ float rsp[NW * 64];
-    // a chained producer's reduced tiles wait here for the epilogue after the
-    // loop (at most CHAIN_MAX_TILES per workgroup, which the host checks)
-    __shared__ float2 pend[CE ? CHAIN_MAX_TILES : 1][64];
+    __shared__ float2 pend[DE ? CHAIN_MAX_TILES : 1][64];  // reduced tiles awaiting the epilogue
 
     const int n_units = (K + UNIT - 1) / UNIT;
     const int n_tiles = (N + 15) / 16;
@@ -1423,17 +1405,17 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     };
     // chained producer: the old residual (EPI_RESID) and the next norm weight
     // of this wave's first epilogue tile, loaded now and used at the end
-    float pre_y[2] = {0.f, 0.f}, pre_w = 1.f;
-    if constexpr (CE) {
-        if (wave < my_tiles && blockIdx.y == 0) {
-            const int tile = (int)blockIdx.x + G * wave;
-            const int r = min(tile * 16 + n_in, N - 1);
-            if (ch.epi == EPI_RESID) {
-                pre_y[0] = Y[(size_t)min(2 * g, M - 1) * ch.ldy + r];
-                pre_y[1] = Y[(size_t)min(2 * g + 1, M - 1) * ch.ldy + r];
-            }
-            if (ch.yw != nullptr) pre_w = ch.yw[ch.epi == EPI_GATE ? tile * 8 + (n_in & 7) : r];
+    float pre_y0 = 0.f, pre_y1 = 0.f, pre_w = 1.f;
+    auto load_pre = [&](int tile) {
+        const int r = min(tile * 16 + n_in, N - 1);
+        if (ch.epi == EPI_RESID) {
+            pre_y0 = Y[(size_t)min(2 * g, M - 1) * ch.ldy + r];
+            pre_y1 = Y[(size_t)min(2 * g + 1, M - 1) * ch.ldy + r];
         }
+        pre_w = ch.yw != nullptr ? ch.yw[ch.epi == EPI_GATE ? tile * 8 + (n_in & 7) : r] : 1.f;
+    };
+    if constexpr (CE) {
+        if (wave < my_tiles) load_pre((int)blockIdx.x + G * wave);
     }
     // chained input: the exponents and tile sums of each unit, before the ring
     XStage xs[XIN ? UPS : 1];
@@ -1466,6 +1448,24 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     }
     rsc.finish(ssq, n_ssq, K, eps, tid, rsp, rs);
 
+    // a finished tile's plain epilogue: row scale, then the output, the
+    // accumulation into it, or this K-slice's partials
+    auto store_tile = [&](const float (&sum)[MT * TPL], int tile) {
+        const int r = tile * 16 + n_in;
+        if (r >= N) return;
+#pragma unroll
+        for (int k = 0; k < MT * TPL; k++) {
+            const int t = lane_token<SPLIT>(k / TPL, g, k % TPL);
+            if (t >= M) continue;
+            const float v = sum[k] * rs[t];
+            if (part != nullptr) {
+                part[((size_t)blockIdx.y * M + t) * N + r] = v;
+            } else {
+                float *dst = Y + (size_t)t * ch.ldy + r;
+                *dst = accum ? *dst + v : v;
+            }
+        }
+    };
     f4 acc[MT], macc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) acc[mt] = macc[mt] = f4{0.f, 0.f, 0.f, 0.f};
@@ -1499,25 +1499,10 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
                 for (int w = 1; w < NW; w++)
 #pragma unroll
                     for (int k = 0; k < MT * TPL; k++) sum[k] += red[hb][wave][w][lane][k];
-                const int tile = (int)blockIdx.x + G * (j - jb + wave);
-                const int r = tile * 16 + n_in;
-                if constexpr (CE) {
+                if constexpr (DE != 0) {
                     pend[j - jb + wave][lane] = make_float2(sum[0], sum[1]);
-                } else if (ch.epi == EPI_STORE) {
-                    if (r < N) {
-#pragma unroll
-                        for (int k = 0; k < MT * TPL; k++) {
-                            const int t = lane_token<SPLIT>(k / TPL, g, k % TPL);
-                            if (t >= M) continue;
-                            const float v = sum[k] * rs[t];
-                            if (part != nullptr) {
-                                part[((size_t)blockIdx.y * M + t) * N + r] = v;
-                            } else {
-                                float *dst = Y + (size_t)t * ch.ldy + r;
-                                *dst = accum ? *dst + v : v;
-                            }
-                        }
-                    }
+                } else {
+                    store_tile(sum, (int)blockIdx.x + G * (j - jb + wave));
                 }
             }
         }
@@ -1538,16 +1523,20 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
         for (int p = 0; p < R - 1; p++)
             if (n_full + p < n_items) consume(jb + p / UPS, p % UPS, buf[p]);
     }
-    if constexpr (CE) {
-        // the chained producer's epilogues, outside the weight loop (its
-        // registers free): tile slot js by wave js % NW
+    if constexpr (DE != 0) {
+        // the epilogues, outside the weight loop: tile slot js by wave js % NW
         __syncthreads();
         for (int js = wave; js < my_tiles; js += NW) {
             const float2 p2 = pend[js][lane];
-            const float sm[2] = {p2.x, p2.y};
-            const bool first = js == wave;
-            chain_epilogue(ch, Y, sm, rs, M, N, (int)blockIdx.x + G * js, n_in, g, first ? pre_y : nullptr,
-                           first ? &pre_w : nullptr);
+            const int tile = (int)blockIdx.x + G * js;
+            if constexpr (CE) {
+                // (the first tile's residual and weight were loaded at the start)
+                if (js != wave) load_pre(tile);
+                chain_epilogue(ch, Y, p2.x, p2.y, rs, M, N, tile, n_in, g, pre_y0, pre_y1, pre_w);
+            } else {
+                const float sm[2] = {p2.x, p2.y};
+                store_tile(sm, tile);
+            }
         }
     }
 }
@@ -1919,18 +1908,19 @@ hipError_t launch_v(const uint8_t *W, const float *X, const ActIn &in, float *Y,
     hipError_t e;
     if (!in.reuse && (e = launch_prep<QT, MT, SPLIT>(X, in, M, K, a, st)) != hipSuccess) return e;
     const int n_units = (K + UNIT - 1) / UNIT;
-    // (the chained-producer epilogue is its own instantiation: classic calls keep their registers)
+    // (a chained producer's epilogue is its own instantiation: classic calls keep their registers)
+    const Chain c = chain != nullptr ? *chain : plain_chain(N);
     if constexpr (SPLIT && MT == 1 && PK && NW == 8) {  // (the chained calls' plan)
-        if (chain != nullptr && chain->epi != EPI_STORE) {
-            gemm_v_kernel<QT, NW, UPS, SPLIT, PK, MT, false, true><<<dim3(G, S), NW * 64, 0, st>>>(
+        if (c.epi != EPI_STORE) {
+            gemm_v_kernel<QT, NW, UPS, SPLIT, PK, MT, false, 2><<<dim3(G, S), NW * 64, 0, st>>>(
                 W, Y, M, N, K, accum, a.afrag, a.inv, a.mfrag, in.op == ACT_RMSNORM ? a.ssq : nullptr, n_units,
-                in.eps, (S > 1 || in.defer) ? part : nullptr, *chain);
+                in.eps, (S > 1 || in.defer) ? part : nullptr, c);
             return hipGetLastError();  // (statistics epilogues: one K-slice, nothing to reduce)
         }
     }
-    gemm_v_kernel<QT, NW, UPS, SPLIT, PK, MT, false, false><<<dim3(G, S), NW * 64, 0, st>>>(
+    gemm_v_kernel<QT, NW, UPS, SPLIT, PK, MT, false, 0><<<dim3(G, S), NW * 64, 0, st>>>(
         W, Y, M, N, K, accum, a.afrag, a.inv, a.mfrag, in.op == ACT_RMSNORM ? a.ssq : nullptr, n_units, in.eps,
-        (S > 1 || in.defer) ? part : nullptr, chain != nullptr ? *chain : plain_chain(N));
+        (S > 1 || in.defer) ? part : nullptr, c);
     e = hipGetLastError();
     if (e != hipSuccess || S == 1 || in.defer) return e;
     const int64_t MN = (int64_t)M * N;
@@ -1944,10 +1934,10 @@ template <int QT, int NW, int UPS>
 hipError_t launch_vx(const uint8_t *W, float *Y, int M, int N, int K, int S, int G, int defer, const float *ssq,
                      int n_ssq, float eps, float *part, const Chain &ch, hipStream_t st) {
     if (ch.epi != EPI_STORE)
-        gemm_v_kernel<QT, NW, UPS, true, true, 1, true, true><<<dim3(G, S), NW * 64, 0, st>>>(
+        gemm_v_kernel<QT, NW, UPS, true, true, 1, true, 2><<<dim3(G, S), NW * 64, 0, st>>>(
             W, Y, M, N, K, 0, nullptr, nullptr, nullptr, ssq, n_ssq, eps, (S > 1 || defer) ? part : nullptr, ch);
     else
-        gemm_v_kernel<QT, NW, UPS, true, true, 1, true, false><<<dim3(G, S), NW * 64, 0, st>>>(
+        gemm_v_kernel<QT, NW, UPS, true, true, 1, true, 0><<<dim3(G, S), NW * 64, 0, st>>>(
             W, Y, M, N, K, 0, nullptr, nullptr, nullptr, ssq, n_ssq, eps, (S > 1 || defer) ? part : nullptr, ch);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || S == 1 || defer) return e;
