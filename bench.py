@@ -497,10 +497,12 @@ def read_peak(ih, sizes=(57_196_544, 510_504_960, 4_398_624_768), replays: int =
     return out
 
 
-def read_traffic():
+def read_traffic(chained: bool):
     """HBM bytes per launch of the roofline kernel, from the committed
-    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (None when absent)."""
-    path = os.path.join(ROOT, "profiles", "q4k_gemm_24576x4096_m5_traffic.md")
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary of the kernel this composition
+    times (None when absent)."""
+    name = "q4k_gemm_24576x4096_m5_traffic.md" if chained else "q4k_gemm_classic_24576x4096_m5_traffic.md"
+    path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as f:
             for line in f:
@@ -1046,7 +1048,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": read_traffic(),
+            "traffic": read_traffic(model.gated),
             "kernel": ("gemm_v_kernel<Q4_K, chained input>: packed Q4_K [gate; up] dequant-matmul 24576x4096, "
                        "M=5, fp32-accurate, operand written by its producer (rescaled per unit in registers), "
                        "h = silu(gate) up and down's operand out"

@@ -1426,10 +1426,7 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     RowScales<TOK, NW * 64> rsc;
     rsc.issue(ssq, n_ssq, tid);
     __builtin_amdgcn_sched_barrier(0);
-    // the ring: slot p holds item p, then p + R, p + 2R, ... (consumed, then
-    // refilled in place: every slot stays live across the loop, so the
-    // register allocator never moves a slot, and a move of a register still
-    // being loaded would wait for every load in flight)
+    // the ring: R - 1 items in flight ahead of the one being consumed
     Unit<QT> buf[R];
 #pragma unroll
     for (int p = 0; p < R - 1; p++) {
