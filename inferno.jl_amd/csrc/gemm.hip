@@ -1443,7 +1443,13 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
             inv[u][0][1] = iv[1];
         }
     }
-    rsc.finish(ssq, n_ssq, K, eps, tid, rsp, rs);
+    // (the row scales multiply outputs only: an epilogue after the loop takes
+    // them there, so no wave waits here for the others' loads)
+    // (without RMSNorm the scale is 1 and no wave waits for the others here)
+    const bool has_rs = ssq != nullptr;
+    if constexpr (DE == 0) {
+        if (has_rs) rsc.finish(ssq, n_ssq, K, eps, tid, rsp, rs);
+    }
 
     // a finished tile's plain epilogue: row scale, then the output, the
     // accumulation into it, or this K-slice's partials
@@ -1454,7 +1460,7 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
         for (int k = 0; k < MT * TPL; k++) {
             const int t = lane_token<SPLIT>(k / TPL, g, k % TPL);
             if (t >= M) continue;
-            const float v = sum[k] * rs[t];
+            const float v = has_rs ? sum[k] * rs[t] : sum[k];
             if (part != nullptr) {
                 part[((size_t)blockIdx.y * M + t) * N + r] = v;
             } else {
@@ -1522,7 +1528,8 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     }
     if constexpr (DE != 0) {
         // the epilogues, outside the weight loop: tile slot js by wave js % NW
-        __syncthreads();
+        // (the row scales' barriers also publish pend)
+        rsc.finish(ssq, n_ssq, K, eps, tid, rsp, rs);
         for (int js = wave; js < my_tiles; js += NW) {
             const float2 p2 = pend[js][lane];
             const int tile = (int)blockIdx.x + G * js;
