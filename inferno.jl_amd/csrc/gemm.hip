@@ -1125,10 +1125,11 @@ struct XStage {
 };
 
 template <int QT>
-__device__ __forceinline__ void stage_unit_x(const Chain &ch, int M, int un, int n_units, int lane, XStage &s) {
+__device__ __forceinline__ void stage_unit_x(const uint8_t *xop, const float *xsum, int xsum_stride, int tpu, int M,
+                                             int un, int n_units, int lane, XStage &s) {
     const int slot = lane & 15, G = lane >> 4;
     const int t = min(slot >> 1, M - 1);
-    const uint8_t *pe = ch.xop + (size_t)n_units * CHAIN_UNIT_LIMBS + (size_t)un * CHAIN_UNIT_EXPS + lane * 16;
+    const uint8_t *pe = xop + (size_t)n_units * CHAIN_UNIT_LIMBS + (size_t)un * CHAIN_UNIT_EXPS + lane * 16;
     if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {  // (8 entries)
         const uint2 e8 = *(const uint2 *)pe;
         s.ex = make_uint4(e8.x, e8.y, 0u, 0u);
@@ -1137,9 +1138,8 @@ __device__ __forceinline__ void stage_unit_x(const Chain &ch, int M, int un, int
     }
     if constexpr (GemmCfg<QT>::MINS) {
         // sub-blocks 4 G .. 4 G + 3 (lane groups G < 2 only): tiles 8 G .. (16-row) or 16 G .. (8-row)
-        const int tpu = ch.x_tiles_per_unit;
         if (G < 2) {
-            const float *ps = ch.xsum + (size_t)t * ch.xsum_stride + (size_t)un * tpu + (tpu / 2) * G;
+            const float *ps = xsum + (size_t)t * xsum_stride + (size_t)un * tpu + (tpu / 2) * G;
             s.ts[0] = *(const float4 *)ps;
             s.ts[1] = *(const float4 *)(ps + 4);
             if (tpu == 32) {
@@ -1155,7 +1155,7 @@ __device__ __forceinline__ void stage_unit_x(const Chain &ch, int M, int un, int
 // the accumulator tokens 2G + k). tok: the lane's token is real and the unit
 // exists. Every lane must call it (the unit exponent crosses lanes).
 template <int QT>
-__device__ __forceinline__ void finish_unit_x(const XStage &s, const Chain &ch, bool tok, int lane, AReg<QT> &a,
+__device__ __forceinline__ void finish_unit_x(const XStage &s, int tpu, bool tok, int lane, AReg<QT> &a,
                                               float (&inv)[2]) {
     constexpr int LK = QT == QT_Q6_K ? 1 : QT == QT_Q8_0 ? 2 : 0;
     constexpr int NE = LK == 0 ? 8 : 16;  // exponent entries per lane
@@ -1199,7 +1199,7 @@ __device__ __forceinline__ void finish_unit_x(const XStage &s, const Chain &ch, 
         const float scale = ldexpf(1.f, eu) * (1.0f / 32.0f);
         const float t[16] = {s.ts[0].x, s.ts[0].y, s.ts[0].z, s.ts[0].w, s.ts[1].x, s.ts[1].y, s.ts[1].z, s.ts[1].w,
                              s.ts[2].x, s.ts[2].y, s.ts[2].z, s.ts[2].w, s.ts[3].x, s.ts[3].y, s.ts[3].z, s.ts[3].w};
-        const bool eight = ch.x_tiles_per_unit == 32;
+        const bool eight = tpu == 32;
         h4 mn;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -1300,10 +1300,10 @@ __device__ __forceinline__ void chain_epilogue(const Chain &ch, float *__restric
 // One token tile (MT = 1; several tiles run gemm_w_kernel).
 template <int QT, int NW, int UPS, bool SPLIT, bool PK, int MT, bool XIN, int DE>
 __global__ __launch_bounds__(NW * 64, 8 / NW)
-void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, int N, int K, int accum,
-                   const uint8_t *__restrict__ afrag, const float *__restrict__ invs,
-                   const uint8_t *__restrict__ mfrag, const float *__restrict__ ssq, int n_ssq, float eps,
-                   float *__restrict__ part, Chain ch) {
+void gemm_v_kernel(const uint8_t *__restrict__ W, const uint8_t *__restrict__ afrag,
+                   const uint8_t *__restrict__ mfrag, const float *__restrict__ invs, int M, int N, int K, int G,
+                   int xs_stride, int x_tpu, float *__restrict__ Y, int accum, const float *__restrict__ ssq,
+                   int n_ssq, float eps, float *__restrict__ part, Chain ch) {
     using C = GemmCfg<QT>;
     static_assert(MT == 1, "one token tile");
     // DE: where the tiles' epilogue runs: 0 in the weight loop as each batch
@@ -1331,7 +1331,6 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
 
     const int n_units = (K + UNIT - 1) / UNIT;
     const int n_tiles = (N + 15) / 16;
-    const int G = gridDim.x;
     // wave index as a scalar: everything derived from it stays in SGPRs
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n_in = lane & 15, g = lane >> 4;
@@ -1350,7 +1349,7 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
         live[u] = unit0 + u < n_units;
         const int un = min(unit0 + u, n_units - 1);
         // (a chained input: the producer's limbs, rescaled once the ring is in flight)
-        const uint8_t *src = (XIN ? ch.xop : afrag) + (size_t)un * UNIT_A1 * MT;
+        const uint8_t *src = afrag + (size_t)un * UNIT_A1 * MT;
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             // slots of padding tokens are zero: not fetched
@@ -1421,10 +1420,12 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     XStage xs[XIN ? UPS : 1];
     if constexpr (XIN) {
 #pragma unroll
-        for (int u = 0; u < UPS; u++) stage_unit_x<QT>(ch, M, min(unit0 + u, n_units - 1), n_units, lane, xs[u]);
+        for (int u = 0; u < UPS; u++)
+            stage_unit_x<QT>(afrag, (const float *)mfrag, xs_stride, x_tpu, M, min(unit0 + u, n_units - 1), n_units,
+                             lane, xs[u]);
     }
     RowScales<TOK, NW * 64> rsc;
-    rsc.issue(ssq, n_ssq, tid);
+    if constexpr (DE == 0) rsc.issue(ssq, n_ssq, tid);
     __builtin_amdgcn_sched_barrier(0);
     // the ring: R - 1 items in flight ahead of the one being consumed
     Unit<QT> buf[R];
@@ -1433,12 +1434,13 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
         load_item(p / UPS, p % UPS, buf[p]);
         __builtin_amdgcn_sched_barrier(0);  // ring slots fill in order
     }
+    if constexpr (DE != 0) rsc.issue(ssq, n_ssq, tid);  // (needed after the loop only)
     if constexpr (XIN) {
         const bool tok = (n_in >> 1) < M;
 #pragma unroll
         for (int u = 0; u < UPS; u++) {
             float iv[2];
-            finish_unit_x<QT>(xs[u], ch, tok && live[u], lane, a[u][0], iv);
+            finish_unit_x<QT>(xs[u], x_tpu, tok && live[u], lane, a[u][0], iv);
             inv[u][0][0] = iv[0];
             inv[u][0][1] = iv[1];
         }
@@ -1917,14 +1919,14 @@ hipError_t launch_v(const uint8_t *W, const float *X, const ActIn &in, float *Y,
     if constexpr (SPLIT && MT == 1 && PK && NW == 8) {  // (the chained calls' plan)
         if (c.epi != EPI_STORE) {
             gemm_v_kernel<QT, NW, UPS, SPLIT, PK, MT, false, 2><<<dim3(G, S), NW * 64, 0, st>>>(
-                W, Y, M, N, K, accum, a.afrag, a.inv, a.mfrag, in.op == ACT_RMSNORM ? a.ssq : nullptr, n_units,
-                in.eps, (S > 1 || in.defer) ? part : nullptr, c);
+                W, a.afrag, a.mfrag, a.inv, M, N, K, G, 0, 0, Y, accum, in.op == ACT_RMSNORM ? a.ssq : nullptr,
+                n_units, in.eps, (S > 1 || in.defer) ? part : nullptr, c);
             return hipGetLastError();  // (statistics epilogues: one K-slice, nothing to reduce)
         }
     }
     gemm_v_kernel<QT, NW, UPS, SPLIT, PK, MT, false, 0><<<dim3(G, S), NW * 64, 0, st>>>(
-        W, Y, M, N, K, accum, a.afrag, a.inv, a.mfrag, in.op == ACT_RMSNORM ? a.ssq : nullptr, n_units, in.eps,
-        (S > 1 || in.defer) ? part : nullptr, c);
+        W, a.afrag, a.mfrag, a.inv, M, N, K, G, 0, 0, Y, accum, in.op == ACT_RMSNORM ? a.ssq : nullptr, n_units,
+        in.eps, (S > 1 || in.defer) ? part : nullptr, c);
     e = hipGetLastError();
     if (e != hipSuccess || S == 1 || in.defer) return e;
     const int64_t MN = (int64_t)M * N;
@@ -1937,12 +1939,17 @@ hipError_t launch_v(const uint8_t *W, const float *X, const ActIn &in, float *Y,
 template <int QT, int NW, int UPS>
 hipError_t launch_vx(const uint8_t *W, float *Y, int M, int N, int K, int S, int G, int defer, const float *ssq,
                      int n_ssq, float eps, float *part, const Chain &ch, hipStream_t st) {
+    // (the operand, its tile sums and their layout travel in the leading
+    // arguments, which the hardware preloads into SGPRs)
+    const uint8_t *xs = (const uint8_t *)ch.xsum;
     if (ch.epi != EPI_STORE)
         gemm_v_kernel<QT, NW, UPS, true, true, 1, true, 2><<<dim3(G, S), NW * 64, 0, st>>>(
-            W, Y, M, N, K, 0, nullptr, nullptr, nullptr, ssq, n_ssq, eps, (S > 1 || defer) ? part : nullptr, ch);
+            W, ch.xop, xs, nullptr, M, N, K, G, ch.xsum_stride, ch.x_tiles_per_unit, Y, 0, ssq, n_ssq, eps,
+            (S > 1 || defer) ? part : nullptr, ch);
     else
         gemm_v_kernel<QT, NW, UPS, true, true, 1, true, 0><<<dim3(G, S), NW * 64, 0, st>>>(
-            W, Y, M, N, K, 0, nullptr, nullptr, nullptr, ssq, n_ssq, eps, (S > 1 || defer) ? part : nullptr, ch);
+            W, ch.xop, xs, nullptr, M, N, K, G, ch.xsum_stride, ch.x_tiles_per_unit, Y, 0, ssq, n_ssq, eps,
+            (S > 1 || defer) ? part : nullptr, ch);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || S == 1 || defer) return e;
     const int64_t MN = (int64_t)M * N;
