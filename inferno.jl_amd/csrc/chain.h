@@ -8,8 +8,9 @@
 enum { EPI_STORE = 0, EPI_STATS = 1, EPI_RESID = 2, EPI_GATE = 3 };
 
 // Bytes of a chained operand for K inputs: per 256-element unit the split
-// fp16 limbs in the input stage's layout (8192 bytes at one token tile),
-// then per unit one exponent byte per lane entry (64 lanes x 16).
+// fp16 limbs in the one-tile input stage's layout (8192 bytes reserved; M
+// tokens use entries of 4 lane groups x 2M slots), then per unit one
+// exponent byte per lane entry (lane group G, slot s at (2M G + s) 16).
 constexpr int CHAIN_UNIT_LIMBS = 8192;
 constexpr int CHAIN_UNIT_EXPS = 1024;
 inline int64_t chain_operand_bytes(int K) { return (int64_t)((K + 255) / 256) * (CHAIN_UNIT_LIMBS + CHAIN_UNIT_EXPS); }

@@ -601,7 +601,7 @@ template <int LK, int MT, bool SPLIT, bool MINS>
 __device__ __forceinline__ void prep_finish(float (&v)[8], float4 wa, float4 wb, int u, int t, int gi, int op,
                                             uint8_t *__restrict__ afrag, float *__restrict__ xs,
                                             float *__restrict__ inv, uint8_t *__restrict__ mfrag,
-                                            float *__restrict__ ssq) {
+                                            float *__restrict__ ssq, int sl) {
     constexpr int TOK = MT * (SPLIT ? 8 : 16);
     constexpr int ENTRY = Layout<LK>::ENTRY;
     if (op == ACT_RMSNORM) {
@@ -679,7 +679,10 @@ __device__ __forceinline__ void prep_finish(float (&v)[8], float4 wa, float4 wb,
         h4 H, L;
 #pragma unroll
         for (int e = 0; e < 4; e++) { H[e] = hi[4 * p + e]; L[e] = lo[4 * p + e]; }
-        uint8_t *dst = base + ((size_t)(c * MT + mt) * 64 + G * 16 + slot) * ENTRY + item * 2;
+        // (sl > 0: the compact one-tile layout, sl slots per lane group, padding tokens absent)
+        if (sl > 0 && slot >= sl) continue;
+        const size_t ent = sl > 0 ? (size_t)(c * 4 + G) * sl + slot : (size_t)(c * MT + mt) * 64 + G * 16 + slot;
+        uint8_t *dst = base + ent * ENTRY + item * 2;
         *(h4 *)dst = H;
         if (SPLIT) *(h4 *)(dst + ENTRY) = L;  // slot + 1
     }
@@ -696,7 +699,7 @@ __global__ __launch_bounds__(32 * TPW) void prep_kernel(const float *__restrict_
                                                    uint8_t *__restrict__ afrag, float *__restrict__ xs,
                                                    float *__restrict__ inv, uint8_t *__restrict__ mfrag,
                                                    float *__restrict__ ssq, const float *__restrict__ add, int n_add,
-                                                   int64_t add_stride, float *__restrict__ xw) {
+                                                   int64_t add_stride, float *__restrict__ xw, int sl) {
     const int u = blockIdx.x, tid = threadIdx.x;
     const int tl = tid >> 5, gi = tid & 31;  // (a token per 32 threads, TPW per workgroup)
     const int t = blockIdx.y * TPW + tl;
@@ -761,7 +764,7 @@ __global__ __launch_bounds__(32 * TPW) void prep_kernel(const float *__restrict_
 #pragma unroll
         for (int e = 0; e < 8; e++) v[e] = 0.f;
     }
-    prep_finish<LK, MT, SPLIT, MINS>(v, wa, wb, u, t, gi, op, afrag, xs, inv, mfrag, ssq);
+    prep_finish<LK, MT, SPLIT, MINS>(v, wa, wb, u, t, gi, op, afrag, xs, inv, mfrag, ssq, sl);
 }
 
 // ---------------------------------------------------------------- gemm
@@ -1129,7 +1132,9 @@ __device__ __forceinline__ void stage_unit_x(const uint8_t *xop, const float *xs
                                              int un, int n_units, int lane, XStage &s) {
     const int slot = lane & 15, G = lane >> 4;
     const int t = min(slot >> 1, M - 1);
-    const uint8_t *pe = xop + (size_t)n_units * CHAIN_UNIT_LIMBS + (size_t)un * CHAIN_UNIT_EXPS + lane * 16;
+    // (compact: lane group G, slot s at G 2M + s; padding slots read a real slot's bytes, unused)
+    const uint8_t *pe = xop + (size_t)n_units * CHAIN_UNIT_LIMBS + (size_t)un * CHAIN_UNIT_EXPS +
+                        (size_t)(G * 2 * M + min(slot, 2 * M - 1)) * 16;
     if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {  // (8 entries)
         const uint2 e8 = *(const uint2 *)pe;
         s.ex = make_uint4(e8.x, e8.y, 0u, 0u);
@@ -1232,7 +1237,7 @@ __device__ __forceinline__ float row16_sum(float v) {
 // selected arithmetically: one copy of the code for the three layouts): hi
 // and lo limbs at slots 2t, 2t + 1; the entry's exponent written by the
 // entry's first element.
-__device__ __forceinline__ void put_operand(const Chain &ch, int t, int k, float v, int e2) {
+__device__ __forceinline__ void put_operand(const Chain &ch, int M, int t, int k, float v, int e2) {
     const int lk = ch.op_lk, o = k & 255, u = k >> 8;
     const int q = (o >> 3) & 3;
     const int c = lk == 0 ? ((o >> 3) & 1) + 2 * ((o >> 5) & 1) + 4 * ((o >> 7) & 1) : lk == 1 ? o >> 4 : o >> 5;
@@ -1242,12 +1247,13 @@ __device__ __forceinline__ void put_operand(const Chain &ch, int t, int k, float
     const int entry = lk == 1 ? 8 : 16;
     const float xs = v * ldexpf(1.f, e2 == 127 ? 0 : e2);
     const _Float16 hi = (_Float16)xs, lo = (_Float16)(xs - (float)hi);
-    uint8_t *p = ch.yop + (size_t)u * CHAIN_UNIT_LIMBS + (size_t)(c * 64 + 16 * G + 2 * t) * entry + item * 2;
+    const int sl = 2 * M;  // (the compact one-tile layout)
+    uint8_t *p = ch.yop + (size_t)u * CHAIN_UNIT_LIMBS + (size_t)((c * 4 + G) * sl + 2 * t) * entry + item * 2;
     *(_Float16 *)p = hi;
     *(_Float16 *)(p + entry) = lo;
     if ((item & 3) == 0 && (lk == 2 || item == 0)) {
         int8_t *x = (int8_t *)ch.yop + (size_t)ch.y_units * CHAIN_UNIT_LIMBS + (size_t)u * CHAIN_UNIT_EXPS +
-                    (16 * G + 2 * t) * 16 + ei;
+                    (G * sl + 2 * t) * 16 + ei;
         x[0] = (int8_t)e2;
         x[16] = (int8_t)e2;
     }
@@ -1286,7 +1292,7 @@ __device__ __forceinline__ void chain_epilogue(const Chain &ch, float *__restric
         const float v = y * w;
         if (ch.yop != nullptr) {
             const int e2 = tile_exp(row16_max(fabsf(v)));
-            if (real && t < M) put_operand(ch, t, kcons, v, e2);
+            if (real && t < M) put_operand(ch, M, t, kcons, v, e2);
         }
         const float ts = ch.ysum != nullptr ? row16_sum(v) : 0.f;
         const float sq = ch.yssq != nullptr ? row16_sum(y * y) : 0.f;
@@ -1334,6 +1340,7 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, const uint8_t *__restrict__ af
     // wave index as a scalar: everything derived from it stays in SGPRs
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n_in = lane & 15, g = lane >> 4;
+    const int SL = SPLIT ? 2 * M : M;  // operand slots per lane group (compact layout)
     const int my_tiles = (n_tiles - 1 - (int)blockIdx.x) / G + 1;  // the plan keeps G <= n_tiles
     const int unit0 = ((int)blockIdx.y * NW + wave) * UPS;
     const size_t row_bytes = (size_t)(K / C::QK) * C::BB;
@@ -1349,17 +1356,18 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, const uint8_t *__restrict__ af
         live[u] = unit0 + u < n_units;
         const int un = min(unit0 + u, n_units - 1);
         // (a chained input: the producer's limbs, rescaled once the ring is in flight)
-        const uint8_t *src = afrag + (size_t)un * UNIT_A1 * MT;
+        // (the compact one-tile layout: entry c, lane group g, slot n_in at (4 c + g) SL + n_in)
+        const uint8_t *src = afrag + (size_t)un * UNIT_A1 + (size_t)(g * SL + n_in) * (QT == QT_Q6_K ? 8 : 16);
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             // slots of padding tokens are zero: not fetched
             if ((SPLIT ? (n_in >> 1) : n_in) + mt * TOKT < M) {
                 if constexpr (QT == QT_Q6_K) {
 #pragma unroll
-                    for (int c = 0; c < 16; c++) a[u][mt].f[c] = *(const h4 *)(src + ((c * MT + mt) * 64 + lane) * 8);
+                    for (int c = 0; c < 16; c++) a[u][mt].f[c] = *(const h4 *)(src + (size_t)c * 4 * SL * 8);
                 } else {
 #pragma unroll
-                    for (int c = 0; c < 8; c++) a[u][mt].f[c] = *(const h8 *)(src + ((c * MT + mt) * 64 + lane) * 16);
+                    for (int c = 0; c < 8; c++) a[u][mt].f[c] = *(const h8 *)(src + (size_t)c * 4 * SL * 16);
                 }
                 if constexpr (C::MINS && !XIN)
                     a[u][mt].mins = *(const h4 *)(mfrag + ((size_t)un * MT + mt) * 512 + lane * 8);
@@ -1882,8 +1890,12 @@ int env_int(const char *name, int dflt) {
     return v ? atoi(v) : dflt;
 }
 
+// compact: the one-token-tile streaming kernel's operand layout (entry c,
+// lane group G, slot s at (4 c + G) sl + s with sl = the slots of M tokens);
+// otherwise 64 lanes per entry (the tall and LDS kernels).
 template <int QT, int MT, bool SPLIT>
-hipError_t launch_prep(const float *X, const ActIn &in, int M, int K, const ActWs &a, hipStream_t st) {
+hipError_t launch_prep(const float *X, const ActIn &in, int M, int K, const ActWs &a, hipStream_t st,
+                       bool compact = false) {
     using C = GemmCfg<QT>;
     constexpr int TOK = MT * (SPLIT ? 8 : 16);
     const int n_units = (K + UNIT - 1) / UNIT;
@@ -1894,7 +1906,8 @@ hipError_t launch_prep(const float *X, const ActIn &in, int M, int K, const ActW
     static const int tpw = env_int("IHIP_PREP_TPW", 2);
 #define PREP(tp) prep_kernel<LK, MT, SPLIT, C::MINS, tp><<<dim3(n_units, TOK / tp), 32 * tp, 0, st>>>( \
         X, in.ldx, M, K, in.op, in.norm_w, a.afrag, a.xs, a.inv, a.mfrag, a.ssq, in.add, in.n_add, in.add_stride, \
-        const_cast<float *>(X))
+        const_cast<float *>(X), sl)
+    const int sl = compact ? (SPLIT ? 2 * M : M) : 0;
     if (tpw == 2) PREP(2); else if (tpw == 4) PREP(4); else PREP(8);
 #undef PREP
     return hipGetLastError();
@@ -1912,7 +1925,7 @@ template <int QT, int NW, int UPS, bool SPLIT, bool PK, int MT>
 hipError_t launch_v(const uint8_t *W, const float *X, const ActIn &in, float *Y, int M, int N, int K, int S, int G,
                     int accum, const ActWs &a, float *part, hipStream_t st, const Chain *chain = nullptr) {
     hipError_t e;
-    if (!in.reuse && (e = launch_prep<QT, MT, SPLIT>(X, in, M, K, a, st)) != hipSuccess) return e;
+    if (!in.reuse && (e = launch_prep<QT, MT, SPLIT>(X, in, M, K, a, st, true)) != hipSuccess) return e;
     const int n_units = (K + UNIT - 1) / UNIT;
     // (a chained producer's epilogue is its own instantiation: classic calls keep their registers)
     const Chain c = chain != nullptr ? *chain : plain_chain(N);
