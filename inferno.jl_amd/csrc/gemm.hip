@@ -1266,40 +1266,38 @@ __device__ __forceinline__ void put_operand(const Chain &ch, int M, int t, int k
 // next norm weight of this lane's row. Written to stay small (one pass per
 // token, one operand writer): it runs once per tile at a kernel's end, where
 // every instruction is fetched cold.
-__device__ __forceinline__ void chain_epilogue(const Chain &ch, float *__restrict__ Y, float s0, float s1,
-                                               const float *rs, int M, int N, int tile, int n_in, int g, float yold0,
-                                               float yold1, float w) {
+// One of the two tokens of each lane (token 2 g + k: s is its sum), so the
+// (tile, token) jobs of a workgroup spread over all its waves.
+__device__ __forceinline__ void chain_epilogue(const Chain &ch, float *__restrict__ Y, float s, const float *rs,
+                                               int M, int N, int tile, int n_in, int g, int k, float yold, float w) {
     const int r = tile * 16 + n_in;
     const bool stats = ch.epi != EPI_STATS || tile * 16 < ch.stat_rows;
     const int kcons = ch.epi == EPI_GATE ? tile * 8 + (n_in & 7) : r;  // the consumer's element
     const bool real = r < N && (ch.epi != EPI_GATE || n_in < 8);
-#pragma unroll 1
-    for (int k = 0; k < 2; k++) {
-        const int t = 2 * g + k;
-        const bool ok = r < N && t < M;
-        const float v0 = ok ? (k ? s1 : s0) * rs[t] : 0.f;
-        float y = v0;
-        if (ch.epi == EPI_GATE) {
-            // rows 16 tile + n are gate channel 8 tile + n (n < 8) and its up row (n + 8)
-            const float u = __shfl_xor(v0, 8);
-            y = (n_in < 8 && ok) ? silu_mul1(v0, u) : 0.f;
-            if (n_in < 8 && ok) Y[(size_t)t * ch.ldy + kcons] = y;
-        } else if (ok) {
-            if (ch.epi == EPI_RESID) y += k ? yold1 : yold0;
-            Y[(size_t)t * ch.ldy + r] = y;
-        }
-        if (!stats) continue;
-        const float v = y * w;
-        if (ch.yop != nullptr) {
-            const int e2 = tile_exp(row16_max(fabsf(v)));
-            if (real && t < M) put_operand(ch, M, t, kcons, v, e2);
-        }
-        const float ts = ch.ysum != nullptr ? row16_sum(v) : 0.f;
-        const float sq = ch.yssq != nullptr ? row16_sum(y * y) : 0.f;
-        if (n_in == 0 && t < M) {
-            if (ch.ysum != nullptr) ch.ysum[(size_t)t * ch.ysum_stride + tile] = ts;
-            if (ch.yssq != nullptr) ch.yssq[(size_t)tile * 8 + t] = sq;
-        }
+    const int t = 2 * g + k;
+    const bool ok = r < N && t < M;
+    const float v0 = ok ? s * rs[t] : 0.f;
+    float y = v0;
+    if (ch.epi == EPI_GATE) {
+        // rows 16 tile + n are gate channel 8 tile + n (n < 8) and its up row (n + 8)
+        const float u = __shfl_xor(v0, 8);
+        y = (n_in < 8 && ok) ? silu_mul1(v0, u) : 0.f;
+        if (n_in < 8 && ok) Y[(size_t)t * ch.ldy + kcons] = y;
+    } else if (ok) {
+        if (ch.epi == EPI_RESID) y += yold;
+        Y[(size_t)t * ch.ldy + r] = y;
+    }
+    if (!stats) return;
+    const float v = y * w;
+    if (ch.yop != nullptr) {
+        const int e2 = tile_exp(row16_max(fabsf(v)));
+        if (real && t < M) put_operand(ch, M, t, kcons, v, e2);
+    }
+    const float ts = ch.ysum != nullptr ? row16_sum(v) : 0.f;
+    const float sq = ch.yssq != nullptr ? row16_sum(y * y) : 0.f;
+    if (n_in == 0 && t < M) {
+        if (ch.ysum != nullptr) ch.ysum[(size_t)t * ch.ysum_stride + tile] = ts;
+        if (ch.yssq != nullptr) ch.yssq[(size_t)tile * 8 + t] = sq;
     }
 }
 
@@ -1412,6 +1410,10 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, const uint8_t *__restrict__ af
     };
     // chained producer: the old residual (EPI_RESID) and the next norm weight
     // of this wave's first epilogue tile, loaded now and used at the end
+    // (the epilogue's jobs: with at most NW / 2 tiles, wave w takes token
+    // 2 g + (w & 1) of tile slot w / 2; else tile slots w, w + NW, .. with both tokens)
+    const bool spread = 2 * my_tiles <= NW;
+    const int js0 = spread ? wave >> 1 : wave, k0 = spread ? wave & 1 : 0, k1 = spread ? k0 : 1;
     float pre_y0 = 0.f, pre_y1 = 0.f, pre_w = 1.f;
     auto load_pre = [&](int tile) {
         const int r = min(tile * 16 + n_in, N - 1);
@@ -1422,7 +1424,7 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, const uint8_t *__restrict__ af
         pre_w = ch.yw != nullptr ? ch.yw[ch.epi == EPI_GATE ? tile * 8 + (n_in & 7) : r] : 1.f;
     };
     if constexpr (CE) {
-        if (wave < my_tiles) load_pre((int)blockIdx.x + G * wave);
+        if (js0 < my_tiles) load_pre((int)blockIdx.x + G * js0);
     }
     // chained input: the exponents and tile sums of each unit, before the ring
     XStage xs[XIN ? UPS : 1];
@@ -1537,20 +1539,18 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, const uint8_t *__restrict__ af
             if (n_full + p < n_items) consume(jb + p / UPS, p % UPS, buf[p]);
     }
     if constexpr (DE != 0) {
-        // the epilogues, outside the weight loop: tile slot js by wave js % NW
-        // (the row scales' barriers also publish pend)
+        // the epilogues, outside the weight loop (jobs as above; the row
+        // scales' barriers also publish pend)
+        static_assert(CE, "after-loop epilogues are the chained producer's");
         rsc.finish(ssq, n_ssq, K, eps, tid, rsp, rs);
-        for (int js = wave; js < my_tiles; js += NW) {
+        for (int js = js0; js < my_tiles; js += NW) {
             const float2 p2 = pend[js][lane];
             const int tile = (int)blockIdx.x + G * js;
-            if constexpr (CE) {
-                // (the first tile's residual and weight were loaded at the start)
-                if (js != wave) load_pre(tile);
-                chain_epilogue(ch, Y, p2.x, p2.y, rs, M, N, tile, n_in, g, pre_y0, pre_y1, pre_w);
-            } else {
-                const float sm[2] = {p2.x, p2.y};
-                store_tile(sm, tile);
-            }
+            // (the first tile's residual and weight were loaded at the start)
+            if (js != js0) load_pre(tile);
+#pragma unroll 1
+            for (int k = k0; k <= k1; k++)
+                chain_epilogue(ch, Y, k ? p2.y : p2.x, rs, M, N, tile, n_in, g, k, k ? pre_y1 : pre_y0, pre_w);
         }
     }
 }
