@@ -679,10 +679,18 @@ __device__ __forceinline__ void prep_finish(float (&v)[8], float4 wa, float4 wb,
         h4 H, L;
 #pragma unroll
         for (int e = 0; e < 4; e++) { H[e] = hi[4 * p + e]; L[e] = lo[4 * p + e]; }
-        // (sl > 0: the compact one-tile layout, sl slots per lane group, padding tokens absent)
-        if (sl > 0 && slot >= sl) continue;
-        const size_t ent = sl > 0 ? (size_t)(c * 4 + G) * sl + slot : (size_t)(c * MT + mt) * 64 + G * 16 + slot;
-        uint8_t *dst = base + ent * ENTRY + item * 2;
+        // (sl > 0: the compact one-tile layout, sl slots of 16 bytes per lane
+        // group, padding tokens absent; Q6_K's 8-byte entries 2j and 2j + 1
+        // share a slot)
+        if (sl > 0) {
+            if (slot >= sl) continue;
+            const int cc = LK == 1 ? c >> 1 : c, sub = LK == 1 ? (c & 1) * 8 : 0;
+            uint8_t *dst = base + ((size_t)(cc * 4 + G) * sl + slot) * 16 + sub + item * 2;
+            *(h4 *)dst = H;
+            if (SPLIT) *(h4 *)(dst + 16) = L;  // slot + 1
+            continue;
+        }
+        uint8_t *dst = base + ((size_t)(c * MT + mt) * 64 + G * 16 + slot) * ENTRY + item * 2;
         *(h4 *)dst = H;
         if (SPLIT) *(h4 *)(dst + ENTRY) = L;  // slot + 1
     }
@@ -1244,13 +1252,14 @@ __device__ __forceinline__ void put_operand(const Chain &ch, int M, int t, int k
     const int G = lk == 0 ? ((o >> 4) & 1) + 2 * ((o >> 6) & 1) : lk == 1 ? (o >> 2) & 3 : 2 * (q & 1) + ((o >> 2) & 1);
     const int item = lk == 0 ? o & 7 : lk == 1 ? o & 3 : (q < 2 ? 0 : 4) + (o & 3);
     const int ei = lk == 2 ? 2 * c + (q >> 1) : c;
-    const int entry = lk == 1 ? 8 : 16;
     const float xs = v * ldexpf(1.f, e2 == 127 ? 0 : e2);
     const _Float16 hi = (_Float16)xs, lo = (_Float16)(xs - (float)hi);
-    const int sl = 2 * M;  // (the compact one-tile layout)
-    uint8_t *p = ch.yop + (size_t)u * CHAIN_UNIT_LIMBS + (size_t)((c * 4 + G) * sl + 2 * t) * entry + item * 2;
+    // (the compact one-tile layout: 16 bytes per slot; Q6_K's 8-byte entries
+    // 2j and 2j + 1 share one)
+    const int sl = 2 * M, cc = lk == 1 ? c >> 1 : c, sub = lk == 1 ? (c & 1) * 8 : 0;
+    uint8_t *p = ch.yop + (size_t)u * CHAIN_UNIT_LIMBS + (size_t)((cc * 4 + G) * sl + 2 * t) * 16 + sub + item * 2;
     *(_Float16 *)p = hi;
-    *(_Float16 *)(p + entry) = lo;
+    *(_Float16 *)(p + 16) = lo;
     if ((item & 3) == 0 && (lk == 2 || item == 0)) {
         int8_t *x = (int8_t *)ch.yop + (size_t)ch.y_units * CHAIN_UNIT_LIMBS + (size_t)u * CHAIN_UNIT_EXPS +
                     (G * sl + 2 * t) * 16 + ei;
@@ -1265,9 +1274,9 @@ __device__ __forceinline__ void put_operand(const Chain &ch, int M, int t, int k
 // each token pair). yold: the residual's old values (EPI_RESID), w: the
 // next norm weight of this lane's row. Written to stay small (one pass per
 // token, one operand writer): it runs once per tile at a kernel's end, where
-// every instruction is fetched cold.
-// One of the two tokens of each lane (token 2 g + k: s is its sum), so the
-// (tile, token) jobs of a workgroup spread over all its waves.
+// every instruction is fetched cold. One call handles one of the two tokens
+// of each lane (token 2 g + k: s is its sum), so a workgroup's (tile, token)
+// jobs can spread over its waves.
 __device__ __forceinline__ void chain_epilogue(const Chain &ch, float *__restrict__ Y, float s, const float *rs,
                                                int M, int N, int tile, int n_in, int g, int k, float yold, float w) {
     const int r = tile * 16 + n_in;
@@ -1354,15 +1363,20 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, const uint8_t *__restrict__ af
         live[u] = unit0 + u < n_units;
         const int un = min(unit0 + u, n_units - 1);
         // (a chained input: the producer's limbs, rescaled once the ring is in flight)
-        // (the compact one-tile layout: entry c, lane group g, slot n_in at (4 c + g) SL + n_in)
-        const uint8_t *src = afrag + (size_t)un * UNIT_A1 + (size_t)(g * SL + n_in) * (QT == QT_Q6_K ? 8 : 16);
+        // (the compact one-tile layout: entry c, lane group g, slot n_in at (4 c + g) SL + n_in, 16
+        // bytes; Q6_K's entries 2j, 2j + 1 as the halves of slot entry j)
+        const uint8_t *src = afrag + (size_t)un * UNIT_A1 + (size_t)(g * SL + n_in) * 16;
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             // slots of padding tokens are zero: not fetched
             if ((SPLIT ? (n_in >> 1) : n_in) + mt * TOKT < M) {
                 if constexpr (QT == QT_Q6_K) {
 #pragma unroll
-                    for (int c = 0; c < 16; c++) a[u][mt].f[c] = *(const h4 *)(src + (size_t)c * 4 * SL * 8);
+                    for (int j = 0; j < 8; j++) {
+                        const h8 v = *(const h8 *)(src + (size_t)j * 4 * SL * 16);
+                        a[u][mt].f[2 * j] = __builtin_shufflevector(v, v, 0, 1, 2, 3);
+                        a[u][mt].f[2 * j + 1] = __builtin_shufflevector(v, v, 4, 5, 6, 7);
+                    }
                 } else {
 #pragma unroll
                     for (int c = 0; c < 8; c++) a[u][mt].f[c] = *(const h8 *)(src + (size_t)c * 4 * SL * 16);
