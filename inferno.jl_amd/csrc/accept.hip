@@ -208,39 +208,41 @@ __device__ __forceinline__ float wave_scan(float v) {
     return v;
 }
 
-// Ratio tests of one verify step (one wave): the statistics of the step's
-// 2k + 1 rows are merged first (wave_merge_row, kept in LDS), then lane i
-// judges draft i (groups of 64 lanes for k > 64). Writes the accepted
-// drafts, out_n, and the decision.
+// Ratio tests of one verify step by a whole workgroup: the statistics of the
+// step's 2k + 1 rows are merged first (row r by wave r % 4: the loads of
+// all its rows in flight before any merge; kept in LDS), then lane i of wave
+// 0 judges draft i (groups of 64 lanes for k > 64). The result is the
+// decision of each draw slot (s_dec[0], s_dec[1]); with publish, the
+// accepted drafts, out_n and the decisions are also written out. Every
+// workgroup that calls it for the same step computes the same decision.
 constexpr int DECIDE_MAX_ROWS = 255;  // 2k + 1, k <= 127
-__global__ __launch_bounds__(64) void decide_kernel(const float *__restrict__ tgt, const float *__restrict__ drf,
-                                                    const int32_t *__restrict__ draft_tok, int k, int V, float T,
-                                                    const float *__restrict__ u_acc, const float *__restrict__ u_res,
-                                                    const float *__restrict__ u_bonus, int mode,
-                                                    const float2 *__restrict__ part, int nchunk,
-                                                    int32_t *__restrict__ out_tok, int32_t *__restrict__ out_n,
-                                                    Decision *__restrict__ dec) {
-    __shared__ float2 ms[DECIDE_MAX_ROWS];  // target rows 0..k, then draft rows 0..k-1
-    const int step = blockIdx.x, lane = threadIdx.x;
+constexpr int DECIDE_WAVES = NT / 64;
+__device__ void decide_block(const float *__restrict__ tgt, const float *__restrict__ drf,
+                             const int32_t *__restrict__ draft_tok, int k, int V, float T,
+                             const float *__restrict__ u_acc, const float *__restrict__ u_res,
+                             const float *__restrict__ u_bonus, int mode, const float2 *__restrict__ part,
+                             int nchunk, int step, int steps, bool publish, int32_t *__restrict__ out_tok,
+                             int32_t *__restrict__ out_n, Decision *__restrict__ dec, float2 *ms, Decision *s_dec) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const float *Lt = tgt + (size_t)step * (k + 1) * V;
     const float *Ld = drf + (size_t)step * k * V;
     const int32_t *dt = draft_tok + (size_t)step * k;
     const float2 *Pt = part + (size_t)step * (k + 1) * nchunk;
-    const float2 *Pd = part + ((size_t)gridDim.x * (k + 1) + (size_t)step * k) * nchunk;
+    const float2 *Pd = part + ((size_t)steps * (k + 1) + (size_t)step * k) * nchunk;
     const float Tr = mode == 0 ? T : 1.0f;
-    // independent loads first: the first 64 drafts' ids and uniforms, then
-    // (once the ids are in) their two logits, issued before the merges
-    const bool has0 = lane < k;
+    // wave 0: the first 64 drafts' ids and uniforms, then (once the ids are
+    // in) their two logits, issued before the merges
+    const bool has0 = wave == 0 && lane < k;
     const int x0 = has0 ? dt[lane] : 0;
     const float ua0 = has0 ? u_acc[(size_t)step * k + lane] : 0.f;
-    // rows in batches of 8: all their partials in flight before any merge
     const int nrows = 2 * k + 1;
     float lx0 = 0.f, dx0 = 0.f;
-    for (int r0 = 0; r0 < nrows; r0 += 8) {
+    // rows wave, wave + W, ..: in batches of 8 per wave
+    for (int r0 = wave; r0 < nrows; r0 += 8 * DECIDE_WAVES) {
         float2 pv[8][2];
 #pragma unroll
         for (int b = 0; b < 8; b++) {
-            const int r = min(r0 + b, nrows - 1);
+            const int r = min(r0 + b * DECIDE_WAVES, nrows - 1);
             const float2 *row = r <= k ? Pt + (size_t)r * nchunk : Pd + (size_t)(r - k - 1) * nchunk;
 #pragma unroll
             for (int h = 0; h < 2; h++) {
@@ -254,7 +256,7 @@ __global__ __launch_bounds__(64) void decide_kernel(const float *__restrict__ tg
         }
 #pragma unroll
         for (int b = 0; b < 8; b++) {
-            const int r = r0 + b;
+            const int r = r0 + b * DECIDE_WAVES;
             if (r >= nrows) break;
             float2 v;
             if (nchunk <= 128) {
@@ -269,84 +271,90 @@ __global__ __launch_bounds__(64) void decide_kernel(const float *__restrict__ tg
         }
     }
     __syncthreads();
-    int first = k;  // first draft that is invalid or rejected
-    bool invalid = false;
-    float f_q = 0.f;
-    for (int base = 0; base < k && first == k; base += 64) {
-        const int i = base + lane;
-        bool bad = false, inv = false;
-        float q = 0.f;
-        if (i < k) {
-            const bool pre = base == 0;  // the first 64 were fetched up front
-            const int x = pre ? x0 : dt[i];
-            if (x < 0 || x >= V) {
-                bad = inv = true;
-            } else {
-                const float2 pt = ms[i], pd = ms[k + 1 + i];
-                const float p = __expf((pre ? lx0 : Lt[(size_t)i * V + x]) / Tr - pt.x) / pt.y;
-                q = __expf((pre ? dx0 : Ld[(size_t)i * V + x]) / Tr - pd.x) / pd.y;
-                const float ratio = q > 0.f ? fminf(1.0f, p / q) : 1.0f;
-                bad = !((pre ? ua0 : u_acc[(size_t)step * k + i]) < ratio);
+    if (wave == 0) {
+        int first = k;  // first draft that is invalid or rejected
+        bool invalid = false;
+        float f_q = 0.f;
+        for (int base = 0; base < k && first == k; base += 64) {
+            const int i = base + lane;
+            bool bad = false, inv = false;
+            float q = 0.f;
+            if (i < k) {
+                const bool pre = base == 0;  // the first 64 were fetched up front
+                const int x = pre ? x0 : dt[i];
+                if (x < 0 || x >= V) {
+                    bad = inv = true;
+                } else {
+                    const float2 pt = ms[i], pd = ms[k + 1 + i];
+                    const float p = __expf((pre ? lx0 : Lt[(size_t)i * V + x]) / Tr - pt.x) / pt.y;
+                    q = __expf((pre ? dx0 : Ld[(size_t)i * V + x]) / Tr - pd.x) / pd.y;
+                    const float ratio = q > 0.f ? fminf(1.0f, p / q) : 1.0f;
+                    bad = !((pre ? ua0 : u_acc[(size_t)step * k + i]) < ratio);
+                }
+            }
+            const uint64_t m = __ballot(bad);
+            if (m) {
+                const int f = __ffsll((unsigned long long)m) - 1;
+                first = base + f;
+                invalid = __shfl(inv ? 1 : 0, f) != 0;
+                f_q = __shfl(q, f);
             }
         }
-        const uint64_t m = __ballot(bad);
-        if (m) {
-            const int f = __ffsll((unsigned long long)m) - 1;
-            first = base + f;
-            invalid = __shfl(inv ? 1 : 0, f) != 0;
-            f_q = __shfl(q, f);
+        // accepted drafts
+        if (publish)
+            for (int i = lane; i < first; i += 64) out_tok[(size_t)step * (k + 1) + i] = dt[i];
+        if (lane == 0) {
+            const int nd = draw_slots(mode);
+            Decision D{}, D2{};
+            D2.kind = -2;
+            if (invalid) {
+                D.kind = -1;
+                D.n = -1;
+            } else {
+                D.n = first;
+                D.pos = first;
+                if (first < k) {
+                    const float2 pt = ms[first], pd = ms[k + 1 + first];
+                    D.kind = mode == 0 ? 1 : 2;
+                    D.prow = first;
+                    D.qrow = first;
+                    D.Tp = Tr; D.mp = pt.x; D.sp = pt.y;
+                    D.Tq = Tr; D.mq = pd.x; D.sq = pd.y;
+                    D.qs = f_q;
+                    D.u = u_res[step];
+                    D.fallback = mode == 0 ? 1 : 2;
+                    if (mode == 1 && first == k - 1) {  // the reference's bonus after the residual
+                        const float2 pk = ms[k];
+                        D2.kind = 0;
+                        D2.n = first;
+                        D2.pos = first + 1;
+                        D2.prow = k;
+                        D2.Tp = T; D2.mp = pk.x; D2.sp = pk.y;
+                        D2.Tq = T; D2.mq = 0.f; D2.sq = 1.f;
+                        D2.u = u_bonus[step];
+                        D2.fallback = 2;
+                    }
+                } else {
+                    const float2 pt = ms[k];
+                    D.kind = 0;
+                    D.prow = k;
+                    D.qrow = 0;
+                    D.Tp = T; D.mp = pt.x; D.sp = pt.y;
+                    D.Tq = T; D.mq = 0.f; D.sq = 1.f; D.qs = 0.f;
+                    D.u = u_bonus[step];
+                    D.fallback = 2;
+                }
+            }
+            s_dec[0] = D;
+            s_dec[1] = D2;
+            if (publish) {
+                out_n[step] = D.n;
+                dec[(size_t)step * nd] = D;
+                if (nd > 1) dec[(size_t)step * nd + 1] = D2;
+            }
         }
     }
-    // accepted drafts
-    for (int i = lane; i < first; i += 64) out_tok[(size_t)step * (k + 1) + i] = dt[i];
-    if (lane != 0) return;
-    const int nd = draw_slots(mode);
-    Decision D{}, D2{};
-    D2.kind = -2;
-    if (invalid) {
-        D.kind = -1;
-        D.n = -1;
-        out_n[step] = -1;
-        dec[(size_t)step * nd] = D;
-        if (nd > 1) dec[(size_t)step * nd + 1] = D2;
-        return;
-    }
-    D.n = first;
-    D.pos = first;
-    if (first < k) {
-        const float2 pt = ms[first], pd = ms[k + 1 + first];
-        D.kind = mode == 0 ? 1 : 2;
-        D.prow = first;
-        D.qrow = first;
-        D.Tp = Tr; D.mp = pt.x; D.sp = pt.y;
-        D.Tq = Tr; D.mq = pd.x; D.sq = pd.y;
-        D.qs = f_q;
-        D.u = u_res[step];
-        D.fallback = mode == 0 ? 1 : 2;
-        if (mode == 1 && first == k - 1) {  // the reference's bonus after the residual
-            const float2 pk = ms[k];
-            D2.kind = 0;
-            D2.n = first;
-            D2.pos = first + 1;
-            D2.prow = k;
-            D2.Tp = T; D2.mp = pk.x; D2.sp = pk.y;
-            D2.Tq = T; D2.mq = 0.f; D2.sq = 1.f;
-            D2.u = u_bonus[step];
-            D2.fallback = 2;
-        }
-    } else {
-        const float2 pt = ms[k];
-        D.kind = 0;
-        D.prow = k;
-        D.qrow = 0;
-        D.Tp = T; D.mp = pt.x; D.sp = pt.y;
-        D.Tq = T; D.mq = 0.f; D.sq = 1.f; D.qs = 0.f;
-        D.u = u_bonus[step];
-        D.fallback = 2;
-    }
-    out_n[step] = first;
-    dec[(size_t)step * nd] = D;
-    if (nd > 1) dec[(size_t)step * nd + 1] = D2;
+    __syncthreads();
 }
 
 // Sampling weights of the PER x NT entries of chunk c: thread t holds entries
@@ -389,15 +397,26 @@ __device__ void chunk_scan(const Decision &D, const float *lt, const float *ld, 
     __syncthreads();
 }
 
-// csum[step][slot][c] = sum of w over chunk c: the sequential sum of its
-// round totals (grid z = draw slot).
-__global__ __launch_bounds__(NT) void chunk_sum_kernel(const float *__restrict__ tgt, const float *__restrict__ drf,
-                                                       int k, int V, const Decision *__restrict__ dec, int nchunk,
-                                                       float *__restrict__ csum) {
+// The decision of verify step `step` (decide_block, computed by every
+// workgroup; the first one publishes it), then csum[step][slot][c] = the
+// sum of w over chunk c: the sequential sum of its round totals (grid: x
+// chunk, y step, z draw slot).
+__global__ __launch_bounds__(NT) void decide_sum_kernel(const float *__restrict__ tgt, const float *__restrict__ drf,
+                                                        const int32_t *__restrict__ draft_tok, int k, int V, float T,
+                                                        const float *__restrict__ u_acc,
+                                                        const float *__restrict__ u_res,
+                                                        const float *__restrict__ u_bonus, int mode,
+                                                        const float2 *__restrict__ part, int nchunk,
+                                                        int32_t *__restrict__ out_tok, int32_t *__restrict__ out_n,
+                                                        Decision *__restrict__ dec, float *__restrict__ csum) {
     __shared__ float sh[PER * 4];
+    __shared__ float2 ms[DECIDE_MAX_ROWS];
+    __shared__ Decision s_dec[2];
     const int c = blockIdx.x, step = blockIdx.y;
+    decide_block(tgt, drf, draft_tok, k, V, T, u_acc, u_res, u_bonus, mode, part, nchunk, step, gridDim.y,
+                 c == 0 && blockIdx.z == 0, out_tok, out_n, dec, ms, s_dec);
     const size_t slot = (size_t)step * gridDim.z + blockIdx.z;
-    const Decision D = dec[slot];
+    const Decision D = s_dec[blockIdx.z];
     if (D.kind < 0) return;
     const float *lt = tgt + ((size_t)step * (k + 1) + D.prow) * V;
     const float *ld = D.kind == 1 ? drf + ((size_t)step * k + D.qrow) * V : nullptr;
@@ -683,10 +702,8 @@ hipError_t launch_spec_accept(const float *tgt, const float *drf, const int32_t 
                                                                       drf, Tr, V, nc, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    decide_kernel<<<steps, 64, 0, st>>>(tgt, drf, draft_tok, k, V, T, u_acc, u_res, u_bonus, mode, part, nc,
-                                        out_tok, out_n, dec);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    chunk_sum_kernel<<<dim3(nc, steps, nd), NT, 0, st>>>(tgt, drf, k, V, dec, nc, csum);
+    decide_sum_kernel<<<dim3(nc, steps, nd), NT, 0, st>>>(tgt, drf, draft_tok, k, V, T, u_acc, u_res, u_bonus,
+                                                          mode, part, nc, out_tok, out_n, dec, csum);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     sample_kernel<<<dim3(steps, nd), NT, 0, st>>>(tgt, drf, k, V, dec, nc, csum, out_tok);
     return hipGetLastError();
