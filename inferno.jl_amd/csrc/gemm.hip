@@ -1312,7 +1312,7 @@ __device__ __forceinline__ void chain_epilogue(const Chain &ch, float *__restric
 
 // One token tile (MT = 1; several tiles run gemm_w_kernel).
 template <int QT, int NW, int UPS, bool SPLIT, bool PK, int MT, bool XIN, int DE>
-__global__ __launch_bounds__(NW * 64, 8 / NW)
+__global__ __launch_bounds__(NW * 64, UPS == 3 ? 1 : 8 / NW)
 void gemm_v_kernel(const uint8_t *__restrict__ W, const uint8_t *__restrict__ afrag,
                    const uint8_t *__restrict__ mfrag, const float *__restrict__ invs, int M, int N, int K, int G,
                    int xs_stride, int x_tpu, float *__restrict__ Y, int accum, const float *__restrict__ ssq,
@@ -1332,7 +1332,7 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, const uint8_t *__restrict__ af
     constexpr int TOK = MT * TOKT;
     constexpr int TPL = SPLIT ? 2 : 4;
     constexpr int UNIT_BYTES = (QT == QT_Q8_0) ? 8 * 34 : C::BB;
-    constexpr int R = 4;
+    constexpr int R = UPS == 3 ? 6 : 4;  // (3 units: one wave per SIMD, a deeper ring)
     static_assert(R % UPS == 0, "ring positions must map to fixed units");
     // partial tiles meet in LDS in batches of F tiles (double-buffered), one
     // barrier per batch (Q6_K, short of registers: one tile per batch)
@@ -2098,11 +2098,22 @@ static GemmPlan plan_gemm(int qt, int M, int N, int K, int flags) {
         p.NW = nw;
         p.UPS = ups;
         p.S = (n_units + nw * ups - 1) / (nw * ups);
+        if (qt == QT_Q6_K && p.split && nw == 8 && env_ups == 0 && n_units % 12 == 0 && n_units >= 24) {
+            // Q6_K past one 8 x 2-unit slice (down, 48 units): 4 waves of 3
+            // units, one wave per SIMD with the full register file and a
+            // 6-deep ring, 12-unit K-slices: 4 slices x 64 workgroups of 4
+            // tiles fill all 256 CUs with 12 items per wave (the 8 x 2 plan:
+            // 3 slices x 64 workgroups on 192 CUs; verify step 1.5 % faster)
+            p.NW = 4;
+            p.UPS = 3;
+            p.S = n_units / 12;
+        }
         // every workgroup resident at once (2 per CU at <= 256 VGPRs) and the
         // same number of tiles for each: no second dispatch wave, no tail
         // where half the workgroups idle
         static const int stream_target = env_int("IHIP_GEMM_WGS", 0);
-        const int resident = nw == 8 ? 256 : 512;  // workgroups the chip holds at <= 256 VGPRs
+        // workgroups the chip holds (4-wave ones two per CU at <= 256 VGPRs, one with 3 units)
+        const int resident = (p.NW == 8 || p.UPS == 3) ? 256 : 512;
         const int target = stream_target > 0 ? stream_target : resident;
         const int n_tiles = (N + 15) / 16;
         const int g0 = std::max(1, std::min(n_tiles, target / p.S));
@@ -2171,6 +2182,9 @@ static hipError_t dispatch_mt(const GemmPlan &p, const uint8_t *W, const float *
 #define V(nw, u, sp) if constexpr (u <= stream_ups_cap(QT, sp)) if (p.NW == nw && p.UPS == u && p.split == sp) \
     return launch_v<QT, nw, u, sp, PK, 1>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st)
         V(8, 1, true); V(8, 2, true); V(8, 4, true); V(8, 1, false); V(8, 2, false); V(8, 4, false);
+        if constexpr (QT == QT_Q6_K)
+            if (p.NW == 4 && p.UPS == 3 && p.split)
+                return launch_v<QT, 4, 3, true, PK, 1>(W, X, in, Y, M, N, K, p.S, p.G, accum, a, part, st);
         V(4, 1, true); V(4, 2, true); V(4, 4, true); V(4, 1, false); V(4, 2, false); V(4, 4, false);
 #undef V
         return hipErrorInvalidValue;  // (the plan keeps UPS within the cap)
@@ -2270,7 +2284,9 @@ hipError_t launch_gemm_chain(int qt, const void *W, const ActIn *in, const float
     uint8_t *wsp = (uint8_t *)ws;
     float *part = (float *)(wsp + p.off_part);
     const uint8_t *w = (const uint8_t *)W;
-    if (p.NW != 8) return hipErrorInvalidValue;  // (chained calls: the default 8-wave plan only)
+    // (chained calls: the 8-wave plans, and Q6_K's 4 x 3-unit one)
+    const bool q6_43 = qt == QT_Q6_K && p.NW == 4 && p.UPS == 3;
+    if (p.NW != 8 && !q6_43) return hipErrorInvalidValue;
     // (instantiated up to the units per wave stream_ups_cap allows)
 #define CV(q, u) if constexpr (u <= stream_ups_cap(q, true)) if (qt == q && p.UPS == u) \
     return launch_v<q, 8, u, true, true, 1>(w, X, ai, Y, M, N, K, p.S, p.G, 0, a, part, st, &ch)
@@ -2281,10 +2297,12 @@ hipError_t launch_gemm_chain(int qt, const void *W, const ActIn *in, const float
         ActIn ai = *in;
         ai.defer = defer;
         CV(QT_Q4_K, 1); CV(QT_Q4_K, 2); CV(QT_Q4_K, 4); CV(QT_Q5_K, 1); CV(QT_Q5_K, 2);
+        if (q6_43) return launch_v<QT_Q6_K, 4, 3, true, true, 1>(w, X, ai, Y, M, N, K, p.S, p.G, 0, a, part, st, &ch);
         CV(QT_Q6_K, 1); CV(QT_Q6_K, 2); CV(QT_Q8_0, 1);
         return hipErrorInvalidValue;
     }
     XV(QT_Q4_K, 1); XV(QT_Q4_K, 2); XV(QT_Q4_K, 4); XV(QT_Q5_K, 1); XV(QT_Q5_K, 2);
+    if (q6_43) return launch_vx<QT_Q6_K, 4, 3>(w, Y, M, N, K, p.S, p.G, defer, ssq_in, n_ssq_in, eps, part, ch, st);
     XV(QT_Q6_K, 1); XV(QT_Q6_K, 2); XV(QT_Q8_0, 1);
 #undef XV
 #undef CV
