@@ -456,6 +456,50 @@ def profile_m5(ih, reps: int = 5):
     log(f"profile_m5: {reps} x (qkv, o, gate/up, down) at M = 5, stream_read 57 MB and 510 MB, 3 x ihip_add")
 
 
+def profile_chain(ih, reps: int = 5):
+    """For rocprofv3 --pmc / --kernel-trace: one config-4 layer of the chained
+    step (M = 5), each call launched `reps` times in a row with the buffers
+    the step uses: [q; k; v] with its input stage (RMSNorm) and STATS
+    epilogue, o (chained input, RESID epilogue), [gate; up] (chained input,
+    GATE epilogue), down (chained input, deferred partials); then the
+    plain-read probe over 57,196,544 B and 510,504,960 B and the calibration
+    kernel (ihip_add over 64 Mi floats), as profile_m5."""
+    import torch
+    F, q = ih.formats, ih.quantized_kernels
+    model = Model(ih, 1, keep_gguf=0, gated=True)
+    step = ChainStep(ih, model, 5, 4, 0.8)
+    step.forward()
+    torch.cuda.synchronize()
+    lw = model.layers[0]
+    chain = ih.gemm_q_chain
+    fl = ih.GEMM_F32 | ih.GEMM_PACKED
+    for _ in range(reps):
+        chain(F.Q4_K, lw["qkv"], NQ + 2 * NKV, H, 5, x=step.x, act=ih.ACT_RMSNORM, norm_w=lw["attn_norm"],
+              ws=step.ws, cout=step.qkv_out)
+    for _ in range(reps):
+        chain(F.Q4_K, lw["o"], H, NQ, 5, cin=step.o_in, ws=step.ws_o, cout=step.o_out[0])
+    for _ in range(reps):
+        chain(F.Q4_K, lw["gu"], 2 * FF, H, 5, ws=step.ws, cin=step.gu_in, cout=step.gu_out)
+    for _ in range(reps):
+        chain(F.Q6_K, lw["down"], H, FF, 5, cin=step.down_in, flags=fl | ih.GEMM_DEFER, ws=step.ws_down)
+    torch.cuda.synchronize()
+    sink = torch.zeros(2048, dtype=torch.int32, device="cuda")
+    for nb in (57_196_544, 510_504_960):
+        buf = torch.ones(nb // 4, dtype=torch.float32, device="cuda").view(torch.uint8)
+        for _ in range(reps):
+            q.stream_read(buf, out=sink)
+        torch.cuda.synchronize()
+        del buf
+    n = 64 << 20
+    a = torch.ones(n, device="cuda")
+    b = torch.ones(n, device="cuda")
+    for _ in range(3):
+        q.add_(a, b)
+    torch.cuda.synchronize()
+    log(f"profile_chain: {reps} x (qkv, o, gate/up, down) chained at M = 5, stream_read 57 MB and 510 MB, "
+        "3 x ihip_add")
+
+
 def profile_tall(ih, reps: int = 5):
     """For rocprofv3 --pmc: the M = 64 (config 5) half-precision matmuls of
     one layer, each launched `reps` times: Q4_K [gate; up] 24576x4096 with
@@ -942,6 +986,9 @@ def main():
     ap.add_argument("--profile-m5", action="store_true",
                     help="only run one layer's four M = 5 matmuls five times each, the plain-read probe and the "
                          "traffic calibration kernel (for rocprofv3 --pmc)")
+    ap.add_argument("--profile-chain", action="store_true",
+                    help="only run one chained layer's four M = 5 calls five times each, the plain-read probe and "
+                         "the traffic calibration kernel (for rocprofv3 --pmc)")
     ap.add_argument("--profile-tall", action="store_true",
                     help="only run the M = 64 gate/up and down matmuls five times each (for rocprofv3 --pmc)")
     ap.add_argument("--configs", type=str, default="",
@@ -964,6 +1011,9 @@ def main():
         return
     if args.profile_m5:
         profile_m5(ih)
+        return
+    if args.profile_chain:
+        profile_chain(ih)
         return
     if args.configs:
         want = [c.strip() for c in args.configs.split(",") if c.strip()]
