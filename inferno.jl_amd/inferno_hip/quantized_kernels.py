@@ -243,6 +243,40 @@ def chain_out(epi: int, y, consumer_qtype: int = Q4_K, operand=None, tile_sum=No
     return co
 
 
+def _check_chain_buffers(m: int, n: int, k: int, cin, cout):
+    """Sizes of the chain descriptors' buffers against the call shape (the
+    descriptors carry raw pointers; chain_in / chain_out keep the tensors):
+    the consumer reads chain_operand_bytes(k) operand bytes and k / 256 *
+    tiles_per_unit tile sums; the producer writes y [m, width] (width = n, or
+    n / 2 for EPI_GATE), and for the width its operand covers (stat_rows for
+    EPI_STATS) the operand, its tile sums and sums of squares [tiles, 8] and
+    reads norm_w."""
+    import torch
+    if cin is not None:
+        operand, tile_sum, tile_ssq = cin._refs
+        tiles = k // 256 * cin.tiles_per_unit
+        check_tensor(operand, "cin operand", torch.uint8, min_numel=chain_operand_bytes(k))
+        if tile_sum is not None and tile_sum.shape[1] < tiles:
+            raise ValueError(f"cin tile_sum must be [8, >= {tiles}]")
+        if tile_ssq is not None:
+            check_tensor(tile_ssq, "cin tile_ssq", torch.float32, (None, 8))
+    if cout is not None:
+        y, operand, tile_sum, norm_w, tile_ssq = cout._refs
+        width = n // 2 if cout.epi == EPI_GATE else n
+        if y.shape[0] < m or y.shape[1] < width:
+            raise ValueError(f"cout y must be [>= {m}, >= {width}]")
+        kn = cout.stat_rows if cout.epi == EPI_STATS else width
+        tiles = kn // 8 if cout.epi == EPI_GATE else kn // 16
+        if operand is not None:
+            check_tensor(operand, "cout operand", torch.uint8, min_numel=chain_operand_bytes(kn))
+        if tile_sum is not None and tile_sum.shape[1] < tiles:
+            raise ValueError(f"cout tile_sum must be [8, >= {tiles}]")
+        if tile_ssq is not None:
+            check_tensor(tile_ssq, "cout tile_ssq", torch.float32, min_numel=tiles * 8)
+        if norm_w is not None:
+            check_tensor(norm_w, "cout norm_w", torch.float32, min_numel=kn)
+
+
 def gemm_q_chain(qtype: int, w_packed, n: int, k: int, m: int, x=None, act: int = ACT_PLAIN, norm_w=None,
                  eps: float = 1e-6, add=None, cin=None, cout=None, flags: int = GEMM_F32 | GEMM_PACKED, ws=None,
                  stream=None):
@@ -255,11 +289,15 @@ def gemm_q_chain(qtype: int, w_packed, n: int, k: int, m: int, x=None, act: int 
     if (x is None) == (cin is None):
         raise ValueError("pass exactly one of x / cin")
     _check_weights(qtype, w_packed, n, k, GEMM_PACKED)
+    _check_chain_buffers(m, n, k, cin, cout)
     gi = None
     if x is not None:
         check_tensor(x, "x", torch.float32, contiguous=False)
-        if x.dim() != 2 or x.stride(1) != 1 or x.shape[0] < m:
-            raise ValueError("x must be [M, K] float32 with unit column stride")
+        width = 2 * k if act == ACT_SILU_MUL else k
+        if x.dim() != 2 or x.stride(1) != 1 or x.shape[0] < m or x.shape[1] < width:
+            raise ValueError(f"x must be [M, >= {width}] float32 with unit column stride")
+        if act == ACT_RMSNORM and norm_w is not None:
+            check_tensor(norm_w, "norm_w", torch.float32, min_numel=k)
         gi = _lib.GemmInput(_ptr(x), x.stride(0), act, None if norm_w is None else _ptr(norm_w), eps,
                             None if add is None else add[0], 0 if add is None else add[1],
                             0 if add is None else add[2])

@@ -225,5 +225,24 @@ def test_chain_argument_checks(ih):
     with pytest.raises(ih.HipError):  # unknown consumer layout
         ih.gemm_q_chain(F.Q4_K, p, 256, 256, 5, x=torch.zeros((5, 256), device="cuda"),
                         cout=ih.chain_out(ih.EPI_STATS, y, 99, op, ts, stat_rows=256))
+    # buffers smaller than the call shape: the wrapper refuses before the C ABI
+    x5 = torch.zeros((5, 256), device="cuda")
+    with pytest.raises(ValueError, match="x must be"):
+        ih.gemm_q_chain(F.Q4_K, p, 256, 256, 5, x=x5[:, :128], cout=ih.chain_out(ih.EPI_STORE, y))
+    with pytest.raises(ValueError, match="cout y"):
+        ih.gemm_q_chain(F.Q4_K, p, 256, 256, 5, x=x5, cout=ih.chain_out(ih.EPI_STORE, y[:5, :128]))
+    with pytest.raises(ValueError, match="cin operand"):
+        ih.gemm_q_chain(F.Q4_K, p, 256, 256, 5, cin=ih.chain_in(op[:64], ts, 16), cout=ih.chain_out(ih.EPI_STORE, y))
+    with pytest.raises(ValueError, match="cin tile_sum"):
+        ih.gemm_q_chain(F.Q4_K, p, 256, 256, 5, cin=ih.chain_in(op, ts[:, :4].contiguous(), 16),
+                        cout=ih.chain_out(ih.EPI_STORE, y))
+    with pytest.raises(ValueError, match="cout tile_ssq"):
+        ih.gemm_q_chain(F.Q4_K, p, 256, 256, 5, x=x5,
+                        cout=ih.chain_out(ih.EPI_STATS, y, F.Q4_K, op, ts, tile_ssq=torch.zeros(8, device="cuda"),
+                                          stat_rows=256))
+    with pytest.raises(ValueError, match="cout norm_w"):
+        ih.gemm_q_chain(F.Q4_K, p, 256, 256, 5, x=x5,
+                        cout=ih.chain_out(ih.EPI_STATS, y, F.Q4_K, op, ts, norm_w=torch.ones(128, device="cuda"),
+                                          stat_rows=256))
     assert L.ihip_pack_weights_gated(F.Q4_K, p.data_ptr(), p.data_ptr(), 12, 256, None) == -22  # F % 8
     assert ih.chain_operand_bytes(4096) == 16 * (8192 + 1024)
