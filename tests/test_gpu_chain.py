@@ -246,3 +246,38 @@ def test_chain_argument_checks(ih):
                                           stat_rows=256))
     assert L.ihip_pack_weights_gated(F.Q4_K, p.data_ptr(), p.data_ptr(), 12, 256, None) == -22  # F % 8
     assert ih.chain_operand_bytes(4096) == 16 * (8192 + 1024)
+
+
+@pytest.mark.parametrize("qt2", F.QTYPES)
+@pytest.mark.parametrize("M", [3, 8])
+def test_chain_ragged_rows(ih, M, qt2):
+    """Row counts that end inside a 16-row tile and tile counts that do not
+    divide over the workgroups: a STATS producer of 1000 rows (operand of
+    its first 768) feeding consumers of 1000 and 200 rows (the last
+    workgroups hold fewer tiles, the last tile 8 rows), against the oracle
+    and the classic call on the same rows."""
+    import torch
+    N1, K1, S = 1000, 512, 768
+    w1 = synth.matrix(F.Q4_K, N1, K1, synth.stream_for(6, "ch.rag1"))
+    p1 = ih.pack_weights(F.Q4_K, _dev(w1), N1, K1)
+    rng = np.random.default_rng(40 + M)
+    x = rng.standard_normal((M, K1)).astype(np.float32)
+    y1 = torch.zeros((M, N1), device="cuda")
+    op, ts, _ = ih.chain_buffers(S)
+    ih.gemm_q_chain(F.Q4_K, p1, N1, K1, M, x=_dev(x), cout=ih.chain_out(ih.EPI_STATS, y1, qt2, op, ts, stat_rows=S))
+    torch.cuda.synchronize()
+    g1 = _h(y1)
+    assert rel_l2(g1, O.gemv_f64(F.Q4_K, w1, x, M, N1, K1)) <= 1e-5
+    assert _sums_ok(_h(ts), g1, M, S // 16)
+    for N2 in (1000, 200):
+        w2 = synth.matrix(qt2, N2, S, synth.stream_for(7, f"ch.rag2.{qt2}.{N2}"))
+        p2 = ih.pack_weights(qt2, _dev(w2), N2, S)
+        y2 = torch.full((M, N2 + 8), 7.0, device="cuda")  # 8 columns past N2 must stay untouched
+        ih.gemm_q_chain(qt2, p2, N2, S, M, cin=ih.chain_in(op, ts, 16),
+                        cout=ih.chain_out(ih.EPI_STORE, y2[:, :N2]))
+        torch.cuda.synchronize()
+        g2 = _h(y2)
+        assert np.all(g2[:, N2:] == 7.0), (M, qt2, N2)
+        assert rel_l2(g2[:, :N2], O.gemv_f64(qt2, w2, g1[:, :S], M, N2, S)) <= 1e-5, (M, qt2, N2)
+        classic = ih.gemm_q_ex(qt2, p2, y1[:, :S], N2, S, flags=FL)
+        assert rel_l2(g2[:, :N2], _h(classic)) <= 1e-6, (M, qt2, N2)
