@@ -29,7 +29,7 @@ def ih():
 
 def _dev(a):
     import torch
-    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return torch.from_numpy(np.array(a, order="C")).cuda()  # (a writable copy: some inputs are read-only views)
 
 
 def _pad4(L):
