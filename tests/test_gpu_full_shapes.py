@@ -208,7 +208,7 @@ def _run_chain_step_with_checks(ih, B, model, step, chk, fold_chk):
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("M", [1, 5, 8])
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 8])  # the token counts of configs[3]
 def test_config4_chained_step(ih, bench, M):
     """configs[3] through the chained composition the benchmark times
     (bench.ChainStep: one input stage per layer), two real layers and the
@@ -294,7 +294,7 @@ def test_config3_lm_head_shapes(ih):
 
 # ----------------------------------------------------------------- config 4
 
-@pytest.mark.parametrize("M", [1, 5, 8])
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 8])  # the token counts of configs[3]
 def test_config4_verify_step(ih, bench, M):
     """configs[3] at hidden 4096 with two real layers and the 151936 x 4096
     Q6_K head, composed by bench.VerifyStep (fp32-accurate), every operation
