@@ -281,3 +281,39 @@ def test_chain_ragged_rows(ih, M, qt2):
         assert rel_l2(g2[:, :N2], O.gemv_f64(qt2, w2, g1[:, :S], M, N2, S)) <= 1e-5, (M, qt2, N2)
         classic = ih.gemm_q_ex(qt2, p2, y1[:, :S], N2, S, flags=FL)
         assert rel_l2(g2[:, :N2], _h(classic)) <= 1e-6, (M, qt2, N2)
+
+
+@pytest.mark.parametrize("qt", [F.Q4_K, F.Q5_K])
+@pytest.mark.parametrize("M,N", [(3, 4096 + 2048), (8, 4096 + 1000)])
+def test_large_statistics_producer(ih, qt, M, N):
+    """[q; k; v]-shaped statistics producers with more tiles than CUs (256
+    statistics tiles and a tail of 128 or 63, the last one ragged; the
+    output starts as NaN, so every row must be written): every row against
+    the oracle and the classic call, the operand through an o-shaped
+    consumer."""
+    import torch
+    K, S = 4096, 4096
+    w = synth.matrix(qt, N, K, synth.stream_for(8, f"ch.split.{qt}.{N}"))
+    p = ih.pack_weights(qt, _dev(w), N, K)
+    rng = np.random.default_rng(60 + M)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    y = torch.full((M, N), float("nan"), device="cuda")
+    op, ts, _ = ih.chain_buffers(S)
+    ih.gemm_q_chain(qt, p, N, K, M, x=_dev(x), act=ih.ACT_RMSNORM, norm_w=_dev(nw), eps=EPS,
+                    cout=ih.chain_out(ih.EPI_STATS, y, F.Q4_K, op, ts, stat_rows=S))
+    torch.cuda.synchronize()
+    gy = _h(y)
+    assert np.all(np.isfinite(gy))
+    ref = O.gemv_f64(qt, w, _rms(x, nw), M, N, K)
+    assert rel_l2(gy, ref) <= 1e-5, (qt, M, N)
+    assert rel_l2(gy[:, S:], ref[:, S:]) <= 1e-5, (qt, M, N)  # the split tail alone
+    classic = ih.gemm_q_ex(qt, p, _dev(x), N, K, act=ih.ACT_RMSNORM, norm_w=_dev(nw), eps=EPS, flags=FL)
+    assert rel_l2(gy, _h(classic)) <= 1e-6, (qt, M, N)
+    assert _sums_ok(_h(ts), gy, M, S // 16)
+    wo = synth.matrix(F.Q4_K, 512, S, synth.stream_for(9, "ch.split.o"))
+    po = ih.pack_weights(F.Q4_K, _dev(wo), 512, S)
+    yo = torch.zeros((M, 512), device="cuda")
+    ih.gemm_q_chain(F.Q4_K, po, 512, S, M, cin=ih.chain_in(op, ts, 16), cout=ih.chain_out(ih.EPI_STORE, yo))
+    torch.cuda.synchronize()
+    assert rel_l2(_h(yo), O.gemv_f64(F.Q4_K, wo, gy[:, :S], M, 512, S)) <= 1e-5
