@@ -267,10 +267,14 @@ __device__ void pick_bucket(const uint32_t *hist, const unsigned long long *mass
     }
 }
 
+// The B passes read only the elements of bucket zb: when it holds at most
+// SK_MAX of them, one more pass gathers their keys and values into LDS
+// (ck, cz; any order: the passes only count) and the B passes run there
+// instead of over the row.
 template <bool MASS>
 __device__ void select_threshold(const float *__restrict__ row, int V, int nround, float T, float zmax, float S,
                                  unsigned long long target, uint32_t *hist, unsigned long long *mass, uint32_t *sel,
-                                 unsigned long long *selm, Select &R) {
+                                 unsigned long long *selm, uint32_t *ck, float *cz, int *ncnt, Select &R) {
     const int t = threadIdx.x;
     R.zb = 255u;
     R.tau = 0u;
@@ -301,6 +305,7 @@ __device__ void select_threshold(const float *__restrict__ row, int V, int nroun
     __syncthreads();
     const uint32_t zb = sel[0];
     const unsigned long long aboveA = selm[0];
+    const uint32_t nzb = hist[zb];
     __syncthreads();
     if (aboveA == ~0ull) {
         R.all = true;
@@ -308,6 +313,22 @@ __device__ void select_threshold(const float *__restrict__ row, int V, int nroun
     }
     R.rem -= aboveA;
     R.zb = zb;
+    const bool gathered = nzb <= (uint32_t)SK_MAX;
+    if (gathered) {
+        if (t == 0) *ncnt = 0;
+        __syncthreads();
+        for_rounds(row, V, nround, T, [&](const float (&z)[4], bool in, int) {
+            if (!in) return;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (zbin(z[e], zmax) == zb) {
+                    const int p = atomicAdd(ncnt, 1);  // < nzb: the predicate pass A counted
+                    ck[p] = okey(z[e]);
+                    cz[p] = z[e];
+                }
+        });
+        __syncthreads();
+    }
     // passes B: the exact key inside bucket zb, 8 bits a pass from the top
     uint32_t prefix = 0, pmask = 0;
     for (int shift = 24; shift >= 0; shift -= 8) {
@@ -316,17 +337,27 @@ __device__ void select_threshold(const float *__restrict__ row, int V, int nroun
             if (MASS) mass[t] = 0;
         }
         __syncthreads();
-        for_rounds(row, V, nround, T, [&](const float (&z)[4], bool in, int) {
-            if (!in) return;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t k = okey(z[e]);
-                if ((k & pmask) != prefix || zbin(z[e], zmax) != zb) continue;
+        if (gathered) {
+            for (int i = t; i < (int)nzb; i += SNT) {
+                const uint32_t k = ck[i];
+                if ((k & pmask) != prefix) continue;
                 const uint32_t b = (k >> shift) & 255u;
                 atomicAdd(&hist[b], 1u);
-                if (MASS) atomicAdd(&mass[b], mass_of(z[e]));
+                if (MASS) atomicAdd(&mass[b], mass_of(cz[i]));
             }
-        });
+        } else {
+            for_rounds(row, V, nround, T, [&](const float (&z)[4], bool in, int) {
+                if (!in) return;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t k = okey(z[e]);
+                    if ((k & pmask) != prefix || zbin(z[e], zmax) != zb) continue;
+                    const uint32_t b = (k >> shift) & 255u;
+                    atomicAdd(&hist[b], 1u);
+                    if (MASS) atomicAdd(&mass[b], mass_of(z[e]));
+                }
+            });
+        }
         __syncthreads();
         pick_bucket<MASS>(hist, mass, R.rem, sel, selm, true);
         __syncthreads();
@@ -370,6 +401,7 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
     __shared__ int s_cidx[SK_MAX];
     __shared__ float s_cp[SK_MAX];
     __shared__ int s_sort[SK_MAX];
+    __shared__ int s_ncnt;
     const int row = blockIdx.x, t = threadIdx.x;
     const float *Lr = L + (size_t)row * V;
     const int nround = (V + SROUND - 1) / SROUND;
@@ -411,7 +443,8 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
         });
         const float zm = block_max(lmax, s_redf);
         Select R;
-        select_threshold<false>(Lr, V, nround, invT, zm, 1.f, (unsigned long long)K, s_hist, s_mass, s_sel, s_selm, R);
+        select_threshold<false>(Lr, V, nround, invT, zm, 1.f, (unsigned long long)K, s_hist, s_mass, s_sel, s_selm,
+                                (uint32_t *)s_cidx, s_cp, &s_ncnt, R);
         const uint32_t zb = R.zb, tau = R.tau;
         const int rem = (int)R.rem;  // elements equal to tau that are kept, lowest index first
         int run_kept = 0, run_eq = 0;
@@ -567,7 +600,8 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
         const float tp = fmaxf(a.top_p, 0.f) * 1099511627776.0f;
         const unsigned long long target = tp < 1.0f ? 1ull : (unsigned long long)ceilf(tp);
         Select R;
-        select_threshold<true>(Lr, V, nround, invT, zmax, S, target, s_hist, s_mass, s_sel, s_selm, R);
+        select_threshold<true>(Lr, V, nround, invT, zmax, S, target, s_hist, s_mass, s_sel, s_selm,
+                               (uint32_t *)s_cidx, s_cp, &s_ncnt, R);
         if (!R.all) {
             zb = R.zb;
             tau = R.tau;
