@@ -33,6 +33,7 @@ constexpr int SNW = SNT / 64;
 constexpr int SROUND = 4 * SNT;
 constexpr int SK_MAX = 4096;
 constexpr int SMAX_ROUNDS = 1024;  // V <= 4194304
+constexpr int SPART_ROUNDS = 64;   // plain draws by per-wave parts: V <= 262144
 
 struct SampleArgs {
     float T;       // 0: argmax
@@ -402,6 +403,7 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
     __shared__ float s_cp[SK_MAX];
     __shared__ int s_sort[SK_MAX];
     __shared__ int s_ncnt;
+    __shared__ float s_pm[SPART_ROUNDS][SNW], s_ps[SPART_ROUNDS][SNW];
     const int row = blockIdx.x, t = threadIdx.x;
     const float *Lr = L + (size_t)row * V;
     const int nround = (V + SROUND - 1) / SROUND;
@@ -575,21 +577,63 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
         return;
     }
 
-    // ---- whole-row path: softmax statistics in one online pass
+    // ---- whole-row path: softmax statistics in one pass
     float zmax = -__builtin_huge_valf(), S = 0.f;
-    for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int) {
-        if (!in) return;
+    // plain draws (no top-p, no min-p) over at most SPART_ROUNDS rounds:
+    // every wave keeps the (max, sum exp(z - max)) of its part of each round,
+    // so the rounds' sums for the draw need no second pass over the row
+    bool by_parts = a.top_p >= 1.0f && a.min_p <= 0.f && nround <= SPART_ROUNDS;
+    if (by_parts) {
+        const int w = t >> 6;
+        for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int r) {
+            float m = -__builtin_huge_valf();
+            if (in)
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            if (z[e] > zmax) {
-                S = S * pexp(zmax - z[e]) + 1.0f;
-                zmax = z[e];
-            } else if (zmax > -__builtin_huge_valf()) {
-                S += pexp(z[e] - zmax);
+                for (int e = 0; e < 4; e++) m = fmaxf(m, z[e]);
+            m = wave_max(m);
+            float sw = 0.f;
+            if (in && m > -__builtin_huge_valf())
+#pragma unroll
+                for (int e = 0; e < 4; e++) sw += pexp(z[e] - m);
+            sw = wave_sum(sw);
+            if ((t & 63) == 0) {
+                s_pm[r][w] = m;
+                s_ps[r][w] = sw;
             }
-        }
-    });
-    block_ms(zmax, S, s_redf);
+        });
+        __syncthreads();
+        const int np = nround * SNW;
+        float lm = -__builtin_huge_valf();
+        for (int i = t; i < np; i += SNT) lm = fmaxf(lm, s_pm[i / SNW][i % SNW]);
+        zmax = block_max(lm, s_redf);
+        float ls = 0.f;
+        if (zmax > -__builtin_huge_valf())
+            for (int i = t; i < np; i += SNT) {
+                const float m = s_pm[i / SNW][i % SNW];
+                if (m > -__builtin_huge_valf()) ls += s_ps[i / SNW][i % SNW] * pexp(m - zmax);
+            }
+        S = block_sum(ls, s_redf);
+        // rows without a finite maximum or sum (all -Inf, NaN) take the
+        // online pass below, as every other draw does
+        by_parts = zmax > -__builtin_huge_valf() && S > 0.f && S < __builtin_huge_valf();
+    }
+    if (!by_parts) {
+        zmax = -__builtin_huge_valf();
+        S = 0.f;
+        for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int) {
+            if (!in) return;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if (z[e] > zmax) {
+                    S = S * pexp(zmax - z[e]) + 1.0f;
+                    zmax = z[e];
+                } else if (zmax > -__builtin_huge_valf()) {
+                    S += pexp(z[e] - zmax);
+                }
+            }
+        });
+        block_ms(zmax, S, s_redf);
+    }
     // kept: above_threshold(zb, tau, tie_lim); everything without top-p
     uint32_t zb = 256u, tau = 0u;
     int tie_lim = V;
@@ -690,9 +734,19 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
         }
         return p;
     };
-    // the draw: each round's sum (batched: one block reduction per RB
-    // rounds), the round, then the index inside it
-    for (int r0 = 0; r0 < nround; r0 += RB) {
+    // the draw: each round's sum (from the waves' parts, or batched: one
+    // block reduction per RB rounds), the round, then the index inside it
+    if (by_parts) {
+        if (t < nround) {
+            float sum = 0.f;
+            for (int w = 0; w < SNW; w++) {
+                const float m = s_pm[t][w];
+                if (m > -__builtin_huge_valf()) sum += s_ps[t][w] * pexp(m - zmax);
+            }
+            s_round[t] = sum * invS;
+        }
+    }
+    for (int r0 = 0; r0 < (by_parts ? 0 : nround); r0 += RB) {
         float part[RB];
 #pragma unroll
         for (int b = 0; b < RB; b++) {

@@ -104,6 +104,33 @@ def test_parity_full_vocab(ih, kw):
     assert bad <= 1
 
 
+def test_plain_draw_paths(ih):
+    """Plain draws (no top-p, no min-p) take their rounds' sums from
+    per-wave parts of the statistics pass up to V = 262144 and the online
+    pass beyond it or when the row has no finite maximum or sum: rows that
+    are all -Inf or hold a NaN (the reference's V - 1), two finite entries
+    among -Inf, and Gaussian rows at V = 262144 and V = 300000."""
+    V = 4096
+    a = np.full(V, -np.inf, np.float32)
+    b = np.zeros(V, np.float32)
+    b[7] = np.nan
+    c = np.full(V, -np.inf, np.float32)
+    c[100] = c[3000] = 1.0
+    us = [0.1, 0.5, 0.9]
+    assert list(_draw(ih, a, us)) == [V - 1] * 3
+    assert list(_draw(ih, b, us)) == [V - 1] * 3
+    assert list(_draw(ih, c, us)) == [100, 100, 3000]
+    rng = np.random.default_rng(11)
+    for Vb in (262144, 300000):
+        L = (3.0 * rng.standard_normal((8, Vb))).astype(np.float32)
+        u8 = rng.random(8).astype(np.float32)
+        got = _draw(ih, L, u8, temperature=0.9)
+        for r in range(8):
+            want = O.softmax_sample(L[r], float(u8[r]), temperature=0.9)
+            assert got[r] == want or _near_boundary(L[r], float(u8[r]), int(got[r]), want,
+                                                    dict(temperature=0.9)), (Vb, r, got[r], want)
+
+
 def test_topk_ties_exact(ih):
     # all equal: top_k = 5 keeps indices 0..4, token = ceil(5 u) - 1
     Z = np.zeros(4096, np.float32)
