@@ -639,6 +639,10 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
     int tie_lim = V;
     bool div_total = false;  // top-p renormalizes by the nucleus mass
     float total_p = 1.0f;
+    // rounds' sums of the final probabilities from the last pass's per-wave
+    // parts (s_ps, times parts_scale) instead of a pass of their own
+    bool round_parts = false;
+    float parts_scale = 1.0f;
     const float invS = 1.0f / S;  // (probabilities by reciprocals: within an ulp of the divisions)
     if (a.top_p < 1.0f) {
         const float tp = fmaxf(a.top_p, 0.f) * 1099511627776.0f;
@@ -682,17 +686,29 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
                 tie_lim = lim;
             }
         }
-        // mass of the nucleus, then p' = p / total
+        // mass of the nucleus, then p' = p / total (without min-p, the
+        // rounds' sums of the draw come from this pass's per-wave parts)
+        const bool parts = a.min_p <= 0.f && nround <= SPART_ROUNDS;
         float lt = 0.f;
         for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int r) {
-            if (!in) return;
+            float c = 0.f;
+            if (in)
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                if (zb == 256u || above_threshold(z[e], r * SROUND + 4 * t + e, zmax, zb, tau, tie_lim))
-                    lt += pexp(z[e] - zmax) * invS;
+                for (int e = 0; e < 4; e++)
+                    if (zb == 256u || above_threshold(z[e], r * SROUND + 4 * t + e, zmax, zb, tau, tie_lim))
+                        c += pexp(z[e] - zmax) * invS;
+            lt += c;
+            if (parts) {
+                c = wave_sum(c);
+                if ((t & 63) == 0) s_ps[r][t >> 6] = c;
+            }
         });
         total_p = block_sum(lt, s_redf);
         div_total = total_p > 0.f;
+        if (parts) {
+            round_parts = true;
+            parts_scale = div_total ? 1.0f / total_p : 1.0f;
+        }
     }
     const float inv_total = div_total ? 1.0f / total_p : 1.0f;
     auto prob = [&](float z) {
@@ -711,18 +727,29 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
         float pmax = invS;
         if (div_total) pmax = pmax * inv_total;
         thr = pmax * a.min_p;
+        const bool parts = nround <= SPART_ROUNDS;
         float lt = 0.f;
         for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int r) {
-            if (!in) return;
+            float c = 0.f;
+            if (in)
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                if (kept(z[e], r * SROUND + 4 * t + e)) {
-                    const float p = prob(z[e]);
-                    if (!(p < thr)) lt += p;
-                }
+                for (int e = 0; e < 4; e++)
+                    if (kept(z[e], r * SROUND + 4 * t + e)) {
+                        const float p = prob(z[e]);
+                        if (!(p < thr)) c += p;
+                    }
+            lt += c;
+            if (parts) {
+                c = wave_sum(c);
+                if ((t & 63) == 0) s_ps[r][t >> 6] = c;
+            }
         });
         total2 = block_sum(lt, s_redf);
         div_total2 = total2 > 0.f;
+        if (parts) {
+            round_parts = true;
+            parts_scale = div_total2 ? 1.0f / total2 : 1.0f;
+        }
     }
     const float inv_total2 = div_total2 ? 1.0f / total2 : 1.0f;
     auto final_p = [&](float z, int j) {
@@ -745,8 +772,14 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
             }
             s_round[t] = sum * invS;
         }
+    } else if (round_parts) {
+        if (t < nround) {
+            float sum = 0.f;
+            for (int w = 0; w < SNW; w++) sum += s_ps[t][w];
+            s_round[t] = sum * parts_scale;
+        }
     }
-    for (int r0 = 0; r0 < (by_parts ? 0 : nround); r0 += RB) {
+    for (int r0 = 0; r0 < (by_parts || round_parts ? 0 : nround); r0 += RB) {
         float part[RB];
 #pragma unroll
         for (int b = 0; b < RB; b++) {
