@@ -18,7 +18,11 @@
 //  * no top-k: softmax statistics by full passes; top-p finds the nucleus by
 //    a radix select over the same keys whose buckets carry the probability
 //    mass in 2^-40 fixed point (integer LDS atomics: deterministic); min-p
-//    is a threshold; the draw sums each round, picks the round, then scans it.
+//    is a threshold; the draw sums each round, picks the round, then scans
+//    it, the rounds' sums taken from per-wave parts kept by the pass before
+//    it (statistics, nucleus mass or min-p mass) where V <= 262144.
+//  * the threshold's refinement passes run over the first pass's bucket
+//    gathered into LDS when it holds at most 4096 elements.
 // Sums and scans are trees, where the reference accumulates sequentially:
 // the drawn token can differ only where u falls within rounding of a CDF
 // step.
