@@ -423,6 +423,18 @@ int ihip_spec_advance_len(int32_t *len_dev, const int32_t *n_accepted_dev,
 int ihip_sample(const float *logits_dev, int rows, int V, float T, int top_k,
                 float top_p, float min_p, const float *u_dev,
                 int32_t *out_tok_dev, void *stream);
+/* ihip_sample with a caller workspace (ihip_sample_ws_bytes; 16-byte
+ * aligned): plain draws (T > 0, no top-k, top-p or min-p: the speculative
+ * defaults) spread each row over workgroups of 4096 logits (their softmax
+ * statistics, then the draw inside the round that holds u); every other
+ * setting runs as ihip_sample. The same softmax_sample
+ * (src/ModelCPU.jl:1123-1200) and the same contract: draws match the exact
+ * cumulative distribution except within rounding of a step. */
+int ihip_sample_ws_bytes(int rows, int V, size_t *bytes);
+int ihip_sample_ex(const float *logits_dev, int rows, int V, float T, int top_k,
+                   float top_p, float min_p, const float *u_dev,
+                   int32_t *out_tok_dev, void *ws, size_t ws_bytes,
+                   void *stream);
 
 /* The penalties the generation loop applies before sampling
  * (apply_presence_penalty!, apply_repetition_penalty!,

@@ -52,6 +52,9 @@ int sample_max_v();
 int penalty_max_v();
 hipError_t launch_sample(const float *L, int rows, int V, float T, int top_k, float top_p, float min_p, const float *u,
                          int32_t *out, hipStream_t st);
+size_t sample_spread_ws(int rows, int V);
+hipError_t launch_sample_spread(const float *L, int rows, int V, float T, int top_k, float top_p, float min_p,
+                                const float *u, int32_t *out, void *ws, hipStream_t st);
 hipError_t launch_penalties(float *L, int rows, int V, const int32_t *tok, int n_tok, int64_t tok_stride,
                             float presence, float repetition, hipStream_t st);
 hipError_t launch_gaussian(uint64_t stream, int64_t n, float scale, const float *add, float *out, hipStream_t st);
@@ -852,6 +855,35 @@ int ihip_sample(const float *logits_dev, int rows, int V, float T, int top_k, fl
     if (top_p != top_p || min_p != min_p) return fail(IHIP_EINVAL, "ihip_sample: NaN top_p/min_p");
     hipError_t e = launch_sample(logits_dev, rows, V, T, top_k, top_p, min_p, u_dev, out_tok_dev, S(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_sample");
+}
+
+int ihip_sample_ws_bytes(int rows, int V, size_t *bytes) {
+    if (!bytes) return fail(IHIP_EFAULT, "ihip_sample_ws_bytes: NULL pointer");
+    if (rows < 1 || V < 4 || (V & 3) || V > sample_max_v())
+        return fail(IHIP_EINVAL, "ihip_sample_ws_bytes: rows=%d V=%d", rows, V);
+    *bytes = sample_spread_ws(rows, V);
+    return ok();
+}
+
+int ihip_sample_ex(const float *logits_dev, int rows, int V, float T, int top_k, float top_p, float min_p,
+                   const float *u_dev, int32_t *out_tok_dev, void *ws, size_t ws_bytes, void *stream) {
+    if (!logits_dev || !u_dev || !out_tok_dev || !ws) return fail(IHIP_EFAULT, "ihip_sample_ex: NULL pointer");
+    if (rows < 1 || V < 4 || (V & 3) || V > sample_max_v())
+        return fail(IHIP_EINVAL, "ihip_sample_ex: rows=%d V=%d (V a multiple of 4 in [4, %d])", rows, V,
+                    sample_max_v());
+    if (!aligned16(logits_dev) || !aligned16(ws))
+        return fail(IHIP_EINVAL, "ihip_sample_ex: logits and workspace must be 16-byte aligned");
+    if (ws_bytes < sample_spread_ws(rows, V))
+        return fail(IHIP_ENOMEM, "ihip_sample_ex: workspace %zu < %zu bytes", ws_bytes, sample_spread_ws(rows, V));
+    if (!(T >= 0.f) || T > 3.0e38f) return fail(IHIP_EINVAL, "ihip_sample_ex: temperature %g", T);
+    if (top_k < 0) return fail(IHIP_EINVAL, "ihip_sample_ex: top_k=%d", top_k);
+    if (top_k >= V) top_k = 0;
+    if (top_k > sample_max_top_k())
+        return fail(IHIP_EINVAL, "ihip_sample_ex: top_k=%d above %d (and below V)", top_k, sample_max_top_k());
+    if (top_p != top_p || min_p != min_p) return fail(IHIP_EINVAL, "ihip_sample_ex: NaN top_p/min_p");
+    hipError_t e = launch_sample_spread(logits_dev, rows, V, T, top_k, top_p, min_p, u_dev, out_tok_dev, ws,
+                                        S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_sample_ex");
 }
 
 int ihip_apply_penalties(float *logits_dev, int rows, int V, const int32_t *tok_dev, int n_tok, int64_t tok_stride,

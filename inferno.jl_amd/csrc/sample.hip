@@ -850,6 +850,111 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
     }
 }
 
+// (max, sum exp(z - max)) of round blockIdx.x of row blockIdx.y: part[row][round].
+__global__ __launch_bounds__(SNT) void chunk_stats_kernel(const float *__restrict__ L, int V, float invT,
+                                                          float2 *__restrict__ part) {
+    __shared__ float s_red[2 * SNW];
+    const int r = blockIdx.x, row = blockIdx.y, nround = gridDim.x;
+    float z[4];
+    bool in;
+    load_round(L + (size_t)row * V, V, r, invT, z, in);
+    float m = -__builtin_huge_valf();
+    if (in)
+#pragma unroll
+        for (int e = 0; e < 4; e++) m = fmaxf(m, z[e]);
+    m = block_max(m, s_red);
+    float sw = 0.f;
+    if (in && m > -__builtin_huge_valf())
+#pragma unroll
+        for (int e = 0; e < 4; e++) sw += pexp(z[e] - m);
+    sw = block_sum(sw, s_red);
+    if (threadIdx.x == 0) part[(size_t)row * nround + r] = make_float2(m, sw);
+}
+
+// The draw of row blockIdx.x from its rounds' statistics: the row's max and
+// sum, each round's probability mass, the round holding u (first with u <=
+// the running sum), then the index inside it. A row without a finite maximum
+// or sum (all -Inf, NaN, +Inf) draws V - 1, as the reference's NaN
+// probabilities do; u <= 0 draws 0.
+__global__ __launch_bounds__(SNT) void chunk_draw_kernel(const float *__restrict__ L, int V, float invT,
+                                                         const float2 *__restrict__ part, const float *__restrict__ u,
+                                                         int32_t *__restrict__ out) {
+    __shared__ float s_redf[2 * SNW];
+    __shared__ int s_redi[SNW];
+    __shared__ float s_round[SMAX_ROUNDS];
+    __shared__ float s_before;
+    __shared__ int s_rr;
+    const int row = blockIdx.x, t = threadIdx.x;
+    const int nround = (V + SROUND - 1) / SROUND;
+    const float ur = u[row];
+    if (!(ur > 0.f)) {
+        if (t == 0) out[row] = 0;
+        return;
+    }
+    const float2 *pr = part + (size_t)row * nround;
+    float lm = -__builtin_huge_valf();
+    for (int i = t; i < nround; i += SNT) lm = fmaxf(lm, pr[i].x);
+    const float zmax = block_max(lm, s_redf);
+    float ls = 0.f;
+    if (zmax > -__builtin_huge_valf())
+        for (int i = t; i < nround; i += SNT) {
+            const float2 p = pr[i];
+            if (p.x > -__builtin_huge_valf()) ls += p.y * pexp(p.x - zmax);
+        }
+    const float S = block_sum(ls, s_redf);
+    if (!(zmax > -__builtin_huge_valf() && S > 0.f && S < __builtin_huge_valf())) {
+        if (t == 0) out[row] = V - 1;
+        return;
+    }
+    const float invS = 1.0f / S;
+    for (int i = t; i < nround; i += SNT) {
+        const float2 p = pr[i];
+        s_round[i] = p.x > -__builtin_huge_valf() ? p.y * pexp(p.x - zmax) * invS : 0.f;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float cum = 0.f;
+        int rr = -1;
+        for (int r = 0; r < nround; r++) {
+            const float nc = cum + s_round[r];
+            if (ur <= nc) {
+                rr = r;
+                break;
+            }
+            cum = nc;
+        }
+        s_rr = rr;
+        s_before = cum;
+    }
+    __syncthreads();
+    const int rr = s_rr;
+    const float before = s_before;
+    if (rr < 0) {
+        if (t == 0) out[row] = V - 1;
+        return;
+    }
+    float z[4], v[4];
+    bool in;
+    load_round(L + (size_t)row * V, V, rr, invT, z, in);
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = in ? pexp(z[e] - zmax) * invS : 0.f;
+    float tot;
+    const int hit = first_cdf_hit(v, in ? 4 : 0, before, ur, s_redf, tot);
+    const int local = block_min_i(hit, s_redi);
+    // (the scan inside the round can end a rounding step below the round's
+    // sum that selected it: then the round's last nonzero entry)
+    int last = INT_MAX;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        if (v[e] > 0.f) last = INT_MAX - (4 * t + e);
+    const int lastk = block_min_i(last, s_redi);
+    if (t == 0) {
+        const int tok =
+            local != INT_MAX ? rr * SROUND + local : lastk != INT_MAX ? rr * SROUND + (INT_MAX - lastk) : V - 1;
+        out[row] = min(tok, V - 1);
+    }
+}
+
 // In place on rows of logits: for every distinct id of the row's list in
 // [0, V): x -= presence (if presence != 0), then x = x > 0 ? x / rep : x * rep
 // (if rep != 1). A bitmap in LDS skips repeated ids.
@@ -887,6 +992,28 @@ hipError_t launch_sample(const float *L, int rows, int V, float T, int top_k, fl
                          int32_t *out, hipStream_t st) {
     const SampleArgs a{T, top_k, top_p, min_p};
     draft_sample_kernel<<<rows, SNT, 0, st>>>(L, V, a, u, out);
+    return hipGetLastError();
+}
+
+size_t sample_spread_ws(int rows, int V) {
+    return (size_t)rows * ((V + SROUND - 1) / SROUND) * sizeof(float2);
+}
+
+// Plain draws (T > 0, no top-k, top-p or min-p) with each row spread over
+// workgroups of one round each: chunk statistics, then one workgroup per row
+// merges them, picks the round and scans it (as draft_sample_kernel's draw);
+// every other setting runs draft_sample_kernel. ws: sample_spread_ws bytes.
+hipError_t launch_sample_spread(const float *L, int rows, int V, float T, int top_k, float top_p, float min_p,
+                                const float *u, int32_t *out, void *ws, hipStream_t st) {
+    if (!(T > 0.f) || top_k != 0 || top_p < 1.0f || min_p > 0.f)
+        return launch_sample(L, rows, V, T, top_k, top_p, min_p, u, out, st);
+    const int nround = (V + SROUND - 1) / SROUND;
+    const float invT = 1.0f / T;
+    float2 *part = (float2 *)ws;
+    chunk_stats_kernel<<<dim3(nround, rows), SNT, 0, st>>>(L, V, invT, part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    chunk_draw_kernel<<<rows, SNT, 0, st>>>(L, V, invT, part, u, out);
     return hipGetLastError();
 }
 

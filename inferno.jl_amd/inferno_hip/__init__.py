@@ -13,7 +13,7 @@ from .quantized_kernels import (ACT_PLAIN, ACT_RMSNORM, ACT_SILU_MUL, EPI_GATE, 
                                 gemm_q_ex, pack_weights_gated,
                                 mlp_forward_, mlp_ws_bytes, pack_weights, packed_bytes, q4_k_gemv_, q5_k_gemv_, q6_k_gemv_, q8_0_gemv_,
                                 quant_kernels_available, rmsnorm)
-from .sampler import apply_penalties_, softmax_sample
+from .sampler import apply_penalties_, sample_ws_bytes, softmax_sample
 from .speculative import (MODE_REFERENCE, MODE_STANDARD, SpeculativeStats, advance_len_, commit_state_, greedy_verify,
                           mtp_verify_step, n_tokens, softmax_stats, spec_accept, tree_accept)
 
@@ -24,5 +24,5 @@ __all__ = [
     "quant_kernels_available", "rmsnorm", "EPI_STORE", "EPI_STATS", "EPI_RESID", "EPI_GATE", "chain_in",
     "chain_out", "chain_buffers", "chain_operand_bytes", "gemm_q_chain", "pack_weights_gated", "MODE_REFERENCE", "MODE_STANDARD", "SpeculativeStats",
     "greedy_verify", "mtp_verify_step", "n_tokens", "softmax_stats", "spec_accept", "tree_accept",
-    "softmax_sample", "apply_penalties_", "commit_state_", "advance_len_",
+    "softmax_sample", "sample_ws_bytes", "apply_penalties_", "commit_state_", "advance_len_",
 ]

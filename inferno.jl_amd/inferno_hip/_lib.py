@@ -57,6 +57,8 @@ SIGNATURES = {
     "ihip_spec_commit_state": (_i, [_vp, _vp, _sz, _i64, _i, _vp, _i, _i64, _i64, _vp]),
     "ihip_spec_advance_len": (_i, [_vp, _vp, _i, _vp]),
     "ihip_sample": (_i, [_vp, _i, _i, _f, _i, _f, _f, _vp, _vp, _vp]),
+    "ihip_sample_ws_bytes": (_i, [_i, _i, C.POINTER(_sz)]),
+    "ihip_sample_ex": (_i, [_vp, _i, _i, _f, _i, _f, _f, _vp, _vp, _vp, _sz, _vp]),
     "ihip_apply_penalties": (_i, [_vp, _i, _i, _vp, _i, _i64, _f, _f, _vp]),
     "ihip_gguf_open": (_i, [C.c_char_p, C.POINTER(_vp)]),
     "ihip_gguf_close": (_i, [_vp]),

@@ -10,14 +10,26 @@ shim adds 1). There is no CPU fallback.
 """
 from __future__ import annotations
 
+import ctypes as C
+
 from . import _lib
 from .quantized_kernels import _ptr, _stream
 
 
+def sample_ws_bytes(rows: int, V: int) -> int:
+    """Workspace bytes of ihip_sample_ex for rows x V."""
+    nb = C.c_size_t()
+    _lib.check(_lib.load().ihip_sample_ws_bytes(rows, V, C.byref(nb)))
+    return max(int(nb.value), 16)
+
+
 def softmax_sample(logits, u, temperature: float = 1.0, top_p: float = 1.0, top_k: int = 0, min_p: float = 0.0,
-                   out=None, stream=None):
+                   out=None, stream=None, spread: bool = True, ws=None):
     """One token per row of logits [rows, V] (float32, contiguous) with the
-    uniforms u [rows]; returns int32 [rows]."""
+    uniforms u [rows]; returns int32 [rows]. spread: ihip_sample_ex, whose
+    plain draws (T > 0, no top-k, top-p or min-p) spread each row over
+    workgroups of 4096 logits, with ws (uint8, sample_ws_bytes; allocated
+    here when None); else ihip_sample (one workgroup per row)."""
     import torch
     if logits.dim() == 1:
         logits = logits.view(1, -1)
@@ -30,8 +42,17 @@ def softmax_sample(logits, u, temperature: float = 1.0, top_p: float = 1.0, top_
         out = torch.empty(rows, dtype=torch.int32, device=logits.device)
     elif not out.is_cuda or out.dtype != torch.int32 or out.numel() < rows:
         raise ValueError("out must be an int32 GPU tensor with one entry per row")
-    _lib.check(_lib.load().ihip_sample(_ptr(logits), rows, V, float(temperature), int(top_k), float(top_p),
-                                       float(min_p), _ptr(u), _ptr(out), _stream(stream)))
+    if not spread:
+        _lib.check(_lib.load().ihip_sample(_ptr(logits), rows, V, float(temperature), int(top_k), float(top_p),
+                                           float(min_p), _ptr(u), _ptr(out), _stream(stream)))
+        return out
+    need = sample_ws_bytes(rows, V)
+    if ws is None:
+        ws = torch.empty(need, dtype=torch.uint8, device=logits.device)
+    elif not ws.is_cuda or ws.dtype != torch.uint8 or ws.numel() < need:
+        raise ValueError(f"ws must be a uint8 GPU tensor of at least {need} bytes")
+    _lib.check(_lib.load().ihip_sample_ex(_ptr(logits), rows, V, float(temperature), int(top_k), float(top_p),
+                                          float(min_p), _ptr(u), _ptr(out), _ptr(ws), ws.numel(), _stream(stream)))
     return out
 
 

@@ -105,30 +105,49 @@ def test_parity_full_vocab(ih, kw):
 
 
 def test_plain_draw_paths(ih):
-    """Plain draws (no top-p, no min-p) take their rounds' sums from
-    per-wave parts of the statistics pass up to V = 262144 and the online
-    pass beyond it or when the row has no finite maximum or sum: rows that
-    are all -Inf or hold a NaN (the reference's V - 1), two finite entries
-    among -Inf, and Gaussian rows at V = 262144 and V = 300000."""
+    """Plain draws (no top-p, no min-p), both ways: spread over workgroups
+    of 4096 logits (ihip_sample_ex), and in one workgroup per row, which
+    takes its rounds' sums from per-wave parts of the statistics pass up to
+    V = 262144 and the online pass beyond it or when the row has no finite
+    maximum or sum: rows that are all -Inf or hold a NaN or +Inf (the
+    reference's V - 1), two finite entries among -Inf, u = 0, and Gaussian
+    rows at V = 262144, 300000 and 151936."""
     V = 4096
     a = np.full(V, -np.inf, np.float32)
     b = np.zeros(V, np.float32)
     b[7] = np.nan
     c = np.full(V, -np.inf, np.float32)
     c[100] = c[3000] = 1.0
+    d = np.zeros(V, np.float32)
+    d[5] = np.inf
     us = [0.1, 0.5, 0.9]
-    assert list(_draw(ih, a, us)) == [V - 1] * 3
-    assert list(_draw(ih, b, us)) == [V - 1] * 3
-    assert list(_draw(ih, c, us)) == [100, 100, 3000]
     rng = np.random.default_rng(11)
-    for Vb in (262144, 300000):
-        L = (3.0 * rng.standard_normal((8, Vb))).astype(np.float32)
-        u8 = rng.random(8).astype(np.float32)
-        got = _draw(ih, L, u8, temperature=0.9)
-        for r in range(8):
-            want = O.softmax_sample(L[r], float(u8[r]), temperature=0.9)
-            assert got[r] == want or _near_boundary(L[r], float(u8[r]), int(got[r]), want,
-                                                    dict(temperature=0.9)), (Vb, r, got[r], want)
+    big = [((3.0 * rng.standard_normal((8, Vb))).astype(np.float32), rng.random(8).astype(np.float32))
+           for Vb in (262144, 300000)]
+    # spread: ihip_sample_ex (rows over workgroups of 4096 logits); else one workgroup per row
+    for spread in (True, False):
+        assert list(_draw(ih, a, us, spread=spread)) == [V - 1] * 3
+        assert list(_draw(ih, b, us, spread=spread)) == [V - 1] * 3
+        assert list(_draw(ih, c, us, spread=spread)) == [100, 100, 3000]
+        assert list(_draw(ih, d, us, spread=spread)) == [V - 1] * 3
+        assert list(_draw(ih, c, [0.0], spread=spread)) == [0]  # r = 0: the first index
+        for L, u8 in big:
+            got = _draw(ih, L, u8, temperature=0.9, spread=spread)
+            for r in range(8):
+                want = O.softmax_sample(L[r], float(u8[r]), temperature=0.9)
+                assert got[r] == want or _near_boundary(L[r], float(u8[r]), int(got[r]), want,
+                                                        dict(temperature=0.9)), (spread, L.shape, r, got[r], want)
+    # the one-workgroup plain path at full vocabulary (the parity tests take the spread one)
+    L = (3.0 * rng.standard_normal((48, VOCAB))).astype(np.float32)
+    u48 = rng.random(48).astype(np.float32)
+    got = _draw(ih, L, u48, spread=False)
+    bad = 0
+    for r in range(48):
+        want = O.softmax_sample(L[r], float(u48[r]))
+        if got[r] != want:
+            assert _near_boundary(L[r], float(u48[r]), int(got[r]), want, {}), (r, got[r], want)
+            bad += 1
+    assert bad <= 1
 
 
 def test_topk_ties_exact(ih):
