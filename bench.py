@@ -896,8 +896,8 @@ def sampler_config(ih):
     """The draft-side sampler (ihip_sample_ex: softmax_sample, src/ModelCPU.jl:
     1123-1200; ihip_apply_penalties: :1202-1225) at the LM head's vocabulary
     V = 151936: microseconds per call for 1 and 64 rows (seeded Gaussian
-    logits, sd 3), each call replayed in a HIP graph, plain draws also with
-    one workgroup per row (ihip_sample); beside it the oracle's numpy
+    logits, sd 3), each call replayed in a HIP graph, plain and top-k draws
+    also with one workgroup per row (ihip_sample); beside it the oracle's numpy
     restatement of one row on the host (argsorts for top-k/top-p)."""
     import torch
     import numpy as np
@@ -916,8 +916,10 @@ def sampler_config(ih):
         for name, kw in settings.items():
             t = graph_time(lambda: [ih.softmax_sample(L, u, out=tok, ws=ws, **kw) for _ in range(10)]) / 10
             out["us_per_call"][f"rows={rows},{name}"] = round(t * 1e6, 1)
-        t = graph_time(lambda: [ih.softmax_sample(L, u, out=tok, spread=False) for _ in range(10)]) / 10
-        out["us_per_call"][f"rows={rows},plain,one_workgroup"] = round(t * 1e6, 1)
+        for name in ("plain", "top_k=40"):
+            kw = settings[name]
+            t = graph_time(lambda: [ih.softmax_sample(L, u, out=tok, spread=False, **kw) for _ in range(10)]) / 10
+            out["us_per_call"][f"rows={rows},{name},one_workgroup"] = round(t * 1e6, 1)
         ids = torch.arange(0, 4096, 7, dtype=torch.int32, device="cuda")
         t = graph_time(lambda: [ih.apply_penalties_(L, ids, presence=0.1, repetition=1.1) for _ in range(10)]) / 10
         out["us_per_call"][f"rows={rows},penalties(586 ids)"] = round(t * 1e6, 1)

@@ -23,6 +23,9 @@
 //    it (statistics, nucleus mass or min-p mass) where V <= 262144.
 //  * the threshold's refinement passes run over the first pass's bucket
 //    gathered into LDS when it holds at most 4096 elements.
+//  * with a workspace, plain draws and top-k up to 64 spread each row over
+//    workgroups of one round (chunk statistics, then each chunk's top-k
+//    candidates), and one workgroup per row finishes the draw from them.
 // Sums and scans are trees, where the reference accumulates sequentially:
 // the drawn token can differ only where u falls within rounding of a CDF
 // step.
@@ -391,6 +394,107 @@ __device__ __forceinline__ bool above_threshold(float z, int j, float zmax, uint
     return k > tau || (k == tau && j < tie_lim);
 }
 
+// The draw over n top-k candidates in LDS in index order (s_cidx: token
+// ids, s_cp: z = L / T; s_sort: scratch), shared by draft_sample_kernel and
+// the spread top-k draw: softmax over the candidates (the rest are
+// exp(-Inf) = 0), top-p by a bitonic sort of their probabilities, min-p,
+// then the inverse CDF in index order.
+__device__ void draw_candidates(int n, const SampleArgs &a, float ur, int V, int *s_cidx, float *s_cp, int *s_sort,
+                                float *s_redf, int *s_redi, int32_t *out_row) {
+    const int t = threadIdx.x;
+    // softmax over the candidates (the rest are exp(-Inf) = 0)
+    float lm = -__builtin_huge_valf();
+    for (int i = t; i < n; i += SNT) lm = fmaxf(lm, s_cp[i]);
+    const float zmax = block_max(lm, s_redf);
+    float ls = 0.f;
+    for (int i = t; i < n; i += SNT) {
+        const float w = pexp(s_cp[i] - zmax);
+        s_cp[i] = w;
+        ls += w;
+    }
+    const float S = block_sum(ls, s_redf);
+    for (int i = t; i < n; i += SNT) s_cp[i] = s_cp[i] / S;
+    __syncthreads();
+    if (a.top_p < 1.0f) {
+        // sort the slots by (p descending, slot ascending) = the stable
+        // descending sortperm of the probabilities
+        int P2 = 1;
+        while (P2 < n) P2 <<= 1;
+        for (int i = t; i < P2; i += SNT) s_sort[i] = i < n ? i : -1;
+        __syncthreads();
+        for (int size = 2; size <= P2; size <<= 1)
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                for (int i = t; i < P2 / 2; i += SNT) {
+                    const int lo = ((i & ~(stride - 1)) << 1) | (i & (stride - 1));
+                    const int hi = lo + stride;
+                    const int A = s_sort[lo], B = s_sort[hi];
+                    bool a_first;
+                    if (A < 0) a_first = false;
+                    else if (B < 0) a_first = true;
+                    else {
+                        const float pa = s_cp[A], pb = s_cp[B];
+                        a_first = pa > pb || (pa == pb && A < B);
+                    }
+                    if (a_first != ((lo & size) == 0)) {
+                        s_sort[lo] = B;
+                        s_sort[hi] = A;
+                    }
+                }
+                __syncthreads();
+            }
+        // the shortest sorted prefix whose mass reaches top_p
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int j = 4 * t + e;
+            v[e] = j < n ? s_cp[s_sort[j]] : 0.f;
+        }
+        float tot;
+        const int hit = first_cdf_hit(v, n - 4 * t, 0.f, a.top_p, s_redf, tot);
+        const int cut = block_min_i(hit, s_redi);
+        const int n_keep = cut == INT_MAX ? n : cut + 1;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int j = 4 * t + e;
+            if (j < n && j >= n_keep) s_cp[s_sort[j]] = 0.f;
+        }
+        __syncthreads();
+        float lt = 0.f;
+        for (int i = t; i < n; i += SNT) lt += s_cp[i];
+        const float total = block_sum(lt, s_redf);
+        if (total > 0.f)
+            for (int i = t; i < n; i += SNT) s_cp[i] = s_cp[i] / total;
+        __syncthreads();
+    }
+    if (a.min_p > 0.f) {
+        float lm2 = 0.f;
+        for (int i = t; i < n; i += SNT) lm2 = fmaxf(lm2, s_cp[i]);
+        const float thr = block_max(lm2, s_redf) * a.min_p;
+        float lt = 0.f;
+        for (int i = t; i < n; i += SNT) {
+            float p = s_cp[i];
+            if (p < thr) p = 0.f;
+            s_cp[i] = p;
+            lt += p;
+        }
+        const float total = block_sum(lt, s_redf);
+        if (total > 0.f)
+            for (int i = t; i < n; i += SNT) s_cp[i] = s_cp[i] / total;
+        __syncthreads();
+    }
+    // inverse CDF in index order over the candidates
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int j = 4 * t + e;
+        v[e] = j < n ? s_cp[j] : 0.f;
+    }
+    float tot;
+    const int hit = first_cdf_hit(v, n - 4 * t, 0.f, ur, s_redf, tot);
+    const int slot = block_min_i(hit, s_redi);
+    if (t == 0) *out_row = slot == INT_MAX ? V - 1 : s_cidx[slot];
+}
+
 __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restrict__ L, int V, SampleArgs a,
                                                            const float *__restrict__ u, int32_t *__restrict__ out) {
     __shared__ float s_redf[2 * SNW];
@@ -487,97 +591,7 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
         });
         __syncthreads();
         const int n = min(run_kept, SK_MAX);  // == K
-        // softmax over the candidates (the rest are exp(-Inf) = 0)
-        float lm = -__builtin_huge_valf();
-        for (int i = t; i < n; i += SNT) lm = fmaxf(lm, s_cp[i]);
-        const float zmax = block_max(lm, s_redf);
-        float ls = 0.f;
-        for (int i = t; i < n; i += SNT) {
-            const float w = pexp(s_cp[i] - zmax);
-            s_cp[i] = w;
-            ls += w;
-        }
-        const float S = block_sum(ls, s_redf);
-        for (int i = t; i < n; i += SNT) s_cp[i] = s_cp[i] / S;
-        __syncthreads();
-        if (a.top_p < 1.0f) {
-            // sort the slots by (p descending, slot ascending) = the stable
-            // descending sortperm of the probabilities
-            int P2 = 1;
-            while (P2 < n) P2 <<= 1;
-            for (int i = t; i < P2; i += SNT) s_sort[i] = i < n ? i : -1;
-            __syncthreads();
-            for (int size = 2; size <= P2; size <<= 1)
-                for (int stride = size >> 1; stride > 0; stride >>= 1) {
-                    for (int i = t; i < P2 / 2; i += SNT) {
-                        const int lo = ((i & ~(stride - 1)) << 1) | (i & (stride - 1));
-                        const int hi = lo + stride;
-                        const int A = s_sort[lo], B = s_sort[hi];
-                        bool a_first;
-                        if (A < 0) a_first = false;
-                        else if (B < 0) a_first = true;
-                        else {
-                            const float pa = s_cp[A], pb = s_cp[B];
-                            a_first = pa > pb || (pa == pb && A < B);
-                        }
-                        if (a_first != ((lo & size) == 0)) {
-                            s_sort[lo] = B;
-                            s_sort[hi] = A;
-                        }
-                    }
-                    __syncthreads();
-                }
-            // the shortest sorted prefix whose mass reaches top_p
-            float v[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int j = 4 * t + e;
-                v[e] = j < n ? s_cp[s_sort[j]] : 0.f;
-            }
-            float tot;
-            const int hit = first_cdf_hit(v, n - 4 * t, 0.f, a.top_p, s_redf, tot);
-            const int cut = block_min_i(hit, s_redi);
-            const int n_keep = cut == INT_MAX ? n : cut + 1;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int j = 4 * t + e;
-                if (j < n && j >= n_keep) s_cp[s_sort[j]] = 0.f;
-            }
-            __syncthreads();
-            float lt = 0.f;
-            for (int i = t; i < n; i += SNT) lt += s_cp[i];
-            const float total = block_sum(lt, s_redf);
-            if (total > 0.f)
-                for (int i = t; i < n; i += SNT) s_cp[i] = s_cp[i] / total;
-            __syncthreads();
-        }
-        if (a.min_p > 0.f) {
-            float lm2 = 0.f;
-            for (int i = t; i < n; i += SNT) lm2 = fmaxf(lm2, s_cp[i]);
-            const float thr = block_max(lm2, s_redf) * a.min_p;
-            float lt = 0.f;
-            for (int i = t; i < n; i += SNT) {
-                float p = s_cp[i];
-                if (p < thr) p = 0.f;
-                s_cp[i] = p;
-                lt += p;
-            }
-            const float total = block_sum(lt, s_redf);
-            if (total > 0.f)
-                for (int i = t; i < n; i += SNT) s_cp[i] = s_cp[i] / total;
-            __syncthreads();
-        }
-        // inverse CDF in index order over the candidates
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int j = 4 * t + e;
-            v[e] = j < n ? s_cp[j] : 0.f;
-        }
-        float tot;
-        const int hit = first_cdf_hit(v, n - 4 * t, 0.f, ur, s_redf, tot);
-        const int slot = block_min_i(hit, s_redi);
-        if (t == 0) out[row] = slot == INT_MAX ? V - 1 : s_cidx[slot];
+        draw_candidates(n, a, ur, V, s_cidx, s_cp, s_sort, s_redf, s_redi, out + row);
         return;
     }
 
@@ -955,6 +969,215 @@ __global__ __launch_bounds__(SNT) void chunk_draw_kernel(const float *__restrict
     }
 }
 
+// Spread top-k (1 <= K <= SK_SPREAD, V <= SPART_ROUNDS rounds): every
+// chunk's own top-K by the one-row kernel's order (the row maximum's bucket,
+// then the key; ties lowest index first), then one workgroup per row picks
+// the row's top-K from the chunks' candidates by the same order. The union
+// of the chunks' top-K holds the row's, and it is in index order, so the
+// draw over the kept candidates is the one-row kernel's.
+constexpr int SK_SPREAD = 64;
+
+// Chunk blockIdx.x of row blockIdx.y: its top-K candidates (z and token id,
+// index order) to cz / ci [row][chunk][SK_SPREAD], their count to cn.
+__global__ __launch_bounds__(SNT) void chunk_topk_kernel(const float *__restrict__ L, int V, float invT, int K,
+                                                         const float2 *__restrict__ part, float *__restrict__ cz,
+                                                         int32_t *__restrict__ ci, int32_t *__restrict__ cn) {
+    __shared__ float s_redf[2 * SNW];
+    __shared__ uint32_t s_redu[SNW];
+    __shared__ uint32_t s_hist[256];
+    __shared__ unsigned long long s_mass[256];
+    __shared__ uint32_t s_sel[2];
+    __shared__ unsigned long long s_selm[2];
+    __shared__ uint32_t s_ck[SK_MAX];
+    __shared__ float s_cz[SK_MAX];
+    __shared__ int s_ncnt;
+    const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x, nround = gridDim.x;
+    float lm = -__builtin_huge_valf();
+    for (int i = t; i < nround; i += SNT) lm = fmaxf(lm, part[(size_t)row * nround + i].x);
+    const float zm = block_max(lm, s_redf);
+    const float *Lc = L + (size_t)row * V + (size_t)c * SROUND;
+    const int Vc = min(SROUND, V - c * SROUND);
+    Select R;
+    select_threshold<false>(Lc, Vc, 1, invT, zm, 1.f, (unsigned long long)K, s_hist, s_mass, s_sel, s_selm, s_ck,
+                            s_cz, &s_ncnt, R);
+    const uint32_t zb = R.zb, tau = R.tau;
+    const int rem = (int)R.rem;
+    float z[4];
+    bool in;
+    load_round(Lc, Vc, 0, invT, z, in);
+    bool g[4], q[4];
+    uint32_t ng = 0, nq = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t b = zbin(z[e], zm);
+        const uint32_t k = okey(z[e]);
+        g[e] = in && (R.all || b < zb || (b == zb && k > tau));
+        q[e] = in && !R.all && b == zb && k == tau;
+        ng += g[e];
+        nq += q[e];
+    }
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan_u(ng | (nq << 16), s_redu, tot);
+    const int eq_before = (int)(ex >> 16);
+    int pos = (int)(ex & 0xffffu) + min(max(rem, 0), eq_before);
+    int er = eq_before;
+    const size_t base = ((size_t)row * nround + c) * SK_SPREAD;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        if (g[e] || (q[e] && er < rem)) {
+            if (pos < SK_SPREAD) {
+                cz[base + pos] = z[e];
+                ci[base + pos] = c * SROUND + 4 * t + e;
+            }
+            pos++;
+        }
+        if (q[e]) er++;
+    }
+    if (t == 0) cn[(size_t)row * nround + c] = min((int)(tot & 0xffffu) + min(max(rem, 0), (int)(tot >> 16)), SK_SPREAD);
+}
+
+// select_threshold over n values in LDS (MASS off): the bucket of pass A,
+// then the key inside it, 8 bits a pass; R.all when fewer than target.
+__device__ void select_lds(const float *z, int n, float zmax, unsigned long long target, uint32_t *hist,
+                           uint32_t *sel, unsigned long long *selm, Select &R) {
+    const int t = threadIdx.x;
+    R.zb = 255u;
+    R.tau = 0u;
+    R.rem = target;
+    R.cnt = 0;
+    R.all = false;
+    if (t < 256) hist[t] = 0;
+    __syncthreads();
+    for (int i = t; i < n; i += SNT) atomicAdd(&hist[zbin(z[i], zmax)], 1u);
+    __syncthreads();
+    pick_bucket<false>(hist, nullptr, R.rem, sel, selm, false);
+    __syncthreads();
+    const uint32_t zb = sel[0];
+    const unsigned long long aboveA = selm[0];
+    __syncthreads();
+    if (aboveA == ~0ull) {
+        R.all = true;
+        return;
+    }
+    R.rem -= aboveA;
+    R.zb = zb;
+    uint32_t prefix = 0, pmask = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        if (t < 256) hist[t] = 0;
+        __syncthreads();
+        for (int i = t; i < n; i += SNT) {
+            const uint32_t k = okey(z[i]);
+            if ((k & pmask) != prefix || zbin(z[i], zmax) != zb) continue;
+            atomicAdd(&hist[(k >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        pick_bucket<false>(hist, nullptr, R.rem, sel, selm, true);
+        __syncthreads();
+        const uint32_t b = sel[0];
+        const unsigned long long above = selm[0];
+        const uint32_t cb = hist[b];
+        __syncthreads();
+        if (above == ~0ull) {
+            R.all = true;
+            return;
+        }
+        R.rem -= above;
+        prefix |= b << shift;
+        pmask |= 255u << shift;
+        R.cnt = cb;
+    }
+    R.tau = prefix;
+}
+
+// Row blockIdx.x: the chunks' candidates gathered in index order, the row's
+// top-K among them, then draw_candidates as draft_sample_kernel's top-k path.
+__global__ __launch_bounds__(SNT) void topk_draw_kernel(int V, SampleArgs a, const float2 *__restrict__ part,
+                                                        const float *__restrict__ cz, const int32_t *__restrict__ ci,
+                                                        const int32_t *__restrict__ cn, const float *__restrict__ u,
+                                                        int32_t *__restrict__ out) {
+    __shared__ float s_redf[2 * SNW];
+    __shared__ uint32_t s_redu[SNW];
+    __shared__ int s_redi[SNW];
+    __shared__ uint32_t s_hist[256];
+    __shared__ uint32_t s_sel[2];
+    __shared__ unsigned long long s_selm[2];
+    __shared__ int s_off[SPART_ROUNDS + 1];
+    __shared__ float s_gz[SK_MAX];
+    __shared__ int s_gi[SK_MAX];
+    __shared__ int s_cidx[SK_MAX];
+    __shared__ float s_cp[SK_MAX];
+    __shared__ int s_sort[SK_MAX];
+    const int row = blockIdx.x, t = threadIdx.x;
+    const int nround = (V + SROUND - 1) / SROUND;
+    const float ur = u[row];
+    if (!(ur > 0.f)) {  // the reference's draw returns index 1 (here 0) when r <= 0
+        if (t == 0) out[row] = 0;
+        return;
+    }
+    float lm = -__builtin_huge_valf();
+    for (int i = t; i < nround; i += SNT) lm = fmaxf(lm, part[(size_t)row * nround + i].x);
+    const float zm = block_max(lm, s_redf);
+    if (t < 64) {  // chunk offsets (nround <= 64: one per lane)
+        const int cnt = t < nround ? cn[(size_t)row * nround + t] : 0;
+        int inc = cnt;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(inc, o);
+            if (t >= o) inc += y;
+        }
+        if (t < nround) s_off[t] = inc - cnt;
+        if (t == 63) s_off[SPART_ROUNDS] = inc;
+    }
+    __syncthreads();
+    const int n = s_off[SPART_ROUNDS];
+    for (int i = t; i < nround * SK_SPREAD; i += SNT) {
+        const int c = i / SK_SPREAD, j = i - c * SK_SPREAD;
+        if (j < cn[(size_t)row * nround + c]) {
+            const size_t src = ((size_t)row * nround + c) * SK_SPREAD + j;
+            s_gz[s_off[c] + j] = cz[src];
+            s_gi[s_off[c] + j] = ci[src];
+        }
+    }
+    __syncthreads();
+    Select R;
+    select_lds(s_gz, n, zm, (unsigned long long)a.top_k, s_hist, s_sel, s_selm, R);
+    const uint32_t zb = R.zb, tau = R.tau;
+    const int rem = (int)R.rem;
+    // the kept candidates in index order (positions 4 t .. 4 t + 3: n <= SK_MAX)
+    bool g[4], q[4];
+    uint32_t ng = 0, nq = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int j = 4 * t + e;
+        const bool live = j < n;
+        const float z = live ? s_gz[j] : 0.f;
+        const uint32_t b = zbin(z, zm), k = okey(z);
+        g[e] = live && (R.all || b < zb || (b == zb && k > tau));
+        q[e] = live && !R.all && b == zb && k == tau;
+        ng += g[e];
+        nq += q[e];
+    }
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan_u(ng | (nq << 16), s_redu, tot);
+    const int eq_before = (int)(ex >> 16);
+    int pos = (int)(ex & 0xffffu) + min(max(rem, 0), eq_before);
+    int er = eq_before;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int j = 4 * t + e;
+        if (g[e] || (q[e] && er < rem)) {
+            if (pos < SK_MAX) {
+                s_cidx[pos] = s_gi[j];
+                s_cp[pos] = s_gz[j];
+            }
+            pos++;
+        }
+        if (q[e]) er++;
+    }
+    __syncthreads();
+    const int nk = min((int)(tot & 0xffffu) + min(max(rem, 0), (int)(tot >> 16)), SK_MAX);  // == K
+    draw_candidates(nk, a, ur, V, s_cidx, s_cp, s_sort, s_redf, s_redi, out + row);
+}
+
 // In place on rows of logits: for every distinct id of the row's list in
 // [0, V): x -= presence (if presence != 0), then x = x > 0 ? x / rep : x * rep
 // (if rep != 1). A bitmap in LDS skips repeated ids.
@@ -995,25 +1218,44 @@ hipError_t launch_sample(const float *L, int rows, int V, float T, int top_k, fl
     return hipGetLastError();
 }
 
+// spread workspace, 524 bytes per chunk of each row: float2 part[rows][nround],
+// then (top-k) float cz[rows][nround][SK_SPREAD], int32 ci[same], int32 cn[rows][nround]
 size_t sample_spread_ws(int rows, int V) {
-    return (size_t)rows * ((V + SROUND - 1) / SROUND) * sizeof(float2);
+    const size_t rc = (size_t)rows * ((V + SROUND - 1) / SROUND);
+    return rc * (sizeof(float2) + 2 * SK_SPREAD * 4 + 4);
 }
 
 // Plain draws (T > 0, no top-k, top-p or min-p) with each row spread over
 // workgroups of one round each: chunk statistics, then one workgroup per row
 // merges them, picks the round and scans it (as draft_sample_kernel's draw);
-// every other setting runs draft_sample_kernel. ws: sample_spread_ws bytes.
+// top-k from 1 to SK_SPREAD over at most SPART_ROUNDS rounds: chunk
+// statistics (the row maximum), each chunk's top-k, then one workgroup per
+// row draws among the candidates; every other setting runs
+// draft_sample_kernel. ws: sample_spread_ws bytes.
 hipError_t launch_sample_spread(const float *L, int rows, int V, float T, int top_k, float top_p, float min_p,
                                 const float *u, int32_t *out, void *ws, hipStream_t st) {
-    if (!(T > 0.f) || top_k != 0 || top_p < 1.0f || min_p > 0.f)
-        return launch_sample(L, rows, V, T, top_k, top_p, min_p, u, out, st);
     const int nround = (V + SROUND - 1) / SROUND;
+    const bool plain = T > 0.f && top_k == 0 && top_p >= 1.0f && min_p <= 0.f;
+    const bool topk = T > 0.f && top_k >= 1 && top_k <= SK_SPREAD && nround <= SPART_ROUNDS;
+    if (!plain && !topk) return launch_sample(L, rows, V, T, top_k, top_p, min_p, u, out, st);
     const float invT = 1.0f / T;
-    float2 *part = (float2 *)ws;
+    const size_t rc = (size_t)rows * nround;
+    uint8_t *w = (uint8_t *)ws;
+    float2 *part = (float2 *)w;
     chunk_stats_kernel<<<dim3(nround, rows), SNT, 0, st>>>(L, V, invT, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    chunk_draw_kernel<<<rows, SNT, 0, st>>>(L, V, invT, part, u, out);
+    if (plain) {
+        chunk_draw_kernel<<<rows, SNT, 0, st>>>(L, V, invT, part, u, out);
+        return hipGetLastError();
+    }
+    float *cz = (float *)(w + rc * sizeof(float2));
+    int32_t *ci = (int32_t *)(cz + rc * SK_SPREAD);
+    int32_t *cn = ci + rc * SK_SPREAD;
+    chunk_topk_kernel<<<dim3(nround, rows), SNT, 0, st>>>(L, V, invT, top_k, part, cz, ci, cn);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const SampleArgs a{T, top_k, top_p, min_p};
+    topk_draw_kernel<<<rows, SNT, 0, st>>>(V, a, part, cz, ci, cn, u, out);
     return hipGetLastError();
 }
 

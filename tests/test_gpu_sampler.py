@@ -150,6 +150,44 @@ def test_plain_draw_paths(ih):
     assert bad <= 1
 
 
+def test_topk_spread_matches_one_workgroup(ih):
+    """Top-k draws with 1 <= k <= 64 over at most 64 chunks of 4096 logits
+    spread over workgroups (each chunk's top-k, then the row's among them)
+    give the one-workgroup kernel's tokens bit for bit: Gaussian and
+    quantized (tied) rows at V = 151936, 262144 and 4100, rows all -Inf or
+    holding NaN or +Inf, u = 0, with top-p and min-p after the cut; k = 65
+    and V = 300000 take the one-workgroup kernel on both calls."""
+    rng = np.random.default_rng(17)
+    cases = []
+    for V in (151936, 262144, 4100):
+        G = (3.0 * rng.standard_normal((24, V))).astype(np.float32)
+        Qz = rng.integers(0, 3, size=(8, V)).astype(np.float32)
+        X = np.concatenate([G, Qz])
+        X[24, :] = -np.inf
+        X[25, 11] = np.nan
+        X[26, V - 3] = np.inf
+        cases.append(X)
+    cases.append((3.0 * rng.standard_normal((4, 300000))).astype(np.float32))
+    settings = [dict(temperature=0.8, top_k=40), dict(temperature=1.0, top_k=1), dict(temperature=0.7, top_k=64),
+                dict(temperature=0.7, top_k=50, top_p=0.95), dict(temperature=1.1, top_k=7, min_p=0.1),
+                dict(temperature=0.9, top_k=37, top_p=0.6, min_p=0.02), dict(temperature=0.8, top_k=65)]
+    for L in cases:
+        us = rng.random(L.shape[0]).astype(np.float32)
+        us[1] = 0.0
+        for kw in settings:
+            a = _draw(ih, L, us, spread=True, **kw)
+            b = _draw(ih, L, us, spread=False, **kw)
+            assert np.array_equal(a, b), (L.shape, kw, np.nonzero(a != b)[0][:8])
+    # against the oracle at k = 40 (V = 151936, quantized ties)
+    L = cases[0][24:]
+    us = rng.random(L.shape[0]).astype(np.float32)
+    got = _draw(ih, L, us, temperature=0.9, top_k=40)
+    for r in range(3, L.shape[0]):
+        want = O.softmax_sample(L[r], float(us[r]), temperature=0.9, top_k=40)
+        assert got[r] == want or _near_boundary(L[r], float(us[r]), int(got[r]), want,
+                                                dict(temperature=0.9, top_k=40)), r
+
+
 def test_topk_ties_exact(ih):
     # all equal: top_k = 5 keeps indices 0..4, token = ceil(5 u) - 1
     Z = np.zeros(4096, np.float32)
