@@ -424,12 +424,14 @@ int ihip_sample(const float *logits_dev, int rows, int V, float T, int top_k,
                 float top_p, float min_p, const float *u_dev,
                 int32_t *out_tok_dev, void *stream);
 /* ihip_sample with a caller workspace (ihip_sample_ws_bytes; 16-byte
- * aligned, 524 bytes per 4096 logits of each row): plain draws (T > 0, no
- * top-k, top-p or min-p: the speculative defaults) spread each row over
- * workgroups of 4096 logits (their softmax statistics, then the draw inside
- * the round that holds u); so does top-k from 1 to 64 at V <= 262144 (each
- * chunk's top-k, then the row's among them: the tokens of ihip_sample);
- * every other setting runs as ihip_sample. The same softmax_sample
+ * aligned; 4104 bytes per 4096 logits of each row plus 49408 per row):
+ * plain draws (T > 0, no top-k, top-p or min-p: the speculative defaults)
+ * spread each row over workgroups of 4096 logits (their softmax
+ * statistics, then the draw inside the round that holds u); so do top-k
+ * from 1 to 64 at V <= 262144 (each chunk's top-k, then the row's among
+ * them: the tokens of ihip_sample), top-p alone (the threshold's histograms
+ * merged per row) and min-p alone; every other setting runs as
+ * ihip_sample. The same softmax_sample
  * (src/ModelCPU.jl:1123-1200) and the same contract: draws match the exact
  * cumulative distribution except within rounding of a step. */
 int ihip_sample_ws_bytes(int rows, int V, size_t *bytes);

@@ -23,9 +23,10 @@
 //    it (statistics, nucleus mass or min-p mass) where V <= 262144.
 //  * the threshold's refinement passes run over the first pass's bucket
 //    gathered into LDS when it holds at most 4096 elements.
-//  * with a workspace, plain draws and top-k up to 64 spread each row over
-//    workgroups of one round (chunk statistics, then each chunk's top-k
-//    candidates), and one workgroup per row finishes the draw from them.
+//  * with a workspace, plain draws, top-k up to 64, and top-p or min-p
+//    alone spread each row over workgroups of one round (chunk statistics,
+//    each chunk's top-k candidates or threshold histograms and kept sums),
+//    and one workgroup per row finishes each stage from them.
 // Sums and scans are trees, where the reference accumulates sequentially:
 // the drawn token can differ only where u falls within rounding of a CDF
 // step.
@@ -275,6 +276,69 @@ __device__ void pick_bucket(const uint32_t *hist, const unsigned long long *mass
     }
 }
 
+// Fixed-point probability mass of z: p = exp(z - zmax) / S in units of 2^-40.
+__device__ __forceinline__ unsigned long long mass_fx(float z, float zmax, float invS) {
+    return (unsigned long long)(pexp(z - zmax) * invS * 1099511627776.0f);
+}
+
+// Passes B: the exact key inside bucket R.zb, 8 bits a pass from the top,
+// R.rem units still to reach; over the nzb gathered keys and values (ck, cz)
+// when gathered, else over the row. R.tau, R.rem and R.cnt on return, or
+// R.all when (MASS) truncated masses fall just short of the target.
+template <bool MASS>
+__device__ void refine_threshold(const float *__restrict__ row, int V, int nround, float T, float zmax, float S,
+                                 bool gathered, int nzb, uint32_t *hist, unsigned long long *mass, uint32_t *sel,
+                                 unsigned long long *selm, const uint32_t *ck, const float *cz, Select &R) {
+    const int t = threadIdx.x;
+    const uint32_t zb = R.zb;
+    const float invS = 1.0f / S;
+    uint32_t prefix = 0, pmask = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        if (t < 256) {
+            hist[t] = 0;
+            if (MASS) mass[t] = 0;
+        }
+        __syncthreads();
+        if (gathered) {
+            for (int i = t; i < nzb; i += SNT) {
+                const uint32_t k = ck[i];
+                if ((k & pmask) != prefix) continue;
+                const uint32_t b = (k >> shift) & 255u;
+                atomicAdd(&hist[b], 1u);
+                if (MASS) atomicAdd(&mass[b], mass_fx(cz[i], zmax, invS));
+            }
+        } else {
+            for_rounds(row, V, nround, T, [&](const float (&z)[4], bool in, int) {
+                if (!in) return;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t k = okey(z[e]);
+                    if ((k & pmask) != prefix || zbin(z[e], zmax) != zb) continue;
+                    const uint32_t b = (k >> shift) & 255u;
+                    atomicAdd(&hist[b], 1u);
+                    if (MASS) atomicAdd(&mass[b], mass_fx(z[e], zmax, invS));
+                }
+            });
+        }
+        __syncthreads();
+        pick_bucket<MASS>(hist, mass, R.rem, sel, selm, true);
+        __syncthreads();
+        const uint32_t b = sel[0];
+        const unsigned long long above = selm[0];
+        const uint32_t cb = hist[b];
+        __syncthreads();
+        if (above == ~0ull) {  // (MASS: truncated masses just short of the target)
+            R.all = true;
+            return;
+        }
+        R.rem -= above;
+        prefix |= b << shift;
+        pmask |= 255u << shift;
+        R.cnt = cb;
+    }
+    R.tau = prefix;
+}
+
 // The B passes read only the elements of bucket zb: when it holds at most
 // SK_MAX of them, one more pass gathers their keys and values into LDS
 // (ck, cz; any order: the passes only count) and the B passes run there
@@ -290,9 +354,6 @@ __device__ void select_threshold(const float *__restrict__ row, int V, int nroun
     R.cnt = 0;
     R.all = false;
     const float invS = 1.0f / S;
-    auto mass_of = [&](float z) {
-        return (unsigned long long)(pexp(z - zmax) * invS * 1099511627776.0f);
-    };
     // pass A: buckets of w = zmax - z, largest z first = bucket 0 first
     if (t < 256) {
         hist[t] = 0;
@@ -305,7 +366,7 @@ __device__ void select_threshold(const float *__restrict__ row, int V, int nroun
         for (int e = 0; e < 4; e++) {
             const uint32_t b = zbin(z[e], zmax);
             atomicAdd(&hist[b], 1u);
-            if (MASS) atomicAdd(&mass[b], mass_of(z[e]));
+            if (MASS) atomicAdd(&mass[b], mass_fx(z[e], zmax, invS));
         }
     });
     __syncthreads();
@@ -337,52 +398,7 @@ __device__ void select_threshold(const float *__restrict__ row, int V, int nroun
         });
         __syncthreads();
     }
-    // passes B: the exact key inside bucket zb, 8 bits a pass from the top
-    uint32_t prefix = 0, pmask = 0;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        if (t < 256) {
-            hist[t] = 0;
-            if (MASS) mass[t] = 0;
-        }
-        __syncthreads();
-        if (gathered) {
-            for (int i = t; i < (int)nzb; i += SNT) {
-                const uint32_t k = ck[i];
-                if ((k & pmask) != prefix) continue;
-                const uint32_t b = (k >> shift) & 255u;
-                atomicAdd(&hist[b], 1u);
-                if (MASS) atomicAdd(&mass[b], mass_of(cz[i]));
-            }
-        } else {
-            for_rounds(row, V, nround, T, [&](const float (&z)[4], bool in, int) {
-                if (!in) return;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const uint32_t k = okey(z[e]);
-                    if ((k & pmask) != prefix || zbin(z[e], zmax) != zb) continue;
-                    const uint32_t b = (k >> shift) & 255u;
-                    atomicAdd(&hist[b], 1u);
-                    if (MASS) atomicAdd(&mass[b], mass_of(z[e]));
-                }
-            });
-        }
-        __syncthreads();
-        pick_bucket<MASS>(hist, mass, R.rem, sel, selm, true);
-        __syncthreads();
-        const uint32_t b = sel[0];
-        const unsigned long long above = selm[0];
-        const uint32_t cb = hist[b];
-        __syncthreads();
-        if (above == ~0ull) {  // (MASS: truncated masses just short of the target)
-            R.all = true;
-            return;
-        }
-        R.rem -= above;
-        prefix |= b << shift;
-        pmask |= 255u << shift;
-        R.cnt = cb;
-    }
-    R.tau = prefix;
+    refine_threshold<MASS>(row, V, nround, T, zmax, S, gathered, (int)nzb, hist, mass, sel, selm, ck, cz, R);
 }
 
 // Kept by a threshold: a larger z than the bucket (smaller bucket index), or
@@ -864,6 +880,42 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
     }
 }
 
+// Workspace of the spread draws: float2 part[rows][nround] (each round's
+// (max, sum exp(z - max))), then a slot of SLOT_BYTES per round of each row
+// (top-k: float cz[SK_SPREAD], int32 ci[SK_SPREAD], int32 cn; top-p: uint32
+// hist[256], uint64 mass[256]; top-p / min-p: float csum at SLOT_CSUM), then
+// ROW_BYTES per row (top-p: the selection state and the gathered threshold
+// bucket: uint32 keys, float z, int32 index, SK_MAX each).
+constexpr int SLOT_BYTES = 4096;
+constexpr int SLOT_CSUM = 3072;
+constexpr int ROW_GATHER = 256;
+constexpr size_t ROW_BYTES = ROW_GATHER + (size_t)SK_MAX * 12;
+struct SpreadWs {
+    float2 *part;
+    uint8_t *slots, *rows;
+    int nround;
+    __device__ uint8_t *slot(int row, int c) const { return slots + ((size_t)row * nround + c) * SLOT_BYTES; }
+    __device__ uint8_t *rowb(int row) const { return rows + (size_t)row * ROW_BYTES; }
+};
+
+// The row's softmax statistics from its rounds' partials (a fixed order: the
+// same bits in every kernel); false when the row has no finite maximum or
+// sum (all -Inf, NaN, +Inf).
+__device__ bool row_stats(const float2 *pr, int nround, float *s_redf, float &zmax, float &S) {
+    const int t = threadIdx.x;
+    float lm = -__builtin_huge_valf();
+    for (int i = t; i < nround; i += SNT) lm = fmaxf(lm, pr[i].x);
+    zmax = block_max(lm, s_redf);
+    float ls = 0.f;
+    if (zmax > -__builtin_huge_valf())
+        for (int i = t; i < nround; i += SNT) {
+            const float2 p = pr[i];
+            if (p.x > -__builtin_huge_valf()) ls += p.y * pexp(p.x - zmax);
+        }
+    S = block_sum(ls, s_redf);
+    return zmax > -__builtin_huge_valf() && S > 0.f && S < __builtin_huge_valf();
+}
+
 // (max, sum exp(z - max)) of round blockIdx.x of row blockIdx.y: part[row][round].
 __global__ __launch_bounds__(SNT) void chunk_stats_kernel(const float *__restrict__ L, int V, float invT,
                                                           float2 *__restrict__ part) {
@@ -906,17 +958,8 @@ __global__ __launch_bounds__(SNT) void chunk_draw_kernel(const float *__restrict
         return;
     }
     const float2 *pr = part + (size_t)row * nround;
-    float lm = -__builtin_huge_valf();
-    for (int i = t; i < nround; i += SNT) lm = fmaxf(lm, pr[i].x);
-    const float zmax = block_max(lm, s_redf);
-    float ls = 0.f;
-    if (zmax > -__builtin_huge_valf())
-        for (int i = t; i < nround; i += SNT) {
-            const float2 p = pr[i];
-            if (p.x > -__builtin_huge_valf()) ls += p.y * pexp(p.x - zmax);
-        }
-    const float S = block_sum(ls, s_redf);
-    if (!(zmax > -__builtin_huge_valf() && S > 0.f && S < __builtin_huge_valf())) {
+    float zmax, S;
+    if (!row_stats(pr, nround, s_redf, zmax, S)) {
         if (t == 0) out[row] = V - 1;
         return;
     }
@@ -980,8 +1023,7 @@ constexpr int SK_SPREAD = 64;
 // Chunk blockIdx.x of row blockIdx.y: its top-K candidates (z and token id,
 // index order) to cz / ci [row][chunk][SK_SPREAD], their count to cn.
 __global__ __launch_bounds__(SNT) void chunk_topk_kernel(const float *__restrict__ L, int V, float invT, int K,
-                                                         const float2 *__restrict__ part, float *__restrict__ cz,
-                                                         int32_t *__restrict__ ci, int32_t *__restrict__ cn) {
+                                                         SpreadWs ws) {
     __shared__ float s_redf[2 * SNW];
     __shared__ uint32_t s_redu[SNW];
     __shared__ uint32_t s_hist[256];
@@ -992,6 +1034,7 @@ __global__ __launch_bounds__(SNT) void chunk_topk_kernel(const float *__restrict
     __shared__ float s_cz[SK_MAX];
     __shared__ int s_ncnt;
     const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x, nround = gridDim.x;
+    const float2 *part = ws.part;
     float lm = -__builtin_huge_valf();
     for (int i = t; i < nround; i += SNT) lm = fmaxf(lm, part[(size_t)row * nround + i].x);
     const float zm = block_max(lm, s_redf);
@@ -1021,19 +1064,22 @@ __global__ __launch_bounds__(SNT) void chunk_topk_kernel(const float *__restrict
     const int eq_before = (int)(ex >> 16);
     int pos = (int)(ex & 0xffffu) + min(max(rem, 0), eq_before);
     int er = eq_before;
-    const size_t base = ((size_t)row * nround + c) * SK_SPREAD;
+    uint8_t *sl = ws.slot(row, c);
+    float *cz = (float *)sl;
+    int32_t *ci = (int32_t *)(sl + SK_SPREAD * 4);
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         if (g[e] || (q[e] && er < rem)) {
             if (pos < SK_SPREAD) {
-                cz[base + pos] = z[e];
-                ci[base + pos] = c * SROUND + 4 * t + e;
+                cz[pos] = z[e];
+                ci[pos] = c * SROUND + 4 * t + e;
             }
             pos++;
         }
         if (q[e]) er++;
     }
-    if (t == 0) cn[(size_t)row * nround + c] = min((int)(tot & 0xffffu) + min(max(rem, 0), (int)(tot >> 16)), SK_SPREAD);
+    if (t == 0)
+        *(int32_t *)(sl + SK_SPREAD * 8) = min((int)(tot & 0xffffu) + min(max(rem, 0), (int)(tot >> 16)), SK_SPREAD);
 }
 
 // select_threshold over n values in LDS (MASS off): the bucket of pass A,
@@ -1091,9 +1137,7 @@ __device__ void select_lds(const float *z, int n, float zmax, unsigned long long
 
 // Row blockIdx.x: the chunks' candidates gathered in index order, the row's
 // top-K among them, then draw_candidates as draft_sample_kernel's top-k path.
-__global__ __launch_bounds__(SNT) void topk_draw_kernel(int V, SampleArgs a, const float2 *__restrict__ part,
-                                                        const float *__restrict__ cz, const int32_t *__restrict__ ci,
-                                                        const int32_t *__restrict__ cn, const float *__restrict__ u,
+__global__ __launch_bounds__(SNT) void topk_draw_kernel(int V, SampleArgs a, SpreadWs ws, const float *__restrict__ u,
                                                         int32_t *__restrict__ out) {
     __shared__ float s_redf[2 * SNW];
     __shared__ uint32_t s_redu[SNW];
@@ -1115,26 +1159,27 @@ __global__ __launch_bounds__(SNT) void topk_draw_kernel(int V, SampleArgs a, con
         return;
     }
     float lm = -__builtin_huge_valf();
-    for (int i = t; i < nround; i += SNT) lm = fmaxf(lm, part[(size_t)row * nround + i].x);
+    for (int i = t; i < nround; i += SNT) lm = fmaxf(lm, ws.part[(size_t)row * nround + i].x);
     const float zm = block_max(lm, s_redf);
     if (t < 64) {  // chunk offsets (nround <= 64: one per lane)
-        const int cnt = t < nround ? cn[(size_t)row * nround + t] : 0;
+        const int cnt = t < nround ? *(const int32_t *)(ws.slot(row, t) + SK_SPREAD * 8) : 0;
         int inc = cnt;
         for (int o = 1; o < 64; o <<= 1) {
             const int y = __shfl_up(inc, o);
             if (t >= o) inc += y;
         }
         if (t < nround) s_off[t] = inc - cnt;
+        if (t == nround - 1) s_off[nround] = inc;
         if (t == 63) s_off[SPART_ROUNDS] = inc;
     }
     __syncthreads();
     const int n = s_off[SPART_ROUNDS];
     for (int i = t; i < nround * SK_SPREAD; i += SNT) {
         const int c = i / SK_SPREAD, j = i - c * SK_SPREAD;
-        if (j < cn[(size_t)row * nround + c]) {
-            const size_t src = ((size_t)row * nround + c) * SK_SPREAD + j;
-            s_gz[s_off[c] + j] = cz[src];
-            s_gi[s_off[c] + j] = ci[src];
+        const uint8_t *sl = ws.slot(row, c);
+        if (j < s_off[c + 1] - s_off[c]) {
+            s_gz[s_off[c] + j] = ((const float *)sl)[j];
+            s_gi[s_off[c] + j] = ((const int32_t *)(sl + SK_SPREAD * 4))[j];
         }
     }
     __syncthreads();
@@ -1178,6 +1223,366 @@ __global__ __launch_bounds__(SNT) void topk_draw_kernel(int V, SampleArgs a, con
     draw_candidates(nk, a, ur, V, s_cidx, s_cp, s_sort, s_redf, s_redi, out + row);
 }
 
+// Spread top-p and min-p (no top-k): the row's statistics from the chunk
+// partials; for top-p the chunks' pass-A histograms (counts and 2^-40 masses
+// of the buckets below the row maximum) merged per row to the threshold
+// bucket, that bucket's elements gathered in index order, the key passes
+// over them (or over the row when the bucket holds more than SK_MAX), the
+// ties at the threshold kept lowest index first; then each chunk's sum of
+// the kept probabilities and one workgroup per row drawing from those sums,
+// as draft_sample_kernel's whole-row path does (the same threshold rules).
+enum : int { SEL_SELECT = 0, SEL_ALL = 1, SEL_DEGEN = 2 };
+struct RowSel {
+    int mode;
+    uint32_t zb, tau;
+    int tie_lim;
+    unsigned long long rem;
+    int nzb;
+    float zmax, S;
+};
+
+__global__ __launch_bounds__(SNT) void chunk_hist_kernel(const float *__restrict__ L, int V, float invT, SpreadWs ws) {
+    __shared__ float s_redf[2 * SNW];
+    __shared__ uint32_t s_hist[256];
+    __shared__ unsigned long long s_mass[256];
+    const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
+    float zmax, S;
+    const bool ok = row_stats(ws.part + (size_t)row * ws.nround, ws.nround, s_redf, zmax, S);
+    if (t < 256) {
+        s_hist[t] = 0;
+        s_mass[t] = 0;
+    }
+    __syncthreads();
+    if (ok) {
+        const float invS = 1.0f / S;
+        float z[4];
+        bool in;
+        load_round(L + (size_t)row * V + (size_t)c * SROUND, min(SROUND, V - c * SROUND), 0, invT, z, in);
+        if (in)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t b = zbin(z[e], zmax);
+                atomicAdd(&s_hist[b], 1u);
+                atomicAdd(&s_mass[b], mass_fx(z[e], zmax, invS));
+            }
+    }
+    __syncthreads();
+    uint8_t *sl = ws.slot(row, c);
+    if (t < 256) {
+        ((uint32_t *)sl)[t] = s_hist[t];
+        ((unsigned long long *)(sl + 1024))[t] = s_mass[t];
+    }
+}
+
+// Row blockIdx.x: the merged histograms, the bucket holding the target mass.
+__global__ __launch_bounds__(SNT) void row_pick_kernel(float top_p, SpreadWs ws) {
+    __shared__ float s_redf[2 * SNW];
+    __shared__ uint32_t s_hist[256];
+    __shared__ unsigned long long s_mass[256];
+    __shared__ uint32_t s_sel[2];
+    __shared__ unsigned long long s_selm[2];
+    const int row = blockIdx.x, t = threadIdx.x, nround = ws.nround;
+    RowSel *rs = (RowSel *)ws.rowb(row);
+    float zmax, S;
+    if (!row_stats(ws.part + (size_t)row * nround, nround, s_redf, zmax, S)) {
+        if (t == 0) rs->mode = SEL_DEGEN;
+        return;
+    }
+    if (t < 256) {
+        uint32_t h = 0;
+        unsigned long long m = 0;
+#pragma unroll 8
+        for (int c = 0; c < nround; c++) {
+            const uint8_t *sl = ws.slot(row, c);
+            h += ((const uint32_t *)sl)[t];
+            m += ((const unsigned long long *)(sl + 1024))[t];
+        }
+        s_hist[t] = h;
+        s_mass[t] = m;
+    }
+    __syncthreads();
+    const float tp = fmaxf(top_p, 0.f) * 1099511627776.0f;
+    const unsigned long long target = tp < 1.0f ? 1ull : (unsigned long long)ceilf(tp);
+    pick_bucket<true>(s_hist, s_mass, target, s_sel, s_selm, false);
+    __syncthreads();
+    if (t == 0) {
+        const uint32_t zb = s_sel[0];
+        const unsigned long long above = s_selm[0];
+        rs->zmax = zmax;
+        rs->S = S;
+        if (above == ~0ull) {
+            rs->mode = SEL_ALL;
+        } else {
+            rs->mode = SEL_SELECT;
+            rs->zb = zb;
+            rs->rem = target - above;
+            rs->nzb = (int)s_hist[zb];
+        }
+    }
+}
+
+// Chunk blockIdx.x of row blockIdx.y: its elements of the threshold bucket
+// (key, z, index) at their index-order place in the row's gather.
+__global__ __launch_bounds__(SNT) void chunk_gather_kernel(const float *__restrict__ L, int V, float invT, SpreadWs ws) {
+    __shared__ uint32_t s_redu[SNW];
+    const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
+    const RowSel *rs = (const RowSel *)ws.rowb(row);
+    if (rs->mode != SEL_SELECT || rs->nzb > SK_MAX) return;
+    const uint32_t zb = rs->zb;
+    const float zmax = rs->zmax;
+    uint32_t tot;
+    const uint32_t before = t < c ? ((const uint32_t *)ws.slot(row, t))[zb] : 0u;  // (c < nround <= SNT)
+    block_excl_scan_u(before, s_redu, tot);
+    const uint32_t off = tot;
+    float z[4];
+    bool in;
+    load_round(L + (size_t)row * V + (size_t)c * SROUND, min(SROUND, V - c * SROUND), 0, invT, z, in);
+    bool q[4];
+    uint32_t nq = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        q[e] = in && zbin(z[e], zmax) == zb;
+        nq += q[e];
+    }
+    uint32_t tq;
+    uint32_t pos = off + block_excl_scan_u(nq, s_redu, tq);
+    uint8_t *g = ws.rowb(row) + ROW_GATHER;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        if (q[e] && pos < (uint32_t)SK_MAX) {  // (pos < nzb: the counts of chunk_hist_kernel)
+            ((uint32_t *)g)[pos] = okey(z[e]);
+            ((float *)(g + SK_MAX * 4))[pos] = z[e];
+            ((int32_t *)(g + SK_MAX * 8))[pos] = c * SROUND + 4 * t + e;
+            pos++;
+        }
+}
+
+// Row blockIdx.x: the key passes inside the threshold bucket, then the ties
+// kept at the threshold (the first n_eq in index order).
+__global__ __launch_bounds__(SNT) void row_select_kernel(const float *__restrict__ L, int V, float invT, SpreadWs ws) {
+    __shared__ uint32_t s_redu[SNW];
+    __shared__ int s_redi[SNW];
+    __shared__ uint32_t s_hist[256];
+    __shared__ unsigned long long s_mass[256];
+    __shared__ uint32_t s_sel[2];
+    __shared__ unsigned long long s_selm[2];
+    __shared__ uint32_t s_ck[SK_MAX];
+    __shared__ float s_cz[SK_MAX];
+    __shared__ int s_ci[SK_MAX];
+    const int row = blockIdx.x, t = threadIdx.x, nround = ws.nround;
+    RowSel *rs = (RowSel *)ws.rowb(row);
+    if (rs->mode != SEL_SELECT) return;
+    const float zmax = rs->zmax, S = rs->S;
+    const int nzb = rs->nzb;
+    const bool gathered = nzb <= SK_MAX;
+    const float *Lr = L + (size_t)row * V;
+    if (gathered) {
+        const uint8_t *g = ws.rowb(row) + ROW_GATHER;
+        for (int i = t; i < nzb; i += SNT) {
+            s_ck[i] = ((const uint32_t *)g)[i];
+            s_cz[i] = ((const float *)(g + SK_MAX * 4))[i];
+            s_ci[i] = ((const int32_t *)(g + SK_MAX * 8))[i];
+        }
+    }
+    __syncthreads();
+    Select R;
+    R.zb = rs->zb;
+    R.tau = 0u;
+    R.rem = rs->rem;
+    R.cnt = 0;
+    R.all = false;
+    refine_threshold<true>(Lr, V, nround, invT, zmax, S, gathered, nzb, s_hist, s_mass, s_sel, s_selm, s_ck, s_cz, R);
+    if (R.all) {
+        if (t == 0) rs->mode = SEL_ALL;
+        return;
+    }
+    const uint32_t zb = R.zb, tau = R.tau;
+    // ties at tau share one probability: keep the first n_eq of them
+    const float ptau = pexp(okey_inv(tau) - zmax) * (1.0f / S);
+    const unsigned long long mt = (unsigned long long)(ptau * 1099511627776.0f);
+    unsigned long long n_eq = mt ? (R.rem + mt - 1) / mt : (unsigned long long)R.cnt;
+    if (n_eq < 1) n_eq = 1;
+    int tie_lim = V;
+    if (n_eq < R.cnt) {
+        if (gathered) {  // the gather is in index order: slots 4 t .. 4 t + 3
+            bool q[4];
+            uint32_t nq = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int j = 4 * t + e;
+                q[e] = j < nzb && s_ck[j] == tau;
+                nq += q[e];
+            }
+            uint32_t tot;
+            int cnum = (int)block_excl_scan_u(nq, s_redu, tot);
+            int cand = INT_MAX;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (q[e]) {
+                    cnum++;
+                    if (cnum == (int)n_eq && cand == INT_MAX) cand = s_ci[4 * t + e] + 1;
+                }
+            tie_lim = block_min_i(cand, s_redi);
+        } else {
+            int run = 0, lim = V;
+            for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int r) {
+                bool q[4];
+                uint32_t nq = 0;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    q[e] = in && zbin(z[e], zmax) == zb && okey(z[e]) == tau;
+                    nq += q[e];
+                }
+                uint32_t tot;
+                const uint32_t ex = block_excl_scan_u(nq, s_redu, tot);
+                int cand = INT_MAX;
+                int cc = run + (int)ex;
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (q[e]) {
+                        cc++;
+                        if (cc == (int)n_eq && cand == INT_MAX) cand = r * SROUND + 4 * t + e + 1;
+                    }
+                const int got = block_min_i(cand, s_redi);
+                if (lim == V && got != INT_MAX) lim = got;
+                run += (int)tot;
+            });
+            tie_lim = lim;
+        }
+    }
+    if (t == 0) {
+        rs->tau = tau;
+        rs->tie_lim = tie_lim;
+    }
+}
+
+// Whether entry j (z) stays in the draw: top-p (TOPP) by the row's
+// selection, min-p by p = exp(z - zmax) / S >= min_p / S.
+struct Keep {
+    bool topp, all;
+    uint32_t zb, tau;
+    int tie_lim;
+    float zmax, invS, thr;
+    __device__ bool operator()(float z, int j, float p) const {
+        if (topp) return all || above_threshold(z, j, zmax, zb, tau, tie_lim);
+        return !(p < thr);
+    }
+};
+__device__ bool load_keep(const SpreadWs &ws, int row, bool topp, float min_p, float zmax, float S, Keep &k) {
+    k.topp = topp;
+    k.zmax = zmax;
+    k.invS = 1.0f / S;
+    k.thr = k.invS * min_p;  // (min-p: the largest probability is exp(0) / S)
+    k.all = false;
+    k.zb = 256u;
+    k.tau = 0u;
+    k.tie_lim = 0;
+    if (!topp) return true;
+    const RowSel *rs = (const RowSel *)ws.rowb(row);
+    if (rs->mode == SEL_DEGEN) return false;
+    k.all = rs->mode == SEL_ALL;
+    k.zb = rs->zb;
+    k.tau = rs->tau;
+    k.tie_lim = rs->tie_lim;
+    return true;
+}
+
+// Chunk blockIdx.x of row blockIdx.y: the sum of its kept probabilities.
+__global__ __launch_bounds__(SNT) void chunk_keptsum_kernel(const float *__restrict__ L, int V, float invT, bool topp,
+                                                            float min_p, SpreadWs ws) {
+    __shared__ float s_redf[2 * SNW];
+    const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
+    float zmax, S;
+    if (!row_stats(ws.part + (size_t)row * ws.nround, ws.nround, s_redf, zmax, S)) return;
+    Keep keep;
+    if (!load_keep(ws, row, topp, min_p, zmax, S, keep)) return;
+    float z[4];
+    bool in;
+    load_round(L + (size_t)row * V + (size_t)c * SROUND, min(SROUND, V - c * SROUND), 0, invT, z, in);
+    float sum = 0.f;
+    if (in)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float p = pexp(z[e] - zmax) * keep.invS;
+            if (keep(z[e], c * SROUND + 4 * t + e, p)) sum += p;
+        }
+    sum = block_sum(sum, s_redf);
+    if (t == 0) *(float *)(ws.slot(row, c) + SLOT_CSUM) = sum;
+}
+
+// Row blockIdx.x: the kept mass, each round's share of it, the round holding
+// u, then the index inside it (as chunk_draw_kernel over the kept entries).
+__global__ __launch_bounds__(SNT) void keep_draw_kernel(const float *__restrict__ L, int V, float invT, bool topp,
+                                                        float min_p, SpreadWs ws, const float *__restrict__ u,
+                                                        int32_t *__restrict__ out) {
+    __shared__ float s_redf[2 * SNW];
+    __shared__ int s_redi[SNW];
+    __shared__ float s_round[SMAX_ROUNDS];
+    __shared__ float s_before;
+    __shared__ int s_rr;
+    const int row = blockIdx.x, t = threadIdx.x, nround = ws.nround;
+    const float ur = u[row];
+    if (!(ur > 0.f)) {
+        if (t == 0) out[row] = 0;
+        return;
+    }
+    float zmax, S;
+    Keep keep;
+    if (!row_stats(ws.part + (size_t)row * nround, nround, s_redf, zmax, S) ||
+        !load_keep(ws, row, topp, min_p, zmax, S, keep)) {
+        if (t == 0) out[row] = V - 1;
+        return;
+    }
+    float lt = 0.f;
+    for (int i = t; i < nround; i += SNT) lt += *(const float *)(ws.slot(row, i) + SLOT_CSUM);
+    const float total = block_sum(lt, s_redf);
+    const float inv = total > 0.f ? 1.0f / total : 1.0f;
+    for (int i = t; i < nround; i += SNT) s_round[i] = *(const float *)(ws.slot(row, i) + SLOT_CSUM) * inv;
+    __syncthreads();
+    if (t == 0) {
+        float cum = 0.f;
+        int rr = -1;
+        for (int r = 0; r < nround; r++) {
+            const float nc = cum + s_round[r];
+            if (ur <= nc) {
+                rr = r;
+                break;
+            }
+            cum = nc;
+        }
+        s_rr = rr;
+        s_before = cum;
+    }
+    __syncthreads();
+    const int rr = s_rr;
+    const float before = s_before;
+    if (rr < 0) {
+        if (t == 0) out[row] = V - 1;
+        return;
+    }
+    float z[4], v[4];
+    bool in;
+    load_round(L + (size_t)row * V, V, rr, invT, z, in);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float p = pexp(z[e] - zmax) * keep.invS;
+        v[e] = in && keep(z[e], rr * SROUND + 4 * t + e, p) ? p * inv : 0.f;
+    }
+    float tot;
+    const int hit = first_cdf_hit(v, in ? 4 : 0, before, ur, s_redf, tot);
+    const int local = block_min_i(hit, s_redi);
+    int last = INT_MAX;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        if (v[e] > 0.f) last = INT_MAX - (4 * t + e);
+    const int lastk = block_min_i(last, s_redi);
+    if (t == 0) {
+        const int tok =
+            local != INT_MAX ? rr * SROUND + local : lastk != INT_MAX ? rr * SROUND + (INT_MAX - lastk) : V - 1;
+        out[row] = min(tok, V - 1);
+    }
+}
+
 // In place on rows of logits: for every distinct id of the row's list in
 // [0, V): x -= presence (if presence != 0), then x = x > 0 ? x / rep : x * rep
 // (if rep != 1). A bitmap in LDS skips repeated ids.
@@ -1218,44 +1623,60 @@ hipError_t launch_sample(const float *L, int rows, int V, float T, int top_k, fl
     return hipGetLastError();
 }
 
-// spread workspace, 524 bytes per chunk of each row: float2 part[rows][nround],
-// then (top-k) float cz[rows][nround][SK_SPREAD], int32 ci[same], int32 cn[rows][nround]
 size_t sample_spread_ws(int rows, int V) {
     const size_t rc = (size_t)rows * ((V + SROUND - 1) / SROUND);
-    return rc * (sizeof(float2) + 2 * SK_SPREAD * 4 + 4);
+    return rc * (sizeof(float2) + SLOT_BYTES) + (size_t)rows * ROW_BYTES;
 }
 
-// Plain draws (T > 0, no top-k, top-p or min-p) with each row spread over
-// workgroups of one round each: chunk statistics, then one workgroup per row
+// Rows spread over workgroups of one round each (chunk statistics first):
+// plain draws (T > 0, no top-k, top-p or min-p), then one workgroup per row
 // merges them, picks the round and scans it (as draft_sample_kernel's draw);
-// top-k from 1 to SK_SPREAD over at most SPART_ROUNDS rounds: chunk
-// statistics (the row maximum), each chunk's top-k, then one workgroup per
-// row draws among the candidates; every other setting runs
-// draft_sample_kernel. ws: sample_spread_ws bytes.
+// top-k from 1 to SK_SPREAD over at most SPART_ROUNDS rounds: each chunk's
+// top-k, then one workgroup per row draws among the candidates; top-p alone
+// (threshold histograms, pick, gather, key passes) or min-p alone: the
+// chunks' kept sums, then the draw. Every other setting runs
+// draft_sample_kernel. ws: sample_spread_ws bytes (8-byte aligned).
 hipError_t launch_sample_spread(const float *L, int rows, int V, float T, int top_k, float top_p, float min_p,
                                 const float *u, int32_t *out, void *ws, hipStream_t st) {
     const int nround = (V + SROUND - 1) / SROUND;
-    const bool plain = T > 0.f && top_k == 0 && top_p >= 1.0f && min_p <= 0.f;
-    const bool topk = T > 0.f && top_k >= 1 && top_k <= SK_SPREAD && nround <= SPART_ROUNDS;
-    if (!plain && !topk) return launch_sample(L, rows, V, T, top_k, top_p, min_p, u, out, st);
+    const bool live = T > 0.f && nround <= SMAX_ROUNDS;
+    const bool plain = live && top_k == 0 && top_p >= 1.0f && min_p <= 0.f;
+    const bool topk = live && top_k >= 1 && top_k <= SK_SPREAD && nround <= SPART_ROUNDS;
+    const bool topp = live && top_k == 0 && top_p < 1.0f && min_p <= 0.f;
+    const bool minp = live && top_k == 0 && top_p >= 1.0f && min_p > 0.f;
+    if (!plain && !topk && !topp && !minp) return launch_sample(L, rows, V, T, top_k, top_p, min_p, u, out, st);
     const float invT = 1.0f / T;
     const size_t rc = (size_t)rows * nround;
     uint8_t *w = (uint8_t *)ws;
-    float2 *part = (float2 *)w;
-    chunk_stats_kernel<<<dim3(nround, rows), SNT, 0, st>>>(L, V, invT, part);
+    const SpreadWs W{(float2 *)w, w + rc * sizeof(float2), w + rc * (sizeof(float2) + SLOT_BYTES), nround};
+    const dim3 chunks(nround, rows);
+    chunk_stats_kernel<<<chunks, SNT, 0, st>>>(L, V, invT, W.part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (plain) {
-        chunk_draw_kernel<<<rows, SNT, 0, st>>>(L, V, invT, part, u, out);
+        chunk_draw_kernel<<<rows, SNT, 0, st>>>(L, V, invT, W.part, u, out);
         return hipGetLastError();
     }
-    float *cz = (float *)(w + rc * sizeof(float2));
-    int32_t *ci = (int32_t *)(cz + rc * SK_SPREAD);
-    int32_t *cn = ci + rc * SK_SPREAD;
-    chunk_topk_kernel<<<dim3(nround, rows), SNT, 0, st>>>(L, V, invT, top_k, part, cz, ci, cn);
+    if (topk) {
+        chunk_topk_kernel<<<chunks, SNT, 0, st>>>(L, V, invT, top_k, W);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        const SampleArgs a{T, top_k, top_p, min_p};
+        topk_draw_kernel<<<rows, SNT, 0, st>>>(V, a, W, u, out);
+        return hipGetLastError();
+    }
+    if (topp) {
+        chunk_hist_kernel<<<chunks, SNT, 0, st>>>(L, V, invT, W);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        row_pick_kernel<<<rows, SNT, 0, st>>>(top_p, W);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        chunk_gather_kernel<<<chunks, SNT, 0, st>>>(L, V, invT, W);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        row_select_kernel<<<rows, SNT, 0, st>>>(L, V, invT, W);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    chunk_keptsum_kernel<<<chunks, SNT, 0, st>>>(L, V, invT, topp, min_p, W);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    const SampleArgs a{T, top_k, top_p, min_p};
-    topk_draw_kernel<<<rows, SNT, 0, st>>>(V, a, part, cz, ci, cn, u, out);
+    keep_draw_kernel<<<rows, SNT, 0, st>>>(L, V, invT, topp, min_p, W, u, out);
     return hipGetLastError();
 }
 

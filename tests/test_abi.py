@@ -141,15 +141,16 @@ def test_sampler_argument_checks(lib):
     assert b"top_k" in lib.ihip_last_error()
     assert lib.ihip_sample(p16, 1, 8, 1.0, -1, 1.0, 0.0, p16, p16, None) == -22
     assert lib.ihip_sample(p16, 1, 8, 1.0, 0, float("nan"), 0.0, p16, p16, None) == -22
-    # ihip_sample_ex: the same checks, plus its workspace (524 bytes per 4096 logits of each row)
+    # ihip_sample_ex: the same checks, plus its workspace (4104 bytes per 4096 logits of each row, and
+    # 49408 bytes per row)
     nb = C.c_size_t()
-    assert lib.ihip_sample_ws_bytes(2, 151936, C.byref(nb)) == 0 and nb.value == 2 * 38 * 524
+    assert lib.ihip_sample_ws_bytes(2, 151936, C.byref(nb)) == 0 and nb.value == 2 * 38 * 4104 + 2 * 49408
     assert lib.ihip_sample_ws_bytes(1, 6, C.byref(nb)) == -22
     assert lib.ihip_sample_ws_bytes(1, 8, None) == -14
-    assert lib.ihip_sample_ex(p16, 1, 8, 1.0, 0, 1.0, 0.0, p16, p16, None, 1024, None) == -14  # no workspace
+    assert lib.ihip_sample_ex(p16, 1, 8, 1.0, 0, 1.0, 0.0, p16, p16, None, 1 << 20, None) == -14  # no workspace
     assert lib.ihip_sample_ex(p16, 2, 151936, 1.0, 0, 1.0, 0.0, p16, p16, p16, 8, None) == -12  # too small
-    assert lib.ihip_sample_ex(p16, 1, 8, 1.0, 0, 1.0, 0.0, p16, p16, p16 + 4, 1024, None) == -22  # alignment
-    assert lib.ihip_sample_ex(p16, 1, 8, -1.0, 0, 1.0, 0.0, p16, p16, p16, 1024, None) == -22
+    assert lib.ihip_sample_ex(p16, 1, 8, 1.0, 0, 1.0, 0.0, p16, p16, p16 + 4, 1 << 20, None) == -22  # alignment
+    assert lib.ihip_sample_ex(p16, 1, 8, -1.0, 0, 1.0, 0.0, p16, p16, p16, 1 << 20, None) == -22
     assert lib.ihip_apply_penalties(None, 1, 8, p16, 1, 0, 0.5, 1.0, None) == -14
     assert lib.ihip_apply_penalties(p16, 1, 300000, p16, 1, 0, 0.5, 1.0, None) == -22
     assert lib.ihip_apply_penalties(p16, 2, 8, p16, 4, 2, 0.5, 1.0, None) == -22  # stride < n_tok

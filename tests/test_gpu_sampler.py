@@ -188,6 +188,51 @@ def test_topk_spread_matches_one_workgroup(ih):
                                                 dict(temperature=0.9, top_k=40)), r
 
 
+def test_topp_minp_spread(ih):
+    """Top-p alone and min-p alone, spread over workgroups of 4096 logits
+    (ihip_sample_ex: threshold histograms, the bucket's gather, key passes,
+    kept sums) and in one workgroup per row, against the oracle: Gaussian
+    rows at V = 151936 and 300000, quantized rows whose threshold bucket
+    holds ties (gathered at V = 8192, over the row at V = 16384), a flat row
+    (every logit tied: the first n kept), rows all -Inf or holding NaN or
+    +Inf (V - 1), and u = 0 (the first index)."""
+    rng = np.random.default_rng(23)
+    cases = [(3.0 * rng.standard_normal((16, VOCAB))).astype(np.float32),
+             (3.0 * rng.standard_normal((4, 300000))).astype(np.float32),
+             rng.integers(0, 3, size=(16, 8192)).astype(np.float32),
+             rng.integers(0, 3, size=(8, 16384)).astype(np.float32)]
+    settings = [dict(temperature=0.8, top_p=0.9), dict(temperature=1.0, top_p=0.5), dict(temperature=0.7, top_p=0.0),
+                dict(temperature=1.0, min_p=0.05), dict(temperature=0.9, min_p=0.3)]
+    for L in cases:
+        us = rng.random(L.shape[0]).astype(np.float32)
+        for kw in settings:
+            want = [O.softmax_sample(L[r], float(us[r]), **kw) for r in range(L.shape[0])]
+            for spread in (True, False):
+                got = _draw(ih, L, us, spread=spread, **kw)
+                bad = 0
+                for r in range(L.shape[0]):
+                    if got[r] != want[r]:
+                        assert _near_boundary(L[r], float(us[r]), int(got[r]), want[r], kw), \
+                            (spread, L.shape, kw, r, got[r], want[r])
+                        bad += 1
+                assert bad <= 1, (spread, L.shape, kw)
+    flat = np.zeros(8192, np.float32)
+    uf = np.array([0.01, 0.3, 0.49, 0.77, 0.999], np.float32)
+    V = 4096
+    a = np.full(V, -np.inf, np.float32)
+    b = np.zeros(V, np.float32)
+    b[7] = np.nan
+    d = np.zeros(V, np.float32)
+    d[5] = np.inf
+    for spread in (True, False):
+        assert list(_draw(ih, flat, uf, top_p=0.5, spread=spread)) == [math.ceil(4096 * u) - 1 for u in uf]
+        assert list(_draw(ih, flat, uf, min_p=0.5, spread=spread)) == [math.ceil(8192 * u) - 1 for u in uf]
+        for kw in (dict(top_p=0.9), dict(min_p=0.05)):
+            for x in (a, b, d):
+                assert list(_draw(ih, x, [0.1, 0.9], spread=spread, **kw)) == [V - 1] * 2, (spread, kw)
+            assert list(_draw(ih, flat, [0.0], spread=spread, **kw)) == [0]
+
+
 def test_topk_ties_exact(ih):
     # all equal: top_k = 5 keeps indices 0..4, token = ceil(5 u) - 1
     Z = np.zeros(4096, np.float32)
