@@ -429,8 +429,8 @@ int ihip_sample(const float *logits_dev, int rows, int V, float T, int top_k,
  * spread each row over workgroups of 4096 logits (their softmax
  * statistics, then the draw inside the round that holds u); so do top-k
  * from 1 to 64 at V <= 262144 (each chunk's top-k, then the row's among
- * them: the tokens of ihip_sample), top-p alone (the threshold's histograms
- * merged per row) and min-p alone; every other setting runs as
+ * them: the tokens of ihip_sample), and top-p and / or min-p without top-k
+ * (the threshold's histograms merged per row); every other setting runs as
  * ihip_sample. The same softmax_sample
  * (src/ModelCPU.jl:1123-1200) and the same contract: draws match the exact
  * cumulative distribution except within rounding of a step. */

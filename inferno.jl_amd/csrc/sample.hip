@@ -23,8 +23,8 @@
 //    it (statistics, nucleus mass or min-p mass) where V <= 262144.
 //  * the threshold's refinement passes run over the first pass's bucket
 //    gathered into LDS when it holds at most 4096 elements.
-//  * with a workspace, plain draws, top-k up to 64, and top-p or min-p
-//    alone spread each row over workgroups of one round (chunk statistics,
+//  * with a workspace, plain draws, top-k up to 64, and top-p and / or
+//    min-p without top-k spread each row over workgroups of one round (chunk statistics,
 //    each chunk's top-k candidates or threshold histograms and kept sums),
 //    and one workgroup per row finishes each stage from them.
 // Sums and scans are trees, where the reference accumulates sequentially:
@@ -1223,7 +1223,7 @@ __global__ __launch_bounds__(SNT) void topk_draw_kernel(int V, SampleArgs a, Spr
     draw_candidates(nk, a, ur, V, s_cidx, s_cp, s_sort, s_redf, s_redi, out + row);
 }
 
-// Spread top-p and min-p (no top-k): the row's statistics from the chunk
+// Spread top-p and / or min-p (no top-k): the row's statistics from the chunk
 // partials; for top-p the chunks' pass-A histograms (counts and 2^-40 masses
 // of the buckets below the row maximum) merged per row to the threshold
 // bucket, that bucket's elements gathered in index order, the key passes
@@ -1456,65 +1456,89 @@ __global__ __launch_bounds__(SNT) void row_select_kernel(const float *__restrict
     }
 }
 
-// Whether entry j (z) stays in the draw: top-p (TOPP) by the row's
-// selection, min-p by p = exp(z - zmax) / S >= min_p / S.
+// An entry's probability through the cuts: p = exp(z - zmax) / S, 0 when
+// top-p (the row's selection) drops it; with min-p, renormalized by the
+// nucleus mass (inv1 = 1 / its total; 1 without top-p) and 0 below
+// thr = inv1 / S * min_p (the largest probability times min_p).
 struct Keep {
-    bool topp, all;
+    bool topp, minp, all;
     uint32_t zb, tau;
     int tie_lim;
-    float zmax, invS, thr;
-    __device__ bool operator()(float z, int j, float p) const {
-        if (topp) return all || above_threshold(z, j, zmax, zb, tau, tie_lim);
-        return !(p < thr);
+    float zmax, invS, inv1, thr;
+    __device__ float p1(float z, int j) const {
+        if (topp && !(all || above_threshold(z, j, zmax, zb, tau, tie_lim))) return 0.f;
+        float p = pexp(z - zmax) * invS;
+        if (minp) {
+            if (topp) p = p * inv1;
+            if (p < thr) return 0.f;
+        }
+        return p;
     }
 };
-__device__ bool load_keep(const SpreadWs &ws, int row, bool topp, float min_p, float zmax, float S, Keep &k) {
+
+// 1 / the sum of the row's chunk values at byte `off` of their slots (a
+// fixed order), or 1 when it is not positive.
+__device__ float kept_inv(const SpreadWs &ws, int row, int off, float *s_redf) {
+    float l = 0.f;
+    for (int i = threadIdx.x; i < ws.nround; i += SNT) l += *(const float *)(ws.slot(row, i) + off);
+    const float total = block_sum(l, s_redf);
+    return total > 0.f ? 1.0f / total : 1.0f;
+}
+
+// false for a row without finite statistics (no draw); minp: the min-p
+// stage (its inv1 from the top-p stage's kept sums).
+__device__ bool load_keep(const SpreadWs &ws, int row, bool topp, bool minp, float min_p, float zmax, float S,
+                          float *s_redf, Keep &k) {
     k.topp = topp;
+    k.minp = minp;
     k.zmax = zmax;
     k.invS = 1.0f / S;
-    k.thr = k.invS * min_p;  // (min-p: the largest probability is exp(0) / S)
     k.all = false;
     k.zb = 256u;
     k.tau = 0u;
     k.tie_lim = 0;
-    if (!topp) return true;
-    const RowSel *rs = (const RowSel *)ws.rowb(row);
-    if (rs->mode == SEL_DEGEN) return false;
-    k.all = rs->mode == SEL_ALL;
-    k.zb = rs->zb;
-    k.tau = rs->tau;
-    k.tie_lim = rs->tie_lim;
+    k.inv1 = 1.0f;
+    if (topp) {
+        const RowSel *rs = (const RowSel *)ws.rowb(row);
+        if (rs->mode == SEL_DEGEN) return false;
+        k.all = rs->mode == SEL_ALL;
+        k.zb = rs->zb;
+        k.tau = rs->tau;
+        k.tie_lim = rs->tie_lim;
+        if (minp) k.inv1 = kept_inv(ws, row, SLOT_CSUM, s_redf);
+    }
+    k.thr = k.invS * k.inv1 * min_p;
     return true;
 }
 
-// Chunk blockIdx.x of row blockIdx.y: the sum of its kept probabilities.
+// Chunk blockIdx.x of row blockIdx.y: the sum of its kept probabilities,
+// stage 0 (top-p) at SLOT_CSUM, stage 1 (min-p, after top-p if topp) at
+// SLOT_CSUM + 4.
 __global__ __launch_bounds__(SNT) void chunk_keptsum_kernel(const float *__restrict__ L, int V, float invT, bool topp,
-                                                            float min_p, SpreadWs ws) {
+                                                            int stage, float min_p, SpreadWs ws) {
     __shared__ float s_redf[2 * SNW];
     const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
     float zmax, S;
     if (!row_stats(ws.part + (size_t)row * ws.nround, ws.nround, s_redf, zmax, S)) return;
     Keep keep;
-    if (!load_keep(ws, row, topp, min_p, zmax, S, keep)) return;
+    if (!load_keep(ws, row, topp, stage == 1, min_p, zmax, S, s_redf, keep)) return;
     float z[4];
     bool in;
     load_round(L + (size_t)row * V + (size_t)c * SROUND, min(SROUND, V - c * SROUND), 0, invT, z, in);
     float sum = 0.f;
     if (in)
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const float p = pexp(z[e] - zmax) * keep.invS;
-            if (keep(z[e], c * SROUND + 4 * t + e, p)) sum += p;
-        }
+        for (int e = 0; e < 4; e++) sum += keep.p1(z[e], c * SROUND + 4 * t + e);
     sum = block_sum(sum, s_redf);
-    if (t == 0) *(float *)(ws.slot(row, c) + SLOT_CSUM) = sum;
+    if (t == 0) *(float *)(ws.slot(row, c) + SLOT_CSUM + 4 * stage) = sum;
 }
 
-// Row blockIdx.x: the kept mass, each round's share of it, the round holding
-// u, then the index inside it (as chunk_draw_kernel over the kept entries).
+// Row blockIdx.x: the kept mass of the last stage, each round's share of
+// it, the round holding u, then the index inside it (as chunk_draw_kernel
+// over the kept entries).
 __global__ __launch_bounds__(SNT) void keep_draw_kernel(const float *__restrict__ L, int V, float invT, bool topp,
-                                                        float min_p, SpreadWs ws, const float *__restrict__ u,
-                                                        int32_t *__restrict__ out) {
+                                                        bool minp, float min_p, SpreadWs ws,
+                                                        const float *__restrict__ u, int32_t *__restrict__ out) {
     __shared__ float s_redf[2 * SNW];
     __shared__ int s_redi[SNW];
     __shared__ float s_round[SMAX_ROUNDS];
@@ -1529,15 +1553,13 @@ __global__ __launch_bounds__(SNT) void keep_draw_kernel(const float *__restrict_
     float zmax, S;
     Keep keep;
     if (!row_stats(ws.part + (size_t)row * nround, nround, s_redf, zmax, S) ||
-        !load_keep(ws, row, topp, min_p, zmax, S, keep)) {
+        !load_keep(ws, row, topp, minp, min_p, zmax, S, s_redf, keep)) {
         if (t == 0) out[row] = V - 1;
         return;
     }
-    float lt = 0.f;
-    for (int i = t; i < nround; i += SNT) lt += *(const float *)(ws.slot(row, i) + SLOT_CSUM);
-    const float total = block_sum(lt, s_redf);
-    const float inv = total > 0.f ? 1.0f / total : 1.0f;
-    for (int i = t; i < nround; i += SNT) s_round[i] = *(const float *)(ws.slot(row, i) + SLOT_CSUM) * inv;
+    const int off = SLOT_CSUM + (minp ? 4 : 0);
+    const float inv = kept_inv(ws, row, off, s_redf);
+    for (int i = t; i < nround; i += SNT) s_round[i] = *(const float *)(ws.slot(row, i) + off) * inv;
     __syncthreads();
     if (t == 0) {
         float cum = 0.f;
@@ -1564,10 +1586,7 @@ __global__ __launch_bounds__(SNT) void keep_draw_kernel(const float *__restrict_
     bool in;
     load_round(L + (size_t)row * V, V, rr, invT, z, in);
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const float p = pexp(z[e] - zmax) * keep.invS;
-        v[e] = in && keep(z[e], rr * SROUND + 4 * t + e, p) ? p * inv : 0.f;
-    }
+    for (int e = 0; e < 4; e++) v[e] = in ? keep.p1(z[e], rr * SROUND + 4 * t + e) * inv : 0.f;
     float tot;
     const int hit = first_cdf_hit(v, in ? 4 : 0, before, ur, s_redf, tot);
     const int local = block_min_i(hit, s_redi);
@@ -1632,18 +1651,18 @@ size_t sample_spread_ws(int rows, int V) {
 // plain draws (T > 0, no top-k, top-p or min-p), then one workgroup per row
 // merges them, picks the round and scans it (as draft_sample_kernel's draw);
 // top-k from 1 to SK_SPREAD over at most SPART_ROUNDS rounds: each chunk's
-// top-k, then one workgroup per row draws among the candidates; top-p alone
-// (threshold histograms, pick, gather, key passes) or min-p alone: the
-// chunks' kept sums, then the draw. Every other setting runs
-// draft_sample_kernel. ws: sample_spread_ws bytes (8-byte aligned).
+// top-k, then one workgroup per row draws among the candidates; top-p
+// and / or min-p without top-k (top-p: threshold histograms, pick, gather,
+// key passes): the chunks' kept sums per stage, then the draw. Every other
+// setting runs draft_sample_kernel. ws: sample_spread_ws bytes (8-byte aligned).
 hipError_t launch_sample_spread(const float *L, int rows, int V, float T, int top_k, float top_p, float min_p,
                                 const float *u, int32_t *out, void *ws, hipStream_t st) {
     const int nround = (V + SROUND - 1) / SROUND;
     const bool live = T > 0.f && nround <= SMAX_ROUNDS;
     const bool plain = live && top_k == 0 && top_p >= 1.0f && min_p <= 0.f;
     const bool topk = live && top_k >= 1 && top_k <= SK_SPREAD && nround <= SPART_ROUNDS;
-    const bool topp = live && top_k == 0 && top_p < 1.0f && min_p <= 0.f;
-    const bool minp = live && top_k == 0 && top_p >= 1.0f && min_p > 0.f;
+    const bool topp = live && top_k == 0 && top_p < 1.0f;
+    const bool minp = live && top_k == 0 && min_p > 0.f;
     if (!plain && !topk && !topp && !minp) return launch_sample(L, rows, V, T, top_k, top_p, min_p, u, out, st);
     const float invT = 1.0f / T;
     const size_t rc = (size_t)rows * nround;
@@ -1674,9 +1693,11 @@ hipError_t launch_sample_spread(const float *L, int rows, int V, float T, int to
         row_select_kernel<<<rows, SNT, 0, st>>>(L, V, invT, W);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    chunk_keptsum_kernel<<<chunks, SNT, 0, st>>>(L, V, invT, topp, min_p, W);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    keep_draw_kernel<<<rows, SNT, 0, st>>>(L, V, invT, topp, min_p, W, u, out);
+    for (int stage = topp ? 0 : 1; stage <= (minp ? 1 : 0); stage++) {
+        chunk_keptsum_kernel<<<chunks, SNT, 0, st>>>(L, V, invT, topp, stage, min_p, W);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    keep_draw_kernel<<<rows, SNT, 0, st>>>(L, V, invT, topp, minp, min_p, W, u, out);
     return hipGetLastError();
 }
 

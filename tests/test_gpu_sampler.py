@@ -189,9 +189,10 @@ def test_topk_spread_matches_one_workgroup(ih):
 
 
 def test_topp_minp_spread(ih):
-    """Top-p alone and min-p alone, spread over workgroups of 4096 logits
-    (ihip_sample_ex: threshold histograms, the bucket's gather, key passes,
-    kept sums) and in one workgroup per row, against the oracle: Gaussian
+    """Top-p and min-p (each alone and together), spread over workgroups of
+    4096 logits (ihip_sample_ex: threshold histograms, the bucket's gather,
+    key passes, kept sums per stage) and in one workgroup per row, against
+    the oracle: Gaussian
     rows at V = 151936 and 300000, quantized rows whose threshold bucket
     holds ties (gathered at V = 8192, over the row at V = 16384), a flat row
     (every logit tied: the first n kept), rows all -Inf or holding NaN or
@@ -202,7 +203,8 @@ def test_topp_minp_spread(ih):
              rng.integers(0, 3, size=(16, 8192)).astype(np.float32),
              rng.integers(0, 3, size=(8, 16384)).astype(np.float32)]
     settings = [dict(temperature=0.8, top_p=0.9), dict(temperature=1.0, top_p=0.5), dict(temperature=0.7, top_p=0.0),
-                dict(temperature=1.0, min_p=0.05), dict(temperature=0.9, min_p=0.3)]
+                dict(temperature=1.0, min_p=0.05), dict(temperature=0.9, min_p=0.3),
+                dict(temperature=0.8, top_p=0.9, min_p=0.02), dict(temperature=1.0, top_p=0.5, min_p=0.3)]
     for L in cases:
         us = rng.random(L.shape[0]).astype(np.float32)
         for kw in settings:
@@ -227,7 +229,8 @@ def test_topp_minp_spread(ih):
     for spread in (True, False):
         assert list(_draw(ih, flat, uf, top_p=0.5, spread=spread)) == [math.ceil(4096 * u) - 1 for u in uf]
         assert list(_draw(ih, flat, uf, min_p=0.5, spread=spread)) == [math.ceil(8192 * u) - 1 for u in uf]
-        for kw in (dict(top_p=0.9), dict(min_p=0.05)):
+        assert list(_draw(ih, flat, uf, top_p=0.5, min_p=0.5, spread=spread)) == [math.ceil(4096 * u) - 1 for u in uf]
+        for kw in (dict(top_p=0.9), dict(min_p=0.05), dict(top_p=0.9, min_p=0.05)):
             for x in (a, b, d):
                 assert list(_draw(ih, x, [0.1, 0.9], spread=spread, **kw)) == [V - 1] * 2, (spread, kw)
             assert list(_draw(ih, flat, [0.0], spread=spread, **kw)) == [0]
