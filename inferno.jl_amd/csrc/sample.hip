@@ -284,7 +284,12 @@ __device__ __forceinline__ unsigned long long mass_fx(float z, float zmax, float
 // Passes B: the exact key inside bucket R.zb, 8 bits a pass from the top,
 // R.rem units still to reach; over the nzb gathered keys and values (ck, cz)
 // when gathered, else over the row. R.tau, R.rem and R.cnt on return, or
-// R.all when (MASS) truncated masses fall just short of the target.
+// R.all when (MASS) truncated masses fall just short of the target. At most
+// SPAIR_MAX gathered elements are ranked directly instead: tau is the key
+// whose larger keys hold less than R.rem units and which with its equals
+// reaches it (integer sums: the key the passes would find; MASS: the
+// elements' units staged in mass[], which holds 256).
+constexpr int SPAIR_MAX = 128;
 template <bool MASS>
 __device__ void refine_threshold(const float *__restrict__ row, int V, int nround, float T, float zmax, float S,
                                  bool gathered, int nzb, uint32_t *hist, unsigned long long *mass, uint32_t *sel,
@@ -292,6 +297,58 @@ __device__ void refine_threshold(const float *__restrict__ row, int V, int nroun
     const int t = threadIdx.x;
     const uint32_t zb = R.zb;
     const float invS = 1.0f / S;
+    if (gathered && nzb <= SPAIR_MAX) {
+        if (t == 0) {
+            sel[0] = 0u;
+            sel[1] = 0u;
+            selm[0] = ~0ull;
+        }
+        if (MASS && t < nzb) mass[t] = mass_fx(cz[t], zmax, invS);  // (each element's units, once)
+        __syncthreads();
+        // element i = t / P compared with every P-th element from t % P (at
+        // most 16 comparisons a lane); the P lanes of an element (adjacent,
+        // in one wave) then add their sums
+        int lp = 0;
+        while (nzb > (16 << lp)) lp++;  // (nzb <= SPAIR_MAX: P = 2^lp <= 8)
+        const int P = 1 << lp, i = t >> lp;
+        const bool act = i < nzb;
+        const uint32_t ki = act ? ck[i] : 0u;
+        unsigned long long gt = 0, eq = 0;
+        uint32_t ne = 0;
+        if (act)
+            for (int j = t & (P - 1); j < nzb; j += P) {
+                const uint32_t kj = ck[j];
+                const unsigned long long mj = MASS ? mass[j] : 1ull;
+                if (kj > ki) {
+                    gt += mj;
+                } else if (kj == ki) {
+                    eq += mj;
+                    ne++;
+                }
+            }
+        for (int o = 1; o < P; o <<= 1) {
+            gt += __shfl_xor(gt, o);
+            eq += __shfl_xor(eq, o);
+            ne += __shfl_xor(ne, o);
+        }
+        if (act && (t & (P - 1)) == 0 && gt < R.rem && R.rem <= gt + eq) {  // (every element of key ki writes the same)
+            sel[0] = ki;
+            sel[1] = ne;
+            selm[0] = gt;
+        }
+        __syncthreads();
+        const uint32_t tau = sel[0], cnt = sel[1];
+        const unsigned long long above = selm[0];
+        __syncthreads();
+        if (above == ~0ull) {
+            R.all = true;
+            return;
+        }
+        R.rem -= above;
+        R.cnt = cnt;
+        R.tau = tau;
+        return;
+    }
     uint32_t prefix = 0, pmask = 0;
     for (int shift = 24; shift >= 0; shift -= 8) {
         if (t < 256) {
@@ -1082,10 +1139,12 @@ __global__ __launch_bounds__(SNT) void chunk_topk_kernel(const float *__restrict
         *(int32_t *)(sl + SK_SPREAD * 8) = min((int)(tot & 0xffffu) + min(max(rem, 0), (int)(tot >> 16)), SK_SPREAD);
 }
 
-// select_threshold over n values in LDS (MASS off): the bucket of pass A,
-// then the key inside it, 8 bits a pass; R.all when fewer than target.
-__device__ void select_lds(const float *z, int n, float zmax, unsigned long long target, uint32_t *hist,
-                           uint32_t *sel, unsigned long long *selm, Select &R) {
+// select_threshold over the n slots of z in LDS whose id is >= 0 (MASS
+// off): the bucket of pass A, its keys gathered into ck (n entries), then
+// refine_threshold; R.all when fewer than target.
+__device__ void select_lds(const float *z, const int *id, int n, float zmax, unsigned long long target,
+                           uint32_t *hist, uint32_t *sel, unsigned long long *selm, uint32_t *ck, int *ncnt,
+                           Select &R) {
     const int t = threadIdx.x;
     R.zb = 255u;
     R.tau = 0u;
@@ -1093,8 +1152,10 @@ __device__ void select_lds(const float *z, int n, float zmax, unsigned long long
     R.cnt = 0;
     R.all = false;
     if (t < 256) hist[t] = 0;
+    if (t == 0) *ncnt = 0;
     __syncthreads();
-    for (int i = t; i < n; i += SNT) atomicAdd(&hist[zbin(z[i], zmax)], 1u);
+    for (int i = t; i < n; i += SNT)
+        if (id[i] >= 0) atomicAdd(&hist[zbin(z[i], zmax)], 1u);
     __syncthreads();
     pick_bucket<false>(hist, nullptr, R.rem, sel, selm, false);
     __syncthreads();
@@ -1107,32 +1168,10 @@ __device__ void select_lds(const float *z, int n, float zmax, unsigned long long
     }
     R.rem -= aboveA;
     R.zb = zb;
-    uint32_t prefix = 0, pmask = 0;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        if (t < 256) hist[t] = 0;
-        __syncthreads();
-        for (int i = t; i < n; i += SNT) {
-            const uint32_t k = okey(z[i]);
-            if ((k & pmask) != prefix || zbin(z[i], zmax) != zb) continue;
-            atomicAdd(&hist[(k >> shift) & 255u], 1u);
-        }
-        __syncthreads();
-        pick_bucket<false>(hist, nullptr, R.rem, sel, selm, true);
-        __syncthreads();
-        const uint32_t b = sel[0];
-        const unsigned long long above = selm[0];
-        const uint32_t cb = hist[b];
-        __syncthreads();
-        if (above == ~0ull) {
-            R.all = true;
-            return;
-        }
-        R.rem -= above;
-        prefix |= b << shift;
-        pmask |= 255u << shift;
-        R.cnt = cb;
-    }
-    R.tau = prefix;
+    for (int i = t; i < n; i += SNT)
+        if (id[i] >= 0 && zbin(z[i], zmax) == zb) ck[atomicAdd(ncnt, 1)] = okey(z[i]);
+    __syncthreads();
+    refine_threshold<false>(nullptr, 0, 0, 1.f, zmax, 1.f, true, *ncnt, hist, nullptr, sel, selm, ck, nullptr, R);
 }
 
 // Row blockIdx.x: the chunks' candidates gathered in index order, the row's
@@ -1145,12 +1184,12 @@ __global__ __launch_bounds__(SNT) void topk_draw_kernel(int V, SampleArgs a, Spr
     __shared__ uint32_t s_hist[256];
     __shared__ uint32_t s_sel[2];
     __shared__ unsigned long long s_selm[2];
-    __shared__ int s_off[SPART_ROUNDS + 1];
     __shared__ float s_gz[SK_MAX];
     __shared__ int s_gi[SK_MAX];
     __shared__ int s_cidx[SK_MAX];
     __shared__ float s_cp[SK_MAX];
     __shared__ int s_sort[SK_MAX];
+    __shared__ int s_ncnt;
     const int row = blockIdx.x, t = threadIdx.x;
     const int nround = (V + SROUND - 1) / SROUND;
     const float ur = u[row];
@@ -1158,42 +1197,30 @@ __global__ __launch_bounds__(SNT) void topk_draw_kernel(int V, SampleArgs a, Spr
         if (t == 0) out[row] = 0;
         return;
     }
-    float lm = -__builtin_huge_valf();
-    for (int i = t; i < nround; i += SNT) lm = fmaxf(lm, ws.part[(size_t)row * nround + i].x);
-    const float zm = block_max(lm, s_redf);
-    if (t < 64) {  // chunk offsets (nround <= 64: one per lane)
-        const int cnt = t < nround ? *(const int32_t *)(ws.slot(row, t) + SK_SPREAD * 8) : 0;
-        int inc = cnt;
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(inc, o);
-            if (t >= o) inc += y;
-        }
-        if (t < nround) s_off[t] = inc - cnt;
-        if (t == nround - 1) s_off[nround] = inc;
-        if (t == 63) s_off[SPART_ROUNDS] = inc;
-    }
-    __syncthreads();
-    const int n = s_off[SPART_ROUNDS];
-    for (int i = t; i < nround * SK_SPREAD; i += SNT) {
+    // chunk c's candidates at slots c * SK_SPREAD + j (j < its count; id -1
+    // beyond): index order, loaded with the statistics, no offsets needed
+    const int n = nround * SK_SPREAD;  // <= SK_MAX
+    for (int i = t; i < n; i += SNT) {
         const int c = i / SK_SPREAD, j = i - c * SK_SPREAD;
         const uint8_t *sl = ws.slot(row, c);
-        if (j < s_off[c + 1] - s_off[c]) {
-            s_gz[s_off[c] + j] = ((const float *)sl)[j];
-            s_gi[s_off[c] + j] = ((const int32_t *)(sl + SK_SPREAD * 4))[j];
-        }
+        const bool live = j < *(const int32_t *)(sl + SK_SPREAD * 8);
+        s_gz[i] = live ? ((const float *)sl)[j] : 0.f;
+        s_gi[i] = live ? ((const int32_t *)(sl + SK_SPREAD * 4))[j] : -1;
     }
-    __syncthreads();
+    float lm = -__builtin_huge_valf();
+    for (int i = t; i < nround; i += SNT) lm = fmaxf(lm, ws.part[(size_t)row * nround + i].x);
+    const float zm = block_max(lm, s_redf);  // (its barriers also publish the slots)
     Select R;
-    select_lds(s_gz, n, zm, (unsigned long long)a.top_k, s_hist, s_sel, s_selm, R);
+    select_lds(s_gz, s_gi, n, zm, (unsigned long long)a.top_k, s_hist, s_sel, s_selm, (uint32_t *)s_sort, &s_ncnt, R);
     const uint32_t zb = R.zb, tau = R.tau;
     const int rem = (int)R.rem;
-    // the kept candidates in index order (positions 4 t .. 4 t + 3: n <= SK_MAX)
+    // the kept candidates in index order (slots 4 t .. 4 t + 3: n <= SK_MAX)
     bool g[4], q[4];
     uint32_t ng = 0, nq = 0;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         const int j = 4 * t + e;
-        const bool live = j < n;
+        const bool live = j < n && s_gi[j] >= 0;
         const float z = live ? s_gz[j] : 0.f;
         const uint32_t b = zbin(z, zm), k = okey(z);
         g[e] = live && (R.all || b < zb || (b == zb && k > tau));
