@@ -906,6 +906,7 @@ def sampler_config(ih):
                 "top_k=50,top_p=0.95": dict(temperature=0.7, top_k=50, top_p=0.95),
                 "top_p=0.9": dict(temperature=0.8, top_p=0.9), "min_p=0.05": dict(temperature=1.0, min_p=0.05),
                 "top_p=0.9,min_p=0.02": dict(temperature=0.8, top_p=0.9, min_p=0.02),
+                "top_k=1000": dict(temperature=0.8, top_k=1000),
                 "greedy": dict(temperature=0.0)}
     g = torch.Generator(device="cuda").manual_seed(SEED)
     out = {"V": V, "us_per_call": {}}
@@ -917,7 +918,7 @@ def sampler_config(ih):
         for name, kw in settings.items():
             t = graph_time(lambda: [ih.softmax_sample(L, u, out=tok, ws=ws, **kw) for _ in range(10)]) / 10
             out["us_per_call"][f"rows={rows},{name}"] = round(t * 1e6, 1)
-        for name in ("plain", "top_k=40", "top_p=0.9", "min_p=0.05", "top_p=0.9,min_p=0.02"):
+        for name in ("plain", "top_k=40", "top_p=0.9", "min_p=0.05", "top_p=0.9,min_p=0.02", "top_k=1000"):
             kw = settings[name]
             t = graph_time(lambda: [ih.softmax_sample(L, u, out=tok, spread=False, **kw) for _ in range(10)]) / 10
             out["us_per_call"][f"rows={rows},{name},one_workgroup"] = round(t * 1e6, 1)

@@ -23,8 +23,8 @@
 //    it (statistics, nucleus mass or min-p mass) where V <= 262144.
 //  * the threshold's refinement passes run over the first pass's bucket
 //    gathered into LDS when it holds at most 4096 elements.
-//  * with a workspace, plain draws, top-k up to 64, and top-p and / or
-//    min-p without top-k spread each row over workgroups of one round (chunk statistics,
+//  * with a workspace, every setting but greedy and top-k above 64 with
+//    top-p spreads each row over workgroups of one round (chunk statistics,
 //    each chunk's top-k candidates or threshold histograms and kept sums),
 //    and one workgroup per row finishes each stage from them.
 // Sums and scans are trees, where the reference accumulates sequentially:
@@ -957,8 +957,10 @@ struct SpreadWs {
 
 // The row's softmax statistics from its rounds' partials (a fixed order: the
 // same bits in every kernel); false when the row has no finite maximum or
-// sum (all -Inf, NaN, +Inf).
-__device__ bool row_stats(const float2 *pr, int nround, float *s_redf, float &zmax, float &S) {
+// sum (all -Inf, NaN, +Inf). count (a top-k threshold, whose softmax is
+// over the kept entries only): S = 1, false only without a finite maximum
+// (a NaN entry falls in the tail bucket and stays out of the top k).
+__device__ bool row_stats(const float2 *pr, int nround, float *s_redf, float &zmax, float &S, bool count = false) {
     const int t = threadIdx.x;
     float lm = -__builtin_huge_valf();
     for (int i = t; i < nround; i += SNT) lm = fmaxf(lm, pr[i].x);
@@ -970,6 +972,10 @@ __device__ bool row_stats(const float2 *pr, int nround, float *s_redf, float &zm
             if (p.x > -__builtin_huge_valf()) ls += p.y * pexp(p.x - zmax);
         }
     S = block_sum(ls, s_redf);
+    if (count) {
+        S = 1.0f;
+        return zmax > -__builtin_huge_valf() && zmax < __builtin_huge_valf();
+    }
     return zmax > -__builtin_huge_valf() && S > 0.f && S < __builtin_huge_valf();
 }
 
@@ -1268,13 +1274,14 @@ struct RowSel {
     float zmax, S;
 };
 
-__global__ __launch_bounds__(SNT) void chunk_hist_kernel(const float *__restrict__ L, int V, float invT, SpreadWs ws) {
+__global__ __launch_bounds__(SNT) void chunk_hist_kernel(const float *__restrict__ L, int V, float invT, bool count,
+                                                         SpreadWs ws) {
     __shared__ float s_redf[2 * SNW];
     __shared__ uint32_t s_hist[256];
     __shared__ unsigned long long s_mass[256];
     const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
     float zmax, S;
-    const bool ok = row_stats(ws.part + (size_t)row * ws.nround, ws.nround, s_redf, zmax, S);
+    const bool ok = row_stats(ws.part + (size_t)row * ws.nround, ws.nround, s_redf, zmax, S, count);
     if (t < 256) {
         s_hist[t] = 0;
         s_mass[t] = 0;
@@ -1290,7 +1297,7 @@ __global__ __launch_bounds__(SNT) void chunk_hist_kernel(const float *__restrict
             for (int e = 0; e < 4; e++) {
                 const uint32_t b = zbin(z[e], zmax);
                 atomicAdd(&s_hist[b], 1u);
-                atomicAdd(&s_mass[b], mass_fx(z[e], zmax, invS));
+                if (!count) atomicAdd(&s_mass[b], mass_fx(z[e], zmax, invS));
             }
     }
     __syncthreads();
@@ -1301,8 +1308,9 @@ __global__ __launch_bounds__(SNT) void chunk_hist_kernel(const float *__restrict
     }
 }
 
-// Row blockIdx.x: the merged histograms, the bucket holding the target mass.
-__global__ __launch_bounds__(SNT) void row_pick_kernel(float top_p, SpreadWs ws) {
+// Row blockIdx.x: the merged histograms, the bucket holding the target mass
+// (top_k > 0: the bucket holding the top_k-th element).
+__global__ __launch_bounds__(SNT) void row_pick_kernel(float top_p, int top_k, SpreadWs ws) {
     __shared__ float s_redf[2 * SNW];
     __shared__ uint32_t s_hist[256];
     __shared__ unsigned long long s_mass[256];
@@ -1311,7 +1319,7 @@ __global__ __launch_bounds__(SNT) void row_pick_kernel(float top_p, SpreadWs ws)
     const int row = blockIdx.x, t = threadIdx.x, nround = ws.nround;
     RowSel *rs = (RowSel *)ws.rowb(row);
     float zmax, S;
-    if (!row_stats(ws.part + (size_t)row * nround, nround, s_redf, zmax, S)) {
+    if (!row_stats(ws.part + (size_t)row * nround, nround, s_redf, zmax, S, top_k > 0)) {
         if (t == 0) rs->mode = SEL_DEGEN;
         return;
     }
@@ -1329,8 +1337,12 @@ __global__ __launch_bounds__(SNT) void row_pick_kernel(float top_p, SpreadWs ws)
     }
     __syncthreads();
     const float tp = fmaxf(top_p, 0.f) * 1099511627776.0f;
-    const unsigned long long target = tp < 1.0f ? 1ull : (unsigned long long)ceilf(tp);
-    pick_bucket<true>(s_hist, s_mass, target, s_sel, s_selm, false);
+    const unsigned long long target =
+        top_k > 0 ? (unsigned long long)top_k : tp < 1.0f ? 1ull : (unsigned long long)ceilf(tp);
+    if (top_k > 0)
+        pick_bucket<false>(s_hist, nullptr, target, s_sel, s_selm, false);
+    else
+        pick_bucket<true>(s_hist, s_mass, target, s_sel, s_selm, false);
     __syncthreads();
     if (t == 0) {
         const uint32_t zb = s_sel[0];
@@ -1385,8 +1397,10 @@ __global__ __launch_bounds__(SNT) void chunk_gather_kernel(const float *__restri
 }
 
 // Row blockIdx.x: the key passes inside the threshold bucket, then the ties
-// kept at the threshold (the first n_eq in index order).
-__global__ __launch_bounds__(SNT) void row_select_kernel(const float *__restrict__ L, int V, float invT, SpreadWs ws) {
+// kept at the threshold (the first n_eq in index order; count: top-k, n_eq
+// the units left at tau).
+__global__ __launch_bounds__(SNT) void row_select_kernel(const float *__restrict__ L, int V, float invT, bool count,
+                                                         SpreadWs ws) {
     __shared__ uint32_t s_redu[SNW];
     __shared__ int s_redi[SNW];
     __shared__ uint32_t s_hist[256];
@@ -1418,16 +1432,24 @@ __global__ __launch_bounds__(SNT) void row_select_kernel(const float *__restrict
     R.rem = rs->rem;
     R.cnt = 0;
     R.all = false;
-    refine_threshold<true>(Lr, V, nround, invT, zmax, S, gathered, nzb, s_hist, s_mass, s_sel, s_selm, s_ck, s_cz, R);
+    if (count)
+        refine_threshold<false>(Lr, V, nround, invT, zmax, 1.f, gathered, nzb, s_hist, s_mass, s_sel, s_selm, s_ck,
+                                s_cz, R);
+    else
+        refine_threshold<true>(Lr, V, nround, invT, zmax, S, gathered, nzb, s_hist, s_mass, s_sel, s_selm, s_ck,
+                               s_cz, R);
     if (R.all) {
         if (t == 0) rs->mode = SEL_ALL;
         return;
     }
     const uint32_t zb = R.zb, tau = R.tau;
     // ties at tau share one probability: keep the first n_eq of them
-    const float ptau = pexp(okey_inv(tau) - zmax) * (1.0f / S);
-    const unsigned long long mt = (unsigned long long)(ptau * 1099511627776.0f);
-    unsigned long long n_eq = mt ? (R.rem + mt - 1) / mt : (unsigned long long)R.cnt;
+    unsigned long long n_eq = R.rem;
+    if (!count) {
+        const float ptau = pexp(okey_inv(tau) - zmax) * (1.0f / S);
+        const unsigned long long mt = (unsigned long long)(ptau * 1099511627776.0f);
+        n_eq = mt ? (R.rem + mt - 1) / mt : (unsigned long long)R.cnt;
+    }
     if (n_eq < 1) n_eq = 1;
     int tie_lim = V;
     if (n_eq < R.cnt) {
@@ -1542,11 +1564,11 @@ __device__ bool load_keep(const SpreadWs &ws, int row, bool topp, bool minp, flo
 // stage 0 (top-p) at SLOT_CSUM, stage 1 (min-p, after top-p if topp) at
 // SLOT_CSUM + 4.
 __global__ __launch_bounds__(SNT) void chunk_keptsum_kernel(const float *__restrict__ L, int V, float invT, bool topp,
-                                                            int stage, float min_p, SpreadWs ws) {
+                                                            bool count, int stage, float min_p, SpreadWs ws) {
     __shared__ float s_redf[2 * SNW];
     const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
     float zmax, S;
-    if (!row_stats(ws.part + (size_t)row * ws.nround, ws.nround, s_redf, zmax, S)) return;
+    if (!row_stats(ws.part + (size_t)row * ws.nround, ws.nround, s_redf, zmax, S, count)) return;
     Keep keep;
     if (!load_keep(ws, row, topp, stage == 1, min_p, zmax, S, s_redf, keep)) return;
     float z[4];
@@ -1564,7 +1586,7 @@ __global__ __launch_bounds__(SNT) void chunk_keptsum_kernel(const float *__restr
 // it, the round holding u, then the index inside it (as chunk_draw_kernel
 // over the kept entries).
 __global__ __launch_bounds__(SNT) void keep_draw_kernel(const float *__restrict__ L, int V, float invT, bool topp,
-                                                        bool minp, float min_p, SpreadWs ws,
+                                                        bool count, bool minp, float min_p, SpreadWs ws,
                                                         const float *__restrict__ u, int32_t *__restrict__ out) {
     __shared__ float s_redf[2 * SNW];
     __shared__ int s_redi[SNW];
@@ -1579,7 +1601,7 @@ __global__ __launch_bounds__(SNT) void keep_draw_kernel(const float *__restrict_
     }
     float zmax, S;
     Keep keep;
-    if (!row_stats(ws.part + (size_t)row * nround, nround, s_redf, zmax, S) ||
+    if (!row_stats(ws.part + (size_t)row * nround, nround, s_redf, zmax, S, count) ||
         !load_keep(ws, row, topp, minp, min_p, zmax, S, s_redf, keep)) {
         if (t == 0) out[row] = V - 1;
         return;
@@ -1679,17 +1701,20 @@ size_t sample_spread_ws(int rows, int V) {
 // merges them, picks the round and scans it (as draft_sample_kernel's draw);
 // top-k from 1 to SK_SPREAD over at most SPART_ROUNDS rounds: each chunk's
 // top-k, then one workgroup per row draws among the candidates; top-p
-// and / or min-p without top-k (top-p: threshold histograms, pick, gather,
-// key passes): the chunks' kept sums per stage, then the draw. Every other
-// setting runs draft_sample_kernel. ws: sample_spread_ws bytes (8-byte aligned).
+// and / or min-p without top-k, or a larger top-k without top-p (its
+// threshold found as top-p's, by count: histograms, pick, gather, key
+// passes): the chunks' kept sums per stage, then the draw. Top-k above
+// SK_SPREAD with top-p runs draft_sample_kernel. ws: sample_spread_ws bytes (8-byte aligned).
 hipError_t launch_sample_spread(const float *L, int rows, int V, float T, int top_k, float top_p, float min_p,
                                 const float *u, int32_t *out, void *ws, hipStream_t st) {
     const int nround = (V + SROUND - 1) / SROUND;
     const bool live = T > 0.f && nround <= SMAX_ROUNDS;
     const bool plain = live && top_k == 0 && top_p >= 1.0f && min_p <= 0.f;
     const bool topk = live && top_k >= 1 && top_k <= SK_SPREAD && nround <= SPART_ROUNDS;
-    const bool topp = live && top_k == 0 && top_p < 1.0f;
-    const bool minp = live && top_k == 0 && min_p > 0.f;
+    // top-k beyond the candidate path, without top-p: the threshold as top-p's, by count
+    const bool bigk = live && top_k > 0 && !topk && top_p >= 1.0f;
+    const bool topp = live && ((top_k == 0 && top_p < 1.0f) || bigk);
+    const bool minp = live && (top_k == 0 || bigk) && min_p > 0.f;
     if (!plain && !topk && !topp && !minp) return launch_sample(L, rows, V, T, top_k, top_p, min_p, u, out, st);
     const float invT = 1.0f / T;
     const size_t rc = (size_t)rows * nround;
@@ -1711,20 +1736,20 @@ hipError_t launch_sample_spread(const float *L, int rows, int V, float T, int to
         return hipGetLastError();
     }
     if (topp) {
-        chunk_hist_kernel<<<chunks, SNT, 0, st>>>(L, V, invT, W);
+        chunk_hist_kernel<<<chunks, SNT, 0, st>>>(L, V, invT, bigk, W);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        row_pick_kernel<<<rows, SNT, 0, st>>>(top_p, W);
+        row_pick_kernel<<<rows, SNT, 0, st>>>(top_p, bigk ? top_k : 0, W);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         chunk_gather_kernel<<<chunks, SNT, 0, st>>>(L, V, invT, W);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        row_select_kernel<<<rows, SNT, 0, st>>>(L, V, invT, W);
+        row_select_kernel<<<rows, SNT, 0, st>>>(L, V, invT, bigk, W);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     for (int stage = topp ? 0 : 1; stage <= (minp ? 1 : 0); stage++) {
-        chunk_keptsum_kernel<<<chunks, SNT, 0, st>>>(L, V, invT, topp, stage, min_p, W);
+        chunk_keptsum_kernel<<<chunks, SNT, 0, st>>>(L, V, invT, topp, bigk, stage, min_p, W);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    keep_draw_kernel<<<rows, SNT, 0, st>>>(L, V, invT, topp, minp, min_p, W, u, out);
+    keep_draw_kernel<<<rows, SNT, 0, st>>>(L, V, invT, topp, bigk, minp, min_p, W, u, out);
     return hipGetLastError();
 }
 

@@ -236,6 +236,53 @@ def test_topp_minp_spread(ih):
             assert list(_draw(ih, flat, [0.0], spread=spread, **kw)) == [0]
 
 
+def test_topk_large_spread(ih):
+    """Top-k above 64 (or at V above 262144), with or without min-p, spread
+    over workgroups of 4096 logits by count (the threshold's histograms
+    merged per row, the bucket's gather and key passes, ties kept lowest
+    index first, softmax over the kept entries) and in one workgroup per
+    row, against the oracle: Gaussian rows at V = 151936 and 300000,
+    quantized rows (ties at the threshold, gathered and over the row), a
+    flat row (the first k), rows all -Inf or +Inf (V - 1) and a row holding
+    a NaN (left out of the top k)."""
+    rng = np.random.default_rng(29)
+    cases = [(3.0 * rng.standard_normal((12, VOCAB))).astype(np.float32),
+             (3.0 * rng.standard_normal((4, 300000))).astype(np.float32),
+             rng.integers(0, 3, size=(12, 8192)).astype(np.float32),
+             rng.integers(0, 3, size=(6, 16384)).astype(np.float32)]
+    settings = [dict(temperature=0.8, top_k=100), dict(temperature=1.0, top_k=1000), dict(temperature=0.7, top_k=4000),
+                dict(temperature=0.9, top_k=100, min_p=0.05), dict(temperature=0.8, top_k=40)]
+    for L in cases:
+        us = rng.random(L.shape[0]).astype(np.float32)
+        for kw in settings:
+            want = [O.softmax_sample(L[r], float(us[r]), **kw) for r in range(L.shape[0])]
+            for spread in (True, False):
+                got = _draw(ih, L, us, spread=spread, **kw)
+                bad = 0
+                for r in range(L.shape[0]):
+                    if got[r] != want[r]:
+                        assert _near_boundary(L[r], float(us[r]), int(got[r]), want[r], kw), \
+                            (spread, L.shape, kw, r, got[r], want[r])
+                        bad += 1
+                assert bad <= 1, (spread, L.shape, kw)
+    flat = np.zeros(8192, np.float32)
+    uf = np.array([0.013, 0.303, 0.487, 0.771, 0.9985], np.float32)
+    V = 4096
+    a = np.full(V, -np.inf, np.float32)
+    d = np.zeros(V, np.float32)
+    d[5] = np.inf
+    b = np.zeros(V, np.float32)
+    b[7] = np.nan
+    for spread in (True, False):
+        assert list(_draw(ih, flat, uf, top_k=100, spread=spread)) == [math.ceil(100 * float(u)) - 1 for u in uf]
+        for kw in (dict(top_k=100), dict(top_k=100, min_p=0.05)):
+            for x in (a, d):
+                assert list(_draw(ih, x, [0.1, 0.9], spread=spread, **kw)) == [V - 1] * 2, (spread, kw)
+            ub = [0.013, 0.303, 0.777]
+            assert list(_draw(ih, b, ub, spread=spread, **kw)) == [O.softmax_sample(b, u, **kw) for u in ub]
+            assert list(_draw(ih, flat, [0.0], spread=spread, **kw)) == [0]
+
+
 def test_topk_ties_exact(ih):
     # all equal: top_k = 5 keeps indices 0..4, token = ceil(5 u) - 1
     Z = np.zeros(4096, np.float32)
