@@ -218,6 +218,46 @@ __device__ int first_cdf_hit(const float (&v)[4], int n_here, float before, floa
     return hit;
 }
 
+// Julia's isless(b, a) (findmax order): NaN above every number, +0.0 above
+// -0.0.
+__device__ __forceinline__ bool jl_beats(float a, float b) {
+    if (isnan(a) || isnan(b)) return isnan(a) && !isnan(b);
+    return a > b || (a == b && signbit(b) && !signbit(a));
+}
+// (v2, i2) before (v, i): a larger value by jl_beats, or an equal one at a
+// lower index; i = INT_MAX is empty.
+__device__ __forceinline__ bool jl_first(float v2, int i2, float v, int i) {
+    if (i2 == INT_MAX) return false;
+    if (i == INT_MAX) return true;
+    return jl_beats(v2, v) || (!jl_beats(v, v2) && i2 < i);
+}
+// The block's first argmax of (v, i) pairs by jl_first: INT_MAX when empty.
+__device__ int block_argmax_jl(float v, int i, float *s_v, int *s_i) {
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v2 = __shfl_xor(v, o);
+        const int i2 = __shfl_xor(i, o);
+        if (jl_first(v2, i2, v, i)) {
+            v = v2;
+            i = i2;
+        }
+    }
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    __syncthreads();
+    if (l == 0) {
+        s_v[w] = v;
+        s_i[w] = i;
+    }
+    __syncthreads();
+    float bv = s_v[0];
+    int bi = s_i[0];
+    for (int k = 1; k < SNW; k++)
+        if (jl_first(s_v[k], s_i[k], bv, bi)) {
+            bv = s_v[k];
+            bi = s_i[k];
+        }
+    return bi;
+}
+
 // Threshold selection counted from the top (the k-th largest z, or the z
 // where the probability mass from the top reaches top_p). Pass A buckets
 // w = zmax - z linearly, 8 buckets per unit of log-probability (bucket 255:
@@ -592,20 +632,21 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
     const float invT = a.T > 0.f ? 1.0f / a.T : 1.0f;
 
     if (a.T == 0.0f) {
-        // first-index argmax (Julia argmax)
+        // Julia's argmax: findmax order (the first NaN above every number,
+        // +0.0 above -0.0), the first index among equals; each thread sees
+        // its indices in increasing order
         float bv = 0.f;
         int bi = INT_MAX;
         for_rounds(Lr, V, nround, 1.0f, [&](const float (&z)[4], bool in, int r) {
             if (!in) return;
 #pragma unroll
             for (int e = 0; e < 4; e++)
-                if (bi == INT_MAX || z[e] > bv) {
+                if (bi == INT_MAX || jl_beats(z[e], bv)) {
                     bv = z[e];
                     bi = r * SROUND + 4 * t + e;
                 }
         });
-        const float m = block_max(bi == INT_MAX ? -__builtin_huge_valf() : bv, s_redf);
-        const int first = block_min_i((bi != INT_MAX && bv == m) ? bi : INT_MAX, s_redi);
+        const int first = block_argmax_jl(bv, bi, s_redf, s_redi);
         if (t == 0) out[row] = first == INT_MAX ? 0 : first;
         return;
     }

@@ -237,11 +237,13 @@ def softmax_sample(logits, r: float, temperature: float = 1.0, top_p: float = 1.
                    min_p: float = 0.0) -> int:
     """softmax_sample (src/ModelCPU.jl:1123-1200), 0-based, with the uniform r
     that the reference draws by rand(Float32) at :1191 given explicitly:
-    T = 0 -> first-index argmax (:1125-1127); otherwise the first i with
-    r <= the (exact, float64) prefix sum of sample_dist, else the last index
-    (:1191-1198); r <= 0 gives index 0 as the reference's loop does."""
+    T = 0 -> Julia's argmax (:1125-1127: findmax order, the first NaN above
+    every number, +0.0 above -0.0, the first of equals; argmax_first);
+    otherwise the first i with r <= the (exact, float64) prefix sum of
+    sample_dist, else the last index (:1191-1198); r <= 0 gives index 0 as
+    the reference's loop does."""
     if temperature == 0.0:
-        return int(np.argmax(np.asarray(logits, dtype=np.float32)))
+        return argmax_first(np.asarray(logits, dtype=np.float32))
     p = sample_dist(logits, temperature, top_p, top_k, min_p)
     c = np.cumsum(p, dtype=np.float64)
     hit = np.nonzero(float(np.float32(r)) <= c)[0]

@@ -67,6 +67,32 @@ def test_known_answers(ih):
     assert set(_draw(ih, ties, np.linspace(0.01, 0.99, 50), top_k=2)) == {1, 2}
 
 
+def test_greedy_julia_order(ih):
+    """T = 0 is Julia's argmax (src/ModelCPU.jl:1125-1127, findmax order):
+    the first NaN above every number, +0.0 above -0.0, the first of equals,
+    index 0 for a row of -Inf; rows of one and of several rounds, against
+    the oracle's argmax_first."""
+    nan, inf = np.nan, np.inf
+    rows = [[1.0, nan, 3.0, nan], [-0.0, 0.0, -0.0, 0.0], [0.0, -0.0, 0.0, 0.0], [-inf] * 4, [-inf, 2.0, inf, inf],
+            [nan, 2.0, 5.0, 1.0], [5.0, 5.0, 1.0, 5.0]]
+    for row in rows:
+        L = np.array(row, np.float32)
+        for spread in (True, False):
+            assert list(_draw(ih, L, [0.5], temperature=0.0, spread=spread)) == [O.argmax_first(L)], (row, spread)
+    rng = np.random.default_rng(31)
+    big = rng.standard_normal((6, 3 * 4096 + 8)).astype(np.float32)
+    big[1, [5000, 9001]] = nan
+    big[2, 4097] = 100.0
+    big[2, 12000] = 100.0
+    big[3, :] = -0.0
+    big[3, 8193] = 0.0
+    big[4, :] = -inf
+    big[5, 7] = inf
+    big[5, 11000] = nan
+    got = _draw(ih, big, np.full(6, 0.5, np.float32), temperature=0.0)
+    assert list(got) == [O.argmax_first(big[r]) for r in range(6)]
+
+
 def _near_boundary(row, u, g, o, kw):
     p = O.sample_dist(row, **kw).astype(np.float64)
     c = np.cumsum(p)

@@ -48,6 +48,11 @@ def test_reference_test_engine_properties():
         assert 0 <= O.softmax_sample(L, r, temperature=0.7) < 4
     ties = np.array([2.0, 3.0, 3.0, 1.0, 3.0], np.float32)
     assert O.softmax_sample(ties, 0.5, temperature=0.0) == 1  # first argmax
+    # T = 0 is Julia's argmax (findmax order): the first NaN wins, +0.0 beats -0.0, -Inf rows give index 0
+    nan, inf = np.nan, np.inf
+    for row, want in (([1.0, nan, 3.0, nan], 1), ([-0.0, 0.0], 1), ([0.0, -0.0, 0.0], 0), ([-inf] * 3, 0),
+                      ([-inf, 2.0, inf, inf], 2), ([nan, 2.0], 0)):
+        assert O.softmax_sample(np.array(row, np.float32), 0.5, temperature=0.0) == want, row
     # top-k ties keep the lowest indices: k = 2 of three 3.0s -> {1, 2}
     assert {O.softmax_sample(ties, r, top_k=2) for r in np.linspace(0.01, 0.99, 50)} == {1, 2}
 
