@@ -270,7 +270,7 @@ def test_topk_large_spread(ih):
     row, against the oracle: Gaussian rows at V = 151936 and 300000,
     quantized rows (ties at the threshold, gathered and over the row), a
     flat row (the first k), rows all -Inf or +Inf (V - 1) and a row holding
-    a NaN (left out of the top k)."""
+    a NaN (left out of the top k; also through the k <= 64 candidate path)."""
     rng = np.random.default_rng(29)
     cases = [(3.0 * rng.standard_normal((12, VOCAB))).astype(np.float32),
              (3.0 * rng.standard_normal((4, 300000))).astype(np.float32),
@@ -301,7 +301,7 @@ def test_topk_large_spread(ih):
     b[7] = np.nan
     for spread in (True, False):
         assert list(_draw(ih, flat, uf, top_k=100, spread=spread)) == [math.ceil(100 * float(u)) - 1 for u in uf]
-        for kw in (dict(top_k=100), dict(top_k=100, min_p=0.05)):
+        for kw in (dict(top_k=100), dict(top_k=100, min_p=0.05), dict(top_k=40), dict(top_k=40, top_p=0.9)):
             for x in (a, d):
                 assert list(_draw(ih, x, [0.1, 0.9], spread=spread, **kw)) == [V - 1] * 2, (spread, kw)
             ub = [0.013, 0.303, 0.777]
