@@ -896,8 +896,8 @@ def sampler_config(ih):
     """The draft-side sampler (ihip_sample_ex: softmax_sample, src/ModelCPU.jl:
     1123-1200; ihip_apply_penalties: :1202-1225) at the LM head's vocabulary
     V = 151936: microseconds per call for 1 and 64 rows (seeded Gaussian
-    logits, sd 3), each call replayed in a HIP graph, plain, top-k, top-p
-    and min-p draws also with one workgroup per row (ihip_sample); beside it the oracle's numpy
+    logits, sd 3), each call replayed in a HIP graph, every setting but
+    top-k 50 + top-p also with one workgroup per row (ihip_sample); beside it the oracle's numpy
     restatement of one row on the host (argsorts for top-k/top-p)."""
     import torch
     import numpy as np
@@ -918,7 +918,7 @@ def sampler_config(ih):
         for name, kw in settings.items():
             t = graph_time(lambda: [ih.softmax_sample(L, u, out=tok, ws=ws, **kw) for _ in range(10)]) / 10
             out["us_per_call"][f"rows={rows},{name}"] = round(t * 1e6, 1)
-        for name in ("plain", "top_k=40", "top_p=0.9", "min_p=0.05", "top_p=0.9,min_p=0.02", "top_k=1000"):
+        for name in ("plain", "top_k=40", "top_p=0.9", "min_p=0.05", "top_p=0.9,min_p=0.02", "top_k=1000", "greedy"):
             kw = settings[name]
             t = graph_time(lambda: [ih.softmax_sample(L, u, out=tok, spread=False, **kw) for _ in range(10)]) / 10
             out["us_per_call"][f"rows={rows},{name},one_workgroup"] = round(t * 1e6, 1)

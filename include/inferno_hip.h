@@ -430,8 +430,9 @@ int ihip_sample(const float *logits_dev, int rows, int V, float T, int top_k,
  * statistics, then the draw inside the round that holds u); so do top-k
  * from 1 to 64 at V <= 262144 (each chunk's top-k, then the row's among
  * them: the tokens of ihip_sample), top-p and / or min-p without top-k,
- * and a larger top-k without top-p (the threshold's histograms merged per
- * row); top-k above 64 with top-p runs as ihip_sample. The same softmax_sample
+ * a larger top-k without top-p (the threshold's histograms merged per
+ * row), and T = 0 (each chunk's first argmax: the tokens of ihip_sample);
+ * top-k above 64 with top-p runs as ihip_sample. The same softmax_sample
  * (src/ModelCPU.jl:1123-1200) and the same contract: draws match the exact
  * cumulative distribution except within rounding of a step. */
 int ihip_sample_ws_bytes(int rows, int V, size_t *bytes);

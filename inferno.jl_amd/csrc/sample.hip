@@ -8,7 +8,8 @@
 // rounds of 4096 logits (one float4 per thread, coalesced), so after the
 // first pass the row (600 KB at V = 151936) is served from L2.
 //
-//  * T = 0: first-index argmax.
+//  * T = 0: Julia's argmax (the first NaN above every number, +0.0 above
+//    -0.0, the first of equals) by an integer key.
 //  * top-k (1 <= k <= 4096, k < V): exact radix select of the k-th largest
 //    z = L / T (8 bits a pass on an order-preserving key), ties at the
 //    threshold kept lowest index first (the stable descending sortperm);
@@ -23,10 +24,10 @@
 //    it (statistics, nucleus mass or min-p mass) where V <= 262144.
 //  * the threshold's refinement passes run over the first pass's bucket
 //    gathered into LDS when it holds at most 4096 elements.
-//  * with a workspace, every setting but greedy and top-k above 64 with
-//    top-p spreads each row over workgroups of one round (chunk statistics,
-//    each chunk's top-k candidates or threshold histograms and kept sums),
-//    and one workgroup per row finishes each stage from them.
+//  * with a workspace, every setting but top-k above 64 with top-p
+//    spreads each row over workgroups of one round (chunk statistics, each
+//    chunk's argmax, top-k candidates or threshold histograms and kept
+//    sums), and one workgroup per row finishes each stage from them.
 // Sums and scans are trees, where the reference accumulates sequentially:
 // the drawn token can differ only where u falls within rounding of a CDF
 // step.
@@ -218,44 +219,25 @@ __device__ int first_cdf_hit(const float (&v)[4], int n_here, float before, floa
     return hit;
 }
 
-// Julia's isless(b, a) (findmax order): NaN above every number, +0.0 above
-// -0.0.
-__device__ __forceinline__ bool jl_beats(float a, float b) {
-    if (isnan(a) || isnan(b)) return isnan(a) && !isnan(b);
-    return a > b || (a == b && signbit(b) && !signbit(a));
+// Julia's findmax order as an unsigned key: the order-preserving key of the
+// float (+0.0 above -0.0), every NaN the largest (NaNs equal: the first
+// wins). A real float's key is at least 1.
+__device__ __forceinline__ uint32_t jl_key(float z) { return isnan(z) ? 0xffffffffu : okey(z); }
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+    for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o));
+    return v;
 }
-// (v2, i2) before (v, i): a larger value by jl_beats, or an equal one at a
-// lower index; i = INT_MAX is empty.
-__device__ __forceinline__ bool jl_first(float v2, int i2, float v, int i) {
-    if (i2 == INT_MAX) return false;
-    if (i == INT_MAX) return true;
-    return jl_beats(v2, v) || (!jl_beats(v, v2) && i2 < i);
-}
-// The block's first argmax of (v, i) pairs by jl_first: INT_MAX when empty.
-__device__ int block_argmax_jl(float v, int i, float *s_v, int *s_i) {
-    for (int o = 32; o > 0; o >>= 1) {
-        const float v2 = __shfl_xor(v, o);
-        const int i2 = __shfl_xor(i, o);
-        if (jl_first(v2, i2, v, i)) {
-            v = v2;
-            i = i2;
-        }
-    }
+// The block's first index holding the largest key (INT_MAX when none: all
+// keys 0); *best_k gets that key.
+__device__ int block_argmax_key(uint32_t k, int i, uint32_t *s_k, int *s_i, uint32_t *best_k = nullptr) {
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    uint32_t m = wave_max_u(k);
     __syncthreads();
-    if (l == 0) {
-        s_v[w] = v;
-        s_i[w] = i;
-    }
+    if (l == 0) s_k[w] = m;
     __syncthreads();
-    float bv = s_v[0];
-    int bi = s_i[0];
-    for (int k = 1; k < SNW; k++)
-        if (jl_first(s_v[k], s_i[k], bv, bi)) {
-            bv = s_v[k];
-            bi = s_i[k];
-        }
-    return bi;
+    m = wave_max_u(l < SNW ? s_k[l] : 0u);
+    if (best_k) *best_k = m;
+    return block_min_i(k == m && m != 0u ? i : INT_MAX, s_i);
 }
 
 // Threshold selection counted from the top (the k-th largest z, or the z
@@ -635,18 +617,20 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
         // Julia's argmax: findmax order (the first NaN above every number,
         // +0.0 above -0.0), the first index among equals; each thread sees
         // its indices in increasing order
-        float bv = 0.f;
+        uint32_t bk = 0u;
         int bi = INT_MAX;
         for_rounds(Lr, V, nround, 1.0f, [&](const float (&z)[4], bool in, int r) {
             if (!in) return;
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                if (bi == INT_MAX || jl_beats(z[e], bv)) {
-                    bv = z[e];
+            for (int e = 0; e < 4; e++) {
+                const uint32_t k = jl_key(z[e]);
+                if (k > bk) {
+                    bk = k;
                     bi = r * SROUND + 4 * t + e;
                 }
+            }
         });
-        const int first = block_argmax_jl(bv, bi, s_redf, s_redi);
+        const int first = block_argmax_key(bk, bi, s_redu, s_redi);
         if (t == 0) out[row] = first == INT_MAX ? 0 : first;
         return;
     }
@@ -1114,6 +1098,54 @@ __global__ __launch_bounds__(SNT) void chunk_draw_kernel(const float *__restrict
             local != INT_MAX ? rr * SROUND + local : lastk != INT_MAX ? rr * SROUND + (INT_MAX - lastk) : V - 1;
         out[row] = min(tok, V - 1);
     }
+}
+
+// Spread greedy draws (T = 0): each chunk's first argmax in Julia's order
+// (its key and index as float bits) into part[row][chunk], then one
+// workgroup per row takes the first of those; an exact order, so the
+// tokens are the one-workgroup kernel's.
+__global__ __launch_bounds__(SNT) void chunk_argmax_kernel(const float *__restrict__ L, int V,
+                                                           float2 *__restrict__ part) {
+    __shared__ uint32_t s_k[SNW];
+    __shared__ int s_i[SNW];
+    const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x, nround = gridDim.x;
+    float z[4];
+    bool in;
+    load_round(L + (size_t)row * V + (size_t)c * SROUND, min(SROUND, V - c * SROUND), 0, 1.0f, z, in);
+    uint32_t bk = 0u;
+    int bi = INT_MAX;
+    if (in)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint32_t k = jl_key(z[e]);
+            if (k > bk) {
+                bk = k;
+                bi = c * SROUND + 4 * t + e;
+            }
+        }
+    uint32_t best;
+    const int first = block_argmax_key(bk, bi, s_k, s_i, &best);
+    if (t == 0) part[(size_t)row * nround + c] = make_float2(__uint_as_float(best), __int_as_float(first));
+}
+
+__global__ __launch_bounds__(SNT) void argmax_draw_kernel(int V, const float2 *__restrict__ part,
+                                                          int32_t *__restrict__ out) {
+    __shared__ uint32_t s_k[SNW];
+    __shared__ int s_i[SNW];
+    const int row = blockIdx.x, t = threadIdx.x;
+    const int nround = (V + SROUND - 1) / SROUND;
+    uint32_t bk = 0u;
+    int bi = INT_MAX;
+    for (int c = t; c < nround; c += SNT) {  // (chunks in index order: the first best stays)
+        const float2 p = part[(size_t)row * nround + c];
+        const uint32_t k = __float_as_uint(p.x);
+        if (k > bk) {
+            bk = k;
+            bi = __float_as_int(p.y);
+        }
+    }
+    const int first = block_argmax_key(bk, bi, s_k, s_i);
+    if (t == 0) out[row] = first == INT_MAX ? 0 : first;
 }
 
 // Spread top-k (1 <= K <= SK_SPREAD, V <= SPART_ROUNDS rounds): every
@@ -1749,6 +1781,14 @@ size_t sample_spread_ws(int rows, int V) {
 hipError_t launch_sample_spread(const float *L, int rows, int V, float T, int top_k, float top_p, float min_p,
                                 const float *u, int32_t *out, void *ws, hipStream_t st) {
     const int nround = (V + SROUND - 1) / SROUND;
+    if (T == 0.f && nround <= SMAX_ROUNDS) {
+        float2 *part = (float2 *)ws;
+        chunk_argmax_kernel<<<dim3(nround, rows), SNT, 0, st>>>(L, V, part);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        argmax_draw_kernel<<<rows, SNT, 0, st>>>(V, part, out);
+        return hipGetLastError();
+    }
     const bool live = T > 0.f && nround <= SMAX_ROUNDS;
     const bool plain = live && top_k == 0 && top_p >= 1.0f && min_p <= 0.f;
     const bool topk = live && top_k >= 1 && top_k <= SK_SPREAD && nround <= SPART_ROUNDS;

@@ -89,8 +89,9 @@ def test_greedy_julia_order(ih):
     big[4, :] = -inf
     big[5, 7] = inf
     big[5, 11000] = nan
-    got = _draw(ih, big, np.full(6, 0.5, np.float32), temperature=0.0)
-    assert list(got) == [O.argmax_first(big[r]) for r in range(6)]
+    want = [O.argmax_first(big[r]) for r in range(6)]
+    for spread in (True, False):  # spread: each chunk's first argmax, then the row's
+        assert list(_draw(ih, big, np.full(6, 0.5, np.float32), temperature=0.0, spread=spread)) == want, spread
 
 
 def _near_boundary(row, u, g, o, kw):
