@@ -1776,8 +1776,9 @@ size_t sample_spread_ws(int rows, int V) {
 // top-k, then one workgroup per row draws among the candidates; top-p
 // and / or min-p without top-k, or a larger top-k without top-p (its
 // threshold found as top-p's, by count: histograms, pick, gather, key
-// passes): the chunks' kept sums per stage, then the draw. Top-k above
-// SK_SPREAD with top-p runs draft_sample_kernel. ws: sample_spread_ws bytes (8-byte aligned).
+// passes): the chunks' kept sums per stage, then the draw; T = 0: each
+// chunk's argmax, then the row's. Top-k above SK_SPREAD with top-p runs
+// draft_sample_kernel. ws: sample_spread_ws bytes (8-byte aligned).
 hipError_t launch_sample_spread(const float *L, int rows, int V, float T, int top_k, float top_p, float min_p,
                                 const float *u, int32_t *out, void *ws, hipStream_t st) {
     const int nround = (V + SROUND - 1) / SROUND;
