@@ -429,10 +429,11 @@ int ihip_sample(const float *logits_dev, int rows, int V, float T, int top_k,
  * spread each row over workgroups of 4096 logits (their softmax
  * statistics, then the draw inside the round that holds u); so do top-k
  * from 1 to 64 at V <= 262144 (each chunk's top-k, then the row's among
- * them: the tokens of ihip_sample), top-p and / or min-p without top-k,
- * a larger top-k without top-p (the threshold's histograms merged per
- * row), and T = 0 (each chunk's first argmax: the tokens of ihip_sample);
- * top-k above 64 with top-p runs as ihip_sample. The same softmax_sample
+ * them: the tokens of ihip_sample), top-p and / or min-p without top-k
+ * (the threshold's histograms merged per row), a larger top-k (its
+ * threshold by count, the kept entries compacted, then ihip_sample's
+ * candidate draw: its tokens), and T = 0 (each chunk's first argmax: the
+ * tokens of ihip_sample). The same softmax_sample
  * (src/ModelCPU.jl:1123-1200) and the same contract: draws match the exact
  * cumulative distribution except within rounding of a step. */
 int ihip_sample_ws_bytes(int rows, int V, size_t *bytes);

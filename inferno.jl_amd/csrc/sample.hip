@@ -24,10 +24,10 @@
 //    it (statistics, nucleus mass or min-p mass) where V <= 262144.
 //  * the threshold's refinement passes run over the first pass's bucket
 //    gathered into LDS when it holds at most 4096 elements.
-//  * with a workspace, every setting but top-k above 64 with top-p
-//    spreads each row over workgroups of one round (chunk statistics, each
-//    chunk's argmax, top-k candidates or threshold histograms and kept
-//    sums), and one workgroup per row finishes each stage from them.
+//  * with a workspace, every setting spreads each row over workgroups of
+//    one round (chunk statistics, each chunk's argmax, top-k candidates,
+//    threshold histograms, kept sums or kept entries), and one workgroup
+//    per row finishes each stage from them.
 // Sums and scans are trees, where the reference accumulates sequentially:
 // the drawn token can differ only where u falls within rounding of a CDF
 // step.
@@ -1637,11 +1637,11 @@ __device__ bool load_keep(const SpreadWs &ws, int row, bool topp, bool minp, flo
 // stage 0 (top-p) at SLOT_CSUM, stage 1 (min-p, after top-p if topp) at
 // SLOT_CSUM + 4.
 __global__ __launch_bounds__(SNT) void chunk_keptsum_kernel(const float *__restrict__ L, int V, float invT, bool topp,
-                                                            bool count, int stage, float min_p, SpreadWs ws) {
+                                                            int stage, float min_p, SpreadWs ws) {
     __shared__ float s_redf[2 * SNW];
     const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
     float zmax, S;
-    if (!row_stats(ws.part + (size_t)row * ws.nround, ws.nround, s_redf, zmax, S, count)) return;
+    if (!row_stats(ws.part + (size_t)row * ws.nround, ws.nround, s_redf, zmax, S)) return;
     Keep keep;
     if (!load_keep(ws, row, topp, stage == 1, min_p, zmax, S, s_redf, keep)) return;
     float z[4];
@@ -1659,7 +1659,7 @@ __global__ __launch_bounds__(SNT) void chunk_keptsum_kernel(const float *__restr
 // it, the round holding u, then the index inside it (as chunk_draw_kernel
 // over the kept entries).
 __global__ __launch_bounds__(SNT) void keep_draw_kernel(const float *__restrict__ L, int V, float invT, bool topp,
-                                                        bool count, bool minp, float min_p, SpreadWs ws,
+                                                        bool minp, float min_p, SpreadWs ws,
                                                         const float *__restrict__ u, int32_t *__restrict__ out) {
     __shared__ float s_redf[2 * SNW];
     __shared__ int s_redi[SNW];
@@ -1674,7 +1674,7 @@ __global__ __launch_bounds__(SNT) void keep_draw_kernel(const float *__restrict_
     }
     float zmax, S;
     Keep keep;
-    if (!row_stats(ws.part + (size_t)row * nround, nround, s_redf, zmax, S, count) ||
+    if (!row_stats(ws.part + (size_t)row * nround, nround, s_redf, zmax, S) ||
         !load_keep(ws, row, topp, minp, min_p, zmax, S, s_redf, keep)) {
         if (t == 0) out[row] = V - 1;
         return;
@@ -1722,6 +1722,101 @@ __global__ __launch_bounds__(SNT) void keep_draw_kernel(const float *__restrict_
             local != INT_MAX ? rr * SROUND + local : lastk != INT_MAX ? rr * SROUND + (INT_MAX - lastk) : V - 1;
         out[row] = min(tok, V - 1);
     }
+}
+
+// Spread top-k above SK_SPREAD (or over more than SPART_ROUNDS rounds), with
+// any top-p / min-p after it: the k-th element's bucket and key by count
+// (as top-p's threshold), then each chunk's kept entries counted, compacted
+// in index order into the row's gather (k <= SK_MAX), and one workgroup per
+// row runs draft_sample_kernel's candidate draw over them: its tokens.
+__global__ __launch_bounds__(SNT) void chunk_keptcount_kernel(const float *__restrict__ L, int V, float invT,
+                                                              SpreadWs ws) {
+    __shared__ uint32_t s_redu[SNW];
+    const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
+    const RowSel *rs = (const RowSel *)ws.rowb(row);
+    const int mode = rs->mode;
+    if (mode == SEL_DEGEN) return;
+    const uint32_t zb = rs->zb, tau = rs->tau;
+    const int tie_lim = rs->tie_lim;
+    const float zmax = rs->zmax;
+    float z[4];
+    bool in;
+    load_round(L + (size_t)row * V + (size_t)c * SROUND, min(SROUND, V - c * SROUND), 0, invT, z, in);
+    uint32_t n = 0;
+    if (in)
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            n += mode == SEL_ALL || above_threshold(z[e], c * SROUND + 4 * t + e, zmax, zb, tau, tie_lim);
+    uint32_t tot;
+    block_excl_scan_u(n, s_redu, tot);
+    if (t == 0) *(uint32_t *)(ws.slot(row, c) + SLOT_CSUM) = tot;
+}
+
+__global__ __launch_bounds__(SNT) void chunk_compact_kernel(const float *__restrict__ L, int V, float invT,
+                                                            SpreadWs ws) {
+    __shared__ uint32_t s_redu[SNW];
+    const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
+    const RowSel *rs = (const RowSel *)ws.rowb(row);
+    const int mode = rs->mode;
+    if (mode == SEL_DEGEN) return;
+    const uint32_t zb = rs->zb, tau = rs->tau;
+    const int tie_lim = rs->tie_lim;
+    const float zmax = rs->zmax;
+    uint32_t tot;
+    const uint32_t before = t < c ? *(const uint32_t *)(ws.slot(row, t) + SLOT_CSUM) : 0u;  // (c < nround <= SNT)
+    block_excl_scan_u(before, s_redu, tot);
+    const uint32_t off = tot;
+    float z[4];
+    bool in;
+    load_round(L + (size_t)row * V + (size_t)c * SROUND, min(SROUND, V - c * SROUND), 0, invT, z, in);
+    bool k[4];
+    uint32_t n = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        k[e] = in && (mode == SEL_ALL || above_threshold(z[e], c * SROUND + 4 * t + e, zmax, zb, tau, tie_lim));
+        n += k[e];
+    }
+    uint32_t tk;
+    uint32_t pos = off + block_excl_scan_u(n, s_redu, tk);
+    uint8_t *g = ws.rowb(row) + ROW_GATHER;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        if (k[e]) {
+            if (pos < (uint32_t)SK_MAX) {
+                ((float *)(g + SK_MAX * 4))[pos] = z[e];
+                ((int32_t *)(g + SK_MAX * 8))[pos] = c * SROUND + 4 * t + e;
+            }
+            pos++;
+        }
+}
+
+__global__ __launch_bounds__(SNT) void cand_draw_kernel(int V, SampleArgs a, SpreadWs ws, const float *__restrict__ u,
+                                                        int32_t *__restrict__ out) {
+    __shared__ float s_redf[2 * SNW];
+    __shared__ int s_redi[SNW];
+    __shared__ int s_cidx[SK_MAX];
+    __shared__ float s_cp[SK_MAX];
+    __shared__ int s_sort[SK_MAX];
+    const int row = blockIdx.x, t = threadIdx.x, nround = ws.nround;
+    const float ur = u[row];
+    if (!(ur > 0.f)) {  // the reference's draw returns index 1 (here 0) when r <= 0
+        if (t == 0) out[row] = 0;
+        return;
+    }
+    if (((const RowSel *)ws.rowb(row))->mode == SEL_DEGEN) {  // (no finite maximum: as the one-row kernel)
+        if (t == 0) out[row] = V - 1;
+        return;
+    }
+    float l = 0.f;
+    for (int c = t; c < nround; c += SNT) l += (float)*(const uint32_t *)(ws.slot(row, c) + SLOT_CSUM);
+    const int n = min((int)block_sum(l, s_redf), SK_MAX);  // (counts below 2^24: exact)
+    const uint8_t *g = ws.rowb(row) + ROW_GATHER;
+    for (int i = t; i < n; i += SNT) {
+        s_cp[i] = ((const float *)(g + SK_MAX * 4))[i];
+        s_cidx[i] = ((const int32_t *)(g + SK_MAX * 8))[i];
+    }
+    __syncthreads();
+    draw_candidates(n, a, ur, V, s_cidx, s_cp, s_sort, s_redf, s_redi, out + row);
 }
 
 // In place on rows of logits: for every distinct id of the row's list in
@@ -1774,11 +1869,12 @@ size_t sample_spread_ws(int rows, int V) {
 // merges them, picks the round and scans it (as draft_sample_kernel's draw);
 // top-k from 1 to SK_SPREAD over at most SPART_ROUNDS rounds: each chunk's
 // top-k, then one workgroup per row draws among the candidates; top-p
-// and / or min-p without top-k, or a larger top-k without top-p (its
-// threshold found as top-p's, by count: histograms, pick, gather, key
-// passes): the chunks' kept sums per stage, then the draw; T = 0: each
-// chunk's argmax, then the row's. Top-k above SK_SPREAD with top-p runs
-// draft_sample_kernel. ws: sample_spread_ws bytes (8-byte aligned).
+// and / or min-p without top-k (threshold histograms, pick, gather, key
+// passes): the chunks' kept sums per stage, then the draw; a larger top-k
+// (any top-p / min-p after it): its threshold as top-p's but by count, the
+// kept entries compacted, then the candidate draw; T = 0: each chunk's
+// argmax, then the row's. Rows over more than SMAX_ROUNDS rounds run draft_sample_kernel.
+// ws: sample_spread_ws bytes (8-byte aligned).
 hipError_t launch_sample_spread(const float *L, int rows, int V, float T, int top_k, float top_p, float min_p,
                                 const float *u, int32_t *out, void *ws, hipStream_t st) {
     const int nround = (V + SROUND - 1) / SROUND;
@@ -1793,10 +1889,10 @@ hipError_t launch_sample_spread(const float *L, int rows, int V, float T, int to
     const bool live = T > 0.f && nround <= SMAX_ROUNDS;
     const bool plain = live && top_k == 0 && top_p >= 1.0f && min_p <= 0.f;
     const bool topk = live && top_k >= 1 && top_k <= SK_SPREAD && nround <= SPART_ROUNDS;
-    // top-k beyond the candidate path, without top-p: the threshold as top-p's, by count
-    const bool bigk = live && top_k > 0 && !topk && top_p >= 1.0f;
+    // top-k beyond the chunk-candidate path: the threshold as top-p's, by count
+    const bool bigk = live && top_k > 0 && !topk;
     const bool topp = live && ((top_k == 0 && top_p < 1.0f) || bigk);
-    const bool minp = live && (top_k == 0 || bigk) && min_p > 0.f;
+    const bool minp = live && top_k == 0 && min_p > 0.f;
     if (!plain && !topk && !topp && !minp) return launch_sample(L, rows, V, T, top_k, top_p, min_p, u, out, st);
     const float invT = 1.0f / T;
     const size_t rc = (size_t)rows * nround;
@@ -1827,11 +1923,20 @@ hipError_t launch_sample_spread(const float *L, int rows, int V, float T, int to
         row_select_kernel<<<rows, SNT, 0, st>>>(L, V, invT, bigk, W);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
+    if (bigk) {
+        chunk_keptcount_kernel<<<chunks, SNT, 0, st>>>(L, V, invT, W);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        chunk_compact_kernel<<<chunks, SNT, 0, st>>>(L, V, invT, W);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        const SampleArgs a{T, top_k, top_p, min_p};
+        cand_draw_kernel<<<rows, SNT, 0, st>>>(V, a, W, u, out);
+        return hipGetLastError();
+    }
     for (int stage = topp ? 0 : 1; stage <= (minp ? 1 : 0); stage++) {
-        chunk_keptsum_kernel<<<chunks, SNT, 0, st>>>(L, V, invT, topp, bigk, stage, min_p, W);
+        chunk_keptsum_kernel<<<chunks, SNT, 0, st>>>(L, V, invT, topp, stage, min_p, W);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    keep_draw_kernel<<<rows, SNT, 0, st>>>(L, V, invT, topp, bigk, minp, min_p, W, u, out);
+    keep_draw_kernel<<<rows, SNT, 0, st>>>(L, V, invT, topp, minp, min_p, W, u, out);
     return hipGetLastError();
 }
 

@@ -27,9 +27,9 @@ def softmax_sample(logits, u, temperature: float = 1.0, top_p: float = 1.0, top_
                    out=None, stream=None, spread: bool = True, ws=None):
     """One token per row of logits [rows, V] (float32, contiguous) with the
     uniforms u [rows]; returns int32 [rows]. spread: ihip_sample_ex, whose
-    every setting except top-k above 64 with top-p spreads each
-    row over workgroups of 4096 logits, with ws (uint8, sample_ws_bytes;
-    allocated here when None); else ihip_sample (one workgroup per row)."""
+    every setting spreads each row over workgroups of 4096 logits, with ws
+    (uint8, sample_ws_bytes; allocated here when None); else ihip_sample
+    (one workgroup per row)."""
     import torch
     if logits.dim() == 1:
         logits = logits.view(1, -1)

@@ -264,34 +264,36 @@ def test_topp_minp_spread(ih):
 
 
 def test_topk_large_spread(ih):
-    """Top-k above 64 (or at V above 262144), with or without min-p, spread
-    over workgroups of 4096 logits by count (the threshold's histograms
-    merged per row, the bucket's gather and key passes, ties kept lowest
-    index first, softmax over the kept entries) and in one workgroup per
-    row, against the oracle: Gaussian rows at V = 151936 and 300000,
-    quantized rows (ties at the threshold, gathered and over the row), a
-    flat row (the first k), rows all -Inf or +Inf (V - 1) and a row holding
-    a NaN (left out of the top k; also through the k <= 64 candidate path)."""
+    """Top-k above 64 (or at V above 262144), with or without top-p and
+    min-p, spread over workgroups of 4096 logits (the k-th element's bucket
+    and key by count from the chunks' histograms, the kept entries compacted
+    in index order, the one-row kernel's candidate draw over them) give the
+    one-workgroup kernel's tokens bit for bit, and match the oracle:
+    Gaussian rows at V = 151936 and 300000, quantized rows (ties at the
+    threshold, gathered and over the row), a flat row (the first k), rows
+    all -Inf or +Inf (V - 1) and a row holding a NaN (left out of the top k;
+    also through the k <= 64 candidate path)."""
     rng = np.random.default_rng(29)
     cases = [(3.0 * rng.standard_normal((12, VOCAB))).astype(np.float32),
              (3.0 * rng.standard_normal((4, 300000))).astype(np.float32),
              rng.integers(0, 3, size=(12, 8192)).astype(np.float32),
              rng.integers(0, 3, size=(6, 16384)).astype(np.float32)]
     settings = [dict(temperature=0.8, top_k=100), dict(temperature=1.0, top_k=1000), dict(temperature=0.7, top_k=4000),
-                dict(temperature=0.9, top_k=100, min_p=0.05), dict(temperature=0.8, top_k=40)]
+                dict(temperature=0.9, top_k=100, min_p=0.05), dict(temperature=0.8, top_k=40),
+                dict(temperature=0.8, top_k=1000, top_p=0.9), dict(temperature=1.0, top_k=300, top_p=0.5, min_p=0.05)]
     for L in cases:
         us = rng.random(L.shape[0]).astype(np.float32)
         for kw in settings:
             want = [O.softmax_sample(L[r], float(us[r]), **kw) for r in range(L.shape[0])]
-            for spread in (True, False):
-                got = _draw(ih, L, us, spread=spread, **kw)
-                bad = 0
-                for r in range(L.shape[0]):
-                    if got[r] != want[r]:
-                        assert _near_boundary(L[r], float(us[r]), int(got[r]), want[r], kw), \
-                            (spread, L.shape, kw, r, got[r], want[r])
-                        bad += 1
-                assert bad <= 1, (spread, L.shape, kw)
+            got = _draw(ih, L, us, spread=False, **kw)
+            assert np.array_equal(_draw(ih, L, us, spread=True, **kw), got), (L.shape, kw)
+            bad = 0
+            for r in range(L.shape[0]):
+                if got[r] != want[r]:
+                    assert _near_boundary(L[r], float(us[r]), int(got[r]), want[r], kw), \
+                        (L.shape, kw, r, got[r], want[r])
+                    bad += 1
+            assert bad <= 1, (L.shape, kw)
     flat = np.zeros(8192, np.float32)
     uf = np.array([0.013, 0.303, 0.487, 0.771, 0.9985], np.float32)
     V = 4096
@@ -302,7 +304,8 @@ def test_topk_large_spread(ih):
     b[7] = np.nan
     for spread in (True, False):
         assert list(_draw(ih, flat, uf, top_k=100, spread=spread)) == [math.ceil(100 * float(u)) - 1 for u in uf]
-        for kw in (dict(top_k=100), dict(top_k=100, min_p=0.05), dict(top_k=40), dict(top_k=40, top_p=0.9)):
+        for kw in (dict(top_k=100), dict(top_k=100, min_p=0.05), dict(top_k=40), dict(top_k=40, top_p=0.9),
+                   dict(top_k=100, top_p=0.9)):
             for x in (a, d):
                 assert list(_draw(ih, x, [0.1, 0.9], spread=spread, **kw)) == [V - 1] * 2, (spread, kw)
             ub = [0.013, 0.303, 0.777]
