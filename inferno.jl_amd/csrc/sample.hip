@@ -1641,7 +1641,14 @@ __global__ __launch_bounds__(SNT) void chunk_keptsum_kernel(const float *__restr
     __shared__ float s_redf[2 * SNW];
     const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
     float zmax, S;
-    if (!row_stats(ws.part + (size_t)row * ws.nround, ws.nround, s_redf, zmax, S)) return;
+    if (topp) {  // (the statistics row_pick_kernel stored: the same bits)
+        const RowSel *rs = (const RowSel *)ws.rowb(row);
+        if (rs->mode == SEL_DEGEN) return;
+        zmax = rs->zmax;
+        S = rs->S;
+    } else if (!row_stats(ws.part + (size_t)row * ws.nround, ws.nround, s_redf, zmax, S)) {
+        return;
+    }
     Keep keep;
     if (!load_keep(ws, row, topp, stage == 1, min_p, zmax, S, s_redf, keep)) return;
     float z[4];
