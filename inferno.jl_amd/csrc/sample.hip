@@ -1680,9 +1680,17 @@ __global__ __launch_bounds__(SNT) void keep_draw_kernel(const float *__restrict_
         return;
     }
     float zmax, S;
+    bool ok;
+    if (topp) {  // (the statistics row_pick_kernel stored: the same bits)
+        const RowSel *rs = (const RowSel *)ws.rowb(row);
+        ok = rs->mode != SEL_DEGEN;
+        zmax = rs->zmax;
+        S = rs->S;
+    } else {
+        ok = row_stats(ws.part + (size_t)row * nround, nround, s_redf, zmax, S);
+    }
     Keep keep;
-    if (!row_stats(ws.part + (size_t)row * nround, nround, s_redf, zmax, S) ||
-        !load_keep(ws, row, topp, minp, min_p, zmax, S, s_redf, keep)) {
+    if (!ok || !load_keep(ws, row, topp, minp, min_p, zmax, S, s_redf, keep)) {
         if (t == 0) out[row] = V - 1;
         return;
     }
