@@ -1279,12 +1279,15 @@ __global__ __launch_bounds__(SNT) void topk_draw_kernel(int V, SampleArgs a, Spr
     // chunk c's candidates at slots c * SK_SPREAD + j (j < its count; id -1
     // beyond): index order, loaded with the statistics, no offsets needed
     const int n = nround * SK_SPREAD;  // <= SK_MAX
-    for (int i = t; i < n; i += SNT) {
+    for (int i = t; i < n; i += SNT) {  // (count and slot loaded together: the slot is workspace either way)
         const int c = i / SK_SPREAD, j = i - c * SK_SPREAD;
         const uint8_t *sl = ws.slot(row, c);
-        const bool live = j < *(const int32_t *)(sl + SK_SPREAD * 8);
-        s_gz[i] = live ? ((const float *)sl)[j] : 0.f;
-        s_gi[i] = live ? ((const int32_t *)(sl + SK_SPREAD * 4))[j] : -1;
+        const int cnt = *(const int32_t *)(sl + SK_SPREAD * 8);
+        const float zj = ((const float *)sl)[j];
+        const int ij = ((const int32_t *)(sl + SK_SPREAD * 4))[j];
+        const bool live = j < cnt;
+        s_gz[i] = live ? zj : 0.f;
+        s_gi[i] = live ? ij : -1;
     }
     float lm = -__builtin_huge_valf();
     for (int i = t; i < nround; i += SNT) lm = fmaxf(lm, ws.part[(size_t)row * nround + i].x);
