@@ -1400,16 +1400,22 @@ __global__ __launch_bounds__(SNT) void row_pick_kernel(float top_p, int top_k, S
         return;
     }
     if (t < 256) {
+        s_hist[t] = 0;
+        s_mass[t] = 0;
+    }
+    __syncthreads();
+    {  // bucket t % 256 over every fourth chunk from t / 256 (integer sums: any order)
+        const int b = t & 255;
         uint32_t h = 0;
         unsigned long long m = 0;
-#pragma unroll 8
-        for (int c = 0; c < nround; c++) {
+#pragma unroll 4
+        for (int c = t >> 8; c < nround; c += SNT / 256) {
             const uint8_t *sl = ws.slot(row, c);
-            h += ((const uint32_t *)sl)[t];
-            m += ((const unsigned long long *)(sl + 1024))[t];
+            h += ((const uint32_t *)sl)[b];
+            if (top_k == 0) m += ((const unsigned long long *)(sl + 1024))[b];
         }
-        s_hist[t] = h;
-        s_mass[t] = m;
+        atomicAdd(&s_hist[b], h);
+        if (top_k == 0) atomicAdd(&s_mass[b], m);
     }
     __syncthreads();
     const float tp = fmaxf(top_p, 0.f) * 1099511627776.0f;
