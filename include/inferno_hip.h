@@ -51,7 +51,8 @@ extern "C" {
 const char *ihip_last_error(void);
 
 /* Select the device and create the library stream used by the host-pointer
- * drop-in entry points. Called implicitly by the first drop-in call.
+ * drop-in entry points; also looks up `device`'s fixed scratch of
+ * ihip_gemm_q_noalloc. Called implicitly by the first drop-in call.
  * Replaces the library probe of QuantizedKernels._load_libquant
  * (src/QuantizedKernels.jl:34-47). */
 int ihip_init(int device);
@@ -145,7 +146,9 @@ int ihip_gemm_q(int qtype, const void *w_dev, const float *x_dev, float *y_dev,
  * overlap in time on one GPU (other streams, other threads) race, so
  * serialize them. The kernels write every scratch byte they read, so the
  * previous call's contents need no clearing. Same results, bit for bit, as
- * ihip_gemm_q with the same arguments. */
+ * ihip_gemm_q with the same arguments. The array's device address is looked
+ * up by ihip_init(device) (else on the first call on a device): call
+ * ihip_init on each device before capturing this entry point. */
 int ihip_gemm_q_noalloc(int qtype, const void *w_dev, const float *x_dev,
                         float *y_dev, int M, int N, int K, int flags,
                         void *stream);
@@ -359,6 +362,29 @@ int ihip_spec_accept(const float *tgt_dev, const float *drf_dev,
                      const float *u_bonus_dev, int mode, int32_t *out_tok_dev,
                      int32_t *out_n_dev, void *ws, size_t ws_bytes,
                      void *stream);
+
+/* ihip_spec_accept with speculate_and_verify's top_k / top_p keywords
+ * (src/SpeculativeDecoding.jl:44-45) and softmax_sample's min_p: every bonus
+ * token (after an all-accept, and mode 1's after a rejection of the last
+ * draft) is softmax_sample(target row k; T, top_p, top_k, min_p) with
+ * u_bonus (src/SpeculativeDecoding.jl:100-104, src/ModelCPU.jl:1123-1200),
+ * drawn by ihip_sample_ex's kernels. The ratio tests and the residual are
+ * unchanged: the reference takes them from the unfiltered softmaxes at
+ * T = 1 (mode 1); mode 0 uses the unfiltered softmaxes at T, so with
+ * filtered drafting its q is not the distribution the drafts came from.
+ * Filters that keep the whole vocabulary (top_k = 0 or >= V, top_p >= 1,
+ * min_p <= 0) give ihip_spec_accept exactly. With a filter, V follows
+ * ihip_sample_ex's limits. ws: ihip_spec_accept_ex_ws_bytes() bytes (the
+ * steps' bonus rows and the sampler's workspace on top of the accept's). */
+int ihip_spec_accept_ex_ws_bytes(int steps, int k, int V, int top_k,
+                                 float top_p, float min_p, size_t *bytes);
+int ihip_spec_accept_ex(const float *tgt_dev, const float *drf_dev,
+                        const int32_t *draft_tok_dev, int steps, int k, int V,
+                        float T, int top_k, float top_p, float min_p,
+                        const float *u_acc_dev, const float *u_res_dev,
+                        const float *u_bonus_dev, int mode,
+                        int32_t *out_tok_dev, int32_t *out_n_dev, void *ws,
+                        size_t ws_bytes, void *stream);
 
 /* Greedy verify (mtp_verify_step!, src/ModelCPU.jl:1914-1930): per step,
  * logits [(k+1) x V]; out_argmax [k+1] = first-index argmax of each row in

@@ -167,6 +167,8 @@ __global__ void stats_merge_kernel(const float2 *__restrict__ part, int rows, in
 //   kind 0: p_j (target row, temperature Tp)       bonus draw
 //   kind 1: max(0, p_j - q_j)  (q: draft row)      standard residual
 //   kind 2: max(0, p_j - qs)   (qs: scalar q_i)    reference residual
+//   kind 3: the bonus token drawn beforehand by the filtered sampler
+//           (top-k / top-p / min-p on target row k at T with u_bonus)
 //   kind -1: invalid draft id (out_n = -1, nothing drawn)
 //   kind -2: no draw in this slot
 // fallback when the weights sum to 0: 1 = draw from p (standard mode),
@@ -221,8 +223,9 @@ __device__ void decide_block(const float *__restrict__ tgt, const float *__restr
                              const int32_t *__restrict__ draft_tok, int k, int V, float T,
                              const float *__restrict__ u_acc, const float *__restrict__ u_res,
                              const float *__restrict__ u_bonus, int mode, const float2 *__restrict__ part,
-                             int nchunk, int step, int steps, bool publish, int32_t *__restrict__ out_tok,
-                             int32_t *__restrict__ out_n, Decision *__restrict__ dec, float2 *ms, Decision *s_dec) {
+                             int nchunk, int step, int steps, bool publish, const int32_t *__restrict__ bonus_pre,
+                             int32_t *__restrict__ out_tok, int32_t *__restrict__ out_n,
+                             Decision *__restrict__ dec, float2 *ms, Decision *s_dec) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const float *Lt = tgt + (size_t)step * (k + 1) * V;
     const float *Ld = drf + (size_t)step * k * V;
@@ -325,7 +328,7 @@ __device__ void decide_block(const float *__restrict__ tgt, const float *__restr
                     D.fallback = mode == 0 ? 1 : 2;
                     if (mode == 1 && first == k - 1) {  // the reference's bonus after the residual
                         const float2 pk = ms[k];
-                        D2.kind = 0;
+                        D2.kind = bonus_pre ? 3 : 0;
                         D2.n = first;
                         D2.pos = first + 1;
                         D2.prow = k;
@@ -336,7 +339,7 @@ __device__ void decide_block(const float *__restrict__ tgt, const float *__restr
                     }
                 } else {
                     const float2 pt = ms[k];
-                    D.kind = 0;
+                    D.kind = bonus_pre ? 3 : 0;
                     D.prow = k;
                     D.qrow = 0;
                     D.Tp = T; D.mp = pt.x; D.sp = pt.y;
@@ -407,6 +410,7 @@ __global__ __launch_bounds__(NT) void decide_sum_kernel(const float *__restrict_
                                                         const float *__restrict__ u_res,
                                                         const float *__restrict__ u_bonus, int mode,
                                                         const float2 *__restrict__ part, int nchunk,
+                                                        const int32_t *__restrict__ bonus_pre,
                                                         int32_t *__restrict__ out_tok, int32_t *__restrict__ out_n,
                                                         Decision *__restrict__ dec, float *__restrict__ csum) {
     __shared__ float sh[PER * 4];
@@ -414,10 +418,10 @@ __global__ __launch_bounds__(NT) void decide_sum_kernel(const float *__restrict_
     __shared__ Decision s_dec[2];
     const int c = blockIdx.x, step = blockIdx.y;
     decide_block(tgt, drf, draft_tok, k, V, T, u_acc, u_res, u_bonus, mode, part, nchunk, step, gridDim.y,
-                 c == 0 && blockIdx.z == 0, out_tok, out_n, dec, ms, s_dec);
+                 c == 0 && blockIdx.z == 0, bonus_pre, out_tok, out_n, dec, ms, s_dec);
     const size_t slot = (size_t)step * gridDim.z + blockIdx.z;
     const Decision D = s_dec[blockIdx.z];
-    if (D.kind < 0) return;
+    if (D.kind < 0 || D.kind == 3) return;
     const float *lt = tgt + ((size_t)step * (k + 1) + D.prow) * V;
     const float *ld = D.kind == 1 ? drf + ((size_t)step * k + D.qrow) * V : nullptr;
     ChunkScan cs;
@@ -435,7 +439,9 @@ __global__ __launch_bounds__(NT) void decide_sum_kernel(const float *__restrict_
 constexpr int MAX_CHUNKS = 1024;
 __global__ __launch_bounds__(NT) void sample_kernel(const float *__restrict__ tgt, const float *__restrict__ drf,
                                                     int k, int V, const Decision *__restrict__ dec, int nchunk,
-                                                    const float *__restrict__ csum, int32_t *__restrict__ out_tok) {
+                                                    const float *__restrict__ csum,
+                                                    const int32_t *__restrict__ bonus_pre,
+                                                    int32_t *__restrict__ out_tok) {
     __shared__ float sh[PER * 4];
     __shared__ float s_psum[MAX_CHUNKS];
     __shared__ float s_csum[MAX_CHUNKS];
@@ -446,6 +452,10 @@ __global__ __launch_bounds__(NT) void sample_kernel(const float *__restrict__ tg
     const size_t slot = (size_t)step * gridDim.y + blockIdx.y;
     const Decision D = dec[slot];
     if (D.kind < 0) return;
+    if (D.kind == 3) {
+        if (t == 0) out_tok[(size_t)step * (k + 1) + D.pos] = bonus_pre[step];
+        return;
+    }
     const float *cw = csum + slot * nchunk;
     const float *lt = tgt + ((size_t)step * (k + 1) + D.prow) * V;
     const float *ld = D.kind == 1 ? drf + ((size_t)step * k + D.qrow) * V : nullptr;
@@ -688,10 +698,13 @@ size_t spec_accept_ws(int steps, int k, int V) {
 }
 
 // ws: float2 part[steps*(k+1) + steps*k][nchunk], Decision dec[steps][slots],
-// float csum[steps][slots][nchunk] (slots = draw_slots(mode)).
+// float csum[steps][slots][nchunk] (slots = draw_slots(mode)). bonus_pre
+// (nullptr: none): each step's bonus token, drawn beforehand from target row
+// k by the filtered sampler; bonus draws then copy it.
 hipError_t launch_spec_accept(const float *tgt, const float *drf, const int32_t *draft_tok, int steps, int k,
                               int V, float T, const float *u_acc, const float *u_res, const float *u_bonus,
-                              int mode, int32_t *out_tok, int32_t *out_n, void *ws, hipStream_t st) {
+                              int mode, const int32_t *bonus_pre, int32_t *out_tok, int32_t *out_n, void *ws,
+                              hipStream_t st) {
     const int nc = accept_nchunk(V);
     const float Tr = mode == 0 ? T : 1.0f;
     const int nd = draw_slots(mode);
@@ -703,9 +716,9 @@ hipError_t launch_spec_accept(const float *tgt, const float *drf, const int32_t 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     decide_sum_kernel<<<dim3(nc, steps, nd), NT, 0, st>>>(tgt, drf, draft_tok, k, V, T, u_acc, u_res, u_bonus,
-                                                          mode, part, nc, out_tok, out_n, dec, csum);
+                                                          mode, part, nc, bonus_pre, out_tok, out_n, dec, csum);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    sample_kernel<<<dim3(steps, nd), NT, 0, st>>>(tgt, drf, k, V, dec, nc, csum, out_tok);
+    sample_kernel<<<dim3(steps, nd), NT, 0, st>>>(tgt, drf, k, V, dec, nc, csum, bonus_pre, out_tok);
     return hipGetLastError();
 }
 

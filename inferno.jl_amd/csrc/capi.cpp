@@ -31,7 +31,8 @@ hipError_t launch_stats(const float *L, int rows, int V, float T, float T_last, 
 hipError_t launch_stats_merge(const float2 *part, int rows, int V, float *zmax, float *zsum, hipStream_t st);
 hipError_t launch_spec_accept(const float *tgt, const float *drf, const int32_t *draft_tok, int steps, int k,
                               int V, float T, const float *u_acc, const float *u_res, const float *u_bonus,
-                              int mode, int32_t *out_tok, int32_t *out_n, void *ws, hipStream_t st);
+                              int mode, const int32_t *bonus_pre, int32_t *out_tok, int32_t *out_n, void *ws,
+                              hipStream_t st);
 size_t spec_accept_ws(int steps, int k, int V);
 hipError_t launch_argmax_partial(const float *L, int rows, int V, float2 *part, hipStream_t st);
 hipError_t launch_greedy(const float2 *part, int V, const int32_t *draft_tok, int steps, int k, int32_t *out_n,
@@ -69,6 +70,7 @@ hipError_t launch_quantize_q8k(const float *x, void *y, int64_t k, hipStream_t s
 hipError_t launch_vec_dot_q8k(int qt, const void *x, const void *y, int nb, float *out, hipStream_t st);
 size_t noalloc_scratch_bytes();
 hipError_t noalloc_scratch(void **out);
+hipError_t noalloc_prepare(int device);
 
 namespace {
 
@@ -401,7 +403,11 @@ int ihip_init(int device) {
     Lib &L = lib();
     std::lock_guard<std::mutex> lk(L.mu);
     const int rc = init_locked(L, device);
-    return rc == IHIP_OK ? ok() : rc;
+    if (rc != IHIP_OK) return rc;
+    // the allocation-free entry point's scratch address on this device, so
+    // that a call under graph capture finds it already resolved
+    const hipError_t e = noalloc_prepare(device);
+    return e == hipSuccess ? ok() : hip_fail(e, "ihip_init: device scratch");
 }
 
 int ihip_available(void) {
@@ -771,24 +777,100 @@ int ihip_spec_accept_ws_bytes(int steps, int k, int V, size_t *bytes) {
     return ok();
 }
 
+// The bonus draw of a verify step goes through softmax_sample's filters
+// (src/SpeculativeDecoding.jl:100-104) when one of them keeps less than the
+// whole vocabulary.
+static bool bonus_filtered(int V, int top_k, float top_p, float min_p) {
+    return (top_k > 0 && top_k < V) || top_p < 1.0f || min_p > 0.f;
+}
+
+static size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Workspace of a filtered accept: the accept's own, then the steps' bonus
+// rows gathered contiguously (steps > 1), the sampler's workspace over them,
+// and the drawn bonus tokens.
+static size_t spec_accept_ex_ws(int steps, int k, int V, bool filtered) {
+    size_t b = round256(spec_accept_ws(steps, k, V));
+    if (!filtered) return b;
+    if (steps > 1) b += round256((size_t)steps * V * sizeof(float));
+    return b + round256(sample_spread_ws(steps, V)) + round256((size_t)steps * sizeof(int32_t));
+}
+
+int ihip_spec_accept_ex_ws_bytes(int steps, int k, int V, int top_k, float top_p, float min_p, size_t *bytes) {
+    if (!bytes) return fail(IHIP_EFAULT, "ihip_spec_accept_ex_ws_bytes: NULL");
+    if (steps < 1 || k < 0 || V < 1 || top_k < 0)
+        return fail(IHIP_EINVAL, "ihip_spec_accept_ex_ws_bytes: steps=%d k=%d V=%d top_k=%d", steps, k, V, top_k);
+    if (V > 1024 * 4096) return fail(IHIP_EINVAL, "ihip_spec_accept_ex_ws_bytes: V=%d above 4194304", V);
+    *bytes = spec_accept_ex_ws(steps, k, V, bonus_filtered(V, top_k, top_p, min_p));
+    return ok();
+}
+
+static int spec_accept_impl(const char *name, const float *tgt_dev, const float *drf_dev,
+                            const int32_t *draft_tok_dev, int steps, int k, int V, float T, int top_k, float top_p,
+                            float min_p, const float *u_acc_dev, const float *u_res_dev, const float *u_bonus_dev,
+                            int mode, int32_t *out_tok_dev, int32_t *out_n_dev, void *ws, size_t ws_bytes,
+                            size_t need, bool filtered, void *stream) {
+    if (!tgt_dev || !u_res_dev || !u_bonus_dev || !out_tok_dev || !out_n_dev)
+        return fail(IHIP_EFAULT, "%s: NULL pointer", name);
+    if (k > 0 && (!drf_dev || !draft_tok_dev || !u_acc_dev)) return fail(IHIP_EFAULT, "%s: NULL pointer", name);
+    if (steps < 1 || k < 0 || V < 1) return fail(IHIP_EINVAL, "%s: steps=%d k=%d V=%d", name, steps, k, V);
+    if (!(T > 0.f)) return fail(IHIP_EINVAL, "%s: T=%g must be > 0 (greedy: ihip_greedy_verify)", name, T);
+    if (mode != 0 && mode != 1) return fail(IHIP_EINVAL, "%s: mode=%d", name, mode);
+    if (V > 1024 * 4096) return fail(IHIP_EINVAL, "%s: V=%d above 4194304", name, V);
+    if (k > 127) return fail(IHIP_EINVAL, "%s: k=%d above 127", name, k);
+    if (top_k < 0 || top_p != top_p || min_p != min_p)
+        return fail(IHIP_EINVAL, "%s: top_k=%d top_p=%g min_p=%g", name, top_k, top_p, min_p);
+    if (!ws) return fail(IHIP_EFAULT, "%s: NULL workspace", name);
+    if (ws_bytes < need) return fail(IHIP_ENOMEM, "%s: workspace %zu < %zu bytes", name, ws_bytes, need);
+    if (((uintptr_t)ws & 15) != 0) return fail(IHIP_EINVAL, "%s: workspace must be 16-byte aligned", name);
+    const int32_t *bonus = nullptr;
+    hipError_t e = hipSuccess;
+    if (filtered) {
+        if (V < 4 || (V & 3) || V > sample_max_v() || !aligned16(tgt_dev))
+            return fail(IHIP_EINVAL, "%s: filtered bonus draw needs V a multiple of 4 (V=%d) and 16-byte aligned "
+                                     "logits", name, V);
+        const int kk = top_k >= V ? 0 : top_k;
+        if (kk > sample_max_top_k())
+            return fail(IHIP_EINVAL, "%s: top_k=%d above %d (and below V)", name, top_k, sample_max_top_k());
+        uint8_t *w = (uint8_t *)ws + round256(spec_accept_ws(steps, k, V));
+        const float *rows = tgt_dev + (size_t)k * V;  // step 0's bonus row; steps apart by (k + 1) V
+        if (steps > 1) {
+            float *g = (float *)w;
+            w += round256((size_t)steps * V * sizeof(float));
+            e = hipMemcpy2DAsync(g, (size_t)V * sizeof(float), rows, (size_t)(k + 1) * V * sizeof(float),
+                                 (size_t)V * sizeof(float), steps, hipMemcpyDeviceToDevice, S(stream));
+            rows = g;
+        }
+        void *sws = w;
+        int32_t *btok = (int32_t *)(w + round256(sample_spread_ws(steps, V)));
+        if (e == hipSuccess)
+            e = launch_sample_spread(rows, steps, V, T, kk, top_p, min_p, u_bonus_dev, btok, sws, S(stream));
+        bonus = btok;
+    }
+    if (e == hipSuccess)
+        e = launch_spec_accept(tgt_dev, drf_dev, draft_tok_dev, steps, k, V, T, u_acc_dev, u_res_dev, u_bonus_dev,
+                               mode, bonus, out_tok_dev, out_n_dev, ws, S(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, name);
+}
+
 int ihip_spec_accept(const float *tgt_dev, const float *drf_dev, const int32_t *draft_tok_dev, int steps, int k,
                      int V, float T, const float *u_acc_dev, const float *u_res_dev, const float *u_bonus_dev,
                      int mode, int32_t *out_tok_dev, int32_t *out_n_dev, void *ws, size_t ws_bytes, void *stream) {
-    if (!tgt_dev || !u_res_dev || !u_bonus_dev || !out_tok_dev || !out_n_dev)
-        return fail(IHIP_EFAULT, "ihip_spec_accept: NULL pointer");
-    if (k > 0 && (!drf_dev || !draft_tok_dev || !u_acc_dev)) return fail(IHIP_EFAULT, "ihip_spec_accept: NULL pointer");
-    if (steps < 1 || k < 0 || V < 1) return fail(IHIP_EINVAL, "ihip_spec_accept: steps=%d k=%d V=%d", steps, k, V);
-    if (!(T > 0.f)) return fail(IHIP_EINVAL, "ihip_spec_accept: T=%g must be > 0 (greedy: ihip_greedy_verify)", T);
-    if (mode != 0 && mode != 1) return fail(IHIP_EINVAL, "ihip_spec_accept: mode=%d", mode);
-    if (V > 1024 * 4096) return fail(IHIP_EINVAL, "ihip_spec_accept: V=%d above 4194304", V);
-    if (k > 127) return fail(IHIP_EINVAL, "ihip_spec_accept: k=%d above 127", k);
-    const size_t need = spec_accept_ws(steps, k, V);
-    if (!ws) return fail(IHIP_EFAULT, "ihip_spec_accept: NULL workspace");
-    if (ws_bytes < need) return fail(IHIP_ENOMEM, "ihip_spec_accept: workspace %zu < %zu bytes", ws_bytes, need);
-    if (((uintptr_t)ws & 15) != 0) return fail(IHIP_EINVAL, "ihip_spec_accept: workspace must be 16-byte aligned");
-    hipError_t e = launch_spec_accept(tgt_dev, drf_dev, draft_tok_dev, steps, k, V, T, u_acc_dev, u_res_dev,
-                                      u_bonus_dev, mode, out_tok_dev, out_n_dev, ws, S(stream));
-    return e == hipSuccess ? ok() : hip_fail(e, "ihip_spec_accept");
+    const size_t need = steps >= 1 && k >= 0 && V >= 1 ? spec_accept_ws(steps, k, V) : 0;
+    return spec_accept_impl("ihip_spec_accept", tgt_dev, drf_dev, draft_tok_dev, steps, k, V, T, 0, 1.0f, 0.f,
+                            u_acc_dev, u_res_dev, u_bonus_dev, mode, out_tok_dev, out_n_dev, ws, ws_bytes, need,
+                            false, stream);
+}
+
+int ihip_spec_accept_ex(const float *tgt_dev, const float *drf_dev, const int32_t *draft_tok_dev, int steps, int k,
+                        int V, float T, int top_k, float top_p, float min_p, const float *u_acc_dev,
+                        const float *u_res_dev, const float *u_bonus_dev, int mode, int32_t *out_tok_dev,
+                        int32_t *out_n_dev, void *ws, size_t ws_bytes, void *stream) {
+    const bool filtered = V >= 1 && bonus_filtered(V, top_k, top_p, min_p);
+    const size_t need = steps >= 1 && k >= 0 && V >= 1 ? spec_accept_ex_ws(steps, k, V, filtered) : 0;
+    return spec_accept_impl("ihip_spec_accept_ex", tgt_dev, drf_dev, draft_tok_dev, steps, k, V, T, top_k, top_p,
+                            min_p, u_acc_dev, u_res_dev, u_bonus_dev, mode, out_tok_dev, out_n_dev, ws, ws_bytes,
+                            need, filtered, stream);
 }
 
 int ihip_greedy_verify(const float *logits_dev, const int32_t *draft_tok_dev, int steps, int k, int V,

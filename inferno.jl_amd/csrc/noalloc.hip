@@ -7,7 +7,9 @@
 // load until the process ends. In host code `scratch` names a host-side
 // stand-in, not a device address: the device address comes from
 // hipGetSymbolAddress, looked up once per device with that device current
-// and kept in a per-device table; only that address is handed to kernels.
+// (by ihip_init, so that no lookup happens inside a graph capture, or else
+// on the first call on a device) and kept in a per-device table; only that
+// address is handed to kernels.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -44,4 +46,20 @@ hipError_t noalloc_scratch(void **out) {
     }
     *out = g_ptr[dev];
     return hipSuccess;
+}
+
+// Looks up `device`'s scratch address now (ihip_init), with that device
+// current for the lookup and the caller's device restored afterwards.
+hipError_t noalloc_prepare(int device) {
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    if (cur != device && (e = hipSetDevice(device)) != hipSuccess) return e;
+    void *p = nullptr;
+    e = noalloc_scratch(&p);
+    if (cur != device) {
+        const hipError_t e2 = hipSetDevice(cur);
+        if (e == hipSuccess) e = e2;
+    }
+    return e;
 }

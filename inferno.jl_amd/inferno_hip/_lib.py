@@ -52,6 +52,9 @@ SIGNATURES = {
     "ihip_softmax_stats": (_i, [_vp, _i, _i, _f, _vp, _vp, _vp, _sz, _vp]),
     "ihip_spec_accept_ws_bytes": (_i, [_i, _i, _i, C.POINTER(_sz)]),
     "ihip_spec_accept": (_i, [_vp, _vp, _vp, _i, _i, _i, _f, _vp, _vp, _vp, _i, _vp, _vp, _vp, _sz, _vp]),
+    "ihip_spec_accept_ex_ws_bytes": (_i, [_i, _i, _i, _i, _f, _f, C.POINTER(_sz)]),
+    "ihip_spec_accept_ex": (_i, [_vp, _vp, _vp, _i, _i, _i, _f, _i, _f, _f, _vp, _vp, _vp, _i, _vp, _vp, _vp, _sz,
+                                 _vp]),
     "ihip_greedy_verify": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _sz, _vp]),
     "ihip_tree_accept": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ihip_spec_commit_state": (_i, [_vp, _vp, _sz, _i64, _i, _vp, _i, _i64, _i64, _vp]),

@@ -42,7 +42,8 @@ def softmax_stats(logits, temperature: float, stream=None):
 
 
 def spec_accept(target_logits, draft_logits, draft_tokens, temperature: float, u_acc, u_res, u_bonus,
-                mode: int = MODE_STANDARD, stream=None, out_tok=None, out_n=None, ws=None):
+                mode: int = MODE_STANDARD, stream=None, out_tok=None, out_n=None, ws=None, top_p: float = 1.0,
+                top_k: int = 0, min_p: float = 0.0):
     """Batched accept step.
 
     target_logits [S, k+1, V], draft_logits [S, k, V], draft_tokens [S, k]
@@ -52,6 +53,9 @@ def spec_accept(target_logits, draft_logits, draft_tokens, temperature: float, u
     MODE_REFERENCE a step whose last draft is rejected (out_n == k - 1) also
     carries the reference's bonus token at index k
     (src/SpeculativeDecoding.jl:100). n_tokens() gives the count.
+    top_p / top_k (speculate_and_verify's keywords, src/SpeculativeDecoding.jl
+    :44-45) and min_p filter every bonus draw as softmax_sample does
+    (:100-104); the ratio tests and residuals stay unfiltered.
     """
     import torch
     import ctypes as C
@@ -74,7 +78,7 @@ def spec_accept(target_logits, draft_logits, draft_tokens, temperature: float, u
     check_tensor(u_bonus, "u_bonus", torch.float32, (S,))
     L = _lib.load()
     nb = C.c_size_t()
-    _lib.check(L.ihip_spec_accept_ws_bytes(S, k, V, C.byref(nb)))
+    _lib.check(L.ihip_spec_accept_ex_ws_bytes(S, k, V, top_k, top_p, min_p, C.byref(nb)))
     dev = target_logits.device
     if ws is None:
         ws = _ws(nb.value, dev)
@@ -85,9 +89,9 @@ def spec_accept(target_logits, draft_logits, draft_tokens, temperature: float, u
         out_n = torch.zeros(S, dtype=torch.int32, device=dev)
     check_tensor(out_tok, "out_tok", torch.int32, (S, k + 1))
     check_tensor(out_n, "out_n", torch.int32, (S,))
-    _lib.check(L.ihip_spec_accept(_ptr(target_logits), _ptr(draft_logits), _ptr(draft_tokens), S, k, V,
-                                  temperature, _ptr(u_acc), _ptr(u_res), _ptr(u_bonus), mode, _ptr(out_tok),
-                                  _ptr(out_n), _ptr(ws), ws.numel(), _stream(stream)))
+    _lib.check(L.ihip_spec_accept_ex(_ptr(target_logits), _ptr(draft_logits), _ptr(draft_tokens), S, k, V,
+                                     temperature, top_k, top_p, min_p, _ptr(u_acc), _ptr(u_res), _ptr(u_bonus),
+                                     mode, _ptr(out_tok), _ptr(out_n), _ptr(ws), ws.numel(), _stream(stream)))
     return out_tok, out_n
 
 

@@ -114,7 +114,39 @@ def argmax_first(L: np.ndarray) -> int:
     return int(lib().orc_argmax_first(L, L.size))
 
 
-def spec_accept(Lt, Ld, draft, T, u_acc, u_res, u_bonus, mode=0):
+def _filtered(V: int, top_p: float, top_k: int, min_p: float) -> bool:
+    return (0 < top_k < V) or top_p < 1.0 or min_p > 0.0
+
+
+def _bonus_slot(n: int, k: int, mode: int) -> int:
+    """Index of the bonus token in a step's tokens, or -1 when the step draws
+    none: after an all-accept (n == k), and in mode 1 after a rejection of
+    the last draft (n == k - 1, src/SpeculativeDecoding.jl:100)."""
+    if n == k and n >= 0:
+        return k
+    if mode == 1 and k >= 1 and n == k - 1:
+        return k
+    return -1
+
+
+def spec_accept(Lt, Ld, draft, T, u_acc, u_res, u_bonus, mode=0, top_p: float = 1.0, top_k: int = 0,
+                min_p: float = 0.0):
+    """speculate_and_verify's accept (src/SpeculativeDecoding.jl:75-104) with
+    explicit uniforms: orc_spec_accept, then, when top_p / top_k / min_p
+    filter, each bonus token redrawn by softmax_sample(Lt[k]; T, top_p,
+    top_k, min_p) with u_bonus (:100-104: the reference's bonus is
+    softmax_sample with the same keywords; the ratio tests and residuals do
+    not see the filters)."""
+    tok, n = _spec_accept_plain(Lt, Ld, draft, T, u_acc, u_res, u_bonus, mode)
+    Lt = np.asarray(Lt, dtype=np.float32)
+    k, V = Lt.shape[0] - 1, Lt.shape[1]
+    b = _bonus_slot(n, k, mode)
+    if b >= 0 and _filtered(V, top_p, top_k, min_p):
+        tok[b] = softmax_sample(Lt[k], float(np.asarray(u_bonus).ravel()[0]), T, top_p, top_k, min_p)
+    return tok, n
+
+
+def _spec_accept_plain(Lt, Ld, draft, T, u_acc, u_res, u_bonus, mode=0):
     Lt = _c(Lt, np.float32)
     k, V = Lt.shape[0] - 1, Lt.shape[1]
     Ld = _c(Ld, np.float32).reshape(max(k, 1) if k else 1, -1) if k else np.zeros((1, V), np.float32)
@@ -137,10 +169,12 @@ def n_tokens(n: int, k: int, mode: int) -> int:
     return n + 1 + (1 if mode == 1 and k >= 1 and n == k - 1 else 0)
 
 
-def spec_accept_batch(Lt, Ld, draft, T, u_acc, u_res, u_bonus, mode=0):
+def spec_accept_batch(Lt, Ld, draft, T, u_acc, u_res, u_bonus, mode=0, top_p: float = 1.0, top_k: int = 0,
+                      min_p: float = 0.0):
     """orc_spec_accept over steps (parallel on the host): Lt [S, k+1, V],
     Ld [S, k, V], draft / u_acc [S, k], u_res / u_bonus [S] ->
-    (out_tok [S, k+1] padded with -1, out_n [S], -1 for an invalid draft)."""
+    (out_tok [S, k+1] padded with -1, out_n [S], -1 for an invalid draft);
+    filtered bonus tokens as in spec_accept."""
     Lt = _c(Lt, np.float32)
     S, k1, V = Lt.shape
     k = k1 - 1
@@ -151,6 +185,15 @@ def spec_accept_batch(Lt, Ld, draft, T, u_acc, u_res, u_bonus, mode=0):
     assert rc == 0, rc
     for s in range(S):  # entries past the step's tokens are left as -1
         out[s, n_tokens(int(n[s]), k, mode):] = -1
+    if _filtered(V, top_p, top_k, min_p):
+        ub = np.asarray(u_bonus, dtype=np.float32).ravel()
+        todo = [(s, _bonus_slot(int(n[s]), k, mode)) for s in range(S)]
+        todo = [(s, b) for s, b in todo if b >= 0]
+        draw = lambda sb: softmax_sample(Lt[sb[0], k], float(ub[sb[0]]), T, top_p, top_k, min_p)  # noqa: E731
+        from concurrent.futures import ThreadPoolExecutor
+        with ThreadPoolExecutor(min(8, os.cpu_count() or 1)) as ex:  # numpy's sorts release the GIL
+            for (s, b), t in zip(todo, ex.map(draw, todo)):
+                out[s, b] = t
     return out, n
 
 

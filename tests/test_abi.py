@@ -67,6 +67,33 @@ def test_argument_checks_without_gpu(lib):
     assert lib.ihip_tree_accept(p16, p16, p16, p16, 4, 10, 0.0, p16, p16, p16, p16, 1 << 20, None) == -22
 
 
+def test_spec_accept_ex_checks_without_gpu(lib):
+    """ihip_spec_accept_ex: filters that keep every token need no more
+    workspace than ihip_spec_accept; a filtered bonus adds the sampler's;
+    bad filters, workspaces and vocabularies are refused before any launch."""
+    nb, nf = C.c_size_t(), C.c_size_t()
+    S, k, V = 3, 4, 151936
+    assert lib.ihip_spec_accept_ws_bytes(S, k, V, C.byref(nb)) == 0
+    assert lib.ihip_spec_accept_ex_ws_bytes(S, k, V, 0, 1.0, 0.0, C.byref(nf)) == 0
+    assert nb.value <= nf.value < nb.value + 256
+    assert lib.ihip_spec_accept_ex_ws_bytes(S, k, V, V, 1.0, 0.0, C.byref(nf)) == 0 and nf.value < nb.value + 256
+    sws = C.c_size_t()
+    assert lib.ihip_sample_ws_bytes(S, V, C.byref(sws)) == 0
+    for kw in ((40, 1.0, 0.0), (0, 0.9, 0.0), (0, 1.0, 0.1)):
+        assert lib.ihip_spec_accept_ex_ws_bytes(S, k, V, *kw, C.byref(nf)) == 0
+        assert nf.value >= nb.value + S * V * 4 + sws.value + S * 4
+    assert lib.ihip_spec_accept_ex_ws_bytes(S, k, V, -1, 1.0, 0.0, C.byref(nf)) == -22
+    buf = (C.c_uint8 * 4096)()
+    p16 = (C.addressof(buf) + 15) & ~15
+    args = lambda top_k, top_p, min_p, ws_bytes, V=V: (p16, p16, p16, S, k, V, 0.8, top_k, top_p, min_p, p16, p16,  # noqa: E731
+                                                        p16, 1, p16, p16, p16, ws_bytes, None)
+    assert lib.ihip_spec_accept_ex(*args(40, 1.0, 0.0, 1024)) == -12  # workspace short of the filtered need
+    assert lib.ihip_spec_accept_ex(*args(-2, 1.0, 0.0, 1 << 40)) == -22
+    assert lib.ihip_spec_accept_ex(*args(0, float("nan"), 0.0, 1 << 40)) == -22
+    assert lib.ihip_spec_accept_ex(*args(40, 1.0, 0.0, 1 << 40, V=151937)) == -22
+    assert b"multiple of 4" in lib.ihip_last_error()
+
+
 def _dropin_child(env_extra, inner_dim, outer_dim=3):
     code = (
         "import ctypes as C, numpy as np, sys; sys.path.insert(0, %r);"

@@ -164,6 +164,62 @@ def test_reference_mode_bonus_only_after_last_draft():
     assert out.tolist() == [[2, -1, -1], [1, 2, 2], [1, 1, 1]]
 
 
+def test_filtered_bonus_hand_cases():
+    """speculate_and_verify passes top_p / top_k to the bonus draw only
+    (src/SpeculativeDecoding.jl:100-104; the ratio tests and the residual
+    use the unfiltered softmaxes, :79-93). Hand-worked on the two-draft
+    V = 3 case above, bonus row p = [0.1, 0.1, 0.8] at T = 1:
+    top_k = 1 keeps index 2 only (any u -> 2); top_k = 2 keeps {2, 0} (the
+    stable descending order puts index 0 before the tied index 1) with
+    probabilities [1/9, 0, 8/9]; top_p = 0.5 keeps index 2 only; min_p = 0.2
+    drops p < 0.16: index 2 only."""
+    Lt = np.log(np.array([[0.5, 0.3, 0.2], [0.5, 0.3, 0.2], [0.1, 0.1, 0.8]], np.float32))
+    Ld = np.log(np.array([[0.1, 0.6, 0.3], [0.1, 0.6, 0.3]], np.float32))
+    d = np.array([1, 1], np.int32)
+    acc_all, rej_last = np.array([0.1, 0.2], np.float32), np.array([0.1, 0.7], np.float32)
+    for mode, ua, want in ((1, acc_all, [1, 1]), (1, rej_last, [1, 2]), (0, acc_all, [1, 1])):
+        for u in (0.05, 0.15, 0.5, 0.99):
+            for kw in (dict(top_k=1), dict(top_p=0.5), dict(min_p=0.2), dict(top_k=1, top_p=0.3)):
+                tok, n = O.spec_accept(Lt, Ld, d, 1.0, ua, 0.5, u, mode, **kw)
+                assert tok.tolist() == want + [2], (mode, u, kw, tok)
+            # top_k = 2: cumsum [1/9, 1/9, 1] -> u <= 1/9 gives 0, else 2 (never the dropped 1)
+            tok, n = O.spec_accept(Lt, Ld, d, 1.0, ua, 0.5, u, mode, top_k=2)
+            assert tok.tolist() == want + [0 if u <= 1 / 9 else 2], (mode, u, tok)
+            # unfiltered: cumsum [0.1, 0.2, 1.0]
+            tok, n = O.spec_accept(Lt, Ld, d, 1.0, ua, 0.5, u, mode, top_k=3, top_p=1.0)
+            assert tok.tolist() == want + [0 if u <= 0.1 else 1 if u <= 0.2 else 2]
+    # an earlier rejection draws no bonus: the filters change nothing
+    tok, n = O.spec_accept(Lt, Ld, d, 1.0, np.array([0.7, 0.1], np.float32), 0.5, 0.05, 1, top_k=1)
+    assert n == 0 and tok.tolist() == [2]
+    # mode 0 rejection at the last draft: the residual only (no bonus), unfiltered
+    tok, n = O.spec_accept(Lt, Ld, d, 1.0, rej_last, 0.01, 0.05, 0, top_k=1)
+    assert n == 1 and tok.tolist() == [1, 0]
+    # the batched oracle applies the same filters per step
+    Lb, Db = np.stack([Lt] * 3), np.stack([Ld] * 3)
+    ua = np.stack([acc_all, rej_last, np.array([0.7, 0.1], np.float32)])
+    out, ns = O.spec_accept_batch(Lb, Db, np.stack([d] * 3), 1.0, ua, np.full(3, 0.5, np.float32),
+                                  np.array([0.05, 0.05, 0.05], np.float32), 1, top_k=1)
+    assert ns.tolist() == [2, 1, 0] and out.tolist() == [[1, 1, 2], [1, 2, 2], [2, -1, -1]]
+
+
+def test_filtered_bonus_matches_sampler_oracle():
+    """At a larger V the filtered bonus equals softmax_sample on the bonus
+    row (itself pinned by test_oracle_sampler), and with filters that keep
+    every entry the accept is unchanged."""
+    rng = np.random.default_rng(11)
+    k, V = 3, 512
+    Lt = (rng.standard_normal((k + 1, V)) * 2).astype(np.float32)
+    Ld = (Lt[:k] + rng.standard_normal((k, V))).astype(np.float32)
+    d = np.array([int(np.argmax(Ld[i])) for i in range(k)], np.int32)
+    for u in rng.random(20):
+        for kw in (dict(top_k=7), dict(top_p=0.6), dict(top_k=50, top_p=0.8, min_p=0.02)):
+            tok, n = O.spec_accept(Lt, Ld, d, 0.7, np.zeros(k, np.float32), 0.5, float(u), 0, **kw)
+            assert n == k and tok[k] == O.softmax_sample(Lt[k], float(u), 0.7, **kw)
+        a = O.spec_accept(Lt, Ld, d, 0.7, np.zeros(k, np.float32), 0.5, float(u), 1)
+        b = O.spec_accept(Lt, Ld, d, 0.7, np.zeros(k, np.float32), 0.5, float(u), 1, top_k=V, top_p=1.0)
+        assert a[1] == b[1] and a[0].tolist() == b[0].tolist()
+
+
 def test_accept_fixtures():
     g = np.load(GOLD, allow_pickle=False)
     for mode in (0, 1):

@@ -84,3 +84,42 @@ def test_noalloc_rejects_oversized_shape(ih):
     y2 = _noalloc(ih, F.Q4_K, g, xx, torch.empty(2, 64, device="cuda"), 64, 1024, ih.GEMM_F32)
     torch.cuda.synchronize()
     assert torch.equal(y1, y2)
+
+
+def test_noalloc_under_graph_capture(ih):
+    """ihip_gemm_q_noalloc captured into a HIP graph (its scratch address
+    looked up by ihip_init beforehand, so the capture makes no lookup) and
+    replayed: every replay, with eager work and synchronisations between,
+    gives ihip_gemm_q's bits; then a smaller eager call after the replays."""
+    import torch
+    L = ih.load()
+    ih._lib.check(L.ihip_init(torch.cuda.current_device()))
+    q = ih.quantized_kernels
+    st = ih.synth.stream_for
+    N, K, M = 4096, 4096, 5
+    w = ih.pack_weights(F.Q4_K, q.synth_blocks(F.Q4_K, st(81, "na.g.w"), N * K // 256), N, K)
+    x = q.synth_gaussian(st(81, "na.g.x"), M * K).view(M, K)
+    fl = ih.GEMM_F32 | ih.GEMM_PACKED
+    y_ref = _with_ws(ih, F.Q4_K, w, x, torch.empty(M, N, device="cuda"), N, K, fl)
+    y = torch.empty(M, N, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _noalloc(ih, F.Q4_K, w, x, y, N, K, fl)  # warm-up outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        ih._lib.check(L.ihip_gemm_q_noalloc(F.Q4_K, w.data_ptr(), x.data_ptr(), y.data_ptr(), M, N, K, fl,
+                                            s.cuda_stream))
+    for r in range(4):
+        y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ref), r
+        _with_ws(ih, F.Q4_K, w, x, torch.empty(M, N, device="cuda"), N, K, fl)  # eager work between replays
+    x2 = x[:2].contiguous()
+    y2 = _noalloc(ih, F.Q4_K, w, x2, torch.empty(2, N, device="cuda"), N, K, fl)
+    y2_ref = _with_ws(ih, F.Q4_K, w, x2, torch.empty(2, N, device="cuda"), N, K, fl)
+    torch.cuda.synchronize()
+    assert torch.equal(y2, y2_ref)
