@@ -6,6 +6,13 @@
 // merge the partials in chunk order (deterministic). z = L / T as the
 // reference computes logits ./ temperature (src/ModelCPU.jl:1130-1132).
 //
+// Probabilities, their sums and every prefix sum of the draws are fp64:
+// exp((double)z - max) with the exponent's argument exact, sums and scans
+// in double. A draw over 151936 entries of mass ~1e-5 each moves when the
+// cumulative sum errs by a fraction of one entry's mass; fp32 sums err by
+// ~1e-7 of the total, which moved ~0.4 % of residual draws against the
+// exact prefix sums, fp64 ones by ~1e-15.
+//
 // Acceptance (src/SpeculativeDecoding.jl:75-104 with explicit uniforms) runs
 // as four launches: statistics of every target and draft row; one wave per
 // verify step for the ratio tests (lane i judges draft i); per (chunk, step)
@@ -22,12 +29,34 @@ namespace {
 constexpr int CHUNK = 4096;      // V elements per partial
 constexpr int NT = 256;          // threads per workgroup
 
-__device__ __forceinline__ void merge_ms(float &m, float &s, float m2, float s2) {
+// exp(z - m) with the subtraction exact (in double) and a double exp.
+__device__ __forceinline__ double dexp(float z, float m) { return exp((double)z - (double)m); }
+
+// Partial softmax statistics: max z and sum exp(z - max) (16 bytes).
+struct __align__(16) MS {
+    float m, pad;
+    double s;
+};
+__device__ __forceinline__ MS make_ms(float m, double s) {
+    MS r;
+    r.m = m;
+    r.pad = 0.f;
+    r.s = s;
+    return r;
+}
+
+// (m, s) merged with (m2, s2): the smaller maximum's sum rescaled. The same
+// bits whichever argument comes first (a single exp, then a commutative
+// add); a NaN or +Inf entry makes the sum NaN, as exp(Inf - Inf) does.
+__device__ __forceinline__ void merge_ms(float &m, double &s, float m2, double s2) {
     if (m2 == -__builtin_huge_valf()) return;
     if (m == -__builtin_huge_valf()) { m = m2; s = s2; return; }
-    const float M = fmaxf(m, m2);
-    s = s * __expf(m - M) + s2 * __expf(m2 - M);
-    m = M;
+    if (m >= m2) {
+        s = s + s2 * dexp(m2, m);
+    } else {
+        s = s * dexp(m, m2) + s2;
+        m = m2;
+    }
 }
 
 // Cross-lane moves on the VALU (DPP) and, across rows, one swizzle or
@@ -47,50 +76,46 @@ template <int O> __device__ __forceinline__ float partner(float v) {
         return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
     return __shfl_xor(v, 32);
 }
+template <int O> __device__ __forceinline__ double partner_d(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = __builtin_bit_cast(uint32_t, partner<O>(__builtin_bit_cast(float, (uint32_t)b)));
+    const uint32_t hi = __builtin_bit_cast(uint32_t, partner<O>(__builtin_bit_cast(float, (uint32_t)(b >> 32))));
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
 
 // Butterfly merge of one (max, sum) pair per lane (levels 1, 2, 4, 8, 16,
-// 32 as above); the lower lane of each pair merges first, so both partners
-// compute the same merge and every lane ends with the same value.
-template <int O> __device__ __forceinline__ void merge_level(float &m, float &s) {
-    const float m2 = partner<O>(m), s2 = partner<O>(s);
-    const bool upper = (threadIdx.x & O) != 0;
-    if (upper) {
-        merge_ms(m, s, m2, s2);
-    } else {
-        float mm = m2, ss = s2;
-        merge_ms(mm, ss, m, s);
-        m = mm;
-        s = ss;
-    }
+// 32 as above); merge_ms is symmetric, so both partners compute the same
+// bits and every lane ends with the same value.
+template <int O> __device__ __forceinline__ void merge_level(float &m, double &s) {
+    const float m2 = partner<O>(m);
+    const double s2 = partner_d<O>(s);
+    merge_ms(m, s, m2, s2);
 }
-__device__ __forceinline__ float2 wave_merge_pairs(float m, float s) {
+__device__ __forceinline__ MS wave_merge_pairs(float m, double s) {
     merge_level<1>(m, s);
     merge_level<2>(m, s);
     merge_level<4>(m, s);
     merge_level<8>(m, s);
     merge_level<16>(m, s);
     merge_level<32>(m, s);
-    return make_float2(m, s);
+    return make_ms(m, s);
 }
 
 // Block-wide (max, sum) merge of per-thread pairs.
-__device__ void block_merge_ms(float &m, float &s, float *sh) {
-    // wave level
-    const float2 wv = wave_merge_pairs(m, s);
-    m = wv.x;
-    s = wv.y;
+__device__ void block_merge_ms(float &m, double &s, MS *sh) {
+    const MS wv = wave_merge_pairs(m, s);
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-    if (l == 0) { sh[2 * w] = m; sh[2 * w + 1] = s; }
+    if (l == 0) sh[w] = wv;
     __syncthreads();
     if (threadIdx.x == 0) {
-        float M = sh[0], S = sh[1];
-        for (int i = 1; i < (int)(blockDim.x >> 6); i++) merge_ms(M, S, sh[2 * i], sh[2 * i + 1]);
-        sh[0] = M;
-        sh[1] = S;
+        float M = sh[0].m;
+        double S = sh[0].s;
+        for (int i = 1; i < (int)(blockDim.x >> 6); i++) merge_ms(M, S, sh[i].m, sh[i].s);
+        sh[0] = make_ms(M, S);
     }
     __syncthreads();
-    m = sh[0];
-    s = sh[1];
+    m = sh[0].m;
+    s = sh[0].s;
     __syncthreads();
 }
 
@@ -101,8 +126,8 @@ __device__ void block_merge_ms(float &m, float &s, float *sh) {
 constexpr int PER = CHUNK / NT;  // 16 entries per thread
 __global__ __launch_bounds__(NT) void stats_partial_kernel(const float *__restrict__ L1, int rows1, float T1,
                                                            float T_last, int period, const float *__restrict__ L2,
-                                                           float T2, int V, int nchunk, float2 *__restrict__ part) {
-    __shared__ float sh[2 * NT / 64];
+                                                           float T2, int V, int nchunk, MS *__restrict__ part) {
+    __shared__ MS sh[NT / 64];
     const int chunk = blockIdx.x, row = blockIdx.y;
     const bool first = row < rows1;
     const float Tr = first ? ((period > 0 && row % period == period - 1) ? T_last : T1) : T2;
@@ -117,49 +142,51 @@ __global__ __launch_bounds__(NT) void stats_partial_kernel(const float *__restri
     float m = -__builtin_huge_valf();
 #pragma unroll
     for (int i = 0; i < PER; i++) m = fmaxf(m, z[i]);
-    float s = 0.f;
+    double s = 0.0;
     if (m > -__builtin_huge_valf()) {
 #pragma unroll
-        for (int i = 0; i < PER; i++) s += __expf(z[i] - m);
+        for (int i = 0; i < PER; i++) s += dexp(z[i], m);
     }
     block_merge_ms(m, s, sh);
-    if (threadIdx.x == 0) part[(size_t)row * nchunk + chunk] = make_float2(m, s);
+    if (threadIdx.x == 0) part[(size_t)row * nchunk + chunk] = make_ms(m, s);
 }
 
 // Sequential merge of a row's chunk partials (chunk order), the loads issued
 // eight at a time.
-__device__ __forceinline__ float2 merge_row(const float2 *part, int nchunk) {
-    float m = -__builtin_huge_valf(), s = 0.f;
+__device__ __forceinline__ MS merge_row(const MS *part, int nchunk) {
+    float m = -__builtin_huge_valf();
+    double s = 0.0;
     for (int c = 0; c < nchunk; c += 8) {
-        float2 v[8];
+        MS v[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) v[j] = part[min(c + j, nchunk - 1)];
 #pragma unroll
         for (int j = 0; j < 8; j++)
-            if (c + j < nchunk) merge_ms(m, s, v[j].x, v[j].y);
+            if (c + j < nchunk) merge_ms(m, s, v[j].m, v[j].s);
     }
-    return make_float2(m, s);
+    return make_ms(m, s);
 }
 
 // Merge of a row's chunk partials by one wave: lane l folds chunks l, l+64,
 // ... in order, then the butterfly.
-__device__ __forceinline__ float2 wave_merge_row(const float2 *part, int nchunk) {
+__device__ __forceinline__ MS wave_merge_row(const MS *part, int nchunk) {
     const int lane = threadIdx.x & 63;
-    float m = -__builtin_huge_valf(), s = 0.f;
+    float m = -__builtin_huge_valf();
+    double s = 0.0;
     for (int c = lane; c < nchunk; c += 64) {
-        const float2 p = part[c];
-        merge_ms(m, s, p.x, p.y);
+        const MS p = part[c];
+        merge_ms(m, s, p.m, p.s);
     }
     return wave_merge_pairs(m, s);
 }
 
-__global__ void stats_merge_kernel(const float2 *__restrict__ part, int rows, int nchunk,
-                                   float *__restrict__ zmax, float *__restrict__ zsum) {
+__global__ void stats_merge_kernel(const MS *__restrict__ part, int rows, int nchunk, float *__restrict__ zmax,
+                                   float *__restrict__ zsum) {
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= rows) return;
-    const float2 ms = merge_row(part + (size_t)r * nchunk, nchunk);
-    zmax[r] = ms.x;
-    zsum[r] = ms.y;
+    const MS ms = merge_row(part + (size_t)r * nchunk, nchunk);
+    zmax[r] = ms.m;
+    zsum[r] = (float)ms.s;
 }
 
 // Sampling distribution of one draw of a verify step, set by the ratio
@@ -178,29 +205,25 @@ __global__ void stats_merge_kernel(const float2 *__restrict__ part, int rows, in
 // second slot holds the bonus the reference appends after a rejection of
 // the last draft (src/SpeculativeDecoding.jl:100: length(accepted) == gamma).
 struct Decision {
-    int kind, n, prow, qrow, fallback, pos, pad1, pad2;
-    float Tp, mp, sp, Tq, mq, sq, qs, u;
+    int kind, n, prow, qrow, fallback, pos;
+    float Tp, mp, Tq, mq, u, pad;
+    double sp, sq, qs;
 };
 __host__ __device__ constexpr int draw_slots(int mode) { return mode == 1 ? 2 : 1; }
-
-__device__ __forceinline__ float p_of(const Decision &D, const float *lt, int j) {
-    return __expf(lt[j] / D.Tp - D.mp) / D.sp;
-}
-__device__ __forceinline__ float w_of(const Decision &D, float p, const float *ld, int j) {
-    if (D.kind == 0) return p;
-    const float q = D.kind == 1 ? __expf(ld[j] / D.Tq - D.mq) / D.sq : D.qs;
-    return fmaxf(p - q, 0.f);
-}
 
 // Inclusive scan over the 64 lanes of a wave (fixed association): a
 // Hillis-Steele scan inside each row of 16 (DPP row shifts by 1, 2, 4, 8;
 // lanes shifted in from outside the row read 0), then row r + 1 adds the
 // total of row r (row broadcast of lane 15 into rows 1 and 3) and rows 2, 3
 // add the total of rows 0, 1 (row broadcast of lane 31).
-template <int CTRL, int ROWS> __device__ __forceinline__ float dpp_row(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, true));
+// A double moves as its two halves.
+template <int CTRL, int ROWS> __device__ __forceinline__ double dpp_row(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROWS, 0xF, true);
+    const uint32_t hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROWS, 0xF, true);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
-__device__ __forceinline__ float wave_scan(float v) {
+__device__ __forceinline__ double wave_scan(double v) {
     v += dpp_row<0x111, 0xF>(v);  // row_shr:1
     v += dpp_row<0x112, 0xF>(v);  // row_shr:2
     v += dpp_row<0x114, 0xF>(v);  // row_shr:4
@@ -222,16 +245,16 @@ constexpr int DECIDE_WAVES = NT / 64;
 __device__ void decide_block(const float *__restrict__ tgt, const float *__restrict__ drf,
                              const int32_t *__restrict__ draft_tok, int k, int V, float T,
                              const float *__restrict__ u_acc, const float *__restrict__ u_res,
-                             const float *__restrict__ u_bonus, int mode, const float2 *__restrict__ part,
+                             const float *__restrict__ u_bonus, int mode, const MS *__restrict__ part,
                              int nchunk, int step, int steps, bool publish, const int32_t *__restrict__ bonus_pre,
                              int32_t *__restrict__ out_tok, int32_t *__restrict__ out_n,
-                             Decision *__restrict__ dec, float2 *ms, Decision *s_dec) {
+                             Decision *__restrict__ dec, MS *ms, Decision *s_dec) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const float *Lt = tgt + (size_t)step * (k + 1) * V;
     const float *Ld = drf + (size_t)step * k * V;
     const int32_t *dt = draft_tok + (size_t)step * k;
-    const float2 *Pt = part + (size_t)step * (k + 1) * nchunk;
-    const float2 *Pd = part + ((size_t)steps * (k + 1) + (size_t)step * k) * nchunk;
+    const MS *Pt = part + (size_t)step * (k + 1) * nchunk;
+    const MS *Pd = part + ((size_t)steps * (k + 1) + (size_t)step * k) * nchunk;
     const float Tr = mode == 0 ? T : 1.0f;
     // wave 0: the first 64 drafts' ids and uniforms, then (once the ids are
     // in) their two logits, issued before the merges
@@ -242,15 +265,15 @@ __device__ void decide_block(const float *__restrict__ tgt, const float *__restr
     float lx0 = 0.f, dx0 = 0.f;
     // rows wave, wave + W, ..: in batches of 8 per wave
     for (int r0 = wave; r0 < nrows; r0 += 8 * DECIDE_WAVES) {
-        float2 pv[8][2];
+        MS pv[8][2];
 #pragma unroll
         for (int b = 0; b < 8; b++) {
             const int r = min(r0 + b * DECIDE_WAVES, nrows - 1);
-            const float2 *row = r <= k ? Pt + (size_t)r * nchunk : Pd + (size_t)(r - k - 1) * nchunk;
+            const MS *row = r <= k ? Pt + (size_t)r * nchunk : Pd + (size_t)(r - k - 1) * nchunk;
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const int c = lane + 64 * h;
-                pv[b][h] = c < nchunk ? row[c] : make_float2(-__builtin_huge_valf(), 0.f);
+                pv[b][h] = c < nchunk ? row[c] : make_ms(-__builtin_huge_valf(), 0.0);
             }
         }
         if (r0 == 0 && has0 && x0 >= 0 && x0 < V) {
@@ -261,11 +284,12 @@ __device__ void decide_block(const float *__restrict__ tgt, const float *__restr
         for (int b = 0; b < 8; b++) {
             const int r = r0 + b * DECIDE_WAVES;
             if (r >= nrows) break;
-            float2 v;
+            MS v;
             if (nchunk <= 128) {
-                float m = -__builtin_huge_valf(), sm = 0.f;
-                merge_ms(m, sm, pv[b][0].x, pv[b][0].y);
-                merge_ms(m, sm, pv[b][1].x, pv[b][1].y);
+                float m = -__builtin_huge_valf();
+                double sm = 0.0;
+                merge_ms(m, sm, pv[b][0].m, pv[b][0].s);
+                merge_ms(m, sm, pv[b][1].m, pv[b][1].s);
                 v = wave_merge_pairs(m, sm);
             } else {
                 v = wave_merge_row(r <= k ? Pt + (size_t)r * nchunk : Pd + (size_t)(r - k - 1) * nchunk, nchunk);
@@ -277,22 +301,22 @@ __device__ void decide_block(const float *__restrict__ tgt, const float *__restr
     if (wave == 0) {
         int first = k;  // first draft that is invalid or rejected
         bool invalid = false;
-        float f_q = 0.f;
+        double f_q = 0.0;
         for (int base = 0; base < k && first == k; base += 64) {
             const int i = base + lane;
             bool bad = false, inv = false;
-            float q = 0.f;
+            double q = 0.0;
             if (i < k) {
                 const bool pre = base == 0;  // the first 64 were fetched up front
                 const int x = pre ? x0 : dt[i];
                 if (x < 0 || x >= V) {
                     bad = inv = true;
                 } else {
-                    const float2 pt = ms[i], pd = ms[k + 1 + i];
-                    const float p = __expf((pre ? lx0 : Lt[(size_t)i * V + x]) / Tr - pt.x) / pt.y;
-                    q = __expf((pre ? dx0 : Ld[(size_t)i * V + x]) / Tr - pd.x) / pd.y;
-                    const float ratio = q > 0.f ? fminf(1.0f, p / q) : 1.0f;
-                    bad = !((pre ? ua0 : u_acc[(size_t)step * k + i]) < ratio);
+                    const MS pt = ms[i], pd = ms[k + 1 + i];
+                    const double p = dexp((pre ? lx0 : Lt[(size_t)i * V + x]) / Tr, pt.m) / pt.s;
+                    q = dexp((pre ? dx0 : Ld[(size_t)i * V + x]) / Tr, pd.m) / pd.s;
+                    const double ratio = q > 0.0 ? fmin(1.0, p / q) : 1.0;
+                    bad = !((double)(pre ? ua0 : u_acc[(size_t)step * k + i]) < ratio);
                 }
             }
             const uint64_t m = __ballot(bad);
@@ -317,33 +341,33 @@ __device__ void decide_block(const float *__restrict__ tgt, const float *__restr
                 D.n = first;
                 D.pos = first;
                 if (first < k) {
-                    const float2 pt = ms[first], pd = ms[k + 1 + first];
+                    const MS pt = ms[first], pd = ms[k + 1 + first];
                     D.kind = mode == 0 ? 1 : 2;
                     D.prow = first;
                     D.qrow = first;
-                    D.Tp = Tr; D.mp = pt.x; D.sp = pt.y;
-                    D.Tq = Tr; D.mq = pd.x; D.sq = pd.y;
+                    D.Tp = Tr; D.mp = pt.m; D.sp = pt.s;
+                    D.Tq = Tr; D.mq = pd.m; D.sq = pd.s;
                     D.qs = f_q;
                     D.u = u_res[step];
                     D.fallback = mode == 0 ? 1 : 2;
                     if (mode == 1 && first == k - 1) {  // the reference's bonus after the residual
-                        const float2 pk = ms[k];
+                        const MS pk = ms[k];
                         D2.kind = bonus_pre ? 3 : 0;
                         D2.n = first;
                         D2.pos = first + 1;
                         D2.prow = k;
-                        D2.Tp = T; D2.mp = pk.x; D2.sp = pk.y;
-                        D2.Tq = T; D2.mq = 0.f; D2.sq = 1.f;
+                        D2.Tp = T; D2.mp = pk.m; D2.sp = pk.s;
+                        D2.Tq = T; D2.mq = 0.f; D2.sq = 1.0;
                         D2.u = u_bonus[step];
                         D2.fallback = 2;
                     }
                 } else {
-                    const float2 pt = ms[k];
+                    const MS pt = ms[k];
                     D.kind = bonus_pre ? 3 : 0;
                     D.prow = k;
                     D.qrow = 0;
-                    D.Tp = T; D.mp = pt.x; D.sp = pt.y;
-                    D.Tq = T; D.mq = 0.f; D.sq = 1.f; D.qs = 0.f;
+                    D.Tp = T; D.mp = pt.m; D.sp = pt.s;
+                    D.Tq = T; D.mq = 0.f; D.sq = 1.0; D.qs = 0.0;
                     D.u = u_bonus[step];
                     D.fallback = 2;
                 }
@@ -365,12 +389,12 @@ __device__ void decide_block(const float *__restrict__ tgt, const float *__restr
 // Per round r: wave inclusive scans, round total R_r = ((T0 + T1) + T2) + T3
 // of the four wave totals.
 struct ChunkScan {
-    float w[PER], cw[PER];  // weights and their wave-inclusive scans
-    float R[PER];           // round totals (uniform)
+    double cw[PER];  // wave-inclusive scans of the weights
+    double R[PER];   // round totals (uniform)
 };
 
 __device__ void chunk_scan(const Decision &D, const float *lt, const float *ld, int V, int c, bool use_p,
-                           ChunkScan &cs, float *sh /* [PER][4] */) {
+                           ChunkScan &cs, double *sh /* [PER][4] */) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     // every load of the chunk in flight before any arithmetic
     float lv[PER], dv[PER];
@@ -384,13 +408,12 @@ __device__ void chunk_scan(const Decision &D, const float *lt, const float *ld, 
 #pragma unroll
     for (int r = 0; r < PER; r++) {
         const int j = c * CHUNK + r * NT + t;
-        float w = 0.f;
+        double w = 0.0;
         if (j < V) {
-            const float p = __expf(lv[r] / D.Tp - D.mp) / D.sp;
+            const double p = dexp(lv[r] / D.Tp, D.mp) / D.sp;
             if (use_p || D.kind == 0) w = p;
-            else w = fmaxf(p - (D.kind == 1 ? __expf(dv[r] / D.Tq - D.mq) / D.sq : D.qs), 0.f);
+            else w = fmax(p - (D.kind == 1 ? dexp(dv[r] / D.Tq, D.mq) / D.sq : D.qs), 0.0);
         }
-        cs.w[r] = w;
         cs.cw[r] = wave_scan(w);
         if (lane == 63) sh[r * 4 + wave] = cs.cw[r];
     }
@@ -409,12 +432,12 @@ __global__ __launch_bounds__(NT) void decide_sum_kernel(const float *__restrict_
                                                         const float *__restrict__ u_acc,
                                                         const float *__restrict__ u_res,
                                                         const float *__restrict__ u_bonus, int mode,
-                                                        const float2 *__restrict__ part, int nchunk,
+                                                        const MS *__restrict__ part, int nchunk,
                                                         const int32_t *__restrict__ bonus_pre,
                                                         int32_t *__restrict__ out_tok, int32_t *__restrict__ out_n,
-                                                        Decision *__restrict__ dec, float *__restrict__ csum) {
-    __shared__ float sh[PER * 4];
-    __shared__ float2 ms[DECIDE_MAX_ROWS];
+                                                        Decision *__restrict__ dec, double *__restrict__ csum) {
+    __shared__ double sh[PER * 4];
+    __shared__ MS ms[DECIDE_MAX_ROWS];
     __shared__ Decision s_dec[2];
     const int c = blockIdx.x, step = blockIdx.y;
     decide_block(tgt, drf, draft_tok, k, V, T, u_acc, u_res, u_bonus, mode, part, nchunk, step, gridDim.y,
@@ -426,7 +449,7 @@ __global__ __launch_bounds__(NT) void decide_sum_kernel(const float *__restrict_
     const float *ld = D.kind == 1 ? drf + ((size_t)step * k + D.qrow) * V : nullptr;
     ChunkScan cs;
     chunk_scan(D, lt, ld, V, c, false, cs, sh);
-    float sw = 0.f;
+    double sw = 0.0;
 #pragma unroll
     for (int r = 0; r < PER; r++) sw += cs.R[r];
     if (threadIdx.x == 0) csum[slot * nchunk + c] = sw;
@@ -439,13 +462,13 @@ __global__ __launch_bounds__(NT) void decide_sum_kernel(const float *__restrict_
 constexpr int MAX_CHUNKS = 1024;
 __global__ __launch_bounds__(NT) void sample_kernel(const float *__restrict__ tgt, const float *__restrict__ drf,
                                                     int k, int V, const Decision *__restrict__ dec, int nchunk,
-                                                    const float *__restrict__ csum,
+                                                    const double *__restrict__ csum,
                                                     const int32_t *__restrict__ bonus_pre,
                                                     int32_t *__restrict__ out_tok) {
-    __shared__ float sh[PER * 4];
-    __shared__ float s_psum[MAX_CHUNKS];
-    __shared__ float s_csum[MAX_CHUNKS];
-    __shared__ float s_before, s_target;
+    __shared__ double sh[PER * 4];
+    __shared__ double s_psum[MAX_CHUNKS];
+    __shared__ double s_csum[MAX_CHUNKS];
+    __shared__ double s_before, s_target;
     __shared__ int s_chunk, s_usep, s_tok;
     __shared__ int s_first[NT / 64];
     const int step = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
@@ -456,17 +479,17 @@ __global__ __launch_bounds__(NT) void sample_kernel(const float *__restrict__ tg
         if (t == 0) out_tok[(size_t)step * (k + 1) + D.pos] = bonus_pre[step];
         return;
     }
-    const float *cw = csum + slot * nchunk;
+    const double *cw = csum + slot * nchunk;
     const float *lt = tgt + ((size_t)step * (k + 1) + D.prow) * V;
     const float *ld = D.kind == 1 ? drf + ((size_t)step * k + D.qrow) * V : nullptr;
     for (int c = t; c < nchunk; c += NT) s_csum[c] = cw[c];
     __syncthreads();
     if (t == 0) {
-        float S = 0.f;
+        double S = 0.0;
         for (int c = 0; c < nchunk; c++) S += s_csum[c];
         s_usep = 0;
         s_tok = -1;
-        if (!(S > 0.f)) {
+        if (!(S > 0.0)) {
             if (D.fallback == 1) s_usep = 1;
             else s_tok = V - 1;
         }
@@ -482,7 +505,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(const float *__restrict__ tg
         for (int c = 0; c < nchunk; c++) {
             chunk_scan(D, lt, ld, V, c, true, cs, sh);
             if (t == 0) {
-                float sp = 0.f;
+                double sp = 0.0;
 #pragma unroll
                 for (int r = 0; r < PER; r++) sp += cs.R[r];
                 s_psum[c] = sp;
@@ -491,13 +514,13 @@ __global__ __launch_bounds__(NT) void sample_kernel(const float *__restrict__ tg
         __syncthreads();
     }
     if (t == 0) {
-        float S = 0.f;
+        double S = 0.0;
         for (int c = 0; c < nchunk; c++) S += usep ? s_psum[c] : s_csum[c];
-        const float target = D.u * S;
-        float before = 0.f;
+        const double target = (double)D.u * S;
+        double before = 0.0;
         int chunk = nchunk - 1;
         for (int c = 0; c < nchunk; c++) {
-            const float nb = before + (usep ? s_psum[c] : s_csum[c]);
+            const double nb = before + (usep ? s_psum[c] : s_csum[c]);
             if (target <= nb) { chunk = c; break; }
             before = nb;
         }
@@ -507,14 +530,14 @@ __global__ __launch_bounds__(NT) void sample_kernel(const float *__restrict__ tg
     }
     __syncthreads();
     const int c = s_chunk;
-    const float before = s_before, target = s_target;
+    const double before = s_before, target = s_target;
     chunk_scan(D, lt, ld, V, c, usep, cs, sh);
     // round: first r with target <= before + P_{r+1}
-    float P = 0.f, Pr = 0.f;
+    double P = 0.0, Pr = 0.0;
     int rr = -1;
 #pragma unroll
     for (int r = 0; r < PER; r++) {
-        const float Pn = P + cs.R[r];
+        const double Pn = P + cs.R[r];
         if (rr < 0 && target <= before + Pn) { rr = r; Pr = P; }
         P = Pn;
     }
@@ -522,15 +545,15 @@ __global__ __launch_bounds__(NT) void sample_kernel(const float *__restrict__ tg
         rr = PER - 1;
         Pr = P - cs.R[PER - 1];
     }
-    float cw_rr = 0.f;
+    double cw_rr = 0.0;
 #pragma unroll
     for (int r = 0; r < PER; r++)
         if (r == rr) cw_rr = cs.cw[r];
     if (lane == 63) sh[wave] = cw_rr;
     __syncthreads();
-    float off = 0.f;
+    double off = 0.0;
     for (int w = 0; w < wave; w++) off += sh[w];
-    const float C = before + (Pr + (off + cw_rr));
+    const double C = before + (Pr + (off + cw_rr));
     const int j = c * CHUNK + rr * NT + t;
     const bool hit = j < V && target <= C;
     const uint64_t m = __ballot(hit);
@@ -619,7 +642,7 @@ constexpr int TREE_LDS = 4096;
 __global__ __launch_bounds__(NT) void tree_kernel(const float *__restrict__ tgt, const float *__restrict__ drf,
                                                   const int32_t *__restrict__ tok, const int32_t *__restrict__ parent,
                                                   int n, int V, float T, const float *__restrict__ u,
-                                                  const float2 *__restrict__ part, int nchunk, float2 *__restrict__ ms,
+                                                  const MS *__restrict__ part, int nchunk, MS *__restrict__ ms,
                                                   int32_t *__restrict__ out_path, int32_t *__restrict__ out_len,
                                                   int32_t *__restrict__ wsi) {
     __shared__ int32_t s_par[TREE_LDS], s_st[TREE_LDS];
@@ -627,7 +650,7 @@ __global__ __launch_bounds__(NT) void tree_kernel(const float *__restrict__ tgt,
     const bool in_lds = n <= TREE_LDS;
     int32_t *par = in_lds ? s_par : wsi;
     int32_t *st = in_lds ? s_st : wsi + n;
-    int8_t *pass = in_lds ? s_pass : (int8_t *)(ms + 2 * n);
+    int8_t *pass = in_lds ? s_pass : (int8_t *)(wsi + 2 * n);
     for (int r = threadIdx.x; r < 2 * n; r += blockDim.x) ms[r] = merge_row(part + (size_t)r * nchunk, nchunk);
     __syncthreads();
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
@@ -639,12 +662,12 @@ __global__ __launch_bounds__(NT) void tree_kernel(const float *__restrict__ tgt,
             if (p < 0 || p >= i || x < 0 || x >= V) {
                 r = -1;  // malformed node: reported as out_len = -1
             } else {
-                const float2 pt = ms[p];
-                const float2 pd = ms[n + p];
-                const float pp = __expf(tgt[(size_t)p * V + x] / T - pt.x) / pt.y;
-                const float qq = __expf(drf[(size_t)p * V + x] / T - pd.x) / pd.y;
-                const float ratio = qq > 0.f ? fminf(1.0f, pp / qq) : 1.0f;
-                r = u[i] < ratio ? 1 : 0;
+                const MS pt = ms[p];
+                const MS pd = ms[n + p];
+                const double pp = dexp(tgt[(size_t)p * V + x] / T, pt.m) / pt.s;
+                const double qq = dexp(drf[(size_t)p * V + x] / T, pd.m) / pd.s;
+                const double ratio = qq > 0.0 ? fmin(1.0, pp / qq) : 1.0;
+                r = (double)u[i] < ratio ? 1 : 0;
             }
         }
         pass[i] = r;
@@ -677,28 +700,32 @@ __global__ __launch_bounds__(NT) void tree_kernel(const float *__restrict__ tgt,
 
 int accept_nchunk(int V) { return (V + CHUNK - 1) / CHUNK; }
 
-hipError_t launch_stats(const float *L, int rows, int V, float T, float T_last, int period, float2 *part,
+// Bytes of one softmax partial (MS) of a (row, chunk); a first-argmax
+// partial (float2) fits in the same slot.
+size_t accept_part_bytes() { return sizeof(MS); }
+
+hipError_t launch_stats(const float *L, int rows, int V, float T, float T_last, int period, void *part,
                         hipStream_t st) {
     if (rows <= 0) return hipSuccess;
     const int nc = accept_nchunk(V);
-    stats_partial_kernel<<<dim3(nc, rows), NT, 0, st>>>(L, rows, T, T_last, period, L, T, V, nc, part);
+    stats_partial_kernel<<<dim3(nc, rows), NT, 0, st>>>(L, rows, T, T_last, period, L, T, V, nc, (MS *)part);
     return hipGetLastError();
 }
 
-hipError_t launch_stats_merge(const float2 *part, int rows, int V, float *zmax, float *zsum, hipStream_t st) {
+hipError_t launch_stats_merge(const void *part, int rows, int V, float *zmax, float *zsum, hipStream_t st) {
     const int nc = accept_nchunk(V);
-    stats_merge_kernel<<<(rows + 63) / 64, 64, 0, st>>>(part, rows, nc, zmax, zsum);
+    stats_merge_kernel<<<(rows + 63) / 64, 64, 0, st>>>((const MS *)part, rows, nc, zmax, zsum);
     return hipGetLastError();
 }
 
 size_t spec_accept_ws(int steps, int k, int V) {
     const size_t nc = accept_nchunk(V);
-    return (size_t)steps * (2 * k + 1) * nc * sizeof(float2) + (size_t)steps * 2 * sizeof(Decision) +
-           (size_t)steps * 2 * nc * sizeof(float) + 256;
+    return (size_t)steps * (2 * k + 1) * nc * sizeof(MS) + (size_t)steps * 2 * sizeof(Decision) +
+           (size_t)steps * 2 * nc * sizeof(double) + 256;
 }
 
-// ws: float2 part[steps*(k+1) + steps*k][nchunk], Decision dec[steps][slots],
-// float csum[steps][slots][nchunk] (slots = draw_slots(mode)). bonus_pre
+// ws: MS part[steps*(k+1) + steps*k][nchunk], Decision dec[steps][slots],
+// double csum[steps][slots][nchunk] (slots = draw_slots(mode)). bonus_pre
 // (nullptr: none): each step's bonus token, drawn beforehand from target row
 // k by the filtered sampler; bonus draws then copy it.
 hipError_t launch_spec_accept(const float *tgt, const float *drf, const int32_t *draft_tok, int steps, int k,
@@ -708,9 +735,9 @@ hipError_t launch_spec_accept(const float *tgt, const float *drf, const int32_t 
     const int nc = accept_nchunk(V);
     const float Tr = mode == 0 ? T : 1.0f;
     const int nd = draw_slots(mode);
-    float2 *part = (float2 *)ws;
+    MS *part = (MS *)ws;
     Decision *dec = (Decision *)(part + (size_t)steps * (2 * k + 1) * nc);
-    float *csum = (float *)(dec + (size_t)steps * nd);
+    double *csum = (double *)(dec + (size_t)steps * nd);
     stats_partial_kernel<<<dim3(nc, steps * (2 * k + 1)), NT, 0, st>>>(tgt, steps * (k + 1), Tr, T, k + 1,
                                                                       drf, Tr, V, nc, part);
     hipError_t e = hipGetLastError();
@@ -735,16 +762,21 @@ hipError_t launch_greedy(const float2 *part, int V, const int32_t *draft_tok, in
     return hipGetLastError();
 }
 
-// part: float2 [2n][nchunk] (target rows then draft rows); wsi: int32 [2n], then
-// ms: float2 [2n], then (above TREE_LDS nodes) int8 [n].
+// ws: MS part[2n][nchunk] (target rows then draft rows), MS ms[2n] (their
+// merged statistics), then (above TREE_LDS nodes) int32 [2n] and int8 [n].
+size_t tree_ws(int n, int V) {
+    return ((size_t)2 * n * accept_nchunk(V) + 2 * (size_t)n) * sizeof(MS) + (size_t)n * 9 + 256;
+}
+
 hipError_t launch_tree(const float *tgt, const float *drf, const int32_t *tok, const int32_t *parent, int n, int V,
-                       float T, const float *u, float2 *part, int32_t *out_path, int32_t *out_len,
-                       int32_t *wsi, hipStream_t st) {
+                       float T, const float *u, void *ws, int32_t *out_path, int32_t *out_len, hipStream_t st) {
     const int nc = accept_nchunk(V);
+    MS *part = (MS *)ws;
+    MS *ms = part + (size_t)2 * n * nc;
+    int32_t *wsi = (int32_t *)(ms + 2 * n);
     stats_partial_kernel<<<dim3(nc, 2 * n), NT, 0, st>>>(tgt, n, T, T, 0, drf, T, V, nc, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    float2 *ms = (float2 *)(wsi + 2 * n);
     tree_kernel<<<1, NT, 0, st>>>(tgt, drf, tok, parent, n, V, T, u, part, nc, ms, out_path, out_len, wsi);
     return hipGetLastError();
 }

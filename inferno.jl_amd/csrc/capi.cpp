@@ -26,9 +26,10 @@ void gemm_partials(int qt, int M, int N, int K, int flags, size_t *offset, int *
 hipError_t launch_pack(int qt, const void *W, void *P, int N, int K, hipStream_t st, int gated);
 hipError_t launch_dequant(int qt, const void *w, float *out, int64_t n_blocks, hipStream_t st);
 int accept_nchunk(int V);
-hipError_t launch_stats(const float *L, int rows, int V, float T, float T_last, int period, float2 *part,
+size_t accept_part_bytes();
+hipError_t launch_stats(const float *L, int rows, int V, float T, float T_last, int period, void *part,
                         hipStream_t st);
-hipError_t launch_stats_merge(const float2 *part, int rows, int V, float *zmax, float *zsum, hipStream_t st);
+hipError_t launch_stats_merge(const void *part, int rows, int V, float *zmax, float *zsum, hipStream_t st);
 hipError_t launch_spec_accept(const float *tgt, const float *drf, const int32_t *draft_tok, int steps, int k,
                               int V, float T, const float *u_acc, const float *u_res, const float *u_bonus,
                               int mode, const int32_t *bonus_pre, int32_t *out_tok, int32_t *out_n, void *ws,
@@ -37,9 +38,9 @@ size_t spec_accept_ws(int steps, int k, int V);
 hipError_t launch_argmax_partial(const float *L, int rows, int V, float2 *part, hipStream_t st);
 hipError_t launch_greedy(const float2 *part, int V, const int32_t *draft_tok, int steps, int k, int32_t *out_n,
                          int32_t *out_argmax, hipStream_t st);
+size_t tree_ws(int n, int V);
 hipError_t launch_tree(const float *tgt, const float *drf, const int32_t *tok, const int32_t *parent, int n, int V,
-                       float T, const float *u, float2 *part, int32_t *out_path, int32_t *out_len, int32_t *wsi,
-                       hipStream_t st);
+                       float T, const float *u, void *ws, int32_t *out_path, int32_t *out_len, hipStream_t st);
 hipError_t launch_rmsnorm(const float *x, const float *w, float *out, int rows, int n, float eps, hipStream_t st);
 hipError_t launch_silu_mul(const float *gu, int M, int F, float *out, hipStream_t st);
 hipError_t launch_add(float *y, const float *x, int64_t n, hipStream_t st);
@@ -744,7 +745,7 @@ int ihip_add(float *y_dev, const float *x_dev, int64_t n, void *stream) {
 int ihip_accept_ws_bytes(int rows, int V, size_t *bytes) {
     if (!bytes) return fail(IHIP_EFAULT, "ihip_accept_ws_bytes: NULL");
     if (rows < 0 || V < 1) return fail(IHIP_EINVAL, "ihip_accept_ws_bytes: rows=%d V=%d", rows, V);
-    *bytes = (size_t)rows * accept_nchunk(V) * sizeof(float2) + (size_t)rows * 8 + 256;
+    *bytes = (size_t)rows * accept_nchunk(V) * accept_part_bytes() + (size_t)rows * 16 + 256;
     return ok();
 }
 
@@ -763,9 +764,8 @@ int ihip_softmax_stats(const float *logits_dev, int rows, int V, float T, float 
     if (rows < 1 || V < 1 || !(T > 0.f)) return fail(IHIP_EINVAL, "ihip_softmax_stats: rows=%d V=%d T=%g", rows, V, T);
     int rc = need_ws("ihip_softmax_stats", rows, V, ws, ws_bytes);
     if (rc != IHIP_OK) return rc;
-    float2 *part = (float2 *)ws;
-    hipError_t e = launch_stats(logits_dev, rows, V, T, T, 0, part, S(stream));
-    if (e == hipSuccess) e = launch_stats_merge(part, rows, V, zmax_dev, zsum_dev, S(stream));
+    hipError_t e = launch_stats(logits_dev, rows, V, T, T, 0, ws, S(stream));
+    if (e == hipSuccess) e = launch_stats_merge(ws, rows, V, zmax_dev, zsum_dev, S(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_softmax_stats");
 }
 
@@ -790,8 +790,8 @@ static size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 // rows gathered contiguously (steps > 1), the sampler's workspace over them,
 // and the drawn bonus tokens.
 static size_t spec_accept_ex_ws(int steps, int k, int V, bool filtered) {
+    if (!filtered) return spec_accept_ws(steps, k, V);
     size_t b = round256(spec_accept_ws(steps, k, V));
-    if (!filtered) return b;
     if (steps > 1) b += round256((size_t)steps * V * sizeof(float));
     return b + round256(sample_spread_ws(steps, V)) + round256((size_t)steps * sizeof(int32_t));
 }
@@ -893,10 +893,10 @@ int ihip_tree_accept(const float *tgt_dev, const float *drf_dev, const int32_t *
     if (n < 1 || V < 1 || !(T > 0.f)) return fail(IHIP_EINVAL, "ihip_tree_accept: n=%d V=%d T=%g", n, V, T);
     int rc = need_ws("ihip_tree_accept", 3 * n, V, ws, ws_bytes);
     if (rc != IHIP_OK) return rc;
-    float2 *part = (float2 *)ws;
-    int32_t *wsi = (int32_t *)(part + (size_t)2 * n * accept_nchunk(V));
-    hipError_t e = launch_tree(tgt_dev, drf_dev, tok_dev, parent_dev, n, V, T, u_dev, part, out_path_dev,
-                               out_len_dev, wsi, S(stream));
+    if (ws_bytes < tree_ws(n, V))  // (ihip_accept_ws_bytes(3 n, V) covers it)
+        return fail(IHIP_ENOMEM, "ihip_tree_accept: workspace %zu < %zu bytes", ws_bytes, tree_ws(n, V));
+    hipError_t e = launch_tree(tgt_dev, drf_dev, tok_dev, parent_dev, n, V, T, u_dev, ws, out_path_dev,
+                               out_len_dev, S(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_tree_accept");
 }
 
