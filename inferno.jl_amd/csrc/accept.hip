@@ -29,8 +29,20 @@ namespace {
 constexpr int CHUNK = 4096;      // V elements per partial
 constexpr int NT = 256;          // threads per workgroup
 
-// exp(z - m) with the subtraction exact (in double) and a double exp.
-__device__ __forceinline__ double dexp(float z, float m) { return exp((double)z - (double)m); }
+// exp(z - m) for an entry's probability: the difference rounded to fp32 plus
+// its exact rounding error (two-sum), the accurate fp32 exp of the former
+// times 1 + the latter (relative error ~1e-7, independent across entries;
+// summed in double, such errors move a prefix sum by far less than one
+// entry's mass). Non-finite differences give exp's own result.
+__device__ __forceinline__ double dexp(float z, float m) {
+    const float d = z - m;
+    const float bz = d - z;
+    const float err = (z - (d - bz)) + (-m - bz);
+    const float e = expf(d);
+    return (double)(e > 0.f && e < __builtin_huge_valf() ? fmaf(e, err, e) : e);
+}
+// exp(m2 - m) in double for rescaling a partial sum (a few per row).
+__device__ __forceinline__ double rescale(float m2, float m) { return exp((double)m2 - (double)m); }
 
 // Partial softmax statistics: max z and sum exp(z - max) (16 bytes).
 struct __align__(16) MS {
@@ -52,9 +64,9 @@ __device__ __forceinline__ void merge_ms(float &m, double &s, float m2, double s
     if (m2 == -__builtin_huge_valf()) return;
     if (m == -__builtin_huge_valf()) { m = m2; s = s2; return; }
     if (m >= m2) {
-        s = s + s2 * dexp(m2, m);
+        s = s + s2 * rescale(m2, m);
     } else {
-        s = s * dexp(m, m2) + s2;
+        s = s * rescale(m, m2) + s2;
         m = m2;
     }
 }
@@ -207,7 +219,7 @@ __global__ void stats_merge_kernel(const MS *__restrict__ part, int rows, int nc
 struct Decision {
     int kind, n, prow, qrow, fallback, pos;
     float Tp, mp, Tq, mq, u, pad;
-    double sp, sq, qs;
+    double isp, isq, qs;  // 1 / (sum of exp) of the p and q rows
 };
 __host__ __device__ constexpr int draw_slots(int mode) { return mode == 1 ? 2 : 1; }
 
@@ -345,8 +357,8 @@ __device__ void decide_block(const float *__restrict__ tgt, const float *__restr
                     D.kind = mode == 0 ? 1 : 2;
                     D.prow = first;
                     D.qrow = first;
-                    D.Tp = Tr; D.mp = pt.m; D.sp = pt.s;
-                    D.Tq = Tr; D.mq = pd.m; D.sq = pd.s;
+                    D.Tp = Tr; D.mp = pt.m; D.isp = 1.0 / pt.s;
+                    D.Tq = Tr; D.mq = pd.m; D.isq = 1.0 / pd.s;
                     D.qs = f_q;
                     D.u = u_res[step];
                     D.fallback = mode == 0 ? 1 : 2;
@@ -356,8 +368,8 @@ __device__ void decide_block(const float *__restrict__ tgt, const float *__restr
                         D2.n = first;
                         D2.pos = first + 1;
                         D2.prow = k;
-                        D2.Tp = T; D2.mp = pk.m; D2.sp = pk.s;
-                        D2.Tq = T; D2.mq = 0.f; D2.sq = 1.0;
+                        D2.Tp = T; D2.mp = pk.m; D2.isp = 1.0 / pk.s;
+                        D2.Tq = T; D2.mq = 0.f; D2.isq = 1.0;
                         D2.u = u_bonus[step];
                         D2.fallback = 2;
                     }
@@ -366,8 +378,8 @@ __device__ void decide_block(const float *__restrict__ tgt, const float *__restr
                     D.kind = bonus_pre ? 3 : 0;
                     D.prow = k;
                     D.qrow = 0;
-                    D.Tp = T; D.mp = pt.m; D.sp = pt.s;
-                    D.Tq = T; D.mq = 0.f; D.sq = 1.0; D.qs = 0.0;
+                    D.Tp = T; D.mp = pt.m; D.isp = 1.0 / pt.s;
+                    D.Tq = T; D.mq = 0.f; D.isq = 1.0; D.qs = 0.0;
                     D.u = u_bonus[step];
                     D.fallback = 2;
                 }
@@ -410,9 +422,9 @@ __device__ void chunk_scan(const Decision &D, const float *lt, const float *ld, 
         const int j = c * CHUNK + r * NT + t;
         double w = 0.0;
         if (j < V) {
-            const double p = dexp(lv[r] / D.Tp, D.mp) / D.sp;
+            const double p = dexp(lv[r] / D.Tp, D.mp) * D.isp;
             if (use_p || D.kind == 0) w = p;
-            else w = fmax(p - (D.kind == 1 ? dexp(dv[r] / D.Tq, D.mq) / D.sq : D.qs), 0.0);
+            else w = fmax(p - (D.kind == 1 ? dexp(dv[r] / D.Tq, D.mq) * D.isq : D.qs), 0.0);
         }
         cs.cw[r] = wave_scan(w);
         if (lane == 63) sh[r * 4 + wave] = cs.cw[r];
