@@ -635,3 +635,90 @@ void orc_rmsnorm(const float *x, const float *w, int n, float eps, float *out) {
     const float scale = 1.0f / sqrtf((float)(ss / n) + eps);
     for (int i = 0; i < n; i++) out[i] = x[i] * scale * (w ? w[i] : 1.0f);
 }
+
+/* ---- CPU baseline: one verify step through the reference's kernels ---- */
+
+#include <time.h>
+
+static double now_s(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+/* y = gemv(w, x) with the time spent inside added to *t */
+static void timed_gemv(orc_gemv_fn f, const uint8_t *w, const float *x, float *y, void *q8, int K, int N,
+                       double *t) {
+    const double t0 = now_s();
+    f(w, x, y, q8, K, N);
+    *t += now_s() - t0;
+}
+
+int orc_cpu_verify_step(orc_gemv_fn q4k, orc_gemv_fn q6k, const struct orc_step_layer *layers, int n_layers,
+                        const uint8_t *lm, const float *out_norm, int M, int H, int NQ, int NKV, int FF, int V,
+                        const float *x0, const float *Ld, const int32_t *draft, float T, const float *u_acc,
+                        float u_res, float u_bonus, float *logits, int32_t *out_tok, int32_t *out_n,
+                        double *sec_layers, double *sec_head, double *sec_gemv) {
+    if (!q4k || !q6k || !layers || n_layers < 0 || M < 1 || H % 256 || NQ % 256 || FF % 256) return -22;
+    const int KMAX = FF > H ? (FF > NQ ? FF : NQ) : (H > NQ ? H : NQ);
+    float *x = (float *)malloc(sizeof(float) * (size_t)M * H);
+    float *h = (float *)malloc(sizeof(float) * (size_t)KMAX);
+    float *q = (float *)malloc(sizeof(float) * (size_t)NQ);
+    float *kv = (float *)malloc(sizeof(float) * (size_t)2 * NKV);
+    float *t = (float *)malloc(sizeof(float) * (size_t)(H > FF ? H : FF));
+    float *g = (float *)malloc(sizeof(float) * (size_t)FF);
+    float *u = (float *)malloc(sizeof(float) * (size_t)FF);
+    void *q8 = malloc((size_t)(KMAX / 256) * 292);
+    int rc = 0;
+    if (!x || !h || !q || !kv || !t || !g || !u || !q8) {
+        rc = -12;
+        goto done;
+    }
+    memcpy(x, x0, sizeof(float) * (size_t)M * H);
+    double tg = 0.0;
+    const double t0 = now_s();
+    for (int m = 0; m < M; m++) {  /* token-major, as forward_cpu! */
+        float *xm = x + (size_t)m * H;
+        for (int l = 0; l < n_layers; l++) {
+            const struct orc_step_layer *L = layers + l;
+            orc_rmsnorm(xm, L->attn_norm, H, 1e-6f, h);
+            timed_gemv(q4k, L->q, h, q, q8, H, NQ, &tg);
+            timed_gemv(q4k, L->k, h, kv, q8, H, NKV, &tg);
+            timed_gemv(q4k, L->v, h, kv + NKV, q8, H, NKV, &tg);
+            timed_gemv(q4k, L->o, q, t, q8, NQ, H, &tg);
+            for (int i = 0; i < H; i++) xm[i] += t[i];
+            orc_rmsnorm(xm, L->ffn_norm, H, 1e-6f, h);
+            timed_gemv(q4k, L->gate, h, g, q8, H, FF, &tg);
+            timed_gemv(q4k, L->up, h, u, q8, H, FF, &tg);
+            for (int i = 0; i < FF; i++) g[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+            timed_gemv(q6k, L->down, g, t, q8, FF, H, &tg);
+            for (int i = 0; i < H; i++) xm[i] += t[i];
+        }
+    }
+    const double t1 = now_s();
+    const double tg_layers = tg;
+    for (int m = 0; m < M; m++) {
+        orc_rmsnorm(x + (size_t)m * H, out_norm, H, 1e-6f, h);
+        timed_gemv(q6k, lm, h, logits + (size_t)m * V, q8, H, V, &tg);
+    }
+    if (Ld && draft && u_acc) rc = orc_spec_accept(logits, Ld, draft, M - 1, V, T, u_acc, u_res, u_bonus, 0, out_tok,
+                                                    out_n);
+    const double t2 = now_s();
+    *sec_layers = t1 - t0;
+    *sec_head = t2 - t1;
+    sec_gemv[0] = tg_layers;
+    sec_gemv[1] = tg - tg_layers;
+done:
+    free(x); free(h); free(q); free(kv); free(t); free(g); free(u); free(q8);
+    return rc;
+}
+
+/* The port's q4_k_gemv / q6_k_gemv with the reference's signature (the
+ * CPU baseline when the reference build is absent): OpenMP's current
+ * thread count. */
+void orc_q4_k_gemv(const uint8_t *w, const float *x, float *out, void *q8, int K, int N) {
+    orc_gemv_q8k(ORC_Q4_K, w, x, out, q8, K, N, omp_get_max_threads());
+}
+void orc_q6_k_gemv(const uint8_t *w, const float *x, float *out, void *q8, int K, int N) {
+    orc_gemv_q8k(ORC_Q6_K, w, x, out, q8, K, N, omp_get_max_threads());
+}

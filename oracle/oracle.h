@@ -27,6 +27,11 @@
  *                        unpinned by construction (no counterpart).
  *   orc_rmsnorm          pinned: closed forms (constant vectors, [3, 4], one
  *                        nonzero element, zeros): tests/test_host_logic.py.
+ *   orc_cpu_verify_step  the CPU baseline's step driver (no result of its own
+ *                        to pin: it calls the reference's gemv kernels and the
+ *                        functions above in forward_cpu!'s order); its
+ *                        logits are checked against the same step composed
+ *                        from the pinned pieces in tests/test_oracle_quant.py.
  */
 #ifndef INFERNO_ORACLE_H
 #define INFERNO_ORACLE_H
@@ -111,6 +116,43 @@ int orc_tree_accept(const float *Lt, const float *Ld, const int32_t *tok,
 
 /* RMSNorm (src/ModelCPU.jl:110-122); w may be NULL (all ones). */
 void orc_rmsnorm(const float *x, const float *w, int n, float eps, float *out);
+
+/* CPU baseline of one verify step, timed: the reference C path as the
+ * Julia host drives it, with its glue in C. forward_cpu! streams the M
+ * tokens one at a time through every layer (src/ModelCPU.jl:970-980); per
+ * token and layer: RMSNorm, q / k / v projections, o projection added to the
+ * residual (attention itself is outside the path), RMSNorm, gate and up,
+ * silu(gate) * up, down added to the residual (src/ModelCPU.jl:447-473,
+ * 755-760, 870-891); then per token the final RMSNorm and the LM head
+ * (full logits, :948-966), then the accept (orc_spec_accept, mode 0, on
+ * the computed logits as target rows). gemv(w, x, out, q8, K, N) are the
+ * reference's exported kernels (src/kernels/quant_kernels.c:602-650), the
+ * Q8_K buffer preallocated as QuantizedKernels does
+ * (src/QuantizedKernels.jl:59-70). Buffers are allocated before the clock
+ * starts. Outputs: logits [M x V]; seconds in the layers, in the head and
+ * the accept, and inside the gemv calls alone (sec_gemv[0]: the layers',
+ * [1]: the head's). 0, or -12 / -22. */
+typedef void (*orc_gemv_fn)(const uint8_t *w, const float *x, float *out,
+                            void *q8, int K, int N);
+struct orc_step_layer {
+    const uint8_t *q, *k, *v, *o, *gate, *up, *down;
+    const float *attn_norm, *ffn_norm;
+};
+int orc_cpu_verify_step(orc_gemv_fn q4k, orc_gemv_fn q6k,
+                        const struct orc_step_layer *layers, int n_layers,
+                        const uint8_t *lm, const float *out_norm, int M, int H,
+                        int NQ, int NKV, int FF, int V, const float *x0,
+                        const float *Ld, const int32_t *draft, float T,
+                        const float *u_acc, float u_res, float u_bonus,
+                        float *logits, int32_t *out_tok, int32_t *out_n,
+                        double *sec_layers, double *sec_head,
+                        double *sec_gemv);
+/* The port's gemv with that signature (orc_gemv_q8k at OpenMP's thread
+ * count). */
+void orc_q4_k_gemv(const uint8_t *w, const float *x, float *out, void *q8,
+                   int K, int N);
+void orc_q6_k_gemv(const uint8_t *w, const float *x, float *out, void *q8,
+                   int K, int N);
 
 #ifdef __cplusplus
 }

@@ -58,6 +58,9 @@ def lib():
         L.orc_tree_accept.argtypes = [_f32p, _f32p, _i32p, _i32p, C.c_int, C.c_int, C.c_float,
                                       _f32p, _i32p, C.POINTER(C.c_int32)]
         L.orc_rmsnorm.argtypes = [_f32p, C.c_void_p, C.c_int, C.c_float, _f32p]
+        L.orc_cpu_verify_step.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, _u8p, _f32p] + \
+            [C.c_int] * 6 + [_f32p, C.c_void_p, C.c_void_p, C.c_float, C.c_void_p, C.c_float, C.c_float, _f32p,
+                             _i32p, C.POINTER(C.c_int32)] + [C.POINTER(C.c_double)] * 2 + [_f64p]
         _lib = L
     return _lib
 
@@ -369,3 +372,54 @@ def ref_vec_dot(qtype: int, w: np.ndarray, q8: np.ndarray, nb: int) -> float:
 def vec_dot(qtype: int, w: np.ndarray, q8: np.ndarray, nb: int) -> float:
     """The oracle's restatement of the same lane order (orc_vec_dot_*)."""
     return float(getattr(lib(), "orc_" + _DOT[qtype])(_c(w, np.uint8), _c(q8, np.uint8), nb))
+
+
+# ---- CPU baseline step driver (bench.py's cpu_baseline leg) ----
+
+class StepLayer(C.Structure):
+    """struct orc_step_layer"""
+    _fields_ = [(n, C.c_void_p) for n in ("q", "k", "v", "o", "gate", "up", "down", "attn_norm", "ffn_norm")]
+
+
+def cpu_verify_step(layers, lm, out_norm, x0, H, NQ, NKV, FF, V, Ld=None, draft=None, T=0.8, u_acc=None,
+                    u_res=0.5, u_bonus=0.5, kernels="reference"):
+    """orc_cpu_verify_step: one verify step of M = x0.shape[0] tokens through
+    `layers` (dicts of host GGUF bytes: q [NQ x H], kv [2 NKV x H] (k rows then
+    v rows), o [H x NQ], gu [2 FF x H] (gate rows then up rows), down
+    [H x FF] (Q6_K), attn_norm / ffn_norm [H]), the Q6_K LM head and, with
+    Ld / draft / u_acc, the accept. kernels: "reference" (oracle/_ref, the
+    reference's own C build) or "port" (orc_q*_gemv). Returns (logits
+    [M x V], tokens, n, seconds in the layers, in head + accept, seconds
+    inside the gemv calls [layers, head])."""
+    L = lib()
+    if kernels == "reference":
+        R = ref()
+        f4, f6 = C.cast(R.q4_k_gemv, C.c_void_p), C.cast(R.q6_k_gemv, C.c_void_p)
+    else:
+        f4, f6 = C.cast(L.orc_q4_k_gemv, C.c_void_p), C.cast(L.orc_q6_k_gemv, C.c_void_p)
+    x0 = _c(x0, np.float32)
+    M = x0.shape[0]
+    keep = []
+
+    def ptr(a, off=0):
+        keep.append(a)
+        return a.ctypes.data + off
+
+    arr = (StepLayer * max(1, len(layers)))()
+    kvb, gub = NKV * (H // 256) * 144, FF * (H // 256) * 144
+    for i, lw in enumerate(layers):
+        arr[i] = StepLayer(ptr(lw["q"]), ptr(lw["kv"]), ptr(lw["kv"], kvb), ptr(lw["o"]), ptr(lw["gu"]),
+                           ptr(lw["gu"], gub), ptr(lw["down"]), ptr(_c(lw["attn_norm"], np.float32)),
+                           ptr(_c(lw["ffn_norm"], np.float32)))
+    logits = np.empty((M, V), np.float32)
+    tok = np.full(M, -1, np.int32)
+    n = C.c_int32(-1)
+    sl, sh, sg = C.c_double(), C.c_double(), np.zeros(2, np.float64)
+    acc = Ld is not None
+    rc = L.orc_cpu_verify_step(f4, f6, C.cast(arr, C.c_void_p), len(layers), _c(lm, np.uint8),
+                               _c(out_norm, np.float32), M, H, NQ, NKV, FF, V, x0,
+                               ptr(_c(Ld, np.float32)) if acc else None, ptr(_c(draft, np.int32)) if acc else None,
+                               T, ptr(_c(u_acc, np.float32)) if acc else None, u_res, u_bonus, logits, tok,
+                               C.byref(n), C.byref(sl), C.byref(sh), sg)
+    assert rc == 0, rc
+    return logits, tok, n.value, sl.value, sh.value, sg

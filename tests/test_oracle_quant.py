@@ -202,3 +202,50 @@ def test_gemv_invariants(qt):
     assert rel(O.gemv_f64(qt, w, (x[0] + 2 * x[1]).astype(np.float32), 1, N, K)[0], y[0] + 2 * y[1]) < 1e-6
     assert rel(O.gemv_seq_f32(qt, w, x, 3, N, K), y) < 1e-6
     assert np.allclose(y, x.astype(np.float64) @ full.T.astype(np.float64), rtol=1e-12, atol=1e-9)
+
+
+@pytest.mark.parametrize("kernels", ["port", "reference"])
+def test_cpu_verify_step_driver(kernels):
+    """The CPU baseline's C step driver (orc_cpu_verify_step) computes the
+    step it times: its logits equal the same step composed in numpy from
+    the pinned pieces (orc_gemv_q8k, bit-exact to the reference kernel;
+    orc_rmsnorm; silu; token-major order of forward_cpu!), and its accept
+    equals orc_spec_accept on those logits."""
+    if kernels == "reference" and not O.ref_available():
+        pytest.skip("oracle/_ref not built (no reference tree)")
+    H, NQ, NKV, FF, V, M, nl = 512, 512, 256, 768, 1000, 3, 2
+    st = lambda n: synth.stream_for(0x5EED, n)  # noqa: E731
+    layers = []
+    for i in range(nl):
+        layers.append({"q": synth.matrix(F.Q4_K, NQ, H, st(f"q{i}")), "kv": synth.matrix(F.Q4_K, 2 * NKV, H, st(f"kv{i}")),
+                       "o": synth.matrix(F.Q4_K, H, NQ, st(f"o{i}")), "gu": synth.matrix(F.Q4_K, 2 * FF, H, st(f"gu{i}")),
+                       "down": synth.matrix(F.Q6_K, H, FF, st(f"d{i}")),
+                       "attn_norm": 1 + 0.1 * synth.gaussian(st(f"an{i}"), H),
+                       "ffn_norm": 1 + 0.1 * synth.gaussian(st(f"fn{i}"), H)})
+    lm = synth.matrix(F.Q6_K, V, H, st("lm"))
+    on = 1 + 0.1 * synth.gaussian(st("on"), H)
+    x0 = synth.gaussian(st("x0"), M * H).reshape(M, H)
+    rng = np.random.default_rng(3)
+    Ld = rng.standard_normal((M - 1, V)).astype(np.float32)
+    draft = np.array([5, 17], np.int32)
+    ua = np.zeros(M - 1, np.float32)
+    logits, tok, n, sl, sh, sg = O.cpu_verify_step(layers, lm, on, x0, H, NQ, NKV, FF, V, Ld, draft, 0.8, ua, 0.5,
+                                                   0.25, kernels=kernels)
+    assert sl > 0 and sh > 0 and 0 < sg[0] <= sl and 0 < sg[1] <= sh
+    g = lambda qt, w, v, K, N: O.gemv_q8k(qt, w, v, K, N, 1)  # noqa: E731
+    want = np.empty((M, V), np.float32)
+    with np.errstate(over="ignore"):  # exp(-g) of very negative gates: silu -> -0, as in fp32 C
+        for m in range(M):
+            x = x0[m].copy()
+            for lw in layers:
+                h = O.rmsnorm(x, w=lw["attn_norm"])
+                q = g(F.Q4_K, lw["q"], h, H, NQ)
+                x = x + g(F.Q4_K, lw["o"], q, NQ, H)
+                h = O.rmsnorm(x, w=lw["ffn_norm"])
+                gu = g(F.Q4_K, lw["gu"], h, H, 2 * FF)
+                a = (gu[:FF] / (np.float32(1) + np.exp(-gu[:FF])) * gu[FF:]).astype(np.float32)
+                x = x + g(F.Q6_K, lw["down"], a, FF, H)
+            want[m] = g(F.Q6_K, lm, O.rmsnorm(x, w=on), H, V)
+    assert rel(logits, want) < 1e-5
+    rt, rn = O.spec_accept(logits, Ld, draft, 0.8, ua, 0.5, 0.25, 0)
+    assert n == rn and tok[: len(rt)].tolist() == rt.tolist()
