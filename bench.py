@@ -874,7 +874,7 @@ def cpu_baseline(ih, model: Model, n_layers: int, M: int, k: int, budget_s: floa
     def run_c():
         _, _, n, sl, sh, sg = O.cpu_verify_step(hostw, lm, model.host_out_norm, x0, H, NQ, NKV, FF, VOCAB, Ld,
                                                 draft, 0.8, u_acc, 0.5, 0.5, kernels=kind)
-        return sl * scale + sh, sg[0] * scale + sg[1]
+        return sl * scale + sh, sg[0] * scale + sg[1], sg[2]
 
     counts = sorted({ref_default, phys})
     per = budget_s * 0.8 / len(counts)
@@ -883,16 +883,17 @@ def cpu_baseline(ih, model: Model, n_layers: int, M: int, k: int, budget_s: floa
         if gomp is not None:
             gomp.omp_set_num_threads(threads)
         run_c()  # warm-up
-        tot, ker, reps = 0.0, 0.0, 0
+        tot, ker, acc, reps = 0.0, 0.0, 0.0, 0
         t_end = time.perf_counter() + per
         while time.perf_counter() < t_end or reps == 0:
-            a, b = run_c()
+            a, b, c = run_c()
             tot += a
             ker += b
+            acc += c
             reps += 1
-        results[threads] = (tot / reps, ker / reps, reps)
+        results[threads] = (tot / reps, ker / reps, acc / reps, reps)
         log(f"cpu baseline (C driver) threads={threads}: {tot / reps * 1e3:.1f} ms/step, "
-            f"{ker / reps * 1e3:.1f} ms inside the gemv calls ({reps} samples)")
+            f"{ker / reps * 1e3:.1f} ms inside the gemv calls, {acc / reps * 1e3:.1f} ms accept ({reps} samples)")
 
     # the previous driver: the same kernels called from Python with numpy glue
     gemv = (lambda qt, w, v, K, N: O.ref_gemv(qt, w, v, K, N)) if kind == "reference" else \
@@ -905,8 +906,8 @@ def cpu_baseline(ih, model: Model, n_layers: int, M: int, k: int, budget_s: floa
         with np.errstate(over="ignore"):
             x = x0.copy()
             t0 = time.perf_counter()
-            for lw in hostw:
-                for m in range(M):
+            for m in range(M):  # token-major, as forward_cpu! and the C driver
+                for lw in hostw:
                     h = rms(x[m], lw["attn_norm"])
                     q = gemv(F.Q4_K, lw["q"], h, H, NQ)
                     gemv(F.Q4_K, lw["kv"], h, H, 2 * NKV)
@@ -941,7 +942,8 @@ def cpu_baseline(ih, model: Model, n_layers: int, M: int, k: int, budget_s: floa
                    f"layers, + final RMSNorm and lm_head x{M} + accept (mode 0, all {k} drafts accepted, bonus draw); "
                    f"one thread count per figure, OpenMP inside the kernels"),
         "threads": {str(t): {"steps_per_s": round(1.0 / r[0], 4), "ms_per_step": round(r[0] * 1e3, 2),
-                             "ms_in_gemv": round(r[1] * 1e3, 2), "samples": r[2]} for t, r in results.items()},
+                             "ms_in_gemv": round(r[1] * 1e3, 2), "ms_accept": round(r[2] * 1e3, 2),
+                             "samples": r[3]} for t, r in results.items()},
         "reference_default_threads": ref_default,
         "python_glue_ms_per_step_no_accept": round(py * 1e3, 2),
         "host": topo,

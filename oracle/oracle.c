@@ -701,9 +701,11 @@ int orc_cpu_verify_step(orc_gemv_fn q4k, orc_gemv_fn q6k, const struct orc_step_
         orc_rmsnorm(x + (size_t)m * H, out_norm, H, 1e-6f, h);
         timed_gemv(q6k, lm, h, logits + (size_t)m * V, q8, H, V, &tg);
     }
+    const double ta = now_s();
     if (Ld && draft && u_acc) rc = orc_spec_accept(logits, Ld, draft, M - 1, V, T, u_acc, u_res, u_bonus, 0, out_tok,
                                                     out_n);
     const double t2 = now_s();
+    sec_gemv[2] = t2 - ta;
     *sec_layers = t1 - t0;
     *sec_head = t2 - t1;
     sec_gemv[0] = tg_layers;

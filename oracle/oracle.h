@@ -131,7 +131,7 @@ void orc_rmsnorm(const float *x, const float *w, int n, float eps, float *out);
  * (src/QuantizedKernels.jl:59-70). Buffers are allocated before the clock
  * starts. Outputs: logits [M x V]; seconds in the layers, in the head and
  * the accept, and inside the gemv calls alone (sec_gemv[0]: the layers',
- * [1]: the head's). 0, or -12 / -22. */
+ * [1]: the head's; sec_gemv[2]: the accept's seconds). 0, or -12 / -22. */
 typedef void (*orc_gemv_fn)(const uint8_t *w, const float *x, float *out,
                             void *q8, int K, int N);
 struct orc_step_layer {

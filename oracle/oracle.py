@@ -390,7 +390,7 @@ def cpu_verify_step(layers, lm, out_norm, x0, H, NQ, NKV, FF, V, Ld=None, draft=
     Ld / draft / u_acc, the accept. kernels: "reference" (oracle/_ref, the
     reference's own C build) or "port" (orc_q*_gemv). Returns (logits
     [M x V], tokens, n, seconds in the layers, in head + accept, seconds
-    inside the gemv calls [layers, head])."""
+    [inside the layers' gemv calls, inside the head's, in the accept])."""
     L = lib()
     if kernels == "reference":
         R = ref()
@@ -414,7 +414,7 @@ def cpu_verify_step(layers, lm, out_norm, x0, H, NQ, NKV, FF, V, Ld=None, draft=
     logits = np.empty((M, V), np.float32)
     tok = np.full(M, -1, np.int32)
     n = C.c_int32(-1)
-    sl, sh, sg = C.c_double(), C.c_double(), np.zeros(2, np.float64)
+    sl, sh, sg = C.c_double(), C.c_double(), np.zeros(3, np.float64)
     acc = Ld is not None
     rc = L.orc_cpu_verify_step(f4, f6, C.cast(arr, C.c_void_p), len(layers), _c(lm, np.uint8),
                                _c(out_norm, np.float32), M, H, NQ, NKV, FF, V, x0,

@@ -231,7 +231,7 @@ def test_cpu_verify_step_driver(kernels):
     ua = np.zeros(M - 1, np.float32)
     logits, tok, n, sl, sh, sg = O.cpu_verify_step(layers, lm, on, x0, H, NQ, NKV, FF, V, Ld, draft, 0.8, ua, 0.5,
                                                    0.25, kernels=kernels)
-    assert sl > 0 and sh > 0 and 0 < sg[0] <= sl and 0 < sg[1] <= sh
+    assert sl > 0 and sh > 0 and 0 < sg[0] <= sl and 0 < sg[1] and sg[1] + sg[2] <= sh
     g = lambda qt, w, v, K, N: O.gemv_q8k(qt, w, v, K, N, 1)  # noqa: E731
     want = np.empty((M, V), np.float32)
     with np.errstate(over="ignore"):  # exp(-g) of very negative gates: silu -> -0, as in fp32 C
