@@ -373,8 +373,8 @@ int ihip_spec_accept(const float *tgt_dev, const float *drf_dev,
  * T = 1 (mode 1); mode 0 uses the unfiltered softmaxes at T, so with
  * filtered drafting its q is not the distribution the drafts came from.
  * Filters that keep the whole vocabulary (top_k = 0 or >= V, top_p >= 1,
- * min_p <= 0) give ihip_spec_accept exactly. With a filter, V follows
- * ihip_sample_ex's limits. ws: ihip_spec_accept_ex_ws_bytes() bytes (the
+ * min_p <= 0) give ihip_spec_accept exactly. ws:
+ * ihip_spec_accept_ex_ws_bytes() bytes (the
  * steps' bonus rows and the sampler's workspace on top of the accept's). */
 int ihip_spec_accept_ex_ws_bytes(int steps, int k, int V, int top_k,
                                  float top_p, float min_p, size_t *bytes);
@@ -440,12 +440,16 @@ int ihip_spec_advance_len(int32_t *len_dev, const int32_t *n_accepted_dev,
  *   softmax; top_p < 1 keeps the shortest prefix of the probabilities in
  *   descending order (ties by index) whose sum reaches top_p, renormalized;
  *   min_p > 0 drops probabilities below max * min_p, renormalized; the token
- *   is the first j with u[r] <= cumsum_j (V - 1 if none; 0 when u[r] <= 0,
- *   as the reference's loop returns its first index then).
- * Limits: top_k <= 4096 unless >= V; V a multiple of 4 and <= 4194304;
- * logits 16-byte aligned. No workspace. Sums are trees where the reference
- * adds sequentially, so a draw can differ only where u lies within rounding
- * of a step of the cumulative distribution. */
+ *   is the first j with u[r] <= cumsum_j (V - 1 if none). A row whose
+ *   reference probabilities are all NaN (all -Inf, a +Inf, or a NaN
+ *   anywhere: the reference's top-k keeps a NaN first) draws V - 1 for any
+ *   u; any other row draws 0 when u[r] <= 0, as the reference's loop
+ *   returns its first index then.
+ * Any V in [1, 4194304], any top_k, logits at any 4-byte alignment (a
+ * top_k above 4096 takes a threshold path: the k-th element by count, the
+ * softmax over the kept entries). No workspace. Sums are trees where the
+ * reference adds sequentially, so a draw can differ only where u lies
+ * within rounding of a step of the cumulative distribution. */
 int ihip_sample(const float *logits_dev, int rows, int V, float T, int top_k,
                 float top_p, float min_p, const float *u_dev,
                 int32_t *out_tok_dev, void *stream);
@@ -458,8 +462,9 @@ int ihip_sample(const float *logits_dev, int rows, int V, float T, int top_k,
  * them: the tokens of ihip_sample), top-p and / or min-p without top-k
  * (the threshold's histograms merged per row), a larger top-k (its
  * threshold by count, the kept entries compacted, then ihip_sample's
- * candidate draw: its tokens), and T = 0 (each chunk's first argmax: the
- * tokens of ihip_sample). The same softmax_sample
+ * candidate draw: its tokens; above 4096, ihip_sample's threshold path),
+ * and T = 0 (each chunk's first argmax: the tokens of ihip_sample). The
+ * same limits and the same softmax_sample
  * (src/ModelCPU.jl:1123-1200) and the same contract: draws match the exact
  * cumulative distribution except within rounding of a step. */
 int ihip_sample_ws_bytes(int rows, int V, size_t *bytes);
@@ -474,7 +479,7 @@ int ihip_sample_ex(const float *logits_dev, int rows, int V, float T, int top_k,
  * ids are tok_dev[r * tok_stride + i], i < n_tok (tok_stride 0: one list for
  * every row); for each distinct id in [0, V): x -= presence (presence != 0),
  * then x = x > 0 ? x / repetition : x * repetition (repetition != 1).
- * V <= 262144. */
+ * Any V >= 1. */
 int ihip_apply_penalties(float *logits_dev, int rows, int V,
                          const int32_t *tok_dev, int n_tok, int64_t tok_stride,
                          float presence, float repetition, void *stream);

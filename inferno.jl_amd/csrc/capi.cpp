@@ -49,9 +49,7 @@ hipError_t launch_commit_state(void *state, const void *snap, int64_t words, int
                                const int32_t *n_acc, int steps, int64_t state_step, int64_t snap_step,
                                hipStream_t st);
 hipError_t launch_advance_len(int32_t *len, const int32_t *n_acc, int steps, hipStream_t st);
-int sample_max_top_k();
 int sample_max_v();
-int penalty_max_v();
 hipError_t launch_sample(const float *L, int rows, int V, float T, int top_k, float top_p, float min_p, const float *u,
                          int32_t *out, hipStream_t st);
 size_t sample_spread_ws(int rows, int V);
@@ -826,12 +824,7 @@ static int spec_accept_impl(const char *name, const float *tgt_dev, const float 
     const int32_t *bonus = nullptr;
     hipError_t e = hipSuccess;
     if (filtered) {
-        if (V < 4 || (V & 3) || V > sample_max_v() || !aligned16(tgt_dev))
-            return fail(IHIP_EINVAL, "%s: filtered bonus draw needs V a multiple of 4 (V=%d) and 16-byte aligned "
-                                     "logits", name, V);
         const int kk = top_k >= V ? 0 : top_k;
-        if (kk > sample_max_top_k())
-            return fail(IHIP_EINVAL, "%s: top_k=%d above %d (and below V)", name, top_k, sample_max_top_k());
         uint8_t *w = (uint8_t *)ws + round256(spec_accept_ws(steps, k, V));
         const float *rows = tgt_dev + (size_t)k * V;  // step 0's bonus row; steps apart by (k + 1) V
         if (steps > 1) {
@@ -926,14 +919,11 @@ int ihip_spec_advance_len(int32_t *len_dev, const int32_t *n_accepted_dev, int s
 int ihip_sample(const float *logits_dev, int rows, int V, float T, int top_k, float top_p, float min_p,
                 const float *u_dev, int32_t *out_tok_dev, void *stream) {
     if (!logits_dev || !u_dev || !out_tok_dev) return fail(IHIP_EFAULT, "ihip_sample: NULL pointer");
-    if (rows < 1 || V < 4 || (V & 3) || V > sample_max_v())
-        return fail(IHIP_EINVAL, "ihip_sample: rows=%d V=%d (V a multiple of 4 in [4, %d])", rows, V, sample_max_v());
-    if (!aligned16(logits_dev)) return fail(IHIP_EINVAL, "ihip_sample: logits must be 16-byte aligned");
+    if (rows < 1 || V < 1 || V > sample_max_v())
+        return fail(IHIP_EINVAL, "ihip_sample: rows=%d V=%d (V in [1, %d])", rows, V, sample_max_v());
     if (!(T >= 0.f) || T > 3.0e38f) return fail(IHIP_EINVAL, "ihip_sample: temperature %g", T);
     if (top_k < 0) return fail(IHIP_EINVAL, "ihip_sample: top_k=%d", top_k);
     if (top_k >= V) top_k = 0;  // keeps every token (sorted_indices[1:min(top_k, V)])
-    if (top_k > sample_max_top_k())
-        return fail(IHIP_EINVAL, "ihip_sample: top_k=%d above %d (and below V)", top_k, sample_max_top_k());
     if (top_p != top_p || min_p != min_p) return fail(IHIP_EINVAL, "ihip_sample: NaN top_p/min_p");
     hipError_t e = launch_sample(logits_dev, rows, V, T, top_k, top_p, min_p, u_dev, out_tok_dev, S(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "ihip_sample");
@@ -941,7 +931,7 @@ int ihip_sample(const float *logits_dev, int rows, int V, float T, int top_k, fl
 
 int ihip_sample_ws_bytes(int rows, int V, size_t *bytes) {
     if (!bytes) return fail(IHIP_EFAULT, "ihip_sample_ws_bytes: NULL pointer");
-    if (rows < 1 || V < 4 || (V & 3) || V > sample_max_v())
+    if (rows < 1 || V < 1 || V > sample_max_v())
         return fail(IHIP_EINVAL, "ihip_sample_ws_bytes: rows=%d V=%d", rows, V);
     *bytes = sample_spread_ws(rows, V);
     return ok();
@@ -950,18 +940,14 @@ int ihip_sample_ws_bytes(int rows, int V, size_t *bytes) {
 int ihip_sample_ex(const float *logits_dev, int rows, int V, float T, int top_k, float top_p, float min_p,
                    const float *u_dev, int32_t *out_tok_dev, void *ws, size_t ws_bytes, void *stream) {
     if (!logits_dev || !u_dev || !out_tok_dev || !ws) return fail(IHIP_EFAULT, "ihip_sample_ex: NULL pointer");
-    if (rows < 1 || V < 4 || (V & 3) || V > sample_max_v())
-        return fail(IHIP_EINVAL, "ihip_sample_ex: rows=%d V=%d (V a multiple of 4 in [4, %d])", rows, V,
-                    sample_max_v());
-    if (!aligned16(logits_dev) || !aligned16(ws))
-        return fail(IHIP_EINVAL, "ihip_sample_ex: logits and workspace must be 16-byte aligned");
+    if (rows < 1 || V < 1 || V > sample_max_v())
+        return fail(IHIP_EINVAL, "ihip_sample_ex: rows=%d V=%d (V in [1, %d])", rows, V, sample_max_v());
+    if (!aligned16(ws)) return fail(IHIP_EINVAL, "ihip_sample_ex: workspace must be 16-byte aligned");
     if (ws_bytes < sample_spread_ws(rows, V))
         return fail(IHIP_ENOMEM, "ihip_sample_ex: workspace %zu < %zu bytes", ws_bytes, sample_spread_ws(rows, V));
     if (!(T >= 0.f) || T > 3.0e38f) return fail(IHIP_EINVAL, "ihip_sample_ex: temperature %g", T);
     if (top_k < 0) return fail(IHIP_EINVAL, "ihip_sample_ex: top_k=%d", top_k);
     if (top_k >= V) top_k = 0;
-    if (top_k > sample_max_top_k())
-        return fail(IHIP_EINVAL, "ihip_sample_ex: top_k=%d above %d (and below V)", top_k, sample_max_top_k());
     if (top_p != top_p || min_p != min_p) return fail(IHIP_EINVAL, "ihip_sample_ex: NaN top_p/min_p");
     hipError_t e = launch_sample_spread(logits_dev, rows, V, T, top_k, top_p, min_p, u_dev, out_tok_dev, ws,
                                         S(stream));
@@ -971,9 +957,9 @@ int ihip_sample_ex(const float *logits_dev, int rows, int V, float T, int top_k,
 int ihip_apply_penalties(float *logits_dev, int rows, int V, const int32_t *tok_dev, int n_tok, int64_t tok_stride,
                          float presence, float repetition, void *stream) {
     if (!logits_dev || (n_tok > 0 && !tok_dev)) return fail(IHIP_EFAULT, "ihip_apply_penalties: NULL pointer");
-    if (rows < 1 || V < 1 || V > penalty_max_v() || n_tok < 0 || (tok_stride != 0 && tok_stride < n_tok))
-        return fail(IHIP_EINVAL, "ihip_apply_penalties: rows=%d V=%d (<= %d) n_tok=%d stride=%lld", rows, V,
-                    penalty_max_v(), n_tok, (long long)tok_stride);
+    if (rows < 1 || V < 1 || n_tok < 0 || (tok_stride != 0 && tok_stride < n_tok))
+        return fail(IHIP_EINVAL, "ihip_apply_penalties: rows=%d V=%d n_tok=%d stride=%lld", rows, V, n_tok,
+                    (long long)tok_stride);
     if (presence != presence || repetition != repetition)
         return fail(IHIP_EINVAL, "ihip_apply_penalties: NaN penalty");
     hipError_t e = launch_penalties(logits_dev, rows, V, tok_dev, n_tok, tok_stride, presence, repetition, S(stream));

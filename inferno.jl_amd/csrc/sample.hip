@@ -139,13 +139,27 @@ __device__ float block_excl_scan_f(float v, float *red, float &total) {
 
 // Round r of a row: this thread's 4 logits z = L * (1 / T) (within an ulp
 // of the reference's L / T, the same order and the same ties), in false past
-// V (the host keeps V a multiple of 4 and rows 16-byte aligned).
+// V. One 16-byte load where the 4 lie inside the row at an aligned address,
+// else 4-byte loads; an entry past V reads -Inf, which no draw can select
+// (probability 0, below every kept entry, the last in index order among
+// ties), so a row of any length or alignment is drawn as the reference
+// draws it (the tokens are clamped to V - 1).
 __device__ __forceinline__ void load_round(const float *__restrict__ row, int V, int r, float invT, float (&z)[4],
                                            bool &in) {
     const int base = r * SROUND + 4 * (int)threadIdx.x;
     in = base < V;
     float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (in) x = *(const float4 *)(row + base);
+    if (in) {
+        if (base + 4 <= V && ((uintptr_t)(row + base) & 15) == 0) {
+            x = *(const float4 *)(row + base);
+        } else {
+            const float ninf = -__builtin_huge_valf();
+            x.x = row[base];
+            x.y = base + 1 < V ? row[base + 1] : ninf;
+            x.z = base + 2 < V ? row[base + 2] : ninf;
+            x.w = base + 3 < V ? row[base + 3] : ninf;
+        }
+    }
     z[0] = x.x; z[1] = x.y; z[2] = x.z; z[3] = x.w;
     if (invT != 1.0f) {
 #pragma unroll
@@ -178,7 +192,10 @@ __device__ __forceinline__ float pexp(float x) { return __expf(x); }
 // butterfly get the same bits
 __device__ __forceinline__ void merge_ms2(float &m, float &s, float m2, float s2) {
     const float mm = fmaxf(m, m2);
-    if (mm == -__builtin_huge_valf()) return;
+    if (mm == -__builtin_huge_valf()) {  // (both sums 0, or NaN from a NaN entry: kept)
+        s = s + s2;
+        return;
+    }
     s = s * pexp(m - mm) + s2 * pexp(m2 - mm);
     m = mm;
 }
@@ -634,22 +651,31 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
         if (t == 0) out[row] = first == INT_MAX ? 0 : first;
         return;
     }
-    // the reference's draw returns index 1 (here 0) when r <= 0: cumsum >= 0
-    if (!(ur > 0.f)) {
-        if (t == 0) out[row] = 0;
-        return;
-    }
-
     const int K = a.top_k;
-    if (K > 0) {
+    if (K > 0 && K <= SK_MAX) {
         // ---- top-k: the k-th largest z, then the k candidates in index order
-        float lmax = -__builtin_huge_valf();
+        float lmax = -__builtin_huge_valf(), nan = 0.f;
         for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int) {
             if (in)
 #pragma unroll
-                for (int e = 0; e < 4; e++) lmax = fmaxf(lmax, z[e]);
+                for (int e = 0; e < 4; e++) {
+                    lmax = fmaxf(lmax, z[e]);
+                    if (z[e] != z[e]) nan = 1.f;
+                }
         });
         const float zm = block_max(lmax, s_redf);
+        // a degenerate row (the reference's top-k keeps a NaN, its maximum is
+        // then NaN; or no finite maximum) has NaN probabilities: last index
+        if (block_max(nan, s_redf) > 0.f || !(zm > -__builtin_huge_valf() && zm < __builtin_huge_valf()) ||
+            ur != ur) {
+            if (t == 0) out[row] = V - 1;
+            return;
+        }
+        // the reference's draw returns index 1 (here 0) when r <= 0: cumsum >= 0
+        if (!(ur > 0.f)) {
+            if (t == 0) out[row] = 0;
+            return;
+        }
         Select R;
         select_threshold<false>(Lr, V, nround, invT, zm, 1.f, (unsigned long long)K, s_hist, s_mass, s_sel, s_selm,
                                 (uint32_t *)s_cidx, s_cp, &s_ncnt, R);
@@ -698,7 +724,7 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
     // plain draws (no top-p, no min-p) over at most SPART_ROUNDS rounds:
     // every wave keeps the (max, sum exp(z - max)) of its part of each round,
     // so the rounds' sums for the draw need no second pass over the row
-    bool by_parts = a.top_p >= 1.0f && a.min_p <= 0.f && nround <= SPART_ROUNDS;
+    bool by_parts = K == 0 && a.top_p >= 1.0f && a.min_p <= 0.f && nround <= SPART_ROUNDS;
     if (by_parts) {
         const int w = t >> 6;
         for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int r) {
@@ -708,9 +734,12 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
                 for (int e = 0; e < 4; e++) m = fmaxf(m, z[e]);
             m = wave_max(m);
             float sw = 0.f;
-            if (in && m > -__builtin_huge_valf())
+            if (in)
 #pragma unroll
-                for (int e = 0; e < 4; e++) sw += pexp(z[e] - m);
+                for (int e = 0; e < 4; e++) {
+                    if (z[e] != z[e]) sw = __builtin_nanf("");  // (a NaN entry flags the row)
+                    else if (m > -__builtin_huge_valf()) sw += pexp(z[e] - m);
+                }
             sw = wave_sum(sw);
             if ((t & 63) == 0) {
                 s_pm[r][w] = m;
@@ -719,9 +748,13 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
         });
         __syncthreads();
         const int np = nround * SNW;
-        float lm = -__builtin_huge_valf();
-        for (int i = t; i < np; i += SNT) lm = fmaxf(lm, s_pm[i / SNW][i % SNW]);
+        float lm = -__builtin_huge_valf(), nan = 0.f;
+        for (int i = t; i < np; i += SNT) {
+            lm = fmaxf(lm, s_pm[i / SNW][i % SNW]);
+            if (s_ps[i / SNW][i % SNW] != s_ps[i / SNW][i % SNW]) nan = 1.f;
+        }
         zmax = block_max(lm, s_redf);
+        const bool has_nan = block_max(nan, s_redf) > 0.f;
         float ls = 0.f;
         if (zmax > -__builtin_huge_valf())
             for (int i = t; i < np; i += SNT) {
@@ -729,6 +762,7 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
                 if (m > -__builtin_huge_valf()) ls += s_ps[i / SNW][i % SNW] * pexp(m - zmax);
             }
         S = block_sum(ls, s_redf);
+        if (has_nan) S = __builtin_nanf("");
         // rows without a finite maximum or sum (all -Inf, NaN) take the
         // online pass below, as every other draw does
         by_parts = zmax > -__builtin_huge_valf() && S > 0.f && S < __builtin_huge_valf();
@@ -740,7 +774,9 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
             if (!in) return;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                if (z[e] > zmax) {
+                if (z[e] != z[e]) {
+                    S = __builtin_nanf("");  // (a NaN entry: the row is degenerate)
+                } else if (z[e] > zmax) {
                     S = S * pexp(zmax - z[e]) + 1.0f;
                     zmax = z[e];
                 } else if (zmax > -__builtin_huge_valf()) {
@@ -750,6 +786,71 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
         });
         block_ms(zmax, S, s_redf);
     }
+    // a degenerate row (no finite maximum, or a NaN entry: the reference's
+    // maximum is NaN then) has NaN probabilities: the draw returns the last
+    // index; otherwise r <= 0 returns the first (cumsum >= 0)
+    if (!(zmax > -__builtin_huge_valf() && zmax < __builtin_huge_valf()) || !(S > 0.f && S < __builtin_huge_valf()) ||
+        ur != ur) {
+        if (t == 0) out[row] = V - 1;
+        return;
+    }
+    if (!(ur > 0.f)) {
+        if (t == 0) out[row] = 0;
+        return;
+    }
+    // the index limit of the ties at a threshold: the first n_eq of the
+    // elements in bucket zb with key tau are kept (index order)
+    auto tie_limit = [&](uint32_t zb, uint32_t tau, unsigned long long n_eq) {
+        int run = 0, lim = V;
+        for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int r) {
+            bool q[4];
+            uint32_t nq = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                q[e] = in && zbin(z[e], zmax) == zb && okey(z[e]) == tau;
+                nq += q[e];
+            }
+            uint32_t tot;
+            const uint32_t ex = block_excl_scan_u(nq, s_redu, tot);
+            int cand = INT_MAX;
+            int c = run + (int)ex;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (q[e]) {
+                    c++;
+                    if (c == (int)n_eq && cand == INT_MAX) cand = r * SROUND + 4 * t + e + 1;
+                }
+            const int got = block_min_i(cand, s_redi);
+            if (lim == V && got != INT_MAX) lim = got;
+            run += (int)tot;
+        });
+        return lim;
+    };
+    // top-k above the candidate limit: the k-th largest z by count (the
+    // candidate path's threshold), kept by comparison; the softmax is over
+    // the kept entries (S their sum), and top-p / min-p act on it below
+    uint32_t zbK = 256u, tauK = 0u;
+    int tieK = V;
+    if (K > 0) {
+        Select RK;
+        select_threshold<false>(Lr, V, nround, invT, zmax, 1.f, (unsigned long long)K, s_hist, s_mass, s_sel, s_selm,
+                                (uint32_t *)s_cidx, s_cp, &s_ncnt, RK);
+        if (!RK.all) {
+            zbK = RK.zb;
+            tauK = RK.tau;
+            if (RK.rem < RK.cnt) tieK = tie_limit(zbK, tauK, RK.rem);
+        }
+        float ls = 0.f;
+        for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int r) {
+            if (in)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (zbK == 256u || above_threshold(z[e], r * SROUND + 4 * t + e, zmax, zbK, tauK, tieK))
+                        ls += pexp(z[e] - zmax);
+        });
+        S = block_sum(ls, s_redf);
+    }
+    auto keptK = [&](float z, int j) { return zbK == 256u || above_threshold(z, j, zmax, zbK, tauK, tieK); };
     // kept: above_threshold(zb, tau, tie_lim); everything without top-p
     uint32_t zb = 256u, tau = 0u;
     int tie_lim = V;
@@ -774,33 +875,7 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
             const unsigned long long mt = (unsigned long long)(ptau * 1099511627776.0f);
             unsigned long long n_eq = mt ? (R.rem + mt - 1) / mt : (unsigned long long)R.cnt;
             if (n_eq < 1) n_eq = 1;
-            if (n_eq < R.cnt) {
-                // index of the n_eq-th tie in index order
-                int run = 0, lim = V;
-                for_rounds(Lr, V, nround, invT, [&](const float (&z)[4], bool in, int r) {
-                    bool q[4];
-                    uint32_t nq = 0;
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        q[e] = in && zbin(z[e], zmax) == zb && okey(z[e]) == tau;
-                        nq += q[e];
-                    }
-                    uint32_t tot;
-                    const uint32_t ex = block_excl_scan_u(nq, s_redu, tot);
-                    int cand = INT_MAX;
-                    int c = run + (int)ex;
-#pragma unroll
-                    for (int e = 0; e < 4; e++)
-                        if (q[e]) {
-                            c++;
-                            if (c == (int)n_eq && cand == INT_MAX) cand = r * SROUND + 4 * t + e + 1;
-                        }
-                    const int got = block_min_i(cand, s_redi);
-                    if (lim == V && got != INT_MAX) lim = got;
-                    run += (int)tot;
-                });
-                tie_lim = lim;
-            }
+            if (n_eq < R.cnt) tie_lim = tie_limit(zb, tau, n_eq);  // index of the n_eq-th tie
         }
         // mass of the nucleus, then p' = p / total (without min-p, the
         // rounds' sums of the draw come from this pass's per-wave parts)
@@ -810,9 +885,11 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
             float c = 0.f;
             if (in)
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (zb == 256u || above_threshold(z[e], r * SROUND + 4 * t + e, zmax, zb, tau, tie_lim))
+                for (int e = 0; e < 4; e++) {
+                    const int j = r * SROUND + 4 * t + e;
+                    if (keptK(z[e], j) && (zb == 256u || above_threshold(z[e], j, zmax, zb, tau, tie_lim)))
                         c += pexp(z[e] - zmax) * invS;
+                }
             lt += c;
             if (parts) {
                 c = wave_sum(c);
@@ -833,7 +910,7 @@ __global__ __launch_bounds__(SNT) void draft_sample_kernel(const float *__restri
         return p;
     };
     auto kept = [&](float z, int j) {
-        return zb == 256u || above_threshold(z, j, zmax, zb, tau, tie_lim);
+        return keptK(z, j) && (zb == 256u || above_threshold(z, j, zmax, zb, tau, tie_lim));
     };
     // min-p: the largest probability is the argmax's, exp(0) / S (renormalized)
     float thr = 0.f;
@@ -981,15 +1058,23 @@ struct SpreadWs {
 };
 
 // The row's softmax statistics from its rounds' partials (a fixed order: the
-// same bits in every kernel); false when the row has no finite maximum or
-// sum (all -Inf, NaN, +Inf). count (a top-k threshold, whose softmax is
-// over the kept entries only): S = 1, false only without a finite maximum
-// (a NaN entry falls in the tail bucket and stays out of the top k).
+// same bits in every kernel); false for a degenerate row, whose reference
+// probabilities are all NaN (the draw returns the last index): no finite
+// maximum (all -Inf, or a +Inf) or a NaN entry anywhere (a round's sum is
+// NaN then). The reference's top-k keeps a NaN (its descending sortperm
+// puts NaN first) and its maximum is then NaN, so this holds with top-k
+// too. count (a top-k threshold, whose softmax is over the kept entries
+// only): S = 1.
 __device__ bool row_stats(const float2 *pr, int nround, float *s_redf, float &zmax, float &S, bool count = false) {
     const int t = threadIdx.x;
-    float lm = -__builtin_huge_valf();
-    for (int i = t; i < nround; i += SNT) lm = fmaxf(lm, pr[i].x);
+    float lm = -__builtin_huge_valf(), nan = 0.f;
+    for (int i = t; i < nround; i += SNT) {
+        const float2 p = pr[i];
+        lm = fmaxf(lm, p.x);
+        if (p.y != p.y) nan = 1.f;
+    }
     zmax = block_max(lm, s_redf);
+    const bool has_nan = block_max(nan, s_redf) > 0.f;
     float ls = 0.f;
     if (zmax > -__builtin_huge_valf())
         for (int i = t; i < nround; i += SNT) {
@@ -997,11 +1082,12 @@ __device__ bool row_stats(const float2 *pr, int nround, float *s_redf, float &zm
             if (p.x > -__builtin_huge_valf()) ls += p.y * pexp(p.x - zmax);
         }
     S = block_sum(ls, s_redf);
+    const bool finite_max = zmax > -__builtin_huge_valf() && zmax < __builtin_huge_valf();
     if (count) {
         S = 1.0f;
-        return zmax > -__builtin_huge_valf() && zmax < __builtin_huge_valf();
+        return finite_max && !has_nan;
     }
-    return zmax > -__builtin_huge_valf() && S > 0.f && S < __builtin_huge_valf();
+    return finite_max && !has_nan && S > 0.f && S < __builtin_huge_valf();
 }
 
 // (max, sum exp(z - max)) of round blockIdx.x of row blockIdx.y: part[row][round].
@@ -1018,9 +1104,12 @@ __global__ __launch_bounds__(SNT) void chunk_stats_kernel(const float *__restric
         for (int e = 0; e < 4; e++) m = fmaxf(m, z[e]);
     m = block_max(m, s_red);
     float sw = 0.f;
-    if (in && m > -__builtin_huge_valf())
+    if (in)
 #pragma unroll
-        for (int e = 0; e < 4; e++) sw += pexp(z[e] - m);
+        for (int e = 0; e < 4; e++) {
+            if (z[e] != z[e]) sw = __builtin_nanf("");  // (flags the row even when m is -Inf)
+            else if (m > -__builtin_huge_valf()) sw += pexp(z[e] - m);
+        }
     sw = block_sum(sw, s_red);
     if (threadIdx.x == 0) part[(size_t)row * nround + r] = make_float2(m, sw);
 }
@@ -1029,7 +1118,7 @@ __global__ __launch_bounds__(SNT) void chunk_stats_kernel(const float *__restric
 // sum, each round's probability mass, the round holding u (first with u <=
 // the running sum), then the index inside it. A row without a finite maximum
 // or sum (all -Inf, NaN, +Inf) draws V - 1, as the reference's NaN
-// probabilities do; u <= 0 draws 0.
+// probabilities do; otherwise u <= 0 draws 0.
 __global__ __launch_bounds__(SNT) void chunk_draw_kernel(const float *__restrict__ L, int V, float invT,
                                                          const float2 *__restrict__ part, const float *__restrict__ u,
                                                          int32_t *__restrict__ out) {
@@ -1041,14 +1130,14 @@ __global__ __launch_bounds__(SNT) void chunk_draw_kernel(const float *__restrict
     const int row = blockIdx.x, t = threadIdx.x;
     const int nround = (V + SROUND - 1) / SROUND;
     const float ur = u[row];
-    if (!(ur > 0.f)) {
-        if (t == 0) out[row] = 0;
-        return;
-    }
     const float2 *pr = part + (size_t)row * nround;
     float zmax, S;
-    if (!row_stats(pr, nround, s_redf, zmax, S)) {
+    if (!row_stats(pr, nround, s_redf, zmax, S) || ur != ur) {
         if (t == 0) out[row] = V - 1;
+        return;
+    }
+    if (!(ur > 0.f)) {  // the reference's draw returns index 1 (here 0) when r <= 0
+        if (t == 0) out[row] = 0;
         return;
     }
     const float invS = 1.0f / S;
@@ -1272,10 +1361,6 @@ __global__ __launch_bounds__(SNT) void topk_draw_kernel(int V, SampleArgs a, Spr
     const int row = blockIdx.x, t = threadIdx.x;
     const int nround = (V + SROUND - 1) / SROUND;
     const float ur = u[row];
-    if (!(ur > 0.f)) {  // the reference's draw returns index 1 (here 0) when r <= 0
-        if (t == 0) out[row] = 0;
-        return;
-    }
     // chunk c's candidates at slots c * SK_SPREAD + j (j < its count; id -1
     // beyond): index order, loaded with the statistics, no offsets needed
     const int n = nround * SK_SPREAD;  // <= SK_MAX
@@ -1289,9 +1374,21 @@ __global__ __launch_bounds__(SNT) void topk_draw_kernel(int V, SampleArgs a, Spr
         s_gz[i] = live ? zj : 0.f;
         s_gi[i] = live ? ij : -1;
     }
-    float lm = -__builtin_huge_valf();
-    for (int i = t; i < nround; i += SNT) lm = fmaxf(lm, ws.part[(size_t)row * nround + i].x);
+    float lm = -__builtin_huge_valf(), nan = 0.f;
+    for (int i = t; i < nround; i += SNT) {
+        const float2 p = ws.part[(size_t)row * nround + i];
+        lm = fmaxf(lm, p.x);
+        if (p.y != p.y) nan = 1.f;
+    }
     const float zm = block_max(lm, s_redf);  // (its barriers also publish the slots)
+    if (block_max(nan, s_redf) > 0.f || !(zm > -__builtin_huge_valf() && zm < __builtin_huge_valf()) || ur != ur) {
+        if (t == 0) out[row] = V - 1;  // degenerate row (a NaN is kept by the reference's top-k): NaN probabilities
+        return;
+    }
+    if (!(ur > 0.f)) {  // the reference's draw returns index 1 (here 0) when r <= 0
+        if (t == 0) out[row] = 0;
+        return;
+    }
     Select R;
     select_lds(s_gz, s_gi, n, zm, (unsigned long long)a.top_k, s_hist, s_sel, s_selm, (uint32_t *)s_sort, &s_ncnt, R);
     const uint32_t zb = R.zb, tau = R.tau;
@@ -1684,10 +1781,6 @@ __global__ __launch_bounds__(SNT) void keep_draw_kernel(const float *__restrict_
     __shared__ int s_rr;
     const int row = blockIdx.x, t = threadIdx.x, nround = ws.nround;
     const float ur = u[row];
-    if (!(ur > 0.f)) {
-        if (t == 0) out[row] = 0;
-        return;
-    }
     float zmax, S;
     bool ok;
     if (topp) {  // (the statistics row_pick_kernel stored: the same bits)
@@ -1699,8 +1792,12 @@ __global__ __launch_bounds__(SNT) void keep_draw_kernel(const float *__restrict_
         ok = row_stats(ws.part + (size_t)row * nround, nround, s_redf, zmax, S);
     }
     Keep keep;
-    if (!ok || !load_keep(ws, row, topp, minp, min_p, zmax, S, s_redf, keep)) {
+    if (!ok || !load_keep(ws, row, topp, minp, min_p, zmax, S, s_redf, keep) || ur != ur) {
         if (t == 0) out[row] = V - 1;
+        return;
+    }
+    if (!(ur > 0.f)) {  // the reference's draw returns index 1 (here 0) when r <= 0
+        if (t == 0) out[row] = 0;
         return;
     }
     const int off = SLOT_CSUM + (minp ? 4 : 0);
@@ -1823,12 +1920,12 @@ __global__ __launch_bounds__(SNT) void cand_draw_kernel(int V, SampleArgs a, Spr
     __shared__ int s_sort[SK_MAX];
     const int row = blockIdx.x, t = threadIdx.x, nround = ws.nround;
     const float ur = u[row];
-    if (!(ur > 0.f)) {  // the reference's draw returns index 1 (here 0) when r <= 0
-        if (t == 0) out[row] = 0;
+    if (((const RowSel *)ws.rowb(row))->mode == SEL_DEGEN || ur != ur) {  // (as the one-row kernel)
+        if (t == 0) out[row] = V - 1;
         return;
     }
-    if (((const RowSel *)ws.rowb(row))->mode == SEL_DEGEN) {  // (no finite maximum: as the one-row kernel)
-        if (t == 0) out[row] = V - 1;
+    if (!(ur > 0.f)) {  // the reference's draw returns index 1 (here 0) when r <= 0
+        if (t == 0) out[row] = 0;
         return;
     }
     float l = 0.f;
@@ -1845,36 +1942,40 @@ __global__ __launch_bounds__(SNT) void cand_draw_kernel(int V, SampleArgs a, Spr
 
 // In place on rows of logits: for every distinct id of the row's list in
 // [0, V): x -= presence (if presence != 0), then x = x > 0 ? x / rep : x * rep
-// (if rep != 1). A bitmap in LDS skips repeated ids.
+// (if rep != 1). A bitmap in LDS skips repeated ids; it covers a window of
+// PEN_WINDOW ids, and a vocabulary past that is taken window by window
+// (each reads the row's list once).
 constexpr int PEN_NT = 256;
-constexpr int PEN_MAX_V = 262144;
+constexpr int PEN_WINDOW = 262144;
 __global__ __launch_bounds__(PEN_NT) void penalty_kernel(float *__restrict__ L, int V, const int32_t *__restrict__ tok,
                                                           int n_tok, int64_t tok_stride, float presence,
                                                           float repetition) {
-    __shared__ uint32_t seen[PEN_MAX_V / 32];
+    __shared__ uint32_t seen[PEN_WINDOW / 32];
     const int row = blockIdx.x, t = threadIdx.x;
-    const int nw = (V + 31) / 32;
-    for (int i = t; i < nw; i += PEN_NT) seen[i] = 0u;
-    __syncthreads();
     const int32_t *ids = tok + (size_t)row * tok_stride;
     float *x = L + (size_t)row * V;
-    for (int i = t; i < n_tok; i += PEN_NT) {
-        const int id = ids[i];
-        if (id < 0 || id >= V) continue;
-        const uint32_t bit = 1u << (id & 31);
-        if (atomicOr(&seen[id >> 5], bit) & bit) continue;
-        float v = x[id];
-        if (presence != 0.f) v -= presence;
-        if (repetition != 1.0f) v = v > 0.f ? v / repetition : v * repetition;
-        x[id] = v;
+    for (int w0 = 0; w0 < V; w0 += PEN_WINDOW) {
+        const int wn = min(PEN_WINDOW, V - w0);
+        const int nw = (wn + 31) / 32;
+        __syncthreads();  // (the previous window's bitmap is no longer read)
+        for (int i = t; i < nw; i += PEN_NT) seen[i] = 0u;
+        __syncthreads();
+        for (int i = t; i < n_tok; i += PEN_NT) {
+            const int id = ids[i] - w0;
+            if (id < 0 || id >= wn) continue;
+            const uint32_t bit = 1u << (id & 31);
+            if (atomicOr(&seen[id >> 5], bit) & bit) continue;
+            float v = x[w0 + id];
+            if (presence != 0.f) v -= presence;
+            if (repetition != 1.0f) v = v > 0.f ? v / repetition : v * repetition;
+            x[w0 + id] = v;
+        }
     }
 }
 
 }  // namespace
 
-int sample_max_top_k() { return SK_MAX; }
 int sample_max_v() { return SMAX_ROUNDS * SROUND; }
-int penalty_max_v() { return PEN_MAX_V; }
 
 hipError_t launch_sample(const float *L, int rows, int V, float T, int top_k, float top_p, float min_p, const float *u,
                          int32_t *out, hipStream_t st) {
@@ -1913,11 +2014,14 @@ hipError_t launch_sample_spread(const float *L, int rows, int V, float T, int to
     const bool live = T > 0.f && nround <= SMAX_ROUNDS;
     const bool plain = live && top_k == 0 && top_p >= 1.0f && min_p <= 0.f;
     const bool topk = live && top_k >= 1 && top_k <= SK_SPREAD && nround <= SPART_ROUNDS;
-    // top-k beyond the chunk-candidate path: the threshold as top-p's, by count
-    const bool bigk = live && top_k > 0 && !topk;
+    // top-k beyond the chunk-candidate path: the threshold as top-p's, by
+    // count, its kept entries compacted (up to SK_MAX of them; a larger top-k
+    // takes the one-workgroup kernel's threshold path)
+    const bool bigk = live && top_k > 0 && top_k <= SK_MAX && !topk;
     const bool topp = live && ((top_k == 0 && top_p < 1.0f) || bigk);
     const bool minp = live && top_k == 0 && min_p > 0.f;
     if (!plain && !topk && !topp && !minp) return launch_sample(L, rows, V, T, top_k, top_p, min_p, u, out, st);
+    if (top_k > SK_MAX) return launch_sample(L, rows, V, T, top_k, top_p, min_p, u, out, st);
     const float invT = 1.0f / T;
     const size_t rc = (size_t)rows * nround;
     uint8_t *w = (uint8_t *)ws;

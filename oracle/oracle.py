@@ -232,13 +232,27 @@ def rmsnorm(x, eps=1e-6, w=None):
 
 # ---- draft-side sampler: numpy restatement (float32 like the reference) ----
 
+def julia_desc_order(L) -> np.ndarray:
+    """sortperm(L, rev=true) (src/ModelCPU.jl:1136): Julia's isless
+    reversed, stable: every NaN first (NaNs equal), then descending values
+    with +0.0 before -0.0, equals in index order."""
+    L = np.asarray(L, dtype=np.float32)
+    nan = np.isnan(L)
+    val = np.where(nan, np.float32(0), L).astype(np.float64)
+    pos_zero_first = np.where(np.signbit(L), 0, 1)
+    idx = np.arange(L.size)
+    return np.lexsort((idx, -pos_zero_first, -val, -nan.astype(np.int8)))
+
+
 def sample_dist(logits, temperature: float = 1.0, top_p: float = 1.0, top_k: int = 0,
                 min_p: float = 0.0) -> np.ndarray:
     """The float32 distribution softmax_sample (src/ModelCPU.jl:1123-1200)
     draws from at temperature > 0: z = L / T (:1130-1132); top-k by the
     stable descending sortperm (:1135-1143); softmax with max subtraction
-    (:1146-1148); top-p: the shortest prefix of the stable descending
-    sortperm of p whose cumulative sum is >= top_p, renormalized when the sum
+    (:1146-1148; a NaN kept by top-k makes the maximum and every
+    probability NaN, as Julia's maximum propagates NaN); top-p: the shortest
+    prefix of the stable descending sortperm of p whose cumulative sum is
+    >= top_p, renormalized when the sum
     is > 0 (:1151-1173); min-p: drop p < max(p) * min_p, renormalize
     (:1176-1188). Probabilities are float32 element by element as in the
     reference; its cumulative sums are sequential float32 loops, which over
@@ -251,7 +265,7 @@ def sample_dist(logits, temperature: float = 1.0, top_p: float = 1.0, top_k: int
     if T != np.float32(1.0):
         L = L / T
     if top_k > 0:
-        order = np.argsort(-L, kind="stable")
+        order = julia_desc_order(L)
         keep = np.zeros(V, dtype=bool)
         keep[order[:min(top_k, V)]] = True
         L[~keep] = -np.inf

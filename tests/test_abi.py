@@ -90,8 +90,8 @@ def test_spec_accept_ex_checks_without_gpu(lib):
     assert lib.ihip_spec_accept_ex(*args(40, 1.0, 0.0, 1024)) == -12  # workspace short of the filtered need
     assert lib.ihip_spec_accept_ex(*args(-2, 1.0, 0.0, 1 << 40)) == -22
     assert lib.ihip_spec_accept_ex(*args(0, float("nan"), 0.0, 1 << 40)) == -22
-    assert lib.ihip_spec_accept_ex(*args(40, 1.0, 0.0, 1 << 40, V=151937)) == -22
-    assert b"multiple of 4" in lib.ihip_last_error()
+    assert lib.ihip_spec_accept_ex(*args(40, 1.0, 0.0, 1 << 40, V=5000000)) == -22
+    assert b"above 4194304" in lib.ihip_last_error()
 
 
 def _dropin_child(env_extra, inner_dim, outer_dim=3):
@@ -157,29 +157,31 @@ def test_mlp_forward_argument_checks(lib):
 
 def test_sampler_argument_checks(lib):
     """ihip_sample / ihip_sample_ex / ihip_apply_penalties validate before
-    touching the GPU."""
+    touching the GPU (any V >= 1, any logits alignment and any top_k pass
+    these checks: only calls that fail here are made without a GPU)."""
     buf = (C.c_uint8 * 64)()
     p16 = (C.addressof(buf) + 15) & ~15
     assert lib.ihip_sample(None, 1, 8, 1.0, 0, 1.0, 0.0, p16, p16, None) == -14
-    assert lib.ihip_sample(p16, 1, 6, 1.0, 0, 1.0, 0.0, p16, p16, None) == -22      # V % 4
-    assert lib.ihip_sample(p16 + 4, 1, 8, 1.0, 0, 1.0, 0.0, p16, p16, None) == -22  # alignment
+    assert lib.ihip_sample(p16, 1, 0, 1.0, 0, 1.0, 0.0, p16, p16, None) == -22      # V
+    assert lib.ihip_sample(p16, 1, 5000000, 1.0, 0, 1.0, 0.0, p16, p16, None) == -22  # V above 4194304
+    assert lib.ihip_sample(p16, 0, 8, 1.0, 0, 1.0, 0.0, p16, p16, None) == -22      # rows
     assert lib.ihip_sample(p16, 1, 8, -1.0, 0, 1.0, 0.0, p16, p16, None) == -22     # temperature
-    assert lib.ihip_sample(p16, 1, 151936, 1.0, 5000, 1.0, 0.0, p16, p16, None) == -22  # top_k above 4096
-    assert b"top_k" in lib.ihip_last_error()
     assert lib.ihip_sample(p16, 1, 8, 1.0, -1, 1.0, 0.0, p16, p16, None) == -22
+    assert b"top_k" in lib.ihip_last_error()
     assert lib.ihip_sample(p16, 1, 8, 1.0, 0, float("nan"), 0.0, p16, p16, None) == -22
     # ihip_sample_ex: the same checks, plus its workspace (4104 bytes per 4096 logits of each row, and
     # 49408 bytes per row)
     nb = C.c_size_t()
     assert lib.ihip_sample_ws_bytes(2, 151936, C.byref(nb)) == 0 and nb.value == 2 * 38 * 4104 + 2 * 49408
-    assert lib.ihip_sample_ws_bytes(1, 6, C.byref(nb)) == -22
+    assert lib.ihip_sample_ws_bytes(1, 6, C.byref(nb)) == 0 and nb.value == 4104 + 49408  # any V
+    assert lib.ihip_sample_ws_bytes(1, 0, C.byref(nb)) == -22
     assert lib.ihip_sample_ws_bytes(1, 8, None) == -14
     assert lib.ihip_sample_ex(p16, 1, 8, 1.0, 0, 1.0, 0.0, p16, p16, None, 1 << 20, None) == -14  # no workspace
     assert lib.ihip_sample_ex(p16, 2, 151936, 1.0, 0, 1.0, 0.0, p16, p16, p16, 8, None) == -12  # too small
     assert lib.ihip_sample_ex(p16, 1, 8, 1.0, 0, 1.0, 0.0, p16, p16, p16 + 4, 1 << 20, None) == -22  # alignment
     assert lib.ihip_sample_ex(p16, 1, 8, -1.0, 0, 1.0, 0.0, p16, p16, p16, 1 << 20, None) == -22
     assert lib.ihip_apply_penalties(None, 1, 8, p16, 1, 0, 0.5, 1.0, None) == -14
-    assert lib.ihip_apply_penalties(p16, 1, 300000, p16, 1, 0, 0.5, 1.0, None) == -22
+    assert lib.ihip_apply_penalties(p16, 1, 0, p16, 1, 0, 0.5, 1.0, None) == -22
     assert lib.ihip_apply_penalties(p16, 2, 8, p16, 4, 2, 0.5, 1.0, None) == -22  # stride < n_tok
 
 

@@ -182,7 +182,8 @@ def test_topk_spread_matches_one_workgroup(ih):
     spread over workgroups (each chunk's top-k, then the row's among them)
     give the one-workgroup kernel's tokens bit for bit: Gaussian and
     quantized (tied) rows at V = 151936, 262144 and 4100, rows all -Inf or
-    holding NaN or +Inf, u = 0, with top-p and min-p after the cut. (Larger
+    holding NaN or +Inf (V - 1 on both), u = 0, with top-p and min-p after
+    the cut. (Larger
     k, and V above 262144, take the threshold kernels by count: tested
     against the oracle below.)"""
     rng = np.random.default_rng(17)
@@ -271,8 +272,9 @@ def test_topk_large_spread(ih):
     one-workgroup kernel's tokens bit for bit, and match the oracle:
     Gaussian rows at V = 151936 and 300000, quantized rows (ties at the
     threshold, gathered and over the row), a flat row (the first k), rows
-    all -Inf or +Inf (V - 1) and a row holding a NaN (left out of the top k;
-    also through the k <= 64 candidate path)."""
+    all -Inf or +Inf (V - 1) and a row holding a NaN (the reference's top-k
+    keeps it, first in its descending sortperm, and every probability is
+    then NaN: V - 1; also through the k <= 64 candidate path)."""
     rng = np.random.default_rng(29)
     cases = [(3.0 * rng.standard_normal((12, VOCAB))).astype(np.float32),
              (3.0 * rng.standard_normal((4, 300000))).astype(np.float32),
@@ -347,3 +349,118 @@ def test_penalties_exact(ih):
     d3 = _dev(L)
     ih.apply_penalties_(d3, torch.from_numpy(ids))  # presence 0, repetition 1: untouched
     np.testing.assert_array_equal(d3.cpu().numpy(), L)
+
+
+DEGENERATE_SETTINGS = [dict(), dict(temperature=0.8, top_k=40), dict(temperature=0.8, top_k=1000),
+                       dict(temperature=0.8, top_k=10000), dict(top_p=0.9), dict(min_p=0.05),
+                       dict(top_k=100, top_p=0.9, min_p=0.05), dict(top_k=6000, top_p=0.9)]
+
+
+def test_degenerate_rows_before_u0(ih):
+    """A row whose reference probabilities are all NaN (all -Inf, a +Inf, a
+    NaN anywhere: kept by top-k too) draws the last index whatever u is,
+    u <= 0 included (the reference's r <= cumsum is false against NaN);
+    a finite row draws index 0 at u <= 0. Every setting and both entry
+    points, one and several rounds, against the oracle."""
+    for V in (4096, 3 * 4096 + 5):
+        a = np.full(V, -np.inf, np.float32)
+        d = np.zeros(V, np.float32)
+        d[V - 2] = np.inf
+        b = np.zeros(V, np.float32)
+        b[V // 2] = np.nan
+        c = np.full(V, -np.inf, np.float32)
+        c[0] = np.nan  # a NaN among -Inf (the round's maximum is -Inf)
+        c[V - 1] = 1.0
+        f = np.linspace(-1, 1, V).astype(np.float32)
+        for kw in DEGENERATE_SETTINGS:
+            for x in (a, d, b, c, f):
+                us = [0.0, -0.5, 0.37]
+                want = [O.softmax_sample(x, u, **kw) for u in us]
+                for spread in (True, False):
+                    got = list(_draw(ih, x, us, spread=spread, **kw))
+                    assert got == want, (V, kw, spread, got, want)
+
+
+ODD_SETTINGS = [dict(temperature=1.0), dict(temperature=0.8, top_p=0.9), dict(temperature=0.8, top_k=40),
+                dict(temperature=0.7, top_k=50, top_p=0.95), dict(temperature=1.0, min_p=0.05),
+                dict(temperature=0.9, top_k=1000, top_p=0.9), dict(temperature=1.0, top_k=10000),
+                dict(temperature=0.0)]
+
+
+@pytest.mark.parametrize("kw", ODD_SETTINGS, ids=lambda kw: ",".join(f"{k}={v}" for k, v in kw.items()))
+def test_any_vocabulary_size(ih, kw):
+    """Vocabularies that are not a multiple of 4 (rows then start at any
+    4-byte address): V = 151937 against the oracle on both entry points, and
+    tiny V = 1, 2, 3, 5, 4099 exactly."""
+    rng = np.random.default_rng(41)
+    rows, V = 24, 151937
+    L = (3.0 * rng.standard_normal((rows, V))).astype(np.float32)
+    us = rng.random(rows).astype(np.float32)
+    want = [O.softmax_sample(L[r], float(us[r]), **kw) for r in range(rows)]
+    for spread in (True, False):
+        got = _draw(ih, L, us, spread=spread, **kw)
+        bad = 0
+        for r in range(rows):
+            if got[r] != want[r]:
+                assert kw.get("temperature", 1.0) != 0.0, (r, got[r], want[r])
+                assert _near_boundary(L[r], float(us[r]), int(got[r]), want[r], kw), (spread, r, got[r], want[r])
+                bad += 1
+        assert bad <= 1, (spread, kw)
+    for Vs in (1, 2, 3, 5, 4099):
+        X = np.round(2.0 * rng.standard_normal((6, Vs))).astype(np.float32)
+        u6 = rng.random(6).astype(np.float32)
+        want = [O.softmax_sample(X[r], float(u6[r]), **kw) for r in range(6)]
+        for spread in (True, False):
+            got = list(_draw(ih, X, u6, spread=spread, **kw))
+            assert got == want, (Vs, spread, got, want)
+
+
+@pytest.mark.parametrize("kw", [dict(temperature=0.8, top_k=10000), dict(temperature=1.0, top_k=5000, top_p=0.9),
+                                dict(temperature=0.9, top_k=20000, min_p=0.01),
+                                dict(temperature=0.7, top_k=150000, top_p=0.8, min_p=0.02)],
+                         ids=lambda kw: ",".join(f"{k}={v}" for k, v in kw.items()))
+def test_topk_above_4096(ih, kw):
+    """top_k from 4097 up to V - 1 (the k-th element's threshold by count,
+    the softmax over the kept entries, then top-p / min-p on it) against the
+    oracle at V = 151936, Gaussian and quantized (tied) rows, both entry
+    points; a flat row keeps its first k."""
+    rng = np.random.default_rng(43)
+    L = np.concatenate([(3.0 * rng.standard_normal((16, VOCAB))).astype(np.float32),
+                        rng.integers(0, 4, size=(8, VOCAB)).astype(np.float32)])
+    us = rng.random(L.shape[0]).astype(np.float32)
+    want = [O.softmax_sample(L[r], float(us[r]), **kw) for r in range(L.shape[0])]
+    for spread in (True, False):
+        got = _draw(ih, L, us, spread=spread, **kw)
+        bad = 0
+        for r in range(L.shape[0]):
+            if got[r] != want[r]:
+                assert _near_boundary(L[r], float(us[r]), int(got[r]), want[r], kw), (spread, r, got[r], want[r])
+                bad += 1
+        assert bad <= 1, (spread, kw)
+    k = kw["top_k"]
+    flat = np.zeros(VOCAB, np.float32)
+    js = [0, 37, 500, 4000, k - 1]
+    uf = ((np.array(js) + 0.5) / k).astype(np.float32)  # mid-step: token j
+    if kw.get("top_p", 1.0) >= 1.0:
+        for spread in (True, False):
+            assert list(_draw(ih, flat, uf, spread=spread, **kw)) == js
+
+
+def test_penalties_beyond_262144(ih):
+    """Penalties over a vocabulary of 300000 (the LDS bitmap taken in two
+    windows): ids on both sides of 262144, repeats, out-of-range ids; one
+    list for every row and one per row, bit-exact against the oracle."""
+    import torch
+    rng = np.random.default_rng(47)
+    V = 300000
+    L = (2.0 * rng.standard_normal((3, V))).astype(np.float32)
+    ids = np.array([5, 262143, 262144, 262144, 299999, 300000, -1, 150000, 5, 280001], np.int32)
+    d = _dev(L)
+    ih.apply_penalties_(d, torch.from_numpy(ids), presence=0.4, repetition=1.3)
+    want = np.stack([O.apply_penalties(L[r], ids, 0.4, 1.3) for r in range(3)])
+    np.testing.assert_array_equal(d.cpu().numpy(), want)
+    per_row = rng.integers(-5, V + 5, size=(3, 2000)).astype(np.int32)
+    d2 = _dev(L)
+    ih.apply_penalties_(d2, torch.from_numpy(per_row), presence=-0.25, repetition=0.8)
+    want2 = np.stack([O.apply_penalties(L[r], per_row[r], -0.25, 0.8) for r in range(3)])
+    np.testing.assert_array_equal(d2.cpu().numpy(), want2)

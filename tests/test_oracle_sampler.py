@@ -109,3 +109,33 @@ def test_penalties_closed_form():
     np.testing.assert_array_equal(out2, np.array([2.0 / np.float32(1.5), -2.0, 0.5, -0.5 * np.float32(1.5), 3.0],
                                                  np.float32))
     np.testing.assert_array_equal(O.apply_penalties(L, [0, 1]), L)  # presence 0, repetition 1: no-op
+
+
+def test_julia_descending_order_and_nan_rows():
+    """julia_desc_order is sortperm(L, rev=true): Julia's isless reversed and
+    stable (brute force over Python's sort by (isless key, index)): NaN
+    first, +0.0 before -0.0, equals by index. With a NaN kept by top-k the
+    reference's maximum and probabilities are NaN and the draw returns the
+    last index for every r, r <= 0 included; a finite row returns the first
+    index at r <= 0 whatever the filters."""
+    nan, inf = np.nan, np.inf
+
+    def key(v):  # Julia's isless as a sort key: NaN largest, -0.0 below +0.0
+        return (2, 0.0, 0) if np.isnan(v) else (1, float(v), 0 if np.signbit(v) else 1)
+
+    rng = np.random.default_rng(3)
+    pool = np.array([nan, inf, -inf, 0.0, -0.0, 1.5, -2.0, 1.5], np.float32)
+    for _ in range(200):
+        L = rng.choice(pool, size=int(rng.integers(1, 12))).astype(np.float32)
+        want = sorted(range(L.size), key=lambda i: (tuple(-x for x in key(L[i])), i))
+        assert O.julia_desc_order(L).tolist() == want, L
+    V = 50
+    x = np.linspace(-2, 2, V).astype(np.float32)
+    y = x.copy()
+    y[17] = nan
+    for kw in (dict(top_k=5), dict(top_k=1), dict(top_k=5, top_p=0.5), dict(top_k=5, min_p=0.1), dict()):
+        for r in (0.0, -1.0, 0.3, 0.999):
+            assert O.softmax_sample(y, r, **kw) == V - 1, (kw, r)
+            if r <= 0:
+                assert O.softmax_sample(x, r, **kw) == 0, (kw, r)
+    assert set(np.nonzero(O.sample_dist(x, top_k=3))[0].tolist()) == {47, 48, 49}
