@@ -276,7 +276,7 @@ def sample_dist(logits, temperature: float = 1.0, top_p: float = 1.0, top_k: int
     if top_p < 1.0:
         order = np.argsort(-p, kind="stable")
         c = np.cumsum(p[order], dtype=np.float64)
-        hit = np.nonzero(c >= top_p)[0]
+        hit = np.nonzero(c >= float(np.float32(top_p)))[0]  # top_p::Float32 (src/ModelCPU.jl:1123)
         n_keep = int(hit[0]) + 1 if hit.size else V
         keep = np.zeros(V, dtype=bool)
         keep[order[:n_keep]] = True

@@ -139,3 +139,13 @@ def test_julia_descending_order_and_nan_rows():
             if r <= 0:
                 assert O.softmax_sample(x, r, **kw) == 0, (kw, r)
     assert set(np.nonzero(O.sample_dist(x, top_k=3))[0].tolist()) == {47, 48, 49}
+
+
+def test_top_p_is_float32():
+    """softmax_sample's top_p is a Float32 (src/ModelCPU.jl:1123): 0.9 is
+    0.899999976..., so 4500 of 5000 equal probabilities fl32(1/5000)
+    (exact sum 0.8999999773) reach it where a float64 0.9 would need 4501."""
+    L = np.zeros(5000, np.float32)
+    p = O.sample_dist(L, top_p=0.9)
+    assert int((p > 0).sum()) == 4500
+    assert 4500 * float(np.float32(1 / 5000)) >= float(np.float32(0.9)) > 0.8999999
