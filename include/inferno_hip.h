@@ -262,12 +262,15 @@ typedef struct ihip_chain_out {
  * input stage, e.g. RMSNorm with the previous layer's partials folded) or cin
  * (a chained producer's operand), and cout (NULL only with IHIP_GEMM_DEFER,
  * which leaves K-slice partials as ihip_gemm_q_ex does). flags: IHIP_GEMM_F32,
- * IHIP_GEMM_PACKED, IHIP_GEMM_DEFER. Epilogues other than IHIP_EPI_STORE need
- * a matmul that is not split over K (K up to 8192 for Q4_K, 4096 for Q5_K /
- * Q6_K, 2048 for Q8_0); shapes off the one-tile streaming plan return
- * IHIP_EINVAL. The width an operand covers (N; N / 2 for IHIP_EPI_GATE;
- * stat_rows for IHIP_EPI_STATS) must be a multiple of 256. Workspace as
- * ihip_gemm_q. */
+ * IHIP_GEMM_PACKED, IHIP_GEMM_DEFER. A matmul split over K (K above 8192 for
+ * Q4_K, 4096 for Q5_K / Q6_K, 2048 for Q8_0: e.g. the down projection)
+ * finishes each 16-row tile in the workgroup of the last K-slice to reach
+ * it, which sums the slices in slice order and runs the epilogue: the
+ * workspace then holds per-tile slice counts that must be zero before the
+ * first such call (a zeroed workspace; the calls leave them zero). Shapes
+ * off the one-tile streaming plan return IHIP_EINVAL. The width an operand
+ * covers (N; N / 2 for IHIP_EPI_GATE; stat_rows for IHIP_EPI_STATS) must be
+ * a multiple of 256. Workspace as ihip_gemm_q. */
 int ihip_gemm_q_chain(int qtype, const void *w_packed, const ihip_gemm_input *in,
                       const ihip_chain_in *cin, const ihip_chain_out *cout,
                       int M, int N, int K, int flags, void *ws, size_t ws_bytes,

@@ -580,8 +580,7 @@ int ihip_gemm_q_chain(int qtype, const void *w_packed, const ihip_gemm_input *in
                                    N, K, flags, ws, S(stream));
     }
     if (err == hipErrorInvalidValue)
-        return fail(IHIP_EINVAL, "%s: shape not on the one-tile streaming plan (or a statistics epilogue on a "
-                                 "K-split matmul)", fn);
+        return fail(IHIP_EINVAL, "%s: shape not on the one-tile streaming plan", fn);
     return err == hipSuccess ? ok() : hip_fail(err, fn);
 }
 

@@ -3,6 +3,7 @@
 // and per-tile statistics, and where the consumer finds them. Field meanings
 // are given with ihip_chain_in / ihip_chain_out in include/inferno_hip.h.
 #pragma once
+#include <hip/hip_runtime.h>
 #include <cstdint>
 
 enum { EPI_STORE = 0, EPI_STATS = 1, EPI_RESID = 2, EPI_GATE = 3 };
@@ -32,4 +33,9 @@ struct Chain {
     int ysum_stride;
     float *yssq;           // [tile][8], or null
     int stat_rows;         // statistics over rows < stat_rows (EPI_STATS)
+    // a K-split producer's epilogue: per 16-row tile, the slices' partial
+    // tiles ([tile][slice][64 lanes] float2) and the count of slices done
+    // (0 between calls: the last slice to arrive resets it)
+    float2 *tile_part;
+    int *tile_cnt;
 };

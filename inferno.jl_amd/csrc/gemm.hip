@@ -1557,6 +1557,37 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, const uint8_t *__restrict__ af
         // scales' barriers also publish pend)
         static_assert(CE, "after-loop epilogues are the chained producer's");
         rsc.finish(ssq, n_ssq, K, eps, tid, rsp, rs);
+        if (gridDim.y > 1) {
+            // split over K: wave w stores its tiles' partial sums (this
+            // slice's) and counts the slice in; the last slice to arrive at a
+            // tile sums the slices in slice order (the same bits whichever
+            // arrives last) and runs the tile's epilogue. No wave waits for
+            // another: a tile's epilogue runs in whichever workgroup
+            // completes it.
+            const int S = (int)gridDim.y, sl = (int)blockIdx.y;
+            for (int js = wave; js < my_tiles; js += NW) {
+                const int tile = (int)blockIdx.x + G * js;
+                float2 *pt = ch.tile_part + (size_t)tile * S * 64 + lane;
+                pt[(size_t)sl * 64] = pend[js][lane];
+                __threadfence();  // (release: the partial is visible before the count)
+                int old = 0;
+                if (lane == 0) old = atomicAdd(ch.tile_cnt + tile, 1);
+                old = __shfl(old, 0);
+                if (old != S - 1) continue;
+                __threadfence();  // (acquire: the other slices' partials)
+                float2 acc = pt[0];
+                for (int q = 1; q < S; q++) {
+                    const float2 v = pt[(size_t)q * 64];
+                    acc.x += v.x;
+                    acc.y += v.y;
+                }
+                if (lane == 0) ch.tile_cnt[tile] = 0;  // (every slice has counted: ready for the next call)
+                if (spread || js != js0) load_pre(tile);
+                chain_epilogue(ch, Y, acc.x, rs, M, N, tile, n_in, g, 0, pre_y0, pre_w);
+                chain_epilogue(ch, Y, acc.y, rs, M, N, tile, n_in, g, 1, pre_y1, pre_w);
+            }
+            return;
+        }
         for (int js = js0; js < my_tiles; js += NW) {
             const float2 p2 = pend[js][lane];
             const int tile = (int)blockIdx.x + G * js;
@@ -1948,7 +1979,7 @@ hipError_t launch_v(const uint8_t *W, const float *X, const ActIn &in, float *Y,
             gemm_v_kernel<QT, NW, UPS, SPLIT, PK, MT, false, 2><<<dim3(G, S), NW * 64, 0, st>>>(
                 W, a.afrag, a.mfrag, a.inv, M, N, K, G, 0, 0, Y, accum, in.op == ACT_RMSNORM ? a.ssq : nullptr,
                 n_units, in.eps, (S > 1 || in.defer) ? part : nullptr, c);
-            return hipGetLastError();  // (statistics epilogues: one K-slice, nothing to reduce)
+            return hipGetLastError();  // (a chained epilogue sums its own K-slices)
         }
     }
     gemm_v_kernel<QT, NW, UPS, SPLIT, PK, MT, false, 0><<<dim3(G, S), NW * 64, 0, st>>>(
@@ -1978,7 +2009,7 @@ hipError_t launch_vx(const uint8_t *W, float *Y, int M, int N, int K, int S, int
             W, ch.xop, xs, nullptr, M, N, K, G, ch.xsum_stride, ch.x_tiles_per_unit, Y, 0, ssq, n_ssq, eps,
             (S > 1 || defer) ? part : nullptr, ch);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || S == 1 || defer) return e;
+    if (e != hipSuccess || S == 1 || defer || ch.epi != EPI_STORE) return e;
     const int64_t MN = (int64_t)M * N;
     reduce_kernel<<<(unsigned)((MN + 1023) / 1024), 256, 0, st>>>(part, Y, S, MN, 0);
     return hipGetLastError();
@@ -2037,7 +2068,7 @@ struct GemmPlan {
     int ups;         // LDS kernel: 256-element units per K-slice
     int S;           // K-slices (grid.y)
     int G;           // workgroups per K-slice (grid.x)
-    size_t off_xs, off_inv, off_mfrag, off_ssq, off_part, ws_bytes;
+    size_t off_xs, off_inv, off_mfrag, off_ssq, off_part, off_cnt, ws_bytes;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -2137,7 +2168,12 @@ static GemmPlan plan_gemm(int qt, int M, int N, int K, int flags) {
     p.off_ssq = o;
     o += align256((size_t)n_units * TOK * 4);
     p.off_part = o;
-    o += align256((size_t)p.S * M * N * 4);  // partials (split-K or accumulate)
+    // partials (split-K or accumulate; a K-split chained epilogue's
+    // [tile][slice][64] float2), then that epilogue's per-tile slice counts
+    const size_t tiles16 = (size_t)(N + 15) / 16;
+    o += align256(std::max((size_t)p.S * M * N * 4, p.S > 1 ? (size_t)p.S * tiles16 * 512 : 0));
+    p.off_cnt = o;
+    o += align256(tiles16 * 4);
     p.ws_bytes = o;
     return p;
 }
@@ -2269,20 +2305,24 @@ hipError_t launch_gemm(int qt, const void *W, const float *X, float *Y, int M, i
 // usual) or a chained producer's operand (in == nullptr: ch.xop, rescaled in
 // registers), the RMSNorm row scales then from the producer's tile
 // sums of squares (ssq_in, n_ssq_in parts; null = none); epilogue ch.epi
-// (EPI_STORE with flags bit 32 leaves K-slice partials in ws). Returns
-// hipErrorInvalidValue where the plan is not the one-tile streaming kernel or
-// a statistics epilogue meets a K-split.
-hipError_t launch_gemm_chain(int qt, const void *W, const ActIn *in, const float *X, const Chain &ch,
+// (EPI_STORE with flags bit 32 leaves K-slice partials in ws; other
+// epilogues of a K-split plan sum the slices per tile themselves, with the
+// per-tile counts kept zero between calls in ws). Returns
+// hipErrorInvalidValue where the plan is not the one-tile streaming kernel.
+hipError_t launch_gemm_chain(int qt, const void *W, const ActIn *in, const float *X, const Chain &chain,
                              const float *ssq_in, int n_ssq_in, float eps, float *Y, int M, int N, int K, int flags,
                              void *ws, hipStream_t st) {
     const bool defer = (flags & 32) != 0;
     const int f = (flags & ~48) | 1 | 8;  // fp32-accurate, packed
     const GemmPlan p = plan_gemm(qt, M, N, K, f);
     if (!p.stream || p.MT != 1 || !p.split) return hipErrorInvalidValue;
-    if (ch.epi != EPI_STORE && (p.S != 1 || defer)) return hipErrorInvalidValue;
-    if (ch.epi != EPI_STORE && ((N + 15) / 16 + p.G - 1) / p.G > CHAIN_MAX_TILES) return hipErrorInvalidValue;
+    if (chain.epi != EPI_STORE && defer) return hipErrorInvalidValue;
+    if (chain.epi != EPI_STORE && ((N + 15) / 16 + p.G - 1) / p.G > CHAIN_MAX_TILES) return hipErrorInvalidValue;
     uint8_t *wsp = (uint8_t *)ws;
     float *part = (float *)(wsp + p.off_part);
+    Chain ch = chain;  // (a K-split epilogue's partials and counts live in ws)
+    ch.tile_part = (float2 *)part;
+    ch.tile_cnt = (int *)(wsp + p.off_cnt);
     const uint8_t *w = (const uint8_t *)W;
     // (chained calls: the 8-wave plans, and Q6_K's 4 x 3-unit one)
     const bool q6_43 = qt == QT_Q6_K && p.NW == 4 && p.UPS == 3;

@@ -284,7 +284,9 @@ def gemm_q_chain(qtype: int, w_packed, n: int, k: int, m: int, x=None, act: int 
     weights whose input is either x through the usual input stage (act,
     norm_w, add as gemm_q_ex) or a chained producer's rows (cin, from
     chain_in), and whose output goes through cout (chain_out), or stays as
-    K-slice partials in ws with GEMM_DEFER."""
+    K-slice partials in ws with GEMM_DEFER. A K-split matmul with an output
+    descriptor keeps per-tile counts in ws, which must start zeroed (a
+    workspace allocated here is)."""
     import torch
     if (x is None) == (cin is None):
         raise ValueError("pass exactly one of x / cin")
@@ -302,8 +304,8 @@ def gemm_q_chain(qtype: int, w_packed, n: int, k: int, m: int, x=None, act: int 
                             None if add is None else add[0], 0 if add is None else add[1],
                             0 if add is None else add[2])
     need = gemm_ws_bytes(qtype, m, n, k, GEMM_F32 | GEMM_PACKED)
-    if ws is None:
-        ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    if ws is None:  # (zeroed: a K-split chained epilogue's per-tile counts start at zero)
+        ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
     check_tensor(ws, "ws", torch.uint8, min_numel=need)
     _lib.check(_lib.load().ihip_gemm_q_chain(qtype, _ptr(w_packed), None if gi is None else C.byref(gi),
                                              None if cin is None else C.byref(cin),

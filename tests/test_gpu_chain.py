@@ -215,11 +215,6 @@ def test_chain_argument_checks(ih):
     with pytest.raises(ih.HipError):  # stat_rows not a multiple of 256
         ih.gemm_q_chain(F.Q4_K, p, 256, 256, 5, x=torch.zeros((5, 256), device="cuda"),
                         cout=ih.chain_out(ih.EPI_STATS, y, F.Q4_K, op, ts, stat_rows=128))
-    with pytest.raises(ih.HipError):  # a statistics epilogue on a K-split matmul
-        big = ih.pack_weights(F.Q6_K, _dev(synth.matrix(F.Q6_K, 256, 12288, 8)), 256, 12288)
-        ih.gemm_q_chain(F.Q6_K, big, 256, 12288, 2, x=torch.zeros((2, 12288), device="cuda"),
-                        cout=ih.chain_out(ih.EPI_STATS, torch.zeros((2, 256), device="cuda"), F.Q4_K, op, ts,
-                                          stat_rows=256))
     with pytest.raises(ih.HipError):  # a Q4_K consumer needs the tile sums (min terms)
         ih.gemm_q_chain(F.Q4_K, p, 256, 256, 5, cin=ih.chain_in(op, None, 16), cout=ih.chain_out(ih.EPI_STORE, y))
     with pytest.raises(ih.HipError):  # unknown consumer layout
@@ -317,3 +312,66 @@ def test_large_statistics_producer(ih, qt, M, N):
     ih.gemm_q_chain(F.Q4_K, po, 512, S, M, cin=ih.chain_in(op, ts, 16), cout=ih.chain_out(ih.EPI_STORE, yo))
     torch.cuda.synchronize()
     assert rel_l2(_h(yo), O.gemv_f64(F.Q4_K, wo, gy[:, :S], M, 512, S)) <= 1e-5
+
+
+@pytest.mark.parametrize("qt,N,K", [(F.Q6_K, 512, 6144), (F.Q6_K, 256, 12288), (F.Q4_K, 256, 12288)])
+@pytest.mark.parametrize("M", [1, 5, 8])
+def test_ksplit_chained_epilogue(ih, M, qt, N, K):
+    """A chained producer split over K (2, 4 or 3 K-slices: the down
+    projection's plan): each tile's slices are summed in slice order by the
+    last slice to arrive, which runs the epilogue. EPI_RESID into the
+    residual with the operand of x w for a Q4_K and a Q6_K consumer (the next
+    [q; k; v], the head) and its tile sums of squares: x_new against x_old +
+    the oracle's product (fp32 rounding of the residual), the statistics
+    against numpy, each consumer against the classic call (input stage with
+    the RMSNorm) on the same rows; EPI_STATS likewise. Two calls in a row
+    give the same bits (the per-tile counts are zero again after each)."""
+    import torch
+    q = ih.quantized_kernels
+    w = synth.matrix(qt, N, K, synth.stream_for(21, f"ks.{qt}.{N}.{K}"))
+    pw = ih.pack_weights(qt, _dev(w), N, K)
+    rng = np.random.default_rng(7 * M + K)
+    xin = (2.0 * rng.standard_normal((M, K))).astype(np.float32)
+    r0 = rng.standard_normal((M, N)).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(N)).astype(np.float32)
+    ref = O.gemv_f64(qt, w, xin, M, N, K)
+    ws = torch.zeros(q.gemm_ws_bytes(qt, M, N, K, FL), dtype=torch.uint8, device="cuda")
+    outs = []
+    for rep in range(2):
+        x = _dev(r0)
+        op, ts, ssq = ih.chain_buffers(N, ssq=True)
+        ih.gemm_q_chain(qt, pw, N, K, M, x=_dev(xin), ws=ws,
+                        cout=ih.chain_out(ih.EPI_RESID, x, F.Q4_K, op, ts, norm_w=_dev(nw), tile_ssq=ssq))
+        torch.cuda.synchronize()
+        outs.append((_h(x), _h(op), _h(ts), _h(ssq)))
+    assert all(np.array_equal(a, b) for a, b in zip(outs[0], outs[1]))
+    xn, _, tsn, ssqn = outs[0]
+    assert rel_l2(xn, r0.astype(np.float64) + ref) <= 1e-6
+    assert _sums_ok(tsn, xn * nw, M, N // 16)
+    sq = (xn.astype(np.float64) ** 2).reshape(M, N // 16, 16).sum(axis=2).T
+    assert np.allclose(ssqn[:, :M], sq, rtol=1e-6, atol=0)
+    # consumers of the chained residual (RMSNorm row scale from the tile sums of squares)
+    x = _dev(xn)
+    for cq in (F.Q4_K, F.Q6_K):
+        wc = synth.matrix(cq, 512, N, synth.stream_for(22, f"ks.c{cq}.{N}"))
+        pc = ih.pack_weights(cq, _dev(wc), 512, N)
+        op, ts, ssq = ih.chain_buffers(N, ssq=True)
+        x2 = _dev(r0)
+        ih.gemm_q_chain(qt, pw, N, K, M, x=_dev(xin), ws=ws,
+                        cout=ih.chain_out(ih.EPI_RESID, x2, cq, op, ts if cq == F.Q4_K else None, norm_w=_dev(nw),
+                                          tile_ssq=ssq))
+        y = torch.zeros((M, 512), device="cuda")
+        ih.gemm_q_chain(cq, pc, 512, N, M, cin=ih.chain_in(op, ts if cq == F.Q4_K else None, 16, tile_ssq=ssq, eps=EPS),
+                        cout=ih.chain_out(ih.EPI_STORE, y))
+        yc = ih.gemm_q_ex(cq, pc, x, 512, N, act=ih.ACT_RMSNORM, norm_w=_dev(nw), eps=EPS, flags=FL)
+        torch.cuda.synchronize()
+        assert rel_l2(_h(y), _h(yc)) <= 1e-6, cq
+        assert rel_l2(_h(y), O.gemv_f64(cq, wc, _rms(xn, nw), M, 512, N)) <= 1e-5, cq
+    # EPI_STATS on the K-split matmul: the product and the operand of all its rows
+    y = torch.zeros((M, N), device="cuda")
+    op, ts, _ = ih.chain_buffers(N)
+    ih.gemm_q_chain(qt, pw, N, K, M, x=_dev(xin), ws=ws,
+                    cout=ih.chain_out(ih.EPI_STATS, y, F.Q4_K, op, ts, stat_rows=N))
+    torch.cuda.synchronize()
+    assert rel_l2(_h(y), ref) <= 1e-5
+    assert _sums_ok(_h(ts), _h(y), M, N // 16)
