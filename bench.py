@@ -224,18 +224,14 @@ class VerifyStep:
 
 class ChainStep(VerifyStep):
     """The verify step with chained matmuls (ihip_gemm_q_chain, gated model
-    weights): one input stage per step, that of the first [q; k; v]
-    (RMSNorm of the step's input rows). [q; k; v] writes o's operand (its q
-    rows, split fp16 at per-tile scales); o adds its product into the
-    residual and writes [gate; up]'s operand (the residual times the FFN norm
-    weight) with the tile sums of squares of the RMSNorm; [gate; up] writes
-    h = silu(gate) up and down's operand; down, split over K, sums its
-    slices per tile in the last slice to arrive, adds the result into the
-    residual and writes the next [q; k; v]'s operand (times the next
-    attention norm weight; the LM head's after the last layer, times the
-    output norm weight) with its tile sums of squares. Same arithmetic as
-    VerifyStep.forward (fp32-accurate, M <= 8), four input-stage launches
-    fewer per layer."""
+    weights): per layer one input stage, that of [q; k; v] (the previous
+    layer's down partials folded into the residual, RMSNorm). [q; k; v]
+    writes o's operand (its q rows, split fp16 at per-tile scales); o adds
+    its product into the residual and writes [gate; up]'s operand (the
+    residual times the FFN norm weight) with the tile sums of squares of the
+    RMSNorm; [gate; up] writes h = silu(gate) up and down's operand; down
+    leaves K-slice partials. Same arithmetic as VerifyStep.forward
+    (fp32-accurate, M <= 8), three input-stage launches fewer per layer."""
 
     def __init__(self, ih, model: Model, M: int, k: int, T: float):
         import torch
@@ -245,28 +241,19 @@ class ChainStep(VerifyStep):
         self.op_q, self.ts_q, _ = ih.chain_buffers(NQ)
         self.op_x, self.ts_x, self.ssq_x = ih.chain_buffers(H, ssq=True)
         self.op_h, _, _ = ih.chain_buffers(FF, tiles_per_unit=32)
-        self.op_d, self.ts_d, self.ssq_d = ih.chain_buffers(H, ssq=True)  # down -> the next [q; k; v] or the head
         super().__init__(ih, model, M, k, T, prec=1)
 
     def _descriptors(self):
         # (built at the first forward: VerifyStep's constructor runs one, after making x and qkv)
         ih, F = self.ih, self.ih.formats
         cin, cout = ih.chain_in, ih.chain_out
-        P = self.model.proj
         self.o_in = cin(self.op_q, self.ts_q, 16)
         self.gu_in = cin(self.op_x, self.ts_x, 16, tile_ssq=self.ssq_x, eps=1e-6)
         self.down_in = cin(self.op_h, None, 32)
-        self.qkv_in = cin(self.op_d, self.ts_d, 16, tile_ssq=self.ssq_d, eps=1e-6)
-        self.head_in = cin(self.op_d, None, 16, tile_ssq=self.ssq_d, eps=1e-6)
-        self.qkv_out = cout(ih.EPI_STATS, self.qkv, P, self.op_q, self.ts_q, stat_rows=NQ)
-        self.o_out = [cout(ih.EPI_RESID, self.x, P, self.op_x, self.ts_x, norm_w=lw["ffn_norm"],
+        self.qkv_out = cout(ih.EPI_STATS, self.qkv, F.Q4_K, self.op_q, self.ts_q, stat_rows=NQ)
+        self.o_out = [cout(ih.EPI_RESID, self.x, F.Q4_K, self.op_x, self.ts_x, norm_w=lw["ffn_norm"],
                            tile_ssq=self.ssq_x) for lw in self.model.layers]
         self.gu_out = cout(ih.EPI_GATE, self.h, F.Q6_K, self.op_h)
-        nxt = [lw["attn_norm"] for lw in self.model.layers[1:]] + [self.model.out_norm]
-        self.down_out = [cout(ih.EPI_RESID, self.x, P if i + 1 < len(nxt) else F.Q6_K, self.op_d,
-                              self.ts_d if i + 1 < len(nxt) else None, norm_w=w, tile_ssq=self.ssq_d)
-                         for i, w in enumerate(nxt)]
-        self.head_out = cout(ih.EPI_STORE, self.logits)
 
     def forward(self, probe=None):
         ih, F, M = self.ih, self.ih.formats, self.M
@@ -274,15 +261,14 @@ class ChainStep(VerifyStep):
             self._descriptors()
         P = self.model.proj
         chain = ih.gemm_q_chain
+        fl = ih.GEMM_F32 | ih.GEMM_PACKED
+        parts = ih.gemm_partials(F.Q6_K, M, H, FF, fl, self.ws_down)
         self.x.copy_(self.x0)
         for i, lw in enumerate(self.model.layers):
             if probe:
                 probe("pre", i)
-            if i == 0:  # the step's input rows: the one input stage
-                chain(P, lw["qkv"], NQ + 2 * NKV, H, M, x=self.x, act=ih.ACT_RMSNORM, norm_w=lw["attn_norm"],
-                      ws=self.ws, cout=self.qkv_out)
-            else:
-                chain(P, lw["qkv"], NQ + 2 * NKV, H, M, cin=self.qkv_in, ws=self.ws, cout=self.qkv_out)
+            chain(P, lw["qkv"], NQ + 2 * NKV, H, M, x=self.x, act=ih.ACT_RMSNORM, norm_w=lw["attn_norm"],
+                  add=parts if i > 0 else None, ws=self.ws, cout=self.qkv_out)
             if probe:
                 probe("qkv", i)
             chain(P, lw["o"], H, NQ, M, cin=self.o_in, ws=self.ws_o, cout=self.o_out[i])
@@ -291,10 +277,9 @@ class ChainStep(VerifyStep):
             chain(P, lw["gu"], 2 * FF, H, M, ws=self.ws, cin=self.gu_in, cout=self.gu_out)
             if probe:
                 probe("gu", i)
-            chain(F.Q6_K, lw["down"], H, FF, M, cin=self.down_in, ws=self.ws_down, cout=self.down_out[i])
-            if probe:
-                probe("down", i)
-        chain(F.Q6_K, self.model.lm, VOCAB, H, M, cin=self.head_in, ws=self.ws, cout=self.head_out)
+            chain(F.Q6_K, lw["down"], H, FF, M, cin=self.down_in, flags=fl | ih.GEMM_DEFER, ws=self.ws_down)
+        ih.gemm_q_ex(F.Q6_K, self.model.lm, self.x, VOCAB, H, act=ih.ACT_RMSNORM, norm_w=self.model.out_norm,
+                     flags=fl, out=self.logits, ws=self.ws, add=parts)
         if probe:
             probe("head", len(self.model.layers))
 

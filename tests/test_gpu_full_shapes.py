@@ -155,23 +155,32 @@ def _run_step_with_checks(ih, B, model, step, chk, fold_chk, prec_flags):
 
 def _run_chain_step_with_checks(ih, B, model, step, chk, fold_chk):
     """The chained composition (bench.ChainStep) checked operation by
-    operation: [q; k; v] on the RMSNorm'd residual and the tile sums of o's
-    operand, o's product added into the residual (x_new against x_old + the
-    oracle's o within fp32 rounding of the residual), h = silu(gate) up from
-    [gate; up] on the RMSNorm'd residual, down (split over K, its slices
-    summed per tile by the last to arrive) added into the residual the same
-    way, and the head on the final RMSNorm, whose input the last down wrote
-    as the head's operand."""
+    operation: [q; k; v] and the tile sums of o's operand, o's product added
+    into the residual (x_new against x_old + the oracle's o within fp32 rounding of
+    the residual), h = silu(gate) up from [gate; up] on the RMSNorm'd
+    residual, down's K-slice partials, the folds, the head."""
     import torch
     P, M = model.proj, step.M
     H, NQ, NKV, FF, V = B.H, B.NQ, B.NKV, B.FF, B.VOCAB
     hw = model.host_gguf
     st = {}
+    fl = ih.GEMM_F32 | ih.GEMM_PACKED
+
+    def down_check(i):
+        d = _partials_sum(ih, F.Q6_K, M, H, FF, fl, step.ws_down)
+        chk("down", d, O.gemv_f64(F.Q6_K, hw[i - 1]["down"], st["h"], M, H, FF))
+        return d
 
     def probe(tag, i):
         torch.cuda.synchronize()
         x = _h(step.x).astype(np.float64)
-        if tag == "qkv":
+        if tag == "pre":
+            st["x_pre"] = x
+            if i > 0:
+                st["down"] = down_check(i)
+        elif tag == "qkv":
+            if i > 0:
+                fold_chk("x += down", x, st["x_pre"] + st["down"])
             wq = np.concatenate([hw[i]["q"], hw[i]["kv"]])
             qkv = _h(step.qkv)
             chk("qkv", qkv, O.gemv_f64(P, wq, _rms(x, hw[i]["attn_norm"]), M, NQ + 2 * NKV, H))
@@ -189,15 +198,15 @@ def _run_chain_step_with_checks(ih, B, model, step, chk, fold_chk):
             st["h"] = _h(step.h)
             chk("h = silu(gate) up", st["h"], h_ref)
             st["x_gu"] = x
-        elif tag == "down":
-            fold_chk("x += down", x, st["x_gu"] + O.gemv_f64(F.Q6_K, hw[i]["down"], st["h"], M, H, FF))
         elif tag == "head":
+            d = down_check(i)
+            fold_chk("x += down", x, st["x_gu"] + d)
             chk("lm_head", _h(step.logits), O.gemv_f64(F.Q6_K, model.host_lm, _rms(x, model.host_out_norm), M, V, H))
             print(f"{chk.label}: every layer and the head checked", flush=True)
 
     step.forward(probe=probe)
     torch.cuda.synchronize()
-    # replayed: the same results (the per-tile slice counts return to zero after each call)
+    # replayed: the same bits
     logits = step.logits.clone()
     step.forward()
     torch.cuda.synchronize()
