@@ -1322,12 +1322,14 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, const uint8_t *__restrict__ af
     // DE: where the tiles' epilogue runs: 0 in the weight loop as each batch
     // of tiles completes (plain stores); 2 (a chained producer's) after the
     // loop, from the reduced tiles kept in LDS, with the loop's registers free
-    // (at most CHAIN_MAX_TILES per workgroup, which the host checks).
+    // (at most CHAIN_MAX_TILES per workgroup, which the host checks); 3 the
+    // same for a producer split over K (each tile finished by the last slice
+    // to arrive: a separate instantiation keeps DE 2's code unchanged).
     // Measured: plain stores after the loop are slower (the step 1.5 %): the
     // stores then all wait at the kernel's end.
-    static_assert(DE == 0 || DE == 2, "epilogue placement");
+    static_assert(DE == 0 || DE == 2 || DE == 3, "epilogue placement");
     static_assert((!XIN && DE == 0) || (SPLIT && MT == 1), "chained calls: fp32-accurate, one token tile");
-    constexpr bool CE = DE == 2;
+    constexpr bool CE = DE >= 2;
     constexpr int TOKT = SPLIT ? 8 : 16;  // tokens per MFMA tile
     constexpr int TOK = MT * TOKT;
     constexpr int TPL = SPLIT ? 2 : 4;
@@ -1557,7 +1559,7 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, const uint8_t *__restrict__ af
         // scales' barriers also publish pend)
         static_assert(CE, "after-loop epilogues are the chained producer's");
         rsc.finish(ssq, n_ssq, K, eps, tid, rsp, rs);
-        if (gridDim.y > 1) {
+        if constexpr (DE == 3) {
             // split over K: wave w stores its tiles' partial sums (this
             // slice's) and counts the slice in; the last slice to arrive at a
             // tile sums the slices in slice order (the same bits whichever
@@ -1986,11 +1988,17 @@ hipError_t launch_v(const uint8_t *W, const float *X, const ActIn &in, float *Y,
     const Chain c = chain != nullptr ? *chain : plain_chain(N);
     // (the chained calls' plans: 8 waves, or Q6_K's 4 waves of 3 units)
     if constexpr (SPLIT && MT == 1 && PK && (NW == 8 || (QT == QT_Q6_K && NW == 4 && UPS == 3))) {
+        if (c.epi != EPI_STORE && S > 1) {  // (a chained epilogue sums its own K-slices)
+            gemm_v_kernel<QT, NW, UPS, SPLIT, PK, MT, false, 3><<<dim3(G, S), NW * 64, 0, st>>>(
+                W, a.afrag, a.mfrag, a.inv, M, N, K, G, 0, 0, Y, accum, in.op == ACT_RMSNORM ? a.ssq : nullptr,
+                n_units, in.eps, part, c);
+            return hipGetLastError();
+        }
         if (c.epi != EPI_STORE) {
             gemm_v_kernel<QT, NW, UPS, SPLIT, PK, MT, false, 2><<<dim3(G, S), NW * 64, 0, st>>>(
                 W, a.afrag, a.mfrag, a.inv, M, N, K, G, 0, 0, Y, accum, in.op == ACT_RMSNORM ? a.ssq : nullptr,
-                n_units, in.eps, (S > 1 || in.defer) ? part : nullptr, c);
-            return hipGetLastError();  // (a chained epilogue sums its own K-slices)
+                n_units, in.eps, in.defer ? part : nullptr, c);
+            return hipGetLastError();
         }
     }
     gemm_v_kernel<QT, NW, UPS, SPLIT, PK, MT, false, 0><<<dim3(G, S), NW * 64, 0, st>>>(
@@ -2011,7 +2019,10 @@ hipError_t launch_vx(const uint8_t *W, float *Y, int M, int N, int K, int S, int
     // (the operand, its tile sums and their layout travel in the leading
     // arguments, which the hardware preloads into SGPRs)
     const uint8_t *xs = (const uint8_t *)ch.xsum;
-    if (ch.epi != EPI_STORE)
+    if (ch.epi != EPI_STORE && S > 1)  // (the last K-slice at a tile finishes it)
+        gemm_v_kernel<QT, NW, UPS, true, true, 1, true, 3><<<dim3(G, S), NW * 64, 0, st>>>(
+            W, ch.xop, xs, nullptr, M, N, K, G, ch.xsum_stride, ch.x_tiles_per_unit, Y, 0, ssq, n_ssq, eps, part, ch);
+    else if (ch.epi != EPI_STORE)
         gemm_v_kernel<QT, NW, UPS, true, true, 1, true, 2><<<dim3(G, S), NW * 64, 0, st>>>(
             W, ch.xop, xs, nullptr, M, N, K, G, ch.xsum_stride, ch.x_tiles_per_unit, Y, 0, ssq, n_ssq, eps,
             (S > 1 || defer) ? part : nullptr, ch);
