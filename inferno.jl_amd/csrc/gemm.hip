@@ -1785,7 +1785,9 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     constexpr int F = NW == 8 ? 2 : 4;
     constexpr int WPT = NW / F;  // waves per tile in a batch's reduction
     static_assert(R % F == 0, "a ring pass holds whole reduction batches");
-    __shared__ __align__(16) float red[2][F][NW][64][NVP];
+    // [batch half][tile][wave][value group][lane]: 16-byte lane stride, so
+    // the 64 lanes' 16-byte accesses of a value group hit distinct banks
+    __shared__ __align__(16) f4 red[2][F][NW][NVP / 4][64];
     __shared__ float rs[TOK];
     __shared__ float rsp[NW * 64];
 
@@ -1871,6 +1873,14 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(dst, (short)0, (int)out_bytes, 0x00020000);
     const int tb = lane_token<SPLIT>(0, g, 0);
     rsc.finish(ssq, n_units, K, eps, tid, rsp, rs);
+    // as many dropped stores (offset past the resource) as a flush issues,
+    // behind the ring's prologue loads: the main loop is entered with the
+    // same memory operations in flight as its back edge leaves, so the wait
+    // at its head lets the ring's later items stay in flight
+    constexpr int FLUSH_STORES = 4 * ((NVP / 4 + WPT - 1) / WPT);
+#pragma unroll
+    for (int i = 0; i < FLUSH_STORES; i++)
+        __builtin_amdgcn_raw_buffer_store_b32(0u, ors, (int)0x80000000u, 4 * i, 0);  // (distinct: kept)
 
     // flush (a batch is complete): wave i sums tile i of the batch in wave
     // order and stores it
@@ -1881,33 +1891,40 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
 #pragma unroll
         for (int k = NV; k < NVP; k++) vals[k] = 0.f;
         const int hb = (j / F) & 1;
-        float *slot = &red[hb][jb][wave][lane][0];
 #pragma unroll
-        for (int k = 0; k < NVP; k += 4) *(f4 *)(slot + k) = f4{vals[k], vals[k + 1], vals[k + 2], vals[k + 3]};
+        for (int k = 0; k < NVP; k += 4) red[hb][jb][wave][k / 4][lane] = f4{vals[k], vals[k + 1], vals[k + 2], vals[k + 3]};
         if (flush) {
             __syncthreads();
+            // Branch-free: every wave issues the same stores on every path
+            // (a wave without a tile or value group stores past the
+            // resource's end), so the wait counts the compiler places for
+            // the ring's next items count these stores exactly instead of
+            // draining the prefetched loads behind them.
             const int tl = wave / WPT, grp = wave % WPT;  // tile of the batch, first value group
-            if (tl <= jb) {
-                const int r = ((int)blockIdx.x + G * (j - jb + tl)) * 16 + n_in;
-                const uint32_t voff = r < N ? (uint32_t)(tb * N + r) * 4u : 0x80000000u;
+            const bool tok = tl <= jb;
+            const int tlc = tok ? tl : jb;
+            const int r = ((int)blockIdx.x + G * (j - jb + tlc)) * 16 + n_in;
+            const uint32_t voff = (tok && r < N) ? (uint32_t)(tb * N + r) * 4u : 0x80000000u;
+            constexpr int QG = NVP / 4, QPW = (QG + WPT - 1) / WPT;  // value groups, per wave
 #pragma unroll
-                for (int q = 0; q < NVP / 4; q++) {
-                    if (q % WPT != grp) continue;
-                    // all waves' slices first (one LDS wait), then the sum in wave order
-                    f4 pv[NW];
+            for (int i = 0; i < QPW; i++) {
+                const int q0 = grp + WPT * i;
+                const int q = q0 < QG ? q0 : QG - 1;
+                // all waves' slices first (one LDS wait), then the sum in wave order
+                f4 pv[NW];
 #pragma unroll
-                    for (int w = 0; w < NW; w++) pv[w] = *(const f4 *)&red[hb][tl][w][lane][4 * q];
-                    f4 sum = pv[0];
+                for (int w = 0; w < NW; w++) pv[w] = red[hb][tlc][w][q][lane];
+                f4 sum = pv[0];
 #pragma unroll
-                    for (int w = 1; w < NW; w++) sum += pv[w];
+                for (int w = 1; w < NW; w++) sum += pv[w];
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const int k = 4 * q + e;
-                        if (k >= NV) continue;
-                        const int tk = lane_token<SPLIT>(k / TPL, 0, k % TPL);
-                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum[e] * rs[tb + tk]),
-                                                              ors, (int)voff, tk * N * 4, 0);
-                    }
+                for (int e = 0; e < 4; e++) {
+                    const int k = min(4 * q + e, NV - 1);
+                    const bool kok = q0 < QG && 4 * q + e < NV;
+                    const int tk = lane_token<SPLIT>(k / TPL, 0, k % TPL);
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum[e] * rs[tb + tk]), ors,
+                                                          kok ? (int)voff : (int)0x80000000u,
+                                                          __builtin_amdgcn_readfirstlane(tk * N * 4), 0);
                 }
             }
         }
