@@ -1803,39 +1803,7 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     const size_t row_bytes = (size_t)(K / C::QK) * C::BB;
     const int tail_blk = (QT == QT_Q8_0 && (K % UNIT)) ? (K % UNIT) / 32 : 8;
 
-    // 1. this wave's A operand (MFMA lane layout: entry (chunk c, tile mt) at
-    //    (c MT + mt) 64 + lane); slots of padding tokens are zero, not fetched
-    AReg<QT> a[MT];
-    float inv[MT][TPL];
-    {
-        const uint8_t *src = afrag + (size_t)un * UNIT_A1 * MT;
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            if ((SPLIT ? (n_in >> 1) : n_in) + mt * TOKT < M) {
-                if constexpr (QT == QT_Q6_K) {
-#pragma unroll
-                    for (int c = 0; c < 16; c++) a[mt].f[c] = *(const h4 *)(src + ((c * MT + mt) * 64 + lane) * 8);
-                } else {
-#pragma unroll
-                    for (int c = 0; c < 8; c++) a[mt].f[c] = *(const h8 *)(src + ((c * MT + mt) * 64 + lane) * 16);
-                }
-                if constexpr (C::MINS) a[mt].mins = *(const h4 *)(mfrag + ((size_t)un * MT + mt) * 512 + lane * 8);
-            } else {
-                if constexpr (QT == QT_Q6_K) {
-#pragma unroll
-                    for (int c = 0; c < 16; c++) a[mt].f[c] = h4{};
-                } else {
-#pragma unroll
-                    for (int c = 0; c < 8; c++) a[mt].f[c] = h8{};
-                }
-                if constexpr (C::MINS) a[mt].mins = h4{};
-            }
-#pragma unroll
-            for (int k = 0; k < TPL; k++) inv[mt][k] = invs[(size_t)un * TOK + lane_token<SPLIT>(mt, g, k)];
-        }
-    }
-
-    // 2. weight stream over this workgroup's tiles; past the last tile the
+    // 1. weight stream over this workgroup's tiles; past the last tile the
     //    loads repeat it so every ring step issues one item
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(W), (short)0, (int)(PK ? (uint32_t)n_tiles * n_units * Packed<QT>::CHUNK : 0u),
@@ -1854,12 +1822,46 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
                           b);
         }
     };
+
+    // 2. loads in the order they are needed: the RMSNorm partial sums
+    //    (waited for before the loop, so issued first), the first weight
+    //    item, this wave's A operand chunk by chunk for all MT tiles (the MFMA
+    //    lane layout: entry (chunk c, tile mt) at (c MT + mt) 64 + lane, so
+    //    the first item's MFMAs start as their chunks land instead of after
+    //    the whole 256-element unit), the inverse unit scales, then the rest
+    //    of the ring. Padding tokens' slots are read too: the input stage
+    //    writes zero operands and unit scales for every token up to TOK.
     RowScales<TOK, NW * 64> rsc;
     rsc.issue(ssq, n_units, tid);
     __builtin_amdgcn_sched_barrier(0);
     Unit<QT> buf[R];
+    load_item(0, buf[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    AReg<QT> a[MT];
+    float inv[MT][TPL];
+    {
+        const uint8_t *src = afrag + (size_t)un * UNIT_A1 * MT;
+        if constexpr (QT == QT_Q6_K) {
 #pragma unroll
-    for (int p = 0; p < R - 1; p++) {
+            for (int c = 0; c < 16; c++)
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) a[mt].f[c] = *(const h4 *)(src + ((c * MT + mt) * 64 + lane) * 8);
+        } else {
+#pragma unroll
+            for (int c = 0; c < 8; c++)
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) a[mt].f[c] = *(const h8 *)(src + ((c * MT + mt) * 64 + lane) * 16);
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            if constexpr (C::MINS) a[mt].mins = *(const h4 *)(mfrag + ((size_t)un * MT + mt) * 512 + lane * 8);
+#pragma unroll
+            for (int k = 0; k < TPL; k++) inv[mt][k] = invs[(size_t)un * TOK + lane_token<SPLIT>(mt, g, k)];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 1; p < R - 1; p++) {
         load_item(p, buf[p]);
         __builtin_amdgcn_sched_barrier(0);  // ring slots fill in order
     }
@@ -1884,7 +1886,7 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
 
     // flush (a batch is complete): wave i sums tile i of the batch in wave
     // order and stores it
-    auto consume = [&](int j, int jb, bool flush, Unit<QT> &b) {
+    auto consume = [&](int j, int jb, bool flush, Unit<QT> &b) __attribute__((always_inline)) {
         if constexpr (!PK) finish_unit<QT>(b);
         float vals[NVP];
         unit_vals<QT, SPLIT, MT>(b, a, inv, g, live, *(float(*)[NV])vals);
@@ -1930,9 +1932,14 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
         }
     };
     // whole ring passes: every R-th item completes a batch at a fixed ring
-    // position (straight-line code); the last partial pass checks the end
+    // position (straight-line code); the last partial pass checks the end.
+    // With two waves per SIMD the first pass is peeled and the loop nested
+    // under it: its memory waits follow the prologue's order (the first
+    // item's MFMAs wait for the A operand chunk by chunk), and the loop is
+    // entered only from a pass that leaves the same operations in flight as
+    // its own back edge, so its waits stay exact.
     const int n_full = my_tiles - my_tiles % R;
-    for (int ib = 0; ib < n_full; ib += R) {
+    auto pass = [&](int ib) __attribute__((always_inline)) {
 #pragma unroll
         for (int p = 0; p < R; p++) {
             load_item(ib + p + R - 1, buf[(p + R - 1) % R]);
@@ -1942,6 +1949,14 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
             if constexpr (NW == 8) __builtin_amdgcn_sched_barrier(0);
             consume(ib + p, p % F, p % F == F - 1, buf[p]);
         }
+    };
+    if constexpr (NW == 8) {  // (one wave per SIMD: the copies would no longer be inlined)
+        if (n_full > 0) {
+            pass(0);
+            for (int ib = R; ib < n_full; ib += R) pass(ib);
+        }
+    } else {
+        for (int ib = 0; ib < n_full; ib += R) pass(ib);
     }
 #pragma unroll
     for (int p = 0; p < R - 1; p++)
