@@ -716,9 +716,11 @@ __global__ __launch_bounds__(32 * TPW) void prep_kernel(const float *__restrict_
     norm_weights(norm_w, op, k, K, wa, wb);
     float v[8];
     if (t < M && k < K) {
-        // the sum of the partial slices at column c of row t, in slice order
-        // (loads issued four slices at a time)
-        auto slices = [&](int64_t rs, int c, float (&sum)[8]) {
+        // the sum of the partial slices at column c of row t, in slice order:
+        // up to MAXS slices (of both columns when two are asked for) in one
+        // round of loads issued before any sum, more four at a time
+        constexpr int MAXS = 8;
+        auto slices_loop = [&](int64_t rs, int c, float (&sum)[8]) {
 #pragma unroll
             for (int e = 0; e < 8; e++) sum[e] = 0.f;
             for (int s0 = 0; s0 < n_add; s0 += 4) {
@@ -737,6 +739,40 @@ __global__ __launch_bounds__(32 * TPW) void prep_kernel(const float *__restrict_
                     for (int e = 0; e < 8; e++) sum[e] = s0 + j == 0 ? pv[e] : sum[e] + pv[e];
                 }
             }
+        };
+        auto issue = [&](int64_t rs, int c, auto &va, auto &vb) {
+            constexpr int NS = sizeof(va) / sizeof(va[0]);
+#pragma unroll
+            for (int j = 0; j < NS; j++) {
+                if (j < n_add) {
+                    const float *pa = add + (size_t)j * add_stride + (size_t)t * rs + c;
+                    va[j] = *(const float4 *)pa;
+                    vb[j] = *(const float4 *)(pa + 4);
+                }
+            }
+        };
+        auto fold = [&](const auto &va, const auto &vb, float (&sum)[8]) {
+            constexpr int NS = sizeof(va) / sizeof(va[0]);
+#pragma unroll
+            for (int e = 0; e < 8; e++) sum[e] = 0.f;  // (no slices: zero, as the loop gives)
+#pragma unroll
+            for (int j = 0; j < NS; j++) {
+                if (j < n_add) {
+                    const float pv[8] = {va[j].x, va[j].y, va[j].z, va[j].w, vb[j].x, vb[j].y, vb[j].z, vb[j].w};
+#pragma unroll
+                    for (int e = 0; e < 8; e++) sum[e] = j == 0 ? pv[e] : sum[e] + pv[e];
+                }
+            }
+        };
+        // one column's slices
+        auto slices = [&](int64_t rs, int c, float (&sum)[8]) {
+            if (n_add > MAXS) {
+                slices_loop(rs, c, sum);
+                return;
+            }
+            float4 va[MAXS], vb[MAXS];
+            issue(rs, c, va, vb);
+            fold(va, vb, sum);
         };
         float up[8];
         if (X != nullptr) {
@@ -760,6 +796,13 @@ __global__ __launch_bounds__(32 * TPW) void prep_kernel(const float *__restrict_
                 up[0] = c.x; up[1] = c.y; up[2] = c.z; up[3] = c.w;
                 up[4] = d.x; up[5] = d.y; up[6] = d.z; up[7] = d.w;
             }
+        } else if (op == ACT_SILU_MUL && n_add <= MAXS / 2) {
+            // gate and up columns' slices in one round
+            float4 va[MAXS / 2], vb[MAXS / 2], ua[MAXS / 2], ub[MAXS / 2];
+            issue(ldx, k, va, vb);
+            issue(ldx, K + k, ua, ub);
+            fold(va, vb, v);
+            fold(ua, ub, up);
         } else {
             slices(ldx, k, v);
             if (op == ACT_SILU_MUL) slices(ldx, K + k, up);
