@@ -1866,23 +1866,24 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
         }
     };
 
-    // 2. loads in the order they are needed: the RMSNorm partial sums
+    // 2. loads. With two waves per SIMD (PEEL: the first ring pass is peeled
+    //    below) in the order they are needed: the RMSNorm partial sums
     //    (waited for before the loop, so issued first), the first weight
-    //    item, this wave's A operand chunk by chunk for all MT tiles (the MFMA
-    //    lane layout: entry (chunk c, tile mt) at (c MT + mt) 64 + lane, so
-    //    the first item's MFMAs start as their chunks land instead of after
-    //    the whole 256-element unit), the inverse unit scales, then the rest
-    //    of the ring. Padding tokens' slots are read too: the input stage
-    //    writes zero operands and unit scales for every token up to TOK.
-    RowScales<TOK, NW * 64> rsc;
-    rsc.issue(ssq, n_units, tid);
-    __builtin_amdgcn_sched_barrier(0);
-    Unit<QT> buf[R];
-    load_item(0, buf[0]);
-    __builtin_amdgcn_sched_barrier(0);
+    //    item, this wave's A operand chunk by chunk for all MT tiles (the
+    //    MFMA lane layout: entry (chunk c, tile mt) at (c MT + mt) 64 + lane,
+    //    so the first item's MFMAs start as their chunks land instead of
+    //    after the whole 256-element unit), the inverse unit scales, then the
+    //    rest of the ring. Without the peeled pass the loop's head is entered
+    //    straight from here, so the A operand goes first and is complete
+    //    when the RMSNorm sums are (in-order completion): otherwise the
+    //    compiler's waits for the A registers inside the loop, merged over
+    //    both ways in, would drain the ring on every pass. Padding tokens'
+    //    slots are read too: the input stage writes zero operands and unit
+    //    scales for every token up to TOK.
+    constexpr bool PEEL = NW == 8;  // (one wave per SIMD: the copies would no longer be inlined)
     AReg<QT> a[MT];
     float inv[MT][TPL];
-    {
+    auto load_a = [&]() __attribute__((always_inline)) {
         const uint8_t *src = afrag + (size_t)un * UNIT_A1 * MT;
         if constexpr (QT == QT_Q6_K) {
 #pragma unroll
@@ -1901,8 +1902,48 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
 #pragma unroll
             for (int k = 0; k < TPL; k++) inv[mt][k] = invs[(size_t)un * TOK + lane_token<SPLIT>(mt, g, k)];
         }
+    };
+    RowScales<TOK, NW * 64> rsc;
+    Unit<QT> buf[R];
+    if constexpr (PEEL) {
+        rsc.issue(ssq, n_units, tid);
+        __builtin_amdgcn_sched_barrier(0);
+        load_item(0, buf[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        load_a();
+        __builtin_amdgcn_sched_barrier(0);
+    } else {
+        // (tile by tile; slots of padding tokens are zero, not fetched)
+        const uint8_t *src = afrag + (size_t)un * UNIT_A1 * MT;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            if ((SPLIT ? (n_in >> 1) : n_in) + mt * TOKT < M) {
+                if constexpr (QT == QT_Q6_K) {
+#pragma unroll
+                    for (int c = 0; c < 16; c++) a[mt].f[c] = *(const h4 *)(src + ((c * MT + mt) * 64 + lane) * 8);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 8; c++) a[mt].f[c] = *(const h8 *)(src + ((c * MT + mt) * 64 + lane) * 16);
+                }
+                if constexpr (C::MINS) a[mt].mins = *(const h4 *)(mfrag + ((size_t)un * MT + mt) * 512 + lane * 8);
+            } else {
+                if constexpr (QT == QT_Q6_K) {
+#pragma unroll
+                    for (int c = 0; c < 16; c++) a[mt].f[c] = h4{};
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 8; c++) a[mt].f[c] = h8{};
+                }
+                if constexpr (C::MINS) a[mt].mins = h4{};
+            }
+#pragma unroll
+            for (int k = 0; k < TPL; k++) inv[mt][k] = invs[(size_t)un * TOK + lane_token<SPLIT>(mt, g, k)];
+        }
+        rsc.issue(ssq, n_units, tid);
+        __builtin_amdgcn_sched_barrier(0);
+        load_item(0, buf[0]);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int p = 1; p < R - 1; p++) {
         load_item(p, buf[p]);
@@ -1993,13 +2034,19 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
             consume(ib + p, p % F, p % F == F - 1, buf[p]);
         }
     };
-    if constexpr (NW == 8) {  // (one wave per SIMD: the copies would no longer be inlined)
+    if constexpr (PEEL) {
         if (n_full > 0) {
             pass(0);
             for (int ib = R; ib < n_full; ib += R) pass(ib);
         }
     } else {
-        for (int ib = 0; ib < n_full; ib += R) pass(ib);
+        for (int ib = 0; ib < n_full; ib += R) {
+#pragma unroll
+            for (int p = 0; p < R; p++) {
+                load_item(ib + p + R - 1, buf[(p + R - 1) % R]);
+                consume(ib + p, p % F, p % F == F - 1, buf[p]);
+            }
+        }
     }
 #pragma unroll
     for (int p = 0; p < R - 1; p++)
