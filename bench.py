@@ -324,6 +324,40 @@ class TreeStep(VerifyStep):
             q._stream(None)))
 
 
+def accept_cost(ih, step, replays: int = 10):
+    """The accept launch of the timed step (ihip_spec_accept, M = 5 target
+    rows, k = 4 draft rows, V = 151936) timed alone, microseconds per call
+    (8 calls per replayed graph), on the step's own logits -- those of the
+    configured synthetic blocks, whose sd of ~260 makes every softmax
+    near one-hot, so nearly every draft is accepted -- and on spread rows of
+    the same shape (target ~ N(0, 4^2), draft = target + N(0, 1.5^2), drafts
+    drawn from the draft softmax), where most steps end in a residual draw
+    over the whole vocabulary; with the accepted-length histogram of 256
+    draws on the spread rows."""
+    import torch
+    st = ih.synth.stream_for
+    M, k, T = step.M, step.k, step.T
+    t_step = graph_launch_time(lambda i: step.accept(), 8, replays, 2)
+    tgt = ih.quantized_kernels.synth_gaussian(st(SEED, "spread_target"), M * VOCAB, 4.0).view(1, M, VOCAB)
+    drf = ih.quantized_kernels.synth_gaussian(st(SEED, "spread_draft"), k * VOCAB, 1.5,
+                                              add=tgt[0, :k].contiguous()).view(1, k, VOCAB)
+    g = torch.Generator(device="cpu").manual_seed(SEED + 21)
+    p = torch.softmax(drf[0].cpu().double() / T, -1)
+    draft = torch.multinomial(p, 1, generator=g).view(1, k).to(torch.int32).cuda()
+    out_tok, out_n = torch.zeros_like(step.out_tok), torch.zeros_like(step.out_n)
+    t_spread = graph_launch_time(lambda i: ih.spec_accept(tgt, drf, draft, T, step.u_acc, step.u_res, step.u_bonus,
+                                                          out_tok=out_tok, out_n=out_n, ws=step.acc_ws),
+                                 8, replays, 2)
+    n_draws = 256
+    drafts = torch.multinomial(p, n_draws, replacement=True, generator=g).t().contiguous().to(torch.int32).cuda()
+    ua = torch.rand((n_draws, k), generator=g).cuda()
+    ur, ub = torch.rand(n_draws, generator=g).cuda(), torch.rand(n_draws, generator=g).cuda()
+    _, n = ih.spec_accept(tgt.expand(n_draws, M, VOCAB).contiguous(), drf.expand(n_draws, k, VOCAB).contiguous(),
+                          drafts, T, ua, ur, ub)
+    hist = torch.bincount(n.cpu().long(), minlength=k + 1).tolist()
+    return round(t_step * 1e6, 2), round(t_spread * 1e6, 2), hist
+
+
 def graph_launch_time(launch, iters: int, replays: int, warm: int) -> float:
     """`iters` calls of launch(i) captured in one HIP graph on a side stream,
     replayed `warm` times untimed, then `replays` times with an event pair
@@ -1133,6 +1167,9 @@ def main():
 
     hist = step.accept_histogram()
     log(f"accepted lengths over 256 draws on the step's logits: {hist}")
+    acc_us, acc_us_spread, hist_spread = accept_cost(ih, step)
+    log(f"accept alone: {acc_us} us on the step's logits, {acc_us_spread} us on spread rows "
+        f"(accepted lengths there over 256 draws: {hist_spread})")
     t_op, alg = gemm_roofline(ih, model, args.layers, args.m)
     achieved = alg / t_op / 1e9
     peaks = read_peak(ih)
@@ -1185,7 +1222,11 @@ def main():
         },
         "accept": {"timed_step_accepted": int(step.out_n[0]),
                    "accepted_length_histogram_256_draws": hist,
-                   "draft_logits": "target + N(0, 1.5^2)"},
+                   "draft_logits": "target + N(0, 1.5^2)",
+                   "us_per_accept_step_logits": acc_us,
+                   "us_per_accept_spread_logits": acc_us_spread,
+                   "spread_logits": "target ~ N(0, 4^2), draft = target + N(0, 1.5^2), same M, k, V, T",
+                   "accepted_length_histogram_256_draws_spread": hist_spread},
         "cpu_baseline": cpu,
         "gemm_gbps_by_M": sweep,
     }
