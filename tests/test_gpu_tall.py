@@ -158,3 +158,40 @@ def test_fold_split_launch(ih, qt):
     assert torch.equal(ya, yb)
     n = np.stack([O.rmsnorm(r, 1e-6) for r in xb.cpu().numpy()]).astype(np.float32)
     assert rel_l2(ya.cpu().numpy(), O.gemv_f64(qt, w, n, M, N, K)) <= TOL_F32
+
+
+@pytest.mark.parametrize("M", [5, 24])  # one token tile (fp32-accurate), several (half)
+@pytest.mark.parametrize("n_add", [1, 3, 4, 5, 8, 9, 12])
+def test_fold_slice_counts(ih, M, n_add):
+    """The input stage folds any number of K-slice partials in slice order:
+    up to 8 slices in one round of loads (gate and up columns together for
+    the SiLU-gating input up to 4), more four at a time. A residual fold of
+    n_add [M x K] slices and a SiLU-gating input given only as n_add [M x 2K]
+    slices both equal the explicit left-to-right sum followed by the plain
+    call, bit for bit, at every count across those paths."""
+    import torch
+    N, K = 64, 512
+    qt = F.Q4_K
+    w = synth.matrix(qt, N, K, synth.stream_for(41, "foldcount"))
+    wp = ih.pack_weights(qt, _dev(w), N, K)
+    fl = ih.GEMM_PACKED
+    g = torch.Generator(device="cpu").manual_seed(100 * M + n_add)
+    sr = torch.randn(n_add, M, K, generator=g).cuda()
+    x0 = torch.randn(M, K, generator=g).cuda()
+    acc = sr[0].clone()
+    for i in range(1, n_add):
+        acc = acc + sr[i]
+    xa = x0.clone()
+    ya = ih.gemm_q_ex(qt, wp, xa, N, K, act=ih.ACT_RMSNORM, flags=fl, add=(sr.data_ptr(), n_add, M * K))
+    xb = x0 + acc
+    yb = ih.gemm_q_ex(qt, wp, xb.clone(), N, K, act=ih.ACT_RMSNORM, flags=fl)
+    assert torch.equal(xa, xb)
+    assert torch.equal(ya, yb)
+    sl = torch.randn(n_add, M, 2 * K, generator=g).cuda()
+    acc2 = sl[0].clone()
+    for i in range(1, n_add):
+        acc2 = acc2 + sl[i]
+    y1 = ih.gemm_q_ex(qt, wp, None, N, K, act=ih.ACT_SILU_MUL, flags=fl,
+                      add=(sl.data_ptr(), n_add, M * 2 * K), m=M, ldx=2 * K)
+    y2 = ih.gemm_q_ex(qt, wp, acc2.contiguous(), N, K, act=ih.ACT_SILU_MUL, flags=fl)
+    assert torch.equal(y1, y2)
