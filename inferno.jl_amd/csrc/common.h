@@ -89,3 +89,12 @@ __device__ __forceinline__ float wave_sum(float v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
     return v;
 }
+
+// Wait until this wave's vector memory operations have completed (gfx9
+// s_waitcnt encoding: vmcnt 0, expcnt and lgkmcnt left at their maxima, i.e.
+// not waited for). A device-scope (agent) atomic store has completed when it
+// has reached the device's coherence point, so a count published after this
+// wait cannot be seen before the data it counts. A workgroup-scope fence
+// emits no such wait on gfx950, and an agent-scope fence would also write
+// back the whole L2.
+__device__ __forceinline__ void wait_stores_done() { __builtin_amdgcn_s_waitcnt(0x0F70); }

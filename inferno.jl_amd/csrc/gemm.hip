@@ -1611,17 +1611,17 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, const uint8_t *__restrict__ af
             // completes it.
             // The partials and counts cross XCDs through device-scope
             // (agent) atomic stores, loads and adds, which the L2s keep
-            // coherent by themselves; the fences are workgroup-scope, i.e.
-            // only waits that order this wave's own accesses (an agent-scope
-            // fence would write back and invalidate the whole L2: measured
-            // 3x slower down projection).
+            // coherent by themselves; a wave waits for its partial's store
+            // to complete before it counts the slice in (an agent-scope
+            // fence would also write back and invalidate the whole L2:
+            // measured 3x slower down projection).
             const int S = (int)gridDim.y, sl = (int)blockIdx.y;
             for (int js = wave; js < my_tiles; js += NW) {
                 const int tile = (int)blockIdx.x + G * js;
                 uint64_t *pt = (uint64_t *)(ch.tile_part + (size_t)tile * S * 64) + lane;
                 __hip_atomic_store(pt + (size_t)sl * 64, __builtin_bit_cast(uint64_t, pend[js][lane]),
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // (the partial lands before the count)
+                wait_stores_done();  // (the partial lands before the count)
                 int old = 0;
                 if (lane == 0)
                     old = __hip_atomic_fetch_add(ch.tile_cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
