@@ -1794,15 +1794,17 @@ __host__ __device__ constexpr int tall_waves(int qt, bool split, int mt) {
     return (qt == QT_Q4_K || qt == QT_Q5_K || (qt == QT_Q6_K && !split) || (qt == QT_Q8_0 && mt <= 2)) ? 8 : 4;
 }
 
-// Several token tiles (M up to 32 fp32-accurate, 64 half): one wave per
-// SIMD, each wave holding one 256-element unit of the A operand for all MT
-// tiles in registers, so a dequantized weight fragment feeds MT MFMAs. A
-// workgroup covers 4 units (one K-slice, grid.y) of every G-th 16-row tile
-// (grid.x). Per tile the four waves' unit results meet in LDS; they are
-// gathered in batches of F = 4 tiles (double-buffered, one barrier per
-// batch) and wave i sums tile i of the batch in wave order, so every wave
-// does the same reduction work. Weight items stream through an 8-deep
-// register ring. Results go out with bounds-checked buffer stores (no
+// Several token tiles (M up to 32 fp32-accurate, 64 half): NW = 4 or 8
+// waves (one or two per SIMD, tall_waves), each holding one 256-element
+// unit of the A operand for all MT tiles in registers, so a dequantized
+// weight fragment feeds MT MFMAs. A workgroup covers NW units (one K-slice,
+// grid.y) of every G-th 16-row tile (grid.x). Per tile the waves' unit
+// results meet in LDS (value-group major, so a group's 64 lanes hit
+// distinct banks); they are gathered in batches of F tiles (4, or 2 with
+// two waves per SIMD; double-buffered, one barrier per batch) and summed in
+// wave order, the work spread evenly over the waves. Weight items stream
+// through a register ring (8, 4 or 2 deep by register budget). Results go
+// out with bounds-checked buffer stores, the same number on every path (no
 // branches, no read-modify-write in the loop): to the K-slice's partials
 // when part is set (the caller reduces or folds them), else to Y.
 template <int QT, bool SPLIT, bool PK, int MT, int NW>
@@ -1873,13 +1875,14 @@ void gemm_w_kernel(const uint8_t *__restrict__ W, float *__restrict__ Y, int M, 
     //    MFMA lane layout: entry (chunk c, tile mt) at (c MT + mt) 64 + lane,
     //    so the first item's MFMAs start as their chunks land instead of
     //    after the whole 256-element unit), the inverse unit scales, then the
-    //    rest of the ring. Without the peeled pass the loop's head is entered
-    //    straight from here, so the A operand goes first and is complete
-    //    when the RMSNorm sums are (in-order completion): otherwise the
-    //    compiler's waits for the A registers inside the loop, merged over
-    //    both ways in, would drain the ring on every pass. Padding tokens'
-    //    slots are read too: the input stage writes zero operands and unit
-    //    scales for every token up to TOK.
+    //    rest of the ring (padding tokens' slots are read too: the input
+    //    stage writes zero operands and unit scales for every token up to
+    //    TOK). Without the peeled pass the loop's head is entered straight
+    //    from here, so the A operand goes first, tile by tile, and is
+    //    complete when the RMSNorm sums are (in-order completion): the
+    //    need-ordered prologue there merged operand waits into every pass
+    //    and drained the ring (the 4-tile fp32-accurate Q6_K kernel, 25 %
+    //    slower).
     constexpr bool PEEL = NW == 8;  // (one wave per SIMD: the copies would no longer be inlined)
     AReg<QT> a[MT];
     float inv[MT][TPL];
