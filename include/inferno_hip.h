@@ -540,7 +540,8 @@ int ihip_synth_gaussian(uint64_t stream, int64_t n, float scale,
                         void *stream_handle);
 
 /* HBM read-bandwidth probe (measurement only): streams `bytes` (a multiple
- * of 16, src 16-byte aligned) with 16-byte loads, each of up to 2048
+ * of 16, src 16-byte aligned) with 16-byte non-temporal loads (the policy
+ * the matmuls read their weights with), each of up to 2048
  * workgroups XORing what it read into its own word of out_dev (2048
  * words), so the plain-read ceiling can be reported beside the vendor peak
  * for the matmul kernels whose bound is HBM. */
