@@ -86,7 +86,7 @@ __device__ __forceinline__ void xpose4(uint32_t &r0, uint32_t &r1, uint32_t &r2,
 }
 
 // Raw loads (issued early); finish_unit() applies the cross-lane transposes
-// right before use. u: first byte of the unit in this lane's row; nblk: Q8_0
+// (and the Q4_K byte order of k_frag) right before use. u: first byte of the unit in this lane's row; nblk: Q8_0
 // blocks present in the unit (a row tail with K % 256 != 0 has fewer than 8).
 template <int QT>
 __device__ __forceinline__ void load_unit(const uint8_t *__restrict__ u, int g, int nblk, Unit<QT> &r) {
@@ -134,7 +134,15 @@ __device__ __forceinline__ void load_unit(const uint8_t *__restrict__ u, int g, 
 
 template <int QT>
 __device__ __forceinline__ void finish_unit(Unit<QT> &r) {
-    if constexpr (QT == QT_Q6_K) {
+    if constexpr (QT == QT_Q4_K) {
+        // GGUF byte order to the order the decoder reads: bytes 1 and 2 of
+        // each quant dword swapped (the packer stores them so)
+        const uint32_t sel = 0x03010200u;
+        r.q0 = make_uint4(__builtin_amdgcn_perm(r.q0.x, r.q0.x, sel), __builtin_amdgcn_perm(r.q0.y, r.q0.y, sel),
+                          __builtin_amdgcn_perm(r.q0.z, r.q0.z, sel), __builtin_amdgcn_perm(r.q0.w, r.q0.w, sel));
+        r.q1 = make_uint4(__builtin_amdgcn_perm(r.q1.x, r.q1.x, sel), __builtin_amdgcn_perm(r.q1.y, r.q1.y, sel),
+                          __builtin_amdgcn_perm(r.q1.z, r.q1.z, sel), __builtin_amdgcn_perm(r.q1.w, r.q1.w, sel));
+    } else if constexpr (QT == QT_Q6_K) {
         xpose4(r.a[0], r.a[1], r.a[2], r.a[3]);
         xpose4(r.b[0], r.b[1], r.b[2], r.b[3]);
         xpose4(r.h[0], r.h[1], r.h[2], r.h[3]);
@@ -153,8 +161,9 @@ __device__ __forceinline__ void finish_unit(Unit<QT> &r) {
 // bytes with 16-byte loads at i * 1024 + 16 l plus per-row header loads. Every
 // load of a wave then covers whole cache lines, and no cross-lane transposes
 // remain. Byte map (row n of the tile, offsets into the GGUF block):
-//  Q4_K (2304 B): [1024 i + 16 l, +16) = qs[64 i + 16 g, +16) (i = 0, 1);
-//                 [2048 + 16 n, +16) = d, dmin, scales
+//  Q4_K (2304 B): [1024 i + 16 l, +16) = qs[64 i + 16 g, +16) (i = 0, 1)
+//                 with bytes 1 and 2 of each dword swapped (the order
+//                 k_frag decodes); [2048 + 16 n, +16) = d, dmin, scales
 //  Q5_K (2816 B): quants as Q4_K; [2048 + 16 (n + 16 h), +16) = qh[16 h, +16)
 //                 (h = 0, 1); [2560 + 16 n, +16) = d, dmin, scales
 //  Q6_K (3360 B): for i = 0..3, p = 64 (i>>1) + 16 (i&1) + 4 g:
@@ -268,7 +277,11 @@ __global__ __launch_bounds__(64) void pack_kernel(const uint8_t *__restrict__ W,
         for (int e = 0; e < nbytes; e++) dst[e] = ok ? s[e] : (uint8_t)0;
     };
     if constexpr (QT == QT_Q4_K) {
-        for (int i = 0; i < 2; i++) cp(ch + 1024 * i + 16 * l, src + 16 + 64 * i + 16 * g, 16, live);
+        for (int i = 0; i < 2; i++)
+            for (int e = 0; e < 16; e++) {
+                const int se = (e & 12) | ((e & 3) == 1 ? 2 : (e & 3) == 2 ? 1 : (e & 3));  // bytes 1, 2 swapped
+                ch[1024 * i + 16 * l + e] = live ? src[16 + 64 * i + 16 * g + se] : (uint8_t)0;
+            }
         if (g == 0) cp(ch + 2048 + 16 * n, src, 16, live);
     } else if constexpr (QT == QT_Q5_K) {
         for (int i = 0; i < 2; i++) cp(ch + 1024 * i + 16 * l, src + 48 + 64 * i + 16 * g, 16, live);
@@ -320,6 +333,90 @@ __device__ __forceinline__ h8 b_frag_scaled(uint32_t x0, uint32_t x1, h2 s, h2 n
     r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
     r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
     return r;
+}
+
+// Exact fp16 pair of v / 16 for a small non-negative integer v (< 1024):
+// 64 + v / 16 has ulp 1/16, so the subtraction rounds nothing.
+__device__ __forceinline__ h2 h2_of_small_16th(uint32_t v) {
+    const uint32_t b = 0x5400u | v;
+    return as_h2(b | (b << 16)) - as_h2(0x54005400u);
+}
+
+// Per-lane scales of a Q4_K/Q5_K unit (lane group g): hs[2 ah + b] is the
+// 6-bit scale sc of sub-block 4 ah + 2 (g >> 1) + b as an exact fp16 pair
+// (sc / 16 for the Q4_K high nibble plane, b = 1: see k_frag), ns = -1024 hs;
+// m_lo / m_hi hold the 6-bit mins of sub-blocks 0..3 / 4..7 as bytes.
+struct KScales { h2 hs[4], ns[4]; uint32_t m_lo, m_hi; };
+
+template <int QT>
+__device__ __forceinline__ KScales k_scales(const uint4 &hdr, int g) {
+    KScales k;
+    const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
+    const uint32_t sc_lo = s0 & 0x3f3f3f3fu;
+    const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
+    k.m_lo = s1 & 0x3f3f3f3fu;
+    k.m_hi = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
+    const int sh = 16 * (g >> 1);
+    k.hs[0] = h2_of_small((sc_lo >> sh) & 0xffu);
+    k.hs[2] = h2_of_small((sc_hi >> sh) & 0xffu);
+    if constexpr (QT == QT_Q4_K) {
+        k.hs[1] = h2_of_small_16th((sc_lo >> (sh + 8)) & 0xffu);
+        k.hs[3] = h2_of_small_16th((sc_hi >> (sh + 8)) & 0xffu);
+    } else {
+        k.hs[1] = h2_of_small((sc_lo >> (sh + 8)) & 0xffu);
+        k.hs[3] = h2_of_small((sc_hi >> (sh + 8)) & 0xffu);
+    }
+    const h2 neg1024 = as_h2(0xE400E400u);
+#pragma unroll
+    for (int i = 0; i < 4; i++) k.ns[i] = k.hs[i] * neg1024;
+    return k;
+}
+
+// B operand of MFMA m (0..7) of a Q4_K/Q5_K unit: from lane group g the 8
+// elements 128(m>>2) + 64(g>>1) + 32((m>>1)&1) + 16(g&1) + 8(m&1) + e of
+// sub-block 4(m>>2) + 2(g>>1) + ((m>>1)&1), i.e. the dwords 2(m&1), +1 of q0
+// (m < 4) or q1, low nibbles for even (m>>1), high for odd, as exact fp16
+// q * sc (fma(1024 + q, sc, -1024 sc) rounds nothing).
+//  Q4_K: each quant dword holds the bytes of elements (0, 2, 1, 3) (the
+//        packer and finish_unit swap bytes 1 and 2 of the GGUF dword), so a
+//        mask-and-or puts the nibbles of elements 0 and 1 of either plane
+//        under the fp16 exponent 0x6400, and the same after a shift by 8
+//        those of elements 2 and 3: 5 bit operations per dword for both
+//        planes instead of 7. The high plane sits at mantissa bits 4..7,
+//        1024 + 16 q, against the scale sc / 16 (and -64 sc): the same exact
+//        q * sc.
+//  Q5_K: GGUF byte order; the plane's nibbles with the qh bit as bit 4,
+//        widened to fp16 pairs by byte permutes.
+template <int QT>
+__device__ __forceinline__ h8 k_frag(const Unit<QT> &r, int m, int g, const KScales &k) {
+    const int ah = m >> 2, b = (m >> 1) & 1, hw = m & 1;
+    const uint4 Q = ah ? r.q1 : r.q0;
+    const uint32_t x0 = hw ? Q.z : Q.x, x1 = hw ? Q.w : Q.y;
+    const h2 s = k.hs[2 * ah + b], ns = k.ns[2 * ah + b];
+    if constexpr (QT == QT_Q4_K) {
+        // the exponent as a VGPR value: a VOP3 and-or has no literal slot and
+        // reads at most one SGPR (the mask), so with two constants it would
+        // split in two
+        const uint32_t mk = b ? 0x00f000f0u : 0x000f000fu;
+        uint32_t ex = 0x64006400u;
+        asm("" : "+v"(ex));
+        const h2 p0 = __builtin_elementwise_fma(as_h2((x0 & mk) | ex), s, ns);
+        const h2 p1 = __builtin_elementwise_fma(as_h2(((x0 >> 8) & mk) | ex), s, ns);
+        const h2 p2 = __builtin_elementwise_fma(as_h2((x1 & mk) | ex), s, ns);
+        const h2 p3 = __builtin_elementwise_fma(as_h2(((x1 >> 8) & mk) | ex), s, ns);
+        h8 f;
+        f[0] = p0[0]; f[1] = p0[1]; f[2] = p1[0]; f[3] = p1[1];
+        f[4] = p2[0]; f[5] = p2[1]; f[6] = p3[0]; f[7] = p3[1];
+        return f;
+    } else {
+        uint32_t n0 = (b ? (x0 >> 4) : x0) & 0x0f0f0f0fu;
+        uint32_t n1 = (b ? (x1 >> 4) : x1) & 0x0f0f0f0fu;
+        const int hb = 4 * ah + 2 * (g >> 1) + b;  // bit 2j + b of qh[l]
+        const uint32_t h0 = hw ? r.qh.z : r.qh.x, h1 = hw ? r.qh.w : r.qh.y;
+        n0 |= ((h0 >> hb) & 0x01010101u) << 4;
+        n1 |= ((h1 >> hb) & 0x01010101u) << 4;
+        return b_frag_scaled(n0, n1, s, ns);
+    }
 }
 
 template <int MT, bool SPLIT>
@@ -394,41 +491,16 @@ __device__ __forceinline__ void compute_unit(const Unit<QT> &r, const uint8_t *a
         for (int u = 0; u < TPL; u++) inv[mt][u] = i_lds[lane_token<SPLIT>(mt, g, u)];
 
     if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {
-        // MFMA m (0..7) of the unit takes from lane group g the 8 elements
-        //   128(m>>2) + 64(g>>1) + 32((m>>1)&1) + 16(g&1) + 8(m&1) + e,
-        // i.e. bytes 8(m&1).. of q0 (m < 4) or q1, low nibbles for even
-        // (m>>1), high nibbles for odd, of sub-block 4(m>>2) + 2(g>>1) + ((m>>1)&1).
+        // MFMA m (0..7) of the unit takes from lane group g the elements k_frag names
         const float d = half_bits(r.hdr.x), dmin = half_bits(r.hdr.x >> 16);
-        const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;
-        const uint32_t sc_lo = s0 & 0x3f3f3f3fu, m_lo = s1 & 0x3f3f3f3fu;
-        const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
-        const uint32_t m_hi = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
-        const int sh = 16 * (g >> 1);
-        const h2 neg1024 = as_h2(0xE400E400u);  // (-1024, -1024)
-        h2 hs[4], ns[4];
-        hs[0] = h2_of_small((sc_lo >> sh) & 0xffu);
-        hs[1] = h2_of_small((sc_lo >> (sh + 8)) & 0xffu);
-        hs[2] = h2_of_small((sc_hi >> sh) & 0xffu);
-        hs[3] = h2_of_small((sc_hi >> (sh + 8)) & 0xffu);
-#pragma unroll
-        for (int i = 0; i < 4; i++) ns[i] = hs[i] * neg1024;
+        const KScales ks = k_scales<QT>(r.hdr, g);
+        const uint32_t m_lo = ks.m_lo, m_hi = ks.m_hi;
         f4 c[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) c[mt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int m = 0; m < 8; m++) {
-            const int ah = m >> 2, b = (m >> 1) & 1, hw = m & 1;
-            const uint4 Q = ah ? r.q1 : r.q0;
-            const uint32_t x0 = hw ? Q.z : Q.x, x1 = hw ? Q.w : Q.y;
-            uint32_t n0 = (b ? (x0 >> 4) : x0) & 0x0f0f0f0fu;
-            uint32_t n1 = (b ? (x1 >> 4) : x1) & 0x0f0f0f0fu;
-            if constexpr (QT == QT_Q5_K) {
-                const int hb = 4 * ah + 2 * (g >> 1) + b;  // bit 2j + b of qh[l]
-                const uint32_t h0 = hw ? r.qh.z : r.qh.x, h1 = hw ? r.qh.w : r.qh.y;
-                n0 |= ((h0 >> hb) & 0x01010101u) << 4;
-                n1 |= ((h1 >> hb) & 0x01010101u) << 4;
-            }
-            const h8 bf = b_frag_scaled(n0, n1, hs[2 * ah + b], ns[2 * ah + b]);
+            const h8 bf = k_frag<QT>(r, m, g, ks);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++)
                 c[mt] = mfma32(*(const h8 *)(a_lane + (m * MT + mt) * 1024), bf, c[mt]);
@@ -1029,36 +1101,15 @@ __device__ __forceinline__ void compute_v(const Unit<QT> &r, const AReg<QT> (&a)
     if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {
         float d = half_bits(r.hdr.x), dmin = half_bits(r.hdr.x >> 16);
         if (!live) { d = 0.f; dmin = 0.f; }
-        const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;
-        const uint32_t sc_lo = s0 & 0x3f3f3f3fu, m_lo = s1 & 0x3f3f3f3fu;
-        const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
-        const uint32_t m_hi = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
-        const int sh = 16 * (g >> 1);
-        const h2 neg1024 = as_h2(0xE400E400u);
-        h2 hs[4], ns[4];
-        hs[0] = h2_of_small((sc_lo >> sh) & 0xffu);
-        hs[1] = h2_of_small((sc_lo >> (sh + 8)) & 0xffu);
-        hs[2] = h2_of_small((sc_hi >> sh) & 0xffu);
-        hs[3] = h2_of_small((sc_hi >> (sh + 8)) & 0xffu);
-#pragma unroll
-        for (int i = 0; i < 4; i++) ns[i] = hs[i] * neg1024;
+        const KScales ks = k_scales<QT>(r.hdr, g);
+        const uint32_t m_lo = ks.m_lo, m_hi = ks.m_hi;
+        const h2 neg1024 = as_h2(0xE400E400u);  // (-1024, -1024)
         f4 c[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) c[mt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int m = 0; m < 8; m++) {
-            const int ah = m >> 2, b = (m >> 1) & 1, hw = m & 1;
-            const uint4 Q = ah ? r.q1 : r.q0;
-            const uint32_t x0 = hw ? Q.z : Q.x, x1 = hw ? Q.w : Q.y;
-            uint32_t n0 = (b ? (x0 >> 4) : x0) & 0x0f0f0f0fu;
-            uint32_t n1 = (b ? (x1 >> 4) : x1) & 0x0f0f0f0fu;
-            if constexpr (QT == QT_Q5_K) {
-                const int hb = 4 * ah + 2 * (g >> 1) + b;
-                const uint32_t h0 = hw ? r.qh.z : r.qh.x, h1 = hw ? r.qh.w : r.qh.y;
-                n0 |= ((h0 >> hb) & 0x01010101u) << 4;
-                n1 |= ((h1 >> hb) & 0x01010101u) << 4;
-            }
-            const h8 bf = b_frag_scaled(n0, n1, hs[2 * ah + b], ns[2 * ah + b]);
+            const h8 bf = k_frag<QT>(r, m, g, ks);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) c[mt] = mfma32(a[mt].f[m], bf, c[mt]);
         }
@@ -1716,36 +1767,15 @@ __device__ __forceinline__ void unit_vals(const Unit<QT> &r, const AReg<QT> (&a)
     } else if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {
         float d = half_bits(r.hdr.x), dmin = half_bits(r.hdr.x >> 16);
         if (!live) { d = 0.f; dmin = 0.f; }
-        const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;
-        const uint32_t sc_lo = s0 & 0x3f3f3f3fu, m_lo = s1 & 0x3f3f3f3fu;
-        const uint32_t sc_hi = (s2 & 0x0f0f0f0fu) | (((s0 >> 6) & 0x03030303u) << 4);
-        const uint32_t m_hi = ((s2 >> 4) & 0x0f0f0f0fu) | (((s1 >> 6) & 0x03030303u) << 4);
-        const int sh = 16 * (g >> 1);
-        const h2 neg1024 = as_h2(0xE400E400u);
-        h2 hs[4], ns[4];
-        hs[0] = h2_of_small((sc_lo >> sh) & 0xffu);
-        hs[1] = h2_of_small((sc_lo >> (sh + 8)) & 0xffu);
-        hs[2] = h2_of_small((sc_hi >> sh) & 0xffu);
-        hs[3] = h2_of_small((sc_hi >> (sh + 8)) & 0xffu);
-#pragma unroll
-        for (int i = 0; i < 4; i++) ns[i] = hs[i] * neg1024;
+        const KScales ks = k_scales<QT>(r.hdr, g);
+        const uint32_t m_lo = ks.m_lo, m_hi = ks.m_hi;
+        const h2 neg1024 = as_h2(0xE400E400u);  // (-1024, -1024)
         f4 c[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) c[mt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int m = 0; m < 8; m++) {
-            const int ah = m >> 2, b = (m >> 1) & 1, hw = m & 1;
-            const uint4 Q = ah ? r.q1 : r.q0;
-            const uint32_t x0 = hw ? Q.z : Q.x, x1 = hw ? Q.w : Q.y;
-            uint32_t n0 = (b ? (x0 >> 4) : x0) & 0x0f0f0f0fu;
-            uint32_t n1 = (b ? (x1 >> 4) : x1) & 0x0f0f0f0fu;
-            if constexpr (QT == QT_Q5_K) {
-                const int hb = 4 * ah + 2 * (g >> 1) + b;
-                const uint32_t h0 = hw ? r.qh.z : r.qh.x, h1 = hw ? r.qh.w : r.qh.y;
-                n0 |= ((h0 >> hb) & 0x01010101u) << 4;
-                n1 |= ((h1 >> hb) & 0x01010101u) << 4;
-            }
-            const h8 bf = b_frag_scaled(n0, n1, hs[2 * ah + b], ns[2 * ah + b]);
+            const h8 bf = k_frag<QT>(r, m, g, ks);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) c[mt] = mfma32(a[mt].f[m], bf, c[mt]);
         }

@@ -27,8 +27,9 @@ def pack_ref(qt, w, N, K):
                 n, g = l & 15, l >> 4
                 src = rows[16 * t + n, u * UB:(u + 1) * UB]
                 if qt == F.Q4_K:
-                    for i in range(2):
-                        ch[1024 * i + 16 * l:1024 * i + 16 * l + 16] = src[16 + 64 * i + 16 * g:32 + 64 * i + 16 * g]
+                    for i in range(2):  # bytes 1 and 2 of each quant dword swapped
+                        q = src[16 + 64 * i + 16 * g:32 + 64 * i + 16 * g].reshape(4, 4)[:, [0, 2, 1, 3]]
+                        ch[1024 * i + 16 * l:1024 * i + 16 * l + 16] = q.reshape(16)
                     if g == 0:
                         ch[2048 + 16 * n:2064 + 16 * n] = src[:16]
                 elif qt == F.Q5_K:
