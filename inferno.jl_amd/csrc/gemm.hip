@@ -58,14 +58,15 @@ template <int QT> struct GemmCfg {
 // needs, fetched with 16-byte loads.
 //  Q4_K: header (d, dmin, scales) and quants qs[16g, +16), qs[64 + 16g, +16)
 //  Q5_K: as Q4_K plus high bits qh[16(g&1), +16)
-//  Q6_K: after a 4x4 transpose across lane groups, a/b/h[i] hold the dwords
+//  Q6_K: after a 4x4 transpose across lane groups, a/b/c[i] hold the dwords
 //        ql[64n + 16h + 4g], ql[64n + 32 + 16h + 4g], qh[32n + 16h + 4g]
-//        for i = 2n + h; sc all 16 scales; d the fp16 super-scale
+//        for i = 2n + h, which finish_unit regroups to the decoder's words
+//        (q6_regroup); sc all 16 scales; d the fp16 super-scale
 //  Q8_0: w0/w1[b] hold qs dwords g and 4 + g of block b (transposed), d[b]
 template <int QT> struct Unit;
 template <> struct Unit<QT_Q4_K> { uint4 hdr, q0, q1; };
 template <> struct Unit<QT_Q5_K> { uint4 hdr, q0, q1, qh; };
-template <> struct Unit<QT_Q6_K> { uint32_t a[4], b[4], h[4]; uint4 sc; uint32_t d; };
+template <> struct Unit<QT_Q6_K> { uint32_t a[4], b[4], c[4]; uint4 sc; uint32_t d; };
 template <> struct Unit<QT_Q8_0> { uint32_t d[8], w0[8], w1[8]; };
 
 __device__ __forceinline__ uint4 ld_u128(const uint8_t *p) {
@@ -83,6 +84,58 @@ __device__ __forceinline__ void xpose4(uint32_t &r0, uint32_t &r1, uint32_t &r2,
     const auto c = __builtin_amdgcn_permlane16_swap(r0, r1, false, false);
     const auto d = __builtin_amdgcn_permlane16_swap(r2, r3, false, false);
     r0 = c[0]; r1 = c[1]; r2 = d[0]; r3 = d[1];
+}
+
+// Q6_K words of one lane and group, from GGUF order (a, b = ql dwords
+// ql[p, +4), ql[p + 32, +4), h = the qh dword qh[p', +4) of the same four
+// elements j: byte j of each) to the order q6_pairs decodes. Pair 2 qq + t
+// is elements 2t, 2t + 1 of sub-block qq (the 6-bit value of element j of
+// sub-block qq is nibble qq>>1 of byte j of a (qq even) or b, with bits
+// 2qq, 2qq + 1 of byte j of h above it), at bits o..o+5 (element 2t) and
+// 16+o..21+o (element 2t + 1) of one word:
+//   A: pair 0 at o = 0, pair 1 at o = 6, the low nibbles of pair 6 at o = 12
+//   B: pair 2 at 0, pair 3 at 6, the low nibbles of pair 7 at 12
+//   C: pair 4 at 0, the high 2 bits of pair 6 at 6 and of pair 7 at 8,
+//      pair 5 at 10
+// The same bits, rearranged (the packer stores them so; the GGUF-layout
+// loader regroups after its transposes).
+__host__ __device__ inline void q6_regroup(uint32_t a, uint32_t b, uint32_t h, uint32_t &A, uint32_t &B,
+                                           uint32_t &C) {
+    const uint32_t q0 = (a & 0x0f0f0f0fu) | ((h & 0x03030303u) << 4);  // (one 6-bit value a byte)
+    const uint32_t q1 = (b & 0x0f0f0f0fu) | (((h >> 2) & 0x03030303u) << 4);
+    const uint32_t q2 = ((a >> 4) & 0x0f0f0f0fu) | (((h >> 4) & 0x03030303u) << 4);
+    const uint32_t q3 = ((b >> 4) & 0x0f0f0f0fu) | (((h >> 6) & 0x03030303u) << 4);
+    // pair t of a byte word: bytes 2t, 2t + 1 at bits 0 and 16
+    auto pr = [](uint32_t q, int t) {
+        return t ? ((q >> 16) & 0xffu) | ((q >> 8) & 0xff0000u) : (q & 0xffu) | ((q << 8) & 0xff0000u);
+    };
+    A = pr(q0, 0) | (pr(q0, 1) << 6) | ((pr(q3, 0) & 0x000f000fu) << 12);
+    B = pr(q1, 0) | (pr(q1, 1) << 6) | ((pr(q3, 1) & 0x000f000fu) << 12);
+    C = pr(q2, 0) | (((pr(q3, 0) >> 4) & 0x00030003u) << 6) | (((pr(q3, 1) >> 4) & 0x00030003u) << 8) |
+        (pr(q2, 1) << 10);
+}
+
+// The eight weight pairs q - 32 (exact fp16) of one group's words A, B, C
+// (q6_regroup's order): a mask-and-or puts a 6-bit field at bits 0..5 under
+// the fp16 exponent 0x6400 (1024 + q, pairs 0-5, one shift first for a field
+// above bit 0); for pairs 6 and 7 one byte permute puts the low nibbles at
+// bits 4..7 and the high bits at 8..9 (1024 + 16 q), another mask-and-or
+// keeps those. 14 bit operations for 8 pairs (GGUF order: 29).
+__device__ __forceinline__ void q6_pairs(uint32_t A, uint32_t B, uint32_t C, h2 (&p)[8]) {
+    uint32_t ex = 0x64006400u;
+    asm("" : "+v"(ex));  // (a VGPR: see k_frag)
+    const uint32_t m6 = 0x003f003fu, m46 = 0x03f003f0u;
+    const h2 off = as_h2(0xE420E420u);                                  // (1024 + q) - 1056
+    const h2 s16 = as_h2(0x2C002C00u), off16 = as_h2(0xD600D600u);      // (1024 + 16 q) / 16 - 96
+    p[0] = as_h2((A & m6) | ex) + off;
+    p[1] = as_h2(((A >> 6) & m6) | ex) + off;
+    p[2] = as_h2((B & m6) | ex) + off;
+    p[3] = as_h2(((B >> 6) & m6) | ex) + off;
+    p[4] = as_h2((C & m6) | ex) + off;
+    p[5] = as_h2(((C >> 10) & m6) | ex) + off;
+    // bytes (A1, C'1, A3, C'3) with C' = C << 2, and (B1, C1, B3, C3)
+    p[6] = __builtin_elementwise_fma(as_h2((__builtin_amdgcn_perm(A, C << 2, 0x03070105u) & m46) | ex), s16, off16);
+    p[7] = __builtin_elementwise_fma(as_h2((__builtin_amdgcn_perm(B, C, 0x03070105u) & m46) | ex), s16, off16);
 }
 
 // Raw loads (issued early); finish_unit() applies the cross-lane transposes
@@ -107,7 +160,7 @@ __device__ __forceinline__ void load_unit(const uint8_t *__restrict__ u, int g, 
         const uint4 H = ld_u128(u + 128 + 32 * n + 16 * h);
         r.a[0] = A.x; r.a[1] = A.y; r.a[2] = A.z; r.a[3] = A.w;
         r.b[0] = B.x; r.b[1] = B.y; r.b[2] = B.z; r.b[3] = B.w;
-        r.h[0] = H.x; r.h[1] = H.y; r.h[2] = H.z; r.h[3] = H.w;
+        r.c[0] = H.x; r.c[1] = H.y; r.c[2] = H.z; r.c[3] = H.w;
         r.sc = ld_u128(u + 192);
         r.d = ld_u16(u + 208);
     } else {
@@ -145,7 +198,9 @@ __device__ __forceinline__ void finish_unit(Unit<QT> &r) {
     } else if constexpr (QT == QT_Q6_K) {
         xpose4(r.a[0], r.a[1], r.a[2], r.a[3]);
         xpose4(r.b[0], r.b[1], r.b[2], r.b[3]);
-        xpose4(r.h[0], r.h[1], r.h[2], r.h[3]);
+        xpose4(r.c[0], r.c[1], r.c[2], r.c[3]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) q6_regroup(r.a[i], r.b[i], r.c[i], r.a[i], r.b[i], r.c[i]);
     } else if constexpr (QT == QT_Q8_0) {
         // before: (w0[2k], w1[2k], w0[2k+1], w1[2k+1]) = dwords 0..3 of this
         // lane group's half-block; after: dword g of each of the 4 halves
@@ -166,11 +221,11 @@ __device__ __forceinline__ void finish_unit(Unit<QT> &r) {
 //                 k_frag decodes); [2048 + 16 n, +16) = d, dmin, scales
 //  Q5_K (2816 B): quants as Q4_K; [2048 + 16 (n + 16 h), +16) = qh[16 h, +16)
 //                 (h = 0, 1); [2560 + 16 n, +16) = d, dmin, scales
-//  Q6_K (3360 B): for i = 0..3, p = 64 (i>>1) + 16 (i&1) + 4 g:
-//                 [16 l + 4 i, +4) = ql[p, +4); [1024 + 16 l + 4 i, +4) =
-//                 ql[p + 32, +4); [2048 + 16 l + 4 i, +4) = qh[32 (i>>1) +
-//                 16 (i&1) + 4 g, +4); [3072 + 16 n, +16) = scales;
-//                 [3328 + 2 n, +2) = d
+//  Q6_K (3360 B): for i = 0..3, p = 64 (i>>1) + 16 (i&1) + 4 g, the
+//                 dwords ql[p, +4), ql[p + 32, +4), qh[32 (i>>1) + 16 (i&1)
+//                 + 4 g, +4) regrouped (q6_regroup) to words A, B, C at
+//                 [16 l + 4 i], [1024 + 16 l + 4 i], [2048 + 16 l + 4 i];
+//                 [3072 + 16 n, +16) = scales; [3328 + 2 n, +2) = d
 //  Q8_0 (4352 B): [1024 i + 16 l + 8 j + 4 h, +4) = qs dword (g + 4 h) of
 //                 block 2 i + j (i = 0..3; j, h = 0, 1); [4096 + 16 n + 2 b,
 //                 +2) = d of block b
@@ -198,7 +253,7 @@ __device__ __forceinline__ void load_unit_packed(const uint8_t *__restrict__ ch,
         const uint4 H = *(const uint4 *)(ch + 2048 + 16 * lane);
         r.a[0] = A.x; r.a[1] = A.y; r.a[2] = A.z; r.a[3] = A.w;
         r.b[0] = B.x; r.b[1] = B.y; r.b[2] = B.z; r.b[3] = B.w;
-        r.h[0] = H.x; r.h[1] = H.y; r.h[2] = H.z; r.h[3] = H.w;
+        r.c[0] = H.x; r.c[1] = H.y; r.c[2] = H.z; r.c[3] = H.w;
         r.sc = *(const uint4 *)(ch + 3072 + 16 * n);
         r.d = ld_u16(ch + 3328 + 2 * n);
     } else {
@@ -241,7 +296,7 @@ __device__ __forceinline__ void load_unit_buf(__amdgpu_buffer_rsrc_t rs, int sof
         const uint4 H = bload16(rs, l16 + 2048, soff);
         r.a[0] = A.x; r.a[1] = A.y; r.a[2] = A.z; r.a[3] = A.w;
         r.b[0] = B.x; r.b[1] = B.y; r.b[2] = B.z; r.b[3] = B.w;
-        r.h[0] = H.x; r.h[1] = H.y; r.h[2] = H.z; r.h[3] = H.w;
+        r.c[0] = H.x; r.c[1] = H.y; r.c[2] = H.z; r.c[3] = H.w;
         r.sc = bload16(rs, n16 + 3072, soff);
         r.d = __builtin_amdgcn_raw_buffer_load_b16(rs, 3328 + 2 * n, soff, 0);
     } else {
@@ -288,11 +343,16 @@ __global__ __launch_bounds__(64) void pack_kernel(const uint8_t *__restrict__ W,
         if (g < 2) cp(ch + 2048 + 16 * (n + 16 * g), src + 16 + 16 * g, 16, live);
         if (g == 0) cp(ch + 2560 + 16 * n, src, 16, live);
     } else if constexpr (QT == QT_Q6_K) {
+        auto dw = [&](const uint8_t *s) {  // (little-endian; rows are not 4-byte aligned)
+            return live ? (uint32_t)s[0] | ((uint32_t)s[1] << 8) | ((uint32_t)s[2] << 16) | ((uint32_t)s[3] << 24) : 0u;
+        };
         for (int i = 0; i < 4; i++) {
             const int p = 64 * (i >> 1) + 16 * (i & 1) + 4 * g;
-            cp(ch + 16 * l + 4 * i, src + p, 4, live);
-            cp(ch + 1024 + 16 * l + 4 * i, src + p + 32, 4, live);
-            cp(ch + 2048 + 16 * l + 4 * i, src + 128 + 32 * (i >> 1) + 16 * (i & 1) + 4 * g, 4, live);
+            uint32_t w[3];
+            q6_regroup(dw(src + p), dw(src + p + 32), dw(src + 128 + 32 * (i >> 1) + 16 * (i & 1) + 4 * g), w[0], w[1],
+                       w[2]);
+            for (int k = 0; k < 3; k++)
+                for (int e = 0; e < 4; e++) ch[1024 * k + 16 * l + 4 * i + e] = (uint8_t)(w[k] >> (8 * e));
         }
         if (g == 0) {
             cp(ch + 3072 + 16 * n, src + 192, 16, live);
@@ -535,19 +595,15 @@ __device__ __forceinline__ void compute_unit(const Unit<QT> &r, const uint8_t *a
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int u = 0; u < TPL; u++) dinv[mt][u] = d * inv[mt][u];
-        const h2 off = as_h2(0xE420E420u);  // (-1056, -1056): (1024 + q) - 1056 = q - 32
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int n = i >> 1, h = i & 1;
-            uint32_t q[4];
-            q[0] = (r.a[i] & 0x0f0f0f0fu) | ((r.h[i] & 0x03030303u) << 4);
-            q[1] = (r.b[i] & 0x0f0f0f0fu) | (((r.h[i] >> 2) & 0x03030303u) << 4);
-            q[2] = ((r.a[i] >> 4) & 0x0f0f0f0fu) | (((r.h[i] >> 4) & 0x03030303u) << 4);
-            q[3] = ((r.b[i] >> 4) & 0x0f0f0f0fu) | (((r.h[i] >> 6) & 0x03030303u) << 4);
+            h2 p[8];
+            q6_pairs(r.a[i], r.b[i], r.c[i], p);
 #pragma unroll
             for (int qq = 0; qq < 4; qq++) {
                 const int s = 8 * n + 2 * qq + h;  // sub-block = chunk of 16
-                const h2 p0 = as_h2(pair_lo(q[qq])) + off, p1 = as_h2(pair_hi(q[qq])) + off;
+                const h2 p0 = p[2 * qq], p1 = p[2 * qq + 1];
                 h4 b;
                 b[0] = p0[0]; b[1] = p0[1]; b[2] = p1[0]; b[3] = p1[1];
                 const uint32_t scw = (s >> 2) == 0 ? r.sc.x : (s >> 2) == 1 ? r.sc.y : (s >> 2) == 2 ? r.sc.z : r.sc.w;
@@ -1134,19 +1190,15 @@ __device__ __forceinline__ void compute_v(const Unit<QT> &r, const AReg<QT> (&a)
         f4 sacc[MT];  // sum over sub-blocks of sc_s * (q . x)_s, per tile
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) sacc[mt] = f4{0.f, 0.f, 0.f, 0.f};
-        const h2 off = as_h2(0xE420E420u);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int n = i >> 1, h = i & 1;
-            uint32_t q[4];
-            q[0] = (r.a[i] & 0x0f0f0f0fu) | ((r.h[i] & 0x03030303u) << 4);
-            q[1] = (r.b[i] & 0x0f0f0f0fu) | (((r.h[i] >> 2) & 0x03030303u) << 4);
-            q[2] = ((r.a[i] >> 4) & 0x0f0f0f0fu) | (((r.h[i] >> 4) & 0x03030303u) << 4);
-            q[3] = ((r.b[i] >> 4) & 0x0f0f0f0fu) | (((r.h[i] >> 6) & 0x03030303u) << 4);
+            h2 p[8];
+            q6_pairs(r.a[i], r.b[i], r.c[i], p);
 #pragma unroll
             for (int qq = 0; qq < 4; qq++) {
                 const int sb = 8 * n + 2 * qq + h;
-                const h2 p0 = as_h2(pair_lo(q[qq])) + off, p1 = as_h2(pair_hi(q[qq])) + off;
+                const h2 p0 = p[2 * qq], p1 = p[2 * qq + 1];
                 h4 b;
                 b[0] = p0[0]; b[1] = p0[1]; b[2] = p1[0]; b[3] = p1[1];
                 const uint32_t scw = (sb >> 2) == 0 ? r.sc.x : (sb >> 2) == 1 ? r.sc.y : (sb >> 2) == 2 ? r.sc.z : r.sc.w;
@@ -1739,21 +1791,17 @@ __device__ __forceinline__ void unit_vals(const Unit<QT> &r, const AReg<QT> (&a)
         f4 c[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) c[mt] = f4{0.f, 0.f, 0.f, 0.f};
-        const h2 off = as_h2(0xE420E420u);  // (1024 + q) - 1056 = q - 32
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int n = i >> 1, h = i & 1;
-            uint32_t q[4];
-            q[0] = (r.a[i] & 0x0f0f0f0fu) | ((r.h[i] & 0x03030303u) << 4);
-            q[1] = (r.b[i] & 0x0f0f0f0fu) | (((r.h[i] >> 2) & 0x03030303u) << 4);
-            q[2] = ((r.a[i] >> 4) & 0x0f0f0f0fu) | (((r.h[i] >> 4) & 0x03030303u) << 4);
-            q[3] = ((r.b[i] >> 4) & 0x0f0f0f0fu) | (((r.h[i] >> 6) & 0x03030303u) << 4);
+            h2 p[8];
+            q6_pairs(r.a[i], r.b[i], r.c[i], p);
 #pragma unroll
             for (int qq = 0; qq < 4; qq++) {
                 const int s = 8 * n + 2 * qq + h;
                 const _Float16 sv = sch[s >> 1][s & 1];
                 const h2 ss = {sv, sv};
-                const h2 p0 = (as_h2(pair_lo(q[qq])) + off) * ss, p1 = (as_h2(pair_hi(q[qq])) + off) * ss;
+                const h2 p0 = p[2 * qq] * ss, p1 = p[2 * qq + 1] * ss;
                 h4 b;
                 b[0] = p0[0]; b[1] = p0[1]; b[2] = p1[0]; b[3] = p1[1];
 #pragma unroll

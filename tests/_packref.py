@@ -1,6 +1,8 @@
 """numpy statement of the packed weight layout of ihip_pack_weights (test
 infrastructure): chunk (tile t, unit u) at (t * n_units + u) * 16 * UB, lane
-l = n + 16 g of row n. Used to pin the device packer byte for byte."""
+l = n + 16 g of row n. Used to pin the device packer byte for byte. Q4_K swaps
+bytes 1 and 2 of each quant dword; Q6_K regroups each lane's quant bits into
+6-bit fields (q6_words); the other bytes are moved whole."""
 import numpy as np
 
 from inferno_hip import formats as F
@@ -8,6 +10,25 @@ from inferno_hip import formats as F
 
 def unit_bytes(qt):
     return 8 * 34 if qt == F.Q8_0 else F.BLOCK_BYTES[qt]
+
+
+def q6_words(a, b, h):
+    """The three Q6_K words of one lane and group from its GGUF bytes (ql
+    a[j] = ql[p + j], b[j] = ql[p + 32 + j], qh h[j]), element by element:
+    value j of the group's sub-block qq is nibble qq >> 1 of a[j] (qq even)
+    or b[j] with bits 2 qq, 2 qq + 1 of h[j] above it; pair (qq, t) is
+    values 2t, 2t + 1, placed at bits o and 16 + o of a word."""
+    v = [[((int(a[j]) if qq % 2 == 0 else int(b[j])) >> (4 * (qq >> 1)) & 0xF) | ((int(h[j]) >> (2 * qq) & 3) << 4)
+          for j in range(4)] for qq in range(4)]
+
+    def put(qq, t, o):
+        return (v[qq][2 * t] << o) | (v[qq][2 * t + 1] << (16 + o))
+
+    A = put(0, 0, 0) | put(0, 1, 6) | ((v[3][0] & 0xF) << 12) | ((v[3][1] & 0xF) << 28)
+    B = put(1, 0, 0) | put(1, 1, 6) | ((v[3][2] & 0xF) << 12) | ((v[3][3] & 0xF) << 28)
+    C = (put(2, 0, 0) | ((v[3][0] >> 4) << 6) | ((v[3][1] >> 4) << 22) | ((v[3][2] >> 4) << 8) |
+         ((v[3][3] >> 4) << 24) | put(2, 1, 10))
+    return A, B, C
 
 
 def pack_ref(qt, w, N, K):
@@ -43,10 +64,11 @@ def pack_ref(qt, w, N, K):
                 elif qt == F.Q6_K:
                     for i in range(4):
                         p = 64 * (i >> 1) + 16 * (i & 1) + 4 * g
-                        ch[16 * l + 4 * i:16 * l + 4 * i + 4] = src[p:p + 4]
-                        ch[1024 + 16 * l + 4 * i:1024 + 16 * l + 4 * i + 4] = src[p + 32:p + 36]
                         q = 128 + 32 * (i >> 1) + 16 * (i & 1) + 4 * g
-                        ch[2048 + 16 * l + 4 * i:2048 + 16 * l + 4 * i + 4] = src[q:q + 4]
+                        words = q6_words(src[p:p + 4], src[p + 32:p + 36], src[q:q + 4])
+                        for k in range(3):
+                            ch[1024 * k + 16 * l + 4 * i:1024 * k + 16 * l + 4 * i + 4] = \
+                                np.frombuffer(int(words[k]).to_bytes(4, "little"), np.uint8)
                     if g == 0:
                         ch[3072 + 16 * n:3088 + 16 * n] = src[192:208]
                         ch[3328 + 2 * n:3330 + 2 * n] = src[208:210]
