@@ -152,7 +152,8 @@ class VerifyStep:
         gating -> down (left as K-slice partials); final residual add +
         RMSNorm -> lm_head -> accept. RMSNorm, SiLU gating and the residual
         adds of o and down run inside the input stage of the matmul that
-        consumes them. probe(tag, layer), when given, is called (outside any
+        consumes them, as does the sum of a K-sliced [q; k; v], which o's
+        input stage also stores into qkv. probe(tag, layer), when given, is called (outside any
         graph capture) before each layer's [q; k; v] ("pre"), after it
         ("qkv"), after o ("o"), after [gate; up] ("gu") and after the
         lm_head ("head"), so a test can read x, qkv, gu, logits and the
@@ -171,15 +172,22 @@ class VerifyStep:
         o_parts = ih.gemm_partials(P, M, H, NQ, f32, self.ws_o)
         gu_parts = ih.gemm_partials(P, M, 2 * FF, H, f32, self.ws)
         fold_o, fold_gu = True, gu_parts[1] > 1
+        # a K-sliced [q; k; v] (several token tiles) is summed by o's input
+        # stage, which also stores it (GEMM_SUM_OUT): no reduce launch
+        qkv_parts = ih.gemm_partials(P, M, NQ + 2 * NKV, H, f32, self.ws)
+        fold_qkv = qkv_parts[1] > 1
         self.x.copy_(self.x0)
         for i, lw in enumerate(self.model.layers):
             if probe:
                 probe("pre", i)
-            ex(P, lw["qkv"], self.x, NQ + 2 * NKV, H, act=ih.ACT_RMSNORM, norm_w=lw["attn_norm"], flags=f32,
-               out=self.qkv, ws=self.ws, add=parts if i > 0 else None)
+            ex(P, lw["qkv"], self.x, NQ + 2 * NKV, H, act=ih.ACT_RMSNORM, norm_w=lw["attn_norm"],
+               flags=dfr if fold_qkv else f32, out=None if fold_qkv else self.qkv, ws=self.ws,
+               add=parts if i > 0 else None)
             if probe:
                 probe("qkv", i)
-            if fold_o:
+            if fold_qkv:
+                ex(P, lw["o"], self.qkv, H, NQ, flags=dfr | ih.GEMM_SUM_OUT, ws=self.ws_o, add=qkv_parts)
+            elif fold_o:
                 ex(P, lw["o"], self.qkv[:, :NQ], H, NQ, flags=dfr, ws=self.ws_o)
             else:
                 ex(P, lw["o"], self.qkv[:, :NQ], H, NQ, flags=acc, out=self.x, ws=self.ws)

@@ -171,8 +171,15 @@ int ihip_gemm_q_noalloc(int qtype, const void *w_dev, const float *x_dev,
  * leaves the product in ws as K-slice partials (ihip_gemm_q_partials) and
  * does not touch y; not with IHIP_GEMM_ACCUM, nor with fp32-accurate M > 32.
  * Same workspace size as ihip_gemm_q; a deferring call and the call that
- * adds its partials need separate workspaces. */
+ * adds its partials need separate workspaces. IHIP_GEMM_SUM_OUT (with add
+ * and x, act PLAIN or RMSNORM, K a multiple of 256, ldx of 8): the input is
+ * the sum of the [M x ldx] add slices, which the input stage also stores
+ * into x (all ldx columns; x is written, not read), so a deferred product
+ * wider than this call's K (e.g. [q; k; v] feeding o from its q columns) is
+ * materialised without a reduce launch of its own. No counterpart in the
+ * reference (its products are never K-split). */
 #define IHIP_GEMM_DEFER 32
+#define IHIP_GEMM_SUM_OUT 64
 typedef struct ihip_gemm_input {
     const float *x;        /* activations (written back when add != NULL), or
                               NULL when the add slices are the input */

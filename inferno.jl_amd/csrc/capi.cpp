@@ -587,10 +587,14 @@ int ihip_gemm_q_chain(int qtype, const void *w_packed, const ihip_gemm_input *in
 int ihip_gemm_q_ex(int qtype, const void *w_dev, const ihip_gemm_input *in, float *y_dev, int M, int N, int K,
                    int flags, void *ws, size_t ws_bytes, void *stream) {
     if (!in) return fail(IHIP_EFAULT, "ihip_gemm_q_ex: NULL input descriptor");
-    const int base = flags & ~(IHIP_GEMM_REUSE | IHIP_GEMM_DEFER);
+    const int base = flags & ~(IHIP_GEMM_REUSE | IHIP_GEMM_DEFER | IHIP_GEMM_SUM_OUT);
     const bool defer = flags & IHIP_GEMM_DEFER;
-    // x absent: the input is the sum of the add slices themselves
+    // x absent: the input is the sum of the add slices themselves; with
+    // SUM_OUT that sum is also stored into x
+    const bool sum_out = flags & IHIP_GEMM_SUM_OUT;
     if (!in->x && !in->add) return fail(IHIP_EFAULT, "ihip_gemm_q_ex: NULL x without add slices");
+    if (sum_out && (!in->x || !in->add))
+        return fail(IHIP_EFAULT, "ihip_gemm_q_ex: IHIP_GEMM_SUM_OUT needs x (the sum's destination) and add slices");
     const float *xin = in->x ? in->x : in->add;
     int rc = check_gemm(qtype, w_dev, xin, defer ? const_cast<float *>(xin) : y_dev, M, N, K, base);
     if (rc != IHIP_OK) return rc;
@@ -602,12 +606,19 @@ int ihip_gemm_q_ex(int qtype, const void *w_dev, const ihip_gemm_input *in, floa
     if ((K & 7) != 0) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: K=%d must be a multiple of 8", K);
     if (act == IHIP_ACT_RMSNORM && !(in->eps >= 0.f)) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: eps=%g", in->eps);
     if (in->norm_w && !aligned16(in->norm_w)) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: norm_w must be 16-byte aligned");
+    if (sum_out) {
+        if (act == IHIP_ACT_SILU_MUL) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: IHIP_GEMM_SUM_OUT with SILU_MUL");
+        if ((K & 255) || (in->ldx & 7))
+            return fail(IHIP_EINVAL, "ihip_gemm_q_ex: IHIP_GEMM_SUM_OUT needs K %% 256 == 0 and ldx %% 8 == 0 (K=%d ldx=%d)",
+                        K, in->ldx);
+        if (!aligned16(in->x)) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: IHIP_GEMM_SUM_OUT x must be 16-byte aligned");
+    }
     if (in->add) {
-        const int64_t slice = (int64_t)M * (in->x ? K : in->ldx);
+        const int64_t slice = (int64_t)M * (in->x && !sum_out ? K : in->ldx);
         if (in->n_add < 1 || in->add_stride < slice || (in->add_stride & 3) || !aligned16(in->add))
             return fail(IHIP_EINVAL, "ihip_gemm_q_ex: add slices n=%d stride=%lld", in->n_add,
                         (long long)in->add_stride);
-        if (act == IHIP_ACT_SILU_MUL && in->x)
+        if (act == IHIP_ACT_SILU_MUL && in->x && !sum_out)
             return fail(IHIP_EINVAL, "ihip_gemm_q_ex: add with SILU_MUL needs x = NULL (the slices are the input)");
         if (flags & IHIP_GEMM_REUSE) return fail(IHIP_EINVAL, "ihip_gemm_q_ex: add with IHIP_GEMM_REUSE");
     }
@@ -680,7 +691,7 @@ int ihip_mlp_forward(int qt_gate_up, const void *w_gate_up, int qt_down, const v
 int ihip_gemm_q_partials(int qtype, int M, int N, int K, int flags, void *ws, float **slices, int *n_slices,
                          int64_t *stride) {
     if (!ws || !slices || !n_slices || !stride) return fail(IHIP_EFAULT, "ihip_gemm_q_partials: NULL pointer");
-    const int base = flags & ~(IHIP_GEMM_REUSE | IHIP_GEMM_DEFER);
+    const int base = flags & ~(IHIP_GEMM_REUSE | IHIP_GEMM_DEFER | IHIP_GEMM_SUM_OUT);
     const int rc = check_gemm_shape(qtype, M, N, K, base);
     if (rc != IHIP_OK) return rc;
     size_t off = 0;

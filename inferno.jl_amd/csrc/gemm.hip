@@ -676,6 +676,7 @@ struct ActIn {
     int n_add;
     int64_t add_stride;  // floats between slices
     bool defer;          // leave the product as K-slice partials in the workspace
+    float *sum_out = nullptr;  // (input = the [M][ldx] slices' sum) also store that sum here, all ldx columns
 };
 
 __device__ __forceinline__ float silu_mul1(float g, float u) { return g / (1.0f + expf(-g)) * u; }
@@ -828,7 +829,9 @@ __device__ __forceinline__ void prep_finish(float (&v)[8], float4 wa, float4 wb,
 // partials of a previous matmul, the order its reduce would use), stored back
 // into x (each element has one owner thread), before the transform; slices
 // [M][K]. X == nullptr: x is that sum itself (slices [M][ldx], rows of 2K
-// for ACT_SILU_MUL), nothing is stored back.
+// for ACT_SILU_MUL), stored into xw when xw != nullptr (all ldx columns: the
+// workgroups past the units of K fold and store columns K.. only; K is then
+// a multiple of 256 and ldx of 8).
 template <int LK, int MT, bool SPLIT, bool MINS, int TPW>
 __global__ __launch_bounds__(32 * TPW) void prep_kernel(const float *__restrict__ X, int ldx, int M, int K, int op,
                                                    const float *__restrict__ norm_w,
@@ -840,10 +843,11 @@ __global__ __launch_bounds__(32 * TPW) void prep_kernel(const float *__restrict_
     const int tl = tid >> 5, gi = tid & 31;  // (a token per 32 threads, TPW per workgroup)
     const int t = blockIdx.y * TPW + tl;
     const int k = u * UNIT + gi * 8;
+    const bool tail = u >= (K + UNIT - 1) / UNIT;  // (whole workgroups: no transform)
     float4 wa, wb;
     norm_weights(norm_w, op, k, K, wa, wb);
     float v[8];
-    if (t < M && k < K) {
+    if (t < M && (k < K || (tail && k < ldx))) {
         // the sum of the partial slices at column c of row t, in slice order:
         // up to MAXS slices (of both columns when two are asked for) in one
         // round of loads issued before any sum, more four at a time
@@ -934,6 +938,11 @@ __global__ __launch_bounds__(32 * TPW) void prep_kernel(const float *__restrict_
         } else {
             slices(ldx, k, v);
             if (op == ACT_SILU_MUL) slices(ldx, K + k, up);
+            if (xw != nullptr) {  // (the sum itself, stored for the caller)
+                float *wrow = xw + (size_t)t * ldx + k;
+                *(float4 *)wrow = make_float4(v[0], v[1], v[2], v[3]);
+                *(float4 *)(wrow + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            }
         }
         if (op == ACT_SILU_MUL) {
 #pragma unroll
@@ -943,6 +952,7 @@ __global__ __launch_bounds__(32 * TPW) void prep_kernel(const float *__restrict_
 #pragma unroll
         for (int e = 0; e < 8; e++) v[e] = 0.f;
     }
+    if (tail) return;
     prep_finish<LK, MT, SPLIT, MINS>(v, wa, wb, u, t, gi, op, afrag, xs, inv, mfrag, ssq, sl);
 }
 
@@ -2164,9 +2174,12 @@ hipError_t launch_prep(const float *X, const ActIn &in, int M, int K, const ActW
     // (measured: the verify step 1.1 % faster than 8 per workgroup; the
     // M = 64 tree forward unchanged); IHIP_PREP_TPW selects 4 or 8
     static const int tpw = env_int("IHIP_PREP_TPW", 2);
-#define PREP(tp) prep_kernel<LK, MT, SPLIT, C::MINS, tp><<<dim3(n_units, TOK / tp), 32 * tp, 0, st>>>( \
+    // (sum_out: workgroups past the input's units fold and store its other columns)
+    const int tail_units = (X == nullptr && in.sum_out != nullptr) ? (in.ldx - K + UNIT - 1) / UNIT : 0;
+    float *xw = X != nullptr ? const_cast<float *>(X) : in.sum_out;
+#define PREP(tp) prep_kernel<LK, MT, SPLIT, C::MINS, tp><<<dim3(n_units + tail_units, TOK / tp), 32 * tp, 0, st>>>( \
         X, in.ldx, M, K, in.op, in.norm_w, a.afrag, a.xs, a.inv, a.mfrag, a.ssq, in.add, in.n_add, in.add_stride, \
-        const_cast<float *>(X), sl)
+        xw, sl)
     const int sl = compact ? (SPLIT ? 2 * M : M) : 0;
     if (tpw == 2) PREP(2); else if (tpw == 4) PREP(4); else PREP(8);
 #undef PREP
@@ -2499,6 +2512,7 @@ static hipError_t gemm_in(int qt, const void *W, const float *X, const ActIn &in
         if (e != hipSuccess) return e;
         ActIn in2 = in;
         if (in2.add != nullptr) in2.add += (size_t)m0 * (X != nullptr ? K : in.ldx);
+        if (in2.sum_out != nullptr) in2.sum_out += (size_t)m0 * in.ldx;
         const float *X2 = X != nullptr ? X + (size_t)m0 * in.ldx : nullptr;  // (absent: the slices are the input)
         return gemm_in(qt, W, X2, in2, Y + (size_t)m0 * N, M - m0, N, K, flags | 1, ws, st);
     }
@@ -2591,8 +2605,11 @@ hipError_t launch_gemm_chain_ex(int qt, const void *W, const float *X, int ldx, 
 hipError_t launch_gemm_ex(int qt, const void *W, const float *X, int ldx, int op, const float *norm_w, float eps,
                           const float *add, int n_add, int64_t add_stride, float *Y, int M, int N, int K, int flags,
                           void *ws, hipStream_t st) {
-    const ActIn in{op, ldx, norm_w, eps, (flags & 16) != 0, add, n_add, add_stride, (flags & 32) != 0};
-    return gemm_in(qt, W, X, in, Y, M, N, K, flags & ~48, ws, st);
+    // (flags 64: the slices are the input and their sum goes to X)
+    const bool sum_out = (flags & 64) != 0;
+    ActIn in{op, ldx, norm_w, eps, (flags & 16) != 0, add, n_add, add_stride, (flags & 32) != 0};
+    in.sum_out = sum_out ? const_cast<float *>(X) : nullptr;
+    return gemm_in(qt, W, sum_out ? nullptr : X, in, Y, M, N, K, flags & ~112, ws, st);
 }
 
 bool gemm_reuse_ok(int M, int flags) { return launch_m(M, flags) == M; }

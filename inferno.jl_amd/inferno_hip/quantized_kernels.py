@@ -22,6 +22,7 @@ from . import _lib
 from .formats import BLOCK_BYTES, BLOCK_ELEMS, Q4_K, Q5_K, Q6_K, Q8_0, NAMES
 
 GEMM_AUTO, GEMM_F32, GEMM_HALF, GEMM_ACCUM, GEMM_PACKED, GEMM_REUSE, GEMM_DEFER = 0, 1, 2, 4, 8, 16, 32
+GEMM_SUM_OUT = 64
 ACT_PLAIN, ACT_RMSNORM, ACT_SILU_MUL = 0, 1, 2
 
 
@@ -151,11 +152,14 @@ def gemm_q_ex(qtype: int, w_dev, x, n: int, k: int, act: int = ACT_PLAIN, norm_w
     be a row-strided view (x.stride(1) == 1); m defaults to x.shape[0].
     add: (pointer, n_slices, slice_stride) of K-slice partials (from
     gemm_partials) folded into x first and stored back; with x None the
-    slices' sum is the input itself ([m, ldx] slices, m and ldx given). With
-    GEMM_DEFER the product stays in ws as partials and `out` is not
-    written."""
+    slices' sum is the input itself ([m, ldx] slices, m and ldx given); with
+    GEMM_SUM_OUT and x given, likewise, and x[:m, :ldx] (ldx = x's row
+    stride) is written with that sum (not read). With GEMM_DEFER the product
+    stays in ws as partials and `out` is not written."""
     import torch
     width = 2 * k if act == ACT_SILU_MUL else k
+    if (flags & GEMM_SUM_OUT) and (x is None or add is None):
+        raise ValueError("GEMM_SUM_OUT needs x (where the slices' sum goes) and add")
     if x is None:
         if add is None or m is None or ldx is None:
             raise ValueError("x=None needs add, m and ldx")
@@ -363,7 +367,8 @@ def gemm_partials(qtype: int, m: int, n: int, k: int, flags: int, ws):
 def gemm_ws_bytes(qtype: int, m: int, n: int, k: int, flags: int = GEMM_AUTO) -> int:
     """Workspace bytes ihip_gemm_q needs for this call shape."""
     nb = C.c_size_t()
-    _lib.check(_lib.load().ihip_gemm_q_ws_bytes(qtype, m, n, k, flags & ~(GEMM_REUSE | GEMM_DEFER), C.byref(nb)))
+    _lib.check(_lib.load().ihip_gemm_q_ws_bytes(qtype, m, n, k, flags & ~(GEMM_REUSE | GEMM_DEFER | GEMM_SUM_OUT),
+                                                    C.byref(nb)))
     return max(int(nb.value), 16)
 
 

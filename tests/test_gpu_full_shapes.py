@@ -71,14 +71,25 @@ def _silu_mul(gu, ff):
         return (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
 
 
-def _partials_sum(ih, qt, m, n, k, flags, ws):
-    """Sum (fp64) of the K-slice partials a GEMM_DEFER call left in ws."""
+def _partials(ih, qt, m, n, k, flags, ws):
+    """The K-slice partials [S, m, n] a GEMM_DEFER call left in ws."""
     import torch
     ptr, ns, stride = ih.gemm_partials(qt, m, n, k, flags, ws)
     off = (ptr - ws.data_ptr()) // 4
     wf = ws.view(torch.float32)
-    sl = wf[off: off + ns * stride].view(ns, stride)[:, : m * n].reshape(ns, m, n)
-    return _h(sl).astype(np.float64).sum(axis=0)
+    return _h(wf[off: off + ns * stride].view(ns, stride)[:, : m * n].reshape(ns, m, n))
+
+
+def _partials_sum(ih, qt, m, n, k, flags, ws):
+    """Sum (fp64) of the K-slice partials a GEMM_DEFER call left in ws."""
+    return _partials(ih, qt, m, n, k, flags, ws).astype(np.float64).sum(axis=0)
+
+
+def _fp32_slice_order_sum(sl):
+    s = sl[0].copy()
+    for j in range(1, sl.shape[0]):
+        s = (s + sl[j]).astype(np.float32)
+    return s
 
 
 class Checker:
@@ -113,6 +124,7 @@ def _run_step_with_checks(ih, B, model, step, chk, fold_chk, prec_flags):
     st = {}
     fl = prec_flags | ih.GEMM_PACKED
     fold_gu = ih.gemm_partials(P, M, 2 * FF, H, fl, step.ws)[1] > 1
+    fold_qkv = ih.gemm_partials(P, M, NQ + 2 * NKV, H, fl, step.ws)[1] > 1
 
     def down_check(i):
         d = _partials_sum(ih, F.Q6_K, M, H, FF, fl, step.ws_down)
@@ -130,10 +142,15 @@ def _run_step_with_checks(ih, B, model, step, chk, fold_chk, prec_flags):
             if i > 0:
                 fold_chk("x += down", x, st["x_pre"] + st["down"])
             wq = np.concatenate([hw[i]["q"], hw[i]["kv"]])
-            qkv = _h(step.qkv)
+            # (K-sliced: still partials, which o's input stage sums and stores)
+            if fold_qkv:
+                st["qkv_sl"] = _partials(ih, P, M, NQ + 2 * NKV, H, fl, step.ws)
+            qkv = st["qkv_sl"].astype(np.float64).sum(axis=0) if fold_qkv else _h(step.qkv)
             chk("qkv", qkv, O.gemv_f64(P, wq, _rms(x, hw[i]["attn_norm"]), M, NQ + 2 * NKV, H))
             st["x_qkv"], st["qkv"] = x, qkv
         elif tag == "o":
+            if fold_qkv:  # the stored sum: the partials' fp32 sum in slice order, every column
+                assert np.array_equal(_h(step.qkv), _fp32_slice_order_sum(st["qkv_sl"])), "qkv stored by o's input"
             o = _partials_sum(ih, P, M, H, NQ, fl, step.ws_o)
             chk("o", o, O.gemv_f64(P, hw[i]["o"], st["qkv"][:, :NQ], M, H, NQ))
             st["o"] = o

@@ -147,6 +147,66 @@ def test_defer_and_fold_residual(ih, qt2):
         assert rel_l2(xf.cpu().numpy(), ref) < 1e-5
 
 
+@pytest.mark.parametrize("M,fl_prod,fl_cons", [(5, 1, 1), (24, 1, 1), (64, 2, 2), (40, 2, 1)])
+def test_sum_out(ih, M, fl_prod, fl_cons):
+    """GEMM_SUM_OUT: a deferred, possibly K-sliced product wider than the
+    consumer's K ([q; k; v] feeding o) is summed by the consumer's input
+    stage, which stores the whole sum (the columns past K by workgroups of
+    their own) as the fp32 sum of the slices in slice order, and the
+    consumer's product equals a plain call on that sum bit for bit. M = 40
+    fp32-accurate runs as two launches over token halves."""
+    import torch
+    H, NQ, NKV, N2 = 4096, 512, 128, 256
+    N1 = NQ + 2 * NKV
+    rng = np.random.default_rng(M)
+    w1 = synth.matrix(F.Q4_K, N1, H, synth.stream_for(3, "so1"))
+    w2 = synth.matrix(F.Q4_K, N2, NQ, synth.stream_for(4, "so2"))
+    p1, p2 = ih.pack_weights(F.Q4_K, _dev(w1), N1, H), ih.pack_weights(F.Q4_K, _dev(w2), N2, NQ)
+    fp, fc = fl_prod | ih.GEMM_PACKED, fl_cons | ih.GEMM_PACKED
+    x = _dev(rng.standard_normal((M, H)).astype(np.float32))
+    ws1 = torch.empty(ih.quantized_kernels.gemm_ws_bytes(F.Q4_K, M, N1, H, fp), dtype=torch.uint8, device="cuda")
+    ih.gemm_q_ex(F.Q4_K, p1, x, N1, H, flags=fp | ih.GEMM_DEFER, ws=ws1)
+    parts = ih.gemm_partials(F.Q4_K, M, N1, H, fp, ws1)
+    ptr, ns, stride = parts
+    wf = ws1.view(torch.float32)
+    off = (ptr - ws1.data_ptr()) // 4
+    sl = wf[off:off + ns * stride].view(ns, stride)[:, :M * N1].reshape(ns, M, N1).cpu().numpy()
+    ref = sl[0].copy()
+    for j in range(1, ns):
+        ref = (ref + sl[j]).astype(np.float32)
+    qkv = torch.full((M, N1), float("nan"), device="cuda")
+    y = ih.gemm_q_ex(F.Q4_K, p2, qkv, N2, NQ, flags=fc | ih.GEMM_SUM_OUT, add=parts)
+    assert np.array_equal(qkv.cpu().numpy(), ref), (M, ns)
+    y_plain = ih.gemm_q_ex(F.Q4_K, p2, qkv[:, :NQ], N2, NQ, flags=fc)
+    assert torch.equal(y, y_plain), (M, ns)
+    assert rel_l2(y.cpu().numpy(), O.gemv_f64(F.Q4_K, w2, ref[:, :NQ], M, N2, NQ)) < (1e-5 if fl_cons == 1 else 1e-2)
+
+
+def test_sum_out_errors(ih):
+    import ctypes as C
+    import torch
+    qt = F.Q4_K
+    w = ih.pack_weights(qt, _dev(synth.matrix(qt, 16, 256, 1)), 16, 256)
+    x = torch.zeros(5, 512, device="cuda")
+    sl = torch.from_numpy(np.random.default_rng(7).standard_normal((2, 5, 512)).astype(np.float32)).cuda()
+    with pytest.raises(ValueError):  # no add slices
+        ih.gemm_q_ex(qt, w, x, 16, 256, flags=ih.GEMM_PACKED | ih.GEMM_SUM_OUT)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    y = torch.empty(5, 16, device="cuda")
+    L = ih.load()
+
+    def call(act, ldx, xp=x.data_ptr(), add=sl.data_ptr()):
+        gi = ih._lib.GemmInput(xp, ldx, act, None, 1e-6, add, 2, 5 * 512)
+        return L.ihip_gemm_q_ex(qt, w.data_ptr(), C.byref(gi), y.data_ptr(), 5, 16, 256,
+                                ih.GEMM_PACKED | ih.GEMM_SUM_OUT, ws.data_ptr(), ws.numel(), None)
+    assert call(ih.ACT_SILU_MUL, 512) == -22   # not with SiLU gating
+    assert call(ih.ACT_PLAIN, 508) == -22      # ldx % 8
+    assert call(ih.ACT_PLAIN, 512, xp=None) != 0  # x is the destination
+    assert call(ih.ACT_PLAIN, 512) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(x, sl[0] + sl[1])
+
+
 @pytest.mark.parametrize("packed", [False, True])
 def test_mlp_forward(ih, packed):
     """ihip_mlp_forward (the MLP half of a decoder layer, src/ModelCPU.jl:884-889
