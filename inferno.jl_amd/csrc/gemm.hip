@@ -1801,21 +1801,29 @@ __device__ __forceinline__ void unit_vals(const Unit<QT> &r, const AReg<QT> (&a)
         f4 c[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) c[mt] = f4{0.f, 0.f, 0.f, 0.f};
+        // sub-blocks 2j and 2j + 1 (groups 2n and 2n + 1, the same qq) share
+        // one 16x16x32 MFMA, which costs the matrix core what a 16x16x16 does:
+        // their A operands are adjacent (f[2j], f[2j + 1]) and the scales are
+        // already in B, so the pair's 32 products sum in one instruction
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int n = i >> 1, h = i & 1;
-            h2 p[8];
-            q6_pairs(r.a[i], r.b[i], r.c[i], p);
+        for (int n = 0; n < 2; n++) {
+            h2 p[2][8];
+            q6_pairs(r.a[2 * n], r.b[2 * n], r.c[2 * n], p[0]);
+            q6_pairs(r.a[2 * n + 1], r.b[2 * n + 1], r.c[2 * n + 1], p[1]);
 #pragma unroll
             for (int qq = 0; qq < 4; qq++) {
-                const int s = 8 * n + 2 * qq + h;
-                const _Float16 sv = sch[s >> 1][s & 1];
-                const h2 ss = {sv, sv};
-                const h2 p0 = p[2 * qq] * ss, p1 = p[2 * qq + 1] * ss;
-                h4 b;
-                b[0] = p0[0]; b[1] = p0[1]; b[2] = p1[0]; b[3] = p1[1];
+                const int s = 8 * n + 2 * qq;  // (and s + 1)
+                h8 b;
 #pragma unroll
-                for (int mt = 0; mt < MT; mt++) c[mt] = mfma16(a[mt].f[s], b, c[mt]);
+                for (int h = 0; h < 2; h++) {
+                    const _Float16 sv = sch[(s + h) >> 1][(s + h) & 1];
+                    const h2 ss = {sv, sv};
+                    const h2 p0 = p[h][2 * qq] * ss, p1 = p[h][2 * qq + 1] * ss;
+                    b[4 * h] = p0[0]; b[4 * h + 1] = p0[1]; b[4 * h + 2] = p1[0]; b[4 * h + 3] = p1[1];
+                }
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+                    c[mt] = mfma32(__builtin_shufflevector(a[mt].f[s], a[mt].f[s + 1], 0, 1, 2, 3, 4, 5, 6, 7), b, c[mt]);
             }
         }
 #pragma unroll
