@@ -1830,6 +1830,59 @@ __device__ __forceinline__ void unit_vals(const Unit<QT> &r, const AReg<QT> (&a)
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int k = 0; k < 4; k++) vals[mt * 4 + k] = (d * inv[mt][k]) * c[mt][k];
+    } else if constexpr (QT == QT_Q6_K && SPLIT && MT >= 2) {
+        // fp32-accurate with several tiles: the scale goes into the weight
+        // operand exactly as two fp16 terms, hi = fp16(sc (q - 32)) and the
+        // residual lo = sc (q - 32) - hi (0 or +-1: |sc (q - 32)| <= 4096, an
+        // integer), each pair of sub-blocks one 16x16x32 MFMA per term. Two
+        // packed ops per weight pair replace an fp32 fma per sub-block, tile
+        // and output (4 MT per sub-block); the products stay exact
+        const float d = live ? half_bits(r.d) : 0.f;
+        const uint32_t scw[4] = {r.sc.x ^ 0x80808080u, r.sc.y ^ 0x80808080u, r.sc.z ^ 0x80808080u,
+                                 r.sc.w ^ 0x80808080u};
+        const h2 off_sc = as_h2(0xE480E480u);
+        h2 sch[8];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            sch[2 * w] = as_h2(pair_lo(scw[w])) + off_sc;
+            sch[2 * w + 1] = as_h2(pair_hi(scw[w])) + off_sc;
+        }
+        f4 c[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) c[mt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int n = 0; n < 2; n++) {
+            h2 p[2][8];
+            q6_pairs(r.a[2 * n], r.b[2 * n], r.c[2 * n], p[0]);
+            q6_pairs(r.a[2 * n + 1], r.b[2 * n + 1], r.c[2 * n + 1], p[1]);
+#pragma unroll
+            for (int qq = 0; qq < 4; qq++) {
+                const int s = 8 * n + 2 * qq;  // (and s + 1)
+                h8 bh, bl;
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const _Float16 sv = sch[(s + h) >> 1][(s + h) & 1];
+                    const h2 ss = {sv, sv};
+#pragma unroll
+                    for (int t = 0; t < 2; t++) {
+                        const h2 hi = p[h][2 * qq + t] * ss;
+                        const h2 lo = __builtin_elementwise_fma(p[h][2 * qq + t], ss, -hi);
+                        bh[4 * h + 2 * t] = hi[0]; bh[4 * h + 2 * t + 1] = hi[1];
+                        bl[4 * h + 2 * t] = lo[0]; bl[4 * h + 2 * t + 1] = lo[1];
+                    }
+                }
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    const h8 a8 = __builtin_shufflevector(a[mt].f[s], a[mt].f[s + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+                    c[mt] = mfma32(a8, bh, c[mt]);
+                    c[mt] = mfma32(a8, bl, c[mt]);
+                }
+            }
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int k = 0; k < TPL; k++) vals[mt * TPL + k] = (d * inv[mt][k]) * (c[mt][2 * k] + c[mt][2 * k + 1]);
     } else if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {
         float d = half_bits(r.hdr.x), dmin = half_bits(r.hdr.x >> 16);
         if (!live) { d = 0.f; dmin = 0.f; }
@@ -1884,10 +1937,12 @@ __host__ __device__ constexpr int stream_ups_cap(int qt, bool split) {
 // tiles, which Q6_K also prefers when it fits) and the rest fit in 256
 // registers without spilling (two waves then
 // overlap one's MFMAs with the other's dequantization), else one per SIMD
-// (4) with the full register file. Independent of the weight layout, so
-// packed and GGUF-layout weights sum the same K-slices in the same order.
+// (4) with the full register file. (fp32-accurate Q6_K fits since its scales
+// go into the weight operand as two exact fp16 terms.) Independent of the
+// weight layout, so packed and GGUF-layout weights sum the same K-slices in
+// the same order.
 __host__ __device__ constexpr int tall_waves(int qt, bool split, int mt) {
-    return (qt == QT_Q4_K || qt == QT_Q5_K || (qt == QT_Q6_K && !split) || (qt == QT_Q8_0 && mt <= 2)) ? 8 : 4;
+    return (qt == QT_Q4_K || qt == QT_Q5_K || qt == QT_Q6_K || (qt == QT_Q8_0 && mt <= 2)) ? 8 : 4;
 }
 
 // Several token tiles (M up to 32 fp32-accurate, 64 half): NW = 4 or 8
