@@ -1156,6 +1156,62 @@ template <> struct AReg<QT_Q5_K> { h8 f[8]; h4 mins; };
 template <> struct AReg<QT_Q6_K> { h4 f[16]; };
 template <> struct AReg<QT_Q8_0> { h8 f[8]; };
 
+// The 16 sub-block products of a Q6_K unit against MT register tiles with
+// the int8 sub-block scales folded into the weight operand: c[mt] = sum_s
+// (sc_s (q - 32) . x)_s. Half (EXACT false): B = fp16(sc (q - 32)), one
+// rounding (|sc (q - 32)| <= 4096), the order of error of the fp16
+// activations. EXACT: two fp16 terms, hi = fp16(sc (q - 32)) and the
+// residual lo = sc (q - 32) - hi (0 or +-1: the product is an integer), so
+// every product is exact. Sub-blocks 2j and 2j + 1 (groups 2n and 2n + 1,
+// the same qq; adjacent A operands f[2j], f[2j + 1]) share one 16x16x32
+// MFMA per term, which costs the matrix core what a 16x16x16 does.
+template <int MT, bool EXACT>
+__device__ __forceinline__ void q6_mfma_folded(const Unit<QT_Q6_K> &r, const AReg<QT_Q6_K> (&a)[MT], f4 (&c)[MT]) {
+    // the 16 scales as exact fp16: (1024 + (sc ^ 0x80)) - 1152 = sc
+    const uint32_t scw[4] = {r.sc.x ^ 0x80808080u, r.sc.y ^ 0x80808080u, r.sc.z ^ 0x80808080u,
+                             r.sc.w ^ 0x80808080u};
+    const h2 off_sc = as_h2(0xE480E480u);
+    h2 sch[8];
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        sch[2 * w] = as_h2(pair_lo(scw[w])) + off_sc;
+        sch[2 * w + 1] = as_h2(pair_hi(scw[w])) + off_sc;
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) c[mt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int n = 0; n < 2; n++) {
+        h2 p[2][8];
+        q6_pairs(r.a[2 * n], r.b[2 * n], r.c[2 * n], p[0]);
+        q6_pairs(r.a[2 * n + 1], r.b[2 * n + 1], r.c[2 * n + 1], p[1]);
+#pragma unroll
+        for (int qq = 0; qq < 4; qq++) {
+            const int s = 8 * n + 2 * qq;  // (and s + 1)
+            h8 bh, bl;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const _Float16 sv = sch[(s + h) >> 1][(s + h) & 1];
+                const h2 ss = {sv, sv};
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const h2 hi = p[h][2 * qq + t] * ss;
+                    bh[4 * h + 2 * t] = hi[0]; bh[4 * h + 2 * t + 1] = hi[1];
+                    if constexpr (EXACT) {
+                        const h2 lo = __builtin_elementwise_fma(p[h][2 * qq + t], ss, -hi);
+                        bl[4 * h + 2 * t] = lo[0]; bl[4 * h + 2 * t + 1] = lo[1];
+                    }
+                }
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const h8 a8 = __builtin_shufflevector(a[mt].f[s], a[mt].f[s + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+                c[mt] = mfma32(a8, bh, c[mt]);
+                if constexpr (EXACT) c[mt] = mfma32(a8, bl, c[mt]);
+            }
+        }
+    }
+}
+
 // One unit against register operands of MT token tiles: each weight
 // fragment is dequantized once and multiplies every tile. acc[mt]: scaled dot
 // products, macc[mt]: the Q4_K/Q5_K min term / 32 (both in the MFMA D layout:
@@ -1788,97 +1844,19 @@ __device__ __forceinline__ void unit_vals(const Unit<QT> &r, const AReg<QT> (&a)
     constexpr int TPL = SPLIT ? 2 : 4;
     if constexpr (QT == QT_Q6_K && !SPLIT) {
         const float d = live ? half_bits(r.d) : 0.f;
-        // the 16 scales as exact fp16: (1024 + (sc ^ 0x80)) - 1152 = sc
-        const uint32_t scw[4] = {r.sc.x ^ 0x80808080u, r.sc.y ^ 0x80808080u, r.sc.z ^ 0x80808080u,
-                                 r.sc.w ^ 0x80808080u};
-        const h2 off_sc = as_h2(0xE480E480u);
-        h2 sch[8];
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            sch[2 * w] = as_h2(pair_lo(scw[w])) + off_sc;
-            sch[2 * w + 1] = as_h2(pair_hi(scw[w])) + off_sc;
-        }
         f4 c[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) c[mt] = f4{0.f, 0.f, 0.f, 0.f};
-        // sub-blocks 2j and 2j + 1 (groups 2n and 2n + 1, the same qq) share
-        // one 16x16x32 MFMA, which costs the matrix core what a 16x16x16 does:
-        // their A operands are adjacent (f[2j], f[2j + 1]) and the scales are
-        // already in B, so the pair's 32 products sum in one instruction
-#pragma unroll
-        for (int n = 0; n < 2; n++) {
-            h2 p[2][8];
-            q6_pairs(r.a[2 * n], r.b[2 * n], r.c[2 * n], p[0]);
-            q6_pairs(r.a[2 * n + 1], r.b[2 * n + 1], r.c[2 * n + 1], p[1]);
-#pragma unroll
-            for (int qq = 0; qq < 4; qq++) {
-                const int s = 8 * n + 2 * qq;  // (and s + 1)
-                h8 b;
-#pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const _Float16 sv = sch[(s + h) >> 1][(s + h) & 1];
-                    const h2 ss = {sv, sv};
-                    const h2 p0 = p[h][2 * qq] * ss, p1 = p[h][2 * qq + 1] * ss;
-                    b[4 * h] = p0[0]; b[4 * h + 1] = p0[1]; b[4 * h + 2] = p1[0]; b[4 * h + 3] = p1[1];
-                }
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++)
-                    c[mt] = mfma32(__builtin_shufflevector(a[mt].f[s], a[mt].f[s + 1], 0, 1, 2, 3, 4, 5, 6, 7), b, c[mt]);
-            }
-        }
+        q6_mfma_folded<MT, false>(r, a, c);
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int k = 0; k < 4; k++) vals[mt * 4 + k] = (d * inv[mt][k]) * c[mt][k];
     } else if constexpr (QT == QT_Q6_K && SPLIT && MT >= 2) {
-        // fp32-accurate with several tiles: the scale goes into the weight
-        // operand exactly as two fp16 terms, hi = fp16(sc (q - 32)) and the
-        // residual lo = sc (q - 32) - hi (0 or +-1: |sc (q - 32)| <= 4096, an
-        // integer), each pair of sub-blocks one 16x16x32 MFMA per term. Two
-        // packed ops per weight pair replace an fp32 fma per sub-block, tile
-        // and output (4 MT per sub-block); the products stay exact
+        // fp32-accurate with several tiles: the scales in the weight operand
+        // as two exact fp16 terms (q6_mfma_folded); two packed ops per weight
+        // pair replace an fp32 fma per sub-block, tile and output
         const float d = live ? half_bits(r.d) : 0.f;
-        const uint32_t scw[4] = {r.sc.x ^ 0x80808080u, r.sc.y ^ 0x80808080u, r.sc.z ^ 0x80808080u,
-                                 r.sc.w ^ 0x80808080u};
-        const h2 off_sc = as_h2(0xE480E480u);
-        h2 sch[8];
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            sch[2 * w] = as_h2(pair_lo(scw[w])) + off_sc;
-            sch[2 * w + 1] = as_h2(pair_hi(scw[w])) + off_sc;
-        }
         f4 c[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) c[mt] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int n = 0; n < 2; n++) {
-            h2 p[2][8];
-            q6_pairs(r.a[2 * n], r.b[2 * n], r.c[2 * n], p[0]);
-            q6_pairs(r.a[2 * n + 1], r.b[2 * n + 1], r.c[2 * n + 1], p[1]);
-#pragma unroll
-            for (int qq = 0; qq < 4; qq++) {
-                const int s = 8 * n + 2 * qq;  // (and s + 1)
-                h8 bh, bl;
-#pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const _Float16 sv = sch[(s + h) >> 1][(s + h) & 1];
-                    const h2 ss = {sv, sv};
-#pragma unroll
-                    for (int t = 0; t < 2; t++) {
-                        const h2 hi = p[h][2 * qq + t] * ss;
-                        const h2 lo = __builtin_elementwise_fma(p[h][2 * qq + t], ss, -hi);
-                        bh[4 * h + 2 * t] = hi[0]; bh[4 * h + 2 * t + 1] = hi[1];
-                        bl[4 * h + 2 * t] = lo[0]; bl[4 * h + 2 * t + 1] = lo[1];
-                    }
-                }
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++) {
-                    const h8 a8 = __builtin_shufflevector(a[mt].f[s], a[mt].f[s + 1], 0, 1, 2, 3, 4, 5, 6, 7);
-                    c[mt] = mfma32(a8, bh, c[mt]);
-                    c[mt] = mfma32(a8, bl, c[mt]);
-                }
-            }
-        }
+        q6_mfma_folded<MT, true>(r, a, c);
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
