@@ -1830,13 +1830,14 @@ void gemm_v_kernel(const uint8_t *__restrict__ W, const uint8_t *__restrict__ af
 // (before the RMSNorm row scale).
 //  Q4_K/Q5_K: inv * (d * (sc q . x) - 32 dmin * (m . X/32)), the 6-bit scales
 //             folded into B exactly as in compute_v.
-//  Q6_K, half mode: the int8 sub-block scale is folded into the fp16 weight
-//             operand, B = fp16(sc * q) (|sc q| <= 4096, one rounding, the
-//             same order of error as the fp16 activations), so the 16 MFMAs
-//             of a unit chain in one accumulator per tile and d * inv is
-//             applied once: 2 VALU ops per weight pair instead of an fp32
-//             fma per sub-block, tile and output.
-//  Q8_0 and fp32-accurate Q6_K: per-chunk fp32 scaling (compute_v).
+//  Q6_K: the int8 sub-block scale is folded into the fp16 weight operand
+//             (q6_mfma_folded): half mode B = fp16(sc * q), one rounding;
+//             fp32-accurate two exact terms. The MFMAs of a unit chain in
+//             one accumulator per tile and d * inv is applied once: 2 (half)
+//             or 3 VALU ops per weight pair instead of an fp32 fma per
+//             sub-block, tile and output. (One tile keeps compute_v's
+//             per-sub-block fp32 scaling, measured faster there.)
+//  Q8_0: per-chunk fp32 scaling (compute_v).
 template <int QT, bool SPLIT, int MT>
 __device__ __forceinline__ void unit_vals(const Unit<QT> &r, const AReg<QT> (&a)[MT],
                                           const float (&inv)[MT][SPLIT ? 2 : 4], int g, bool live,
